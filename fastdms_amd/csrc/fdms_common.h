@@ -1,0 +1,157 @@
+// Shared device helpers for the fastdms_amd HIP library (gfx950, wave64).
+//
+// Storage dtypes are passed across the C-ABI as small integer codes so one
+// entry point serves every K/V / q dtype the reference's kernels accept
+// (its Triton kernels cast implicitly on load/store).  Conversions are done
+// in integer arithmetic so their rounding is fixed by this file, not by a
+// hardware mode: f32->bf16 and f32->fp8 round to nearest-even, fp8 saturates
+// to +-448 (the behaviour of the reference's Triton store casts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fdms {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kFP8 = 3 };
+
+struct bf16_t { uint16_t bits; };
+struct fp8_t { uint8_t bits; };
+typedef _Float16 f16_t;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- fp8 e4m3fn
+__device__ __forceinline__ float fp8_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t em = b & 0x7Fu;
+  float mag;
+  if (em >= 8u) {
+    mag = __uint_as_float((em << 20) + (120u << 23));
+  } else {
+    mag = (float)em * 0.001953125f;  // subnormal: m * 2^-9
+  }
+  uint32_t r = __float_as_uint(mag) | sign;
+  if (em == 0x7Fu) r = 0x7FC00000u | sign;
+  return __uint_as_float(r);
+}
+
+__device__ __forceinline__ uint32_t f32_to_fp8(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;   // NaN
+  if (a >= 0x43E00000u) return sign | 0x7Eu;  // |x| >= 448 (and inf) saturate
+  if (a >= 0x3C800000u) {                     // normal e4m3 range, |x| >= 2^-6
+    uint32_t base = (((a >> 23) - 120u) << 3) | ((a >> 20) & 7u);
+    const uint32_t rem = a & 0xFFFFFu;
+    base += (rem > 0x80000u) || (rem == 0x80000u && (base & 1u));
+    return sign | base;
+  }
+  const float f = __uint_as_float(a) * 512.0f;  // exact power-of-two scale
+  return sign | (uint32_t)__builtin_rintf(f);  // 0..8, half-to-even
+}
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// ---------------------------------------------------------------- typed load/store
+template <typename T> struct Conv;
+template <> struct Conv<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+template <> struct Conv<f16_t> {
+  static __device__ __forceinline__ float load(const f16_t* p) { return (float)*p; }
+  static __device__ __forceinline__ void store(f16_t* p, float v) { *p = (f16_t)v; }
+};
+template <> struct Conv<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p) { return bf16_to_f32(p->bits); }
+  static __device__ __forceinline__ void store(bf16_t* p, float v) { p->bits = (uint16_t)f32_to_bf16(v); }
+};
+template <> struct Conv<fp8_t> {
+  static __device__ __forceinline__ float load(const fp8_t* p) { return fp8_to_f32(p->bits); }
+  static __device__ __forceinline__ void store(fp8_t* p, float v) { p->bits = (uint8_t)f32_to_fp8(v); }
+};
+
+template <typename T> __device__ __forceinline__ float ld(const T* p) { return Conv<T>::load(p); }
+template <typename T> __device__ __forceinline__ void st(T* p, float v) { Conv<T>::store(p, v); }
+
+// Same-type copies keep the bits (a cast fp8->fp8 is the identity).
+template <typename TI, typename TO> struct Copy {
+  static __device__ __forceinline__ void run(TO* d, const TI* s) { st<TO>(d, ld<TI>(s)); }
+};
+template <typename T> struct Copy<T, T> {
+  static __device__ __forceinline__ void run(T* d, const T* s) { *d = *s; }
+};
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// DMS threshold (dms.py:37-40): v > offset/scale (quotient pre-rounded to
+// fp32 on the host) when scale > 0, else v*scale - offset > 0 with each step
+// rounded to fp32.
+__device__ __forceinline__ bool dms_decide(float v, float alpha_scale, float alpha_offset, float threshold,
+                                           int positive_scale) {
+#pragma clang fp contract(off)
+  if (positive_scale) return v > threshold;
+  const float prod = v * alpha_scale;
+  return (prod - alpha_offset) > 0.0f;
+}
+
+// Rotate-half RoPE pair in fp32 with each product and sum rounded separately
+// (rotary_embedding.py:12-14: y1 = x1*cos - x2*sin, y2 = x2*cos + x1*sin).
+__device__ __forceinline__ void rope_f32(float x1, float x2, float c, float s, float* y1, float* y2) {
+#pragma clang fp contract(off)
+  const float a = x1 * c, b = x2 * s, cc = x2 * c, d = x1 * s;
+  *y1 = a - b;
+  *y2 = cc + d;
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
+
+}  // namespace fdms
+
+#define FDMS_LAUNCH_CHECK()                         \
+  do {                                              \
+    hipError_t _e = hipGetLastError();              \
+    if (_e != hipSuccess) return (int)_e;           \
+  } while (0)
+
+#define FDMS_EXPORT extern "C" __attribute__((visibility("default")))
+
+// Dispatch a runtime dtype code to a C++ storage type.
+#define FDMS_DISPATCH_DTYPE(code, T, ...)                     \
+  switch (code) {                                             \
+    case fdms::kF32: { typedef float T; __VA_ARGS__; break; } \
+    case fdms::kF16: { typedef fdms::f16_t T; __VA_ARGS__; break; } \
+    case fdms::kBF16: { typedef fdms::bf16_t T; __VA_ARGS__; break; } \
+    case fdms::kFP8: { typedef fdms::fp8_t T; __VA_ARGS__; break; } \
+    default: return (int)hipErrorInvalidValue;                \
+  }
+
+#define FDMS_DISPATCH_FLOAT(code, T, ...)                     \
+  switch (code) {                                             \
+    case fdms::kF32: { typedef float T; __VA_ARGS__; break; } \
+    case fdms::kF16: { typedef fdms::f16_t T; __VA_ARGS__; break; } \
+    case fdms::kBF16: { typedef fdms::bf16_t T; __VA_ARGS__; break; } \
+    default: return (int)hipErrorInvalidValue;                \
+  }

@@ -1,0 +1,41 @@
+// Vectorised row copy with dtype conversion, shared by the pack / append /
+// expiry kernels.  VEC elements are moved per call; the host picks VEC so
+// that every source and destination address is VEC*sizeof aligned.
+#pragma once
+
+#include "fdms_common.h"
+
+namespace fdms {
+
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Vec {
+  T v[N];
+};
+
+template <typename TI, typename TO, int N>
+__device__ __forceinline__ void copy_vec(TO* __restrict__ dst, const TI* __restrict__ src) {
+  const Vec<TI, N> in = *reinterpret_cast<const Vec<TI, N>*>(src);
+  Vec<TO, N> out;
+#pragma unroll
+  for (int i = 0; i < N; ++i) Copy<TI, TO>::run(&out.v[i], &in.v[i]);
+  *reinterpret_cast<Vec<TO, N>*>(dst) = out;
+}
+
+// Byte-level moves for same-dtype arenas (expiry): N bytes per call.
+template <int N>
+__device__ __forceinline__ void move_bytes(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src) {
+  *reinterpret_cast<Vec<uint8_t, N>*>(dst) = *reinterpret_cast<const Vec<uint8_t, N>*>(src);
+}
+
+}  // namespace fdms
+
+// Dispatch a runtime vector width (elements) to a compile-time constant.
+#define FDMS_DISPATCH_VEC(vec, V, ...)              \
+  switch (vec) {                                    \
+    case 16: { constexpr int V = 16; __VA_ARGS__; break; } \
+    case 8: { constexpr int V = 8; __VA_ARGS__; break; } \
+    case 4: { constexpr int V = 4; __VA_ARGS__; break; } \
+    case 2: { constexpr int V = 2; __VA_ARGS__; break; } \
+    case 1: { constexpr int V = 1; __VA_ARGS__; break; } \
+    default: return (int)hipErrorInvalidValue;      \
+  }

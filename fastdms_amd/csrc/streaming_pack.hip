@@ -1,0 +1,232 @@
+// Streaming prefill pack into compact K/V spans (reference:
+// fastdms/engine/compact_kv.py:38-296 and streaming_pack_layer 915-1099).
+//
+// keep[t,h] = ~evict[t,h] | t >= max(0, len-1-W); rank = exclusive prefix of
+// keep down the token axis; kept rows land at compact[base[b,h] + rank].
+//
+// MI355X layout of the work: one launch covers every sequence of a ragged
+// prefill batch (cu_seqlens), grid = (chunk, seq*head).  A 256-token chunk is
+// ranked with wave ballots (64-bit masks + popcount) and an LDS prefix over
+// the 4 waves; kept rows are listed in LDS and copied cooperatively, VEC
+// elements per lane, so each row moves as whole 16-byte vectors.  HBM-bound:
+// only kept rows are read (2*D*in_bytes per kept token per head) and written
+// (2*D*out_bytes), plus one evict byte per token per head.
+#include "fdms_vec.h"
+
+using namespace fdms;
+
+namespace {
+
+constexpr int kChunk = 256;  // compact_kv.py:276, 318 (chunk the block offsets index)
+
+__device__ __forceinline__ int block_rank(bool keep, int* s_wave, int* total) {
+  const uint64_t m = __ballot(keep);
+  const int lane = __lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int prefix = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) s_wave[wave] = __popcll(m);
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kChunk / kWave; ++w) {
+    const int c = s_wave[w];
+    off += (w < wave) ? c : 0;
+    tot += c;
+  }
+  *total = tot;
+  return off + prefix;
+}
+
+struct SeqSpan {
+  int64_t tok0;  // first token of the sequence in k/v
+  int64_t ev0;   // first token of the sequence in the evict array
+  int len;
+};
+
+__device__ __forceinline__ SeqSpan seq_span(const int32_t* cu, int b, int single_start, int single_len) {
+  SeqSpan s;
+  if (cu) {
+    s.tok0 = cu[b];
+    s.ev0 = cu[b];
+    s.len = cu[b + 1] - cu[b];
+  } else {
+    s.tok0 = single_start;
+    s.ev0 = 0;
+    s.len = single_len;
+  }
+  return s;
+}
+
+}  // namespace
+
+// One block per (seq, head): chunk keep counts -> exclusive chunk offsets and
+// live count (compact_kv.py:140-165 + the torch scan at 294-295).  Optionally
+// resets the (seq, head) metadata row to (-1, False) first (compact_kv.py:1031-1032).
+__global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
+    const uint8_t* __restrict__ evict, int64_t es_t, int64_t es_h, const int32_t* __restrict__ cu,
+    int single_len, int window, int num_kv_heads, int max_chunks, int32_t* __restrict__ live_out, int64_t lo_b,
+    int64_t lo_h, int32_t* __restrict__ offsets, int64_t of_b, int64_t of_h, int64_t of_c,
+    int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta, const int32_t* __restrict__ meta_rows,
+    int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap) {
+  __shared__ int s_wave[kChunk / kWave];
+  const int h = blockIdx.x % num_kv_heads;
+  const int b = blockIdx.x / num_kv_heads;
+  const SeqSpan sp = seq_span(cu, b, 0, single_len);
+  const int thresh = max(0, sp.len - 1 - window);
+  if (positions) {
+    const int64_t row = meta_rows ? meta_rows[b] : b;
+    int32_t* pr = positions + row * tp_b + h * tp_h;
+    uint8_t* er = evict_meta + row * em_b + h * em_h;
+    for (int s = threadIdx.x; s < meta_cap; s += kChunk) {
+      pr[s] = -1;
+      er[s] = 0;
+    }
+  }
+  const int nchunks = (sp.len + kChunk - 1) / kChunk;
+  int running = 0;
+  for (int c = 0; c < max_chunks; ++c) {
+    int total = 0;
+    if (c < nchunks) {
+      const int t = c * kChunk + threadIdx.x;
+      bool keep = false;
+      if (t < sp.len) keep = (evict[(sp.ev0 + t) * es_t + h * es_h] == 0) || (t >= thresh);
+      block_rank(keep, s_wave, &total);
+    }
+    if (threadIdx.x == 0) offsets[b * of_b + h * of_h + c * of_c] = running;
+    running += total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) live_out[b * lo_b + h * lo_h] = running;
+}
+
+template <typename TI, typename TO, int VEC, bool FUSED>
+__global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
+    const TI* __restrict__ k, const TI* __restrict__ v, int64_t ks_t, int64_t ks_h, int64_t vs_t, int64_t vs_h,
+    const uint8_t* __restrict__ evict, int64_t es_t, int64_t es_h, const int32_t* __restrict__ cu, int single_start,
+    int single_len, const int32_t* __restrict__ block_offsets, int64_t bo_b, int64_t bo_h, int64_t bo_c,
+    const uint8_t* __restrict__ keep_in, int64_t kp_t, int64_t kp_h, const int32_t* __restrict__ rank_in,
+    int64_t rk_t, int64_t rk_h, const int32_t* __restrict__ base, int64_t bs_b, int64_t bs_h, TO* __restrict__ ck,
+    TO* __restrict__ cv, int64_t cs_s, int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta,
+    const int32_t* __restrict__ meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s, int64_t em_b, int64_t em_h,
+    int64_t em_s, int window, int num_kv_heads, int head_dim) {
+  __shared__ int s_wave[kChunk / kWave];
+  __shared__ int64_t s_src[kChunk];
+  __shared__ int64_t s_dst[kChunk];
+  const int c = blockIdx.x;
+  const int h = blockIdx.y % num_kv_heads;
+  const int b = blockIdx.y / num_kv_heads;
+  const SeqSpan sp = seq_span(cu, b, single_start, single_len);
+  if (c * kChunk >= sp.len) return;  // uniform per block
+  const int t = c * kChunk + threadIdx.x;
+  const bool valid = t < sp.len;
+  uint8_t e = 0;
+  if (valid) e = evict[(sp.ev0 + t) * es_t + h * es_h];
+  bool keep;
+  if (FUSED) {
+    keep = valid && ((e == 0) || (t >= max(0, sp.len - 1 - window)));
+  } else {
+    keep = valid && keep_in[(int64_t)t * kp_t + h * kp_h] != 0;
+  }
+  int total = 0;
+  const int local = block_rank(keep, s_wave, &total);
+  if (keep) {
+    int64_t rank;
+    if (FUSED) {
+      rank = (int64_t)block_offsets[b * bo_b + h * bo_h + c * bo_c] + local;
+    } else {
+      rank = rank_in[(int64_t)t * rk_t + h * rk_h];
+    }
+    const int64_t row = meta_rows ? meta_rows[b] : b;
+    positions[row * tp_b + h * tp_h + rank * tp_s] = t;
+    evict_meta[row * em_b + h * em_h + rank * em_s] = e;
+    s_src[local] = sp.tok0 + t;
+    s_dst[local] = (int64_t)base[b * bs_b + h * bs_h] + rank;
+  }
+  __syncthreads();
+  const int units = head_dim / VEC;
+  const int n = total * units;
+  for (int u = threadIdx.x; u < n; u += kChunk) {
+    const int r = u / units;
+    const int j = (u - r * units) * VEC;
+    const int64_t src = s_src[r];
+    const int64_t dst = s_dst[r] * cs_s + j;
+    copy_vec<TI, TO, VEC>(ck + dst, k + src * ks_t + h * ks_h + j);
+    copy_vec<TI, TO, VEC>(cv + dst, v + src * vs_t + h * vs_h + j);
+  }
+}
+
+FDMS_EXPORT int fdms_streaming_pack_prepare(const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens,
+                                            int single_len, int num_seqs, int window, int num_kv_heads,
+                                            int max_chunks, int32_t* live_out, int64_t lo_b, int64_t lo_h,
+                                            int32_t* block_offsets, int64_t of_b, int64_t of_h, int64_t of_c,
+                                            int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows,
+                                            int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap,
+                                            void* stream) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || max_chunks < 0) return (int)hipErrorInvalidValue;
+  if (!evict || !live_out || (max_chunks > 0 && !block_offsets)) return (int)hipErrorInvalidValue;
+  if (positions && !evict_meta) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_prepare_kernel, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0, (hipStream_t)stream,
+                     evict, es_t, es_h, cu_seqlens, single_len, window, num_kv_heads, max_chunks, live_out, lo_b,
+                     lo_h, block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
+                     meta_cap);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+template <bool FUSED>
+static int launch_scatter(const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t,
+                          int64_t vs_h, const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu,
+                          int single_start, int single_len, int num_seqs, const int32_t* bo, int64_t bo_b,
+                          int64_t bo_h, int64_t bo_c, const uint8_t* keep, int64_t kp_t, int64_t kp_h,
+                          const int32_t* rank, int64_t rk_t, int64_t rk_h, const int32_t* base, int64_t bs_b,
+                          int64_t bs_h, void* ck, void* cv, int compact_dtype, int64_t cs_s, int32_t* positions,
+                          uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s,
+                          int64_t em_b, int64_t em_h, int64_t em_s, int window, int num_kv_heads, int head_dim,
+                          int max_chunks, int vec, void* stream) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_chunks <= 0) return (int)hipErrorInvalidValue;
+  if (vec <= 0 || head_dim % vec != 0) return (int)hipErrorInvalidValue;
+  if (!k || !v || !evict || !base || !ck || !cv || !positions || !evict_meta) return (int)hipErrorInvalidValue;
+  const dim3 grid(max_chunks, num_seqs * num_kv_heads);
+  FDMS_DISPATCH_DTYPE(kv_dtype, TI,
+    FDMS_DISPATCH_DTYPE(compact_dtype, TO,
+      FDMS_DISPATCH_VEC(vec, V,
+        hipLaunchKernelGGL((pack_scatter_kernel<TI, TO, V, FUSED>), grid, dim3(kChunk), 0, (hipStream_t)stream,
+                           (const TI*)k, (const TI*)v, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
+                           single_len, bo, bo_b, bo_h, bo_c, keep, kp_t, kp_h, rank, rk_t, rk_h, base, bs_b, bs_h,
+                           (TO*)ck, (TO*)cv, cs_s, positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h,
+                           em_s, window, num_kv_heads, head_dim))));
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+FDMS_EXPORT int fdms_streaming_pack_rank_scatter(
+    const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t, int64_t vs_h,
+    const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens, int single_start, int single_len,
+    int num_seqs, const int32_t* block_offsets, int64_t bo_b, int64_t bo_h, int64_t bo_c, const int32_t* base,
+    int64_t bs_b, int64_t bs_h, void* compact_k, void* compact_v, int compact_dtype, int64_t cs_s,
+    int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s,
+    int64_t em_b, int64_t em_h, int64_t em_s, int window, int num_kv_heads, int head_dim, int max_chunks, int vec,
+    void* stream) {
+  if (!block_offsets) return (int)hipErrorInvalidValue;
+  return launch_scatter<true>(k, v, kv_dtype, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu_seqlens, single_start,
+                              single_len, num_seqs, block_offsets, bo_b, bo_h, bo_c, nullptr, 0, 0, nullptr, 0, 0,
+                              base, bs_b, bs_h, compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta,
+                              meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s, window, num_kv_heads, head_dim,
+                              max_chunks, vec, stream);
+}
+
+FDMS_EXPORT int fdms_streaming_pack_scatter(
+    const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t, int64_t vs_h,
+    const uint8_t* keep, int64_t kp_t, int64_t kp_h, const int32_t* rank, int64_t rk_t, int64_t rk_h,
+    const uint8_t* seq_evict, int64_t es_t, int64_t es_h, const int32_t* base, int64_t bs_h, void* compact_k,
+    void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions, int64_t tp_h, int64_t tp_s,
+    uint8_t* evict_meta, int64_t em_h, int64_t em_s, int start, int seq_len, int num_kv_heads, int head_dim, int vec,
+    void* stream) {
+  if (!keep || !rank) return (int)hipErrorInvalidValue;
+  if (seq_len <= 0) return 0;
+  const int max_chunks = (seq_len + kChunk - 1) / kChunk;
+  return launch_scatter<false>(k, v, kv_dtype, ks_t, ks_h, vs_t, vs_h, seq_evict, es_t, es_h, nullptr, start,
+                               seq_len, 1, nullptr, 0, 0, 0, keep, kp_t, kp_h, rank, rk_t, rk_h, base, 0, bs_h,
+                               compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta, nullptr, 0, tp_h,
+                               tp_s, 0, em_h, em_s, 0, num_kv_heads, head_dim, max_chunks, vec, stream);
+}

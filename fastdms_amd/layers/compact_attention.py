@@ -1,0 +1,308 @@
+"""Compact-KV attention and expiry ops (mirror of fastdms/layers/compact_attention.py).
+
+Same public names, arguments and ValueError checks as the reference; every op
+runs one HIP kernel of libfastdms_amd.  Triton tuning knobs of the reference
+(``block_n``, ``grouped``, the split-K / block-N env flags) are accepted and do
+not change the math; the split count is chosen here from the batch shape.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _native as nat
+from ..engine.dms import dms_threshold_args
+
+_TRUTHY = {"1", "true", "yes", "on"}
+_FALSY = {"0", "false", "no", "off"}
+
+
+def _env_on(name: str, default: str) -> bool:
+    return os.environ.get(name, default).strip().lower() not in _FALSY
+
+
+# Env flags of the reference (compact_attention.py:7-64), read at import like
+# the reference.  They select behaviour of the engine glue, not kernel math.
+_COMPACT_DEBUG_CHECKS = os.environ.get("FASTDMS_COMPACT_DEBUG_CHECKS") == "1"
+_COMPACT_ATTN_SPLITK = _env_on("FASTDMS_COMPACT_ATTN_SPLITK", "auto")
+_DMS_FUSED_DECODE_PREPROCESS = _env_on("FASTDMS_DMS_FUSED_DECODE_PREPROCESS", "1")
+_COMPACT_ATTN_INLINE_Q_ROPE = os.environ.get("FASTDMS_COMPACT_ATTN_INLINE_Q_ROPE", "1").strip().lower() in _TRUTHY
+
+
+def compact_attention_splitk_enabled() -> bool:
+    return _COMPACT_ATTN_SPLITK
+
+
+def dms_fused_decode_preprocess_enabled() -> bool:
+    return _DMS_FUSED_DECODE_PREPROCESS
+
+
+def dms_decode_store_transient_k_enabled() -> bool:
+    return os.environ.get("FASTDMS_DMS_DECODE_STORE_TRANSIENT_K", "0").strip().lower() in _TRUTHY
+
+
+def compact_attention_inline_q_rope_enabled() -> bool:
+    return _COMPACT_ATTN_INLINE_Q_ROPE
+
+
+def _next_power_of_2(value: int) -> int:
+    if value < 1:
+        raise ValueError(f"value must be positive, got {value}")
+    return 1 << (value - 1).bit_length()
+
+
+# ---------------------------------------------------------------------------
+# split-K workspace: per device, grown on demand; counters start (and stay) 0
+# ---------------------------------------------------------------------------
+_WORKSPACE: dict[int, list] = {}
+_TARGET_BLOCKS_PER_CU = 4
+_NUM_CUS: dict[int, int] = {}
+
+
+def _num_cus(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _NUM_CUS:
+        _NUM_CUS[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _NUM_CUS[idx]
+
+
+def attention_workspace(device: torch.device, n_floats: int, n_counters: int):
+    """Return (workspace, counters) with at least the requested sizes."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    entry = _WORKSPACE.setdefault(idx, [None, None])
+    if entry[0] is None or entry[0].numel() < n_floats:
+        entry[0] = torch.empty(max(n_floats, 1), device=device, dtype=torch.float32)
+    if entry[1] is None or entry[1].numel() < n_counters:
+        entry[1] = torch.zeros(max(n_counters, 1), device=device, dtype=torch.int32)
+    return entry[0], entry[1]
+
+
+def choose_num_splits(device: torch.device, pairs: int, max_live: int) -> int:
+    """Splits per (seq, kv head): fill the CUs (~4 blocks each) but keep at
+    least ~64 live tokens per split."""
+    target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
+    s = max(1, -(-target // max(1, pairs)))
+    s = min(s, max(1, -(-int(max_live) // 64)))
+    return int(min(s, 1024))
+
+
+def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, live_counts, scale, max_live,
+                      rope_positions=None, rope_cache=None, out=None):
+    batch, num_q_heads, head_dim = q.shape
+    num_kv_heads = live_counts.shape[1]
+    group = num_q_heads // num_kv_heads
+    if out is None:
+        out = torch.empty_like(q)
+    pairs = batch * num_kv_heads
+    splits = choose_num_splits(q.device, pairs, max_live)
+    ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
+    if q.stride(2) != 1 or kv_k.stride(1) != 1 or out.stride(2) != 1:
+        raise ValueError("compact attention needs a contiguous head_dim axis")
+    bt = block_tables
+    nat.call("fdms_compact_decode_attention", q.data_ptr(), nat.dtype_code(q.dtype), q.stride(0), q.stride(1),
+             kv_k.data_ptr(), kv_v.data_ptr(), nat.dtype_code(kv_k.dtype), kv_k.stride(0),
+             nat.ptr(base_offsets), 0 if base_offsets is None else base_offsets.stride(0),
+             0 if base_offsets is None else base_offsets.stride(1),
+             nat.ptr(bt), 0 if bt is None else bt.stride(0), 0 if bt is None else bt.stride(1), int(page_size),
+             live_counts.data_ptr(), live_counts.stride(0), live_counts.stride(1), out.data_ptr(), out.stride(0),
+             out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads, group, head_dim, splits,
+             float(scale), nat.ptr(rope_cache), 0 if rope_cache is None else rope_cache.stride(0),
+             0 if rope_cache is None else rope_cache.stride(2), nat.ptr(rope_positions), nat.stream())
+    return out
+
+
+def compact_decode_attention(q: torch.Tensor, compact_k: torch.Tensor, compact_v: torch.Tensor,
+                             base_offsets: torch.Tensor, live_counts: torch.Tensor, scale: float | None = None,
+                             max_live_count: int | None = None, block_n: int = 128, grouped: bool = True,
+                             q_rope_positions: torch.Tensor | None = None,
+                             q_rope_cos_sin_cache: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention over flat compact K/V spans (compact_attention.py:1116-1336)."""
+    if q.ndim != 3:
+        raise ValueError(f"expected q as [batch, q_heads, head_dim], got {q.shape}")
+    if compact_k.shape != compact_v.shape:
+        raise ValueError(f"compact k/v shape mismatch: {compact_k.shape} != {compact_v.shape}")
+    if compact_k.ndim != 2:
+        raise ValueError(f"expected compact K/V as [total_live, head_dim], got {compact_k.shape}")
+    batch, num_q_heads, head_dim = q.shape
+    if compact_k.shape[1] != head_dim:
+        raise ValueError(f"K/V head_dim {compact_k.shape[1]} does not match q head_dim {head_dim}")
+    if base_offsets.shape != live_counts.shape or base_offsets.ndim != 2:
+        raise ValueError("base_offsets and live_counts must both be [batch, kv_heads]")
+    if base_offsets.shape[0] != batch:
+        raise ValueError(f"metadata batch {base_offsets.shape[0]} does not match q batch {batch}")
+    num_kv_heads = base_offsets.shape[1]
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError(f"q_heads={num_q_heads} must be divisible by kv_heads={num_kv_heads}")
+    nat.require_cuda(q, compact_k, compact_v, base_offsets, live_counts, what="compact_decode_attention")
+    if max_live_count is None:
+        max_live_count = int(live_counts.max().item())
+    if max_live_count <= 0:
+        raise ValueError("compact decode requires at least one live token per active KV head")
+    if _COMPACT_DEBUG_CHECKS and bool(torch.any(live_counts <= 0).item()):
+        raise ValueError("compact decode prototype expects every active KV head to have live_count > 0")
+    if head_dim > 256:
+        raise ValueError(f"head_dim={head_dim} is above the kernel limit")
+    if num_q_heads // num_kv_heads > 8:
+        raise ValueError(f"group_size={num_q_heads // num_kv_heads} is above the grouped kernel limit")
+    compact_k = compact_k.contiguous()
+    compact_v = compact_v.contiguous()
+    base_offsets = base_offsets.to(device=q.device, dtype=torch.int32).contiguous()
+    live_counts = live_counts.to(device=q.device, dtype=torch.int32).contiguous()
+    if scale is None:
+        scale = head_dim ** -0.5
+    inline = q_rope_positions is not None or q_rope_cos_sin_cache is not None
+    if inline:
+        if q_rope_positions is None or q_rope_cos_sin_cache is None:
+            raise ValueError("inline q RoPE requires both positions and cos_sin_cache")
+        if head_dim % 2 != 0:
+            raise ValueError(f"inline q RoPE requires even head_dim, got {head_dim}")
+        if q_rope_positions.shape != (batch,):
+            raise ValueError(f"expected q_rope_positions {(batch,)}, got {tuple(q_rope_positions.shape)}")
+        q_rope_positions = q_rope_positions.to(device=q.device, dtype=torch.int64).contiguous()
+        q_rope_cos_sin_cache = q_rope_cos_sin_cache.to(device=q.device, dtype=torch.float32)
+        if q_rope_cos_sin_cache.ndim != 3 or q_rope_cos_sin_cache.shape[2] != head_dim:
+            raise ValueError(f"expected q_rope_cos_sin_cache [positions, 1, {head_dim}], "
+                             f"got {tuple(q_rope_cos_sin_cache.shape)}")
+    return _attention_launch(q, compact_k, compact_v, base_offsets=base_offsets, block_tables=None, page_size=0,
+                             live_counts=live_counts, scale=scale, max_live=max_live_count,
+                             rope_positions=q_rope_positions if inline else None,
+                             rope_cache=q_rope_cos_sin_cache if inline else None)
+
+
+def compact_decode_attention_paged(q: torch.Tensor, kv_k: torch.Tensor, kv_v: torch.Tensor,
+                                   block_tables: torch.Tensor, live_counts: torch.Tensor, page_size: int,
+                                   scale: float | None = None, max_live_count: int | None = None,
+                                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Same attention over paged compact storage: rank r of (b, h) lives at
+    block_tables[b, h, r // page_size] * page_size + r % page_size.
+    (No reference counterpart: the reference stores flat spans.)"""
+    if q.ndim != 3 or kv_k.ndim != 2 or kv_k.shape != kv_v.shape or kv_k.shape[1] != q.shape[2]:
+        raise ValueError("expected q [B, Hq, D] and paged K/V [slots, D]")
+    if block_tables.ndim != 3 or block_tables.shape[:2] != live_counts.shape:
+        raise ValueError("block_tables must be [batch, kv_heads, max_pages] matching live_counts")
+    if page_size <= 0 or page_size & (page_size - 1):
+        raise ValueError("page_size must be a power of two")
+    nat.require_cuda(q, kv_k, kv_v, block_tables, live_counts, what="compact_decode_attention_paged")
+    if max_live_count is None:
+        max_live_count = int(live_counts.max().item())
+    if scale is None:
+        scale = q.shape[2] ** -0.5
+    block_tables = block_tables.to(dtype=torch.int32)
+    if block_tables.stride(2) != 1:
+        block_tables = block_tables.contiguous()
+    return _attention_launch(q, kv_k, kv_v, base_offsets=None, block_tables=block_tables, page_size=page_size,
+                             live_counts=live_counts.to(dtype=torch.int32), scale=scale, max_live=max_live_count,
+                             out=out)
+
+
+def store_compact_kvcache(key: torch.Tensor, value: torch.Tensor, compact_k: torch.Tensor, compact_v: torch.Tensor,
+                          slot_mapping: torch.Tensor) -> None:
+    """compact[slot] = key/value for slot >= 0 (compact_attention.py:968-1007)."""
+    if key.shape != value.shape:
+        raise ValueError(f"key/value shape mismatch: {key.shape} != {value.shape}")
+    if key.ndim != 3:
+        raise ValueError(f"expected key/value as [batch, kv_heads, head_dim], got {key.shape}")
+    batch, num_kv_heads, head_dim = key.shape
+    if compact_k.shape != compact_v.shape:
+        raise ValueError(f"compact cache shape mismatch: {compact_k.shape} != {compact_v.shape}")
+    if compact_k.ndim != 2 or compact_k.shape[1] != head_dim:
+        raise ValueError(f"expected compact cache [slots, {head_dim}], got {compact_k.shape}")
+    if slot_mapping.shape != (batch, num_kv_heads):
+        raise ValueError(f"expected slot_mapping {(batch, num_kv_heads)}, got {tuple(slot_mapping.shape)}")
+    nat.require_cuda(key, value, compact_k, compact_v, what="store_compact_kvcache")
+    slot_mapping = slot_mapping.to(device=key.device, dtype=torch.int32).contiguous()
+    if key.stride(2) != 1 or value.stride(2) != 1 or compact_k.stride(1) != 1:
+        raise ValueError("store_compact_kvcache needs a contiguous head_dim axis")
+    nat.call("fdms_store_compact_kvcache", key.data_ptr(), value.data_ptr(), nat.dtype_code(key.dtype),
+             key.stride(0), key.stride(1), value.stride(0), value.stride(1), compact_k.data_ptr(),
+             compact_v.data_ptr(), nat.dtype_code(compact_k.dtype), compact_k.stride(0), slot_mapping.data_ptr(),
+             slot_mapping.stride(0), slot_mapping.stride(1), batch, num_kv_heads, head_dim, nat.stream())
+
+
+def fused_dms_rope_store_compact_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                        cos_sin_cache: torch.Tensor, compact_k: torch.Tensor,
+                                        compact_v: torch.Tensor, slot_mapping: torch.Tensor,
+                                        evict_out: torch.Tensor, positions: torch.Tensor, *, num_kv_heads: int,
+                                        alpha_scale: float, alpha_offset: float, store_q: bool = True,
+                                        store_transient_k: bool = True) -> None:
+    """Decode DMS extraction + RoPE + compact append (compact_attention.py:1010-1113)."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("expected q/k/v as [batch, heads, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"k/value shape mismatch: {k.shape} != {v.shape}")
+    batch, num_q_heads, head_dim = q.shape
+    if k.shape[0] != batch or k.shape[1] != num_kv_heads or k.shape[2] != head_dim:
+        raise ValueError(f"q/k shape mismatch: q={q.shape}, k={k.shape}, num_kv_heads={num_kv_heads}")
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError(f"q_heads={num_q_heads} must be divisible by kv_heads={num_kv_heads}")
+    if head_dim % 2 != 0:
+        raise ValueError(f"RoPE head_dim must be even, got {head_dim}")
+    if compact_k.shape != compact_v.shape or compact_k.ndim != 2 or compact_k.shape[1] != head_dim:
+        raise ValueError(f"expected compact cache [slots, {head_dim}], got {compact_k.shape}/{compact_v.shape}")
+    if slot_mapping.shape != (batch, num_kv_heads):
+        raise ValueError(f"expected slot_mapping {(batch, num_kv_heads)}, got {tuple(slot_mapping.shape)}")
+    if evict_out.shape != (batch, num_kv_heads) or evict_out.dtype != torch.bool:
+        raise ValueError(f"expected evict_out bool {(batch, num_kv_heads)}, got {tuple(evict_out.shape)} "
+                         f"{evict_out.dtype}")
+    if positions.shape != (batch,):
+        raise ValueError(f"expected positions {(batch,)}, got {tuple(positions.shape)}")
+    if head_dim > 256:
+        raise ValueError(f"head_dim={head_dim} is above the fused decode preprocess kernel limit")
+    nat.require_cuda(q, k, v, compact_k, positions, what="fused decode preprocess")
+    slot_mapping = slot_mapping.to(device=q.device, dtype=torch.int32)
+    if evict_out.device != q.device:
+        raise ValueError(f"expected evict_out on {q.device}, got {evict_out.device}")
+    positions = positions.to(device=q.device, dtype=torch.int64)
+    cos_sin_cache = cos_sin_cache.to(device=q.device, dtype=torch.float32)
+    if cos_sin_cache.ndim != 3 or cos_sin_cache.shape[2] != head_dim:
+        raise ValueError(f"expected cos_sin_cache [positions, 1, {head_dim}], got {tuple(cos_sin_cache.shape)}")
+    if num_q_heads // num_kv_heads > 8:
+        raise ValueError(f"group_size={num_q_heads // num_kv_heads} is above the fused prototype limit")
+    if q.stride(2) != 1 or k.stride(2) != 1 or v.stride(2) != 1 or compact_k.stride(1) != 1:
+        raise ValueError("fused decode preprocess needs a contiguous head_dim axis")
+    scale, offset, thr, positive = dms_threshold_args(alpha_scale, alpha_offset)
+    nat.call("fdms_dms_rope_store_compact_decode", q.data_ptr(), nat.dtype_code(q.dtype), q.stride(0), q.stride(1),
+             k.data_ptr(), v.data_ptr(), nat.dtype_code(k.dtype), k.stride(0), k.stride(1), v.stride(0),
+             v.stride(1), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.stride(2),
+             compact_k.data_ptr(), compact_v.data_ptr(), nat.dtype_code(compact_k.dtype), compact_k.stride(0),
+             slot_mapping.data_ptr(), slot_mapping.stride(0), slot_mapping.stride(1), evict_out.data_ptr(),
+             evict_out.stride(0), evict_out.stride(1), positions.data_ptr(), batch, num_kv_heads,
+             num_q_heads // num_kv_heads, head_dim, scale, offset, thr, positive, int(bool(store_q)),
+             int(bool(store_transient_k)), nat.stream())
+
+
+def _expiry(incremental: bool, *, positions_per_lh, evict_per_lh, live_counts, base_offsets, compact_k, compact_v,
+            current_positions, window_size):
+    num_seqs, num_kv_heads, max_capacity = positions_per_lh.shape
+    if evict_per_lh.shape != positions_per_lh.shape:
+        raise ValueError("positions_per_lh and evict_per_lh must match")
+    if live_counts.shape != (num_seqs, num_kv_heads) or base_offsets.shape != (num_seqs, num_kv_heads):
+        raise ValueError("live_counts/base_offsets must be [num_seqs, num_kv_heads]")
+    if positions_per_lh.stride(2) != 1 or evict_per_lh.stride(2) != 1:
+        raise ValueError("expiry metadata needs a contiguous slot axis")
+    nat.require_cuda(positions_per_lh, evict_per_lh, live_counts, compact_k, what="dms expiry")
+    cur = current_positions.to(device=positions_per_lh.device, dtype=torch.int64).contiguous()
+    esz = compact_k.element_size()
+    nat.call("fdms_dms_expiry", int(incremental), positions_per_lh.data_ptr(), 0, positions_per_lh.stride(0),
+             positions_per_lh.stride(1), evict_per_lh.data_ptr(), 0, evict_per_lh.stride(0), evict_per_lh.stride(1),
+             live_counts.data_ptr(), 0, live_counts.stride(0), live_counts.stride(1), base_offsets.data_ptr(), 0,
+             base_offsets.stride(0), base_offsets.stride(1), compact_k.data_ptr(), compact_v.data_ptr(), None, None,
+             compact_k.shape[-1] * esz, compact_k.stride(0) * esz, cur.data_ptr(), 1, num_seqs, num_kv_heads,
+             int(window_size), nat.stream())
+
+
+def dms_expiry_one_layer(*, positions_per_lh, evict_per_lh, live_counts, base_offsets, compact_k, compact_v,
+                         current_positions, window_size: int) -> None:
+    """Full per-(seq, head) re-compaction of one layer (compact_attention.py:861-911)."""
+    _expiry(False, positions_per_lh=positions_per_lh, evict_per_lh=evict_per_lh, live_counts=live_counts,
+            base_offsets=base_offsets, compact_k=compact_k, compact_v=compact_v,
+            current_positions=current_positions, window_size=window_size)
+
+
+def dms_expiry_incremental_one_layer(*, positions_per_lh, evict_per_lh, live_counts, base_offsets, compact_k,
+                                     compact_v, current_positions, window_size: int) -> None:
+    """Steady-state single-slot expiry of one layer (compact_attention.py:914-965)."""
+    _expiry(True, positions_per_lh=positions_per_lh, evict_per_lh=evict_per_lh, live_counts=live_counts,
+            base_offsets=base_offsets, compact_k=compact_k, compact_v=compact_v,
+            current_positions=current_positions, window_size=window_size)

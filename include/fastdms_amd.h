@@ -1,0 +1,174 @@
+/*
+ * fastdms_amd C-ABI — MI355X (gfx950) HIP kernels for FastDMS's compact-DMS
+ * inference hot path.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, a hipError_t code otherwise (hipErrorInvalidValue = 1
+ *     for rejected arguments; nothing is launched then);
+ *   - tensors are raw device pointers; strides are in ELEMENTS of the pointed
+ *     type unless the name ends in _bytes; the innermost (head_dim / slot)
+ *     dimension is contiguous;
+ *   - dtype codes: 0 = float32, 1 = float16, 2 = bfloat16, 3 = float8_e4m3fn
+ *     (OCP; stores round to nearest-even and saturate to +-448);
+ *   - bool tensors are uint8_t (0/1);
+ *   - `stream` is a hipStream_t; kernels are enqueued on it and never
+ *     synchronise, allocate or call hipMemset, so every call is capturable in a
+ *     HIP graph.
+ *
+ * Reference citations are path:line in shisa-ai/FastDMS.
+ */
+#ifndef FASTDMS_AMD_H
+#define FASTDMS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header (1). */
+int fdms_abi_version(void);
+
+/* Plain 16-byte-vector copy used to calibrate HBM byte counters and the copy
+ * roofline (no reference counterpart: measurement support). */
+int fdms_copy_bytes(const void* src, void* dst, int64_t nbytes, int num_blocks, void* stream);
+
+/* Element-wise dtype conversion with the library's store rounding (no
+ * reference counterpart: exposes the cast the reference's Triton stores apply,
+ * compact_kv.py:243-252, for exhaustive tests). */
+int fdms_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
+
+/* A1 — DMS decision extraction.  Replaces _extract_dms_eviction_decisions_kernel
+ * and the CUDA branch of extract_dms_eviction_decisions (fastdms/engine/dms.py:12-42,
+ * 196-220).  evict[t,h] = q[t, h*G, D-1] > threshold (positive_scale, threshold =
+ * fp32(alpha_offset/alpha_scale)) or q*alpha_scale - alpha_offset > 0; then
+ * q[t, h*G, D-1] = 0. */
+int fdms_extract_dms_decisions(void* q, int q_dtype, int64_t qs_t, int64_t qs_h, int64_t qs_d, uint8_t* evict,
+                               int64_t es_t, int64_t es_h, int64_t num_tokens, int num_kv_heads, int group_size,
+                               int head_dim, float alpha_scale, float alpha_offset, float threshold,
+                               int positive_scale, void* stream);
+
+/* A4 — prefill pack counts + exclusive chunk scan.  Replaces
+ * _streaming_pack_count_kernel + _streaming_pack_fused_rank_prepare
+ * (fastdms/engine/compact_kv.py:140-165, 265-296).  One call covers a ragged
+ * batch: cu_seqlens [num_seqs+1] (device) or, when NULL, one sequence of
+ * single_len tokens.  Outputs live[b,h] and block_offsets[b,h,chunk] (256-token
+ * chunks).  When positions != NULL the (seq, head) metadata rows are first reset
+ * to (-1, 0) over meta_cap slots (compact_kv.py:1031-1032); meta_rows maps a
+ * batch index to its metadata row (NULL = identity). */
+int fdms_streaming_pack_prepare(const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens,
+                                int single_len, int num_seqs, int window, int num_kv_heads, int max_chunks,
+                                int32_t* live_out, int64_t lo_b, int64_t lo_h, int32_t* block_offsets, int64_t of_b,
+                                int64_t of_h, int64_t of_c, int32_t* positions, uint8_t* evict_meta,
+                                const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h,
+                                int meta_cap, void* stream);
+
+/* A5 — fused rank scatter of kept K/V rows into compact spans.  Replaces
+ * _streaming_pack_rank_scatter_kernel / _streaming_pack_rank_scatter_triton
+ * (compact_kv.py:168-262, 299-361).  compact[base[b,h] + rank] = cast(k/v[t,h]),
+ * positions[row_b,h,rank] = t, evict_meta[row_b,h,rank] = evict[t,h].  Ragged
+ * batch via cu_seqlens as above (k/v indexed at cu[b]+t, or single_start+t). */
+int fdms_streaming_pack_rank_scatter(const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h,
+                                     int64_t vs_t, int64_t vs_h, const uint8_t* evict, int64_t es_t, int64_t es_h,
+                                     const int32_t* cu_seqlens, int single_start, int single_len, int num_seqs,
+                                     const int32_t* block_offsets, int64_t bo_b, int64_t bo_h, int64_t bo_c,
+                                     const int32_t* base, int64_t bs_b, int64_t bs_h, void* compact_k,
+                                     void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions,
+                                     uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h,
+                                     int64_t tp_s, int64_t em_b, int64_t em_h, int64_t em_s, int window,
+                                     int num_kv_heads, int head_dim, int max_chunks, int vec, void* stream);
+
+/* A6 — scatter with precomputed keep/rank.  Replaces _streaming_pack_scatter_kernel
+ * / _streaming_pack_scatter_triton (compact_kv.py:38-137, 364-423). */
+int fdms_streaming_pack_scatter(const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h,
+                                int64_t vs_t, int64_t vs_h, const uint8_t* keep, int64_t kp_t, int64_t kp_h,
+                                const int32_t* rank, int64_t rk_t, int64_t rk_h, const uint8_t* seq_evict,
+                                int64_t es_t, int64_t es_h, const int32_t* base, int64_t bs_h, void* compact_k,
+                                void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions, int64_t tp_h,
+                                int64_t tp_s, uint8_t* evict_meta, int64_t em_h, int64_t em_s, int start,
+                                int seq_len, int num_kv_heads, int head_dim, int vec, void* stream);
+
+/* A9 — fused decode DMS decision + RoPE + compact append.  Replaces
+ * _dms_rope_store_compact_decode_kernel / fused_dms_rope_store_compact_decode
+ * (fastdms/layers/compact_attention.py:67-209, 1010-1113).  cos_sin is the fp32
+ * [max_pos, 1, D] cat(cos, sin) cache; positions are int64. */
+int fdms_dms_rope_store_compact_decode(void* q, int q_dtype, int64_t qs_b, int64_t qs_h, void* k, const void* v,
+                                       int kv_dtype, int64_t ks_b, int64_t ks_h, int64_t vs_b, int64_t vs_h,
+                                       const float* cos_sin, int64_t cs_p, int64_t cs_d, void* compact_k,
+                                       void* compact_v, int compact_dtype, int64_t c_s, const int32_t* slot_mapping,
+                                       int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+                                       const int64_t* positions, int batch, int num_kv_heads, int group_size,
+                                       int head_dim, float alpha_scale, float alpha_offset, float threshold,
+                                       int positive_scale, int store_q, int store_transient_k, void* stream);
+
+/* B8 — prefill RoPE in place on a [tokens, heads, D] view.  Replaces
+ * RotaryEmbedding.forward / apply_rotary_emb (fastdms/layers/rotary_embedding.py:7-15,
+ * 75-86): x = cast(x1*cos - x2*sin, x2*cos + x1*sin) computed in fp32. */
+int fdms_rope_inplace(void* x, int dtype, int64_t xs_t, int64_t xs_h, int64_t num_tokens, int num_heads,
+                      int head_dim, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+                      void* stream);
+
+/* A10 — unfused append store.  Replaces _store_compact_kvcache_kernel /
+ * store_compact_kvcache (compact_attention.py:212-246, 968-1007). */
+int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype, int64_t ks_b, int64_t ks_h,
+                               int64_t vs_b, int64_t vs_h, void* compact_k, void* compact_v, int compact_dtype,
+                               int64_t c_s, const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, int batch,
+                               int num_kv_heads, int head_dim, void* stream);
+
+/* B2/B3/B5 — split-K GQA decode attention over compact spans with the split
+ * merge fused into the same launch.  Replaces compact_decode_attention and its
+ * partial + reduce kernels (compact_attention.py:334-415, 537-603, 1116-1336).
+ * Span addressing: base_offsets[b,h] + r (block_tables == NULL); paged:
+ * block_tables[b,h,r/page_size]*page_size + r%page_size.  workspace holds
+ * batch*num_kv_heads*num_splits*group_size*(head_dim+2) floats and counters
+ * batch*num_kv_heads ints that must be zero before the first call (every call
+ * leaves them zero).  Calls that share counters must not overlap in time.
+ * rope_positions != NULL rotates q in-kernel with the decision lane zeroed
+ * (B4, _compact_decode_grouped_splitk_partial_qrope_kernel, compact_attention.py:418-534). */
+int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int64_t qs_h, const void* compact_k,
+                                  const void* compact_v, int kv_dtype, int64_t c_s, const int32_t* base_offsets,
+                                  int64_t bo_b, int64_t bo_h, const int32_t* block_tables, int64_t bt_b,
+                                  int64_t bt_h, int page_size, const int32_t* live_counts, int64_t lc_b,
+                                  int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace,
+                                  int* counters, int batch, int num_kv_heads, int group_size, int head_dim,
+                                  int num_splits, float scale, const float* rope_cos_sin, int64_t rcs_p,
+                                  int64_t rcs_d, const int64_t* rope_positions, void* stream);
+
+/* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
+ * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /
+ * dms_expiry_incremental_one_layer (compact_attention.py:690-965) and the
+ * per-layer loops of compact_kv.py:1396-1560; semantics of the exact torch path
+ * compact_kv.py:1263-1337.  Metadata is [layer, seq, head, slot] with strides;
+ * arenas come from layer_k/layer_v (device tables of per-layer base addresses)
+ * or, for num_layers == 1, compact_k/compact_v.  Rows move as row_bytes bytes
+ * at a c_s_bytes slot stride.  Slots at or beyond live are expected to hold
+ * (-1, 0) already, as the reference's append/record path leaves them. */
+int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h, uint8_t* evict,
+                    int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts, int64_t lc_l, int64_t lc_s,
+                    int64_t lc_h, const int32_t* base_offsets, int64_t bo_l, int64_t bo_s, int64_t bo_h,
+                    void* compact_k, void* compact_v, const uint64_t* layer_k, const uint64_t* layer_v,
+                    int64_t row_bytes, int64_t c_s_bytes, const int64_t* current_positions, int num_layers,
+                    int num_seqs, int num_kv_heads, int window, void* stream);
+
+/* A15 — decode append slots.  Replaces prepare_decode_metadata
+ * (compact_kv.py:1727-1770): slot_out[l,b,h] = base + live; live += 1. */
+int fdms_prepare_decode_metadata(const int32_t* base, int64_t b_l, int64_t b_b, int64_t b_h, int32_t* live,
+                                 int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out, int num_layers,
+                                 int num_seqs, int num_kv_heads, void* stream);
+
+/* A14 — record the appended token's decision.  Replaces
+ * _record_dms_decisions_layer_major_kernel / record_appended_dms_decisions
+ * (compact_kv.py:426-484, 1562-1725): positions[l,row,h,live-1] = pos[b],
+ * evict[l,row,h,live-1] = evict_all[l,b,h]; row = meta_rows[b] or row_start + b. */
+int fdms_record_dms_decisions(int32_t* positions, int64_t p_l, int64_t p_s, int64_t p_h, int64_t p_c,
+                              uint8_t* evict, int64_t e_l, int64_t e_s, int64_t e_h, int64_t e_c,
+                              const int32_t* live, int64_t l_l, int64_t l_s, int64_t l_h, const uint8_t* evict_all,
+                              int64_t a_l, int64_t a_b, int64_t a_h, const void* cur_positions, int pos_is_64,
+                              const int32_t* meta_rows, int row_start, int num_layers, int num_seqs,
+                              int num_kv_heads, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTDMS_AMD_H */

@@ -1,0 +1,192 @@
+"""B2-B7: compact decode attention on the GPU vs the float64 oracle.
+
+Tolerance: max|out - ref| / max|ref| <= 2e-2 for bf16 q with FP8/bf16 K/V
+(the north-star bound); <= 1e-5 when q and K/V are fp32.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TORCH_DTYPE, from_values, require_gpu, values_of
+from oracle import attention as oatt
+from oracle import numerics
+
+pytestmark = pytest.mark.gpu
+TOL_LOWP = 2e-2
+TOL_F32 = 1e-5
+
+
+def _rel_err(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _force_splits(monkeypatch, n):
+    import fastdms_amd.layers.compact_attention as ca
+    monkeypatch.setattr(ca, "choose_num_splits", lambda device, pairs, max_live: n)
+
+
+@pytest.mark.parametrize("splits", [None, 1, 2, 3, 20])
+def test_reference_splitk_case(monkeypatch, splits):
+    """q [2,8,16], spans at [[0,24],[48,72]] with live [[17,13],[19,11]] (test_compact_kv.py:1244-1280)."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    if splits is not None:
+        _force_splits(monkeypatch, splits)
+    rng = np.random.default_rng(17)
+    q = rng.standard_normal((2, 8, 16)).astype(np.float32)
+    ck = rng.standard_normal((96, 16)).astype(np.float32)
+    cv = rng.standard_normal((96, 16)).astype(np.float32)
+    base = np.array([[0, 24], [48, 72]], np.int32)
+    live = np.array([[17, 13], [19, 11]], np.int32)
+    ref = oatt.compact_decode_attention(q, ck, cv, base, live)
+    out = compact_decode_attention(torch.from_numpy(q).cuda(), torch.from_numpy(ck).cuda(),
+                                   torch.from_numpy(cv).cuda(), torch.from_numpy(base).cuda(),
+                                   torch.from_numpy(live).cuda(), max_live_count=20, block_n=16)
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_F32
+
+
+def _config1_case(rng, b=1, hkv=8, g=4, d=64, ctx=2048, window=256, page=16):
+    """keep = last 256 tokens | Bernoulli(1/8); pages of 16 with a random permutation."""
+    keep = rng.random((b, hkv, ctx)) < 1.0 / 8
+    keep[..., ctx - window:] = True
+    live = keep.sum(-1).astype(np.int32)
+    max_pages = int(-(-live.max() // page))
+    total_pages = b * hkv * max_pages
+    bt = rng.permutation(total_pages).reshape(b, hkv, max_pages).astype(np.int32)
+    kd = numerics.cast(rng.standard_normal((total_pages * page, d)).astype(np.float32), numerics.DT_FP8)
+    vd = numerics.cast(rng.standard_normal((total_pages * page, d)).astype(np.float32), numerics.DT_FP8)
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    return q, kd, vd, bt, live, page
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_config1_paged_fp8_matches_oracle(seed):
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention_paged
+    rng = np.random.default_rng(seed)
+    q, kd, vd, bt, live, page = _config1_case(rng)
+    ref = oatt.compact_decode_attention_paged(q, kd, vd, bt, live, page)
+    out = compact_decode_attention_paged(from_values(q, numerics.DT_BF16), from_values(kd, numerics.DT_FP8),
+                                         from_values(vd, numerics.DT_FP8), torch.from_numpy(bt).cuda(),
+                                         torch.from_numpy(live).cuda(), page, max_live_count=int(live.max()))
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
+
+
+def test_paged_is_invariant_to_page_permutation():
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention_paged
+    rng = np.random.default_rng(3)
+    q, kd, vd, bt, live, page = _config1_case(rng)
+    # move every page to a new physical location, keeping contents
+    total = bt.size
+    perm = rng.permutation(total)
+    kd2 = np.zeros_like(kd)
+    vd2 = np.zeros_like(vd)
+    for old in range(total):
+        kd2[perm[old] * page:(perm[old] + 1) * page] = kd[old * page:(old + 1) * page]
+        vd2[perm[old] * page:(perm[old] + 1) * page] = vd[old * page:(old + 1) * page]
+    bt2 = perm[bt].astype(np.int32)
+    args = dict(page_size=page, max_live_count=int(live.max()))
+    o1 = compact_decode_attention_paged(from_values(q, numerics.DT_BF16), from_values(kd, numerics.DT_FP8),
+                                        from_values(vd, numerics.DT_FP8), torch.from_numpy(bt).cuda(),
+                                        torch.from_numpy(live).cuda(), **args)
+    o2 = compact_decode_attention_paged(from_values(q, numerics.DT_BF16), from_values(kd2, numerics.DT_FP8),
+                                        from_values(vd2, numerics.DT_FP8), torch.from_numpy(bt2).cuda(),
+                                        torch.from_numpy(live).cuda(), **args)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("d,kv_code", [(64, numerics.DT_FP8), (128, numerics.DT_FP8), (64, numerics.DT_BF16),
+                                       (128, numerics.DT_F32)])
+def test_ragged_batch_spans_match_oracle(d, kv_code):
+    """c=8 ragged live counts in flat spans with gaps between them (reference layout)."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    rng = np.random.default_rng(d + kv_code)
+    b, hkv, g = 8, 8, 4
+    live = rng.integers(1, 1400, (b, hkv)).astype(np.int32)
+    live[0, 0] = 1
+    base = np.zeros((b, hkv), np.int32)
+    cur = 0
+    for bi in range(b):
+        for h in range(hkv):
+            base[bi, h] = cur
+            cur += int(live[bi, h]) + int(rng.integers(0, 40))
+    ck = numerics.cast(rng.standard_normal((cur, d)).astype(np.float32), kv_code)
+    cv = numerics.cast(rng.standard_normal((cur, d)).astype(np.float32), kv_code)
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    ref = oatt.compact_decode_attention(q, ck, cv, base, live)
+    out = compact_decode_attention(from_values(q, numerics.DT_BF16), from_values(ck, kv_code),
+                                   from_values(cv, kv_code), torch.from_numpy(base).cuda(),
+                                   torch.from_numpy(live).cuda(), max_live_count=8320)
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
+
+
+def test_split_count_does_not_change_fp32_result(monkeypatch):
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    rng = np.random.default_rng(11)
+    b, hkv, g, d = 2, 4, 2, 32
+    live = np.array([[700, 1, 33, 256], [5, 999, 1000, 64]], np.int32)
+    base = (np.arange(b * hkv).reshape(b, hkv) * 1024).astype(np.int32)
+    ck = rng.standard_normal((b * hkv * 1024, d)).astype(np.float32)
+    cv = rng.standard_normal((b * hkv * 1024, d)).astype(np.float32)
+    q = rng.standard_normal((b, hkv * g, d)).astype(np.float32)
+    ref = oatt.compact_decode_attention(q, ck, cv, base, live)
+    args = [torch.from_numpy(x).cuda() for x in (q, ck, cv, base, live)]
+    for s in (1, 2, 7, 64, 300):
+        _force_splits(monkeypatch, s)
+        out = compact_decode_attention(*args, max_live_count=1000)
+        torch.cuda.synchronize()
+        assert _rel_err(values_of(out), ref) <= TOL_F32, s
+
+
+def test_inline_q_rope_equals_prerotated_q():
+    """B4: rotate q inside attention (decision lane zeroed) == fused preprocess with store_q."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    rng = np.random.default_rng(12)
+    b, hkv, g, d = 1, 8, 4, 64
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    live = rng.integers(10, 500, (b, hkv)).astype(np.int32)
+    base = (np.arange(hkv) * 512).reshape(1, hkv).astype(np.int32)
+    ck = numerics.cast(rng.standard_normal((hkv * 512, d)).astype(np.float32), numerics.DT_FP8)
+    cv = numerics.cast(rng.standard_normal((hkv * 512, d)).astype(np.float32), numerics.DT_FP8)
+    cache = oatt.rope_cos_sin_cache(d, 4096, 500000.0)
+    pos = np.array([3000])
+    # oracle: zero the decision lane, rotate in fp32 (not rounded to bf16), attend
+    qr = q.astype(np.float32).copy()
+    half = d // 2
+    cs = cache[pos[0], 0]
+    for hh in range(hkv * g):
+        x2 = qr[0, hh, half:].copy()
+        if hh % g == 0:
+            x2[half - 1] = 0.0
+        y1, y2 = oatt.rotate(qr[0, hh, :half], x2, cs[:half], cs[half:])
+        qr[0, hh] = np.concatenate([y1, y2])
+    ref = oatt.compact_decode_attention(qr, ck, cv, base, live)
+    out = compact_decode_attention(from_values(q, numerics.DT_BF16), from_values(ck, numerics.DT_FP8),
+                                   from_values(cv, numerics.DT_FP8), torch.from_numpy(base).cuda(),
+                                   torch.from_numpy(live).cuda(), max_live_count=512,
+                                   q_rope_positions=torch.from_numpy(pos).cuda(),
+                                   q_rope_cos_sin_cache=torch.from_numpy(cache).cuda())
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
+
+
+def test_argument_errors():
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    q = torch.zeros((1, 8, 16), device="cuda")
+    kv = torch.zeros((4, 16), device="cuda")
+    meta = torch.zeros((1, 2), device="cuda", dtype=torch.int32)
+    with pytest.raises(ValueError):
+        compact_decode_attention(q, kv, kv, meta, meta, max_live_count=0)
+    with pytest.raises(ValueError):
+        compact_decode_attention(q, kv, torch.zeros((4, 8), device="cuda"), meta, meta, max_live_count=1)
+    with pytest.raises(ValueError):
+        compact_decode_attention(q, kv, kv, meta, meta[:, :1].expand(1, 3), max_live_count=1)

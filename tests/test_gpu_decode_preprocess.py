@@ -1,0 +1,139 @@
+"""A9/A10/B8: fused decode DMS + RoPE + append, unfused append and prefill
+RoPE on the GPU vs the oracle (bit-exact: RoPE is computed with separately
+rounded fp32 products and sums on both sides)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TORCH_DTYPE, from_values, require_gpu, storage_of, values_of
+from oracle import attention as oatt
+from oracle import numerics
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("q_code,cc,store_q,store_k", [
+    (numerics.DT_F32, numerics.DT_F32, True, True),     # the reference test's dtypes
+    (numerics.DT_F32, numerics.DT_F32, True, False),
+    (numerics.DT_F32, numerics.DT_F32, False, True),
+    (numerics.DT_BF16, numerics.DT_FP8, True, False),   # engine dtypes
+])
+def test_fused_preprocess_small_case(q_code, cc, store_q, store_k):
+    """B=3, Hkv=2, G=2, D=32 with hand-set decision values (test_compact_kv.py:973-1120)."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import fused_dms_rope_store_compact_decode
+    rng = np.random.default_rng(19)
+    b, hkv, g, d = 3, 2, 2, 32
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), q_code)
+    k = numerics.cast(rng.standard_normal((b, hkv, d)).astype(np.float32), q_code)
+    v = numerics.cast(rng.standard_normal((b, hkv, d)).astype(np.float32), q_code)
+    q[:, 0::g, -1] = numerics.cast(np.array([[0.01, 0.06], [0.05, 0.08], [0.10, -0.01]], np.float32), q_code)
+    positions = np.array([0, 3, 7])
+    slot = np.array([[0, 3], [6, 9], [12, 15]], np.int32)
+    cache = oatt.rope_cos_sin_cache(d, 16, 10000.0)
+    sd = numerics.storage_dtype(cc)
+    ck, cv = np.zeros((18, d), sd), np.zeros((18, d), sd)
+    qo, ko = q.copy(), k.copy()
+    ev = oatt.fused_dms_rope_store_compact_decode(q=qo, k=ko, v=v, cos_sin_cache=cache, compact_k=ck, compact_v=cv,
+                                                  slot_mapping=slot, positions=positions, num_kv_heads=hkv,
+                                                  alpha_scale=100.0, alpha_offset=5.0, q_dtype_code=q_code,
+                                                  k_dtype_code=q_code, compact_dtype_code=cc, store_q=store_q,
+                                                  store_transient_k=store_k)
+    qd, kd, vd = from_values(q, q_code), from_values(k, q_code), from_values(v, q_code)
+    ckd = torch.zeros((18, d), device="cuda", dtype=TORCH_DTYPE[cc])
+    cvd = torch.zeros_like(ckd)
+    evd = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
+    fused_dms_rope_store_compact_decode(qd, kd, vd, torch.from_numpy(cache).cuda(), ckd, cvd,
+                                        torch.from_numpy(slot).cuda(), evd, torch.from_numpy(positions).cuda(),
+                                        num_kv_heads=hkv, alpha_scale=100.0, alpha_offset=5.0, store_q=store_q,
+                                        store_transient_k=store_k)
+    torch.cuda.synchronize()
+    assert np.array_equal(evd.cpu().numpy(), ev)
+    assert np.array_equal(values_of(qd), qo)
+    assert np.array_equal(values_of(kd), ko)
+    assert np.array_equal(storage_of(ckd), ck) and np.array_equal(storage_of(cvd), cv)
+
+
+def test_fused_preprocess_llama_shape_strided_views():
+    """Llama-3.2-1B decode shape: q/k/v are views of one qkv row (llama.py:92-96), bf16 -> FP8 arena,
+    slot -1 skips the append (compact_attention.py:190)."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import fused_dms_rope_store_compact_decode
+    rng = np.random.default_rng(5)
+    b, hq, hkv, d = 8, 32, 8, 64
+    qkv = numerics.cast(rng.standard_normal((b, (hq + 2 * hkv) * d)).astype(np.float32), numerics.DT_BF16)
+    q = qkv[:, :hq * d].reshape(b, hq, d).copy()
+    k = qkv[:, hq * d:(hq + hkv) * d].reshape(b, hkv, d).copy()
+    v = qkv[:, (hq + hkv) * d:].reshape(b, hkv, d).copy()
+    positions = rng.integers(0, 8192, b)
+    slot = rng.permutation(4 * b * hkv)[:b * hkv].reshape(b, hkv).astype(np.int32)
+    slot[2, 3] = -1
+    cache = oatt.rope_cos_sin_cache(d, 8192, 500000.0)
+    ck = np.zeros((4 * b * hkv, d), np.uint8)
+    cv = np.zeros_like(ck)
+    qo, ko = q.copy(), k.copy()
+    ev = oatt.fused_dms_rope_store_compact_decode(q=qo, k=ko, v=v, cos_sin_cache=cache, compact_k=ck, compact_v=cv,
+                                                  slot_mapping=slot, positions=positions, num_kv_heads=hkv,
+                                                  alpha_scale=10.0, alpha_offset=5.0, q_dtype_code=numerics.DT_BF16,
+                                                  k_dtype_code=numerics.DT_BF16, compact_dtype_code=numerics.DT_FP8,
+                                                  store_q=True, store_transient_k=False)
+    qkv_d = from_values(qkv, numerics.DT_BF16)
+    qd = qkv_d[:, :hq * d].view(b, hq, d)
+    kd = qkv_d[:, hq * d:(hq + hkv) * d].view(b, hkv, d)
+    vd = qkv_d[:, (hq + hkv) * d:].view(b, hkv, d)
+    ckd = torch.zeros((4 * b * hkv, d), device="cuda", dtype=torch.float8_e4m3fn)
+    cvd = torch.zeros_like(ckd)
+    evd = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
+    fused_dms_rope_store_compact_decode(qd, kd, vd, torch.from_numpy(cache).cuda(), ckd, cvd,
+                                        torch.from_numpy(slot).cuda(), evd, torch.from_numpy(positions).cuda(),
+                                        num_kv_heads=hkv, alpha_scale=10.0, alpha_offset=5.0, store_q=True,
+                                        store_transient_k=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(evd.cpu().numpy(), ev)
+    assert np.array_equal(values_of(qd), qo)
+    assert np.array_equal(values_of(kd), k)  # transient k not stored
+    assert np.array_equal(storage_of(ckd), ck) and np.array_equal(storage_of(cvd), cv)
+
+
+def test_store_compact_kvcache_matches_oracle():
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import store_compact_kvcache
+    rng = np.random.default_rng(6)
+    b, hkv, d = 4, 3, 16
+    key = numerics.cast(rng.standard_normal((b, hkv, d)).astype(np.float32), numerics.DT_BF16)
+    val = numerics.cast(rng.standard_normal((b, hkv, d)).astype(np.float32), numerics.DT_BF16)
+    slot = rng.permutation(40)[:b * hkv].reshape(b, hkv).astype(np.int32)
+    slot[0, 0] = -1
+    ck = np.zeros((40, d), np.uint8)
+    cv = np.zeros_like(ck)
+    oatt.store_compact_kvcache(key, val, ck, cv, slot, numerics.DT_FP8)
+    ckd = torch.zeros((40, d), device="cuda", dtype=torch.float8_e4m3fn)
+    cvd = torch.zeros_like(ckd)
+    store_compact_kvcache(from_values(key, numerics.DT_BF16), from_values(val, numerics.DT_BF16), ckd, cvd,
+                          torch.from_numpy(slot).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(storage_of(ckd), ck) and np.array_equal(storage_of(cvd), cv)
+
+
+def test_prefill_rope_matches_apply_rotary_emb():
+    require_gpu()
+    from fastdms_amd.layers.rotary_embedding import get_rope
+    rng = np.random.default_rng(8)
+    t, hq, hkv, d = 300, 32, 8, 64
+    rope = get_rope(d, d, 8192, 500000.0, {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                                          "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
+    cache = rope.cos_sin_cache.numpy()
+    pos = rng.integers(0, 8192, t)
+    q = numerics.cast(rng.standard_normal((t, hq, d)).astype(np.float32), numerics.DT_BF16)
+    k = numerics.cast(rng.standard_normal((t, hkv, d)).astype(np.float32), numerics.DT_BF16)
+    cs = cache[pos]
+    cos, sin = cs[..., :d // 2], cs[..., d // 2:]
+    qe = oatt.apply_rotary_emb(q, cos, sin, numerics.DT_BF16)
+    ke = oatt.apply_rotary_emb(k, cos, sin, numerics.DT_BF16)
+    qd, kd = from_values(q, numerics.DT_BF16), from_values(k, numerics.DT_BF16)
+    dev_cache = rope.cos_sin_cache.cuda()
+    from fastdms_amd.layers.rotary_embedding import rope_inplace
+    rope_inplace(qd, torch.from_numpy(pos).cuda(), dev_cache)
+    rope_inplace(kd, torch.from_numpy(pos).cuda(), dev_cache)
+    torch.cuda.synchronize()
+    assert np.array_equal(values_of(qd), qe) and np.array_equal(values_of(kd), ke)
