@@ -40,6 +40,11 @@ SIGNATURES: dict[str, str] = {
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpiiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",
+    "fdms_argmax_rows": "pillipp",
+    "fdms_mfma_probe": "pppp",
+    "fdms_prefill_attention": "pllpllpllpllpiiiiifp",
+    "fdms_rmsnorm": "pllippplplifp",
+    "fdms_silu_mul": "pplip",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

@@ -1,0 +1,69 @@
+"""Engine configuration (mirror of fastdms/config.py:42-107).
+
+``model`` names a synthetic preset ("llama-3.2-1b", "qwen3-8b", "tiny-llama",
+"tiny-qwen3"), a ``ModelConfig`` or a dict of its fields: this build has no
+checkpoint loader, so weights are seeded random values (``seed``).  The DMS /
+compact-KV fields keep the reference's names and meaning; the compact-DMS path
+is the only KV mode here (``compact_kv_retention_mode == "dms"``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+_KV_CACHE_DTYPES = {"auto": None, "float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32,
+                    "float8_e4m3fn": torch.float8_e4m3fn}
+
+
+@dataclass(slots=True)
+class Config:
+    model: object = "llama-3.2-1b"
+    max_num_batched_tokens: int = 16384
+    max_num_seqs: int = 512
+    max_model_len: int = 4096
+    gpu_memory_utilization: float = 0.9
+    tensor_parallel_size: int = 1
+    enforce_eager: bool = False
+    hf_config: object = None
+    eos: int = -1
+    kvcache_block_size: int = 256
+    kv_cache_dtype: str = "float8_e4m3fn"
+    num_kvcache_blocks: int = 0
+    compact_kv_enabled: bool = True
+    compact_kv_capacity_tokens: int = 0
+    compact_kv_retention_mode: str = "dms"
+    compact_kv_retention_stride: int = 1
+    compact_kv_retention_recent_tokens: int = 0
+    dms_metadata_path: str | None = None
+    dms_window_size: int | None = None
+    dms_alpha_scale: float | None = None
+    dms_alpha_offset: float | None = None
+    num_page_override: int | None = None
+    token_pool_tokens: int | None = None
+    compact_kv_budget_bytes: int | None = None
+    compact_kv_target_live_tokens_per_seq: int | None = None
+    compact_kv_layer_major_metadata: bool = True
+    seed: int = 0
+    dms_survive_fraction: float = 0.125
+    compact_decode_cudagraph: bool = True
+
+    def __post_init__(self):
+        from .models.synthetic import model_config
+        assert self.kvcache_block_size % 256 == 0
+        if self.tensor_parallel_size != 1:
+            raise ValueError("this build runs on one GPU (tensor_parallel_size must be 1)")
+        assert self.kv_cache_dtype in _KV_CACHE_DTYPES, f"kv_cache_dtype must be one of {sorted(_KV_CACHE_DTYPES)}"
+        if not self.compact_kv_enabled or self.compact_kv_retention_mode != "dms":
+            raise ValueError("this build implements the compact-DMS KV path only "
+                             "(compact_kv_enabled=True, compact_kv_retention_mode='dms')")
+        if self.dms_window_size is not None:
+            assert self.dms_window_size >= 0
+        if self.dms_alpha_scale is not None:
+            assert self.dms_alpha_scale != 0.0
+        self.hf_config = model_config(self.model)
+        self.max_model_len = min(self.max_model_len, self.hf_config.max_position_embeddings)
+
+    def resolve_kv_cache_dtype(self) -> torch.dtype:
+        dtype = _KV_CACHE_DTYPES[self.kv_cache_dtype]
+        return torch.bfloat16 if dtype is None else dtype

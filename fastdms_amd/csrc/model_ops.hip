@@ -1,0 +1,193 @@
+// Element-wise model ops around the DMS path, fused so a decode layer issues
+// few launches: residual-add + RMSNorm (reference layernorm.py:16-40) and
+// SiLU(gate) * up (activation.py:8-11).  bf16 in/out, fp32 math; one block
+// per row, 16-byte vector loads.  HBM-bound: 2-3 bf16 reads + 2 writes per
+// element.
+#include "fdms_vec.h"
+
+using namespace fdms;
+
+namespace {
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float* s_red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) t += s_red[i];
+  __syncthreads();
+  return t;
+}
+}  // namespace
+
+// x_out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w), where x = in (+ residual
+// in fp32, and residual_out = bf16(x)) — layernorm.py:19-40.
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restrict__ in, const bf16_t* residual,
+                                                           const bf16_t* __restrict__ weight, bf16_t* __restrict__ out,
+                                                           bf16_t* residual_out, int hidden, int64_t in_stride,
+                                                           int64_t in_head_stride, int heads, int64_t out_stride,
+                                                           float eps) {
+  __shared__ float s_red[kThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const bf16_t* x = in + (row / heads) * in_stride + (row % heads) * in_head_stride;
+  const bf16_t* rs = residual ? residual + row * (int64_t)hidden : nullptr;
+  constexpr int V = 8;
+  constexpr int kMaxPer = 4;  // hidden <= 8192
+  float vals[kMaxPer][V];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = (threadIdx.x + j * kThreads) * V;
+    if (c < hidden) {
+      const Vec<bf16_t, V> xv = *reinterpret_cast<const Vec<bf16_t, V>*>(x + c);
+      Vec<bf16_t, V> rv;
+      if (rs) rv = *reinterpret_cast<const Vec<bf16_t, V>*>(rs + c);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        float f = bf16_to_f32(xv.v[i].bits);
+        if (rs) f += bf16_to_f32(rv.v[i].bits);
+        vals[j][i] = f;
+        ss += f * f;
+      }
+      if (residual_out) {
+        Vec<bf16_t, V> ro;
+#pragma unroll
+        for (int i = 0; i < V; ++i) ro.v[i].bits = (uint16_t)f32_to_bf16(vals[j][i]);
+        *reinterpret_cast<Vec<bf16_t, V>*>(residual_out + row * (int64_t)hidden + c) = ro;
+      }
+    }
+  }
+  const float total = block_sum(ss, s_red);
+  const float inv = 1.0f / sqrtf(total / (float)hidden + eps);
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = (threadIdx.x + j * kThreads) * V;
+    if (c < hidden) {
+      const Vec<bf16_t, V> wv = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + c);
+      Vec<bf16_t, V> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float xn = bf16_to_f32(f32_to_bf16(vals[j][i] * inv));
+        o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv.v[i].bits));
+      }
+      *reinterpret_cast<Vec<bf16_t, V>*>(out + row * out_stride + c) = o;
+    }
+  }
+}
+
+// Row r of the input is at in + (r / heads) * in_stride + (r % heads) * in_head_stride
+// (heads = 1 for plain rows; heads > 1 normalises every head of a strided
+// [tokens, heads, head_dim] view, as Qwen3's q_norm / k_norm do).  Output row r
+// is at out + r * out_stride; residual / residual_out are contiguous rows.
+FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int heads,
+                             const void* residual, const void* weight, void* out, int64_t out_stride,
+                             void* residual_out, int64_t rows, int hidden, float eps, void* stream) {
+  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 8 * kThreads * 4 || heads <= 0) return (int)hipErrorInvalidValue;
+  if (heads > 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!in || !weight || !out || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,
+                     (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// out[r, j] = bf16(silu(x[r, j]) * x[r, F + j]) in fp32 (activation.py:8-11).
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const bf16_t* __restrict__ x, bf16_t* __restrict__ out,
+                                                            int64_t rows, int f) {
+  constexpr int V = 8;
+  const int64_t per_row = f / V;
+  const int64_t total = rows * per_row;
+  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < total; u += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = u / per_row;
+    const int64_t c = (u - r * per_row) * V;
+    const Vec<bf16_t, V> g = *reinterpret_cast<const Vec<bf16_t, V>*>(x + r * 2 * f + c);
+    const Vec<bf16_t, V> up = *reinterpret_cast<const Vec<bf16_t, V>*>(x + r * 2 * f + f + c);
+    Vec<bf16_t, V> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float a = bf16_to_f32(g.v[i].bits);
+      const float s = a / (1.0f + expf(-a));
+      o.v[i].bits = (uint16_t)f32_to_bf16(s * bf16_to_f32(up.v[i].bits));
+    }
+    *reinterpret_cast<Vec<bf16_t, V>*>(out + r * f + c) = o;
+  }
+}
+
+FDMS_EXPORT int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream) {
+  if (rows < 0 || f <= 0 || f % 8) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!x || !out) return (int)hipErrorInvalidValue;
+  const int64_t units = rows * (f / 8);
+  const int64_t want = (units + kThreads - 1) / kThreads;
+  const int64_t blocks = want < 4096 ? want : 4096;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const bf16_t*)x, (bf16_t*)out, rows, f);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Row argmax with ties to the lowest index (embed_head.py:142, 160).
+// One block per row; fp32 or bf16 logits; int64 output.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t stride, int n,
+                                                               int64_t* __restrict__ out) {
+  __shared__ float s_v[kThreads / kWave];
+  __shared__ int s_i[kThreads / kWave];
+  const T* row = x + (int64_t)blockIdx.x * stride;
+  float best = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int j = threadIdx.x; j < n; j += kThreads) {
+    const float v = ld<T>(row + j);
+    if (v > best) {  // strided scan visits indices in increasing order per thread
+      best = v;
+      bi = j;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v[w] = best;
+    s_i[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kThreads / kWave; ++i) {
+      if (s_v[i] > best || (s_v[i] == best && s_i[i] < bi)) {
+        best = s_v[i];
+        bi = s_i[i];
+      }
+    }
+    out[blockIdx.x] = bi;
+  }
+}
+
+FDMS_EXPORT int fdms_argmax_rows(const void* x, int dtype, int64_t stride, int64_t rows, int n, int64_t* out,
+                                 void* stream) {
+  if (rows < 0 || n <= 0 || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!x || !out) return (int)hipErrorInvalidValue;
+  if (dtype == kF32) {
+    hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                       (const float*)x, stride, n, out);
+  } else if (dtype == kBF16) {
+    hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, stride, n, out);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}

@@ -1,0 +1,244 @@
+// Dense causal prefill attention over a ragged batch (the reference calls
+// flash_attn_varlen_func(q, k, v, cu_seqlens, causal=True), attention.py:85-92:
+// evictions act only at pack time, so prefill attends to the full prompt).
+//
+// bf16 in/out, fp32 softmax, GQA.  One workgroup = 64 query rows of one query
+// head (4 waves x 16 rows); key/value blocks of 64 tokens are staged in LDS
+// (K row-major, V transposed) and shared by the 4 waves.  Per wave:
+//   S^T (keys x queries) = K . Q^T   with v_mfma_f32_16x16x32_bf16
+//   online softmax in the log2 domain (row max across 4 lane groups)
+//   O (queries x d) += P . V         with v_mfma_f32_16x16x32_bf16
+// MFMA 16x16x32 bf16 operand layout (lane l, 8 values each):
+//   A[row = l%16][k = 8*(l/16) + i],  B[k = 8*(l/16) + i][col = l%16],
+//   C[row = 4*(l/16) + r][col = l%16], r = 0..3.
+// S^T's C layout gives lane l the scores of query l%16 for keys
+// 16t + 4*(l/16) + r, which is directly the A operand of P.V once the key
+// order inside each 32-key MFMA step is permuted the same way for V.
+#include "fdms_common.h"
+
+using namespace fdms;
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kQRows = 64;   // query rows per workgroup
+constexpr int kKeys = 64;    // keys per LDS block
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return f32_to_bf16(a) | (f32_to_bf16(b) << 16);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
+    int64_t ks_h, const bf16_t* __restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t* __restrict__ out, int64_t os_t,
+    int64_t os_h, const int32_t* __restrict__ cu_seqlens, int group, float scale_log2) {
+  constexpr int KPAD = D + 8;       // sK row stride (bf16)
+  constexpr int VPAD = kKeys + 8;   // sVt row stride (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t sK[kKeys * KPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VPAD];
+
+  const int seq = blockIdx.z;
+  const int qh = blockIdx.y;
+  const int kvh = qh / group;
+  const int start = cu_seqlens[seq];
+  const int len = cu_seqlens[seq + 1] - start;
+  const int nqb = (len + kQRows - 1) / kQRows;
+  if ((int)blockIdx.x >= nqb) return;
+  const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest (diagonal-last) blocks first
+  const int q0 = qb * kQRows;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lg = lane >> 4;   // lane group 0..3
+  const int lc = lane & 15;   // lane column 0..15
+  const int my_q = q0 + wave * 16 + lc;  // query row this lane's S^T column belongs to
+
+  // Q^T as the B operand of S^T = K.Q^T: lane holds Q[my_q][32j + 8*lg + i]
+  bf16x8 qop[D / 32];
+  {
+    const int qrow = min(my_q, len - 1);
+    const bf16_t* qp = q + (int64_t)(start + qrow) * qs_t + (int64_t)qh * qs_h;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) qop[j] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 * j + 8 * lg));
+  }
+
+  float m_run = -INFINITY;  // running max of query my_q (same in the 4 lane groups)
+  float l_part = 0.0f;      // this lane's partial softmax denominator
+  f32x4 o[D / 16];          // O[q = 4*lg + r][d = 16c + lc] of this wave's 16 rows
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nkb = min((len + kKeys - 1) / kKeys, qb + 1);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * kKeys;
+    __syncthreads();
+    // stage K (row-major) and V (transposed) for keys k0..k0+63; zero beyond len
+    for (int u = tid; u < kKeys * D / 8; u += kThreads) {
+      const int key = u / (D / 8);
+      const int d0 = (u - key * (D / 8)) * 8;
+      uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+      if (k0 + key < len) {
+        kv = *reinterpret_cast<const uint4*>(k + (int64_t)(start + k0 + key) * ks_t + (int64_t)kvh * ks_h + d0);
+        vv = *reinterpret_cast<const uint4*>(v + (int64_t)(start + k0 + key) * vs_t + (int64_t)kvh * vs_h + d0);
+      }
+      *reinterpret_cast<uint4*>(&sK[key * KPAD + d0]) = kv;
+      const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sVt[(d0 + i) * VPAD + key] = vh[i];
+    }
+    __syncthreads();
+
+    // S^T for the 4 key tiles of 16: lane gets keys 16t + 4*lg + r for query my_q
+    float s[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&sK[(16 * t + lc) * KPAD + 32 * j + 8 * lg]));
+        acc = mfma16x16x32(a, qop[j], acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * t + 4 * lg + r;
+        const bool ok = key <= my_q && key < len;
+        s[t][r] = ok ? acc[r] * scale_log2 : -INFINITY;
+      }
+    }
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, s[t][r]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float m_new = fmaxf(m_run, bmax);
+    const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = (s[t][r] == -INFINITY) ? 0.0f : exp2f(s[t][r] - m_new);
+        s[t][r] = p;
+        psum += p;
+      }
+    l_part = l_part * alpha + psum;
+    // rescale O rows q = 4*lg + r by alpha of that query (held by lane 4*lg + r)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * lg + r);
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) o[c][r] *= ar;
+    }
+    // O += P.V over two 32-key steps; k index i of lane group lg = key 32*st + 16*(i/4) + 4*lg + i%4
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      uint4 pa;
+      pa.x = pack_bf16x2(s[2 * st][0], s[2 * st][1]);
+      pa.y = pack_bf16x2(s[2 * st][2], s[2 * st][3]);
+      pa.z = pack_bf16x2(s[2 * st + 1][0], s[2 * st + 1][1]);
+      pa.w = pack_bf16x2(s[2 * st + 1][2], s[2 * st + 1][3]);
+      const bf16x8 a = as_bf16x8(pa);
+      const int key_a = 32 * st + 4 * lg;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const uint16_t* vr = &sVt[(16 * c + lc) * VPAD];
+        uint4 b;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr + key_a);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + key_a + 16);
+        b.x = lo.x;
+        b.y = lo.y;
+        b.z = hi.x;
+        b.w = hi.y;
+        o[c] = mfma16x16x32(a, as_bf16x8(b), o[c]);
+      }
+    }
+  }
+
+  float l_tot = l_part;
+  l_tot += __shfl_xor(l_tot, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float inv = 1.0f / __shfl(l_tot, 4 * lg + r);
+    const int row = q0 + wave * 16 + 4 * lg + r;
+    if (row < len) {
+      bf16_t* op = out + (int64_t)(start + row) * os_t + (int64_t)qh * os_h;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) op[16 * c + lc].bits = (uint16_t)f32_to_bf16(o[c][r] * inv);
+    }
+  }
+}
+
+FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t,
+                                       int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h, void* out,
+                                       int64_t os_t, int64_t os_h, const int32_t* cu_seqlens, int num_seqs,
+                                       int max_seqlen, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                                       void* stream) {
+  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return (int)hipErrorInvalidValue;
+  if (num_seqs == 0 || max_seqlen <= 0) return 0;
+  if (!q || !k || !v || !out || !cu_seqlens) return (int)hipErrorInvalidValue;
+  if (num_seqs > 65535 || num_q_heads > 65535) return (int)hipErrorInvalidValue;
+  const dim3 grid((max_seqlen + kQRows - 1) / kQRows, num_q_heads, num_seqs);
+  const float sl2 = scale * 1.4426950408889634f;
+  const int group = num_q_heads / num_kv_heads;
+  if (head_dim == 64) {
+    hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)q, qs_t,
+                       qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h, (bf16_t*)out, os_t, os_h,
+                       cu_seqlens, group, sl2);
+  } else if (head_dim == 128) {
+    hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)q,
+                       qs_t, qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h, (bf16_t*)out, os_t,
+                       os_h, cu_seqlens, group, sl2);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// One v_mfma_f32_16x16x32_bf16 of a 16x32 A and a 32x16 B (row-major bf16)
+// loaded with the operand layout the kernels above assume; C row-major fp32.
+// Exists so a test can confirm that layout against a host matmul.
+__global__ void mfma_probe_kernel(const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, float* __restrict__ c) {
+  const int l = threadIdx.x;
+  uint16_t av[8], bv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    av[i] = a[(l % 16) * 32 + 8 * (l / 16) + i].bits;
+    bv[i] = b[(8 * (l / 16) + i) * 16 + (l % 16)].bits;
+  }
+  uint4 ua, ub;
+  __builtin_memcpy(&ua, av, 16);
+  __builtin_memcpy(&ub, bv, 16);
+  const f32x4 r = mfma16x16x32(as_bf16x8(ua), as_bf16x8(ub), f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[(4 * (l / 16) + i) * 16 + (l % 16)] = r[i];
+}
+
+FDMS_EXPORT int fdms_mfma_probe(const void* a, const void* b, float* c, void* stream) {
+  if (!a || !b || !c) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (const bf16_t*)a,
+                     (const bf16_t*)b, c);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}

@@ -1,0 +1,233 @@
+"""Model runner for the compact-DMS path (mirror of fastdms/engine/model_runner.py,
+single GPU).
+
+Prefill (eager): token batch -> per layer DMS capture, RoPE, streaming pack of
+the prompt into compact FP8 spans, dense causal attention -> greedy token of
+each sequence's last position.
+
+Decode: the host decides the expiry action (the reference's policy, which
+depends only on positions the host knows) and launches it; the rest of the
+step — append-slot preparation, the whole forward, LM head + argmax and
+recording of the appended tokens' DMS decisions — is captured once per batch
+composition as a HIP graph and replayed, so a step costs one graph launch
+and one device->host copy of the token ids.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native as nat
+from ..config import Config
+from ..models.synthetic import build_synthetic_model
+from ..utils.context import get_context, reset_context, set_context
+from .compact_kv import CompactKVManager
+from .dms import DMSMetadata, load_dms_metadata
+from .sequence import Sequence
+
+
+class ModelRunner:
+
+    def __init__(self, config: Config, device: str | torch.device = "cuda"):
+        self.config = config
+        hf = config.hf_config
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("ModelRunner needs a HIP device")
+        torch.cuda.set_device(self.device)
+        self.model = build_synthetic_model(hf, seed=config.seed, device=self.device,
+                                           survive_fraction=config.dms_survive_fraction)
+        self.dms_metadata = self._dms_metadata()
+        self.num_layers = hf.num_hidden_layers
+        self.num_kv_heads = hf.num_key_value_heads
+        self.head_dim = hf.head_dim
+        self.kv_dtype = config.resolve_kv_cache_dtype()
+        self.max_num_seqs = config.max_num_seqs
+        self.allocate_kv_cache()
+        self.evict_buffer = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads),
+                                        device=self.device, dtype=torch.bool)
+        self.static_input_ids = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        self.static_positions = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        self.static_slot = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads), device=self.device,
+                                       dtype=torch.int32)
+        self.static_tokens = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        self.pinned_ids = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
+        self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
+        self.graphs: dict[tuple, tuple] = {}
+        self.graph_pool = None
+        self._warm: set = set()
+        self.last_compact_prefill_stats: dict = {}
+        self.last_dms_decode_stats: list = []
+        self.compact_live_tokens_peak = 0
+
+    # -- setup -----------------------------------------------------------------
+    def _dms_metadata(self) -> DMSMetadata:
+        """Config overrides on top of the loaded/default metadata (model_runner.py:133-146)."""
+        c = self.config
+        if c.dms_metadata_path:
+            base = load_dms_metadata(".", c.dms_metadata_path)
+        else:
+            base = DMSMetadata(model_path=str(c.model), source_path="", source_kind="synthetic_defaults",
+                               packaged_metadata_found=False, window_size=256, alpha_scale=100.0, alpha_offset=5.0)
+        return DMSMetadata(model_path=base.model_path, source_path=base.source_path, source_kind=base.source_kind,
+                           packaged_metadata_found=base.packaged_metadata_found,
+                           window_size=c.dms_window_size if c.dms_window_size is not None else base.window_size,
+                           alpha_scale=c.dms_alpha_scale if c.dms_alpha_scale is not None else base.alpha_scale,
+                           alpha_offset=c.dms_alpha_offset if c.dms_alpha_offset is not None else base.alpha_offset,
+                           target_cr=base.target_cr, context_len=base.context_len,
+                           compression_mode=base.compression_mode)
+
+    def allocate_kv_cache(self) -> None:
+        """Per-layer compact arenas, allocated up front so their addresses never
+        change (captured decode graphs stay valid).  Capacity per layer:
+        compact_kv_capacity_tokens, else compact_kv_budget_bytes, else the
+        worst case max_num_seqs * kv_heads * max_model_len."""
+        c = self.config
+        itemsize = torch.empty((), dtype=self.kv_dtype).element_size()
+        if c.compact_kv_capacity_tokens > 0:
+            cap = int(c.compact_kv_capacity_tokens)
+        elif c.compact_kv_budget_bytes is not None:
+            cap = int(c.compact_kv_budget_bytes) // (2 * self.num_layers * self.head_dim * itemsize)
+        else:
+            cap = self.max_num_seqs * self.num_kv_heads * c.max_model_len
+        if cap <= 0:
+            raise ValueError("compact KV capacity must be positive")
+        self.compact_kv_manager = CompactKVManager(
+            num_layers=self.num_layers, num_kv_heads=self.num_kv_heads, capacity_tokens=cap,
+            max_model_len=c.max_model_len, device=self.device,
+            target_live_tokens_per_seq=c.compact_kv_target_live_tokens_per_seq, head_dim=self.head_dim,
+            compact_dtype=self.kv_dtype, per_layer_storage=True, layer_major_metadata=True,
+            max_active_seqs=self.max_num_seqs, preallocate=True)
+        attn_modules = []
+        for layer_id, layer in enumerate(self.model.model.layers):
+            layer.self_attn.attn.layer_id = layer_id
+            attn_modules.append(layer.self_attn.attn)
+        self.compact_kv_manager.attach_attention_modules(attn_modules)
+
+    # -- prefill -----------------------------------------------------------------
+    def prepare_prefill(self, seqs: list[Sequence]):
+        input_ids, positions, cu = [], [], [0]
+        max_q = 0
+        for seq in seqs:
+            n = len(seq)
+            start = min(seq.num_cached_tokens, n - 1)
+            nq = seq.num_scheduled_tokens
+            input_ids.extend(seq[start:start + nq])
+            positions.extend(range(start, start + nq))
+            cu.append(cu[-1] + nq)
+            max_q = max(max_q, nq)
+        ids_t = torch.tensor(input_ids, dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
+        pos_t = torch.tensor(positions, dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
+        cu_t = torch.tensor(cu, dtype=torch.int32, pin_memory=True).to(self.device, non_blocking=True)
+        pack_ids = []
+        for seq in seqs:
+            if min(seq.num_cached_tokens + seq.num_scheduled_tokens, seq.num_tokens) < seq.num_tokens:
+                raise NotImplementedError("chunked DMS prefill is not supported (the reference packs only "
+                                          "completed prompts, model_runner.py:652-659)")
+            self.compact_kv_manager.allocate(seq)
+            pack_ids.append(seq.seq_id)
+        md = self.dms_metadata
+        set_context(True, cu_t, cu_t, max_q, max_q, dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale,
+                    dms_alpha_offset=md.alpha_offset, dms_layer_evictions={},
+                    streaming_pack_manager=self.compact_kv_manager, streaming_pack_seq_ids=pack_ids,
+                    streaming_pack_window_size=md.window_size, cu_seqlens_q_host=cu)
+        return ids_t, pos_t
+
+    @torch.inference_mode()
+    def run_prefill(self, seqs: list[Sequence]) -> list[int]:
+        ids, pos = self.prepare_prefill(seqs)
+        hidden = self.model(ids, pos)
+        tokens = self.model.compute_greedy_token_ids(hidden)
+        ctx = get_context()
+        total = sum(e.numel() for e in ctx.dms_layer_evictions.values())
+        true = sum(e.sum() for e in ctx.dms_layer_evictions.values())
+        reset_context()
+        out = tokens.tolist()
+        self.last_compact_prefill_stats = {"eviction_decisions_total": total,
+                                           "eviction_decisions_true": int(true) if total else 0}
+        return out
+
+    # -- decode ------------------------------------------------------------------
+    def _decode_body(self, start: int, batch: int, max_live_hint: int) -> None:
+        """One decode step on static buffers; captured into a graph."""
+        mgr = self.compact_kv_manager
+        L, H = self.num_layers, self.num_kv_heads
+        base = mgr.layer_major_base_offsets[:, start:start + batch]
+        live = mgr.layer_major_live_counts[:, start:start + batch]
+        slot = self.static_slot[:, :batch]
+        nat.call("fdms_prepare_decode_metadata", base.data_ptr(), base.stride(0), base.stride(1), base.stride(2),
+                 live.data_ptr(), live.stride(0), live.stride(1), live.stride(2), slot.data_ptr(), L, batch, H,
+                 nat.stream())
+        md = self.dms_metadata
+        evict = self.evict_buffer[:, :batch]
+        set_context(False, compact_kv_enabled=True, compact_base_offsets=base, compact_live_counts=live,
+                    compact_slot_mapping=slot, compact_max_live_count=max_live_hint, dms_capture_enabled=True,
+                    dms_alpha_scale=md.alpha_scale, dms_alpha_offset=md.alpha_offset,
+                    dms_layer_evictions_buffer=evict)
+        ids = self.static_input_ids[:batch]
+        pos = self.static_positions[:batch]
+        hidden = self.model(ids, pos)
+        head = self.model.lm_head
+        logits = head.quant(hidden, None) if head.quant is not None else torch.nn.functional.linear(hidden, head.weight)
+        nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0), batch,
+                 logits.shape[1], self.static_tokens.data_ptr(), nat.stream())
+        p, e = mgr.layer_major_token_positions, mgr.layer_major_evict_mask.view(torch.uint8)
+        ev = evict.view(torch.uint8)
+        nat.call("fdms_record_dms_decisions", p.data_ptr(), p.stride(0), p.stride(1), p.stride(2), p.stride(3),
+                 e.data_ptr(), e.stride(0), e.stride(1), e.stride(2), e.stride(3), mgr.layer_major_live_counts.data_ptr(),
+                 *mgr.layer_major_live_counts.stride(), ev.data_ptr(), ev.stride(0), ev.stride(1), ev.stride(2),
+                 pos.data_ptr(), 1, None, start, L, batch, H, nat.stream())
+        reset_context()
+
+    @torch.inference_mode()
+    def run_decode(self, seqs: list[Sequence]) -> list[int]:
+        mgr = self.compact_kv_manager
+        batch = len(seqs)
+        positions = [len(seq) - 1 for seq in seqs]
+        stats = mgr.apply_dms_evictions(seqs, positions, window_size=self.dms_metadata.window_size, sync_stats=False)
+        self.last_dms_decode_stats = [dict(stats, phase="expire")]
+        states = [mgr.seq_states[s.seq_id] for s in seqs]
+        start = mgr._contiguous_active_slot_start(states)
+        if start is None:
+            raise RuntimeError("decode batch must occupy contiguous active slots")
+        for st in states:
+            st.live_upper_bound += 1
+        hint = mgr.max_live_upper_bound(seqs)
+        for i, seq in enumerate(seqs):
+            self.pinned_ids[i] = seq.last_token
+            self.pinned_pos[i] = positions[i]
+        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+        self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
+        use_graph = self.config.compact_decode_cudagraph and not self.config.enforce_eager
+        key = (start, batch)
+        if use_graph and key not in self._warm:
+            self._warm.add(key)  # first step of a shape runs eagerly: library GEMMs pick kernels outside capture
+            use_graph = False
+        if use_graph:
+            entry = self.graphs.get(key)
+            if entry is not None and (entry[1] != mgr.storage_version or hint > entry[2]):
+                entry = None
+            if entry is None:
+                cap_hint = hint + 256
+                graph = torch.cuda.CUDAGraph()
+                torch.cuda.synchronize()
+                with torch.cuda.graph(graph, pool=self.graph_pool):
+                    self._decode_body(start, batch, cap_hint)
+                self.graph_pool = graph.pool()
+                entry = (graph, mgr.storage_version, cap_hint)
+                self.graphs[key] = entry
+            entry[0].replay()
+        else:
+            self._decode_body(start, batch, hint)
+        self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, hint)
+        return self.static_tokens[:batch].tolist()
+
+    def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
+        return self.run_prefill(seqs) if is_prefill else self.run_decode(seqs)
+
+    def free_compact(self, seq_ids: list[int]) -> None:
+        for sid in seq_ids:
+            self.compact_kv_manager.free(sid)
+
+    def exit(self) -> None:
+        self.graphs.clear()
+        self.graph_pool = None

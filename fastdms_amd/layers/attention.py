@@ -1,0 +1,70 @@
+"""Attention dispatch (mirror of fastdms/layers/attention.py:50-151).
+
+Prefill: dense causal attention over the whole prompt (HIP MFMA kernel
+``fdms_prefill_attention``; the reference uses flash_attn_varlen_func).
+Decode with compact KV: per-layer slice of the [layers, batch, kv_heads]
+metadata, optional unfused append, then ``compact_decode_attention``.
+The dense paged decode path of the reference is not part of this build.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import _native as nat
+from ..utils.context import get_context
+from .compact_attention import compact_decode_attention, store_compact_kvcache
+
+
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                      max_seqlen: int, scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal varlen attention: q [T, Hq, D], k/v [T, Hkv, D] bf16 -> [T, Hq, D]."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("prefill attention expects bf16 q/k/v")
+    t, hq, d = q.shape
+    hkv = k.shape[1]
+    if d not in (64, 128):
+        raise ValueError(f"prefill attention supports head_dim 64 or 128, got {d}")
+    for x in (q, k, v):
+        if x.stride(2) != 1 or (x.stride(0) * 2) % 16 or (x.stride(1) * 2) % 16 or x.data_ptr() % 16:
+            raise ValueError("prefill attention needs 16-byte aligned rows with a contiguous head_dim")
+    if out is None:
+        out = torch.empty((t, hq, d), device=q.device, dtype=q.dtype)
+    cu = cu_seqlens.to(torch.int32)
+    nat.call("fdms_prefill_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+             k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+             cu.data_ptr(), cu.numel() - 1, int(max_seqlen), hq, hkv, d, float(scale), nat.stream())
+    return out
+
+
+class Attention(nn.Module):
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.compact_k_cache = self.compact_v_cache = torch.tensor([])
+        self.layer_id = -1
+
+    def forward(self, q, k, v, *, compact_append_stored: bool = False, compact_q_rope: bool = False,
+                positions: torch.Tensor | None = None, cos_sin_cache: torch.Tensor | None = None, out=None):
+        ctx = get_context()
+        if ctx.is_prefill:
+            return prefill_attention(q, k, v, ctx.cu_seqlens_q, ctx.max_seqlen_q, self.scale, out=out)
+        if not ctx.compact_kv_enabled:
+            raise RuntimeError("dense paged decode is not part of this build; enable compact KV")
+        if ctx.compact_base_offsets is None or ctx.compact_live_counts is None:
+            raise RuntimeError("compact KV decode requires compact_base_offsets and compact_live_counts")
+        base, live, slot = ctx.compact_base_offsets, ctx.compact_live_counts, ctx.compact_slot_mapping
+        if base.ndim == 3:
+            base, live = base[self.layer_id], live[self.layer_id]
+            slot = None if slot is None else slot[self.layer_id]
+        if slot is not None and not compact_append_stored:
+            store_compact_kvcache(k, v, self.compact_k_cache, self.compact_v_cache, slot)
+        return compact_decode_attention(q, self.compact_k_cache, self.compact_v_cache, base, live, scale=self.scale,
+                                        max_live_count=ctx.compact_max_live_count,
+                                        q_rope_positions=positions if compact_q_rope else None,
+                                        q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None)

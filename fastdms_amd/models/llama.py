@@ -1,0 +1,201 @@
+"""Llama / Qwen3 decoder glue (mirror of fastdms/models/llama.py:40-330 and
+qwen3.py:82-197).
+
+Per layer, the order of operations is the reference's: qkv projection ->
+[Qwen3: per-head q/k RMSNorm] -> DMS decision capture (prefill: extract on q;
+decode: fused decision + RoPE + compact append) -> RoPE (prefill) -> streaming
+pack of post-RoPE k / v into compact spans (prefill) -> attention -> o_proj.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+from torch import nn
+
+from ..engine.dms import extract_dms_eviction_decisions
+from ..layers.activation import silu_and_mul
+from ..layers.attention import Attention
+from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled, compact_attention_splitk_enabled,
+                                        dms_decode_store_transient_k_enabled, dms_fused_decode_preprocess_enabled,
+                                        fused_dms_rope_store_compact_decode)
+from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
+from ..layers.layernorm import RMSNorm, rms_norm
+from ..layers.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
+from ..layers.rotary_embedding import get_rope
+from ..utils.context import get_context
+
+
+@dataclass
+class ModelConfig:
+    """The HF config fields the model reads (names as in transformers)."""
+    model_type: str = "llama"
+    vocab_size: int = 128256
+    hidden_size: int = 2048
+    intermediate_size: int = 8192
+    num_hidden_layers: int = 16
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 64
+    rope_theta: float = 500000.0
+    rope_scaling: dict | None = field(default_factory=lambda: {
+        "rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+        "original_max_position_embeddings": 8192})
+    rms_norm_eps: float = 1e-5
+    max_position_embeddings: int = 131072
+    tie_word_embeddings: bool = True
+    attention_bias: bool = False
+    qk_norm: bool = False
+    hidden_act: str = "silu"
+    dtype: str = "bfloat16"
+
+
+class LlamaAttention(nn.Module):
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim or config.hidden_size // self.num_heads
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.scaling = self.head_dim ** -0.5
+        self.qkv_proj = QKVParallelLinear(config.hidden_size, self.head_dim, self.num_heads, self.num_kv_heads,
+                                          bias=config.attention_bias)
+        self.o_proj = RowParallelLinear(self.num_heads * self.head_dim, config.hidden_size, bias=False)
+        self.rotary_emb = get_rope(self.head_dim, self.head_dim, config.max_position_embeddings, config.rope_theta,
+                                   config.rope_scaling)
+        self.attn = Attention(self.num_heads, self.head_dim, self.scaling, self.num_kv_heads)
+        self.qk_norm = config.qk_norm
+        if self.qk_norm:
+            self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+            self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+
+    def forward(self, positions: torch.Tensor, hidden_states: torch.Tensor) -> torch.Tensor:
+        qkv = self.qkv_proj(hidden_states)
+        q = qkv[:, :self.q_size].view(-1, self.num_heads, self.head_dim)
+        k = qkv[:, self.q_size:self.q_size + self.kv_size].view(-1, self.num_kv_heads, self.head_dim)
+        v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
+        if self.qk_norm:  # Qwen3: QK-norm before DMS extraction (qwen3.py:92-94)
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        ctx = get_context()
+        fused = False
+        inline_q_rope = False
+        layer_id = self.attn.layer_id
+        if ctx.dms_capture_enabled:
+            can_fuse = (dms_fused_decode_preprocess_enabled() and not ctx.is_prefill and ctx.compact_kv_enabled
+                        and ctx.compact_slot_mapping is not None and self.attn.compact_k_cache.numel() > 0)
+            if ctx.dms_layer_evictions is None and ctx.dms_layer_evictions_buffer is None and not can_fuse:
+                raise RuntimeError("DMS capture requires a layer eviction recorder")
+            if layer_id < 0:
+                raise RuntimeError("DMS capture requires assigned attention layer ids")
+            evict_out = None
+            if ctx.dms_layer_evictions_buffer is not None:
+                evict_out = ctx.dms_layer_evictions_buffer[layer_id]
+            if can_fuse:
+                inline_q_rope = (compact_attention_inline_q_rope_enabled() and compact_attention_splitk_enabled()
+                                 and q.shape[0] == 1 and self.head_dim % 2 == 0 and self.head_dim >= 32)
+                slot = ctx.compact_slot_mapping
+                if slot.ndim == 3:
+                    slot = slot[layer_id]
+                if evict_out is None:
+                    evict_out = torch.empty((q.shape[0], self.num_kv_heads), device=q.device, dtype=torch.bool)
+                fused_dms_rope_store_compact_decode(
+                    q, k, v, self.rotary_emb.cos_sin_cache, self.attn.compact_k_cache, self.attn.compact_v_cache,
+                    slot, evict_out, positions, num_kv_heads=self.num_kv_heads, alpha_scale=ctx.dms_alpha_scale,
+                    alpha_offset=ctx.dms_alpha_offset, store_q=not inline_q_rope,
+                    store_transient_k=dms_decode_store_transient_k_enabled())
+                evict_mask = evict_out
+                fused = True
+            else:
+                q, evict_mask = extract_dms_eviction_decisions(
+                    q, num_kv_heads=self.num_kv_heads, num_qo_heads=self.num_heads, head_dim=self.head_dim,
+                    alpha_scale=ctx.dms_alpha_scale, alpha_offset=ctx.dms_alpha_offset, inplace=True, out=evict_out)
+            if ctx.dms_layer_evictions is not None:
+                ctx.dms_layer_evictions[layer_id] = evict_mask
+        if not fused:
+            q, k = self.rotary_emb(positions, q, k)
+        if (ctx.is_prefill and ctx.streaming_pack_manager is not None and ctx.streaming_pack_seq_ids
+                and ctx.dms_capture_enabled):
+            ctx.streaming_pack_manager.streaming_pack_layer(
+                layer_id=layer_id, k=k, v=v, evict_mask=evict_mask, cu_seqlens_q=ctx.cu_seqlens_q,
+                seq_ids=ctx.streaming_pack_seq_ids, window_size=ctx.streaming_pack_window_size,
+                cu_seqlens_host=ctx.cu_seqlens_q_host)
+        o = self.attn(q, k, v, compact_append_stored=fused, compact_q_rope=fused and inline_q_rope,
+                      positions=positions, cos_sin_cache=self.rotary_emb.cos_sin_cache)
+        return self.o_proj(o.view(o.shape[0], -1))
+
+
+class LlamaMLP(nn.Module):
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        assert config.hidden_act == "silu"
+        self.gate_up_proj = MergedColumnParallelLinear(config.hidden_size, [config.intermediate_size] * 2)
+        self.down_proj = RowParallelLinear(config.intermediate_size, config.hidden_size)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(silu_and_mul(self.gate_up_proj(x)))
+
+
+class LlamaDecoderLayer(nn.Module):
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        self.self_attn = LlamaAttention(config)
+        self.mlp = LlamaMLP(config)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, positions, hidden_states, residual):
+        if residual is None:
+            hidden_states, residual = self.input_layernorm(hidden_states), hidden_states
+        else:
+            hidden_states, residual = self.input_layernorm(hidden_states, residual)
+        hidden_states = self.self_attn(positions, hidden_states)
+        hidden_states, residual = self.post_attention_layernorm(hidden_states, residual)
+        return self.mlp(hidden_states), residual
+
+
+class LlamaModel(nn.Module):
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        self.embed_tokens = VocabParallelEmbedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([LlamaDecoderLayer(config) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        hidden_states = self.embed_tokens(input_ids)
+        residual = None
+        for layer in self.layers:
+            hidden_states, residual = layer(positions, hidden_states, residual)
+        hidden_states, _ = self.norm(hidden_states, residual)
+        return hidden_states
+
+
+class LlamaForCausalLM(nn.Module):
+    packed_modules_mapping = {"q_proj": ("qkv_proj", "q"), "k_proj": ("qkv_proj", "k"),
+                              "v_proj": ("qkv_proj", "v"), "gate_proj": ("gate_up_proj", 0),
+                              "up_proj": ("gate_up_proj", 1)}
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.model = LlamaModel(config)
+        self.lm_head = ParallelLMHead(config.vocab_size, config.hidden_size)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        return self.model(input_ids, positions)
+
+    def compute_logits(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(hidden_states)
+
+    def compute_greedy_token_ids(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self.lm_head.greedy_token_ids(hidden_states)
+
+
+Qwen3ForCausalLM = LlamaForCausalLM  # the same glue with config.qk_norm = True

@@ -167,6 +167,34 @@ int fdms_record_dms_decisions(int32_t* positions, int64_t p_l, int64_t p_s, int6
                               const int32_t* meta_rows, int row_start, int num_layers, int num_seqs,
                               int num_kv_heads, void* stream);
 
+/* B1 — dense causal prefill attention over a ragged batch (bf16, head_dim 64
+ * or 128, GQA).  Replaces the reference's flash_attn_varlen_func(causal=True)
+ * call (fastdms/layers/attention.py:85-92).  Rows are 16-byte aligned;
+ * cu_seqlens [num_seqs+1] on the device; max_seqlen bounds the grid. */
+int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t, int64_t ks_h,
+                           const void* v, int64_t vs_t, int64_t vs_h, void* out, int64_t os_t, int64_t os_h,
+                           const int32_t* cu_seqlens, int num_seqs, int max_seqlen, int num_q_heads,
+                           int num_kv_heads, int head_dim, float scale, void* stream);
+
+/* One v_mfma_f32_16x16x32_bf16 with the operand layout the attention kernels
+ * assume (no reference counterpart: a lane-layout self-check for tests). */
+int fdms_mfma_probe(const void* a, const void* b, float* c, void* stream);
+
+/* Residual-add + RMSNorm, bf16 (fastdms/layers/layernorm.py:16-40).  Row r of the
+ * input is at in + (r/heads)*in_stride + (r%heads)*in_head_stride (heads > 1
+ * normalises each head of a strided [tokens, heads, D] view, Qwen3 QK-norm,
+ * qwen3.py:92-94). */
+int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int heads, const void* residual,
+                 const void* weight, void* out, int64_t out_stride, void* residual_out, int64_t rows, int hidden,
+                 float eps, void* stream);
+
+/* out = silu(x[:, :F]) * x[:, F:], bf16 (fastdms/layers/activation.py:8-11). */
+int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
+
+/* Row argmax, ties to the lowest index (fastdms/layers/embed_head.py:142, 160,
+ * and the torch argmax of ParallelLMHead.greedy_token_ids, 491-543). */
+int fdms_argmax_rows(const void* x, int dtype, int64_t stride, int64_t rows, int n, int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

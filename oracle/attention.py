@@ -151,6 +151,27 @@ def compact_decode_attention(q, compact_k, compact_v, base_offsets, live_counts,
     return out
 
 
+def compact_decode_attention_storage(q, ck_storage, cv_storage, dtype_code, base_offsets, live_counts, scale=None):
+    """compact_decode_attention over arena *storage* arrays, decoding only the
+    live span of each (b, kv head)."""
+    q = np.asarray(q, dtype=np.float64)
+    b, hq, d = q.shape
+    hkv = np.asarray(base_offsets).shape[1]
+    g = hq // hkv
+    scale = d ** -0.5 if scale is None else scale
+    out = np.zeros((b, hq, d), dtype=np.float64)
+    for bi in range(b):
+        for h in range(hkv):
+            base, live = int(base_offsets[bi, h]), int(live_counts[bi, h])
+            keys = numerics.from_storage(ck_storage[base:base + live], dtype_code).astype(np.float64)
+            vals = numerics.from_storage(cv_storage[base:base + live], dtype_code).astype(np.float64)
+            s = q[bi, h * g:(h + 1) * g] @ keys.T * scale
+            s = s - s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            out[bi, h * g:(h + 1) * g] = (p @ vals) / p.sum(axis=1, keepdims=True)
+    return out
+
+
 def paged_rows(block_table_row, live: int, page_size: int) -> np.ndarray:
     """Physical slot of every rank r < live: table[r // P] * P + r % P."""
     r = np.arange(live)

@@ -1,0 +1,189 @@
+"""Model-level oracle — TEST INFRASTRUCTURE / CPU BASELINE ONLY.
+
+A CPU restatement of the compact-DMS Llama / Qwen3 step in torch fp32 (the
+"fp32 PyTorch CPU restatement" the benchmark times beside the GPU), rounding
+to bf16 at the points the GPU path stores bf16 tensors.  The order of
+operations follows fastdms/models/llama.py:87-330 (qwen3.py:82-197 for
+QK-norm), fastdms/engine/model_runner.py:594-772 (prefill / decode
+preparation) and fastdms/engine/compact_kv.py (pack, expiry, append, record).
+
+Linear layers accumulate in fp32 in a different order than the GPU GEMMs, so
+model-level agreement is checked on greedy tokens, not bits (parity unpinned
+at the bit level for whole-model outputs; every kernel it composes is pinned
+individually in tests/test_oracle_*.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import attention as oatt
+from . import compact_kv as ock
+from . import dms as odms
+from . import linear as olin
+from . import numerics
+
+
+def bf16(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+class OracleModel:
+    """weights: name -> fp32 CPU tensor (values of the bf16 GPU weights), with
+    the names of fastdms_amd.models.llama.LlamaForCausalLM.state_dict()."""
+
+    def __init__(self, weights: dict, cfg, *, window_size: int, alpha_scale: float, alpha_offset: float,
+                 capacity_tokens: int, max_model_len: int, kv_code: int = numerics.DT_FP8,
+                 manager: ock.OracleCompactKVManager | None = None, fp8_linear: dict | None = None):
+        self.w = weights
+        self.cfg = cfg
+        self.window = int(window_size)
+        self.alpha_scale = float(alpha_scale)
+        self.alpha_offset = float(alpha_offset)
+        self.kv_code = kv_code
+        self.L = cfg.num_hidden_layers
+        self.Hq = cfg.num_attention_heads
+        self.Hkv = cfg.num_key_value_heads
+        self.D = cfg.head_dim
+        self.cos_sin = oatt.rope_cos_sin_cache(self.D, cfg.max_position_embeddings, cfg.rope_theta,
+                                               cfg.rope_scaling)
+        self.mgr = manager or ock.OracleCompactKVManager(self.L, self.Hkv, capacity_tokens, max_model_len,
+                                                         head_dim=self.D, dtype_code=kv_code)
+        self.fp8_linear = fp8_linear or {}
+
+    # -- building blocks ------------------------------------------------------
+    def rmsnorm(self, x, weight, residual=None):
+        """fdms_rmsnorm: fp32 sum of squares, bf16 normalised value, bf16 product."""
+        eps = self.cfg.rms_norm_eps
+        if residual is not None:
+            x = x + residual
+            residual = bf16(x)
+        var = (x * x).mean(dim=-1, keepdim=True)
+        xn = bf16(x * (1.0 / torch.sqrt(var + eps)))
+        return bf16(xn * weight), residual
+
+    def linear(self, x, name, bias=True):
+        if name in self.fp8_linear:
+            w8_t, scale_inv = self.fp8_linear[name]
+            y = torch.from_numpy(olin.fp8_linear(x.numpy(), w8_t, scale_inv, quantize_x=True).astype(np.float32))
+        else:
+            y = x @ self.w[name + ".weight"].T
+        b = self.w.get(name + ".bias") if bias else None
+        if b is not None:
+            y = y + b
+        return bf16(y)
+
+    def qkv_split(self, qkv):
+        qs, ks = self.Hq * self.D, self.Hkv * self.D
+        t = qkv.shape[0]
+        return (qkv[:, :qs].reshape(t, self.Hq, self.D), qkv[:, qs:qs + ks].reshape(t, self.Hkv, self.D),
+                qkv[:, qs + ks:].reshape(t, self.Hkv, self.D))
+
+    def qk_norm(self, layer, q, k):
+        if not self.cfg.qk_norm:
+            return q, k
+        pre = f"model.layers.{layer}.self_attn."
+        q, _ = self.rmsnorm(q, self.w[pre + "q_norm.weight"])
+        k, _ = self.rmsnorm(k, self.w[pre + "k_norm.weight"])
+        return q, k
+
+    def mlp(self, layer, h):
+        gu = self.linear(h, f"model.layers.{layer}.mlp.gate_up_proj", bias=False)
+        f = gu.shape[1] // 2
+        g, u = gu[:, :f], gu[:, f:]
+        act = bf16((g / (1.0 + torch.exp(-g))) * u)
+        return self.linear(act, f"model.layers.{layer}.mlp.down_proj", bias=False)
+
+    def logits(self, x):
+        name = "lm_head" if "lm_head.weight" in self.w else "model.embed_tokens"
+        if name in self.fp8_linear:
+            return self.linear(x, name, bias=False)
+        return bf16(x @ self.w[name + ".weight"].T)
+
+    def lm_head(self, x):
+        self.last_logits = self.logits(x)
+        return olin.argmax_lowest(self.last_logits.numpy())
+
+    # -- prefill (model_runner.py:594-679, llama.py:87-202) --------------------
+    def prefill(self, seqs: list[tuple[int, list[int], int]]) -> list[int]:
+        """seqs: (seq_id, prompt token ids, max_tokens).  Returns each sequence's first token."""
+        for sid, prompt, max_tokens in seqs:
+            self.mgr.allocate(sid, len(prompt), max_tokens)
+        ids = torch.tensor([t for _, p, _ in seqs for t in p])
+        cu = np.concatenate([[0], np.cumsum([len(p) for _, p, _ in seqs])]).astype(np.int64)
+        pos = np.concatenate([np.arange(len(p)) for _, p, _ in seqs])
+        cs = self.cos_sin[pos][:, None, 0]
+        cos, sin = cs[..., :self.D // 2], cs[..., self.D // 2:]
+        x = self.w["model.embed_tokens.weight"][ids]
+        residual = None
+        for layer in range(self.L):
+            pre = f"model.layers.{layer}."
+            if residual is None:
+                h, _ = self.rmsnorm(x, self.w[pre + "input_layernorm.weight"])
+                residual = x
+            else:
+                h, residual = self.rmsnorm(x, self.w[pre + "input_layernorm.weight"], residual)
+            q, k, v = self.qkv_split(self.linear(h, pre + "self_attn.qkv_proj"))
+            q, k = self.qk_norm(layer, q, k)
+            qn, evict = odms.extract_dms_eviction_decisions(q.numpy(), num_kv_heads=self.Hkv, num_qo_heads=self.Hq,
+                                                            head_dim=self.D, alpha_scale=self.alpha_scale,
+                                                            alpha_offset=self.alpha_offset)
+            qr = oatt.apply_rotary_emb(qn, cos, sin, numerics.DT_BF16)
+            kr = oatt.apply_rotary_emb(k.numpy(), cos, sin, numerics.DT_BF16)
+            vn = v.numpy()
+            self.mgr.streaming_pack_layer(layer_id=layer, k=kr, v=vn, evict_mask=evict, cu_seqlens_q=cu,
+                                          seq_ids=[s for s, _, _ in seqs], window_size=self.window)
+            att = numerics.bf16_round(oatt.causal_prefill_attention(qr, kr, vn, cu).astype(np.float32))
+            o = self.linear(torch.from_numpy(att.reshape(att.shape[0], -1)), pre + "self_attn.o_proj", bias=False)
+            h, residual = self.rmsnorm(o, self.w[pre + "post_attention_layernorm.weight"], residual)
+            x = self.mlp(layer, h)
+        x, _ = self.rmsnorm(x, self.w["model.norm.weight"], residual)
+        return self.lm_head(x[torch.from_numpy(cu[1:] - 1)]).tolist()
+
+    # -- decode (model_runner.py:713-772, 1055-1084; llama.py:121-156) ---------
+    def decode(self, seq_ids: list[int], last_tokens: list[int], positions: list[int],
+               expiry_mode: str = "auto") -> list[int]:
+        self.mgr.apply_dms_evictions(seq_ids, positions, window_size=self.window, triton_mode=expiry_mode)
+        base, live, slot, _ = self.mgr.prepare_decode_metadata(seq_ids)
+        b = len(seq_ids)
+        x = self.w["model.embed_tokens.weight"][torch.tensor(last_tokens)]
+        residual = None
+        pos = np.asarray(positions)
+        evict_all = np.zeros((self.L, b, self.Hkv), dtype=bool)
+        for layer in range(self.L):
+            pre = f"model.layers.{layer}."
+            if residual is None:
+                h, _ = self.rmsnorm(x, self.w[pre + "input_layernorm.weight"])
+                residual = x
+            else:
+                h, residual = self.rmsnorm(x, self.w[pre + "input_layernorm.weight"], residual)
+            q, k, v = self.qkv_split(self.linear(h, pre + "self_attn.qkv_proj"))
+            q, k = self.qk_norm(layer, q, k)
+            qn, kn = q.numpy().copy(), k.numpy().copy()
+            ck, cv = self.mgr.compact_k_per_layer[layer], self.mgr.compact_v_per_layer[layer]
+            evict_all[layer] = oatt.fused_dms_rope_store_compact_decode(
+                q=qn, k=kn, v=v.numpy(), cos_sin_cache=self.cos_sin, compact_k=ck, compact_v=cv,
+                slot_mapping=slot[layer], positions=pos, num_kv_heads=self.Hkv, alpha_scale=self.alpha_scale,
+                alpha_offset=self.alpha_offset, q_dtype_code=numerics.DT_BF16, k_dtype_code=numerics.DT_BF16,
+                compact_dtype_code=self.kv_code, store_q=True, store_transient_k=False)
+            att = oatt.compact_decode_attention_storage(qn, ck, cv, self.kv_code, base[layer], live[layer])
+            att = numerics.bf16_round(att.astype(np.float32))
+            o = self.linear(torch.from_numpy(att.reshape(b, -1)), pre + "self_attn.o_proj", bias=False)
+            h, residual = self.rmsnorm(o, self.w[pre + "post_attention_layernorm.weight"], residual)
+            x = self.mlp(layer, h)
+        x, _ = self.rmsnorm(x, self.w["model.norm.weight"], residual)
+        tokens = self.lm_head(x).tolist()
+        self.mgr.record_appended_dms_decisions(seq_ids, positions, evict_all)
+        return tokens
+
+
+def weights_from_model(model) -> dict:
+    """fp32 CPU copies of a fastdms_amd model's (bf16) parameters and buffers by name."""
+    out = {}
+    for name, p in model.state_dict().items():
+        if name.endswith("cos_sin_cache"):
+            continue
+        out[name] = p.detach().float().cpu()
+    if "lm_head.weight" not in out:
+        out["lm_head.weight"] = out["model.embed_tokens.weight"]
+    return out

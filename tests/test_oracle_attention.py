@@ -148,3 +148,16 @@ def test_fused_decode_preprocess_equals_unfused_composition(q_code, cc):
             assert np.array_equal(ck[slot[bi, h]], numerics.to_storage(krot[bi, h], cc))
             assert np.array_equal(cv[slot[bi, h]], numerics.to_storage(v[bi, h], cc))
     assert np.array_equal(kf, numerics.cast(krot, q_code))
+
+
+def test_storage_attention_equals_value_attention():
+    rng = np.random.default_rng(9)
+    b, hkv, g, d = 2, 2, 4, 16
+    live = np.array([[5, 17], [1, 30]])
+    base = np.array([[0, 40], [80, 120]])
+    ck = numerics.e4m3fn_encode(rng.standard_normal((160, d)).astype(np.float32))
+    cv = numerics.e4m3fn_encode(rng.standard_normal((160, d)).astype(np.float32))
+    q = rng.standard_normal((b, hkv * g, d)).astype(np.float32)
+    a = oatt.compact_decode_attention_storage(q, ck, cv, numerics.DT_FP8, base, live)
+    ref = oatt.compact_decode_attention(q, numerics.e4m3fn_decode(ck), numerics.e4m3fn_decode(cv), base, live)
+    np.testing.assert_allclose(a, ref, rtol=1e-12, atol=1e-12)
