@@ -65,17 +65,18 @@ def attention_roofline(llm, seqs, replays: int):
     b = len(seqs)
     base = mgr.layer_major_base_offsets[:, start:start + b]
     live = mgr.layer_major_live_counts[:, start:start + b]
-    hint = mgr.max_live_upper_bound(seqs) + 256
+    hint = runner.attention_hint(seqs)  # the bound (and so the split count) the decode step uses
     q = torch.randn((b, cfg.num_attention_heads, cfg.head_dim), device="cuda").to(torch.bfloat16)
     layers = list(range(cfg.num_hidden_layers))
     arenas = [(mgr.compact_k_per_layer[l], mgr.compact_v_per_layer[l]) for l in layers]
-    for l in layers:  # warm (allocates the split workspace outside capture)
-        compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
-    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for l in layers:
+    with torch.inference_mode():  # the engine's tensors are inference tensors
+        for l in layers:  # warm-up outside capture
             compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for l in layers:
+                compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
     g.replay()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

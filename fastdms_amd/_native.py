@@ -38,7 +38,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_store_compact_kvcache": "ppillllppilplliiip",
     "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiifpllpp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
-    "fdms_prepare_decode_metadata": "plllplllpiiip",
+    "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",
     "fdms_argmax_rows": "pillipp",
     "fdms_mfma_probe": "pppp",

@@ -10,7 +10,8 @@
 
 __global__ void prepare_decode_kernel(const int32_t* __restrict__ base, int64_t b_l, int64_t b_b, int64_t b_h,
                                       int32_t* __restrict__ live, int64_t l_l, int64_t l_b, int64_t l_h,
-                                      int32_t* __restrict__ slot, int num_seqs, int num_kv_heads, int total) {
+                                      int32_t* __restrict__ slot, int64_t s_l, int64_t s_b, int64_t s_h, int num_seqs,
+                                      int num_kv_heads, int total) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int h = i % num_kv_heads;
@@ -18,20 +19,20 @@ __global__ void prepare_decode_kernel(const int32_t* __restrict__ base, int64_t 
   const int l = i / (num_kv_heads * num_seqs);
   int32_t* lp = live + l * l_l + b * l_b + h * l_h;
   const int32_t old = *lp;
-  slot[i] = base[l * b_l + b * b_b + h * b_h] + old;
+  slot[l * s_l + b * s_b + h * s_h] = base[l * b_l + b * b_b + h * b_h] + old;
   *lp = old + 1;
 }
 
 FDMS_EXPORT int fdms_prepare_decode_metadata(const int32_t* base, int64_t b_l, int64_t b_b, int64_t b_h,
                                              int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h,
-                                             int32_t* slot_out, int num_layers, int num_seqs, int num_kv_heads,
-                                             void* stream) {
+                                             int32_t* slot_out, int64_t s_l, int64_t s_b, int64_t s_h,
+                                             int num_layers, int num_seqs, int num_kv_heads, void* stream) {
   if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0) return (int)hipErrorInvalidValue;
   const int total = num_layers * num_seqs * num_kv_heads;
   if (total == 0) return 0;
   if (!base || !live || !slot_out) return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(prepare_decode_kernel, dim3((total + 255) / 256), dim3(256), 0, (hipStream_t)stream, base, b_l,
-                     b_b, b_h, live, l_l, l_b, l_h, slot_out, num_seqs, num_kv_heads, total);
+                     b_b, b_h, live, l_l, l_b, l_h, slot_out, s_l, s_b, s_h, num_seqs, num_kv_heads, total);
   FDMS_LAUNCH_CHECK();
   return 0;
 }

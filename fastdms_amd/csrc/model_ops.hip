@@ -131,7 +131,15 @@ FDMS_EXPORT int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, voi
   return 0;
 }
 
-// Row argmax with ties to the lowest index (embed_head.py:142, 160).
+// Row argmax with torch.argmax's semantics (embed_head.py:142, 160): ties go
+// to the lowest index and NaN counts as larger than every number (the lowest
+// NaN index wins), so a row always yields an index in [0, n).
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
 // One block per row; fp32 or bf16 logits; int64 output.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t stride, int n,
@@ -140,19 +148,20 @@ __global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restri
   __shared__ int s_i[kThreads / kWave];
   const T* row = x + (int64_t)blockIdx.x * stride;
   float best = -INFINITY;
-  int bi = 0x7FFFFFFF;
+  int bi = threadIdx.x < n ? (int)threadIdx.x : 0;
   for (int j = threadIdx.x; j < n; j += kThreads) {
     const float v = ld<T>(row + j);
-    if (v > best) {  // strided scan visits indices in increasing order per thread
+    if (argmax_better(v, j, best, bi) || j == (int)threadIdx.x) {  // first element seeds the scan
       best = v;
       bi = j;
     }
   }
+  if ((int)threadIdx.x >= n) bi = 0x7FFFFFFF;  // no element: loses every comparison below
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o);
     const int oi = __shfl_xor(bi, o);
-    if (ov > best || (ov == best && oi < bi)) {
+    if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || argmax_better(ov, oi, best, bi))) {
       best = ov;
       bi = oi;
     }
@@ -165,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restri
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int i = 1; i < kThreads / kWave; ++i) {
-      if (s_v[i] > best || (s_v[i] == best && s_i[i] < bi)) {
+      if (s_i[i] != 0x7FFFFFFF && (bi == 0x7FFFFFFF || argmax_better(s_v[i], s_i[i], best, bi))) {
         best = s_v[i];
         bi = s_i[i];
       }

@@ -733,7 +733,7 @@ class CompactKVManager:
             nat.require_cuda(base, what="prepare_decode_metadata")
             nat.call("fdms_prepare_decode_metadata", base.data_ptr(), base.stride(0), base.stride(1),
                      base.stride(2), live.data_ptr(), live.stride(0), live.stride(1), live.stride(2),
-                     slot.data_ptr(), L, batch, H, nat.stream())
+                     slot.data_ptr(), slot.stride(0), slot.stride(1), slot.stride(2), L, batch, H, nat.stream())
             return base, live, slot, max_capacity
         base = torch.empty((L, batch, H), device=self.device, dtype=torch.int32)
         live = torch.empty_like(base)

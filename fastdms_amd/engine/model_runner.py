@@ -18,6 +18,7 @@ import torch
 
 from .. import _native as nat
 from ..config import Config
+from ..layers.compact_attention import reserve_attention_workspace
 from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
 from .compact_kv import CompactKVManager
@@ -33,6 +34,8 @@ class ModelRunner:
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("ModelRunner needs a HIP device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         torch.cuda.set_device(self.device)
         self.model = build_synthetic_model(hf, seed=config.seed, device=self.device,
                                            survive_fraction=config.dms_survive_fraction)
@@ -43,6 +46,8 @@ class ModelRunner:
         self.kv_dtype = config.resolve_kv_cache_dtype()
         self.max_num_seqs = config.max_num_seqs
         self.allocate_kv_cache()
+        reserve_attention_workspace(self.device, self.max_num_seqs * self.num_kv_heads,
+                                    hf.num_attention_heads // hf.num_key_value_heads, hf.head_dim)
         self.evict_buffer = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads),
                                         device=self.device, dtype=torch.bool)
         self.static_input_ids = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
@@ -147,16 +152,17 @@ class ModelRunner:
         return out
 
     # -- decode ------------------------------------------------------------------
-    def _decode_body(self, start: int, batch: int, max_live_hint: int) -> None:
-        """One decode step on static buffers; captured into a graph."""
+    def _decode_body(self, start: int, batch: int, max_live_hint: int) -> torch.Tensor:
+        """One decode step on static buffers; captured into a graph.  Returns the
+        logits tensor (graph-owned under capture: each replay refreshes it)."""
         mgr = self.compact_kv_manager
         L, H = self.num_layers, self.num_kv_heads
         base = mgr.layer_major_base_offsets[:, start:start + batch]
         live = mgr.layer_major_live_counts[:, start:start + batch]
         slot = self.static_slot[:, :batch]
         nat.call("fdms_prepare_decode_metadata", base.data_ptr(), base.stride(0), base.stride(1), base.stride(2),
-                 live.data_ptr(), live.stride(0), live.stride(1), live.stride(2), slot.data_ptr(), L, batch, H,
-                 nat.stream())
+                 live.data_ptr(), live.stride(0), live.stride(1), live.stride(2), slot.data_ptr(), slot.stride(0),
+                 slot.stride(1), slot.stride(2), L, batch, H, nat.stream())
         md = self.dms_metadata
         evict = self.evict_buffer[:, :batch]
         set_context(False, compact_kv_enabled=True, compact_base_offsets=base, compact_live_counts=live,
@@ -177,6 +183,15 @@ class ModelRunner:
                  *mgr.layer_major_live_counts.stride(), ev.data_ptr(), ev.stride(0), ev.stride(1), ev.stride(2),
                  pos.data_ptr(), 1, None, start, L, batch, H, nat.stream())
         reset_context()
+        return logits
+
+    def attention_hint(self, seqs: list[Sequence]) -> int:
+        """Bound on the live count of every (layer, seq, kv head) of the batch,
+        which sets the attention split count.  It is the host's upper bound
+        rounded up to the next 256-token bucket, so eager and graph-replayed
+        steps use the same split count (bit-identical results) and one graph
+        serves up to 256 steps."""
+        return (self.compact_kv_manager.max_live_upper_bound(seqs) // 256 + 1) * 256
 
     @torch.inference_mode()
     def run_decode(self, seqs: list[Sequence]) -> list[int]:
@@ -191,7 +206,7 @@ class ModelRunner:
             raise RuntimeError("decode batch must occupy contiguous active slots")
         for st in states:
             st.live_upper_bound += 1
-        hint = mgr.max_live_upper_bound(seqs)
+        hint = self.attention_hint(seqs)
         for i, seq in enumerate(seqs):
             self.pinned_ids[i] = seq.last_token
             self.pinned_pos[i] = positions[i]
@@ -204,20 +219,20 @@ class ModelRunner:
             use_graph = False
         if use_graph:
             entry = self.graphs.get(key)
-            if entry is not None and (entry[1] != mgr.storage_version or hint > entry[2]):
+            if entry is not None and (entry[1] != mgr.storage_version or hint != entry[2]):
                 entry = None
             if entry is None:
-                cap_hint = hint + 256
                 graph = torch.cuda.CUDAGraph()
                 torch.cuda.synchronize()
                 with torch.cuda.graph(graph, pool=self.graph_pool):
-                    self._decode_body(start, batch, cap_hint)
+                    logits = self._decode_body(start, batch, hint)
                 self.graph_pool = graph.pool()
-                entry = (graph, mgr.storage_version, cap_hint)
+                entry = (graph, mgr.storage_version, hint, logits)
                 self.graphs[key] = entry
             entry[0].replay()
+            self.model.lm_head.last_logits = entry[3]
         else:
-            self._decode_body(start, batch, hint)
+            self.model.lm_head.last_logits = self._decode_body(start, batch, hint)
         self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, hint)
         return self.static_tokens[:batch].tolist()
 

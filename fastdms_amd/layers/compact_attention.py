@@ -67,15 +67,34 @@ def _num_cus(device: torch.device) -> int:
     return _NUM_CUS[idx]
 
 
+_RETIRED: list[torch.Tensor] = []  # outgrown workspaces: captured graphs may still point at them
+
+
 def attention_workspace(device: torch.device, n_floats: int, n_counters: int):
-    """Return (workspace, counters) with at least the requested sizes."""
+    """Return (workspace, counters) with at least the requested sizes.
+
+    A buffer that is outgrown is replaced but never freed, so a HIP graph
+    captured against the old one stays valid.  Size it up front with
+    reserve_attention_workspace() before capturing."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     entry = _WORKSPACE.setdefault(idx, [None, None])
     if entry[0] is None or entry[0].numel() < n_floats:
+        if entry[0] is not None:
+            _RETIRED.append(entry[0])
         entry[0] = torch.empty(max(n_floats, 1), device=device, dtype=torch.float32)
     if entry[1] is None or entry[1].numel() < n_counters:
+        if entry[1] is not None:
+            _RETIRED.append(entry[1])
         entry[1] = torch.zeros(max(n_counters, 1), device=device, dtype=torch.int32)
     return entry[0], entry[1]
+
+
+def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size: int, head_dim: int) -> None:
+    """Allocate the split workspace for the largest split count choose_num_splits
+    can return for up to max_pairs (seq, kv head) pairs."""
+    target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
+    worst = max(p * min(1024, -(-target // p)) for p in range(1, max_pairs + 1))
+    attention_workspace(device, worst * group_size * (head_dim + 2), max_pairs)
 
 
 def choose_num_splits(device: torch.device, pairs: int, max_live: int) -> int:

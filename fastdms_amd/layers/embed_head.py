@@ -27,6 +27,7 @@ class ParallelLMHead(VocabParallelEmbedding):
     def __init__(self, num_embeddings: int, embedding_dim: int, bias: bool = False):
         super().__init__(num_embeddings, embedding_dim)
         self.quant = None
+        self.last_logits: torch.Tensor | None = None
         assert not bias
 
     def _last_rows(self, x: torch.Tensor) -> torch.Tensor:
@@ -46,4 +47,5 @@ class ParallelLMHead(VocabParallelEmbedding):
         if self.quant is not None and hasattr(self.quant, "argmax"):
             return self.quant.argmax(x)
         logits = self.quant(x, None) if self.quant is not None else F.linear(x, self.weight)
+        self.last_logits = logits  # the rows the ids came from (kept for inspection; no copy)
         return logits.argmax(dim=-1)

@@ -151,10 +151,12 @@ int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t p
                     int num_seqs, int num_kv_heads, int window, void* stream);
 
 /* A15 — decode append slots.  Replaces prepare_decode_metadata
- * (compact_kv.py:1727-1770): slot_out[l,b,h] = base + live; live += 1. */
+ * (compact_kv.py:1727-1770): slot_out[l,b,h] = base + live; live += 1.  Every
+ * operand is a strided [layers, seqs, kv_heads] view. */
 int fdms_prepare_decode_metadata(const int32_t* base, int64_t b_l, int64_t b_b, int64_t b_h, int32_t* live,
-                                 int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out, int num_layers,
-                                 int num_seqs, int num_kv_heads, void* stream);
+                                 int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out, int64_t s_l,
+                                 int64_t s_b, int64_t s_h, int num_layers, int num_seqs, int num_kv_heads,
+                                 void* stream);
 
 /* A14 — record the appended token's decision.  Replaces
  * _record_dms_decisions_layer_major_kernel / record_appended_dms_decisions

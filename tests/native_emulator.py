@@ -1,0 +1,633 @@
+"""CPU emulator of libfastdms_amd's C-ABI — TEST INFRASTRUCTURE ONLY.
+
+Lets the CPU test suite drive the real engine glue (fastdms_amd/engine,
+layers, models) end to end without a GPU: ``nat.call(name, *args)`` is
+replaced by a function that resolves every raw pointer to the torch storage
+that owns it, builds strided views with exactly the strides and extents the
+HIP kernel would use (``as_strided`` refuses any view that leaves its
+storage, and data-dependent indices are range-checked explicitly), and applies
+the entry point's documented semantics (include/fastdms_amd.h) with the
+oracle's numerics.  An access a kernel would make outside the buffer it was
+handed raises ``OutOfBounds`` naming the entry point and the argument.
+
+This never stands in for the HIP library in the product: only tests install
+it, and only over CPU tensors.
+"""
+from __future__ import annotations
+
+import bisect
+import gc
+import warnings
+from contextlib import contextmanager
+
+import numpy as np
+import torch
+
+from oracle import numerics
+
+DT_F32, DT_F16, DT_BF16, DT_FP8 = 0, 1, 2, 3
+_TORCH = {DT_F32: torch.float32, DT_F16: torch.float16, DT_BF16: torch.bfloat16, DT_FP8: torch.uint8}
+_ITEM = {DT_F32: 4, DT_F16: 2, DT_BF16: 2, DT_FP8: 1}
+
+
+class OutOfBounds(RuntimeError):
+    pass
+
+
+class _Registry:
+    """Maps raw addresses to the CPU storages that own them."""
+
+    def __init__(self):
+        self.bases: list[int] = []
+        self.entries: list[tuple[int, int, torch.UntypedStorage]] = []
+
+    def refresh(self):
+        seen = {}
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            for o in gc.get_objects():
+                try:
+                    if isinstance(o, torch.Tensor) and o.device.type == "cpu":
+                        s = o.untyped_storage()
+                        seen[s.data_ptr()] = (s.data_ptr(), s.nbytes(), s)
+                except Exception:  # noqa: BLE001 - fake/meta tensors
+                    continue
+        self.entries = sorted(seen.values(), key=lambda e: e[0])
+        self.bases = [e[0] for e in self.entries]
+
+    def find(self, ptr: int):
+        for attempt in range(2):
+            i = bisect.bisect_right(self.bases, ptr) - 1
+            if i >= 0:
+                base, nbytes, s = self.entries[i]
+                if base <= ptr < base + max(nbytes, 1):
+                    return base, nbytes, s
+            if attempt == 0:
+                self.refresh()
+        return None
+
+
+class Emulator:
+    def __init__(self):
+        self.reg = _Registry()
+        self.calls: list[str] = []
+        self.name = ""
+
+    # -- views ---------------------------------------------------------------
+    def _flat(self, ptr, dtype, what):
+        if not ptr:
+            raise OutOfBounds(f"{self.name}: NULL {what}")
+        hit = self.reg.find(int(ptr))
+        if hit is None:
+            raise OutOfBounds(f"{self.name}: {what} pointer {ptr:#x} is not inside any live CPU tensor")
+        base, nbytes, s = hit
+        item = torch.empty((), dtype=dtype).element_size()
+        off = int(ptr) - base
+        if off % item:
+            raise OutOfBounds(f"{self.name}: {what} pointer not aligned to {item} bytes")
+        flat = torch.empty(0, dtype=dtype)
+        flat.set_(s, 0, (nbytes // item,), (1,))
+        return flat, off // item
+
+    def view(self, ptr, dtype, size, stride, what):
+        flat, off = self._flat(ptr, dtype, what)
+        size = tuple(int(x) for x in size)
+        stride = tuple(int(x) for x in stride)
+        if any(x < 0 for x in stride):
+            raise OutOfBounds(f"{self.name}: negative stride for {what}")
+        if all(x > 0 for x in size):
+            last = off + sum((n - 1) * st for n, st in zip(size, stride))
+            if last >= flat.numel():
+                raise OutOfBounds(f"{self.name}: {what} needs element {last} of a {flat.numel()}-element buffer "
+                                  f"(size {size}, stride {stride}, offset {off})")
+        return flat.as_strided(size, stride, off)
+
+    def view_at(self, ptr, dtype, elem_offset, size, stride, what):
+        """view() of the buffer starting elem_offset elements after ptr."""
+        item = torch.empty((), dtype=dtype).element_size()
+        return self.view(int(ptr) + int(elem_offset) * item, dtype, size, stride, what)
+
+    def flat_at(self, ptr, dtype, what):
+        """(flat storage view, element offset of ptr) for data-dependent indexing."""
+        return self._flat(ptr, dtype, what)
+
+    def gather_idx(self, flat, idx, what):
+        idx = torch.as_tensor(idx, dtype=torch.int64)
+        if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= flat.numel()):
+            raise OutOfBounds(f"{self.name}: {what} index range [{int(idx.min())}, {int(idx.max())}] outside "
+                              f"[0, {flat.numel()})")
+        return idx
+
+    # -- value conversion ----------------------------------------------------
+    @staticmethod
+    def load(t: torch.Tensor, code: int) -> torch.Tensor:
+        if code == DT_FP8:
+            return torch.from_numpy(numerics.e4m3fn_decode(t.contiguous().numpy()))
+        return t.to(torch.float32)
+
+    @staticmethod
+    def store(dst: torch.Tensor, vals: torch.Tensor, code: int) -> None:
+        vals = vals.to(torch.float32)
+        if code == DT_FP8:
+            dst.copy_(torch.from_numpy(numerics.e4m3fn_encode(vals.contiguous().numpy())))
+        else:
+            dst.copy_(vals.to(_TORCH[code]))
+
+    # -- dispatch --------------------------------------------------------------
+    def __call__(self, name, *args):
+        self.name = name
+        self.calls.append(name)
+        fn = getattr(self, name[len("fdms_"):], None)
+        if fn is None:
+            raise NotImplementedError(f"emulator has no {name}")
+        rc = fn(*args)
+        if rc:
+            raise RuntimeError(f"{name} failed with HIP error {rc}")
+
+    # -- entry points ------------------------------------------------------------
+    def abi_version(self):
+        return 0
+
+    def copy_bytes(self, src, dst, n, blocks, stream):
+        self.view(dst, torch.uint8, (n,), (1,), "dst").copy_(self.view(src, torch.uint8, (n,), (1,), "src"))
+
+    def convert(self, src, sdt, dst, ddt, n, stream):
+        v = self.load(self.view(src, _TORCH[sdt], (n,), (1,), "src"), sdt)
+        self.store(self.view(dst, _TORCH[ddt], (n,), (1,), "dst"), v, ddt)
+
+    @staticmethod
+    def _decide(v, alpha_scale, alpha_offset, threshold, positive):
+        if positive:
+            return v > np.float32(threshold)
+        return (v * np.float32(alpha_scale)) - np.float32(alpha_offset) > 0
+
+    def extract_dms_decisions(self, q, qdt, qs_t, qs_h, qs_d, evict, es_t, es_h, T, H, G, D, a_s, a_o, thr, pos,
+                              stream):
+        if T < 0 or H <= 0 or G <= 0 or D <= 0:
+            return 1
+        if T == 0:
+            return 0
+        lane = self.view_at(q, _TORCH[qdt], (D - 1) * qs_d, (T, H), (qs_t, G * qs_h), "q decision lane")
+        v = self.load(lane, qdt)
+        e = self._decide(v, a_s, a_o, thr, pos)
+        self.view(evict, torch.uint8, (T, H), (es_t, es_h), "evict").copy_(e.to(torch.uint8))
+        lane.zero_()
+        return 0
+
+    def _seq_spans(self, cu, single_start, single_len, num_seqs):
+        if cu:
+            c = self.view(cu, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens").tolist()
+            return [(c[b], c[b], c[b + 1] - c[b]) for b in range(num_seqs)]
+        return [(single_start, 0, single_len)]
+
+    def streaming_pack_prepare(self, evict, es_t, es_h, cu, single_len, num_seqs, window, H, max_chunks, live_out,
+                               lo_b, lo_h, offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h,
+                               em_b, em_h, meta_cap, stream):
+        if num_seqs <= 0 or H <= 0 or max_chunks < 0:
+            return 1
+        spans = self._seq_spans(cu, 0, single_len, num_seqs)
+        live = self.view(live_out, torch.int32, (num_seqs, H), (lo_b, lo_h), "live_out")
+        offs = self.view(offsets, torch.int32, (num_seqs, H, max_chunks), (of_b, of_h, of_c), "block_offsets") \
+            if max_chunks > 0 else None
+        rows = list(range(num_seqs))
+        if meta_rows:
+            rows = self.view(meta_rows, torch.int32, (num_seqs,), (1,), "meta_rows").tolist()
+        for b, (tok0, ev0, n) in enumerate(spans):
+            ev = self.view_at(evict, torch.uint8, ev0 * es_t, (n, H), (es_t, es_h), "evict")
+            if positions:
+                for h in range(H):
+                    self.view_at(positions, torch.int32, rows[b] * tp_b + h * tp_h, (meta_cap,), (1,),
+                                 "positions").fill_(-1)
+                    self.view_at(evict_meta, torch.uint8, rows[b] * em_b + h * em_h, (meta_cap,), (1,),
+                                 "evict_meta").zero_()
+            nch = (n + 255) // 256
+            thresh = max(0, n - 1 - window)
+            for h in range(H):
+                keep = torch.zeros(0, dtype=torch.bool)
+                if n > 0:
+                    t = torch.arange(n)
+                    keep = (ev[:, h] == 0) | (t >= thresh)
+                running = 0
+                for c in range(max_chunks):
+                    offs[b, h, c] = running
+                    if c < nch:
+                        running += int(keep[c * 256:(c + 1) * 256].sum())
+                live[b, h] = running
+        return 0
+
+    def streaming_pack_rank_scatter(self, k, v, kvdt, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
+                                    single_len, num_seqs, bo, bo_b, bo_h, bo_c, base, bs_b, bs_h, ck, cv, cdt, cs_s,
+                                    positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s, window, H,
+                                    D, max_chunks, vec, stream):
+        if num_seqs <= 0 or H <= 0 or D <= 0 or max_chunks <= 0 or vec <= 0 or D % vec:
+            return 1
+        spans = self._seq_spans(cu, single_start, single_len, num_seqs)
+        rows = list(range(num_seqs))
+        if meta_rows:
+            rows = self.view(meta_rows, torch.int32, (num_seqs,), (1,), "meta_rows").tolist()
+        offs = self.view(bo, torch.int32, (num_seqs, H, max_chunks), (bo_b, bo_h, bo_c), "block_offsets")
+        bases = self.view(base, torch.int32, (num_seqs, H), (bs_b, bs_h), "base")
+        ckf, ck0 = self.flat_at(ck, _TORCH[cdt], "compact_k")
+        cvf, cv0 = self.flat_at(cv, _TORCH[cdt], "compact_v")
+        pflat, poff = self.flat_at(positions, torch.int32, "positions")
+        eflat, eoff = self.flat_at(evict_meta, torch.uint8, "evict_meta")
+        for b, (tok0, ev0, n) in enumerate(spans):
+            if n <= 0:
+                continue
+            n_do = min(n, max_chunks * 256)  # the grid covers max_chunks chunks
+            ev = self.view_at(evict, torch.uint8, ev0 * es_t, (n, H), (es_t, es_h), "evict")
+            kview = self.view_at(k, _TORCH[kvdt], tok0 * ks_t, (n, H, D), (ks_t, ks_h, 1), "k")
+            vview = self.view_at(v, _TORCH[kvdt], tok0 * vs_t, (n, H, D), (vs_t, vs_h, 1), "v")
+            thresh = max(0, n - 1 - window)
+            t = torch.arange(n_do)
+            for h in range(H):
+                e = ev[:n_do, h]
+                keep = (e == 0) | (t >= thresh)
+                local = torch.zeros(n_do, dtype=torch.int64)
+                for c in range((n_do + 255) // 256):
+                    kc = keep[c * 256:(c + 1) * 256]
+                    local[c * 256:(c + 1) * 256] = torch.cumsum(kc.to(torch.int64), 0) - 1 + int(offs[b, h, c])
+                src = torch.nonzero(keep).flatten()
+                rank = local[src]
+                pidx = self.gather_idx(pflat, poff + rows[b] * tp_b + h * tp_h + rank * tp_s, "positions")
+                eidx = self.gather_idx(eflat, eoff + rows[b] * em_b + h * em_h + rank * em_s, "evict_meta")
+                pflat[pidx] = src.to(torch.int32)
+                eflat[eidx] = e[src]
+                dst_rows = int(bases[b, h]) + rank
+                didx = dst_rows[:, None] * cs_s + torch.arange(D)[None, :]
+                self.gather_idx(ckf, ck0 + didx, "compact_k")
+                self.gather_idx(cvf, cv0 + didx, "compact_v")
+                kvals = self.load(kview[src, h], kvdt)
+                vvals = self.load(vview[src, h], kvdt)
+                tmp = torch.empty(didx.shape, dtype=_TORCH[cdt])
+                self.store(tmp, kvals, cdt)
+                ckf[ck0 + didx] = tmp
+                self.store(tmp, vvals, cdt)
+                cvf[cv0 + didx] = tmp
+        return 0
+
+    def _rotate(self, x1, x2, c, s):
+        return x1 * c - x2 * s, x2 * c + x1 * s
+
+    def _cos_sin(self, cos_sin, cs_p, cs_d, pos, D):
+        flat, off = self.flat_at(cos_sin, torch.float32, "cos_sin")
+        half = D // 2
+        pos = torch.as_tensor(pos, dtype=torch.int64)
+        ci = off + pos[:, None] * cs_p + torch.arange(half)[None, :] * cs_d
+        si = off + pos[:, None] * cs_p + (torch.arange(half)[None, :] + half) * cs_d
+        self.gather_idx(flat, ci, "cos_sin")
+        self.gather_idx(flat, si, "cos_sin")
+        return flat[ci], flat[si]
+
+    def rope_inplace(self, x, dt, xs_t, xs_h, T, NH, D, cos_sin, cs_p, cs_d, positions, stream):
+        if T == 0:
+            return 0
+        xv = self.view(x, _TORCH[dt], (T, NH, D), (xs_t, xs_h, 1), "x")
+        pos = self.view(positions, torch.int64, (T,), (1,), "positions")
+        c, s = self._cos_sin(cos_sin, cs_p, cs_d, pos, D)
+        f = self.load(xv, dt)
+        half = D // 2
+        y1, y2 = self._rotate(f[..., :half], f[..., half:], c[:, None, :], s[:, None, :])
+        self.store(xv, torch.cat([y1, y2], -1), dt)
+        return 0
+
+    def dms_rope_store_compact_decode(self, q, qdt, qs_b, qs_h, k, v, kvdt, ks_b, ks_h, vs_b, vs_h, cos_sin, cs_p,
+                                      cs_d, ck, cv, cdt, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h, positions, B, H,
+                                      G, D, a_s, a_o, thr, pos_scale, store_q, store_tk, stream):
+        if B == 0:
+            return 0
+        qv = self.view(q, _TORCH[qdt], (B, H * G, D), (qs_b, qs_h, 1), "q")
+        kv_ = self.view(k, _TORCH[kvdt], (B, H, D), (ks_b, ks_h, 1), "k")
+        vv = self.view(v, _TORCH[kvdt], (B, H, D), (vs_b, vs_h, 1), "v")
+        sl = self.view(slot, torch.int32, (B, H), (sm_b, sm_h), "slot_mapping")
+        ev = self.view(ev_out, torch.uint8, (B, H), (ev_b, ev_h), "evict_out")
+        pos = self.view(positions, torch.int64, (B,), (1,), "positions")
+        c, s = self._cos_sin(cos_sin, cs_p, cs_d, pos, D)
+        half = D // 2
+        qf = self.load(qv, qdt)
+        dec = qf[:, ::G, D - 1]
+        ev.copy_(self._decide(dec, a_s, a_o, thr, pos_scale).to(torch.uint8))
+        if store_q:
+            q2 = qf.clone()
+            q2[:, ::G, D - 1] = 0.0
+            y1, y2 = self._rotate(q2[..., :half], q2[..., half:], c[:, None, :], s[:, None, :])
+            self.store(qv, torch.cat([y1, y2], -1), qdt)
+        kf = self.load(kv_, kvdt)
+        y1, y2 = self._rotate(kf[..., :half], kf[..., half:], c[:, None, :], s[:, None, :])
+        krot = torch.cat([y1, y2], -1)
+        if store_tk:
+            self.store(kv_, krot, kvdt)
+        vf = self.load(vv, kvdt)
+        ckf, ck0 = self.flat_at(ck, _TORCH[cdt], "compact_k")
+        cvf, cv0 = self.flat_at(cv, _TORCH[cdt], "compact_v")
+        for b in range(B):
+            for h in range(H):
+                r = int(sl[b, h])
+                if r < 0:
+                    continue
+                idx = self.gather_idx(ckf, ck0 + r * c_s + torch.arange(D), "compact_k slot")
+                self.gather_idx(cvf, cv0 + r * c_s + torch.arange(D), "compact_v slot")
+                tmp = torch.empty(D, dtype=_TORCH[cdt])
+                self.store(tmp, krot[b, h], cdt)
+                ckf[idx] = tmp
+                self.store(tmp, vf[b, h], cdt)
+                cvf[cv0 + r * c_s + torch.arange(D)] = tmp
+        return 0
+
+    def store_compact_kvcache(self, key, value, kvdt, ks_b, ks_h, vs_b, vs_h, ck, cv, cdt, c_s, slot, sm_b, sm_h,
+                              B, H, D, stream):
+        if B == 0:
+            return 0
+        kv_ = self.load(self.view(key, _TORCH[kvdt], (B, H, D), (ks_b, ks_h, 1), "key"), kvdt)
+        vv = self.load(self.view(value, _TORCH[kvdt], (B, H, D), (vs_b, vs_h, 1), "value"), kvdt)
+        sl = self.view(slot, torch.int32, (B, H), (sm_b, sm_h), "slot_mapping")
+        ckf, ck0 = self.flat_at(ck, _TORCH[cdt], "compact_k")
+        cvf, cv0 = self.flat_at(cv, _TORCH[cdt], "compact_v")
+        for b in range(B):
+            for h in range(H):
+                r = int(sl[b, h])
+                if r < 0:
+                    continue
+                idx = self.gather_idx(ckf, ck0 + r * c_s + torch.arange(D), "compact_k slot")
+                self.gather_idx(cvf, cv0 + r * c_s + torch.arange(D), "compact_v slot")
+                tmp = torch.empty(D, dtype=_TORCH[cdt])
+                self.store(tmp, kv_[b, h], cdt)
+                ckf[idx] = tmp
+                self.store(tmp, vv[b, h], cdt)
+                cvf[cv0 + r * c_s + torch.arange(D)] = tmp
+        return 0
+
+    def compact_decode_attention(self, q, qdt, qs_b, qs_h, ck, cv, kvdt, c_s, base, bo_b, bo_h, bt, bt_b, bt_h,
+                                 page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
+                                 scale, rope_cs, rcs_p, rcs_d, rope_pos, stream):
+        if B == 0:
+            return 0
+        if splits > 1:
+            self.view(ws, torch.float32, (B * H * splits * G * (D + 2),), (1,), "workspace")
+            cnt = self.view(counters, torch.int32, (B * H,), (1,), "counters")
+            if bool((cnt != 0).any()):
+                raise OutOfBounds(f"{self.name}: split counters are not zero before the launch")
+        qv = self.view(q, _TORCH[qdt], (B, H * G, D), (qs_b, qs_h, 1), "q")
+        ov = self.view(out, _TORCH[qdt], (B, H * G, D), (os_b, os_h, 1), "out")
+        lv = self.view(live, torch.int32, (B, H), (lc_b, lc_h), "live_counts")
+        qf = self.load(qv, qdt)
+        if rope_pos:
+            pos = self.view(rope_pos, torch.int64, (B,), (1,), "rope_positions")
+            c, s = self._cos_sin(rope_cs, rcs_p, rcs_d, pos, D)
+            half = D // 2
+            q2 = qf.clone()
+            q2[:, ::G, D - 1] = 0.0
+            y1, y2 = self._rotate(q2[..., :half], q2[..., half:], c[:, None, :], s[:, None, :])
+            qf = self.load(torch.cat([y1, y2], -1).to(_TORCH[qdt]) if qdt != DT_FP8 else torch.cat([y1, y2], -1),
+                           qdt if qdt != DT_FP8 else DT_F32)
+        ckf, ck0 = self.flat_at(ck, _TORCH[kvdt], "compact_k")
+        cvf, cv0 = self.flat_at(cv, _TORCH[kvdt], "compact_v")
+        res = torch.empty((B, H * G, D), dtype=torch.float32)
+        for b in range(B):
+            for h in range(H):
+                n = int(lv[b, h])
+                if n <= 0:
+                    raise OutOfBounds(f"{self.name}: live count {n} at (b={b}, h={h})")
+                r = torch.arange(n)
+                if bt:
+                    btf, bt0 = self.flat_at(bt, torch.int32, "block_tables")
+                    pidx = self.gather_idx(btf, bt0 + b * bt_b + h * bt_h + r // page_size, "block_tables")
+                    rows = btf[pidx].to(torch.int64) * page_size + r % page_size
+                else:
+                    bv = self.view(base, torch.int32, (B, H), (bo_b, bo_h), "base_offsets")
+                    rows = int(bv[b, h]) + r
+                idx = rows[:, None] * c_s + torch.arange(D)[None, :]
+                kk = self.load(ckf[self.gather_idx(ckf, ck0 + idx, "compact_k span")], kvdt).double()
+                vv = self.load(cvf[self.gather_idx(cvf, cv0 + idx, "compact_v span")], kvdt).double()
+                qq = qf[b, h * G:(h + 1) * G].double()
+                sc = qq @ kk.T * scale
+                p = torch.softmax(sc, dim=-1)
+                res[b, h * G:(h + 1) * G] = (p @ vv).float()
+        self.store(ov, res, qdt)
+        return 0
+
+    def dms_expiry(self, incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live, lc_l, lc_s, lc_h,
+                   base, bo_l, bo_s, bo_h, ck, cv, layer_k, layer_v, row_bytes, c_s_bytes, cur, L, S, H, window,
+                   stream):
+        from oracle import compact_kv as ock
+        if S == 0:
+            return 0
+        lv = self.view(live, torch.int32, (L, S, H), (lc_l, lc_s, lc_h), "live_counts")
+        bv = self.view(base, torch.int32, (L, S, H), (bo_l, bo_s, bo_h), "base_offsets")
+        cp = self.view(cur, torch.int64, (S,), (1,), "current_positions")
+        pflat, poff = self.flat_at(positions, torch.int32, "positions")
+        eflat, eoff = self.flat_at(evict, torch.uint8, "evict")
+        if layer_k:
+            lk = self.view(layer_k, torch.int64, (L,), (1,), "layer_k").tolist()
+            lvv = self.view(layer_v, torch.int64, (L,), (1,), "layer_v").tolist()
+        for l in range(L):
+            ka = lk[l] if layer_k else ck
+            va = lvv[l] if layer_k else cv
+            kf, k0 = self.flat_at(ka, torch.uint8, "compact_k arena")
+            vf, v0 = self.flat_at(va, torch.uint8, "compact_v arena")
+            for s_ in range(S):
+                for h in range(H):
+                    n = int(lv[l, s_, h])
+                    if n == 0:
+                        continue
+                    pi = self.gather_idx(pflat, poff + l * ps_l + s_ * ps_s + h * ps_h + torch.arange(n), "positions")
+                    ei = self.gather_idx(eflat, eoff + l * es_l + s_ * es_s + h * es_h + torch.arange(n), "evict")
+                    b0 = int(bv[l, s_, h])
+                    rows_b = (b0 + torch.arange(n))[:, None] * c_s_bytes + torch.arange(row_bytes)[None, :]
+                    self.gather_idx(kf, k0 + rows_b, "compact_k rows")
+                    self.gather_idx(vf, v0 + rows_b, "compact_v rows")
+                    pos_row = pflat[pi].numpy().copy()
+                    ev_row = (eflat[ei].numpy() != 0)
+                    krows = kf[k0 + rows_b].numpy().copy()
+                    vrows = vf[v0 + rows_b].numpy().copy()
+                    fn = ock.expiry_incremental if incremental else ock.expiry_exact
+                    new_live = fn(positions=pos_row, evict=ev_row, live=n, base=0, compact_k=krows,
+                                  compact_v=vrows, current_position=int(cp[s_]), window_size=int(window))
+                    pflat[pi] = torch.from_numpy(pos_row.astype(np.int32))
+                    eflat[ei] = torch.from_numpy(ev_row.astype(np.uint8))
+                    kf[k0 + rows_b] = torch.from_numpy(krows)
+                    vf[v0 + rows_b] = torch.from_numpy(vrows)
+                    lv[l, s_, h] = new_live
+        return 0
+
+    def prepare_decode_metadata(self, base, b_l, b_b, b_h, live, l_l, l_b, l_h, slot, s_l, s_b, s_h, L, B, H,
+                                stream):
+        if L <= 0 or B < 0 or H <= 0:
+            return 1
+        if B == 0:
+            return 0
+        bv = self.view(base, torch.int32, (L, B, H), (b_l, b_b, b_h), "base")
+        lv = self.view(live, torch.int32, (L, B, H), (l_l, l_b, l_h), "live")
+        sv = self.view(slot, torch.int32, (L, B, H), (s_l, s_b, s_h), "slot_out")
+        sv.copy_(bv + lv)
+        lv.add_(1)
+        return 0
+
+    def record_dms_decisions(self, positions, p_l, p_s, p_h, p_c, evict, e_l, e_s, e_h, e_c, live, l_l, l_s, l_h,
+                             evict_all, a_l, a_b, a_h, cur, pos64, meta_rows, row_start, L, B, H, stream):
+        if L <= 0 or B < 0 or H <= 0:
+            return 1
+        if B == 0:
+            return 0
+        rows = list(range(row_start, row_start + B))
+        if meta_rows:
+            rows = self.view(meta_rows, torch.int32, (B,), (1,), "meta_rows").tolist()
+        cp = self.view(cur, torch.int64 if pos64 else torch.int32, (B,), (1,), "cur_positions")
+        av = self.view(evict_all, torch.uint8, (L, B, H), (a_l, a_b, a_h), "evict_all")
+        pflat, poff = self.flat_at(positions, torch.int32, "positions")
+        eflat, eoff = self.flat_at(evict, torch.uint8, "evict")
+        lflat, loff = self.flat_at(live, torch.int32, "live")
+        for l in range(L):
+            for b in range(B):
+                for h in range(H):
+                    li = self.gather_idx(lflat, [loff + l * l_l + rows[b] * l_s + h * l_h], "live")
+                    idx = int(lflat[li][0]) - 1
+                    if idx < 0:
+                        raise OutOfBounds(f"{self.name}: live count 0 at (l={l}, row={rows[b]}, h={h})")
+                    pi = self.gather_idx(pflat, [poff + l * p_l + rows[b] * p_s + h * p_h + idx * p_c], "positions")
+                    ei = self.gather_idx(eflat, [eoff + l * e_l + rows[b] * e_s + h * e_h + idx * e_c], "evict")
+                    pflat[pi] = int(cp[b])
+                    eflat[ei] = int(av[l, b, h])
+        return 0
+
+    def argmax_rows(self, x, dt, stride, rows, n, out, stream):
+        if rows == 0:
+            return 0
+        xv = self.load(self.view(x, _TORCH[dt], (rows, n), (stride, 1), "x"), dt)
+        m = xv.max(dim=1, keepdim=True).values  # NaN if the row holds one (torch.argmax semantics)
+        hit = torch.where(torch.isnan(m), torch.isnan(xv), xv == m)
+        first = torch.where(hit, torch.arange(n)[None, :], n).min(dim=1).values
+        self.view(out, torch.int64, (rows,), (1,), "out").copy_(first)
+        return 0
+
+    def rmsnorm(self, x, in_stride, in_head_stride, heads, residual, weight, out, out_stride, residual_out, rows,
+                hidden, eps, stream):
+        if rows < 0 or hidden <= 0 or hidden % 8 or hidden > 8192 or heads <= 0:
+            return 1
+        if rows == 0:
+            return 0
+        tokens = rows // heads
+        xv = self.view(x, torch.bfloat16, (tokens, heads, hidden), (in_stride, in_head_stride, 1), "in")
+        f = xv.float().reshape(rows, hidden)
+        if residual:
+            f = f + self.view(residual, torch.bfloat16, (rows, hidden), (hidden, 1), "residual").float()
+        if residual_out:
+            self.view(residual_out, torch.bfloat16, (rows, hidden), (hidden, 1), "residual_out").copy_(
+                f.to(torch.bfloat16))
+        w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
+        inv = 1.0 / torch.sqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
+        xn = (f * inv).to(torch.bfloat16).float()
+        self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
+        return 0
+
+    def silu_mul(self, x, out, rows, f, stream):
+        if rows == 0:
+            return 0
+        xv = self.view(x, torch.bfloat16, (rows, 2 * f), (2 * f, 1), "x").float()
+        g, u = xv[:, :f], xv[:, f:]
+        self.view(out, torch.bfloat16, (rows, f), (f, 1), "out").copy_((g / (1.0 + torch.exp(-g)) * u)
+                                                                         .to(torch.bfloat16))
+        return 0
+
+    def prefill_attention(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, num_seqs,
+                          max_seqlen, hq, hkv, d, scale, stream):
+        if num_seqs == 0 or max_seqlen <= 0:
+            return 0
+        c = self.view(cu, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens").tolist()
+        t = c[-1]
+        if max(c[i + 1] - c[i] for i in range(num_seqs)) > max_seqlen:
+            raise OutOfBounds(f"{self.name}: a sequence is longer than max_seqlen (rows would be skipped)")
+        qv = self.view(q, torch.bfloat16, (t, hq, d), (qs_t, qs_h, 1), "q").float()
+        kv_ = self.view(k, torch.bfloat16, (t, hkv, d), (ks_t, ks_h, 1), "k").float()
+        vv = self.view(v, torch.bfloat16, (t, hkv, d), (vs_t, vs_h, 1), "v").float()
+        ov = self.view(out, torch.bfloat16, (t, hq, d), (os_t, os_h, 1), "out")
+        g = hq // hkv
+        res = torch.empty((t, hq, d), dtype=torch.float32)
+        for i in range(num_seqs):
+            s0, s1 = c[i], c[i + 1]
+            n = s1 - s0
+            mask = torch.ones(n, n, dtype=torch.bool).tril()
+            for h in range(hq):
+                sc = (qv[s0:s1, h].double() @ kv_[s0:s1, h // g].double().T) * scale
+                sc = sc.masked_fill(~mask, float("-inf"))
+                res[s0:s1, h] = (torch.softmax(sc, -1) @ vv[s0:s1, h // g].double()).float()
+        ov.copy_(res.to(torch.bfloat16))
+        return 0
+
+
+@contextmanager
+def cpu_engine():
+    """Run fastdms_amd's engine on CPU tensors through the emulator.
+
+    Patches device placement (every "cuda" tensor lands on the CPU), the few
+    torch.cuda calls the engine makes, and ``_native.call``; restores all of
+    them on exit.  Graph capture is unavailable: use enforce_eager=True."""
+    import fastdms_amd._native as nat
+    import fastdms_amd.engine.model_runner as mr
+    import fastdms_amd.layers.compact_attention as ca
+
+    emu = Emulator()
+    saved = []
+
+    def patch(obj, name, value):
+        saved.append((obj, name, getattr(obj, name)))
+        setattr(obj, name, value)
+
+    def strip(fn):
+        def wrapped(*a, **k):
+            k.pop("device", None)
+            k.pop("pin_memory", None)
+            return fn(*a, **k)
+        return wrapped
+
+    for fname in ("zeros", "full", "tensor", "ones", "arange", "randn", "zeros_like", "full_like", "ones_like",
+                  "as_tensor"):
+        patch(torch, fname, strip(getattr(torch, fname)))
+
+    def poisoned(fn):
+        """torch.empty* whose memory reads as NaN / -1 until written, so a kernel
+        that consumes memory nobody wrote shows up in the results."""
+        def wrapped(*a, **k):
+            k.pop("device", None)
+            k.pop("pin_memory", None)
+            t = fn(*a, **k)
+            if t.dtype != torch.bool and t.numel():
+                t.view(-1).view(torch.uint8).fill_(0xFF) if t.is_contiguous() else t.fill_(float("nan"))
+            return t
+        return wrapped
+
+    patch(torch, "empty", poisoned(torch.empty))
+    patch(torch, "empty_like", poisoned(torch.empty_like))
+    orig_to = torch.Tensor.to
+
+    def to(self, *a, **k):
+        a = tuple(x for x in a if not (isinstance(x, torch.device) or (isinstance(x, str))))
+        k.pop("device", None)
+        k.pop("non_blocking", None)
+        return orig_to(self, *a, **k) if (a or k) else self
+
+    patch(torch.Tensor, "to", to)
+    orig_copy = torch.Tensor.copy_
+    patch(torch.Tensor, "copy_", lambda self, src, non_blocking=False: orig_copy(self, src))
+    def linear(x, w, b=None):  # fp32 accumulation then one bf16 rounding, as the oracle model computes
+        y = x.float() @ w.float().T
+        if b is not None:
+            y = y + b.float()
+        return y.to(x.dtype)
+
+    patch(torch.nn.functional, "linear", linear)
+    patch(torch.cuda, "set_device", lambda d: None)
+    patch(torch.cuda, "current_device", lambda: 0)
+    patch(torch.cuda, "synchronize", lambda *a, **k: None)
+    patch(torch.cuda, "is_available", lambda: True)
+    patch(nat, "call", emu)
+    patch(nat, "stream", lambda: 0)
+    patch(nat, "require_cuda", lambda *a, **k: None)
+    patch(ca, "_num_cus", lambda device: 256)
+    orig_build = mr.build_synthetic_model
+    patch(mr, "build_synthetic_model", lambda cfg, **k: orig_build(cfg, **{**k, "device": "cpu"}))
+    try:
+        yield emu
+    finally:
+        for obj, name, value in reversed(saved):
+            setattr(obj, name, value)

@@ -42,46 +42,119 @@ def test_graph_decode_equals_eager(model, lens):
     assert all(len(t) == 80 for t in outs[0])
 
 
-@pytest.mark.parametrize("model,lens", [("tiny-llama", [300, 517, 800, 64]), ("tiny-llama", [1000]),
-                                        ("tiny-llama", [200, 400]), ("tiny-qwen3", [129, 700])])
-def test_engine_follows_cpu_oracle(model, lens):
-    require_gpu()
+def _fp32_linear(x, w, b=None):
+    """The oracle's linear: fp32 accumulation, one bf16 rounding (test-only patch)."""
+    y = x.float() @ w.float().t()
+    if b is not None:
+        y = y + b.float()
+    return y.to(x.dtype)
+
+
+def _sync_oracle_state(orc, mgr, seqs):
+    """Give the oracle the GPU's compact state (arenas, spans, live counts,
+    positions, decisions), so its next decode step starts from the same KV."""
+    from oracle import compact_kv as ock
+    om = orc.mgr
+    om.free_ranges_per_layer = [list(r) for r in mgr.free_ranges_per_layer]
+    om.compact_k_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_k_per_layer]
+    om.compact_v_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_v_per_layer]
+    for s in seqs:
+        st = mgr.seq_states[s.seq_id]
+        om.seq_states[s.seq_id] = ock.SeqState(
+            s.seq_id, st.base_offsets.cpu().numpy().copy(), st.range_capacity.cpu().numpy().copy(),
+            st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
+            st.evict_mask.cpu().numpy().copy(), st.max_capacity_per_lh, st.decode_headroom,
+            st.dms_initial_expiry_done, st.last_dms_expiry_position)
+
+
+def _follow_oracle(model, lens, *, oracle_gemm: bool, gen: int = 40, sync_state: bool = False):
+    """Teacher-forced comparison; returns per-step (relative RMS, max-abs-rel)
+    logit errors and the (exact, near-tie) token counts.  With sync_state the
+    oracle decodes every step from the GPU's compact state, which removes the
+    effect of DMS decisions that flip on threshold ties."""
     from oracle.model import OracleModel, weights_from_model
     from fastdms_amd import SamplingParams
-    rng = np.random.default_rng(1)
-    prompts = _prompts(rng, lens, 512)
-    gen = 40
-    llm = _llm(model)
-    runner = llm.model_runner
-    orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
-                      alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
-                      max_model_len=llm.config.max_model_len)
-    sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
-    seqs = [llm.add_request(p, sp) for p in prompts]
-    llm.step()  # prefill
-    gpu_first = [s.completion_token_ids[0] for s in seqs]
-    orc_first = orc.prefill([(s.seq_id, s.prompt_token_ids, gen) for s in seqs])
-    exact = mismatch = 0
+    saved = torch.nn.functional.linear
+    if oracle_gemm:
+        torch.nn.functional.linear = _fp32_linear
+    try:
+        rng = np.random.default_rng(1)
+        prompts = _prompts(rng, lens, 512)
+        llm = _llm(model)
+        runner = llm.model_runner
+        orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
+                          alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
+                          max_model_len=llm.config.max_model_len)
+        sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+        seqs = [llm.add_request(p, sp) for p in prompts]
+        llm.step()  # prefill
+        gpu_first = [s.completion_token_ids[0] for s in seqs]
+        orc_first = orc.prefill([(s.seq_id, s.prompt_token_ids, gen) for s in seqs])
+        counts = [0, 0]
+        errors = []
 
-    def check(g, o, row):
-        nonlocal exact, mismatch
-        if g == o:
-            exact += 1
-            return
-        lg = orc.last_logits[row]
-        gap = float(abs(lg[o] - lg[g]))
-        assert gap <= 2e-2 * max(1.0, float(lg.abs().max())), (g, o, gap)
-        mismatch += 1
+        def check(g, o, row):
+            if g == o:
+                counts[0] += 1
+                return
+            lg = orc.last_logits[row]
+            gap = float(abs(lg[o] - lg[g]))
+            assert gap <= 2e-2 * max(1.0, float(lg.abs().max())), (g, o, gap)
+            counts[1] += 1
 
-    for i, (g, o) in enumerate(zip(gpu_first, orc_first)):
-        check(g, o, i)
-    for _ in range(gen - 1):
-        pos = [len(s) - 1 for s in seqs]
-        last = [s.last_token for s in seqs]
-        o_tok = orc.decode([s.seq_id for s in seqs], last, pos)
-        llm.step()
-        g_tok = [s.completion_token_ids[-1] for s in seqs]
-        for i, (g, o) in enumerate(zip(g_tok, o_tok)):
+        def logit_error():
+            got = runner.model.lm_head.last_logits.float().cpu()
+            want = orc.last_logits
+            assert torch.isfinite(got).all(), "non-finite logits"
+            rms = float((got - want).pow(2).mean().sqrt()) / max(1e-6, float(want.pow(2).mean().sqrt()))
+            mx = float((got - want).abs().max()) / max(1e-6, float(want.abs().max()))
+            errors.append((rms, mx))
+
+        for i, (g, o) in enumerate(zip(gpu_first, orc_first)):
             check(g, o, i)
-    assert exact >= 0.9 * (exact + mismatch), (exact, mismatch)
-    llm.exit()
+        logit_error()
+        for _ in range(gen - 1):
+            pos = [len(s) - 1 for s in seqs]
+            last = [s.last_token for s in seqs]
+            if sync_state:
+                torch.cuda.synchronize()
+                _sync_oracle_state(orc, runner.compact_kv_manager, seqs)
+            o_tok = orc.decode([s.seq_id for s in seqs], last, pos)
+            llm.step()
+            for i, (g, o) in enumerate(zip([s.completion_token_ids[-1] for s in seqs], o_tok)):
+                check(g, o, i)
+            logit_error()
+        llm.exit()
+    finally:
+        torch.nn.functional.linear = saved
+    print(f"{model} {lens} oracle_gemm={oracle_gemm} sync_state={sync_state}: tokens exact/near-tie {counts}; logit rel-RMS per step "
+          f"{[round(e[0], 4) for e in errors]}; max-abs-rel {max(e[1] for e in errors):.4f}", flush=True)
+    return errors, counts
+
+
+CASES = [("tiny-llama", [300, 517, 800, 64]), ("tiny-llama", [1000]), ("tiny-llama", [200, 400]),
+         ("tiny-qwen3", [129, 700])]
+
+
+@pytest.mark.parametrize("model,lens", CASES)
+def test_engine_step_matches_cpu_oracle(model, lens):
+    """Each decode step from the same compact state, with the oracle's GEMM
+    numerics: what is left is the kernels' own rounding (fp32 reduction order,
+    bf16 P in the prefill MFMA, one bf16 rounding of each output)."""
+    require_gpu()
+    errors, (exact, near) = _follow_oracle(model, lens, oracle_gemm=True, sync_state=True)
+    assert max(e[0] for e in errors) <= 1e-2
+    assert max(e[1] for e in errors) <= 2e-2
+    assert exact >= 0.95 * (exact + near)
+
+
+@pytest.mark.parametrize("model,lens", CASES)
+def test_engine_follows_cpu_oracle_native_gemm(model, lens):
+    """Free-running with production bf16 GEMMs (hipBLASLt): reduction order
+    differs from the CPU, which can flip a DMS decision sitting on the
+    threshold and so which tokens a head keeps; logits stay within a few
+    percent and greedy tokens agree except on near-ties."""
+    require_gpu()
+    errors, (exact, near) = _follow_oracle(model, lens, oracle_gemm=False)
+    assert max(e[0] for e in errors) <= 5e-2
+    assert exact >= 0.9 * (exact + near)

@@ -1,0 +1,174 @@
+"""Kernels around the DMS path that the model runs every layer: MFMA operand
+layout, RMSNorm (+ residual, + per-head strided rows), SiLU*up, row argmax,
+dense causal prefill attention and the strided decode-slot preparation."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import require_gpu
+from oracle import attention as oatt
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(x: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
+
+
+def test_mfma_operand_layout():
+    """v_mfma_f32_16x16x32_bf16 with the lane layout the prefill kernel assumes.
+    Small integers keep every product and sum exact, so the check is exact."""
+    require_gpu()
+    from fastdms_amd import _native as nat
+    rng = np.random.default_rng(0)
+    a = rng.integers(-3, 4, (16, 32)).astype(np.float32)
+    b = rng.integers(-3, 4, (32, 16)).astype(np.float32)
+    ad, bd = _bf16(a).cuda(), _bf16(b).cuda()
+    c = torch.empty((16, 16), device="cuda", dtype=torch.float32)
+    nat.call("fdms_mfma_probe", ad.data_ptr(), bd.data_ptr(), c.data_ptr(), nat.stream())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(c.cpu().numpy(), a @ b)
+
+
+def _rms_ref(x, w, eps, residual=None):
+    """layernorm.py:19-40 in fp32 on the CPU; returns (out, residual_out)."""
+    x = x.float()
+    res_out = None
+    if residual is not None:
+        x = x + residual.float()
+        res_out = x.to(torch.bfloat16)
+    inv = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return (x * inv).to(torch.bfloat16).float().mul(w.float()).to(torch.bfloat16), res_out
+
+
+def _ulp_close(got: torch.Tensor, want: torch.Tensor, what: str):
+    """bf16 results may differ by one unit in the last place (fp32 reduction order)."""
+    g, w = got.float().cpu(), want.float().cpu()
+    tol = w.abs() * 2.0 ** -7 + 1e-6
+    bad = (g - w).abs() > tol
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())} elements beyond 1 bf16 ulp"
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 2048), (37, 256), (9, 4096), (3, 8192)])
+def test_rmsnorm(rows, hidden):
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    g = torch.Generator().manual_seed(rows * 7 + hidden)
+    x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    r = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    out = rms_norm(x.cuda(), w.cuda(), 1e-5)
+    want, _ = _rms_ref(x, w, 1e-5)
+    _ulp_close(out, want, "rmsnorm")
+    out, res = rms_norm(x.cuda(), w.cuda(), 1e-5, residual=r.cuda())
+    want, want_res = _rms_ref(x, w, 1e-5, residual=r)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), want_res), "residual_out must be bf16(x + residual) exactly"
+    _ulp_close(out, want, "rmsnorm+residual")
+
+
+def test_rmsnorm_per_head_strided_view():
+    """Qwen3 q_norm / k_norm: RMSNorm of every head of a [T, H, D] view that
+    lives inside the fused qkv rows (qwen3.py:82-197)."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    t, hq, hkv, d = 13, 8, 2, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(t, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    qkv_d = qkv.cuda()
+    k_view = qkv_d[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    out = rms_norm(k_view, w.cuda(), 1e-6)
+    want, _ = _rms_ref(qkv[:, hq * d:(hq + hkv) * d].reshape(t * hkv, d), w, 1e-6)
+    _ulp_close(out.reshape(t * hkv, d), want, "per-head rmsnorm")
+    torch.cuda.synchronize()
+    assert torch.equal(qkv_d.cpu(), qkv), "the input view must not be modified"
+
+
+@pytest.mark.parametrize("rows,f", [(1, 8192), (29, 512), (8, 12288)])
+def test_silu_mul(rows, f):
+    require_gpu()
+    from fastdms_amd.layers.activation import silu_and_mul
+    g = torch.Generator().manual_seed(rows + f)
+    x = (3 * torch.randn(rows, 2 * f, generator=g)).to(torch.bfloat16)
+    out = silu_and_mul(x.cuda())
+    xf = x.float()
+    want = (torch.nn.functional.silu(xf[:, :f]) * xf[:, f:]).to(torch.bfloat16)
+    _ulp_close(out, want, "silu_mul")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_rows_matches_torch(dtype):
+    """Lowest index on ties; NaN wins (torch.argmax semantics), so the id is
+    always a valid token."""
+    require_gpu()
+    from fastdms_amd import _native as nat
+    g = torch.Generator().manual_seed(11)
+    n = 128256
+    x = torch.randn(7, n, generator=g).to(dtype)
+    x[1, 5000] = x[1, 90000] = 50.0           # tie: lowest index
+    x[2, :] = -float("inf")                  # all -inf: index 0
+    x[3, 77] = float("nan")                  # NaN beats every number
+    x[4, 1000] = x[4, 600] = float("nan")    # lowest NaN
+    x[5, n - 1] = 99.0                       # last element
+    x[6, :] = float("nan")
+    xd = x.cuda()
+    out = torch.empty(7, device="cuda", dtype=torch.int64)
+    nat.call("fdms_argmax_rows", xd.data_ptr(), nat.dtype_code(dtype), xd.stride(0), 7, n, out.data_ptr(),
+             nat.stream())
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == [int(torch.argmax(x[i].float())) for i in range(7)]
+    assert out.cpu().tolist()[1:7] == [5000, 0, 77, 600, n - 1, 0]
+
+
+@pytest.mark.parametrize("d,lens", [(64, [1, 63, 64, 65, 200, 517]), (128, [129, 700, 2])])
+def test_prefill_attention_vs_oracle(d, lens):
+    """Causal varlen attention (flash_attn_varlen_func semantics, attention.py:85-92)
+    on q/k/v that are strided views of fused qkv rows, GQA 8/2."""
+    require_gpu()
+    from fastdms_amd.layers.attention import prefill_attention
+    hq, hkv = 8, 2
+    t = sum(lens)
+    rng = np.random.default_rng(d)
+    qkv = rng.standard_normal((t, (hq + 2 * hkv) * d)).astype(np.float32)
+    qkv_b = _bf16(qkv)
+    qkv_v = qkv_b.float().numpy()
+    q = qkv_v[:, :hq * d].reshape(t, hq, d)
+    k = qkv_v[:, hq * d:(hq + hkv) * d].reshape(t, hkv, d)
+    v = qkv_v[:, (hq + hkv) * d:].reshape(t, hkv, d)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    want = oatt.causal_prefill_attention(q, k, v, cu)
+    dq = qkv_b.cuda()
+    qd = dq[:, :hq * d].view(t, hq, d)
+    kd = dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    vd = dq[:, (hq + hkv) * d:].view(t, hkv, d)
+    out = prefill_attention(qd, kd, vd, torch.from_numpy(cu).cuda(), max(lens), d ** -0.5)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err <= 2e-2, f"max-abs-rel error {err:.3g}"
+    # bf16 output: most elements are within a couple of bf16 ulps of the exact value
+    assert np.mean(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
+
+
+def test_prepare_decode_metadata_strided_slot_output():
+    """slot_out as a [:, :B] view of a wider [L, max_seqs, H] buffer (the decode
+    graph's static buffer): only the view's elements are written."""
+    require_gpu()
+    from fastdms_amd import _native as nat
+    L, S, H, B, start = 3, 8, 2, 3, 2
+    g = torch.Generator().manual_seed(2)
+    base = torch.randint(0, 10000, (L, S, H), generator=g, dtype=torch.int32)
+    live = torch.randint(1, 500, (L, S, H), generator=g, dtype=torch.int32)
+    slot_buf = torch.full((L, S, H), -7, dtype=torch.int32)
+    bd, ld, sd = base.cuda(), live.cuda(), slot_buf.cuda()
+    bv, lv, sv = bd[:, start:start + B], ld[:, start:start + B], sd[:, :B]
+    nat.call("fdms_prepare_decode_metadata", bv.data_ptr(), *bv.stride(), lv.data_ptr(), *lv.stride(), sv.data_ptr(),
+             *sv.stride(), L, B, H, nat.stream())
+    torch.cuda.synchronize()
+    want_slot = slot_buf.clone()
+    want_slot[:, :B] = base[:, start:start + B] + live[:, start:start + B]
+    want_live = live.clone()
+    want_live[:, start:start + B] += 1
+    assert torch.equal(sd.cpu(), want_slot)
+    assert torch.equal(ld.cpu(), want_live)
