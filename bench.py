@@ -95,7 +95,7 @@ def attention_roofline(llm, seqs, replays: int):
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "decode_attn_generic_kernel", "avg_launch_us": round(per_launch_s * 1e6, 3),
+            "kernel": "decode_attn_wave_kernel", "avg_launch_us": round(per_launch_s * 1e6, 3),
             "bytes_per_launch": int(bytes_per_launch), "splits": splits,
             "live_tokens_mean_per_head": round(float(lv.float().mean()), 1)}
 

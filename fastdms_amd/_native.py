@@ -29,6 +29,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_abi_version": "",
     "fdms_copy_bytes": "pplip",
     "fdms_convert": "pipilp",
+    "fdms_fp8_decode_hw": "pplp",
     "fdms_extract_dms_decisions": "pilllpllliiifffip",
     "fdms_streaming_pack_prepare": "pllpiiiiipllplllpppllllip",
     "fdms_streaming_pack_rank_scatter": "ppillllpllpiiiplllpllppilppplllllliiiiip",

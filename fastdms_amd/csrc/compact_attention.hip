@@ -14,9 +14,18 @@
 // (device-scope atomic ticket) merges them and writes the output, then resets
 // its ticket to 0 so the next call (or graph replay) starts clean.  Softmax is
 // computed in the log2 domain (q pre-scaled by scale*log2 e, exp2).
+#include <cstdlib>
+
 #include "fdms_common.h"
 
 using namespace fdms;
+
+// FASTDMS_AMD_ATTN_GENERIC=1 routes every call to the generic kernel (read per
+// call on the host; used to compare the two kernels on the same inputs).
+static bool fdms_force_generic_attention() {
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_GENERIC");
+  return e && e[0] == '1';
+}
 
 namespace {
 
@@ -221,6 +230,635 @@ __global__ __launch_bounds__(kThreads) void decode_attn_generic_kernel(
   if (tid == 0) counters[pair] = 0;
 }
 
+// ---------------------------------------------------------------------------
+// Tiled fast path: bf16 q, FP8 or bf16 K/V rows of 16-byte-aligned D = 64 / 128
+// elements, G in {1, 2, 4, 8}.
+//
+// A tile of T rows is read with lane-contiguous 16-byte loads (C = row bytes /
+// 16 lanes per row, RP = 256 / C rows per pass, NP passes in flight per
+// thread), so every wave instruction covers 1 KiB of one contiguous span.
+//   scores: each lane dots its 16-byte chunk with q (kept in LDS, pre-scaled
+//           by scale*log2 e) and the C lanes of a row reduce with xor shuffles;
+//   V:      the same lanes convert their chunk to bf16 into an LDS tile;
+//   P.V:    lane l of wave w owns DPL = G*D/64 outputs (head g = l / (64/G... ))
+//           over rows w, w+4, ...; the four waves' partial sums are reduced
+//           once after the last tile (the online-softmax rescale is applied
+//           per tile to every wave's partials alike).
+// FP8 is decoded with v_cvt_pk_f32_fp8 (OCP e4m3fn on gfx950).
+// Workgroups are dispatched round-robin over the 8 XCDs; the linear block id
+// is remapped so all splits of one (b, h) run on the same XCD and their
+// partials meet in that XCD's L2.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kXcds = 8;
+constexpr int kMergeBatch = 8;  // split partials loaded per round trip in the merge
+
+template <typename KT> struct RowLoad;
+template <> struct RowLoad<fp8_t> {
+  static constexpr int kEpc = 16;  // elements per 16-byte chunk
+  static __device__ __forceinline__ void to_f32(const uint4& c, float* f) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+      f[4 * i + 0] = lo[0];
+      f[4 * i + 1] = lo[1];
+      f[4 * i + 2] = hi[0];
+      f[4 * i + 3] = hi[1];
+    }
+  }
+};
+template <> struct RowLoad<bf16_t> {
+  static constexpr int kEpc = 8;
+  static __device__ __forceinline__ void to_f32(const uint4& c, float* f) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+
+template <int D, int G, typename KT>
+struct TiledCfg {
+  static constexpr int kEpc = RowLoad<KT>::kEpc;
+  static constexpr int kC = D / kEpc;            // lanes per row
+  static constexpr int kRP = kThreads / kC;      // rows per pass
+  static constexpr int kNP = 4;                  // passes per tile
+  static constexpr int kT = kRP * kNP;           // rows per tile
+  static constexpr int kDPL = G * D / 64;        // P.V outputs per lane
+  static constexpr int kLanesPerHead = 64 / G;   // P.V lanes per head
+};
+
+}  // namespace
+
+template <int D, int G, typename KT>
+__global__ __launch_bounds__(kThreads) void decode_attn_tiled_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, const KT* __restrict__ ck, const KT* __restrict__ cv,
+    int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b, int64_t bo_h,
+    const int32_t* __restrict__ block_tables, int64_t bt_b, int64_t bt_h, int page_shift, int paged,
+    const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
+    int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int num_pairs,
+    int num_splits, float scale, const float* __restrict__ rope_cs, int64_t rcs_p, int64_t rcs_d,
+    const int64_t* __restrict__ rope_pos) {
+  using Cfg = TiledCfg<D, G, KT>;
+  constexpr int C = Cfg::kC, RP = Cfg::kRP, NP = Cfg::kNP, T = Cfg::kT, EPC = Cfg::kEpc;
+  constexpr int DPL = Cfg::kDPL, LPH = Cfg::kLanesPerHead;
+  __shared__ __attribute__((aligned(16))) float s_q[G][D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[T][D];   // bf16 bits
+  __shared__ float s_p[G][T];
+  __shared__ __attribute__((aligned(16))) float s_red[kThreads / kWave][64][DPL];
+  __shared__ float s_m[G], s_l[G], s_alpha[G];
+  __shared__ int s_last;
+
+  // XCD-aware (pair, split) of this workgroup
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds;
+  const int slot = lin / kXcds;
+  const int pair = (slot / num_splits) * kXcds + xcd;
+  const int split = slot - (slot / num_splits) * num_splits;
+  if (pair >= num_pairs) return;  // uniform per workgroup
+  const int b = pair / num_kv_heads;
+  const int h = pair - b * num_kv_heads;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+
+  const int live = live_counts[b * lc_b + h * lc_h];
+  const int per = (live + num_splits - 1) / num_splits;
+  const int t0 = min(live, split * per);
+  const int t1 = min(live, t0 + per);
+  const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
+  const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
+  const float qscale = scale * kLog2e;
+
+  // q -> LDS (fp32, pre-scaled), optional inline RoPE with the decision lane zeroed
+  if (rope_pos) {
+    constexpr int half = D / 2;
+    const int64_t pos = rope_pos[b];
+    for (int i = tid; i < G * half; i += kThreads) {
+      const int g = i / half, j = i - g * half;
+      const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
+      const float x1 = ld<bf16_t>(qh + j);
+      const float x2 = (g == 0 && j == half - 1) ? 0.0f : ld<bf16_t>(qh + j + half);
+      float y1, y2;
+      rope_f32(x1, x2, rope_cs[pos * rcs_p + (int64_t)j * rcs_d], rope_cs[pos * rcs_p + (int64_t)(j + half) * rcs_d],
+               &y1, &y2);
+      s_q[g][j] = y1 * qscale;
+      s_q[g][j + half] = y2 * qscale;
+    }
+  } else {
+    for (int i = tid; i < G * D; i += kThreads) {
+      const int g = i / D, d = i - g * D;
+      s_q[g][d] = ld<bf16_t>(q + b * qs_b + (int64_t)(h * G + g) * qs_h + d) * qscale;
+    }
+  }
+  if (tid < G) {
+    s_m[tid] = -INFINITY;
+    s_l[tid] = 0.0f;
+  }
+  __syncthreads();
+
+  const int chunk = tid % C;        // this lane's 16-byte chunk of a row
+  const int prow = tid / C;         // this lane's row within a pass
+  const int pv_g = lane / LPH;      // P.V: head and output columns of this lane
+  const int pv_d0 = (lane - pv_g * LPH) * DPL;
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
+
+  for (int tile = t0; tile < t1; tile += T) {
+    const int n = min(T, t1 - tile);
+    uint4 kr[NP], vr[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int r = p * RP + prow;
+      kr[p] = uint4{0u, 0u, 0u, 0u};
+      vr[p] = uint4{0u, 0u, 0u, 0u};
+      if (r < n) {
+        const int64_t row = addr.row(b, h, bo, tile + r);
+        kr[p] = *reinterpret_cast<const uint4*>(ck + row * c_s + chunk * EPC);
+        vr[p] = *reinterpret_cast<const uint4*>(cv + row * c_s + chunk * EPC);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int r = p * RP + prow;
+      float kf[EPC];
+      RowLoad<KT>::to_f32(kr[p], kf);
+      float sc[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4* qg = reinterpret_cast<const float4*>(&s_q[g][chunk * EPC]);
+        float a = 0.0f;
+#pragma unroll
+        for (int e4 = 0; e4 < EPC / 4; ++e4) {
+          const float4 qq = qg[e4];
+          a += qq.x * kf[4 * e4] + qq.y * kf[4 * e4 + 1] + qq.z * kf[4 * e4 + 2] + qq.w * kf[4 * e4 + 3];
+        }
+        sc[g] = a;
+      }
+#pragma unroll
+      for (int o = 1; o < C; o <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] += __shfl_xor(sc[g], o);
+      if (chunk == 0 && r < T) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) s_p[g][r] = (r < n) ? sc[g] : -INFINITY;
+      }
+      // V chunk -> LDS as bf16
+      float vf[EPC];
+      RowLoad<KT>::to_f32(vr[p], vf);
+      uint32_t packed[EPC / 2];
+#pragma unroll
+      for (int e = 0; e < EPC / 2; ++e)
+        packed[e] = f32_to_bf16(vf[2 * e]) | (f32_to_bf16(vf[2 * e + 1]) << 16);
+      uint4* dst = reinterpret_cast<uint4*>(&s_v[r][chunk * EPC]);
+#pragma unroll
+      for (int e = 0; e < EPC / 8; ++e) dst[e] = uint4{packed[4 * e], packed[4 * e + 1], packed[4 * e + 2], packed[4 * e + 3]};
+    }
+    __syncthreads();
+    // online softmax over the tile, one wave per head (heads w, w+4)
+    for (int g = wave; g < G; g += kThreads / kWave) {
+      float mx = -INFINITY;
+      for (int i = lane; i < n; i += kWave) mx = fmaxf(mx, s_p[g][i]);
+      mx = wave_max(mx);
+      const float m_old = s_m[g];
+      const float m_new = fmaxf(m_old, mx);
+      float sum = 0.0f;
+      for (int i = lane; i < n; i += kWave) {
+        const float pr = exp2f(s_p[g][i] - m_new);
+        s_p[g][i] = pr;
+        sum += pr;
+      }
+      sum = wave_sum(sum);
+      if (lane == 0) {
+        const float alpha = exp2f(m_old - m_new);
+        s_alpha[g] = alpha;
+        s_l[g] = s_l[g] * alpha + sum;
+        s_m[g] = m_new;
+      }
+    }
+    __syncthreads();
+    // P.V over rows wave, wave+4, ...
+    {
+      const float alpha = s_alpha[pv_g];
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
+      for (int r = wave; r < n; r += kThreads / kWave) {
+        const float pr = s_p[pv_g][r];
+        const uint16_t* vrow = &s_v[r][pv_d0];
+#pragma unroll
+        for (int i2 = 0; i2 < DPL / 2; ++i2) {
+          const uint32_t w2 = *reinterpret_cast<const uint32_t*>(vrow + 2 * i2);
+          acc[2 * i2] += pr * __uint_as_float(w2 << 16);
+          acc[2 * i2 + 1] += pr * __uint_as_float(w2 & 0xFFFF0000u);
+        }
+        if (DPL == 1) acc[0] += pr * __uint_as_float((uint32_t)vrow[0] << 16);
+      }
+    }
+    __syncthreads();
+  }
+
+  // reduce the four waves' partial sums
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) s_red[wave][lane][i] = acc[i];
+  __syncthreads();
+  // thread tid < 64 (wave 0) now owns (pv_g, pv_d0 .. pv_d0 + DPL)
+  float tot[DPL];
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) tot[i] = s_red[0][lane][i] + s_red[1][lane][i] + s_red[2][lane][i] + s_red[3][lane][i];
+  }
+  if (num_splits == 1) {
+    if (wave == 0) {
+      const float inv = 1.0f / s_l[pv_g];
+      bf16_t* op = out + b * os_b + (int64_t)(h * G + pv_g) * os_h + pv_d0;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) op[i].bits = (uint16_t)f32_to_bf16(tot[i] * inv);
+    }
+    return;
+  }
+  constexpr int64_t kStride = (int64_t)G * (D + 2);
+  float* mine = ws + ((int64_t)pair * num_splits + split) * kStride;
+  if (tid < G) {
+    mine[tid] = s_m[tid];
+    mine[G + tid] = s_l[tid];
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) mine[2 * G + pv_g * D + pv_d0 + i] = tot[i];
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == num_splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const float* all = ws + (int64_t)pair * num_splits * kStride;
+  for (int o = tid; o < G * D; o += kThreads) {
+    const int g = o / D;
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < num_splits; ++s2) M = fmaxf(M, all[s2 * kStride + g]);
+    float L = 0.0f, A = 0.0f;
+    for (int s2 = 0; s2 < num_splits; ++s2) {
+      const float* ps = all + s2 * kStride;
+      const float ms = ps[g];
+      const float wgt = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+      L += ps[G + g] * wgt;
+      A += ps[2 * G + o] * wgt;
+    }
+    out[b * os_b + (int64_t)(h * G + g) * os_h + (o - g * D)].bits = (uint16_t)f32_to_bf16(A / L);
+  }
+  if (tid == 0) counters[pair] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-local fast path (G <= 4): each wave owns a contiguous run of the
+// workgroup's rows and streams it in wave tiles of RT = NP * 64 / C rows, the
+// next tile's K/V already in flight while the current one is computed.  C
+// lanes share a row (one 16-byte chunk each): their partial dots are summed
+// with DPP, so every lane of the row holds the row's score and can apply its
+// probability to its own V chunk -- P.V accumulates in registers with a
+// per-lane running max and no barrier or LDS traffic inside the loop.  Lanes
+// and waves are combined once at the end (DPP row rotations, then LDS), and
+// split partials are merged by the last workgroup of a (b, h) pair.  The
+// partials travel as agent-scope atomic stores / loads (coherent across XCDs
+// without an L2 write-back), ordered by a wait for their completion before
+// the ticket increment.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// sum over the C consecutive lanes of a row group (C = 4, 8, 16)
+template <int C>
+__device__ __forceinline__ float row_group_sum(float v) {
+  v += dpp_f<0xB1>(v);                       // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);                       // quad_perm [2,3,0,1]
+  if constexpr (C >= 8) v += dpp_f<0x141>(v);   // row_half_mirror
+  if constexpr (C >= 16) v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+
+// sum over the lanes of a 16-lane row that hold the same chunk (lane % C)
+template <int C>
+__device__ __forceinline__ float same_chunk_row_sum(float v) {
+  if constexpr (C <= 4) v += dpp_f<0x124>(v);   // row_ror:4
+  if constexpr (C <= 8) v += dpp_f<0x128>(v);   // row_ror:8
+  return v;
+}
+
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+template <int D, int G, typename KT, int NP>
+__global__ __launch_bounds__(kThreads) void decode_attn_wave_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, const KT* __restrict__ ck, const KT* __restrict__ cv,
+    int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b, int64_t bo_h,
+    const int32_t* __restrict__ block_tables, int64_t bt_b, int64_t bt_h, int page_shift, int paged,
+    const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
+    int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int num_pairs,
+    int num_splits, float scale, const float* __restrict__ rope_cs, int64_t rcs_p, int64_t rcs_d,
+    const int64_t* __restrict__ rope_pos) {
+  constexpr int EPC = RowLoad<KT>::kEpc;
+  constexpr int C = D / EPC;       // lanes per row
+  constexpr int RPI = 64 / C;      // rows per load instruction (per wave)
+  constexpr int RT = RPI * NP;     // rows per wave tile
+  constexpr int kWaves = kThreads / kWave;
+  constexpr int kRows16 = 4;       // 16-lane rows per wave
+  static_assert(C == 4 || C == 8 || C == 16, "row split");
+  __shared__ __attribute__((aligned(16))) float s_q[G][D];
+  __shared__ float s_wm[kWaves][G], s_wl[kWaves][G];
+  __shared__ __attribute__((aligned(16))) float s_buf[kWaves][kRows16][C][G][EPC];
+  __shared__ float s_M[G], s_L[G];
+  __shared__ int s_last;
+
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds;
+  const int slot = lin / kXcds;
+  const int pair = (slot / num_splits) * kXcds + xcd;
+  const int split = slot - (slot / num_splits) * num_splits;
+  if (pair >= num_pairs) return;  // uniform per workgroup
+  const int b = pair / num_kv_heads;
+  const int h = pair - b * num_kv_heads;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+
+  const int live = live_counts[b * lc_b + h * lc_h];
+  const int per = (live + num_splits - 1) / num_splits;
+  const int t0 = min(live, split * per);
+  const int t1 = min(live, t0 + per);
+  const int wq = (t1 - t0 + kWaves - 1) / kWaves;
+  const int w0 = min(t1, t0 + wave * wq);
+  const int w1 = min(t1, w0 + wq);
+  const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
+  const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
+  const float qscale = scale * kLog2e;
+
+  if (rope_pos) {
+    constexpr int half = D / 2;
+    const int64_t pos = rope_pos[b];
+    for (int i = tid; i < G * half; i += kThreads) {
+      const int g = i / half, j = i - g * half;
+      const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
+      const float x1 = ld<bf16_t>(qh + j);
+      const float x2 = (g == 0 && j == half - 1) ? 0.0f : ld<bf16_t>(qh + j + half);
+      float y1, y2;
+      rope_f32(x1, x2, rope_cs[pos * rcs_p + (int64_t)j * rcs_d], rope_cs[pos * rcs_p + (int64_t)(j + half) * rcs_d],
+               &y1, &y2);
+      s_q[g][j] = y1 * qscale;
+      s_q[g][j + half] = y2 * qscale;
+    }
+  } else {
+    for (int i = tid; i < G * D; i += kThreads) {
+      const int g = i / D, d = i - g * D;
+      s_q[g][d] = ld<bf16_t>(q + b * qs_b + (int64_t)(h * G + g) * qs_h + d) * qscale;
+    }
+  }
+  __syncthreads();
+
+  const int chunk = lane % C;
+  const int rowi = lane / C;
+  float qf[G][EPC];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) qf[g][e] = s_q[g][chunk * EPC + e];
+
+  float m[G], l[G], acc[G][EPC];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc[g][e] = 0.0f;
+  }
+
+  uint4 kc[NP], vc[NP], kn[NP], vn[NP];
+  auto load_tile = [&](int ts, uint4* kk, uint4* vv) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int r = ts + p * RPI + rowi;
+      kk[p] = uint4{0u, 0u, 0u, 0u};
+      vv[p] = uint4{0u, 0u, 0u, 0u};
+      if (r < w1) {
+        const int64_t row = addr.row(b, h, bo, r);
+        kk[p] = *reinterpret_cast<const uint4*>(ck + row * c_s + chunk * EPC);
+        vv[p] = *reinterpret_cast<const uint4*>(cv + row * c_s + chunk * EPC);
+      }
+    }
+  };
+  if (w0 < w1) load_tile(w0, kc, vc);
+  for (int ts = w0; ts < w1; ts += RT) {
+    const bool more = ts + RT < w1;
+    if (more) load_tile(ts + RT, kn, vn);
+    float sc[NP][G];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float kf[EPC];
+      RowLoad<KT>::to_f32(kc[p], kf);
+      const bool valid = ts + p * RPI + rowi < w1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) a += qf[g][e] * kf[e];
+        a = row_group_sum<C>(a);
+        sc[p][g] = valid ? a : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[0][g];
+#pragma unroll
+      for (int p = 1; p < NP; ++p) mx = fmaxf(mx, sc[p][g]);
+      const float m_new = fmaxf(m[g], mx);
+      if (m_new != -INFINITY) {  // lanes whose rows are all past the end keep their state
+        const float alpha = exp2f(m[g] - m_new);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[g][e] *= alpha;
+        m[g] = m_new;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float vf[EPC];
+      RowLoad<KT>::to_f32(vc[p], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = (sc[p][g] == -INFINITY) ? 0.0f : exp2f(sc[p][g] - m[g]);
+        l[g] += (chunk == 0) ? pr : 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[g][e] += pr * vf[e];
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        kc[p] = kn[p];
+        vc[p] = vn[p];
+      }
+    }
+  }
+
+  // workgroup max per head, then rescale every lane to it
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float wm = wave_max(m[g]);
+    if (lane == 0) s_wm[wave][g] = wm;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = s_wm[0][tid];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_wm[w][tid]);
+    s_M[tid] = M;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float M = s_M[g];
+    const float f = (m[g] == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m[g] - M);
+    const float lw = wave_sum(l[g] * f);
+    if (lane == 0) s_wl[wave][g] = lw;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc[g][e] = same_chunk_row_sum<C>(acc[g][e] * f);
+  }
+  // lanes 0..C-1 of each 16-lane row now hold that row's sums for their chunk
+  if ((lane & 15) < C) {
+    const int r16 = lane >> 4;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) s_buf[wave][r16][lane & 15][g][e] = acc[g][e];
+  }
+  __syncthreads();
+  if (tid < G) {
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) L += s_wl[w][tid];
+    s_L[tid] = L;
+  }
+  __syncthreads();
+
+  constexpr int kOut = G * D;
+  if (num_splits == 1) {
+    for (int o = tid; o < kOut; o += kThreads) {
+      const int g = o / D, d = o - g * D;
+      const int cidx = d / EPC, e = d - cidx * EPC;
+      float A = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+        for (int r = 0; r < kRows16; ++r) A += s_buf[w][r][cidx][g][e];
+      out[b * os_b + (int64_t)(h * G + g) * os_h + d].bits = (uint16_t)f32_to_bf16(A / s_L[g]);
+    }
+    return;
+  }
+  constexpr int64_t kStride = (int64_t)G * (D + 2);
+  float* mine = ws + ((int64_t)pair * num_splits + split) * kStride;
+  if (tid < G) {
+    store_agent(mine + tid, s_M[tid]);
+    store_agent(mine + G + tid, s_L[tid]);
+  }
+  for (int o = tid; o < kOut; o += kThreads) {
+    const int g = o / D, d = o - g * D;
+    const int cidx = d / EPC, e = d - cidx * EPC;
+    float A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+      for (int r = 0; r < kRows16; ++r) A += s_buf[w][r][cidx][g][e];
+    store_agent(mine + 2 * G + o, A);
+  }
+  // every partial store has completed (device-coherent) before the ticket
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == num_splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  const float* all = ws + (int64_t)pair * num_splits * kStride;
+  for (int o = tid; o < kOut; o += kThreads) {
+    const int g = o / D;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    for (int s0 = 0; s0 < num_splits; s0 += kMergeBatch) {
+      // issue the batch's loads together: one memory round trip per batch
+      float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        mv[j] = -INFINITY;
+        lv[j] = av[j] = 0.0f;
+        if (s0 + j < num_splits) {
+          const float* ps = all + (s0 + j) * kStride;
+          mv[j] = load_agent(ps + g);
+          lv[j] = load_agent(ps + G + g);
+          av[j] = load_agent(ps + 2 * G + o);
+        }
+      }
+      float bm = M;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, mv[j]);
+      const float f = (M == -INFINITY || bm == -INFINITY) ? 0.0f : exp2f(M - bm);
+      L *= f;
+      A *= f;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float wgt = (mv[j] == -INFINITY) ? 0.0f : exp2f(mv[j] - bm);
+        L += lv[j] * wgt;
+        A += av[j] * wgt;
+      }
+      M = bm;
+    }
+    out[b * os_b + (int64_t)(h * G + g) * os_h + (o - g * D)].bits = (uint16_t)f32_to_bf16(A / L);
+  }
+  if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+namespace {
+
+template <int D, typename KT>
+bool launch_tiled_d(int G, dim3 grid, hipStream_t stream, const bf16_t* q, int64_t qs_b, int64_t qs_h, const KT* ck,
+                    const KT* cv, int64_t c_s, const int32_t* bo, int64_t bo_b, int64_t bo_h, const int32_t* bt,
+                    int64_t bt_b, int64_t bt_h, int page_shift, int paged, const int32_t* lc, int64_t lc_b,
+                    int64_t lc_h, bf16_t* out, int64_t os_b, int64_t os_h, float* ws, int* counters, int hkv,
+                    int pairs, int splits, float scale, const float* rcs, int64_t rcs_p, int64_t rcs_d,
+                    const int64_t* rpos) {
+#define FDMS_TILED(GG)                                                                                          \
+  hipLaunchKernelGGL((decode_attn_tiled_kernel<D, GG, KT>), grid, dim3(kThreads), 0, stream, q, qs_b, qs_h, ck, cv, \
+                     c_s, bo, bo_b, bo_h, bt, bt_b, bt_h, page_shift, paged, lc, lc_b, lc_h, out, os_b, os_h, ws,      \
+                     counters, hkv, pairs, splits, scale, rcs, rcs_p, rcs_d, rpos)
+#define FDMS_WAVE(GG)                                                                                          \
+  hipLaunchKernelGGL((decode_attn_wave_kernel<D, GG, KT, 2>), grid, dim3(kThreads), 0, stream, q, qs_b, qs_h, ck, cv, \
+                     c_s, bo, bo_b, bo_h, bt, bt_b, bt_h, page_shift, paged, lc, lc_b, lc_h, out, os_b, os_h, ws,      \
+                     counters, hkv, pairs, splits, scale, rcs, rcs_p, rcs_d, rpos)
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_TILED");
+  const bool tiled = e && e[0] == '1';
+  switch (G) {
+    case 1: if (tiled) FDMS_TILED(1); else FDMS_WAVE(1); return true;
+    case 2: if (tiled) FDMS_TILED(2); else FDMS_WAVE(2); return true;
+    case 4: if (tiled) FDMS_TILED(4); else FDMS_WAVE(4); return true;
+    case 8: FDMS_TILED(8); return true;
+    default: return false;
+  }
+#undef FDMS_TILED
+#undef FDMS_WAVE
+}
+
+}  // namespace
+
 FDMS_EXPORT int fdms_compact_decode_attention(
     const void* q, int q_dtype, int64_t qs_b, int64_t qs_h, const void* compact_k, const void* compact_v,
     int kv_dtype, int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* block_tables,
@@ -244,6 +882,31 @@ FDMS_EXPORT int fdms_compact_decode_attention(
   if (rope_positions && (!rope_cos_sin || head_dim % 2)) return (int)hipErrorInvalidValue;
   const int pairs = batch * num_kv_heads;
   if (pairs > 65535) return (int)hipErrorInvalidValue;
+  // tiled fast path: bf16 q, FP8 / bf16 K/V, D = 64 / 128, 16-byte aligned rows
+  const int kv_size = kv_dtype == kFP8 ? 1 : (kv_dtype == kBF16 ? 2 : 0);
+  const bool tiled_ok = q_dtype == kBF16 && kv_size > 0 && (head_dim == 64 || head_dim == 128) &&
+                        (c_s * kv_size) % 16 == 0 && ((uintptr_t)compact_k % 16) == 0 &&
+                        ((uintptr_t)compact_v % 16) == 0 && (group_size == 1 || group_size == 2 ||
+                        group_size == 4 || group_size == 8) && !fdms_force_generic_attention();
+  if (tiled_ok) {
+    const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
+    if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    const dim3 tgrid((unsigned)blocks);
+    bool done = false;
+#define FDMS_TILED_ARGS(KT)                                                                                         group_size, tgrid, (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (const KT*)compact_k, (const KT*)compact_v,       c_s, base_offsets, bo_b, bo_h, block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h,                (bf16_t*)out, os_b, os_h, workspace, counters, num_kv_heads, pairs, num_splits, scale, rope_cos_sin, rcs_p,         rcs_d, rope_positions
+    if (kv_dtype == kFP8) {
+      done = head_dim == 64 ? launch_tiled_d<64, fp8_t>(FDMS_TILED_ARGS(fp8_t))
+                            : launch_tiled_d<128, fp8_t>(FDMS_TILED_ARGS(fp8_t));
+    } else {
+      done = head_dim == 64 ? launch_tiled_d<64, bf16_t>(FDMS_TILED_ARGS(bf16_t))
+                            : launch_tiled_d<128, bf16_t>(FDMS_TILED_ARGS(bf16_t));
+    }
+#undef FDMS_TILED_ARGS
+    if (done) {
+      FDMS_LAUNCH_CHECK();
+      return 0;
+    }
+  }
   const dim3 grid(num_splits, pairs);
   FDMS_DISPATCH_FLOAT(q_dtype, QT,
     FDMS_DISPATCH_DTYPE(kv_dtype, KT,

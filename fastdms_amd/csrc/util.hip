@@ -43,3 +43,29 @@ FDMS_EXPORT int fdms_convert(const void* src, int src_dtype, void* dst, int dst_
   FDMS_LAUNCH_CHECK();
   return 0;
 }
+
+// Decode FP8 e4m3fn bytes to fp32 with the hardware conversion the attention
+// kernels use (v_cvt_pk_f32_fp8, bytes 0-1 / 2-3 of each dword), so a test can
+// compare it with the format's definition on all 256 codes.
+__global__ void fp8_decode_hw_kernel(const uint32_t* __restrict__ in, float* __restrict__ out, int64_t words) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const uint32_t w = in[i];
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  out[4 * i + 0] = lo[0];
+  out[4 * i + 1] = lo[1];
+  out[4 * i + 2] = hi[0];
+  out[4 * i + 3] = hi[1];
+}
+
+FDMS_EXPORT int fdms_fp8_decode_hw(const void* in, float* out, int64_t n, void* stream) {
+  if (n < 0 || n % 4) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  if (!in || !out || ((uintptr_t)in % 4)) return (int)hipErrorInvalidValue;
+  const int64_t words = n / 4;
+  hipLaunchKernelGGL(fp8_decode_hw_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint32_t*)in, out, words);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}

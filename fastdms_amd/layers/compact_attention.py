@@ -56,7 +56,7 @@ def _next_power_of_2(value: int) -> int:
 # split-K workspace: per device, grown on demand; counters start (and stay) 0
 # ---------------------------------------------------------------------------
 _WORKSPACE: dict[int, list] = {}
-_TARGET_BLOCKS_PER_CU = 4
+_TARGET_BLOCKS_PER_CU = 1
 _NUM_CUS: dict[int, int] = {}
 
 
@@ -98,11 +98,13 @@ def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size
 
 
 def choose_num_splits(device: torch.device, pairs: int, max_live: int) -> int:
-    """Splits per (seq, kv head): fill the CUs (~4 blocks each) but keep at
-    least ~64 live tokens per split."""
+    """Splits per (seq, kv head).  The kernel is latency-bound at decode sizes:
+    about one workgroup per CU lets every workgroup issue all of its K/V loads
+    in one round trip, and each split keeps at least ~128 live tokens so the
+    merge stays cheap."""
     target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
     s = max(1, -(-target // max(1, pairs)))
-    s = min(s, max(1, -(-int(max_live) // 64)))
+    s = min(s, max(1, -(-int(max_live) // 128)))
     return int(min(s, 1024))
 
 

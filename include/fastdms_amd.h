@@ -38,6 +38,11 @@ int fdms_copy_bytes(const void* src, void* dst, int64_t nbytes, int num_blocks, 
  * compact_kv.py:243-252, for exhaustive tests). */
 int fdms_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 
+/* Decode n (multiple of 4) FP8 e4m3fn bytes to fp32 with the hardware
+ * conversion the attention kernels use (no reference counterpart: lets a test
+ * check that instruction against the format on all 256 codes). */
+int fdms_fp8_decode_hw(const void* in, float* out, int64_t n, void* stream);
+
 /* A1 — DMS decision extraction.  Replaces _extract_dms_eviction_decisions_kernel
  * and the CUDA branch of extract_dms_eviction_decisions (fastdms/engine/dms.py:12-42,
  * 196-220).  evict[t,h] = q[t, h*G, D-1] > threshold (positive_scale, threshold =

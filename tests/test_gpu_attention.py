@@ -190,3 +190,124 @@ def test_argument_errors():
         compact_decode_attention(q, kv, torch.zeros((4, 8), device="cuda"), meta, meta, max_live_count=1)
     with pytest.raises(ValueError):
         compact_decode_attention(q, kv, kv, meta, meta[:, :1].expand(1, 3), max_live_count=1)
+
+
+def test_fp8_hardware_decode_is_e4m3fn():
+    """v_cvt_pk_f32_fp8 (used by the tiled kernel) decodes OCP e4m3fn: all 256
+    codes in each byte position of a dword, NaN codes included."""
+    require_gpu()
+    from fastdms_amd import _native as nat
+    codes = np.arange(256, dtype=np.uint8)
+    data = np.stack([np.roll(codes, s) for s in range(4)], axis=1).reshape(-1)  # every code at every byte lane
+    src = torch.from_numpy(data).cuda()
+    out = torch.empty(data.size, device="cuda", dtype=torch.float32)
+    nat.call("fdms_fp8_decode_hw", src.data_ptr(), out.data_ptr(), data.size, nat.stream())
+    torch.cuda.synchronize()
+    want = numerics.e4m3fn_decode(data)
+    got = out.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))  # bit-exact, signed zeros too
+
+
+def _span_case(rng, lives, hkv, g, d, kv_code, gap=5):
+    """Ragged spans laid out back to back with gaps in one arena."""
+    b = len(lives) // hkv
+    live = np.asarray(lives, np.int32).reshape(b, hkv)
+    base = np.zeros((b, hkv), np.int32)
+    cur = 3
+    for i in range(b):
+        for h in range(hkv):
+            base[i, h] = cur
+            cur += int(live[i, h]) + gap
+    ck = numerics.cast(rng.standard_normal((cur + 2, d)).astype(np.float32) * 2, kv_code)
+    cv = numerics.cast(rng.standard_normal((cur + 2, d)).astype(np.float32), kv_code)
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    return q, ck, cv, base, live
+
+
+@pytest.mark.parametrize("d,g,kv_code", [(64, 4, numerics.DT_FP8), (128, 4, numerics.DT_FP8),
+                                         (64, 1, numerics.DT_FP8), (64, 2, numerics.DT_FP8),
+                                         (64, 8, numerics.DT_FP8), (128, 8, numerics.DT_FP8),
+                                         (128, 1, numerics.DT_FP8), (64, 4, numerics.DT_BF16),
+                                         (128, 4, numerics.DT_BF16), (128, 8, numerics.DT_BF16)])
+@pytest.mark.parametrize("splits", [None, 1, 7])
+def test_tiled_kernel_spans(monkeypatch, d, g, kv_code, splits):
+    """The tiled fast path (bf16 q, D 64/128, G 1-8) against the float64 oracle:
+    live counts from 1 to several tiles, ragged over (b, h)."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    if splits is not None:
+        _force_splits(monkeypatch, splits)
+    rng = np.random.default_rng(d * 100 + g + kv_code)
+    hkv = 2
+    lives = [1, 2, 63, 64, 65, 255, 256, 257, 1000, 1300]
+    q, ck, cv, base, live = _span_case(rng, lives, hkv, g, d, kv_code)
+    ref = oatt.compact_decode_attention(q, ck, cv, base, live)
+    out = compact_decode_attention(from_values(q, numerics.DT_BF16), from_values(ck, kv_code),
+                                   from_values(cv, kv_code), torch.from_numpy(base).cuda(),
+                                   torch.from_numpy(live).cuda(), max_live_count=int(live.max()))
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
+    # per (b, head) too: a short span must not hide behind a long one's scale
+    got = values_of(out)
+    for i in range(got.shape[0]):
+        for hh in range(got.shape[1]):
+            e = np.abs(got[i, hh] - ref[i, hh]).max() / max(np.abs(ref[i, hh]).max(), 1e-30)
+            assert e <= TOL_LOWP, (i, hh, e)
+
+
+def test_tiled_and_generic_kernels_agree(monkeypatch):
+    """Same inputs through both kernels (FASTDMS_AMD_ATTN_GENERIC=1 selects the
+    generic one): both within bf16 rounding of each other."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention
+    rng = np.random.default_rng(5)
+    q, ck, cv, base, live = _span_case(rng, [700, 33, 1, 1200, 400, 90, 256, 512], 8, 4, 64, numerics.DT_FP8)
+    args = (from_values(q, numerics.DT_BF16), from_values(ck, numerics.DT_FP8), from_values(cv, numerics.DT_FP8),
+            torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda())
+    tiled = values_of(compact_decode_attention(*args, max_live_count=1200))
+    monkeypatch.setenv("FASTDMS_AMD_ATTN_GENERIC", "1")
+    generic = values_of(compact_decode_attention(*args, max_live_count=1200))
+    torch.cuda.synchronize()
+    assert _rel_err(tiled, generic) <= 1e-2
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_tiled_paged_and_inline_rope(d):
+    """Paged addressing and inline q RoPE through the tiled kernel."""
+    require_gpu()
+    from fastdms_amd.layers.compact_attention import compact_decode_attention, compact_decode_attention_paged
+    rng = np.random.default_rng(d)
+    q, kd, vd, bt, live, page = _config1_case(rng, b=2, hkv=4, g=4, d=d, ctx=1500)
+    ref = oatt.compact_decode_attention_paged(q, kd, vd, bt, live, page)
+    out = compact_decode_attention_paged(from_values(q, numerics.DT_BF16), from_values(kd, numerics.DT_FP8),
+                                         from_values(vd, numerics.DT_FP8), torch.from_numpy(bt).cuda(),
+                                         torch.from_numpy(live).cuda(), page)
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
+    # inline RoPE (B = 1)
+    q1 = q[:1]
+    cache = oatt.rope_cos_sin_cache(d, 4096, 500000.0)
+    pos = np.array([2999])
+    qr = q1.astype(np.float32).copy()
+    half = d // 2
+    cs = cache[pos[0], 0]
+    for hh in range(q1.shape[1]):
+        x2 = qr[0, hh, half:].copy()
+        if hh % 4 == 0:
+            x2[half - 1] = 0.0
+        y1, y2 = oatt.rotate(qr[0, hh, :half], x2, cs[:half], cs[half:])
+        qr[0, hh] = np.concatenate([y1, y2])
+    base = np.arange(4, dtype=np.int32).reshape(1, 4) * 2000
+    live1 = np.array([[700, 1, 1999, 300]], np.int32)
+    ck = numerics.cast(rng.standard_normal((8000, d)).astype(np.float32), numerics.DT_FP8)
+    cv = numerics.cast(rng.standard_normal((8000, d)).astype(np.float32), numerics.DT_FP8)
+    ref = oatt.compact_decode_attention(qr, ck, cv, base, live1)
+    out = compact_decode_attention(from_values(q1, numerics.DT_BF16), from_values(ck, numerics.DT_FP8),
+                                   from_values(cv, numerics.DT_FP8), torch.from_numpy(base).cuda(),
+                                   torch.from_numpy(live1).cuda(), max_live_count=2000,
+                                   q_rope_positions=torch.from_numpy(pos).cuda(),
+                                   q_rope_cos_sin_cache=torch.from_numpy(cache).cuda())
+    torch.cuda.synchronize()
+    assert _rel_err(values_of(out), ref) <= TOL_LOWP
