@@ -140,23 +140,73 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
   return v > bv || (v == bv && i < bi);
 }
 
-// One block per row; fp32 or bf16 logits; int64 output.
+// One 1024-thread block per row; 16-byte vector loads, four in flight per
+// thread, when the row is 16-byte aligned; fp32 or bf16 logits; int64 output.
+constexpr int kArgmaxThreads = 1024;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t stride, int n,
-                                                               int64_t* __restrict__ out) {
-  __shared__ float s_v[kThreads / kWave];
-  __shared__ int s_i[kThreads / kWave];
+struct ArgmaxVec;
+template <>
+struct ArgmaxVec<float> {
+  static constexpr int kN = 4;
+  static __device__ __forceinline__ void load(const float* p, float* v) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  }
+};
+template <>
+struct ArgmaxVec<bf16_t> {
+  static constexpr int kN = 8;
+  static __device__ __forceinline__ void load(const bf16_t* p, float* v) {
+    const uint4 x = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t stride, int n,
+                                                                     int64_t* __restrict__ out) {
+  constexpr int kW = kArgmaxThreads / kWave;
+  __shared__ float s_v[kW];
+  __shared__ int s_i[kW];
   const T* row = x + (int64_t)blockIdx.x * stride;
   float best = -INFINITY;
-  int bi = threadIdx.x < n ? (int)threadIdx.x : 0;
-  for (int j = threadIdx.x; j < n; j += kThreads) {
-    const float v = ld<T>(row + j);
-    if (argmax_better(v, j, best, bi) || j == (int)threadIdx.x) {  // first element seeds the scan
+  int bi = 0x7FFFFFFF;  // no element yet: loses every comparison
+  auto take = [&](float v, int j) {
+    if (bi == 0x7FFFFFFF || argmax_better(v, j, best, bi)) {
       best = v;
       bi = j;
     }
+  };
+  int tail = 0;
+  if (VEC) {
+    constexpr int N = ArgmaxVec<T>::kN;
+    constexpr int kU = 4;  // vectors in flight per thread
+    const int nvec = n / N;
+    for (int v0 = threadIdx.x; v0 < nvec; v0 += kArgmaxThreads * kU) {
+      float vals[kU][N];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int vi = v0 + u * kArgmaxThreads;
+        if (vi < nvec) ArgmaxVec<T>::load(row + (int64_t)vi * N, vals[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int vi = v0 + u * kArgmaxThreads;
+        if (vi < nvec) {
+#pragma unroll
+          for (int e = 0; e < N; ++e) take(vals[u][e], vi * N + e);
+        }
+      }
+    }
+    tail = nvec * N;
   }
-  if ((int)threadIdx.x >= n) bi = 0x7FFFFFFF;  // no element: loses every comparison below
+  for (int j = tail + threadIdx.x; j < n; j += kArgmaxThreads) take(ld<T>(row + j), j);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o);
@@ -173,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void argmax_rows_kernel(const T* __restri
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int i = 1; i < kThreads / kWave; ++i) {
+    for (int i = 1; i < kW; ++i) {
       if (s_i[i] != 0x7FFFFFFF && (bi == 0x7FFFFFFF || argmax_better(s_v[i], s_i[i], best, bi))) {
         best = s_v[i];
         bi = s_i[i];
@@ -188,12 +238,15 @@ FDMS_EXPORT int fdms_argmax_rows(const void* x, int dtype, int64_t stride, int64
   if (rows < 0 || n <= 0 || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   if (!x || !out) return (int)hipErrorInvalidValue;
+  const int esz = dtype == kF32 ? 4 : 2;
+  const bool vec = ((uintptr_t)x % 16) == 0 && (stride * esz) % 16 == 0;
+  const dim3 grid((unsigned)rows), block(kArgmaxThreads);
   if (dtype == kF32) {
-    hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
-                       (const float*)x, stride, n, out);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<float, true>), grid, block, 0, (hipStream_t)stream, (const float*)x, stride, n, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<float, false>), grid, block, 0, (hipStream_t)stream, (const float*)x, stride, n, out);
   } else if (dtype == kBF16) {
-    hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
-                       (const bf16_t*)x, stride, n, out);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<bf16_t, true>), grid, block, 0, (hipStream_t)stream, (const bf16_t*)x, stride, n, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<bf16_t, false>), grid, block, 0, (hipStream_t)stream, (const bf16_t*)x, stride, n, out);
   } else {
     return (int)hipErrorInvalidValue;
   }

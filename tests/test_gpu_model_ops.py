@@ -172,3 +172,22 @@ def test_prepare_decode_metadata_strided_slot_output():
     want_live[:, start:start + B] += 1
     assert torch.equal(sd.cpu(), want_slot)
     assert torch.equal(ld.cpu(), want_live)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,stride", [(1001, 1003), (77, 80), (4104, 4104), (151936, 151936), (3, 8)])
+def test_argmax_rows_tails_and_unaligned_rows(dtype, n, stride):
+    """Vector path with a scalar tail, and the scalar path for rows that are
+    not 16-byte aligned; values drawn from a few levels so ties are common."""
+    require_gpu()
+    from fastdms_amd import _native as nat
+    g = torch.Generator().manual_seed(n)
+    rows = 5
+    buf = torch.randint(0, 7, (rows, stride), generator=g).to(dtype)
+    x = buf[:, :n]
+    xd = buf.cuda()[:, :n]
+    out = torch.empty(rows, device="cuda", dtype=torch.int64)
+    nat.call("fdms_argmax_rows", xd.data_ptr(), nat.dtype_code(dtype), xd.stride(0), rows, n, out.data_ptr(),
+             nat.stream())
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == [int(torch.argmax(x[i].float())) for i in range(rows)]
