@@ -46,6 +46,8 @@ SIGNATURES: dict[str, str] = {
     "fdms_prefill_attention": "pllpllpllpllpiiiiifp",
     "fdms_rmsnorm": "pllippplplifp",
     "fdms_silu_mul": "pplip",
+    "fdms_quantize_fp8_rows": "pilliplpip",
+    "fdms_linear_small_m": "pliipilppiipfplpliiippplp",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

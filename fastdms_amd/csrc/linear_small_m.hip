@@ -1,0 +1,538 @@
+// Decode-shaped linear layers (M <= 16 rows): y[m, n] = sum_k a[m, k] * W[n, k]
+// with W in bf16 or FP8 e4m3fn + per-output-channel scale.
+//
+// Reference semantics (fastdms/layers/linear.py):
+//   bf16 weights: F.linear(x, W, bias) -> bf16(acc + bias)            (926)
+//   FP8 weights (quantize_weight_to_fp8, 813-847): W8[n, k] = fp8(W[n, k] *
+//     s[n]), s[n] = 448 / amax(W[n, :]) (1 if 0), scale_inv[n] = 1 / s[n];
+//     small-M / row1 kernels (492-632, 665-763): per-row dynamic activation
+//     quantisation x_s[m] = 448 / amax(x[m, :]), xq = fp8(x * x_s), then
+//     y = bf16(sum_k xq * W8 * (1 / x_s[m]) * scale_inv[n]), bias added in bf16.
+//
+// The activation may be produced on the fly by a fused prologue:
+//   PRO = 1: RMSNorm with the residual add of layernorm.py:19-40:
+//            f = fp32(x) + fp32(residual) (residual optional), residual_out =
+//            bf16(f) (written by workgroup 0), a = bf16(bf16(f * rsqrt(mean(f^2)
+//            + eps)) * norm_w) -- the normalised value is the unrounded sum.
+// and the output may go through a fused epilogue:
+//   EPI = 1: the weight holds [gate; up] (n = 2 * n_out rows, gate_up_proj) and
+//            the output is bf16(silu(bf16 gate) * bf16 up) (activation.py:8-11).
+//
+// MI355X mapping: one workgroup per 16-column output strip (per gate/up strip
+// pair for EPI 1) and K split; its NW waves split the workgroup's K range.  A
+// k-block is 64 columns: a lane group of 16 lanes reads 32 contiguous bytes of
+// 16 weight rows; each wave double-buffers groups of U k-blocks (the next
+// group's loads are in flight while the current one runs
+// v_mfma_f32_16x16x32_bf16 with A = 16 weight rows, B = the activation rows,
+// M <= 16 padded with zeros, C = y^T).  FP8 weights are exact in bf16, so the
+// FP8 path converts in registers and uses the same MFMA; products are exact and
+// accumulate in fp32 like the reference's FP8 dot.  The waves' C fragments are
+// summed through LDS.  When there are fewer strips than CUs, K is split across
+// workgroups: each split publishes its fragment with agent-scope atomic stores
+// and the last split of a strip to arrive (device-scope ticket) sums them and
+// runs the epilogue, then resets its ticket.  HBM-bound on W.
+#include "fdms_vec.h"
+
+using namespace fdms;
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kKB = 64;       // k-block: columns per lane group step
+constexpr int kMaxM = 16;
+constexpr float kFp8Max = 448.0f;
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const __bf16 x = (__bf16)a, y = (__bf16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+__device__ __forceinline__ float rbf(float a) { return (float)(__bf16)a; }  // round to bf16
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+template <typename WT> struct WBlock;
+// bf16 weights: a lane group reads 16 bf16 = 32 B per k-block
+template <> struct WBlock<bf16_t> {
+  static constexpr int kLoads = 2;
+  static __device__ __forceinline__ void to_ops(const uint4* r, uint4* op0, uint4* op1) {
+    *op0 = r[0];
+    *op1 = r[1];
+  }
+};
+// FP8 weights: 16 fp8 = 16 B per k-block, converted to two bf16x8 operands
+template <> struct WBlock<fp8_t> {
+  static constexpr int kLoads = 1;
+  static __device__ __forceinline__ void to_ops(const uint4* r, uint4* op0, uint4* op1) {
+    const uint32_t w[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+      o[2 * i] = pack2(lo[0], lo[1]);   // fp8 values are exact in bf16
+      o[2 * i + 1] = pack2(hi[0], hi[1]);
+    }
+    *op0 = uint4{o[0], o[1], o[2], o[3]};
+    *op1 = uint4{o[4], o[5], o[6], o[7]};
+  }
+};
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// 8 bf16 of x (+ 8 of r when r != nullptr) as fp32 sums
+__device__ __forceinline__ void load_sum8(const bf16_t* x, const bf16_t* r, float* f) {
+  const uint4 v = *reinterpret_cast<const uint4*>(x);
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf_lo(u[i]);
+    f[2 * i + 1] = bf_hi(u[i]);
+  }
+  if (r) {
+    const uint4 q = *reinterpret_cast<const uint4*>(r);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] += bf_lo(w[i]);
+      f[2 * i + 1] += bf_hi(w[i]);
+    }
+  }
+}
+
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Row statistics of the RMSNorm prologue / activation quantisation for row m,
+// computed by one wave with every load of a batch in flight together.
+template <int PRO, bool QX>
+__device__ __forceinline__ void row_stats(const bf16_t* xr, const bf16_t* rr, const bf16_t* norm_w, int K, float eps,
+                                          int lane, bf16_t* res_out_row, float* inv_out, float* xs_out) {
+  constexpr int kB = 8;  // 16-byte chunks per lane per batch
+  float inv = 1.0f;
+  if (PRO == 1) {
+    float ss = 0.0f;
+    for (int k0 = lane * 8; k0 < K; k0 += 64 * 8 * kB) {
+      float f[kB][8];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int k = k0 + j * 64 * 8;
+        if (k < K) load_sum8(xr + k, rr ? rr + k : nullptr, f[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int k = k0 + j * 64 * 8;
+        if (k < K) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss += f[j][i] * f[j][i];
+          if (res_out_row) {
+            *reinterpret_cast<uint4*>(res_out_row + k) =
+                uint4{pack2(f[j][0], f[j][1]), pack2(f[j][2], f[j][3]), pack2(f[j][4], f[j][5]), pack2(f[j][6], f[j][7])};
+          }
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    inv = 1.0f / sqrtf(ss / (float)K + eps);
+  }
+  float amax = 0.0f;
+  if (QX) {
+    for (int k0 = lane * 8; k0 < K; k0 += 64 * 8 * kB) {
+      float f[kB][8];
+      uint4 wv[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int k = k0 + j * 64 * 8;
+        if (k < K) {
+          load_sum8(xr + k, (PRO == 1 && rr) ? rr + k : nullptr, f[j]);
+          if (PRO == 1) wv[j] = *reinterpret_cast<const uint4*>(norm_w + k);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int k = k0 + j * 64 * 8;
+        if (k < K) {
+          const uint32_t uw[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float a = f[j][i];
+            if (PRO == 1) a = rbf(rbf(a * inv) * ((i & 1) ? bf_hi(uw[i >> 1]) : bf_lo(uw[i >> 1])));
+            amax = fmaxf(amax, fabsf(a));
+          }
+        }
+      }
+    }
+    amax = wave_max(amax);
+  }
+  *inv_out = inv;
+  *xs_out = (amax > 0.0f) ? kFp8Max / amax : 1.0f;
+}
+
+}  // namespace
+
+// y[m, n] = a[m, :] . W[n, :] for one 16-column strip (two for EPI 1) and one
+// K split.  EPI 0: y = the finalised value.  EPI 1 (gate_up): the workgroup
+// computes gate strip n0 and up strip n0 + n_out and writes
+// bf16(silu(bf16 gate) * bf16 up) -- gate_up followed by SiluAndMul.
+template <typename WT, int PRO, bool QX, int EPI, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
+    const bf16_t* __restrict__ x, int64_t x_s, int M, int K, const WT* __restrict__ w, int64_t w_s,
+    const float* __restrict__ w_scale_inv, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ norm_w,
+    float eps, const bf16_t* __restrict__ res, int64_t res_s, bf16_t* __restrict__ res_out, int64_t ro_s,
+    bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
+    int* __restrict__ counters) {
+  constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
+  __shared__ float s_inv[kMaxM], s_xs[kMaxM];
+  __shared__ f32x4 s_acc[NA][NW][64];
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  // XCD-aware (strip, split): the K splits of one strip run on the same XCD
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds;
+  const int slot = lin / kXcds;
+  const int strip = (slot / ksplit) * kXcds + xcd;
+  const int ks = slot - (slot / ksplit) * ksplit;
+  if (strip >= strips) return;  // uniform per workgroup
+  const int n0 = strip * 16;
+
+  const int kc = K / ksplit;            // this workgroup's K range
+  const int kw = kc / NW;               // this wave's part of it
+  const int kw0 = ks * kc + wave * kw;
+  const int kend = kw0 + kw;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const WT* wrow[NA];
+  wrow[0] = w + (int64_t)(n0 + c) * w_s;
+  if (EPI == 1) wrow[NA - 1] = w + (int64_t)(n0 + n_out + c) * w_s;
+  const bool has_row = c < M;
+  const bf16_t* xrow = x + (int64_t)(has_row ? c : 0) * x_s;
+  const bf16_t* rrow = (PRO == 1 && res) ? res + (int64_t)(has_row ? c : 0) * res_s : nullptr;
+  float inv = 1.0f, xsc = 1.0f;  // row statistics, read after the stats pass below
+  f32x4 acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  struct Buf {
+    uint4 w[NA][U][WBlock<WT>::kLoads];
+    uint4 x[U][2];
+    uint4 r[U][2];   // residual (PRO 1)
+    uint4 nw[U][2];  // norm weight (PRO 1)
+  };
+  auto load = [&](int kb0, Buf& b) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = kb0 + u * kKB + 16 * g;
+      if (kb0 + u * kKB < kend) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint4* wp = reinterpret_cast<const uint4*>(wrow[a] + k);
+#pragma unroll
+          for (int j = 0; j < WBlock<WT>::kLoads; ++j) b.w[a][u][j] = wp[j];
+        }
+        b.x[u][0] = b.x[u][1] = b.r[u][0] = b.r[u][1] = uint4{0u, 0u, 0u, 0u};
+        if (has_row) {
+          const uint4* xp = reinterpret_cast<const uint4*>(xrow + k);
+          b.x[u][0] = xp[0];
+          b.x[u][1] = xp[1];
+          if (PRO == 1) {
+            const uint4* np = reinterpret_cast<const uint4*>(norm_w + k);
+            b.nw[u][0] = np[0];
+            b.nw[u][1] = np[1];
+            if (rrow) {
+              const uint4* rp = reinterpret_cast<const uint4*>(rrow + k);
+              b.r[u][0] = rp[0];
+              b.r[u][1] = rp[1];
+            }
+          }
+        }
+      }
+    }
+  };
+  auto compute = [&](int kb0, const Buf& b) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kb0 + u * kKB >= kend) break;
+      uint4 bo[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (PRO == 0 && !QX) {
+          bo[h] = b.x[u][h];
+        } else {
+          const uint32_t v[4] = {b.x[u][h].x, b.x[u][h].y, b.x[u][h].z, b.x[u][h].w};
+          const uint32_t q[4] = {b.nw[u][h].x, b.nw[u][h].y, b.nw[u][h].z, b.nw[u][h].w};
+          const uint32_t rs[4] = {b.r[u][h].x, b.r[u][h].y, b.r[u][h].z, b.r[u][h].w};
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float lo = bf_lo(v[i]), hi = bf_hi(v[i]);
+            if (PRO == 1) {
+              lo = rbf(rbf((lo + bf_lo(rs[i])) * inv) * bf_lo(q[i]));
+              hi = rbf(rbf((hi + bf_hi(rs[i])) * inv) * bf_hi(q[i]));
+            }
+            if (QX) {  // fp8 quantised activation, exact in bf16
+              lo = fp8_to_f32(f32_to_fp8(lo * xsc));
+              hi = fp8_to_f32(f32_to_fp8(hi * xsc));
+            }
+            o[i] = pack2(lo, hi);
+          }
+          bo[h] = uint4{o[0], o[1], o[2], o[3]};
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        uint4 a0, a1;
+        WBlock<WT>::to_ops(b.w[a][u], &a0, &a1);
+        acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(bo[0]), acc[a], 0, 0, 0);
+        acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(bo[1]), acc[a], 0, 0, 0);
+      }
+    }
+  };
+
+  Buf cur, nxt;
+  if (kw0 < kend) load(kw0, cur);  // the first weight group is in flight during the stats pass
+
+  if (PRO == 1 || QX) {
+    for (int m = wave; m < M; m += NW) {
+      float inv, xs;
+      row_stats<PRO, QX>(x + (int64_t)m * x_s, (PRO == 1 && res) ? res + (int64_t)m * res_s : nullptr, norm_w, K,
+                         eps, lane, (res_out && blockIdx.x == 0) ? res_out + (int64_t)m * ro_s : nullptr, &inv, &xs);
+      if (lane == 0) {
+        s_inv[m] = inv;
+        s_xs[m] = xs;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (PRO == 1 && has_row) inv = s_inv[c];
+  if (QX && has_row) xsc = s_xs[c];
+  for (int kb0 = kw0; kb0 < kend; kb0 += U * kKB) {
+    const bool more = kb0 + U * kKB < kend;
+    if (more) load(kb0 + U * kKB, nxt);  // next group in flight while this one computes
+    compute(kb0, cur);
+    if (more) cur = nxt;
+  }
+
+  // ---- reduce the waves' C fragments; lane l holds C[n = 4*(l/16) + r][m = l%16]
+#pragma unroll
+  for (int a = 0; a < NA; ++a) s_acc[a][wave][lane] = acc[a];
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 t[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) {
+    t[a] = s_acc[a][0][lane];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) {
+      const f32x4 o = s_acc[a][w2][lane];
+      t[a][0] += o[0];
+      t[a][1] += o[1];
+      t[a][2] += o[2];
+      t[a][3] += o[3];
+    }
+  }
+  if (ksplit > 1) {
+    // split-K: publish this split's fragments (agent-coherent stores), the last
+    // split of the strip to arrive sums them all
+    float* mine = ws + ((int64_t)strip * ksplit + ks) * (NA * 256);
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) store_agent(mine + a * 256 + lane * 4 + r, t[a][r]);
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) s_last = (atomicAdd(&counters[strip], 1) == ksplit - 1);
+    __builtin_amdgcn_wave_barrier();
+    if (!s_last) return;
+    const float* all = ws + (int64_t)strip * ksplit * (NA * 256);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) t[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ksplit; s0 += 4) {
+      float v[4][NA][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[j][a][r] = (s0 + j < ksplit) ? load_agent(all + (s0 + j) * (NA * 256) + a * 256 + lane * 4 + r) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t[a][r] += v[j][a][r];
+    }
+    if (lane == 0) __hip_atomic_store(&counters[strip], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const int m = lane & 15;
+  if (m >= M) return;
+  const float xsi = QX ? 1.0f / s_xs[m] : 1.0f;
+  auto finalize = [&](float acc_v, int n) {
+    float v;
+    if (sizeof(WT) == 1 || QX) {
+      v = acc_v * xsi;
+      if (sizeof(WT) == 1) v *= w_scale_inv[n];
+      v = rbf(v);
+      if (bias) v = rbf(v + ld<bf16_t>(bias + n));
+    } else {
+      v = rbf(acc_v + (bias ? ld<bf16_t>(bias + n) : 0.0f));
+    }
+    return v;
+  };
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = n0 + 4 * (lane >> 4) + r;
+    float v;
+    if (EPI == 1) {
+      const float gt = finalize(t[0][r], n);
+      const float up = finalize(t[NA - 1][r], n + n_out);
+      v = rbf(silu(gt) * up);
+    } else {
+      v = finalize(t[0][r], n);
+    }
+    y[(int64_t)m * y_s + n].bits = __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+}
+
+namespace {
+
+struct LinArgs {
+  const bf16_t* x; int64_t x_s; int M, K; const void* w; int64_t w_s; const float* wsi; const bf16_t* bias;
+  const bf16_t* norm_w; float eps; const bf16_t* res; int64_t res_s; bf16_t* res_out; int64_t ro_s;
+  bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters;
+};
+
+template <typename WT, int PRO, bool QX, int EPI>
+void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
+  const WT* w = (const WT*)a.w;
+  constexpr int U = (PRO == 1 || QX) ? 2 : 4;  // k-blocks per double-buffered group (register budget)
+#define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
+                      a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters
+  if (nw == 8) {
+    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
+  } else {
+    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 4, U>), grid, dim3(256), 0, st, FDMS_LIN_ARGS);
+  }
+#undef FDMS_LIN_ARGS
+}
+
+template <typename WT>
+void dispatch_linear(int prologue, int qx, int epi, int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
+#define FDMS_LIN_E(P, Q) \
+  if (epi) launch_linear<WT, P, Q, 1>(nw, grid, st, a); else launch_linear<WT, P, Q, 0>(nw, grid, st, a)
+#define FDMS_LIN_Q(P) \
+  if (qx) { FDMS_LIN_E(P, true); } else { FDMS_LIN_E(P, false); }
+  if (prologue == 1) {
+    FDMS_LIN_Q(1);
+  } else {
+    FDMS_LIN_Q(0);
+  }
+#undef FDMS_LIN_E
+#undef FDMS_LIN_Q
+}
+
+}  // namespace
+
+FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const void* w, int w_dtype,
+                                    int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int prologue,
+                                    const void* norm_weight, float eps, const void* residual, int64_t res_stride,
+                                    void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue,
+                                    int k_splits, float* workspace, int* counters, void* y, int64_t y_stride,
+                                    void* stream) {
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 || epilogue > 1)
+    return (int)hipErrorInvalidValue;
+  if (m == 0 || n == 0) return 0;
+  if (!x || !w || !y || (prologue == 1 && !norm_weight)) return (int)hipErrorInvalidValue;
+  if (w_dtype != kBF16 && w_dtype != kFP8) return (int)hipErrorInvalidValue;
+  if (w_dtype == kFP8 && !w_scale_inv) return (int)hipErrorInvalidValue;
+  if (prologue != 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
+  // other workgroups still read x / residual while workgroup 0 writes residual_out
+  if (residual_out && (residual_out == residual || residual_out == x)) return (int)hipErrorInvalidValue;
+  if (y == x || (residual && y == residual)) return (int)hipErrorInvalidValue;
+  // n = weight rows; epilogue 1 pairs row n0 with n0 + n/2 and writes n/2 columns
+  const int n_out = epilogue == 1 ? n / 2 : n;
+  if (n_out % 16 || (epilogue == 1 && n % 2)) return (int)hipErrorInvalidValue;
+  if (k_splits < 1 || k_splits > 64) return (int)hipErrorInvalidValue;
+  if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
+  const int kc = k / k_splits;
+  if (k % k_splits) return (int)hipErrorInvalidValue;
+  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;  // whole k-blocks per wave
+  const int wsz = w_dtype == kFP8 ? 1 : 2;
+  auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+  if (!al16(x) || !al16(w) || (x_stride * 2) % 16 || (w_stride * wsz) % 16) return (int)hipErrorInvalidValue;
+  if (prologue == 1 && (!al16(norm_weight) || (residual && (!al16(residual) || (res_stride * 2) % 16)) ||
+                        (residual_out && (!al16(residual_out) || (res_out_stride * 2) % 16))))
+    return (int)hipErrorInvalidValue;
+  if (x_stride < k || w_stride < k || y_stride < n_out) return (int)hipErrorInvalidValue;
+  if ((residual && res_stride < k) || (residual_out && res_out_stride < k)) return (int)hipErrorInvalidValue;
+  const int strips = n_out / 16;
+  const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks);
+  const LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias,
+                  (const bf16_t*)norm_weight, eps, (const bf16_t*)residual, res_stride, (bf16_t*)residual_out,
+                  res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters};
+  if (w_dtype == kFP8) {
+    dispatch_linear<fp8_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
+  } else {
+    dispatch_linear<bf16_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
+  }
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Per-row FP8 quantisation (linear.py:386-388, 813-823 for weight rows;
+// 514-523, 683-694, 652-654 for activation rows): s = 448 / amax(row) (1 when
+// the row is all zero), q = e4m3fn(v * s) rounded to nearest even, scale_inv =
+// 1 / s.  torch_form selects how 448 / amax is rounded: the reference's torch
+// expressions (weights, _fp8_linear) evaluate reciprocal(amax) * 448; its
+// Triton kernels divide directly.  One workgroup per row.
+template <typename TI>
+__global__ __launch_bounds__(256) void quantize_fp8_rows_kernel(const TI* __restrict__ in, int64_t in_s, int k,
+                                                                uint8_t* __restrict__ out, int64_t out_s,
+                                                                float* __restrict__ scale_inv, int torch_form) {
+  __shared__ float s_red[256 / kWave];
+  const int64_t row = blockIdx.x;
+  const TI* r = in + row * in_s;
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(ld<TI>(r + j)));
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  // torch's tensor expression 448 / amax is reciprocal(amax) * 448 (two roundings)
+  const float sc = amax > 0.0f ? (torch_form ? (1.0f / amax) * kFp8Max : kFp8Max / amax) : 1.0f;
+  uint8_t* o = out + row * out_s;
+  for (int j = threadIdx.x; j < k; j += 256) o[j] = (uint8_t)f32_to_fp8(ld<TI>(r + j) * sc);
+  if (threadIdx.x == 0) scale_inv[row] = 1.0f / sc;
+}
+
+FDMS_EXPORT int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int64_t rows, int k,
+                                       void* out, int64_t out_stride, float* scale_inv, int torch_form,
+                                       void* stream) {
+  if (rows < 0 || k <= 0 || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!in || !out || !scale_inv || in_stride < k || out_stride < k) return (int)hipErrorInvalidValue;
+  if (in_dtype == kBF16) {
+    hipLaunchKernelGGL(quantize_fp8_rows_kernel<bf16_t>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)in, in_stride, k, (uint8_t*)out, out_stride, scale_inv, torch_form);
+  } else if (in_dtype == kF32) {
+    hipLaunchKernelGGL(quantize_fp8_rows_kernel<float>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)in, in_stride, k, (uint8_t*)out, out_stride, scale_inv, torch_form);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}

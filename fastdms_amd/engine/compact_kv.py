@@ -571,6 +571,12 @@ class CompactKVManager:
                 raise ValueError("explicit compact_k/compact_v apply only to single-tensor storage")
             self.compact_k, self.compact_v = compact_k, compact_v
             self._layer_ptrs = None
+        if action == "skip" and not sync_stats:
+            # compact_kv.py:1363-1379: a skipped step without synced stats touches no device memory
+            for st, cur in zip(states, current_positions):
+                st.last_dms_expiry_position = int(cur)
+            return {"evicted_tokens": 0, "live_tokens_before_min": 0, "live_tokens_before_max": 0,
+                    "live_tokens_after_min": 0, "live_tokens_after_max": 0}
         live_before = self._stack_live(states)
         if action != "skip":
             self._run_expiry(states, current_positions, window_size, incremental=(action == "incremental"))
@@ -588,8 +594,6 @@ class CompactKVManager:
         stats = {"evicted_tokens": evicted, "live_tokens_before_min": live_before.min(),
                  "live_tokens_before_max": live_before.max(), "live_tokens_after_min": live_after.min(),
                  "live_tokens_after_max": live_after.max()}
-        if action == "skip" and not sync_stats:
-            return {key: 0 for key in stats}
         if sync_stats:
             return {key: int(value.item()) for key, value in stats.items()}
         return stats

@@ -19,6 +19,7 @@ import torch
 from .. import _native as nat
 from ..config import Config
 from ..layers.compact_attention import reserve_attention_workspace
+from ..layers.linear import reserve_linear_workspace
 from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
 from .compact_kv import CompactKVManager
@@ -48,6 +49,8 @@ class ModelRunner:
         self.allocate_kv_cache()
         reserve_attention_workspace(self.device, self.max_num_seqs * self.num_kv_heads,
                                     hf.num_attention_heads // hf.num_key_value_heads, hf.head_dim)
+        reserve_linear_workspace(self.device, max(hf.vocab_size, 2 * hf.intermediate_size,
+                                                  (hf.num_attention_heads + 2 * hf.num_key_value_heads) * hf.head_dim))
         self.evict_buffer = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads),
                                         device=self.device, dtype=torch.bool)
         self.static_input_ids = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
@@ -171,9 +174,13 @@ class ModelRunner:
                     dms_layer_evictions_buffer=evict)
         ids = self.static_input_ids[:batch]
         pos = self.static_positions[:batch]
-        hidden = self.model(ids, pos)
-        head = self.model.lm_head
-        logits = head.quant(hidden, None) if head.quant is not None else torch.nn.functional.linear(hidden, head.weight)
+        if self.model.decode_fused_supported(batch):
+            logits = self.model.forward_decode_fused(ids, pos)
+        else:
+            hidden = self.model(ids, pos)
+            head = self.model.lm_head
+            logits = (head.quant(hidden, None) if head.quant is not None
+                      else torch.nn.functional.linear(hidden, head.weight))
         nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0), batch,
                  logits.shape[1], self.static_tokens.data_ptr(), nat.stream())
         p, e = mgr.layer_major_token_positions, mgr.layer_major_evict_mask.view(torch.uint8)

@@ -29,6 +29,10 @@ class ParallelLMHead(VocabParallelEmbedding):
         self.quant = None
         self.last_logits: torch.Tensor | None = None
         assert not bias
+        # linear-layer view of the head (the decode step runs it as a fused linear)
+        self.input_size, self.output_size = embedding_dim, num_embeddings
+        self.bias = None
+        self._fp8_weight_enabled = False
 
     def _last_rows(self, x: torch.Tensor) -> torch.Tensor:
         ctx = get_context()

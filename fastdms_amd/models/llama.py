@@ -21,7 +21,8 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
                                         fused_dms_rope_store_compact_decode)
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm, rms_norm
-from ..layers.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
+from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
+                             QKVParallelLinear, RowParallelLinear, linear_small_m, small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -50,6 +51,20 @@ class ModelConfig:
     dtype: str = "bfloat16"
 
 
+def _fused_linear(lin: LinearBase, x: torch.Tensor, prologue: int, norm: RMSNorm | None = None,
+                  residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
+                  epilogue: int = EPI_NONE) -> torch.Tensor:
+    """One fdms_linear_small_m launch for a decode-shaped linear layer, with its
+    bf16 or FP8 weights and optional fused prologue / epilogue."""
+    if lin._fp8_weight_enabled:
+        w, sinv = lin.weight_fp8, lin.weight_scale_inv
+    else:
+        w, sinv = lin.weight, None
+    return linear_small_m(x, w, lin.bias, weight_scale_inv=sinv, prologue=prologue,
+                          norm_weight=None if norm is None else norm.weight, eps=1e-6 if norm is None else norm.eps,
+                          residual=residual, residual_out=residual_out, epilogue=epilogue)
+
+
 class LlamaAttention(nn.Module):
 
     def __init__(self, config: ModelConfig) -> None:
@@ -73,6 +88,10 @@ class LlamaAttention(nn.Module):
 
     def forward(self, positions: torch.Tensor, hidden_states: torch.Tensor) -> torch.Tensor:
         qkv = self.qkv_proj(hidden_states)
+        return self.o_proj(self.attend(positions, qkv))
+
+    def attend(self, positions: torch.Tensor, qkv: torch.Tensor) -> torch.Tensor:
+        """Everything between the qkv and o projections; returns [T, Hq*D]."""
         q = qkv[:, :self.q_size].view(-1, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size:self.q_size + self.kv_size].view(-1, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
@@ -124,7 +143,7 @@ class LlamaAttention(nn.Module):
                 cu_seqlens_host=ctx.cu_seqlens_q_host)
         o = self.attn(q, k, v, compact_append_stored=fused, compact_q_rope=fused and inline_q_rope,
                       positions=positions, cos_sin_cache=self.rotary_emb.cos_sin_cache)
-        return self.o_proj(o.view(o.shape[0], -1))
+        return o.view(o.shape[0], -1)
 
 
 class LlamaMLP(nn.Module):
@@ -174,6 +193,39 @@ class LlamaModel(nn.Module):
         hidden_states, _ = self.norm(hidden_states, residual)
         return hidden_states
 
+    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor,
+                             lm_head: LinearBase) -> torch.Tensor:
+        """The decode step (same math as forward + LM head) on the decode-shaped
+        linear kernel: per layer RMSNorm(+residual add), qkv, attention, o_proj,
+        RMSNorm(+add), gate_up with SiLU*up as its epilogue, down_proj; then the
+        final RMSNorm(+add) and the LM head.  Returns the logits [rows, vocab].
+
+        (The RMSNorm stays a kernel of its own: folded into the GEMM prologue,
+        every workgroup would re-read and re-normalise the whole activation,
+        which costs more at M <= 16 than the launch it saves.)"""
+        x = self.embed_tokens(input_ids)
+        res = None
+        for layer in self.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            if res is None:
+                h, res = layer.input_layernorm(x), x
+            else:
+                h, res = layer.input_layernorm(x, res)
+            qkv = _fused_linear(attn.qkv_proj, h, PRO_NONE)
+            o = _fused_linear(attn.o_proj, attn.attend(positions, qkv), PRO_NONE)
+            h, res = layer.post_attention_layernorm(o, res)
+            act = _fused_linear(mlp.gate_up_proj, h, PRO_NONE, epilogue=EPI_SILU_MUL)
+            x = _fused_linear(mlp.down_proj, act, PRO_NONE)
+        h, _ = self.norm(x, res)
+        return _fused_linear(lm_head, h, PRO_NONE)
+
+    def decode_fused_supported(self, rows: int, lm_head: LinearBase) -> bool:
+        mods = [lm_head]
+        for layer in self.layers:
+            mods += [layer.self_attn.qkv_proj, layer.self_attn.o_proj, layer.mlp.gate_up_proj, layer.mlp.down_proj]
+        return all(m.quant is None and small_m_supported(rows, m.input_size, m.output_size) for m in mods) and all(
+            layer.mlp.gate_up_proj.output_size % 32 == 0 for layer in self.layers)
+
 
 class LlamaForCausalLM(nn.Module):
     packed_modules_mapping = {"q_proj": ("qkv_proj", "q"), "k_proj": ("qkv_proj", "k"),
@@ -196,6 +248,13 @@ class LlamaForCausalLM(nn.Module):
 
     def compute_greedy_token_ids(self, hidden_states: torch.Tensor) -> torch.Tensor:
         return self.lm_head.greedy_token_ids(hidden_states)
+
+    def decode_fused_supported(self, rows: int) -> bool:
+        return self.model.decode_fused_supported(rows, self.lm_head)
+
+    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """Decode step through the decode-shaped linear kernels; returns the logits."""
+        return self.model.forward_decode_fused(input_ids, positions, self.lm_head)
 
 
 Qwen3ForCausalLM = LlamaForCausalLM  # the same glue with config.qk_norm = True

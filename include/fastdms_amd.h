@@ -202,6 +202,38 @@ int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
  * and the torch argmax of ParallelLMHead.greedy_token_ids, 491-543). */
 int fdms_argmax_rows(const void* x, int dtype, int64_t stride, int64_t rows, int n, int64_t* out, void* stream);
 
+/* C1 — per-row FP8 quantisation.  Replaces LinearBase.quantize_weight_to_fp8 /
+ * _amax_to_scale (fastdms/layers/linear.py:386-388, 813-823) for weight rows
+ * [N, K] and the per-row dynamic activation quantisation of the FP8 paths
+ * (514-523, 683-694, 652-654): s = 448/amax(row) (1 if zero), out = e4m3fn(v*s)
+ * (RNE), scale_inv[row] = 1/s.  in_dtype bf16 or f32.  torch_form = 1 rounds
+ * 448/amax the way the reference's torch expressions evaluate it
+ * (reciprocal(amax) * 448: weights, _fp8_linear); 0 divides directly (its
+ * Triton kernels). */
+int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int64_t rows, int k, void* out,
+                           int64_t out_stride, float* scale_inv, int torch_form, void* stream);
+
+/* C2 / C3 / C6 (decode rows) — y[m,n] = a[m,:] . W[n,:] for m <= 16 rows.
+ * Replaces _fp8_row1_matvec(_dot)_kernel and _fp8_small_m_linear_kernel
+ * (linear.py:492-632, 665-763) for w_dtype FP8 (W row-major [N, K] = the
+ * reference's column-major W8^T [K, N], per-row scale_inv [N]; quantize_x = the
+ * per-row dynamic activation quantisation, 448/amax divided directly as its
+ * Triton kernels do; y = bf16(acc/x_s*scale_inv), bias added in bf16), and the
+ * BF16 F.linear of the decode step (linear.py:926; y = bf16(acc + bias)) for
+ * w_dtype bf16.  prologue 1 = RMSNorm of x (+ residual, fp32 sum; the bf16 sum
+ * goes to residual_out, written by one workgroup; layernorm.py:19-40).
+ * epilogue 1 = W is [gate; up] (n rows), the output has n/2 columns
+ * bf16(silu(gate) * up) (activation.py:8-11).  k_splits > 1 splits K over
+ * workgroups: workspace holds (n_out/16) * k_splits * 256 floats (x2 for
+ * epilogue 1) and counters n_out/16 ints, zero before the first call and left
+ * zero.  k / k_splits a multiple of 256, n_out of 16, 16-byte aligned rows; y
+ * and residual_out must not alias x / residual. */
+int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const void* w, int w_dtype,
+                        int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int prologue,
+                        const void* norm_weight, float eps, const void* residual, int64_t res_stride,
+                        void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue, int k_splits,
+                        float* workspace, int* counters, void* y, int64_t y_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,17 +16,26 @@ from . import numerics
 FP8_MAX = np.float32(448.0)
 
 
-def amax_to_scale(amax) -> np.ndarray:
-    """linear.py:386-388: 448/amax in fp32, 1 where amax == 0."""
+def amax_to_scale(amax, torch_form: bool = True) -> np.ndarray:
+    """448/amax in fp32, 1 where amax == 0.
+
+    torch_form: the reference's tensor expression ``_FP8_MAX / amax``
+    (linear.py:386-388) evaluates as torch's ``__rtruediv__``, i.e.
+    reciprocal(amax) * 448 with two fp32 roundings.  The Triton kernels
+    (linear.py:514-523, 683-694) divide in fp32 directly (torch_form=False).
+    """
     a = np.asarray(amax, dtype=np.float32)
-    with np.errstate(divide="ignore"):
-        s = np.where(a > 0, FP8_MAX / np.where(a > 0, a, 1), np.float32(1.0))
-    return s.astype(np.float32)
+    safe = np.where(a > 0, a, np.float32(1.0)).astype(np.float32)
+    if torch_form:
+        q = ((np.float32(1.0) / safe).astype(np.float32) * FP8_MAX).astype(np.float32)
+    else:
+        q = (FP8_MAX / safe).astype(np.float32)
+    return np.where(a > 0, q, np.float32(1.0)).astype(np.float32)
 
 
 def quantize_weight_to_fp8(weight):
-    """linear.py:813-823: per output channel scale; W8^T [K, N] e4m3 bits and
-    scale_inv [1, N] = 1/scale in fp32."""
+    """linear.py:813-823: per output channel scale (torch form); W8^T [K, N]
+    e4m3 bits and scale_inv [1, N] = reciprocal(scale) in fp32."""
     w = np.asarray(weight, dtype=np.float32)             # [N, K]
     scale = amax_to_scale(np.abs(w).max(axis=1))         # [N]
     w8_t = numerics.e4m3fn_encode((w.T * scale[None, :]).astype(np.float32))  # [K, N]
@@ -34,29 +43,30 @@ def quantize_weight_to_fp8(weight):
     return w8_t, scale_inv
 
 
-def quantize_rows_fp8(x):
-    """Per-row dynamic activation quantisation (linear.py:514-523, 683-694):
-    x_scale = 448/amax(row), xq = e4m3(x * x_scale).  Returns (xq bits, x_scale)."""
+def quantize_rows_fp8(x, torch_form: bool = False):
+    """Per-row dynamic activation quantisation: x_scale = 448/amax(row), xq =
+    e4m3(x * x_scale).  torch_form=False: the row-1 / small-M Triton kernels
+    (linear.py:514-523, 683-694); True: _fp8_linear (652-654).  Returns (xq bits, x_scale)."""
     x = np.asarray(x, dtype=np.float32)
-    x_scale = amax_to_scale(np.abs(x).max(axis=-1))
+    x_scale = amax_to_scale(np.abs(x).max(axis=-1), torch_form=torch_form)
     xq = numerics.e4m3fn_encode((x * x_scale[..., None]).astype(np.float32))
     return xq, x_scale
 
 
-def fp8_linear(x, w8_t, scale_inv, quantize_x: bool = True):
+def fp8_linear(x, w8_t, scale_inv, quantize_x: bool = True, torch_form: bool = False):
     """y[m, n] = sum_k xq[m,k] w8[k,n] * (1/x_scale[m]) * scale_inv[n].
 
     Covers the row-1 (linear.py:492-578), small-M (665-719) and _scaled_mm
-    (635-662) paths, which share this closed form; with quantize_x=False the
-    activation is used unquantised (linear.py:509-527 QUANTIZE_X=False).
-    Returns float64 [M, N].
+    (635-662, torch_form=True) paths, which share this closed form; with
+    quantize_x=False the activation is used unquantised (linear.py:509-527
+    QUANTIZE_X=False).  Returns float64 [M, N].
     """
     x = np.atleast_2d(np.asarray(x, dtype=np.float32))
     w = numerics.e4m3fn_decode(w8_t).astype(np.float64)
     if quantize_x:
-        xq, xs = quantize_rows_fp8(x)
+        xq, xs = quantize_rows_fp8(x, torch_form=torch_form)
         xv = numerics.e4m3fn_decode(xq).astype(np.float64)
-        inv = 1.0 / xs.astype(np.float64)
+        inv = (np.float32(1.0) / xs).astype(np.float64)
     else:
         xv = x.astype(np.float64)
         inv = np.ones(x.shape[0])

@@ -529,6 +529,63 @@ class Emulator:
                                                                          .to(torch.bfloat16))
         return 0
 
+    def quantize_fp8_rows(self, x, dt, x_s, rows, k, out, out_s, scale_inv, torch_form, stream):
+        from oracle import linear as olin
+        if rows == 0:
+            return 0
+        xv = self.load(self.view(x, _TORCH[dt], (rows, k), (x_s, 1), "in"), dt).numpy()
+        q, xs = olin.quantize_rows_fp8(xv, torch_form=bool(torch_form))
+        self.view(out, torch.uint8, (rows, k), (out_s, 1), "out").copy_(torch.from_numpy(q))
+        sinv = (np.float32(1.0) / xs).astype(np.float32)
+        self.view(scale_inv, torch.float32, (rows,), (1,), "scale_inv").copy_(torch.from_numpy(sinv))
+        return 0
+
+    def linear_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, prologue, norm_w, eps, res, res_s,
+                       res_out, ro_s, qx, epilogue, k_splits, ws, counters, y, y_s, stream):
+        """Same expressions as oracle/model.py (rmsnorm, mlp, linear) and oracle/linear.py."""
+        from oracle import linear as olin
+        if m == 0 or n == 0:
+            return 0
+        n_out = n // 2 if epilogue == 1 else n
+        if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1):
+            return 1
+        if k_splits > 1:
+            strips = n_out // 16
+            self.view(ws, torch.float32, (strips * k_splits * 256 * (2 if epilogue else 1),), (1,), "workspace")
+            cnt = self.view(counters, torch.int32, (strips,), (1,), "counters")
+            if bool((cnt != 0).any()):
+                raise OutOfBounds(f"{self.name}: split-K counters are not zero before the launch")
+        xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
+        if prologue == 1:
+            f = xv + (self.view(res, torch.bfloat16, (m, k), (res_s, 1), "residual").float() if res else 0.0)
+            if res_out:
+                self.view(res_out, torch.bfloat16, (m, k), (ro_s, 1), "residual_out").copy_(f.to(torch.bfloat16))
+            var = (f * f).mean(dim=-1, keepdim=True)
+            a = (f * (1.0 / torch.sqrt(var + eps))).to(torch.bfloat16).float()
+            nw = self.view(norm_w, torch.bfloat16, (k,), (1,), "norm_weight").float()
+            a = (a * nw).to(torch.bfloat16).float()
+        else:
+            a = xv
+        bv = self.view(bias, torch.bfloat16, (n,), (1,), "bias").float() if bias else None
+        if w_dtype == DT_FP8:
+            w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
+            si = self.view(wsi, torch.float32, (n,), (1,), "scale_inv").numpy()
+            acc = olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx))
+            out = torch.from_numpy(acc.astype(np.float32)).to(torch.bfloat16).float()
+            if bv is not None:
+                out = (out + bv).to(torch.bfloat16).float()
+        else:
+            wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float()
+            out = a @ wv.T
+            if bv is not None:
+                out = out + bv
+            out = out.to(torch.bfloat16).float()
+        if epilogue == 1:  # gate_up -> SiluAndMul, the oracle model's mlp expression
+            g, u = out[:, :n_out], out[:, n_out:]
+            out = (g / (1.0 + torch.exp(-g))) * u
+        self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
+        return 0
+
     def prefill_attention(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, num_seqs,
                           max_seqlen, hq, hkv, d, scale, stream):
         if num_seqs == 0 or max_seqlen <= 0:
@@ -624,6 +681,8 @@ def cpu_engine():
     patch(nat, "stream", lambda: 0)
     patch(nat, "require_cuda", lambda *a, **k: None)
     patch(ca, "_num_cus", lambda device: 256)
+    import fastdms_amd.layers.linear as lin
+    patch(lin, "_num_cus", lambda device: 256)
     orig_build = mr.build_synthetic_model
     patch(mr, "build_synthetic_model", lambda cfg, **k: orig_build(cfg, **{**k, "device": "cpu"}))
     try:

@@ -1,0 +1,168 @@
+"""C1-C3/C6: FP8 weight quantisation and decode-shaped linears on the GPU.
+
+Per-row FP8 quantisation is bit-exact against the oracle (linear.py:813-823).
+Linear outputs are bf16: the kernel accumulates in fp32 in MFMA order, the
+references in float64 / fp32, so each output may differ by one bf16 unit in
+the last place (plus the reference tests' FP8 tolerance for the FP8 paths).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import require_gpu
+from oracle import linear as olin
+from oracle import numerics
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(shape, g, scale=1.0):
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _close_bf16(got, want, what, ulps=1.0, atol=0.0):
+    """Within `ulps` bf16 units of the larger of the two magnitudes (a value on
+    a binade edge may round either way), plus fp32-accumulation noise relative
+    to the output's scale for values that cancel to near zero."""
+    g, w = got.float().cpu(), want.float()
+    tol = torch.maximum(w.abs(), g.abs()) * (ulps * 2.0 ** -7) + atol + 1e-5 * float(w.abs().max())
+    bad = (g - w).abs() > tol
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{bad.numel()} beyond {ulps} ulp; "
+                                 f"max err {float((g - w).abs().max()):.4g}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quantize_fp8_rows_bit_exact(dtype):
+    require_gpu()
+    from fastdms_amd.layers.linear import quantize_fp8_rows
+    g = torch.Generator().manual_seed(1)
+    w = (torch.randn(37, 520, generator=g) * 0.05).to(dtype)
+    w[3] = 0.0                     # all-zero row: scale 1
+    w[5, 7] = 3.0                  # one large element
+    q, sinv = quantize_fp8_rows(w.cuda())
+    torch.cuda.synchronize()
+    w8_t, sinv_ref = olin.quantize_weight_to_fp8(w.float().numpy())
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), w8_t.T)
+    assert np.array_equal(sinv.cpu().numpy().view(np.uint32), sinv_ref.reshape(-1).view(np.uint32))
+
+
+def _ref_linear(a, w, bias):
+    """bf16(a @ W^T + bias) with fp32 accumulation (F.linear semantics)."""
+    y = a.float() @ w.float().T
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8, 16])
+@pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 8192), (512, 256), (1024, 4096)])
+def test_linear_small_m_bf16(m, n, k):
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_small_m
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    bias = _bf16((n,), g, 0.1)
+    y = linear_small_m(x.cuda(), w.cuda())
+    _close_bf16(y, _ref_linear(x, w, None), "no bias")
+    y = linear_small_m(x.cuda(), w.cuda(), bias.cuda())
+    _close_bf16(y, _ref_linear(x, w, bias), "bias")
+
+
+def _rms_ref(x, r, nw, eps):
+    f = x.float() + (r.float() if r is not None else 0.0)
+    inv = torch.rsqrt(f.pow(2).mean(-1, keepdim=True) + eps)
+    return (f * inv).to(torch.bfloat16).float().mul(nw.float()).to(torch.bfloat16), f.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+@pytest.mark.parametrize("m,n,k", [(8, 3072, 2048), (1, 256, 512), (16, 2048, 4096)])
+def test_linear_small_m_rmsnorm_prologue(with_res, m, n, k):
+    """RMSNorm(x + residual) feeding the GEMM (layernorm.py:19-40 + linear):
+    residual_out = bf16(x + residual) bit-exact; the output matches
+    rmsnorm -> linear up to the norm's fp32 reduction order."""
+    require_gpu()
+    from fastdms_amd.layers.linear import PRO_RMSNORM, linear_small_m
+    g = torch.Generator().manual_seed(m + n + k + with_res)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    r = _bf16((m, k), g) if with_res else None
+    nw = (1.0 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16)
+    bias = _bf16((n,), g, 0.1)
+    ro = torch.empty((m, k), device="cuda", dtype=torch.bfloat16)
+    y = linear_small_m(x.cuda(), w.cuda(), bias.cuda(), prologue=PRO_RMSNORM, norm_weight=nw.cuda(), eps=1e-5,
+                       residual=None if r is None else r.cuda(), residual_out=ro)
+    a, r_new = _rms_ref(x, r, nw, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(ro.cpu(), r_new)
+    _close_bf16(y, _ref_linear(a, w, bias), "rmsnorm prologue", ulps=2.0, atol=2e-3)
+
+
+@pytest.mark.parametrize("m,f,k", [(8, 8192, 2048), (2, 256, 512), (16, 1024, 4096)])
+def test_linear_small_m_silu_epilogue(m, f, k):
+    """gate_up_proj followed by SiluAndMul in one launch: W = [gate; up] (2F
+    rows) and the output is bf16(silu(bf16 gate) * bf16 up) (activation.py:8-11)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_small_m
+    g = torch.Generator().manual_seed(m + f + k)
+    x, w = _bf16((m, k), g), _bf16((2 * f, k), g, 0.05)
+    y = linear_small_m(x.cuda(), w.cuda(), epilogue=EPI_SILU_MUL)
+    gu = _ref_linear(x, w, None).float()
+    want = (torch.nn.functional.silu(gu[:, :f]) * gu[:, f:]).to(torch.bfloat16)
+    assert y.shape == (m, f)
+    _close_bf16(y, want, "silu epilogue", ulps=2.0, atol=2e-3)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
+def test_linear_small_m_split_k_is_consistent(splits):
+    """K split over workgroups (merged by the last split through agent-scope
+    atomics) gives the same result for every split count, bf16 and FP8, with and
+    without the SiLU epilogue; repeated calls (counters reset) agree."""
+    require_gpu()
+    from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(splits)
+    m, n, k = 8, 512, 8192
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    bias = _bf16((n,), g, 0.1).cuda()
+    want = _ref_linear(x.cpu(), w.cpu(), bias.cpu())
+    for _ in range(2):
+        _close_bf16(linear_small_m(x, w, bias, k_splits=splits), want, f"bf16 split {splits}")
+    w8, si = quantize_fp8_rows(w)
+    base = linear_small_m(x, w8, weight_scale_inv=si, k_splits=1)
+    _close_bf16(linear_small_m(x, w8, weight_scale_inv=si, k_splits=splits), base.cpu(), f"fp8 split {splits}")
+    ye = linear_small_m(x, w, epilogue=EPI_SILU_MUL, k_splits=splits)
+    gu = _ref_linear(x.cpu(), w.cpu(), None).float()
+    _close_bf16(ye, (torch.nn.functional.silu(gu[:, :n // 2]) * gu[:, n // 2:]).to(torch.bfloat16),
+                f"silu split {splits}", ulps=2.0, atol=2e-3)
+
+
+@pytest.mark.parametrize("quantize_x", [True, False])
+@pytest.mark.parametrize("m,n,k", [(1, 3072, 2048), (8, 2048, 8192), (5, 512, 256)])
+def test_linear_small_m_fp8_matches_oracle(quantize_x, m, n, k):
+    """FP8 weights (C2/C3): y = bf16(sum xq*w8 / x_s * scale_inv) + bias in bf16,
+    against the float64 oracle (linear.py:492-763)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m * 3 + n + k + quantize_x)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    bias = _bf16((n,), g, 0.1)
+    w8, sinv = quantize_fp8_rows(w.cuda())
+    y = linear_small_m(x.cuda(), w8, bias.cuda(), weight_scale_inv=sinv, quantize_x=quantize_x)
+    w8_t, sinv_ref = olin.quantize_weight_to_fp8(w.float().numpy())
+    acc = olin.fp8_linear(x.float().numpy(), w8_t, sinv_ref, quantize_x=quantize_x)
+    want = torch.from_numpy(numerics.bf16_round(acc.astype(np.float32)))
+    want = (want + bias.float()).to(torch.bfloat16)
+    _close_bf16(y, want, "fp8", ulps=2.0, atol=1e-3)
+
+
+def test_linear_small_m_argument_errors():
+    require_gpu()
+    from fastdms_amd.layers.linear import PRO_RMSNORM, linear_small_m
+    x = torch.zeros((17, 256), device="cuda", dtype=torch.bfloat16)
+    w = torch.zeros((32, 256), device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        linear_small_m(x, w)                      # 17 rows
+    with pytest.raises(ValueError):
+        linear_small_m(x[:4, :200], w[:, :200])   # K not a multiple of 256
+    with pytest.raises(RuntimeError):
+        xx = x[:4]
+        linear_small_m(xx, w, prologue=PRO_RMSNORM, norm_weight=torch.ones(256, device="cuda", dtype=torch.bfloat16),
+                       residual=xx, residual_out=xx)   # residual_out aliases the input
