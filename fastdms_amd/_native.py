@@ -48,6 +48,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_silu_mul": "pplip",
     "fdms_quantize_fp8_rows": "pilliplpip",
     "fdms_linear_small_m": "pliipilppiipfplpliiippplp",
+    "fdms_linear_argmax_small_m": "pliipilppiiipppppp",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

@@ -47,6 +47,8 @@ class Config:
     seed: int = 0
     dms_survive_fraction: float = 0.125
     compact_decode_cudagraph: bool = True
+    # decode: LM-head GEMV fused with the greedy argmax (no logits materialised)
+    fused_greedy_head: bool = True
 
     def __post_init__(self):
         from .models.synthetic import model_config

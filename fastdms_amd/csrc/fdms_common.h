@@ -104,6 +104,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// torch.argmax order: NaN beats every number (lowest NaN index wins), ties go
+// to the lowest index.  True if (v, i) should replace the current best (bv, bi).
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
 // DMS threshold (dms.py:37-40): v > offset/scale (quotient pre-rounded to
 // fp32 on the host) when scale > 0, else v*scale - offset > 0 with each step
 // rounded to fp32.

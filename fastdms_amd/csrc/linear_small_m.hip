@@ -189,7 +189,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     const float* __restrict__ w_scale_inv, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ norm_w,
     float eps, const bf16_t* __restrict__ res, int64_t res_s, bf16_t* __restrict__ res_out, int64_t ro_s,
     bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
-    int* __restrict__ counters) {
+    int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx) {
   constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
   __shared__ float s_inv[kMaxM], s_xs[kMaxM];
   __shared__ f32x4 s_acc[NA][NW][64];
@@ -375,6 +375,47 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     if (lane == 0) __hip_atomic_store(&counters[strip], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const int m = lane & 15;
+  if (EPI == 2) {
+    // greedy head: the strip's best score per row (torch.argmax order), as the
+    // reference scores it -- bf16 logits for bf16 weights (F.linear then
+    // argmax), fp32 scores for FP8 weights (embed_head.py:96-144)
+    constexpr int kNone = 0x7FFFFFFF;
+    float bv = 0.0f;
+    int bi = kNone;
+    if (m < M) {
+      const float xsi2 = QX ? 1.0f / s_xs[m] : 1.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 4 * (lane >> 4) + r;
+        float v;
+        if (sizeof(WT) == 1) {
+          v = t[0][r] * xsi2 * w_scale_inv[n];
+          if (bias) v += ld<bf16_t>(bias + n);
+        } else {
+          v = QX ? t[0][r] * xsi2 : t[0][r];
+          v = rbf(v + (bias ? ld<bf16_t>(bias + n) : 0.0f));
+        }
+        if (bi == kNone || argmax_better(v, n, bv, bi)) {
+          bv = v;
+          bi = n;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (oi != kNone && (bi == kNone || argmax_better(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane < 16 && m < M) {
+      part_val[(int64_t)m * strips + strip] = bv;
+      part_idx[(int64_t)m * strips + strip] = bi;
+    }
+    return;
+  }
   if (m >= M) return;
   const float xsi = QX ? 1.0f / s_xs[m] : 1.0f;
   auto finalize = [&](float acc_v, int n) {
@@ -409,7 +450,7 @@ namespace {
 struct LinArgs {
   const bf16_t* x; int64_t x_s; int M, K; const void* w; int64_t w_s; const float* wsi; const bf16_t* bias;
   const bf16_t* norm_w; float eps; const bf16_t* res; int64_t res_s; bf16_t* res_out; int64_t ro_s;
-  bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters;
+  bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters; float* pval; int* pidx;
 };
 
 template <typename WT, int PRO, bool QX, int EPI>
@@ -417,7 +458,7 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   const WT* w = (const WT*)a.w;
   constexpr int U = (PRO == 1 || QX) ? 2 : 4;  // k-blocks per double-buffered group (register budget)
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
-                      a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters
+                      a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx
   if (nw == 8) {
     hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
   } else {
@@ -428,8 +469,10 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
 
 template <typename WT>
 void dispatch_linear(int prologue, int qx, int epi, int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
-#define FDMS_LIN_E(P, Q) \
-  if (epi) launch_linear<WT, P, Q, 1>(nw, grid, st, a); else launch_linear<WT, P, Q, 0>(nw, grid, st, a)
+#define FDMS_LIN_E(P, Q)                                    \
+  if (epi == 2) launch_linear<WT, P, Q, 2>(nw, grid, st, a); \
+  else if (epi) launch_linear<WT, P, Q, 1>(nw, grid, st, a); \
+  else launch_linear<WT, P, Q, 0>(nw, grid, st, a)
 #define FDMS_LIN_Q(P) \
   if (qx) { FDMS_LIN_E(P, true); } else { FDMS_LIN_E(P, false); }
   if (prologue == 1) {
@@ -482,12 +525,94 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   const dim3 grid((unsigned)blocks);
   const LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias,
                   (const bf16_t*)norm_weight, eps, (const bf16_t*)residual, res_stride, (bf16_t*)residual_out,
-                  res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters};
+                  res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, nullptr,
+                  nullptr};
   if (w_dtype == kFP8) {
     dispatch_linear<fp8_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
   } else {
     dispatch_linear<bf16_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
   }
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Second stage of the greedy head: per row, the best of the strips' partial
+// (score, index) pairs in torch.argmax order (embed_head.py:147-160).
+__global__ __launch_bounds__(1024) void argmax_partials_kernel(const float* __restrict__ pval,
+                                                               const int* __restrict__ pidx, int strips,
+                                                               int64_t* __restrict__ out) {
+  constexpr int kNone = 0x7FFFFFFF;
+  __shared__ float s_v[1024 / kWave];
+  __shared__ int s_i[1024 / kWave];
+  const int64_t row = blockIdx.x;
+  float bv = 0.0f;
+  int bi = kNone;
+  for (int j = threadIdx.x; j < strips; j += 1024) {
+    const float v = pval[row * strips + j];
+    const int i = pidx[row * strips + j];
+    if (bi == kNone || argmax_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (oi != kNone && (bi == kNone || argmax_better(ov, oi, bv, bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = bv;
+    s_i[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int wv = 1; wv < 1024 / kWave; ++wv) {
+      if (s_i[wv] != kNone && (bi == kNone || argmax_better(s_v[wv], s_i[wv], bv, bi))) {
+        bv = s_v[wv];
+        bi = s_i[wv];
+      }
+    }
+    out[row] = bi;
+  }
+}
+
+FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int m, int k, const void* w,
+                                           int w_dtype, int64_t w_stride, const float* w_scale_inv,
+                                           const void* bias, int n, int quantize_x, int k_splits, float* workspace,
+                                           int* counters, float* part_val, int* part_idx, int64_t* out_tokens,
+                                           void* stream) {
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0) return (int)hipErrorInvalidValue;
+  if (m == 0) return 0;
+  if (n == 0 || !x || !w || !part_val || !part_idx || !out_tokens) return (int)hipErrorInvalidValue;
+  if (w_dtype != kBF16 && w_dtype != kFP8) return (int)hipErrorInvalidValue;
+  if (w_dtype == kFP8 && !w_scale_inv) return (int)hipErrorInvalidValue;
+  if (n % 16 || k_splits < 1 || k_splits > 64 || k % k_splits) return (int)hipErrorInvalidValue;
+  if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
+  const int kc = k / k_splits;
+  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
+  const int wsz = w_dtype == kFP8 ? 1 : 2;
+  if (((uintptr_t)x % 16) || ((uintptr_t)w % 16) || (x_stride * 2) % 16 || (w_stride * wsz) % 16 ||
+      x_stride < k || w_stride < k)
+    return (int)hipErrorInvalidValue;
+  const int strips = n / 16;
+  const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  const LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias, nullptr, 0.0f,
+                  nullptr, 0, nullptr, 0, nullptr, 0, n, strips, k_splits, workspace, counters, part_val, part_idx};
+  const dim3 grid((unsigned)blocks);
+  if (w_dtype == kFP8) {
+    dispatch_linear<fp8_t>(0, quantize_x, 2, nw, grid, (hipStream_t)stream, a);
+  } else {
+    dispatch_linear<bf16_t>(0, quantize_x, 2, nw, grid, (hipStream_t)stream, a);
+  }
+  FDMS_LAUNCH_CHECK();
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3((unsigned)m), dim3(1024), 0, (hipStream_t)stream, part_val,
+                     part_idx, strips, out_tokens);
   FDMS_LAUNCH_CHECK();
   return 0;
 }

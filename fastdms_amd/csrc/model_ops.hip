@@ -134,11 +134,6 @@ FDMS_EXPORT int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, voi
 // Row argmax with torch.argmax's semantics (embed_head.py:142, 160): ties go
 // to the lowest index and NaN counts as larger than every number (the lowest
 // NaN index wins), so a row always yields an index in [0, n).
-__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
-  const bool vn = v != v, bn = bv != bv;
-  if (vn || bn) return vn && (!bn || i < bi);
-  return v > bv || (v == bv && i < bi);
-}
 
 // One 1024-thread block per row; 16-byte vector loads, four in flight per
 // thread, when the row is 16-byte aligned; fp32 or bf16 logits; int64 output.

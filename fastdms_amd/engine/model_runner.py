@@ -174,15 +174,20 @@ class ModelRunner:
                     dms_layer_evictions_buffer=evict)
         ids = self.static_input_ids[:batch]
         pos = self.static_positions[:batch]
+        logits = None
         if self.model.decode_fused_supported(batch):
-            logits = self.model.forward_decode_fused(ids, pos)
+            if self.config.fused_greedy_head:
+                self.model.forward_decode_fused(ids, pos, greedy_out=self.static_tokens[:batch])
+            else:
+                logits = self.model.forward_decode_fused(ids, pos)
         else:
             hidden = self.model(ids, pos)
             head = self.model.lm_head
             logits = (head.quant(hidden, None) if head.quant is not None
                       else torch.nn.functional.linear(hidden, head.weight))
-        nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0), batch,
-                 logits.shape[1], self.static_tokens.data_ptr(), nat.stream())
+        if logits is not None:
+            nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0), batch,
+                     logits.shape[1], self.static_tokens.data_ptr(), nat.stream())
         p, e = mgr.layer_major_token_positions, mgr.layer_major_evict_mask.view(torch.uint8)
         ev = evict.view(torch.uint8)
         nat.call("fdms_record_dms_decisions", p.data_ptr(), p.stride(0), p.stride(1), p.stride(2), p.stride(3),

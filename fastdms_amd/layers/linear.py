@@ -146,6 +146,41 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
     return out
 
 
+def linear_argmax_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+                          weight_scale_inv: torch.Tensor | None = None, quantize_x: bool | None = None,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy head for at most 16 rows: int64 token ids argmax_n (x @ W^T)[m, n]
+    in torch.argmax order.  bf16 weights score bf16 logits (F.linear + argmax);
+    FP8 weights score fp32 x-quantised products (embed_head.py:96-211)."""
+    n, k = weight.shape
+    rows = x.shape[0]
+    fp8 = weight.dtype == torch.float8_e4m3fn
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.shape[1] != k:
+        raise ValueError("linear_argmax_small_m expects bf16 activations [rows, K] with a contiguous last axis")
+    if fp8 and weight_scale_inv is None:
+        raise ValueError("FP8 weights need weight_scale_inv")
+    if not small_m_supported(rows, k, n):
+        raise ValueError(f"linear_argmax_small_m does not support rows={rows}, K={k}, N={n}")
+    if quantize_x is None:
+        quantize_x = fp8
+    strips = n // 16
+    k_splits = choose_k_splits(x.device, strips, k)
+    ws = counters = None
+    if k_splits > 1:
+        ws, counters = linear_workspace(x.device, strips * k_splits * 256, strips)
+    part_val = torch.empty((rows, strips), device=x.device, dtype=torch.float32)
+    part_idx = torch.empty((rows, strips), device=x.device, dtype=torch.int32)
+    if out is None:
+        out = torch.empty(rows, device=x.device, dtype=torch.int64)
+    sinv = None if weight_scale_inv is None else weight_scale_inv.reshape(-1)
+    nat.require_cuda(x, weight, out, what="linear_argmax_small_m")
+    nat.call("fdms_linear_argmax_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
+             nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), nat.ptr(bias), n,
+             int(bool(quantize_x)), int(k_splits), nat.ptr(ws), nat.ptr(counters), part_val.data_ptr(),
+             part_idx.data_ptr(), out.data_ptr(), nat.stream())
+    return out
+
+
 class LinearBase(nn.Module):
 
     def __init__(self, input_size: int, output_size: int, bias: bool = False):

@@ -22,7 +22,8 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm, rms_norm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
-                             QKVParallelLinear, RowParallelLinear, linear_small_m, small_m_supported)
+                             QKVParallelLinear, RowParallelLinear, linear_argmax_small_m, linear_small_m,
+                             small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -193,12 +194,14 @@ class LlamaModel(nn.Module):
         hidden_states, _ = self.norm(hidden_states, residual)
         return hidden_states
 
-    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor,
-                             lm_head: LinearBase) -> torch.Tensor:
+    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor, lm_head: LinearBase,
+                             greedy_out: torch.Tensor | None = None) -> torch.Tensor | None:
         """The decode step (same math as forward + LM head) on the decode-shaped
         linear kernel: per layer RMSNorm(+residual add), qkv, attention, o_proj,
         RMSNorm(+add), gate_up with SiLU*up as its epilogue, down_proj; then the
-        final RMSNorm(+add) and the LM head.  Returns the logits [rows, vocab].
+        final RMSNorm(+add) and the LM head.  Returns the logits [rows, vocab], or
+        with ``greedy_out`` writes the greedy token ids there (the head's GEMV
+        fused with the argmax) and returns None.
 
         (The RMSNorm stays a kernel of its own: folded into the GEMM prologue,
         every workgroup would re-read and re-normalise the whole activation,
@@ -217,6 +220,11 @@ class LlamaModel(nn.Module):
             act = _fused_linear(mlp.gate_up_proj, h, PRO_NONE, epilogue=EPI_SILU_MUL)
             x = _fused_linear(mlp.down_proj, act, PRO_NONE)
         h, _ = self.norm(x, res)
+        if greedy_out is not None:
+            w, sinv = ((lm_head.weight_fp8, lm_head.weight_scale_inv) if lm_head._fp8_weight_enabled
+                       else (lm_head.weight, None))
+            linear_argmax_small_m(h, w, lm_head.bias, weight_scale_inv=sinv, out=greedy_out)
+            return None
         return _fused_linear(lm_head, h, PRO_NONE)
 
     def decode_fused_supported(self, rows: int, lm_head: LinearBase) -> bool:
@@ -252,9 +260,11 @@ class LlamaForCausalLM(nn.Module):
     def decode_fused_supported(self, rows: int) -> bool:
         return self.model.decode_fused_supported(rows, self.lm_head)
 
-    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """Decode step through the decode-shaped linear kernels; returns the logits."""
-        return self.model.forward_decode_fused(input_ids, positions, self.lm_head)
+    def forward_decode_fused(self, input_ids: torch.Tensor, positions: torch.Tensor,
+                             greedy_out: torch.Tensor | None = None) -> torch.Tensor | None:
+        """Decode step through the decode-shaped linear kernels; returns the
+        logits, or writes greedy token ids into ``greedy_out``."""
+        return self.model.forward_decode_fused(input_ids, positions, self.lm_head, greedy_out)
 
 
 Qwen3ForCausalLM = LlamaForCausalLM  # the same glue with config.qk_norm = True

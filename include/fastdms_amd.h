@@ -234,6 +234,19 @@ int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const voi
                         void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue, int k_splits,
                         float* workspace, int* counters, void* y, int64_t y_stride, void* stream);
 
+/* C7 — greedy LM head: token[m] = argmax_n a[m,:] . W[n,:] for m <= 16 rows,
+ * ties to the lowest index, NaN first (torch.argmax order).  Replaces
+ * _fp8_row1_argmax_stage/reduce + _fp8_row1_argmax (fastdms/layers/embed_head.py:
+ * 96-211; FP8 weights, per-row quantised activation, scores in fp32) and
+ * greedy_token_ids' F.linear + argmax (491-598; bf16 weights, bf16 logits).
+ * One GEMV launch writes each strip's best (part_val / part_idx, m * n/16
+ * each), a second reduces them into out_tokens (int64).  Arguments as
+ * fdms_linear_small_m. */
+int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int m, int k, const void* w, int w_dtype,
+                               int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int quantize_x,
+                               int k_splits, float* workspace, int* counters, float* part_val, int* part_idx,
+                               int64_t* out_tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

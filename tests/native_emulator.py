@@ -586,6 +586,36 @@ class Emulator:
         self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
         return 0
 
+    def linear_argmax_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, qx, k_splits, ws, counters,
+                              part_val, part_idx, out, stream):
+        """Greedy head: scores as the oracle model's lm_head (bf16 logits) or
+        oracle/linear.py's fp32 FP8 scores, torch.argmax order."""
+        from oracle import linear as olin
+        if m == 0:
+            return 0
+        strips = n // 16
+        self.view(part_val, torch.float32, (m, strips), (strips, 1), "part_val")
+        self.view(part_idx, torch.int32, (m, strips), (strips, 1), "part_idx")
+        a = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
+        bv = self.view(bias, torch.bfloat16, (n,), (1,), "bias").float() if bias else None
+        if w_dtype == DT_FP8:
+            w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
+            si = self.view(wsi, torch.float32, (n,), (1,), "scale_inv").numpy()
+            sc = torch.from_numpy(olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx)).astype(np.float32))
+            if bv is not None:
+                sc = sc + bv
+        else:
+            wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float()
+            sc = a @ wv.T
+            if bv is not None:
+                sc = sc + bv
+            sc = sc.to(torch.bfloat16).float()
+        mx = sc.max(dim=1, keepdim=True).values
+        hit = torch.where(torch.isnan(mx), torch.isnan(sc), sc == mx)
+        tok = torch.where(hit, torch.arange(n)[None, :], n).min(dim=1).values
+        self.view(out, torch.int64, (m,), (1,), "out_tokens").copy_(tok)
+        return 0
+
     def prefill_attention(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, num_seqs,
                           max_seqlen, hq, hkv, d, scale, stream):
         if num_seqs == 0 or max_seqlen <= 0:

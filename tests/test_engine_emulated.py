@@ -31,11 +31,22 @@ def _check_logits(got: torch.Tensor, want: torch.Tensor, what: str):
                                             ("tiny-qwen3", [129, 700], 12),
                                             ("tiny-llama", [40], 6)])
 def test_engine_glue_matches_oracle(model, lens, gen):
+    _run(model, lens, gen, fused_head=False)
+
+
+@pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 64], 12), ("tiny-qwen3", [129, 700], 8)])
+def test_engine_fused_greedy_head_matches_oracle_tokens(model, lens, gen):
+    """Decode with the LM-head GEMV fused with the argmax: no logits, tokens
+    equal to the oracle model's greedy tokens step for step."""
+    _run(model, lens, gen, fused_head=True)
+
+
+def _run(model, lens, gen, fused_head):
     from oracle.model import OracleModel, weights_from_model
     with cpu_engine() as emu:
         from fastdms_amd import LLM, SamplingParams
         llm = LLM(model, max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384, enforce_eager=True,
-                  **DMS)
+                  fused_greedy_head=fused_head, **DMS)
         runner = llm.model_runner
         orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
                           alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
@@ -49,9 +60,12 @@ def test_engine_glue_matches_oracle(model, lens, gen):
         for step in range(gen - 1):
             pos = [len(s) - 1 for s in seqs]
             last = [s.last_token for s in seqs]
-            orc.decode([s.seq_id for s in seqs], last, pos)
+            o_tok = orc.decode([s.seq_id for s in seqs], last, pos)
             llm.step()
-            _check_logits(runner.model.lm_head.last_logits, orc.last_logits, f"decode step {step}")
+            if fused_head:
+                assert [s.completion_token_ids[-1] for s in seqs] == list(o_tok), f"tokens at decode step {step}"
+            else:
+                _check_logits(runner.model.lm_head.last_logits, orc.last_logits, f"decode step {step}")
             # the compact state the manager keeps must follow the oracle's: layer 0
             # exactly; deeper layers' decisions see GEMM-order noise, and a
             # decision sitting on the threshold may flip

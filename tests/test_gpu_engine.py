@@ -18,10 +18,10 @@ def _prompts(rng, lens, vocab):
     return [rng.integers(0, vocab, n).tolist() for n in lens]
 
 
-def _llm(model, max_num_seqs=8, eager=False, seed=0):
+def _llm(model, max_num_seqs=8, eager=False, seed=0, fused_head=True):
     from fastdms_amd import LLM
     return LLM(model, max_model_len=2048, max_num_seqs=max_num_seqs, max_num_batched_tokens=16384,
-               enforce_eager=eager, seed=seed, **DMS)
+               enforce_eager=eager, seed=seed, fused_greedy_head=fused_head, **DMS)
 
 
 @pytest.mark.parametrize("model,lens", [("tiny-llama", [300, 517, 800, 64]), ("tiny-qwen3", [129, 700])])
@@ -80,7 +80,7 @@ def _follow_oracle(model, lens, *, oracle_gemm: bool, gen: int = 40, sync_state:
     try:
         rng = np.random.default_rng(1)
         prompts = _prompts(rng, lens, 512)
-        llm = _llm(model)
+        llm = _llm(model, fused_head=False)  # logits are compared, so materialise them
         runner = llm.model_runner
         orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
                           alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
@@ -158,3 +158,22 @@ def test_engine_follows_cpu_oracle_native_gemm(model, lens):
     errors, (exact, near) = _follow_oracle(model, lens, oracle_gemm=False)
     assert max(e[0] for e in errors) <= 5e-2
     assert exact >= 0.9 * (exact + near)
+
+
+@pytest.mark.parametrize("model,lens", [("tiny-llama", [300, 517, 800, 64]), ("tiny-qwen3", [129, 700])])
+def test_fused_greedy_head_equals_logits_argmax(model, lens):
+    """The LM-head GEMV fused with the argmax picks the same tokens as logits +
+    argmax, in graph-replayed decode."""
+    require_gpu()
+    from fastdms_amd import SamplingParams
+    rng = np.random.default_rng(4)
+    prompts = _prompts(rng, lens, 512)
+    sp = SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True)
+    outs = []
+    for fused in (False, True):
+        llm = _llm(model, fused_head=fused)
+        outs.append([o["token_ids"] for o in llm.generate(prompts, sp)])
+        llm.exit()
+        del llm
+        torch.cuda.synchronize()
+    assert outs[0] == outs[1]

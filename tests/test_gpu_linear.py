@@ -166,3 +166,45 @@ def test_linear_small_m_argument_errors():
         xx = x[:4]
         linear_small_m(xx, w, prologue=PRO_RMSNORM, norm_weight=torch.ones(256, device="cuda", dtype=torch.bfloat16),
                        residual=xx, residual_out=xx)   # residual_out aliases the input
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("m,n,k", [(1, 128256, 2048), (8, 4096, 2048), (3, 512, 256), (8, 2048, 8192)])
+def test_linear_argmax_small_m(fp8, m, n, k):
+    """C7: greedy head = argmax of bf16 logits (bf16 weights) or of fp32 FP8
+    scores (embed_head.py:96-211), lowest index on ties; a mismatch is allowed
+    only where the reference scores of the two picks are within accumulation
+    noise."""
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_argmax_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m + n + k + fp8)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    if fp8:
+        w8, si = quantize_fp8_rows(w.cuda())
+        tok = linear_argmax_small_m(x.cuda(), w8, weight_scale_inv=si).cpu()
+        w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
+        sc = torch.from_numpy(olin.fp8_linear(x.float().numpy(), w8_t, sref))
+    else:
+        tok = linear_argmax_small_m(x.cuda(), w.cuda()).cpu()
+        sc = _ref_linear(x, w, None).double()
+    want = sc.argmax(dim=1)
+    for i in range(m):
+        if int(tok[i]) != int(want[i]):
+            gap = float(sc[i, want[i]] - sc[i, tok[i]])
+            assert gap <= 1e-3 * float(sc[i].abs().max()), (i, int(tok[i]), int(want[i]), gap)
+
+
+def test_linear_argmax_ties_and_nan():
+    """Ties pick the lowest index; a NaN score wins (torch.argmax order)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_argmax_small_m
+    k, n = 256, 4096
+    w = torch.zeros((n, k), dtype=torch.bfloat16)
+    w[100, 0] = w[3000, 0] = w[4000, 0] = 1.0     # row 0: three-way tie -> 100
+    w[2000, 1] = 2.0                               # row 1: strict max at 2000
+    x = torch.zeros((2, k), dtype=torch.bfloat16)
+    x[0, 0] = 1.0
+    x[1, 1] = 1.0
+    assert linear_argmax_small_m(x.cuda(), w.cuda()).cpu().tolist() == [100, 2000]
+    w[777, 2] = float("nan")                       # a NaN weight makes score 777 NaN for every row
+    assert linear_argmax_small_m(x.cuda(), w.cuda()).cpu().tolist() == [777, 777]
