@@ -48,7 +48,10 @@ SIGNATURES: dict[str, str] = {
     "fdms_silu_mul": "pplip",
     "fdms_quantize_fp8_rows": "pilliplpip",
     "fdms_linear_small_m": "pliipilppiipfplpliiippplp",
-    "fdms_linear_argmax_small_m": "pliipilppiiipppppp",
+    "fdms_linear_argmax_small_m": "pliipilppiiiipppppp",
+    "fdms_linear_int4_small_m": "pliiplppilpiiipppppplp",
+    "fdms_quantize_int4_groups": "pilliiiplpplp",
+    "fdms_fp8_rerank_topk": "pliiplpipipp",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

@@ -12,6 +12,8 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .layers.quant_env import env_bool as _env_flag
+
 _KV_CACHE_DTYPES = {"auto": None, "float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32,
                     "float8_e4m3fn": torch.float8_e4m3fn}
 
@@ -47,8 +49,9 @@ class Config:
     seed: int = 0
     dms_survive_fraction: float = 0.125
     compact_decode_cudagraph: bool = True
-    # decode: LM-head GEMV fused with the greedy argmax (no logits materialised)
-    fused_greedy_head: bool = True
+    # LM-head GEMV fused with the greedy argmax (no logits materialised);
+    # FASTDMS_GREEDY_FUSED_ARGMAX, default on (embed_head.py:62-63)
+    fused_greedy_head: bool = field(default_factory=lambda: _env_flag("FASTDMS_GREEDY_FUSED_ARGMAX", True))
 
     def __post_init__(self):
         from .models.synthetic import model_config

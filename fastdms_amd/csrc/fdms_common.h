@@ -17,6 +17,7 @@ enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kFP8 = 3 };
 
 struct bf16_t { uint16_t bits; };
 struct fp8_t { uint8_t bits; };
+struct u4x2_t { uint8_t bits; };  // two INT4 codes: low nibble = even k, high nibble = odd k
 typedef _Float16 f16_t;
 
 constexpr int kWave = 64;

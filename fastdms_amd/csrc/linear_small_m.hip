@@ -57,17 +57,27 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 template <typename WT> struct WBlock;
 // bf16 weights: a lane group reads 16 bf16 = 32 B per k-block
 template <> struct WBlock<bf16_t> {
-  static constexpr int kLoads = 2;
-  static __device__ __forceinline__ void to_ops(const uint4* r, uint4* op0, uint4* op1) {
-    *op0 = r[0];
-    *op1 = r[1];
+  struct Raw { uint4 v[2]; };
+  static constexpr bool kGrouped = false;
+  static __device__ __forceinline__ void load(const bf16_t* row, int k, Raw& r) {
+    const uint4* p = reinterpret_cast<const uint4*>(row + k);
+    r.v[0] = p[0];
+    r.v[1] = p[1];
+  }
+  static __device__ __forceinline__ void to_ops(const Raw& r, float, float, uint4* op0, uint4* op1) {
+    *op0 = r.v[0];
+    *op1 = r.v[1];
   }
 };
 // FP8 weights: 16 fp8 = 16 B per k-block, converted to two bf16x8 operands
 template <> struct WBlock<fp8_t> {
-  static constexpr int kLoads = 1;
-  static __device__ __forceinline__ void to_ops(const uint4* r, uint4* op0, uint4* op1) {
-    const uint32_t w[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+  using Raw = uint4;
+  static constexpr bool kGrouped = false;
+  static __device__ __forceinline__ void load(const fp8_t* row, int k, Raw& r) {
+    r = *reinterpret_cast<const uint4*>(row + k);
+  }
+  static __device__ __forceinline__ void to_ops(const Raw& r, float, float, uint4* op0, uint4* op1) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -80,6 +90,35 @@ template <> struct WBlock<fp8_t> {
     *op1 = uint4{o[4], o[5], o[6], o[7]};
   }
 };
+// INT4 weights: byte j of a row holds k = 2j (low nibble) and 2j + 1 (high);
+// 16 k = 8 B per k-block; w = bf16((q - 8) * scale + zero) with the bf16
+// scale / zero of the k-block's group (linear.py:436-458, 462-478).
+template <> struct WBlock<u4x2_t> {
+  using Raw = uint2;
+  static constexpr bool kGrouped = true;
+  static __device__ __forceinline__ void load(const u4x2_t* row, int k, Raw& r) {
+    r = *reinterpret_cast<const uint2*>(row + k / 2);
+  }
+  static __device__ __forceinline__ void to_ops(const Raw& r, float s, float z, uint4* op0, uint4* op1) {
+    const uint32_t w[2] = {r.x, r.y};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t word = w[i >> 2];
+      const int sh = (i & 3) * 8;
+      const float lo = (float)((int)((word >> sh) & 0xFu) - 8) * s + z;
+      const float hi = (float)((int)((word >> (sh + 4)) & 0xFu) - 8) * s + z;
+      o[i] = pack2(lo, hi);
+    }
+    *op0 = uint4{o[0], o[1], o[2], o[3]};
+    *op1 = uint4{o[4], o[5], o[6], o[7]};
+  }
+};
+
+template <typename WT> __device__ __forceinline__ constexpr bool is_fp8() { return false; }
+template <> __device__ __forceinline__ constexpr bool is_fp8<fp8_t>() { return true; }
+template <typename WT> __device__ __forceinline__ constexpr bool is_int4() { return false; }
+template <> __device__ __forceinline__ constexpr bool is_int4<u4x2_t>() { return true; }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -116,7 +155,8 @@ __device__ __forceinline__ float load_agent(const float* p) {
 // computed by one wave with every load of a batch in flight together.
 template <int PRO, bool QX>
 __device__ __forceinline__ void row_stats(const bf16_t* xr, const bf16_t* rr, const bf16_t* norm_w, int K, float eps,
-                                          int lane, bf16_t* res_out_row, float* inv_out, float* xs_out) {
+                                          int qx_torch, int lane, bf16_t* res_out_row, float* inv_out,
+                                          float* xs_out) {
   constexpr int kB = 8;  // 16-byte chunks per lane per batch
   float inv = 1.0f;
   if (PRO == 1) {
@@ -174,7 +214,9 @@ __device__ __forceinline__ void row_stats(const bf16_t* xr, const bf16_t* rr, co
     amax = wave_max(amax);
   }
   *inv_out = inv;
-  *xs_out = (amax > 0.0f) ? kFp8Max / amax : 1.0f;
+  // 448 / amax: the Triton kernels divide; torch's tensor expression
+  // (_fp8_linear) multiplies the reciprocal of amax by 448 (two roundings)
+  *xs_out = (amax > 0.0f) ? (qx_torch ? (1.0f / amax) * kFp8Max : kFp8Max / amax) : 1.0f;
 }
 
 }  // namespace
@@ -189,7 +231,9 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     const float* __restrict__ w_scale_inv, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ norm_w,
     float eps, const bf16_t* __restrict__ res, int64_t res_s, bf16_t* __restrict__ res_out, int64_t ro_s,
     bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
-    int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx) {
+    int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx,
+    const bf16_t* __restrict__ g_scale, const bf16_t* __restrict__ g_zero, int group, int64_t g_s, int qx_torch,
+    int bf16_scores) {
   constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
   __shared__ float s_inv[kMaxM], s_xs[kMaxM];
   __shared__ f32x4 s_acc[NA][NW][64];
@@ -223,7 +267,8 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   for (int a = 0; a < NA; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   struct Buf {
-    uint4 w[NA][U][WBlock<WT>::kLoads];
+    typename WBlock<WT>::Raw w[NA][U];
+    float gs[NA][U], gz[NA][U];  // INT4 group scale / zero
     uint4 x[U][2];
     uint4 r[U][2];   // residual (PRO 1)
     uint4 nw[U][2];  // norm weight (PRO 1)
@@ -235,9 +280,12 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       if (kb0 + u * kKB < kend) {
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
-          const uint4* wp = reinterpret_cast<const uint4*>(wrow[a] + k);
-#pragma unroll
-          for (int j = 0; j < WBlock<WT>::kLoads; ++j) b.w[a][u][j] = wp[j];
+          WBlock<WT>::load(wrow[a], k, b.w[a][u]);
+          if (WBlock<WT>::kGrouped) {
+            const int64_t gi = (int64_t)(n0 + c + (a ? n_out : 0)) * g_s + k / group;
+            b.gs[a][u] = ld<bf16_t>(g_scale + gi);
+            b.gz[a][u] = ld<bf16_t>(g_zero + gi);
+          }
         }
         b.x[u][0] = b.x[u][1] = b.r[u][0] = b.r[u][1] = uint4{0u, 0u, 0u, 0u};
         if (has_row) {
@@ -291,7 +339,8 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
 #pragma unroll
       for (int a = 0; a < NA; ++a) {
         uint4 a0, a1;
-        WBlock<WT>::to_ops(b.w[a][u], &a0, &a1);
+        WBlock<WT>::to_ops(b.w[a][u], WBlock<WT>::kGrouped ? b.gs[a][u] : 0.0f,
+                           WBlock<WT>::kGrouped ? b.gz[a][u] : 0.0f, &a0, &a1);
         acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(bo[0]), acc[a], 0, 0, 0);
         acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(bo[1]), acc[a], 0, 0, 0);
       }
@@ -305,7 +354,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     for (int m = wave; m < M; m += NW) {
       float inv, xs;
       row_stats<PRO, QX>(x + (int64_t)m * x_s, (PRO == 1 && res) ? res + (int64_t)m * res_s : nullptr, norm_w, K,
-                         eps, lane, (res_out && blockIdx.x == 0) ? res_out + (int64_t)m * ro_s : nullptr, &inv, &xs);
+                         eps, qx_torch, lane, (res_out && blockIdx.x == 0) ? res_out + (int64_t)m * ro_s : nullptr, &inv, &xs);
       if (lane == 0) {
         s_inv[m] = inv;
         s_xs[m] = xs;
@@ -377,8 +426,9 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   const int m = lane & 15;
   if (EPI == 2) {
     // greedy head: the strip's best score per row (torch.argmax order), as the
-    // reference scores it -- bf16 logits for bf16 weights (F.linear then
-    // argmax), fp32 scores for FP8 weights (embed_head.py:96-144)
+    // reference scores it -- bf16 logits for bf16 / INT4 weights and for FP8
+    // weights at more than one row (forward().argmax(), embed_head.py:543-598),
+    // fp32 scores for the FP8 row-1 argmax (embed_head.py:96-144)
     constexpr int kNone = 0x7FFFFFFF;
     float bv = 0.0f;
     int bi = kNone;
@@ -388,9 +438,17 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       for (int r = 0; r < 4; ++r) {
         const int n = n0 + 4 * (lane >> 4) + r;
         float v;
-        if (sizeof(WT) == 1) {
+        if (is_fp8<WT>() && !bf16_scores) {
           v = t[0][r] * xsi2 * w_scale_inv[n];
           if (bias) v += ld<bf16_t>(bias + n);
+        } else if (is_fp8<WT>()) {
+          v = rbf(t[0][r] * xsi2 * w_scale_inv[n]);
+          if (bias) v = rbf(v + ld<bf16_t>(bias + n));
+        } else if (is_int4<WT>()) {
+          // INT4 logits: the bf16 matmul result, then the bias in bf16
+          // (linear.py:475-477)
+          v = rbf(t[0][r]);
+          if (bias) v = rbf(v + ld<bf16_t>(bias + n));
         } else {
           v = QX ? t[0][r] * xsi2 : t[0][r];
           v = rbf(v + (bias ? ld<bf16_t>(bias + n) : 0.0f));
@@ -420,9 +478,9 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   const float xsi = QX ? 1.0f / s_xs[m] : 1.0f;
   auto finalize = [&](float acc_v, int n) {
     float v;
-    if (sizeof(WT) == 1 || QX) {
+    if (is_fp8<WT>() || is_int4<WT>() || QX) {  // matmul rounded to bf16, then the bias
       v = acc_v * xsi;
-      if (sizeof(WT) == 1) v *= w_scale_inv[n];
+      if (is_fp8<WT>()) v *= w_scale_inv[n];
       v = rbf(v);
       if (bias) v = rbf(v + ld<bf16_t>(bias + n));
     } else {
@@ -451,6 +509,8 @@ struct LinArgs {
   const bf16_t* x; int64_t x_s; int M, K; const void* w; int64_t w_s; const float* wsi; const bf16_t* bias;
   const bf16_t* norm_w; float eps; const bf16_t* res; int64_t res_s; bf16_t* res_out; int64_t ro_s;
   bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters; float* pval; int* pidx;
+  const bf16_t* g_scale = nullptr; const bf16_t* g_zero = nullptr; int group = 1; int64_t g_s = 0;
+  int qx_torch = 0; int bf16_scores = 1;
 };
 
 template <typename WT, int PRO, bool QX, int EPI>
@@ -458,7 +518,8 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   const WT* w = (const WT*)a.w;
   constexpr int U = (PRO == 1 || QX) ? 2 : 4;  // k-blocks per double-buffered group (register budget)
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
-                      a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx
+                      a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
+                      a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores
   if (nw == 8) {
     hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
   } else {
@@ -492,7 +553,8 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
                                     void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue,
                                     int k_splits, float* workspace, int* counters, void* y, int64_t y_stride,
                                     void* stream) {
-  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 || epilogue > 1)
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 || epilogue > 1 ||
+      quantize_x < 0 || quantize_x > 2)
     return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
   if (!x || !w || !y || (prologue == 1 && !norm_weight)) return (int)hipErrorInvalidValue;
@@ -523,10 +585,11 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   const dim3 grid((unsigned)blocks);
-  const LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias,
-                  (const bf16_t*)norm_weight, eps, (const bf16_t*)residual, res_stride, (bf16_t*)residual_out,
-                  res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, nullptr,
-                  nullptr};
+  LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias,
+            (const bf16_t*)norm_weight, eps, (const bf16_t*)residual, res_stride, (bf16_t*)residual_out,
+            res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, nullptr,
+            nullptr};
+  a.qx_torch = quantize_x == 2;
   if (w_dtype == kFP8) {
     dispatch_linear<fp8_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
   } else {
@@ -582,10 +645,10 @@ __global__ __launch_bounds__(1024) void argmax_partials_kernel(const float* __re
 
 FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int m, int k, const void* w,
                                            int w_dtype, int64_t w_stride, const float* w_scale_inv,
-                                           const void* bias, int n, int quantize_x, int k_splits, float* workspace,
-                                           int* counters, float* part_val, int* part_idx, int64_t* out_tokens,
-                                           void* stream) {
-  if (m < 0 || m > kMaxM || k <= 0 || n < 0) return (int)hipErrorInvalidValue;
+                                           const void* bias, int n, int quantize_x, int bf16_scores, int k_splits,
+                                           float* workspace, int* counters, float* part_val, int* part_idx,
+                                           int64_t* out_tokens, void* stream) {
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || quantize_x < 0 || quantize_x > 2) return (int)hipErrorInvalidValue;
   if (m == 0) return 0;
   if (n == 0 || !x || !w || !part_val || !part_idx || !out_tokens) return (int)hipErrorInvalidValue;
   if (w_dtype != kBF16 && w_dtype != kFP8) return (int)hipErrorInvalidValue;
@@ -602,8 +665,10 @@ FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int 
   const int strips = n / 16;
   const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-  const LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias, nullptr, 0.0f,
-                  nullptr, 0, nullptr, 0, nullptr, 0, n, strips, k_splits, workspace, counters, part_val, part_idx};
+  LinArgs a{(const bf16_t*)x, x_stride, m, k, w, w_stride, w_scale_inv, (const bf16_t*)bias, nullptr, 0.0f,
+            nullptr, 0, nullptr, 0, nullptr, 0, n, strips, k_splits, workspace, counters, part_val, part_idx};
+  a.qx_torch = quantize_x == 2;
+  a.bf16_scores = bf16_scores != 0;
   const dim3 grid((unsigned)blocks);
   if (w_dtype == kFP8) {
     dispatch_linear<fp8_t>(0, quantize_x, 2, nw, grid, (hipStream_t)stream, a);
@@ -613,6 +678,224 @@ FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int 
   FDMS_LAUNCH_CHECK();
   hipLaunchKernelGGL(argmax_partials_kernel, dim3((unsigned)m), dim3(1024), 0, (hipStream_t)stream, part_val,
                      part_idx, strips, out_tokens);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Re-ranking of the INT4 head's top-k candidates in FP8 (embed_head.py:214-302):
+// one workgroup per row; the activation is quantised as the row-1 kernels do
+// (448/amax divided, RNE to e4m3fn), each wave scores candidates t = wave,
+// wave + 4, ... (fp32 products of e4m3 values are exact), and thread 0 picks
+// the best, the lowest id on ties; an id outside [0, N) scores -inf.
+__global__ __launch_bounds__(256) void fp8_rerank_topk_kernel(const bf16_t* __restrict__ x, int64_t x_s, int K,
+                                                              const uint8_t* __restrict__ w, int64_t w_s,
+                                                              const float* __restrict__ w_scale_inv, int N,
+                                                              const int64_t* __restrict__ cand, int topk,
+                                                              int64_t* __restrict__ out) {
+  __shared__ float s_red[4];
+  __shared__ float s_score[32];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const bf16_t* xr = x + row * x_s;
+  float am = 0.0f;
+  for (int k = tid * 8; k < K; k += 256 * 8) {
+    float f[8];
+    load_sum8(xr + k, nullptr, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(f[i]));
+  }
+  am = wave_max(am);
+  if (lane == 0) s_red[wave] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float xs = am > 0.0f ? kFp8Max / am : 1.0f;
+  const float xsi = 1.0f / xs;
+  for (int t = wave; t < topk; t += 4) {
+    const int64_t id = cand[row * topk + t];
+    float score = -INFINITY;
+    if (id >= 0 && id < N) {
+      const uint8_t* wr = w + id * w_s;
+      float acc = 0.0f;
+      for (int k = lane * 16; k < K; k += 64 * 16) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(wr + k);
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+        float f[16];
+        load_sum8(xr + k, nullptr, f);
+        load_sum8(xr + k + 8, nullptr, f + 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float xq = fp8_to_f32(f32_to_fp8(f[i] * xs));
+          acc += xq * fp8_to_f32((ww[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+        }
+      }
+      score = wave_sum(acc) * xsi * w_scale_inv[id];
+    }
+    if (lane == 0) s_score[t] = score;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float best = -INFINITY;
+    int64_t bid = N;
+    for (int t = 0; t < topk; ++t) {
+      const int64_t id = cand[row * topk + t];
+      const float v = s_score[t];
+      if (v > best || (v == best && id < bid)) {
+        best = v;
+        bid = id;
+      }
+    }
+    out[row] = bid;
+  }
+}
+
+FDMS_EXPORT int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, int k, const void* w_fp8,
+                                     int64_t w_stride, const float* w_scale_inv, int n, const int64_t* candidates,
+                                     int topk, int64_t* out_tokens, void* stream) {
+  if (rows < 0 || k <= 0 || n <= 0 || (topk != 2 && topk != 4 && topk != 8 && topk != 16 && topk != 32))
+    return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!x || !w_fp8 || !w_scale_inv || !candidates || !out_tokens) return (int)hipErrorInvalidValue;
+  if (k % 16 || ((uintptr_t)x % 16) || ((uintptr_t)w_fp8 % 16) || (x_stride * 2) % 16 || w_stride % 16 ||
+      x_stride < k || w_stride < k)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(fp8_rerank_topk_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)x, x_stride, k, (const uint8_t*)w_fp8, w_stride, w_scale_inv, n, candidates,
+                     topk, out_tokens);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// C5 — W4A16 decode linear: the small-M kernel with INT4 weights (no
+// activation quantisation or prologue; epilogue 0 plain, 1 SiLU*up, 2 greedy).
+FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
+                                         int64_t w_stride_bytes, const void* group_scale, const void* group_zero,
+                                         int group_size, int64_t g_stride, const void* bias, int n, int epilogue,
+                                         int k_splits, float* workspace, int* counters, float* part_val,
+                                         int* part_idx, int64_t* out_tokens, void* y, int64_t y_stride,
+                                         void* stream) {
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || epilogue < 0 || epilogue > 2) return (int)hipErrorInvalidValue;
+  if (m == 0 || n == 0) return 0;
+  if (!x || !w_packed || !group_scale || !group_zero) return (int)hipErrorInvalidValue;
+  if (group_size < 16 || (group_size & (group_size - 1)) || k % group_size || g_stride < k / group_size)
+    return (int)hipErrorInvalidValue;
+  if (epilogue == 2 ? (!part_val || !part_idx || !out_tokens) : !y) return (int)hipErrorInvalidValue;
+  const int n_out = epilogue == 1 ? n / 2 : n;
+  if (n_out % 16 || (epilogue == 1 && n % 2)) return (int)hipErrorInvalidValue;
+  if (k_splits < 1 || k_splits > 64 || k % k_splits || (k_splits > 1 && (!workspace || !counters)))
+    return (int)hipErrorInvalidValue;
+  const int kc = k / k_splits;
+  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
+  if (((uintptr_t)x % 16) || ((uintptr_t)w_packed % 8) || (x_stride * 2) % 16 || w_stride_bytes % 8 ||
+      x_stride < k || w_stride_bytes * 2 < k || (epilogue != 2 && y_stride < n_out))
+    return (int)hipErrorInvalidValue;
+  if (y && (y == x)) return (int)hipErrorInvalidValue;
+  const int strips = n_out / 16;
+  const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  LinArgs a{(const bf16_t*)x, x_stride, m, k, w_packed, w_stride_bytes, nullptr, (const bf16_t*)bias, nullptr, 0.0f,
+            nullptr, 0, nullptr, 0, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, part_val,
+            part_idx};
+  a.g_scale = (const bf16_t*)group_scale;
+  a.g_zero = (const bf16_t*)group_zero;
+  a.group = group_size;
+  a.g_s = g_stride;
+  const dim3 grid((unsigned)blocks);
+  const hipStream_t st = (hipStream_t)stream;
+  if (epilogue == 2) launch_linear<u4x2_t, 0, false, 2>(nw, grid, st, a);
+  else if (epilogue == 1) launch_linear<u4x2_t, 0, false, 1>(nw, grid, st, a);
+  else launch_linear<u4x2_t, 0, false, 0>(nw, grid, st, a);
+  FDMS_LAUNCH_CHECK();
+  if (epilogue == 2) {
+    hipLaunchKernelGGL(argmax_partials_kernel, dim3((unsigned)m), dim3(1024), 0, st, part_val, part_idx, strips,
+                       out_tokens);
+    FDMS_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
+// C5 — INT4 group quantisation of weight rows [N, K] (linear.py:414-459):
+// symmetric s = amax/7 (1 for a zero group), zero = 0, q = clamp(rint(w/s), -8, 7) + 8;
+// asymmetric s = (max-min)/15 (1 if flat), zero = min + 8s (min if flat),
+// q = clamp(rint((w - zero)/s + 8), 0, 15); q uses the fp32 scale / zero, the
+// stored scale / zero are rounded to bf16.  One wave per (row, group).
+template <typename TI>
+__global__ __launch_bounds__(256) void quantize_int4_kernel(const TI* __restrict__ w, int64_t w_s, int k, int group,
+                                                            int asym, uint8_t* __restrict__ out, int64_t out_s,
+                                                            bf16_t* __restrict__ scale, bf16_t* __restrict__ zero,
+                                                            int64_t g_s, int64_t total_groups) {
+  const int64_t gid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gid >= total_groups) return;
+  const int lane = threadIdx.x & 63;
+  const int groups_per_row = k / group;
+  const int64_t row = gid / groups_per_row;
+  const int gi = (int)(gid - row * groups_per_row);
+  const TI* src = w + row * w_s + (int64_t)gi * group;
+  float mn = INFINITY, mx = -INFINITY, am = 0.0f;
+  for (int j = lane; j < group; j += 64) {
+    const float v = ld<TI>(src + j);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+    am = fmaxf(am, fabsf(v));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o));
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    am = fmaxf(am, __shfl_xor(am, o));
+  }
+  // amax / 7.0 and span / 15.0 as torch evaluates them on a GPU: a multiply by
+  // the fp32 reciprocal of the scalar.
+  float s, z;
+  if (asym) {
+    const float span = mx - mn;
+    s = span > 0.0f ? span * (1.0f / 15.0f) : 1.0f;
+    z = span > 0.0f ? mn + 8.0f * s : mn;
+  } else {
+    s = am > 0.0f ? am * (1.0f / 7.0f) : 1.0f;
+    z = 0.0f;
+  }
+  uint8_t* dst = out + row * out_s + (int64_t)gi * (group / 2);
+  for (int j = lane; j < group / 2; j += 64) {
+    int q[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float v = ld<TI>(src + 2 * j + h);
+      float r;
+      if (asym) r = fminf(fmaxf(rintf((v - z) / s + 8.0f), 0.0f), 15.0f);
+      else r = fminf(fmaxf(rintf(v / s), -8.0f), 7.0f) + 8.0f;
+      q[h] = (int)r;
+    }
+    dst[j] = (uint8_t)(q[0] | (q[1] << 4));
+  }
+  if (lane == 0) {
+    scale[row * g_s + gi].bits = (uint16_t)f32_to_bf16(s);
+    zero[row * g_s + gi].bits = (uint16_t)f32_to_bf16(z);
+  }
+}
+
+FDMS_EXPORT int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int64_t rows, int k,
+                                          int group_size, int asymmetric, void* out_packed, int64_t out_stride,
+                                          void* group_scale, void* group_zero, int64_t g_stride, void* stream) {
+  if (rows < 0 || k <= 0 || group_size < 2 || group_size % 2 || k % group_size) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!w || !out_packed || !group_scale || !group_zero || w_stride < k || out_stride * 2 < k ||
+      g_stride < k / group_size)
+    return (int)hipErrorInvalidValue;
+  const int64_t total = rows * (k / group_size);
+  const int64_t blocks = (total + 3) / 4;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if (w_dtype == kBF16) {
+    hipLaunchKernelGGL(quantize_int4_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const bf16_t*)w, w_stride, k, group_size, asymmetric, (uint8_t*)out_packed, out_stride,
+                       (bf16_t*)group_scale, (bf16_t*)group_zero, g_stride, total);
+  } else if (w_dtype == kF32) {
+    hipLaunchKernelGGL(quantize_int4_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)w, w_stride, k, group_size, asymmetric, (uint8_t*)out_packed, out_stride,
+                       (bf16_t*)group_scale, (bf16_t*)group_zero, g_stride, total);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
   FDMS_LAUNCH_CHECK();
   return 0;
 }

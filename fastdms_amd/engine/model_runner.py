@@ -19,12 +19,44 @@ import torch
 from .. import _native as nat
 from ..config import Config
 from ..layers.compact_attention import reserve_attention_workspace
-from ..layers.linear import reserve_linear_workspace
+from ..layers import quant_env as qe
+from ..layers.linear import convert_linear_modules_to_fp8, reserve_linear_workspace
 from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
 from .compact_kv import CompactKVManager
 from .dms import DMSMetadata, load_dms_metadata
 from .sequence import Sequence
+
+
+def convert_model_weights(model) -> tuple[int, bool, bool]:
+    """FP8 / INT4 weights from the environment, as model_runner.py:72-113:
+    FASTDMS_FP8_WEIGHTS converts the linear layers in scope, FASTDMS_FP8_LM_HEAD
+    (or a head scope) the LM head, and then FASTDMS_FP8_EMBEDDING the token
+    table (shared with the head's FP8 rows under
+    FASTDMS_FP8_EMBEDDING_SHARE_LM_HEAD).  Returns (converted linears, FP8
+    head, FP8 embedding)."""
+    if not qe.fp8_weights_enabled():
+        return 0, False, False
+    converted = convert_linear_modules_to_fp8(model)
+    lm_head = model.lm_head
+    embed = model.model.embed_tokens
+    fp8_embedding = qe.env_bool("FASTDMS_FP8_EMBEDDING", True)
+    fp8_head = False
+    if qe.fp8_lm_head_enabled():
+        tied = (fp8_embedding and embed.weight.untyped_storage().data_ptr()
+                == lm_head.weight.untyped_storage().data_ptr())
+        keep = qe.fp8_keep_bf16_lm_head_weight()
+        if tied and not qe.env_bool("FASTDMS_FP8_KEEP_BF16_EMBEDDING", False):
+            keep = False
+        lm_head.quantize_weight_to_fp8(keep_bf16_weight=keep)
+        fp8_head = True
+    if fp8_embedding:
+        keep_embed = qe.env_bool("FASTDMS_FP8_KEEP_BF16_EMBEDDING", False)
+        if qe.env_bool("FASTDMS_FP8_EMBEDDING_SHARE_LM_HEAD", False) and fp8_head:
+            embed.enable_fp8_embedding_from_lm_head(lm_head, keep_bf16_weight=keep_embed)
+        else:
+            embed.quantize_embedding_to_fp8(keep_bf16_weight=keep_embed)
+    return converted, fp8_head, fp8_embedding
 
 
 class ModelRunner:
@@ -40,6 +72,7 @@ class ModelRunner:
         torch.cuda.set_device(self.device)
         self.model = build_synthetic_model(hf, seed=config.seed, device=self.device,
                                            survive_fraction=config.dms_survive_fraction)
+        self.fp8_weight_modules, self.fp8_lm_head, self.fp8_embedding = convert_model_weights(self.model)
         self.dms_metadata = self._dms_metadata()
         self.num_layers = hf.num_hidden_layers
         self.num_kv_heads = hf.num_key_value_heads
@@ -144,7 +177,16 @@ class ModelRunner:
     def run_prefill(self, seqs: list[Sequence]) -> list[int]:
         ids, pos = self.prepare_prefill(seqs)
         hidden = self.model(ids, pos)
-        tokens = self.model.compute_greedy_token_ids(hidden)
+        head = self.model.lm_head
+        if self.config.fused_greedy_head:
+            tokens = self.model.compute_greedy_token_ids(hidden)
+            head.last_logits = None
+        else:
+            logits = self.model.compute_logits(hidden)
+            head.last_logits = logits
+            tokens = torch.empty(logits.shape[0], device=logits.device, dtype=torch.int64)
+            nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0),
+                     logits.shape[0], logits.shape[1], tokens.data_ptr(), nat.stream())
         ctx = get_context()
         total = sum(e.numel() for e in ctx.dms_layer_evictions.values())
         true = sum(e.sum() for e in ctx.dms_layer_evictions.values())
@@ -183,8 +225,10 @@ class ModelRunner:
         else:
             hidden = self.model(ids, pos)
             head = self.model.lm_head
-            logits = (head.quant(hidden, None) if head.quant is not None
-                      else torch.nn.functional.linear(hidden, head.weight))
+            if self.config.fused_greedy_head:
+                head.greedy_into(hidden.contiguous(), self.static_tokens[:batch])
+            else:
+                logits = head.logits(hidden.contiguous())
         if logits is not None:
             nat.call("fdms_argmax_rows", logits.data_ptr(), nat.dtype_code(logits.dtype), logits.stride(0), batch,
                      logits.shape[1], self.static_tokens.data_ptr(), nat.stream())

@@ -1,24 +1,34 @@
 """Linear layers (mirror of fastdms/layers/linear.py class names, single GPU).
 
-Decode-shaped calls (at most 16 rows) run the HIP kernel
-``fdms_linear_small_m`` for bf16 or FP8 weights, optionally with a fused
-RMSNorm(+residual) or SiLU*up prologue.  Larger row counts (prefill) use the
-ROCm GEMM library (hipBLASLt through torch) for bf16 weights; FP8 weights are
-quantised per output channel by ``fdms_quantize_fp8_rows`` exactly as the
-reference's ``quantize_weight_to_fp8`` (linear.py:813-847).
+Decode-shaped calls (at most 16 rows) run the HIP kernels
+``fdms_linear_small_m`` (bf16 or FP8 weights, optional fused RMSNorm prologue
+or SiLU*up epilogue) and ``fdms_linear_int4_small_m`` (INT4 weights).  FP8 /
+INT4 weights are made by ``fdms_quantize_fp8_rows`` / ``fdms_quantize_int4_groups``
+as the reference's ``quantize_weight_to_fp8`` makes them (linear.py:813-847,
+414-459), and ``LinearBase.route`` picks the path in the reference's order
+(linear.py:855-926) under the same environment switches.  Prefill row counts
+use the ROCm GEMM library (hipBLASLt through torch) for bf16 weights.
 """
 from __future__ import annotations
+
+import os
 
 import torch
 import torch.nn.functional as F
 from torch import nn
 
 from .. import _native as nat
+from . import quant_env as qe
 
 PRO_NONE, PRO_RMSNORM = 0, 1
 EPI_NONE, EPI_SILU_MUL = 0, 1
+QX_NONE, QX_DIVIDE, QX_TORCH = 0, 1, 2   # activation quantisation: none / 448/amax / reciprocal(amax)*448
 SMALL_M_MAX_ROWS = 16
 _MAX_K_SPLITS = 8
+
+
+def int4_max_rows() -> int:
+    return qe.int4_max_rows()
 
 
 def small_m_supported(rows: int, in_features: int, out_features: int) -> bool:
@@ -101,14 +111,15 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
                    weight_scale_inv: torch.Tensor | None = None, prologue: int = PRO_NONE,
                    norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
                    residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
-                   quantize_x: bool | None = None, epilogue: int = EPI_NONE, k_splits: int | None = None,
+                   quantize_x: bool | int | None = None, epilogue: int = EPI_NONE, k_splits: int | None = None,
                    out: torch.Tensor | None = None) -> torch.Tensor:
     """y = a @ W^T for at most 16 rows.  ``weight`` is [N, K] bf16, or FP8
     e4m3fn with ``weight_scale_inv`` [N] (or [1, N]).  ``a`` is x, or RMSNorm of
     x (+ residual) with ``norm_weight`` (prologue 1; the bf16 sum goes to
     ``residual_out``).  epilogue 1: W = [gate; up] and the result is
-    silu(gate) * up, [rows, N/2].  FP8 weights quantise the activation per row
-    unless ``quantize_x`` is False."""
+    silu(gate) * up, [rows, N/2].  quantize_x: QX_DIVIDE (True; the default for
+    FP8 weights, the row-1 / small-M kernels), QX_TORCH (_fp8_linear's form) or
+    QX_NONE (False)."""
     if weight.dim() != 2:
         raise ValueError("weight must be [out_features, in_features]")
     n, k = weight.shape
@@ -125,8 +136,9 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
         raise ValueError(f"linear_small_m does not support rows={rows}, K={k}, N={n}")
     if x.shape[1] != k:
         raise ValueError(f"activation width {x.shape[1]} does not match K={k}")
-    if quantize_x is None:
-        quantize_x = fp8
+    qx = (QX_DIVIDE if fp8 else QX_NONE) if quantize_x is None else int(quantize_x)
+    if qx not in (QX_NONE, QX_DIVIDE, QX_TORCH):
+        raise ValueError(f"quantize_x must be one of 0, 1, 2; got {quantize_x!r}")
     if out is None:
         out = torch.empty((rows, n_out), device=x.device, dtype=torch.bfloat16)
     strips = n_out // 16
@@ -140,18 +152,20 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
     nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
              nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), nat.ptr(bias), n, int(prologue),
              nat.ptr(norm_weight), float(eps), nat.ptr(residual), 0 if residual is None else residual.stride(0),
-             nat.ptr(residual_out), 0 if residual_out is None else residual_out.stride(0), int(bool(quantize_x)),
+             nat.ptr(residual_out), 0 if residual_out is None else residual_out.stride(0), qx,
              int(epilogue), int(k_splits), nat.ptr(ws), nat.ptr(counters), out.data_ptr(), out.stride(0),
              nat.stream())
     return out
 
 
 def linear_argmax_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
-                          weight_scale_inv: torch.Tensor | None = None, quantize_x: bool | None = None,
-                          out: torch.Tensor | None = None) -> torch.Tensor:
+                          weight_scale_inv: torch.Tensor | None = None, quantize_x: bool | int | None = None,
+                          bf16_scores: bool | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy head for at most 16 rows: int64 token ids argmax_n (x @ W^T)[m, n]
-    in torch.argmax order.  bf16 weights score bf16 logits (F.linear + argmax);
-    FP8 weights score fp32 x-quantised products (embed_head.py:96-211)."""
+    in torch.argmax order.  bf16 weights score bf16 logits (F.linear + argmax).
+    FP8 weights score the x-quantised products in fp32 (the row-1 argmax,
+    embed_head.py:96-211; the default), or with ``bf16_scores`` as the bf16
+    logits of forward() (quantize_x=QX_TORCH for its _fp8_linear)."""
     n, k = weight.shape
     rows = x.shape[0]
     fp8 = weight.dtype == torch.float8_e4m3fn
@@ -161,8 +175,11 @@ def linear_argmax_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Ten
         raise ValueError("FP8 weights need weight_scale_inv")
     if not small_m_supported(rows, k, n):
         raise ValueError(f"linear_argmax_small_m does not support rows={rows}, K={k}, N={n}")
-    if quantize_x is None:
-        quantize_x = fp8
+    qx = (QX_DIVIDE if fp8 else QX_NONE) if quantize_x is None else int(quantize_x)
+    if qx not in (QX_NONE, QX_DIVIDE, QX_TORCH):
+        raise ValueError(f"quantize_x must be one of 0, 1, 2; got {quantize_x!r}")
+    if bf16_scores is None:
+        bf16_scores = not fp8
     strips = n // 16
     k_splits = choose_k_splits(x.device, strips, k)
     ws = counters = None
@@ -176,12 +193,95 @@ def linear_argmax_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Ten
     nat.require_cuda(x, weight, out, what="linear_argmax_small_m")
     nat.call("fdms_linear_argmax_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
              nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), nat.ptr(bias), n,
-             int(bool(quantize_x)), int(k_splits), nat.ptr(ws), nat.ptr(counters), part_val.data_ptr(),
+             qx, int(bool(bf16_scores)), int(k_splits), nat.ptr(ws), nat.ptr(counters), part_val.data_ptr(),
              part_idx.data_ptr(), out.data_ptr(), nat.stream())
     return out
 
 
+def quantize_int4_groups(w: torch.Tensor, group_size: int, mode: str = "symmetric"):
+    """INT4 group quantisation of weight rows [N, K] (linear.py:414-459).
+    Returns (packed [N, K/2] uint8: q[2j] low nibble, q[2j+1] high nibble,
+    scale [N, K/group] bf16, zero [N, K/group] bf16); dequant (q - 8) * scale + zero."""
+    mode = mode.strip().lower()
+    if mode not in {"sym", "symmetric", "asym", "asymmetric", "affine"}:
+        raise ValueError("int4 quant_mode must be symmetric or asymmetric")
+    if w.dim() != 2 or w.stride(1) != 1 or w.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("quantize_int4_groups expects bf16/fp32 rows with a contiguous last axis")
+    n, k = w.shape
+    if group_size not in (32, 64, 128, 256) or k % group_size:
+        raise ValueError(f"group size {group_size} must be one of 32/64/128/256 and divide K={k}")
+    packed = torch.empty((n, k // 2), device=w.device, dtype=torch.uint8)
+    scale = torch.empty((n, k // group_size), device=w.device, dtype=torch.bfloat16)
+    zero = torch.empty_like(scale)
+    nat.require_cuda(w, what="quantize_int4_groups")
+    nat.call("fdms_quantize_int4_groups", w.data_ptr(), nat.dtype_code(w.dtype), w.stride(0), n, k, group_size,
+             int(mode in {"asym", "asymmetric", "affine"}), packed.data_ptr(), packed.stride(0), scale.data_ptr(),
+             zero.data_ptr(), scale.stride(0), nat.stream())
+    return packed, scale, zero
+
+
+def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor,
+                        group_size: int, bias: torch.Tensor | None = None, *, epilogue: int = EPI_NONE,
+                        out: torch.Tensor | None = None, greedy: bool = False) -> torch.Tensor:
+    """W4A16 for at most 16 rows (linear.py:462-478 semantics): y = x @
+    dequant(W)^T, or SiLU*up (epilogue 1), or greedy token ids (greedy=True)."""
+    n, k = packed.shape[0], packed.shape[1] * 2
+    rows = x.shape[0]
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.shape[1] != k:
+        raise ValueError("linear_int4_small_m expects bf16 activations [rows, K]")
+    n_out = n // 2 if epilogue == EPI_SILU_MUL else n
+    if not small_m_supported(rows, k, n_out):
+        raise ValueError(f"linear_int4_small_m does not support rows={rows}, K={k}, N={n}")
+    strips = n_out // 16
+    k_splits = choose_k_splits(x.device, strips, k)
+    ws = counters = None
+    if k_splits > 1:
+        ws, counters = linear_workspace(x.device, strips * k_splits * 256 * (2 if epilogue else 1), strips)
+    pv = pi = tok = None
+    if greedy:
+        pv = torch.empty((rows, strips), device=x.device, dtype=torch.float32)
+        pi = torch.empty((rows, strips), device=x.device, dtype=torch.int32)
+        tok = out if out is not None else torch.empty(rows, device=x.device, dtype=torch.int64)
+        y = None
+    else:
+        y = out if out is not None else torch.empty((rows, n_out), device=x.device, dtype=torch.bfloat16)
+    nat.require_cuda(x, packed, scale, zero, what="linear_int4_small_m")
+    nat.call("fdms_linear_int4_small_m", x.data_ptr(), x.stride(0), rows, k, packed.data_ptr(), packed.stride(0),
+             scale.data_ptr(), zero.data_ptr(), int(group_size), scale.stride(0), nat.ptr(bias), n,
+             2 if greedy else int(epilogue), int(k_splits), nat.ptr(ws), nat.ptr(counters), nat.ptr(pv), nat.ptr(pi),
+             nat.ptr(tok), nat.ptr(y), 0 if y is None else y.stride(0), nat.stream())
+    return tok if greedy else y
+
+
+def fp8_rows_gemm(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor,
+                  bias: torch.Tensor | None, quantize_x: int) -> torch.Tensor:
+    """FP8 linear for any row count, the reference's _fp8_linear semantics
+    (linear.py:635-662; QX_TORCH) or its Triton kernels' (QX_DIVIDE / QX_NONE):
+    y = bf16(sum_k xq*w8 / x_s * scale_inv), bias added in bf16.  Rows <= 16 of a
+    supported shape run fdms_linear_small_m; larger row counts quantise the rows
+    with fdms_quantize_fp8_rows and multiply the decoded FP8 values in fp32 (the
+    products of two e4m3 values are exact in fp32)."""
+    rows, k = x.shape
+    n = weight_fp8.shape[0]
+    if small_m_supported(rows, k, n):
+        return linear_small_m(x.contiguous(), weight_fp8, bias, weight_scale_inv=weight_scale_inv,
+                              quantize_x=quantize_x)
+    sinv = weight_scale_inv.reshape(1, -1).float()
+    w = weight_fp8.float()
+    if quantize_x == QX_NONE:
+        acc = x.float() @ w.t()
+    else:
+        xq, xsi = quantize_fp8_rows(x.contiguous(), torch_form=quantize_x == QX_TORCH)
+        acc = (xq.float() @ w.t()) * xsi.reshape(-1, 1)
+    y = (acc * sinv).to(torch.bfloat16)
+    return y if bias is None else y + bias.to(torch.bfloat16)
+
+
 class LinearBase(nn.Module):
+    """Weights [out_features, in_features] bf16, optionally shadowed or replaced
+    by FP8 rows (``weight_fp8`` [N, K] = the reference's column-major
+    ``weight_fp8_t``, ``weight_scale_inv`` [1, N]) and INT4 groups
+    (``weight_int4`` [N, K/2], ``weight_int4_scale`` / ``_zero`` [N, K/group])."""
 
     def __init__(self, input_size: int, output_size: int, bias: bool = False):
         super().__init__()
@@ -192,52 +292,142 @@ class LinearBase(nn.Module):
             self.bias = nn.Parameter(torch.zeros(output_size), requires_grad=False)
         else:
             self.register_parameter("bias", None)
-        self.quant = None
         self._fp8_weight_enabled = False
         self._fp8_module_name = ""
+        self._fp8_row1_only = False
+        self._fp8_min_rows = 1
+        self._int4_enabled = False
+        self._int4_group_size = 0
 
+    # -- weight conversion ----------------------------------------------------
     def quantize_weight_to_fp8(self, *, keep_bf16_weight: bool = False, module_name: str | None = None,
                                row1_only: bool = False) -> None:
-        """linear.py:813-847: per-output-channel FP8 weights.  ``weight_fp8``
-        is [N, K] row-major, i.e. the reference's column-major ``weight_fp8_t``
-        [K, N] (exposed as that view); ``weight_scale_inv`` is [1, N] fp32."""
+        """linear.py:813-847: per-output-channel FP8 weights, plus the INT4
+        shadow when FASTDMS_INT4_ROW1_WEIGHTS is on and the module is in
+        FASTDMS_INT4_ROW1_SCOPE (829-836)."""
         if row1_only and not keep_bf16_weight:
             raise ValueError("row1-only FP8 shadow requires keeping the BF16 weight")
         w8, sinv = quantize_fp8_rows(self.weight.detach())
-        self.register_buffer("weight_fp8", w8, persistent=False)
-        self.register_buffer("weight_scale_inv", sinv.reshape(1, -1), persistent=False)
+        self._set_buffer("weight_fp8", w8)
+        self._set_buffer("weight_scale_inv", sinv.reshape(1, -1))
+        if qe.int4_weights_enabled() and qe.int4_module_in_scope(module_name):
+            self.quantize_weight_to_int4()
+        self._fp8_min_rows = qe.fp8_module_min_rows(module_name)
+        self._fp8_module_name = module_name or ""
         if not keep_bf16_weight:
-            del self._parameters["weight"]
-            self.register_buffer("weight", torch.empty(0, device=w8.device, dtype=torch.bfloat16), persistent=False)
+            self._drop_bf16_weight()
         self._fp8_weight_enabled = True
         self._fp8_row1_only = bool(row1_only)
-        self._fp8_module_name = module_name or ""
+
+    def quantize_weight_to_int4(self, *, group_size: int | None = None, mode: str | None = None) -> bool:
+        """The INT4 row-1 shadow (linear.py:414-459) with FASTDMS_INT4_ROW1_GROUP_SIZE /
+        _QUANT_MODE by default.  Like the reference it is skipped (False) for a
+        shape the INT4 kernel does not take."""
+        group = qe.int4_group_size() if group_size is None else int(group_size)
+        mode = qe.int4_quant_mode() if mode is None else mode
+        k, n = self.input_size, self.output_size
+        if self.weight.numel() == 0 or k % group or not small_m_supported(1, k, n):
+            return False
+        packed, scale, zero = quantize_int4_groups(self.weight.detach(), group, mode)
+        self._set_buffer("weight_int4", packed)
+        self._set_buffer("weight_int4_scale", scale)
+        self._set_buffer("weight_int4_zero", zero)
+        self._int4_group_size = group
+        self._int4_enabled = True
+        return True
+
+    def _set_buffer(self, name: str, value: torch.Tensor) -> None:
+        if name in self._buffers:
+            self._buffers[name] = value
+        else:
+            self.register_buffer(name, value, persistent=False)
+
+    def _drop_bf16_weight(self) -> None:
+        dev = self.weight.device
+        del self._parameters["weight"]
+        self.register_buffer("weight", torch.empty(0, device=dev, dtype=torch.bfloat16), persistent=False)
 
     @property
     def weight_fp8_t(self) -> torch.Tensor:
         return self.weight_fp8.t()
 
-    def _linear(self, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-        """Dispatch (linear.py:855-926): decode rows -> fdms_linear_small_m (FP8 or
-        bf16 weights); prefill rows -> dequantised or bf16 library GEMM."""
-        x2 = x.reshape(-1, x.shape[-1])
+    # -- dispatch ---------------------------------------------------------------
+    def _row1_mode(self) -> str:
+        """linear.py:860-868: the module's row-1 kernel mode."""
+        name = self._fp8_module_name
+        if name.endswith(".down_proj") and self.weight.numel() == 0:
+            return qe.fp8_down_row1_mode()
+        if name.endswith(".gate_up_proj"):
+            return qe.fp8_gate_up_row1_mode()
+        if ".self_attn." in name:
+            return qe.fp8_attention_row1_mode()
+        return qe.fp8_row1_mode()
+
+    def route(self, rows: int) -> tuple[str, int]:
+        """(path, activation quantisation) for a call of ``rows`` rows, in the
+        reference's order (linear.py:855-926): "int4" (rows <= the INT4 row
+        limit, row-1 mode on), "fp8" row 1 (mode on; quantised or raw
+        activation), "bf16" for a row-1-only shadow, "fp8" small-M (2 <= rows <=
+        FASTDMS_FP8_SMALL_M_TRITON_MAX_ROWS, N % 16 == 0) or "fp8" _fp8_linear
+        (QX_TORCH) once rows >= the module's FP8 minimum or the bf16 weight is
+        gone ("fp8_dequant" when FASTDMS_FP8_LINEAR_IMPL=dequant or K % 16), else "bf16"."""
+        if not self._fp8_weight_enabled:
+            return "bf16", QX_NONE
+        mode = self._row1_mode()
+        if self._int4_enabled and 1 <= rows <= qe.int4_max_rows() and mode != "off":
+            return "int4", QX_NONE
+        if rows == 1 and mode != "off":
+            return "fp8", QX_DIVIDE if mode == "quantized" else QX_NONE
+        if self._fp8_row1_only:
+            return "bf16", QX_NONE
+        if self.weight.numel() == 0 or rows >= self._fp8_min_rows:
+            if (qe.fp8_small_m_enabled() and 1 < rows <= qe.fp8_small_m_max_rows()
+                    and self.output_size % 16 == 0):
+                return "fp8", QX_DIVIDE
+            if (os.environ.get("FASTDMS_FP8_LINEAR_IMPL", "").strip().lower() == "dequant"
+                    or self.input_size % 16):
+                return "fp8_dequant", QX_NONE
+            return "fp8", QX_TORCH
+        return "bf16", QX_NONE
+
+    def run(self, x2: torch.Tensor, bias: torch.Tensor | None, *, epilogue: int = EPI_NONE,
+            route: tuple[str, int] | None = None) -> torch.Tensor:
+        """Execute ``route`` (default: self.route) on rows x2 [rows, K].  With
+        epilogue EPI_SILU_MUL the weight is [gate; up] and the result is the
+        SiluAndMul of the linear's output (fused into the decode kernels)."""
         rows = x2.shape[0]
-        if self._fp8_weight_enabled:
-            if small_m_supported(rows, self.input_size, self.output_size):
-                y = linear_small_m(x2.contiguous(), self.weight_fp8, bias, weight_scale_inv=self.weight_scale_inv)
-                return y.reshape(*x.shape[:-1], self.output_size)
-            if self.weight.numel() == 0:
-                w = (self.weight_fp8.to(torch.bfloat16) * self.weight_scale_inv.reshape(-1, 1).to(torch.bfloat16))
-                return F.linear(x, w, bias)
-            return F.linear(x, self.weight, bias)
-        if small_m_supported(rows, self.input_size, self.output_size) and x2.stride(-1) == 1:
-            y = linear_small_m(x2, self.weight, bias)
-            return y.reshape(*x.shape[:-1], self.output_size)
-        return F.linear(x, self.weight, bias)
+        path, qx = self.route(rows) if route is None else route
+        n_out = self.output_size // 2 if epilogue == EPI_SILU_MUL else self.output_size
+        fused = small_m_supported(rows, self.input_size, n_out) and x2.stride(-1) == 1
+        if path == "int4":
+            return linear_int4_small_m(x2.contiguous(), self.weight_int4, self.weight_int4_scale,
+                                       self.weight_int4_zero, self._int4_group_size, bias, epilogue=epilogue)
+        if path == "fp8" and fused:
+            return linear_small_m(x2.contiguous(), self.weight_fp8, bias, weight_scale_inv=self.weight_scale_inv,
+                                  quantize_x=qx, epilogue=epilogue)
+        if path == "bf16" and fused:
+            return linear_small_m(x2, self.weight, bias, epilogue=epilogue)
+        if path == "fp8":
+            y = fp8_rows_gemm(x2, self.weight_fp8, self.weight_scale_inv, bias, qx)
+        elif path == "fp8_dequant":  # linear.py:645-647: the weight dequantised in the activation dtype
+            w = (self.weight_fp8.to(x2.dtype) * self.weight_scale_inv.reshape(-1, 1).to(x2.dtype))
+            y = F.linear(x2, w, bias)
+        else:
+            y = F.linear(x2, self.weight, bias)
+        if epilogue == EPI_SILU_MUL:
+            g, u = y.float().chunk(2, -1)
+            y = (F.silu(g) * u).to(y.dtype)
+        return y
+
+    def int4_applies(self, rows: int) -> bool:
+        return self.route(rows)[0] == "int4"
+
+    def _linear(self, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        """Dispatch (linear.py:855-926) through ``route``."""
+        y = self.run(x.reshape(-1, x.shape[-1]), bias)
+        return y.reshape(*x.shape[:-1], self.output_size)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.quant is not None:
-            return self.quant(x, self.bias)
         return self._linear(x, self.bias)
 
 
@@ -267,3 +457,26 @@ class QKVParallelLinear(ColumnParallelLinear):
 
 class RowParallelLinear(LinearBase):
     pass
+
+
+def convert_linear_modules_to_fp8(module: nn.Module) -> int:
+    """linear.py:1076-1095: FP8 weights for every LinearBase in
+    FASTDMS_FP8_WEIGHT_SCOPE, attention modules as a row-1-only shadow
+    (FASTDMS_FP8_ATTENTION_ROW1_SHADOW) unless FASTDMS_FP8_ATTENTION_FULL;
+    returns the number of converted modules."""
+    scope = qe.fp8_weight_scope()
+    shadow = qe.fp8_attention_row1_shadow_enabled()
+    full = qe.fp8_attention_full_enabled()
+    converted = 0
+    for name, child in module.named_modules():
+        if not isinstance(child, LinearBase):
+            continue
+        is_attn = ".self_attn." in name
+        use_shadow = shadow and is_attn and not full
+        force_full = full and is_attn
+        if not use_shadow and not force_full and not qe.fp8_module_in_scope(name, scope):
+            continue
+        keep = True if use_shadow else qe.fp8_module_keep_bf16_weight(name)
+        child.quantize_weight_to_fp8(keep_bf16_weight=keep, module_name=name, row1_only=use_shadow)
+        converted += 1
+    return converted

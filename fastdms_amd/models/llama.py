@@ -22,8 +22,8 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm, rms_norm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
-                             QKVParallelLinear, RowParallelLinear, linear_argmax_small_m, linear_small_m,
-                             small_m_supported)
+                             QKVParallelLinear, RowParallelLinear, linear_argmax_small_m, linear_int4_small_m,
+                             linear_small_m, small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -55,13 +55,14 @@ class ModelConfig:
 def _fused_linear(lin: LinearBase, x: torch.Tensor, prologue: int, norm: RMSNorm | None = None,
                   residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
                   epilogue: int = EPI_NONE) -> torch.Tensor:
-    """One fdms_linear_small_m launch for a decode-shaped linear layer, with its
-    bf16 or FP8 weights and optional fused prologue / epilogue."""
-    if lin._fp8_weight_enabled:
-        w, sinv = lin.weight_fp8, lin.weight_scale_inv
-    else:
-        w, sinv = lin.weight, None
-    return linear_small_m(x, w, lin.bias, weight_scale_inv=sinv, prologue=prologue,
+    """One decode-shaped linear launch on the path ``lin.route`` picks (the
+    reference's dispatch order), with the SiLU*up epilogue fused; the RMSNorm
+    prologue is fused for bf16 weights only."""
+    if prologue == PRO_NONE:
+        return lin.run(x, lin.bias, epilogue=epilogue)
+    if lin.route(x.shape[0])[0] != "bf16":
+        raise ValueError("the RMSNorm prologue is fused for bf16 weights only")
+    return linear_small_m(x, lin.weight, lin.bias, prologue=prologue,
                           norm_weight=None if norm is None else norm.weight, eps=1e-6 if norm is None else norm.eps,
                           residual=residual, residual_out=residual_out, epilogue=epilogue)
 
@@ -221,17 +222,15 @@ class LlamaModel(nn.Module):
             x = _fused_linear(mlp.down_proj, act, PRO_NONE)
         h, _ = self.norm(x, res)
         if greedy_out is not None:
-            w, sinv = ((lm_head.weight_fp8, lm_head.weight_scale_inv) if lm_head._fp8_weight_enabled
-                       else (lm_head.weight, None))
-            linear_argmax_small_m(h, w, lm_head.bias, weight_scale_inv=sinv, out=greedy_out)
+            lm_head.greedy_into(h, greedy_out)
             return None
-        return _fused_linear(lm_head, h, PRO_NONE)
+        return lm_head.logits(h)
 
     def decode_fused_supported(self, rows: int, lm_head: LinearBase) -> bool:
         mods = [lm_head]
         for layer in self.layers:
             mods += [layer.self_attn.qkv_proj, layer.self_attn.o_proj, layer.mlp.gate_up_proj, layer.mlp.down_proj]
-        return all(m.quant is None and small_m_supported(rows, m.input_size, m.output_size) for m in mods) and all(
+        return all(small_m_supported(rows, m.input_size, m.output_size) for m in mods) and all(
             layer.mlp.gate_up_proj.output_size % 32 == 0 for layer in self.layers)
 
 

@@ -217,8 +217,10 @@ int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int6
  * Replaces _fp8_row1_matvec(_dot)_kernel and _fp8_small_m_linear_kernel
  * (linear.py:492-632, 665-763) for w_dtype FP8 (W row-major [N, K] = the
  * reference's column-major W8^T [K, N], per-row scale_inv [N]; quantize_x = the
- * per-row dynamic activation quantisation, 448/amax divided directly as its
- * Triton kernels do; y = bf16(acc/x_s*scale_inv), bias added in bf16), and the
+ * per-row dynamic activation quantisation: 1 = 448/amax divided directly as its
+ * Triton kernels do, 2 = reciprocal(amax) * 448 as _fp8_linear's torch
+ * expression (635-662, the torch._scaled_mm path at rows <= 16), 0 = none;
+ * y = bf16(acc/x_s*scale_inv), bias added in bf16), and the
  * BF16 F.linear of the decode step (linear.py:926; y = bf16(acc + bias)) for
  * w_dtype bf16.  prologue 1 = RMSNorm of x (+ residual, fp32 sum; the bf16 sum
  * goes to residual_out, written by one workgroup; layernorm.py:19-40).
@@ -237,15 +239,47 @@ int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const voi
 /* C7 — greedy LM head: token[m] = argmax_n a[m,:] . W[n,:] for m <= 16 rows,
  * ties to the lowest index, NaN first (torch.argmax order).  Replaces
  * _fp8_row1_argmax_stage/reduce + _fp8_row1_argmax (fastdms/layers/embed_head.py:
- * 96-211; FP8 weights, per-row quantised activation, scores in fp32) and
- * greedy_token_ids' F.linear + argmax (491-598; bf16 weights, bf16 logits).
- * One GEMV launch writes each strip's best (part_val / part_idx, m * n/16
- * each), a second reduces them into out_tokens (int64).  Arguments as
- * fdms_linear_small_m. */
+ * 96-211; FP8 weights, per-row quantised activation, scores in fp32:
+ * bf16_scores = 0) and greedy_token_ids' forward + argmax (491-598; bf16
+ * logits: bf16_scores = 1, with FP8 weights the _fp8_linear scores rounded to
+ * bf16).  One GEMV launch writes each strip's best (part_val / part_idx,
+ * m * n/16 each), a second reduces them into out_tokens (int64).  Other
+ * arguments as fdms_linear_small_m. */
 int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int m, int k, const void* w, int w_dtype,
                                int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int quantize_x,
-                               int k_splits, float* workspace, int* counters, float* part_val, int* part_idx,
-                               int64_t* out_tokens, void* stream);
+                               int bf16_scores, int k_splits, float* workspace, int* counters, float* part_val,
+                               int* part_idx, int64_t* out_tokens, void* stream);
+
+/* C7 — FP8 re-ranking of the INT4 head's candidates.  Replaces
+ * _fp8_row1_rerank_topk_kernel / _fp8_row1_rerank_topk (fastdms/layers/
+ * embed_head.py:214-302): per row, score the candidate ids [rows, topk] (int64,
+ * topk in {2, 4, 8, 16, 32}) with the FP8 rows (448/amax activation
+ * quantisation, fp32 scores) and write the best id, the lowest on ties; ids
+ * outside [0, n) score -inf.  k % 16 == 0, 16-byte aligned rows. */
+int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, int k, const void* w_fp8, int64_t w_stride,
+                         const float* w_scale_inv, int n, const int64_t* candidates, int topk, int64_t* out_tokens,
+                         void* stream);
+
+/* C5 — W4A16 decode linear.  Replaces _int4_row1_matvec /
+ * torch._weight_int4pack_mm (fastdms/layers/linear.py:462-478): y[m,n] =
+ * x[m,:] . bf16((q[n,:] - 8) * scale + zero) with per-group bf16 scale / zero
+ * [N, k/group_size] (g_stride per row).  The packing is this library's own:
+ * w_packed[n, j] holds q[n, 2j] (low nibble) and q[n, 2j+1] (high nibble).
+ * epilogue 0 = bf16(acc + bias) into y, 1 = SiLU*up of [gate; up] rows (as
+ * fdms_linear_small_m), 2 = greedy argmax into out_tokens (as
+ * fdms_linear_argmax_small_m).  m <= 16. */
+int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
+                             int64_t w_stride_bytes, const void* group_scale, const void* group_zero,
+                             int group_size, int64_t g_stride, const void* bias, int n, int epilogue, int k_splits,
+                             float* workspace, int* counters, float* part_val, int* part_idx, int64_t* out_tokens,
+                             void* y, int64_t y_stride, void* stream);
+
+/* C5 — INT4 group quantisation of weight rows (linear.py:414-459, symmetric or
+ * asymmetric); q is computed with the fp32 scale / zero, which are stored in
+ * bf16 (456-458).  Output packed as fdms_linear_int4_small_m reads it. */
+int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int64_t rows, int k, int group_size,
+                              int asymmetric, void* out_packed, int64_t out_stride, void* group_scale,
+                              void* group_zero, int64_t g_stride, void* stream);
 
 #ifdef __cplusplus
 }

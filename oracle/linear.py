@@ -80,18 +80,46 @@ def fp8_row1_argmax(x, w8_t, scale_inv) -> int:
     return int(np.flatnonzero(s == s.max())[0])
 
 
+def fp8_rerank_topk(x, candidates, w8_t, scale_inv) -> int:
+    """embed_head.py:214-262: FP8 scores (row-1 activation quantisation) of
+    the candidate ids only; the best one, the lowest id on ties; ids outside
+    [0, N) score -inf."""
+    n = np.asarray(w8_t).shape[1]
+    cand = np.asarray(candidates, np.int64).reshape(-1)
+    ok = (cand >= 0) & (cand < n)
+    s = np.full(cand.shape, -np.inf)
+    if ok.any():
+        sinv = np.asarray(scale_inv, np.float32).reshape(-1)
+        sc = fp8_linear(np.asarray(x, np.float32).reshape(1, -1), np.asarray(w8_t)[:, cand[ok]], sinv[cand[ok]])[0]
+        s[ok] = sc
+    best = s.max()
+    return int(cand[s == best].min())
+
+
 def argmax_lowest(scores) -> np.ndarray:
     """Row-wise argmax, lowest index on ties."""
     s = np.asarray(scores)
     return np.array([int(np.flatnonzero(r == r.max())[0]) for r in s.reshape(-1, s.shape[-1])])
 
 
-def quantize_weight_int4(weight, group_size: int, mode: str = "symmetric"):
+def _div_scalar(a, d: float, device_form: bool) -> np.ndarray:
+    """fp32 ``tensor / python_float``.  On the GPU torch evaluates it as
+    a * fp32(1/d) (its CUDA true-divide kernel multiplies by the reciprocal of
+    a CPU scalar); on the CPU it divides.  The reference quantises on the GPU."""
+    a = np.asarray(a, np.float32)
+    if device_form:
+        return (a * (np.float32(1.0) / np.float32(d))).astype(np.float32)
+    return (a / np.float32(d)).astype(np.float32)
+
+
+def quantize_weight_int4(weight, group_size: int, mode: str = "symmetric", device_form: bool = True):
     """linear.py:414-459 quantisation math (the packing is this build's own).
 
     Returns q [N, K] uint8 in 0..15, scale [N, K/gs] and zero [N, K/gs], both
-    rounded to bf16 (the reference stores scale_zeros in bf16, linear.py:456-458).
-    Dequant: (q - 8) * scale + zero.
+    rounded to bf16 (the reference stores scale_zeros in bf16, linear.py:456-458);
+    the codes use the fp32 scale / zero before that rounding.
+    Dequant: (q - 8) * scale + zero.  device_form: amax / 7.0 and span / 15.0
+    as torch computes them on the GPU (see _div_scalar).
     """
     w = np.asarray(weight, dtype=np.float32)
     n, k = w.shape
@@ -99,7 +127,7 @@ def quantize_weight_int4(weight, group_size: int, mode: str = "symmetric"):
     mode = mode.strip().lower()
     if mode in {"sym", "symmetric"}:
         amax = np.abs(g).max(axis=2)
-        scale = np.where(amax > 0, (amax / np.float32(7.0)).astype(np.float32), np.float32(1.0))
+        scale = np.where(amax > 0, _div_scalar(amax, 7.0, device_form), np.float32(1.0))
         zero = np.zeros_like(scale)
         qs = np.clip(np.rint(g / scale[..., None]), -8, 7)
         q = (qs + 8).astype(np.uint8)
@@ -107,7 +135,7 @@ def quantize_weight_int4(weight, group_size: int, mode: str = "symmetric"):
         wmin, wmax = g.min(axis=2), g.max(axis=2)
         span = (wmax - wmin).astype(np.float32)
         nz = span > 0
-        scale = np.where(nz, (span / np.float32(15.0)).astype(np.float32), np.float32(1.0)).astype(np.float32)
+        scale = np.where(nz, _div_scalar(span, 15.0, device_form), np.float32(1.0)).astype(np.float32)
         zero = np.where(nz, (wmin + np.float32(8.0) * scale).astype(np.float32), wmin).astype(np.float32)
         q = np.clip(np.rint((g - zero[..., None]) / scale[..., None] + 8.0), 0, 15).astype(np.uint8)
     else:

@@ -54,3 +54,27 @@ def require_gpu():
     import pytest
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
+
+
+def torch_int4_reference(w: torch.Tensor, group: int, mode: str):
+    """The reference's quantisation expressions (linear.py:433-452) evaluated by
+    torch on w's device (on the CPU tensor / scalar is a true division, on the GPU
+    a multiply by the scalar's fp32 reciprocal)."""
+    n, k = w.shape
+    grouped = w.reshape(n, k // group, group).to(torch.float32)
+    one = torch.ones((), device=w.device, dtype=torch.float32)
+    if mode == "symmetric":
+        amax = grouped.abs().amax(dim=2)
+        scale = torch.where(amax > 0, amax / 7.0, one)
+        zero = torch.zeros_like(scale)
+        q = (torch.round(grouped / scale.unsqueeze(2)).clamp(-8, 7).to(torch.int16) + 8).to(torch.uint8)
+    else:
+        w_min, w_max = grouped.amin(dim=2), grouped.amax(dim=2)
+        span = w_max - w_min
+        nz = span > 0
+        scale = torch.where(nz, span / 15.0, one)
+        zero = torch.where(nz, w_min + 8.0 * scale, w_min)
+        q = torch.round((grouped - zero.unsqueeze(2)) / scale.unsqueeze(2) + 8.0).clamp(0, 15).to(torch.uint8)
+    return (q.reshape(n, k).cpu().numpy(), scale.to(torch.bfloat16).float().cpu().numpy(),
+            zero.to(torch.bfloat16).float().cpu().numpy())
+

@@ -570,7 +570,7 @@ class Emulator:
         if w_dtype == DT_FP8:
             w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
             si = self.view(wsi, torch.float32, (n,), (1,), "scale_inv").numpy()
-            acc = olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx))
+            acc = olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx), torch_form=qx == 2)
             out = torch.from_numpy(acc.astype(np.float32)).to(torch.bfloat16).float()
             if bv is not None:
                 out = (out + bv).to(torch.bfloat16).float()
@@ -586,10 +586,10 @@ class Emulator:
         self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
         return 0
 
-    def linear_argmax_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, qx, k_splits, ws, counters,
-                              part_val, part_idx, out, stream):
+    def linear_argmax_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, qx, bf16_scores, k_splits, ws,
+                              counters, part_val, part_idx, out, stream):
         """Greedy head: scores as the oracle model's lm_head (bf16 logits) or
-        oracle/linear.py's fp32 FP8 scores, torch.argmax order."""
+        oracle/linear.py's FP8 scores (fp32, or bf16 logits), torch.argmax order."""
         from oracle import linear as olin
         if m == 0:
             return 0
@@ -601,8 +601,13 @@ class Emulator:
         if w_dtype == DT_FP8:
             w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
             si = self.view(wsi, torch.float32, (n,), (1,), "scale_inv").numpy()
-            sc = torch.from_numpy(olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx)).astype(np.float32))
-            if bv is not None:
+            sc = torch.from_numpy(olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx),
+                                                  torch_form=qx == 2).astype(np.float32))
+            if bf16_scores:
+                sc = sc.to(torch.bfloat16).float()
+                if bv is not None:
+                    sc = (sc + bv).to(torch.bfloat16).float()
+            elif bv is not None:
                 sc = sc + bv
         else:
             wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float()
@@ -614,6 +619,70 @@ class Emulator:
         hit = torch.where(torch.isnan(mx), torch.isnan(sc), sc == mx)
         tok = torch.where(hit, torch.arange(n)[None, :], n).min(dim=1).values
         self.view(out, torch.int64, (m,), (1,), "out_tokens").copy_(tok)
+        return 0
+
+    def fp8_rerank_topk(self, x, x_s, rows, k, w, w_s, sinv, n, cand, topk, out, stream):
+        from oracle import linear as olin
+        if rows == 0:
+            return 0
+        a = self.view(x, torch.bfloat16, (rows, k), (x_s, 1), "x").float().numpy()
+        c = self.view(cand, torch.int64, (rows, topk), (topk, 1), "candidates").numpy()
+        w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
+        si = self.view(sinv, torch.float32, (n,), (1,), "scale_inv").numpy()
+        toks = [olin.fp8_rerank_topk(a[r], c[r], w8.T, si) for r in range(rows)]
+        self.view(out, torch.int64, (rows,), (1,), "out").copy_(torch.tensor(toks, dtype=torch.int64))
+        return 0
+
+    def quantize_int4_groups(self, w, w_dtype, w_s, rows, k, group, asym, out, out_s, scale, zero, g_s, stream):
+        from oracle import linear as olin
+        if rows < 0 or k <= 0 or group < 2 or group % 2 or k % group:
+            return 1
+        if rows == 0:
+            return 0
+        wv = self.load(self.view(w, _TORCH[w_dtype], (rows, k), (w_s, 1), "weight"), w_dtype).numpy()
+        q, sc, z = olin.quantize_weight_int4(wv, group, "asymmetric" if asym else "symmetric")
+        packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+        self.view(out, torch.uint8, (rows, k // 2), (out_s, 1), "packed").copy_(torch.from_numpy(packed))
+        self.view(scale, torch.bfloat16, (rows, k // group), (g_s, 1), "scale").copy_(
+            torch.from_numpy(sc).to(torch.bfloat16))
+        self.view(zero, torch.bfloat16, (rows, k // group), (g_s, 1), "zero").copy_(
+            torch.from_numpy(z).to(torch.bfloat16))
+        return 0
+
+    def linear_int4_small_m(self, x, x_s, m, k, w, w_s, scale, zero, group, g_s, bias, n, epilogue, k_splits, ws,
+                            counters, part_val, part_idx, out_tokens, y, y_s, stream):
+        """W4A16 with each weight dequantised to bf16 ((q - 8) * s + z), fp32
+        accumulation, the bf16 linear's bias / epilogue / greedy semantics."""
+        from oracle import linear as olin
+        from oracle import numerics
+        if m == 0 or n == 0:
+            return 0
+        n_out = n // 2 if epilogue == 1 else n
+        if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or k % group or epilogue not in (0, 1, 2):
+            return 1
+        p = self.view(w, torch.uint8, (n, k // 2), (w_s, 1), "packed").numpy()
+        q = np.empty((n, k), np.uint8)
+        q[:, 0::2], q[:, 1::2] = p & 0xF, p >> 4
+        sc = self.view(scale, torch.bfloat16, (n, k // group), (g_s, 1), "scale").float().numpy()
+        z = self.view(zero, torch.bfloat16, (n, k // group), (g_s, 1), "zero").float().numpy()
+        deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, sc, z, group).astype(np.float32)))
+        a = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
+        out = (a @ deq.T).to(torch.bfloat16).float()
+        if bias:  # linear.py:475-477: bias added to the bf16 matmul result
+            out = (out + self.view(bias, torch.bfloat16, (n,), (1,), "bias").float()).to(torch.bfloat16).float()
+        if epilogue == 2:
+            strips = n // 16
+            self.view(part_val, torch.float32, (m, strips), (strips, 1), "part_val")
+            self.view(part_idx, torch.int32, (m, strips), (strips, 1), "part_idx")
+            mx = out.max(dim=1, keepdim=True).values
+            hit = torch.where(torch.isnan(mx), torch.isnan(out), out == mx)
+            tok = torch.where(hit, torch.arange(n)[None, :], n).min(dim=1).values
+            self.view(out_tokens, torch.int64, (m,), (1,), "out_tokens").copy_(tok)
+            return 0
+        if epilogue == 1:
+            g, u = out[:, :n_out], out[:, n_out:]
+            out = (g / (1.0 + torch.exp(-g))) * u
+        self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
         return 0
 
     def prefill_attention(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, num_seqs,

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from native_emulator import cpu_engine
+from oracle import linear as olin
 
 DMS = dict(dms_window_size=32, dms_alpha_scale=10.0, dms_alpha_offset=5.0)
 
@@ -56,7 +57,11 @@ def _run(model, lens, gen, fused_head):
         seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in lens]
         llm.step()
         orc.prefill([(s.seq_id, s.prompt_token_ids, gen) for s in seqs])
-        _check_logits(runner.model.lm_head.last_logits, orc.last_logits, "prefill")
+        if fused_head:
+            want = olin.argmax_lowest(orc.last_logits.float().numpy()).tolist()
+            assert [s.completion_token_ids[0] for s in seqs] == want, "prefill tokens"
+        else:
+            _check_logits(runner.model.lm_head.last_logits, orc.last_logits, "prefill")
         for step in range(gen - 1):
             pos = [len(s) - 1 for s in seqs]
             last = [s.last_token for s in seqs]

@@ -177,3 +177,42 @@ def test_fused_greedy_head_equals_logits_argmax(model, lens):
         del llm
         torch.cuda.synchronize()
     assert outs[0] == outs[1]
+
+
+_QUANT_ENVS = {
+    "fp8_all": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "1"},
+    "fp8_mlp_int4": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "mlp_lm_head",
+                     "FASTDMS_INT4_ROW1_WEIGHTS": "1", "FASTDMS_INT4_ROW1_MAX_ROWS": "8",
+                     "FASTDMS_INT4_ROW1_GROUP_SIZE": "128", "FASTDMS_INT4_ROW1_QUANT_MODE": "asymmetric"},
+}
+
+
+@pytest.mark.parametrize("env", sorted(_QUANT_ENVS))
+def test_quantized_weights_graph_equals_eager(monkeypatch, env):
+    """FP8 / INT4 weights selected by the reference's environment switches
+    (model_runner.py:72-113): graph-replayed decode equals eager decode, and
+    the fused greedy head equals logits + argmax (at more than one row both
+    score the bf16 logits)."""
+    require_gpu()
+    from fastdms_amd import SamplingParams
+    for k, v in _QUANT_ENVS[env].items():
+        monkeypatch.setenv(k, v)
+    rng = np.random.default_rng(6)
+    prompts = _prompts(rng, [300, 517, 64], 512)
+    sp = SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True)
+    outs = []
+    for eager, fused in ((True, True), (False, True), (False, False)):
+        llm = _llm("tiny-llama", eager=eager, fused_head=fused)
+        runner = llm.model_runner
+        assert runner.fp8_weight_modules > 0 and runner.fp8_lm_head
+        layer = runner.model.model.layers[0]
+        if env == "fp8_mlp_int4":
+            assert layer.mlp.down_proj._int4_enabled and not layer.self_attn.o_proj._int4_enabled
+            assert layer.mlp.down_proj.route(3)[0] == "int4"
+        else:
+            assert layer.self_attn.qkv_proj._fp8_weight_enabled and not layer.mlp.down_proj._int4_enabled
+        outs.append([o["token_ids"] for o in llm.generate(prompts, sp)])
+        llm.exit()
+        del llm
+        torch.cuda.synchronize()
+    assert outs[0] == outs[1] == outs[2]

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import require_gpu
+from helpers import require_gpu, torch_int4_reference
 from oracle import linear as olin
 from oracle import numerics
 
@@ -134,11 +134,12 @@ def test_linear_small_m_split_k_is_consistent(splits):
                 f"silu split {splits}", ulps=2.0, atol=2e-3)
 
 
-@pytest.mark.parametrize("quantize_x", [True, False])
+@pytest.mark.parametrize("quantize_x", [0, 1, 2])
 @pytest.mark.parametrize("m,n,k", [(1, 3072, 2048), (8, 2048, 8192), (5, 512, 256)])
 def test_linear_small_m_fp8_matches_oracle(quantize_x, m, n, k):
-    """FP8 weights (C2/C3): y = bf16(sum xq*w8 / x_s * scale_inv) + bias in bf16,
-    against the float64 oracle (linear.py:492-763)."""
+    """FP8 weights (C2/C3, and C4's _fp8_linear at decode rows with
+    quantize_x=2): y = bf16(sum xq*w8 / x_s * scale_inv) + bias in bf16, against
+    the float64 oracle (linear.py:492-763)."""
     require_gpu()
     from fastdms_amd.layers.linear import linear_small_m, quantize_fp8_rows
     g = torch.Generator().manual_seed(m * 3 + n + k + quantize_x)
@@ -147,7 +148,8 @@ def test_linear_small_m_fp8_matches_oracle(quantize_x, m, n, k):
     w8, sinv = quantize_fp8_rows(w.cuda())
     y = linear_small_m(x.cuda(), w8, bias.cuda(), weight_scale_inv=sinv, quantize_x=quantize_x)
     w8_t, sinv_ref = olin.quantize_weight_to_fp8(w.float().numpy())
-    acc = olin.fp8_linear(x.float().numpy(), w8_t, sinv_ref, quantize_x=quantize_x)
+    acc = olin.fp8_linear(x.float().numpy(), w8_t, sinv_ref, quantize_x=bool(quantize_x),
+                          torch_form=quantize_x == 2)
     want = torch.from_numpy(numerics.bf16_round(acc.astype(np.float32)))
     want = (want + bias.float()).to(torch.bfloat16)
     _close_bf16(y, want, "fp8", ulps=2.0, atol=1e-3)
@@ -208,3 +210,119 @@ def test_linear_argmax_ties_and_nan():
     assert linear_argmax_small_m(x.cuda(), w.cuda()).cpu().tolist() == [100, 2000]
     w[777, 2] = float("nan")                       # a NaN weight makes score 777 NaN for every row
     assert linear_argmax_small_m(x.cuda(), w.cuda()).cpu().tolist() == [777, 777]
+
+
+@pytest.mark.parametrize("mode", ["symmetric", "asymmetric"])
+@pytest.mark.parametrize("group", [32, 128, 256])
+def test_quantize_int4_groups_bit_exact(mode, group):
+    """C5 quantisation (linear.py:414-459): codes bit-exact vs the oracle,
+    bf16 scale / zero bit-exact; the packing puts q[2j] in the low nibble."""
+    require_gpu()
+    from fastdms_amd.layers.linear import quantize_int4_groups
+    g = torch.Generator().manual_seed(group + len(mode))
+    w = (torch.randn(48, 1024, generator=g) * 0.05 + (0.02 if mode == "asymmetric" else 0.0)).to(torch.bfloat16)
+    w[3, :group] = 0.0
+    packed, scale, zero = quantize_int4_groups(w.cuda(), group, mode)
+    q_ref, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group, mode)
+    p = packed.cpu().numpy()
+    q = np.empty((48, 1024), np.uint8)
+    q[:, 0::2] = p & 0xF
+    q[:, 1::2] = p >> 4
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(scale.float().cpu().numpy(), s_ref)
+    assert np.array_equal(zero.float().cpu().numpy(), z_ref)
+    # the reference's torch expressions evaluated on this GPU agree too
+    q_t, s_t, z_t = torch_int4_reference(w.cuda(), group, mode)
+    assert np.array_equal(q, q_t) and np.array_equal(s_ref, s_t) and np.array_equal(z_ref, z_t)
+
+
+@pytest.mark.parametrize("m,n,k,group", [(1, 3072, 2048, 128), (8, 2048, 8192, 256), (5, 512, 256, 32)])
+def test_linear_int4_small_m_matches_oracle(m, n, k, group):
+    """W4A16: x @ dequant(W)^T with dequant = bf16((q-8)*s + z) (the oracle's
+    float64 dequant differs by the bf16 rounding of each weight only)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_int4_small_m, quantize_int4_groups
+    gen = torch.Generator().manual_seed(m + n + k)
+    x, w = _bf16((m, k), gen), _bf16((n, k), gen, 0.05)
+    bias = _bf16((n,), gen, 0.1)
+    packed, scale, zero = quantize_int4_groups(w.cuda(), group)
+    q, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group)
+    deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, s_ref, z_ref, group).astype(np.float32)))
+    y = linear_int4_small_m(x.cuda(), packed, scale, zero, group, bias.cuda())
+    want = (_ref_linear(x, deq, None).float() + bias.float()).to(torch.bfloat16)  # linear.py:475-477
+    _close_bf16(y, want, "int4", ulps=2.0, atol=2e-3)
+    tok = linear_int4_small_m(x.cuda(), packed, scale, zero, group, greedy=True).cpu()
+    sc = _ref_linear(x, deq, None).double()
+    for i in range(m):
+        if int(tok[i]) != int(sc[i].argmax()):
+            assert float(sc[i].max() - sc[i, tok[i]]) <= 1e-3 * float(sc[i].abs().max())
+    if n % 32 == 0:
+        ye = linear_int4_small_m(x.cuda(), packed, scale, zero, group, epilogue=EPI_SILU_MUL)
+        gu = _ref_linear(x, deq, None).float()
+        f = n // 2
+        _close_bf16(ye, (torch.nn.functional.silu(gu[:, :f]) * gu[:, f:]).to(torch.bfloat16), "int4 silu",
+                    ulps=2.0, atol=2e-3)
+
+
+@pytest.mark.parametrize("m,n,k", [(9, 2048, 2048), (40, 768, 512), (16, 3072, 1000)])
+def test_fp8_rows_gemm_prefill_rows(m, n, k):
+    """_fp8_linear for prefill row counts (linear.py:635-662): torch-form
+    activation quantisation, fp32 products, bf16 output, bias in bf16."""
+    require_gpu()
+    from fastdms_amd.layers.linear import QX_TORCH, fp8_rows_gemm, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m + n + k)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    bias = _bf16((n,), g, 0.1)
+    w8, sinv = quantize_fp8_rows(w.cuda())
+    y = fp8_rows_gemm(x.cuda(), w8, sinv.reshape(1, -1), bias.cuda(), QX_TORCH)
+    w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
+    acc = olin.fp8_linear(x.float().numpy(), w8_t, sref, quantize_x=True, torch_form=True)
+    want = (torch.from_numpy(numerics.bf16_round(acc.astype(np.float32))) + bias.float()).to(torch.bfloat16)
+    _close_bf16(y, want, "fp8 rows gemm", ulps=2.0, atol=1e-3)
+
+
+@pytest.mark.parametrize("m", [2, 8])
+def test_linear_argmax_fp8_bf16_scores(m):
+    """The FP8 head at more than one row: argmax of the _fp8_linear logits
+    rounded to bf16 (forward().argmax(), embed_head.py:543-583); bf16 ties go to
+    the lowest index, so the result equals the argmax of the fused logits."""
+    require_gpu()
+    from fastdms_amd.layers.linear import QX_TORCH, linear_argmax_small_m, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(31 + m)
+    n, k = 32768, 2048
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    w8, si = quantize_fp8_rows(w.cuda())
+    tok = linear_argmax_small_m(x.cuda(), w8, weight_scale_inv=si, quantize_x=QX_TORCH, bf16_scores=True).cpu()
+    logits = linear_small_m(x.cuda(), w8, weight_scale_inv=si, quantize_x=QX_TORCH).cpu()
+    assert tok.tolist() == olin.argmax_lowest(logits.float().numpy()).tolist()
+    w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
+    sc = numerics.bf16_round(olin.fp8_linear(x.float().numpy(), w8_t, sref, torch_form=True).astype(np.float32))
+    for i in range(m):
+        gap = float(sc[i].max() - sc[i, int(tok[i])])
+        assert gap <= 2 ** -7 * float(np.abs(sc[i]).max()), (i, gap)
+
+
+def test_fp8_rerank_topk_matches_oracle():
+    """embed_head.py:214-302: FP8 re-scoring of candidate ids, lowest id on
+    ties, invalid ids never chosen."""
+    require_gpu()
+    from fastdms_amd.layers.embed_head import fp8_rerank_topk
+    from fastdms_amd.layers.linear import quantize_fp8_rows
+    g = torch.Generator().manual_seed(5)
+    n, k = 4096, 2048
+    x, w = _bf16((3, k), g), _bf16((n, k), g, 0.02)
+    w[17] = w[9]                                      # identical rows: a tie between ids 9 and 17
+    w8, si = quantize_fp8_rows(w.cuda())
+    cand = torch.randint(0, n, (3, 16), generator=g)
+    cand[1, :2] = torch.tensor([17, 9])
+    cand[2, 5] = n + 3                                # out of range: scores -inf
+    x[1] = 0.0
+    x[1, :k] = (w[9].float() * 10).to(torch.bfloat16)  # row 1 prefers the duplicated rows
+    got = fp8_rerank_topk(x.cuda(), cand.cuda(), w8, si.reshape(1, -1)).cpu().tolist()
+    w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
+    want = [olin.fp8_rerank_topk(x[r].float().numpy(), cand[r].numpy(), w8_t, sref) for r in range(3)]
+    assert got[1] == 9 and want[1] == 9
+    for r in range(3):
+        if got[r] != want[r]:     # accumulation order only: the two scores are within noise
+            sc = olin.fp8_linear(x[r:r + 1].float().numpy(), w8_t[:, [got[r], want[r]]], sref[:, [got[r], want[r]]])
+            assert abs(sc[0, 0] - sc[0, 1]) <= 1e-5 * abs(sc[0, 1]), (r, got[r], want[r])

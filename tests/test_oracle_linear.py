@@ -6,6 +6,8 @@ import torch
 from oracle import linear as olin
 from oracle import numerics
 
+from helpers import torch_int4_reference
+
 
 def test_fp8_weight_quantisation_matches_torch_formula():
     """The reference's own torch expression (linear.py:386-388, 813-823),
@@ -118,3 +120,19 @@ def test_int4_linear_is_dequantised_matmul():
     q, s, z = olin.quantize_weight_int4(w, 64)
     assert np.allclose(olin.int4_linear(x, q, s, z, 64), x.astype(np.float64) @ olin.int4_dequant(q, s, z, 64).T)
     assert numerics.bf16_round(s).dtype == np.float32
+
+
+def test_int4_quantisation_matches_torch_formula():
+    """With true division (torch on the CPU) the oracle equals the reference's
+    torch expressions bit for bit; the device form (reciprocal multiply) is a
+    different rounding that changes some fp32 scales."""
+    g = torch.Generator().manual_seed(9)
+    w = (torch.randn(64, 512, generator=g) * 0.05 + 0.01).to(torch.bfloat16)
+    w[7, :128] = 0.0
+    w[9, 128:256] = 0.25
+    for mode in ("symmetric", "asymmetric"):
+        q_t, s_t, z_t = torch_int4_reference(w, 128, mode)
+        q, s, z = olin.quantize_weight_int4(w.float().numpy(), 128, mode, device_form=False)
+        assert np.array_equal(q, q_t) and np.array_equal(s, s_t) and np.array_equal(z, z_t)
+    a = np.random.default_rng(11).random(4000).astype(np.float32) + 0.01
+    assert 0 < int((olin._div_scalar(a, 7.0, True) != olin._div_scalar(a, 7.0, False)).sum()) < a.size
