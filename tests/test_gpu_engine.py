@@ -182,7 +182,8 @@ def test_fused_greedy_head_equals_logits_argmax(model, lens):
 _QUANT_ENVS = {
     "fp8_all": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "1"},
     "fp8_mlp_int4": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "mlp_lm_head",
-                     "FASTDMS_INT4_ROW1_WEIGHTS": "1", "FASTDMS_INT4_ROW1_MAX_ROWS": "8",
+                     "FASTDMS_INT4_ROW1_WEIGHTS": "1", "FASTDMS_INT4_ROW1_SCOPE": "mlp+lm_head",
+                     "FASTDMS_INT4_ROW1_MAX_ROWS": "8",
                      "FASTDMS_INT4_ROW1_GROUP_SIZE": "128", "FASTDMS_INT4_ROW1_QUANT_MODE": "asymmetric"},
 }
 
