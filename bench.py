@@ -55,7 +55,8 @@ def attention_roofline(llm, seqs, replays: int):
     kernel on the live decode state: one graph holds the kernel of every layer
     with the exact decode-step arguments; HIP events bracket `replays` replays."""
     import torch
-    from fastdms_amd.layers.compact_attention import choose_num_splits, compact_decode_attention
+    from fastdms_amd.layers.compact_attention import (attention_split_plan, compact_decode_attention,
+                                                      mfma_attention_path)
 
     runner = llm.model_runner
     mgr = runner.compact_kv_manager
@@ -91,11 +92,15 @@ def attention_roofline(llm, seqs, replays: int):
     qo_bytes = 2 * b * cfg.num_attention_heads * cfg.head_dim * 2                # q read + out write (bf16)
     meta_bytes = 2 * 4 * b * cfg.num_key_value_heads * len(layers)               # base + live (int32)
     bytes_per_launch = (kv_bytes + qo_bytes * len(layers) + meta_bytes) / len(layers)
-    splits = choose_num_splits(q.device, b * cfg.num_key_value_heads, hint)
+    mfma = mfma_attention_path(q, arenas[0][0], cfg.num_attention_heads // cfg.num_key_value_heads)
+    splits, split_rows = attention_split_plan(q.device, b * cfg.num_key_value_heads, hint, mfma)
+    if split_rows:  # per-pair split counts, as the kernel derives them
+        splits = int(((lv + split_rows - 1) // split_rows).clamp(1, splits).max())
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "decode_attn_wave_kernel", "avg_launch_us": round(per_launch_s * 1e6, 3),
+            "kernel": "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel",
+            "avg_launch_us": round(per_launch_s * 1e6, 3),
             "bytes_per_launch": int(bytes_per_launch), "splits": splits,
             "live_tokens_mean_per_head": round(float(lv.float().mean()), 1)}
 

@@ -37,7 +37,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_dms_rope_store_compact_decode": "pillppillllpllppilpllpllpiiiifffiiip",
     "fdms_rope_inplace": "pillliipllpp",
     "fdms_store_compact_kvcache": "ppillllppilplliiip",
-    "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiifpllpp",
+    "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",

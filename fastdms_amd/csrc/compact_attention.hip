@@ -27,6 +27,13 @@ static bool fdms_force_generic_attention() {
   return e && e[0] == '1';
 }
 
+// FASTDMS_AMD_ATTN_MFMA=0 keeps FP8 calls off the matrix-core kernel (read per
+// call; used to compare kernels on the same inputs).
+static bool fdms_mfma_attention_enabled() {
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_MFMA");
+  return !(e && e[0] == '0');
+}
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -827,6 +834,391 @@ __global__ __launch_bounds__(kThreads) void decode_attn_wave_kernel(
   if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path (FP8 K/V, bf16 q, G <= 4, D = 64 / 128).
+//
+// Both products run on the 16-block 4x4x4 MFMA (v_mfma_f32_4x4x4_16b_*).  A
+// wave takes its tokens in groups of 64; lane l = 4*s + k (s = 0..15,
+// k = 0..3) owns token s + 16*k of the group.
+//   QK^T: block s, A = K rows of the lane's token, D/4 dims at a time
+//         (fp8 -> bf16 is exact), B = Q[head j][dims] (bf16).  Register r of
+//         lane (s, j) ends up holding S[token s + 16*r][head j].
+//   P.V:  16 steps; at step s every block multiplies block s's A -- lane
+//         (s, i)'s four probabilities P[head i][tokens s + 16*k], broadcast
+//         by the instruction itself (CBSZ = 4, ABID = s) -- with
+//         B = V[tokens s + 16*k][dim 4*b + j] (fp8 -> f16, exact).  Each
+//         lane (b, j) accumulates O[heads 0..3][dim 4*b + j] (+ 64 for
+//         D = 128): no reduction across lanes is needed afterwards.
+//         The B operands come from a per-wave transposed copy of the group's
+//         V in LDS (VT[dim][s] = bytes of tokens s, s+16, s+32, s+48), made
+//         with byte permutes from the lane's own 16-byte row slices.
+// Scores are scaled (scale * log2 e) in fp32 after the product; the softmax
+// is online per group with a wave-wide maximum per head, so a rescale costs
+// four multiplies.  P enters the P.V product rounded to f16 (relative error
+// <= 2^-11); the denominator sums the fp32 values.  A workgroup covers one
+// (seq, kv head) pair, or one 64-aligned split of it; splits are merged by
+// the last workgroup of the pair as in the kernels above.
+// ---------------------------------------------------------------------------
+namespace {
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef _Float16 v4f16_t __attribute__((ext_vector_type(4)));
+typedef float v4f32_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ v4i16_t fp8x4_to_bf16x4(uint32_t w) {
+  const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false));
+  const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true));
+  return __builtin_bit_cast(v4i16_t, v2u32_t{lo, hi});
+}
+__device__ __forceinline__ v4f16_t fp8x4_to_f16x4(uint32_t w) {
+  const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false));
+  const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true));
+  return __builtin_bit_cast(v4f16_t, v2u32_t{lo, hi});
+}
+
+// Sum / max over the 16 lanes of a wave that share lane % 4.
+__device__ __forceinline__ float blocks_sum(float v) {
+  v += dpp_f<0x128>(v);  // row_ror:8
+  v += dpp_f<0x124>(v);  // row_ror:4
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float blocks_max(float v) {
+  v = fmaxf(v, dpp_f<0x128>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+// value of lane (l & ~3) + I (quad broadcast)
+template <int I>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), I * 0x55, 0xF, 0xF, true));
+}
+
+// A group's K row words (the lane's token) and V row slices (tokens s + 16*kk,
+// bytes [D/4 * q, D/4 * (q + 1)) with q = lane % 4), zero past `end`.
+template <int D>
+struct MfmaGroup {
+  static constexpr int kW = D / 4;   // words of K per lane, and of V per lane
+  uint32_t k[kW];
+  uint32_t v[4][kW / 4];
+};
+
+// Row of span rank r (flat: bo + r; paged: through the block table).
+template <bool PAGED>
+__device__ __forceinline__ int64_t span_row(const SpanAddr& addr, int b, int h, int64_t bo, int r) {
+  if constexpr (PAGED) {
+    const int32_t page = addr.table[b * addr.tb_b + h * addr.tb_h + (r >> addr.page_shift)];
+    return ((int64_t)page << addr.page_shift) + (r & ((1 << addr.page_shift) - 1));
+  } else {
+    return bo + r;
+  }
+}
+
+// Loads are unconditional: ranks past `end` read row end-1 (live, so finite)
+// instead, which keeps the wait counters exact across the loop.  Their
+// scores are masked to -inf, so their K and V never reach the output.
+// Flat spans address rows from the span's first row (kspan / vspan, uniform)
+// with 32-bit offsets; paged spans go through the block table per row.
+template <int D, bool PAGED>
+__device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* __restrict__ kspan,
+                                                const uint8_t* __restrict__ vspan, int64_t c_s,
+                                                const SpanAddr& addr, int b, int h, int g0, int end, int lane) {
+  constexpr int KQ = D / 16;  // 16-byte chunks per K row
+  constexpr int VQ = D / 64;  // 16-byte chunks per V slice
+  const int s = lane >> 2, q = lane & 3;
+  const uint4* ksrc;
+  const uint4* vsrc[4];
+  if constexpr (PAGED) {
+    ksrc = reinterpret_cast<const uint4*>(kspan + span_row<true>(addr, b, h, 0, min(g0 + s + 16 * q, end - 1)) * c_s);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + span_row<true>(addr, b, h, 0, min(g0 + s + 16 * kk, end - 1)) * c_s +
+                                                q * (D / 4));
+  } else {
+    const uint32_t cs = (uint32_t)c_s;
+    ksrc = reinterpret_cast<const uint4*>(kspan + __umul24((uint32_t)min(g0 + s + 16 * q, end - 1), cs));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + (__umul24((uint32_t)min(g0 + s + 16 * kk, end - 1), cs) +
+                                                         (uint32_t)(q * (D / 4))));
+  }
+#pragma unroll
+  for (int m = 0; m < KQ; ++m) {
+    const uint4 x = ksrc[m];
+    g.k[4 * m] = x.x;
+    g.k[4 * m + 1] = x.y;
+    g.k[4 * m + 2] = x.z;
+    g.k[4 * m + 3] = x.w;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int m = 0; m < VQ; ++m) {
+      const uint4 x = vsrc[kk][m];
+      g.v[kk][4 * m] = x.x;
+      g.v[kk][4 * m + 1] = x.y;
+      g.v[kk][4 * m + 2] = x.z;
+      g.v[kk][4 * m + 3] = x.w;
+    }
+}
+
+constexpr int kVtStride = 20;  // dwords per dim row of the transposed V tile (16 steps + pad)
+
+}  // namespace
+
+template <int D, int NW, bool PAGED>
+__global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, const uint8_t* __restrict__ ck,
+    const uint8_t* __restrict__ cv, int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b,
+    int64_t bo_h, const int32_t* __restrict__ block_tables, int64_t bt_b, int64_t bt_h, int page_shift, int paged,
+    const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
+    int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int group_size,
+    int num_pairs, int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
+    int64_t rcs_d, const int64_t* __restrict__ rope_pos) {
+  constexpr int NT = NW * kWave;
+  constexpr int KW = MfmaGroup<D>::kW;
+  constexpr int VW = KW / 4;    // V words per token slice
+  constexpr int NA = D / 64;    // accumulator quads per lane
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[4][D];  // bf16 q, heads >= G zero
+  __shared__ __attribute__((aligned(16))) uint32_t s_vt[NW][D * kVtStride];
+  __shared__ float s_wm[NW][4], s_wl[NW][4];
+  __shared__ __attribute__((aligned(16))) float s_wacc[NW][4][D];
+  __shared__ int s_last;
+
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds;
+  const int slot = lin / kXcds;
+  const int pair = (slot / num_splits) * kXcds + xcd;
+  const int split = slot - (slot / num_splits) * num_splits;
+  if (pair >= num_pairs) return;  // uniform per workgroup
+  const int b = pair / num_kv_heads;
+  const int h = pair - b * num_kv_heads;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the group loop scalar
+  const int lane = tid & 63;
+  const int jj = lane & 3, ss = lane >> 2;
+  const int G = group_size;
+
+  // q elements of this thread (issued before anything they do not depend on)
+  constexpr int QPT = (4 * D + NT - 1) / NT;  // q elements per thread
+  uint32_t qraw[QPT];
+#pragma unroll
+  for (int x = 0; x < QPT; ++x) {
+    const int i = tid + x * NT;
+    const int g = i / D, d = i - g * D;
+    qraw[x] = (i < 4 * D && g < G) ? (uint32_t)q[b * qs_b + (int64_t)(h * G + g) * qs_h + d].bits : 0u;
+  }
+
+  const int live = live_counts[b * lc_b + h * lc_h];
+  const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
+  const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
+  // this pair's split count: ceil(live / split_rows) (at most num_splits) when
+  // split_rows > 0, else num_splits; workgroups past it have nothing to do
+  const int ns = split_rows > 0 ? min(num_splits, max(1, (live + split_rows - 1) / split_rows)) : num_splits;
+  if (split >= ns) return;  // uniform per workgroup
+  const int per = (((live + ns - 1) / ns) + 63) & ~63;
+  const int t0 = min(live, split * per);
+  const int t1 = min(live, t0 + per);
+  const int ngroups = (t1 - t0 + 63) >> 6;
+
+  const uint8_t* kspan = PAGED ? ck : ck + bo * c_s;  // flat: the span's first row
+  const uint8_t* vspan = PAGED ? cv : cv + bo * c_s;
+  MfmaGroup<D> cur;
+  int gi = wave;
+  if (gi < ngroups) mfma_load_group<D, PAGED>(cur, kspan, vspan, c_s, addr, b, h, t0 + gi * 64, t1, lane);
+
+  if (rope_pos) {
+    // rotate q here (decision lane zeroed), rounded to bf16 like a stored q
+    constexpr int half = D / 2;
+    const int64_t pos = rope_pos[b];
+    for (int i = tid; i < 4 * half; i += NT) {
+      const int g = i / half, jx = i - g * half;
+      uint32_t y1b = 0u, y2b = 0u;
+      if (g < G) {
+        const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
+        const float x1 = ld<bf16_t>(qh + jx);
+        const float x2 = (g == 0 && jx == half - 1) ? 0.0f : ld<bf16_t>(qh + jx + half);
+        float y1, y2;
+        rope_f32(x1, x2, rope_cs[pos * rcs_p + (int64_t)jx * rcs_d], rope_cs[pos * rcs_p + (int64_t)(jx + half) * rcs_d],
+                 &y1, &y2);
+        y1b = f32_to_bf16(y1);
+        y2b = f32_to_bf16(y2);
+      }
+      s_q[g][jx] = (uint16_t)y1b;
+      s_q[g][jx + half] = (uint16_t)y2b;
+    }
+  } else {
+#pragma unroll
+    for (int x = 0; x < QPT; ++x) {
+      const int i = tid + x * NT;
+      if (i < 4 * D) s_q[i / D][i % D] = (uint16_t)qraw[x];
+    }
+  }
+  __syncthreads();
+
+  const float qscale = scale * kLog2e;
+  float m_j = -INFINITY;  // running max of head jj (same in every lane of that head)
+  float l_j = 0.0f;       // this lane's share of the denominator of head jj
+  v4f32_t acc[NA][2];  // even / odd P.V steps (two independent chains)
+#pragma unroll
+  for (int a = 0; a < NA; ++a) acc[a][0] = acc[a][1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
+  uint32_t* vt = s_vt[wave];
+
+  // One group: QK^T, V -> transposed LDS tile, online softmax, P.V.
+  auto process = [&](MfmaGroup<D>& grp, int gidx) {
+    // S^T for the group: register r of lane (s, j) = S[token s + 16r][head j]
+    v4f32_t sq[2];  // two independent chains
+    sq[0] = sq[1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < KW; ++n) {
+      const v4i16_t qn = *reinterpret_cast<const v4i16_t*>(&s_q[jj][4 * n]);
+      sq[n & 1] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(fp8x4_to_bf16x4(grp.k[n]), qn, sq[n & 1], 0, 0, 0);
+    }
+    // V slices -> transposed tile: VT[dim][s] = bytes of tokens s, s+16, s+32, s+48
+#pragma unroll
+    for (int w = 0; w < VW; ++w) {
+      const uint32_t x01l = __builtin_amdgcn_perm(grp.v[1][w], grp.v[0][w], 0x05010400u);
+      const uint32_t x01h = __builtin_amdgcn_perm(grp.v[1][w], grp.v[0][w], 0x07030602u);
+      const uint32_t x23l = __builtin_amdgcn_perm(grp.v[3][w], grp.v[2][w], 0x05010400u);
+      const uint32_t x23h = __builtin_amdgcn_perm(grp.v[3][w], grp.v[2][w], 0x07030602u);
+      const int d0 = jj * (D / 4) + 4 * w;  // dim of byte 0 of word w of this lane's slice
+      vt[(d0 + 0) * kVtStride + ss] = __builtin_amdgcn_perm(x23l, x01l, 0x05040100u);
+      vt[(d0 + 1) * kVtStride + ss] = __builtin_amdgcn_perm(x23l, x01l, 0x07060302u);
+      vt[(d0 + 2) * kVtStride + ss] = __builtin_amdgcn_perm(x23h, x01h, 0x05040100u);
+      vt[(d0 + 3) * kVtStride + ss] = __builtin_amdgcn_perm(x23h, x01h, 0x07060302u);
+    }
+    // the registers are free again: the wave's next group goes in flight now
+    // and lands while the softmax and P.V below run
+    if (gidx + NW < ngroups)
+      mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
+    // scores, online softmax per head
+    const int tb = t0 + gidx * 64 + ss;
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sc[r] = (tb + 16 * r < t1) ? (sq[0][r] + sq[1][r]) * qscale : -INFINITY;
+    const float gmax = blocks_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    const float m_new = fmaxf(m_j, gmax);
+    const float alpha_j = (m_j == m_new) ? 1.0f : __builtin_amdgcn_exp2f(m_j - m_new);
+    m_j = m_new;
+    const float al[4] = {quad_bcast<0>(alpha_j), quad_bcast<1>(alpha_j), quad_bcast<2>(alpha_j),
+                         quad_bcast<3>(alpha_j)};
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[a][0][i] *= al[i];
+        acc[a][1][i] *= al[i];
+      }
+    v4f16_t pa;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[r] - m_new);  // -inf -> 0
+      pa[r] = (_Float16)p;
+      lsum += p;
+    }
+    l_j = l_j * alpha_j + lsum;
+    __builtin_amdgcn_wave_barrier();  // VT writes of the wave before its reads (LDS is in order per wave)
+    // P.V: step s broadcasts block s's probabilities
+#define FDMS_PV_STEP(S)                                                                                            \
+    {                                                                                                              \
+      _Pragma("unroll") for (int a = 0; a < NA; ++a) {                                                             \
+        const uint32_t vw = vt[(64 * a + lane) * kVtStride + (S)];                                                 \
+        acc[a][(S) & 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(pa, fp8x4_to_f16x4(vw), acc[a][(S) & 1], 4, (S), 0);  \
+      }                                                                                                            \
+    }
+    FDMS_PV_STEP(0) FDMS_PV_STEP(1) FDMS_PV_STEP(2) FDMS_PV_STEP(3) FDMS_PV_STEP(4) FDMS_PV_STEP(5)
+    FDMS_PV_STEP(6) FDMS_PV_STEP(7) FDMS_PV_STEP(8) FDMS_PV_STEP(9) FDMS_PV_STEP(10) FDMS_PV_STEP(11)
+    FDMS_PV_STEP(12) FDMS_PV_STEP(13) FDMS_PV_STEP(14) FDMS_PV_STEP(15)
+#undef FDMS_PV_STEP
+    __builtin_amdgcn_wave_barrier();  // reads done before the next group's writes
+  };
+  for (; gi < ngroups; gi += NW) process(cur, gi);  // wave-uniform
+
+  // per wave: max, denominator, accumulators -> LDS; combine the waves
+  const float lw = blocks_sum(l_j);
+  if (lane < 4) {
+    s_wm[wave][lane] = m_j;
+    s_wl[wave][lane] = lw;
+  }
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_wacc[wave][i][64 * a + lane] = acc[a][0][i] + acc[a][1][i];
+  __syncthreads();
+  const int n_out = G * D;
+  const int64_t stride = (int64_t)G * (D + 2);
+  float* mine = ws + ((int64_t)pair * num_splits + split) * stride;
+  for (int o = tid; o < n_out; o += NT) {
+    const int og = o / D, od = o - og * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][og]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float mw = s_wm[w][og];
+      const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      L += s_wl[w][og] * f;
+      A += s_wacc[w][og][od] * f;
+    }
+    if (ns == 1) {
+      out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(A / L);
+    } else {
+      store_agent(mine + 2 * G + o, A);
+      if (od == 0) {
+        store_agent(mine + og, M);
+        store_agent(mine + G + og, L);
+      }
+    }
+  }
+  if (ns == 1) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == ns - 1);
+  __syncthreads();
+  if (!s_last) return;
+  const float* all = ws + (int64_t)pair * num_splits * stride;
+  for (int o = tid; o < n_out; o += NT) {
+    const int og = o / D, od = o - og * D;
+    float M = -INFINITY, L = 0.0f, Acc = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+      float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+      for (int x = 0; x < kMergeBatch; ++x) {
+        mv[x] = -INFINITY;
+        lv[x] = av[x] = 0.0f;
+        if (s0 + x < ns) {
+          const float* ps = all + (s0 + x) * stride;
+          mv[x] = load_agent(ps + og);
+          lv[x] = load_agent(ps + G + og);
+          av[x] = load_agent(ps + 2 * G + o);
+        }
+      }
+      float bm = M;
+#pragma unroll
+      for (int x = 0; x < kMergeBatch; ++x) bm = fmaxf(bm, mv[x]);
+      const float f = (M == -INFINITY || bm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - bm);
+      L *= f;
+      Acc *= f;
+#pragma unroll
+      for (int x = 0; x < kMergeBatch; ++x) {
+        const float wgt = (mv[x] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mv[x] - bm);
+        L += lv[x] * wgt;
+        Acc += av[x] * wgt;
+      }
+      M = bm;
+    }
+    out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(Acc / L);
+  }
+  if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 namespace {
 
 template <int D, typename KT>
@@ -864,10 +1256,11 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     int kv_dtype, int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* block_tables,
     int64_t bt_b, int64_t bt_h, int page_size, const int32_t* live_counts, int64_t lc_b, int64_t lc_h, void* out,
     int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads, int group_size,
-    int head_dim, int num_splits, float scale, const float* rope_cos_sin, int64_t rcs_p, int64_t rcs_d,
-    const int64_t* rope_positions, void* stream) {
+    int head_dim, int num_splits, int split_rows, float scale, const float* rope_cos_sin, int64_t rcs_p,
+    int64_t rcs_d, const int64_t* rope_positions, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > kMaxG) return (int)hipErrorInvalidValue;
-  if (head_dim <= 0 || head_dim > kMaxD || num_splits <= 0 || num_splits > 65535) return (int)hipErrorInvalidValue;
+  if (head_dim <= 0 || head_dim > kMaxD || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
+    return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
   if (!q || !compact_k || !compact_v || !live_counts || !out) return (int)hipErrorInvalidValue;
   int paged = 0, page_shift = 0;
@@ -888,6 +1281,33 @@ FDMS_EXPORT int fdms_compact_decode_attention(
                         (c_s * kv_size) % 16 == 0 && ((uintptr_t)compact_k % 16) == 0 &&
                         ((uintptr_t)compact_v % 16) == 0 && (group_size == 1 || group_size == 2 ||
                         group_size == 4 || group_size == 8) && !fdms_force_generic_attention();
+  const bool mfma_ok = tiled_ok && kv_dtype == kFP8 && group_size <= 4 && fdms_mfma_attention_enabled();
+  if (mfma_ok) {
+    const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
+    if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+#define FDMS_MFMA_ARGS                                                                                          \
+  (const bf16_t*)q, qs_b, qs_h, (const uint8_t*)compact_k, (const uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, \
+      block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h, (bf16_t*)out, os_b, os_h, workspace,     \
+      counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, rope_cos_sin, rcs_p, rcs_d,        \
+      rope_positions
+#define FDMS_MFMA_LAUNCH(DD, NWV, PG)                                                                       \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
+                     (hipStream_t)stream, FDMS_MFMA_ARGS)
+    if (head_dim == 64) {
+      const char* ew = std::getenv("FASTDMS_AMD_ATTN_WAVES");
+      if (ew && ew[0] == '1' && ew[1] == '6') {
+        if (paged) FDMS_MFMA_LAUNCH(64, 16, true); else FDMS_MFMA_LAUNCH(64, 16, false);
+      } else {
+        if (paged) FDMS_MFMA_LAUNCH(64, 8, true); else FDMS_MFMA_LAUNCH(64, 8, false);
+      }
+    } else {
+      if (paged) FDMS_MFMA_LAUNCH(128, 8, true); else FDMS_MFMA_LAUNCH(128, 8, false);
+    }
+#undef FDMS_MFMA_LAUNCH
+#undef FDMS_MFMA_ARGS
+    FDMS_LAUNCH_CHECK();
+    return 0;
+  }
   if (tiled_ok) {
     const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;

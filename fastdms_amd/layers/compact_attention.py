@@ -89,19 +89,47 @@ def attention_workspace(device: torch.device, n_floats: int, n_counters: int):
     return entry[0], entry[1]
 
 
+_MFMA_CAP_SPLITS = 64
+
+
 def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size: int, head_dim: int) -> None:
     """Allocate the split workspace for the largest split count choose_num_splits
     can return for up to max_pairs (seq, kv head) pairs."""
     target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
-    worst = max(p * min(1024, -(-target // p)) for p in range(1, max_pairs + 1))
+    worst = max(p * max(min(1024, -(-target // p)), _MFMA_CAP_SPLITS) for p in range(1, max_pairs + 1))
     attention_workspace(device, worst * group_size * (head_dim + 2), max_pairs)
 
 
+def mfma_attention_path(q: torch.Tensor, kv: torch.Tensor, group: int) -> bool:
+    """True when fdms_compact_decode_attention runs the matrix-core kernel for
+    these operands (bf16 q, FP8 K/V, G <= 4, D = 64 / 128, 16-byte rows)."""
+    if os.environ.get("FASTDMS_AMD_ATTN_MFMA", "1").strip() == "0":
+        return False
+    if os.environ.get("FASTDMS_AMD_ATTN_GENERIC", "0").strip() == "1":
+        return False
+    fp8 = getattr(torch, "float8_e4m3fn", None)
+    return (q.dtype == torch.bfloat16 and kv.dtype == fp8 and group <= 4 and q.shape[-1] in (64, 128)
+            and kv.stride(0) % 16 == 0 and kv.data_ptr() % 16 == 0)
+
+
+def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: bool) -> tuple[int, int]:
+    """(num_splits, split_rows) for fdms_compact_decode_attention.
+
+    Matrix-core kernel: a pair gets one workgroup per `split_rows` live rows
+    (2048 with >= 32 pairs, 512 with fewer), decided per pair inside the
+    kernel, because merging splits costs three memory round trips while the
+    per-pair work at decode sizes is small; num_splits only bounds it from
+    the batch's live bound.  Other kernels: choose_num_splits, even splits."""
+    if mfma:
+        rows = 2048 if pairs >= 32 else 512
+        return int(min(_MFMA_CAP_SPLITS, max(1, -(-int(max_live) // rows)))), rows
+    return choose_num_splits(device, pairs, max_live), 0
+
+
 def choose_num_splits(device: torch.device, pairs: int, max_live: int) -> int:
-    """Splits per (seq, kv head).  The kernel is latency-bound at decode sizes:
-    about one workgroup per CU lets every workgroup issue all of its K/V loads
-    in one round trip, and each split keeps at least ~128 live tokens so the
-    merge stays cheap."""
+    """Even splits per (seq, kv head) for the VALU kernels: about one
+    workgroup per CU, each split keeping >= 128 live tokens so the merge
+    stays cheap."""
     target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
     s = max(1, -(-target // max(1, pairs)))
     s = min(s, max(1, -(-int(max_live) // 128)))
@@ -116,7 +144,7 @@ def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, l
     if out is None:
         out = torch.empty_like(q)
     pairs = batch * num_kv_heads
-    splits = choose_num_splits(q.device, pairs, max_live)
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma_attention_path(q, kv_k, group))
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     if q.stride(2) != 1 or kv_k.stride(1) != 1 or out.stride(2) != 1:
         raise ValueError("compact attention needs a contiguous head_dim axis")
@@ -128,7 +156,7 @@ def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, l
              nat.ptr(bt), 0 if bt is None else bt.stride(0), 0 if bt is None else bt.stride(1), int(page_size),
              live_counts.data_ptr(), live_counts.stride(0), live_counts.stride(1), out.data_ptr(), out.stride(0),
              out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads, group, head_dim, splits,
-             float(scale), nat.ptr(rope_cache), 0 if rope_cache is None else rope_cache.stride(0),
+             split_rows, float(scale), nat.ptr(rope_cache), 0 if rope_cache is None else rope_cache.stride(0),
              0 if rope_cache is None else rope_cache.stride(2), nat.ptr(rope_positions), nat.stream())
     return out
 

@@ -129,15 +129,20 @@ int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype,
  * batch*num_kv_heads ints that must be zero before the first call (every call
  * leaves them zero).  Calls that share counters must not overlap in time.
  * rope_positions != NULL rotates q in-kernel with the decision lane zeroed
- * (B4, _compact_decode_grouped_splitk_partial_qrope_kernel, compact_attention.py:418-534). */
+ * (B4, _compact_decode_grouped_splitk_partial_qrope_kernel, compact_attention.py:418-534).
+ * split_rows == 0 divides every pair's live span evenly over num_splits; with
+ * split_rows > 0 the matrix-core kernel (bf16 q, FP8 K/V, group_size <= 4,
+ * head_dim 64 / 128) gives each pair ceil(live / split_rows) splits, at most
+ * num_splits, and a pair with one split skips the merge (other kernels ignore
+ * split_rows). */
 int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int64_t qs_h, const void* compact_k,
                                   const void* compact_v, int kv_dtype, int64_t c_s, const int32_t* base_offsets,
                                   int64_t bo_b, int64_t bo_h, const int32_t* block_tables, int64_t bt_b,
                                   int64_t bt_h, int page_size, const int32_t* live_counts, int64_t lc_b,
                                   int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace,
                                   int* counters, int batch, int num_kv_heads, int group_size, int head_dim,
-                                  int num_splits, float scale, const float* rope_cos_sin, int64_t rcs_p,
-                                  int64_t rcs_d, const int64_t* rope_positions, void* stream);
+                                  int num_splits, int split_rows, float scale, const float* rope_cos_sin,
+                                  int64_t rcs_p, int64_t rcs_d, const int64_t* rope_positions, void* stream);
 
 /* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
  * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /

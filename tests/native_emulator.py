@@ -359,7 +359,7 @@ class Emulator:
 
     def compact_decode_attention(self, q, qdt, qs_b, qs_h, ck, cv, kvdt, c_s, base, bo_b, bo_h, bt, bt_b, bt_h,
                                  page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
-                                 scale, rope_cs, rcs_p, rcs_d, rope_pos, stream):
+                                 split_rows, scale, rope_cs, rcs_p, rcs_d, rope_pos, stream):
         if B == 0:
             return 0
         if splits > 1:

@@ -22,7 +22,7 @@ def _rel_err(got, ref):
 
 def _force_splits(monkeypatch, n):
     import fastdms_amd.layers.compact_attention as ca
-    monkeypatch.setattr(ca, "choose_num_splits", lambda device, pairs, max_live: n)
+    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (n, 0))
 
 
 @pytest.mark.parametrize("splits", [None, 1, 2, 3, 20])
@@ -124,6 +124,49 @@ def test_ragged_batch_spans_match_oracle(d, kv_code):
                                    torch.from_numpy(live).cuda(), max_live_count=8320)
     torch.cuda.synchronize()
     assert _rel_err(values_of(out), ref) <= TOL_LOWP
+
+
+@pytest.mark.parametrize("d,paged", [(64, False), (128, False), (64, True)])
+def test_matrix_core_per_pair_splits(monkeypatch, d, paged):
+    """Matrix-core kernel with split_rows > 0: pairs of one launch take 1, 2 or
+    3 splits from their own live counts (workgroups past a pair's count exit,
+    one-split pairs skip the merge), twice in a row so the counters are reused."""
+    require_gpu()
+    import fastdms_amd.layers.compact_attention as ca
+    rng = np.random.default_rng(d + paged)
+    b, hkv, g, page = 4, 4, 4, 16
+    live = np.array([[1, 64, 65, 511], [512, 513, 1024, 1025], [1535, 1536, 7, 900], [130, 1200, 2, 333]], np.int32)
+    span = 1600
+    base = (np.arange(b * hkv).reshape(b, hkv) * span).astype(np.int32)
+    ck = numerics.cast(rng.standard_normal((b * hkv * span, d)).astype(np.float32), numerics.DT_FP8)
+    cv = numerics.cast(rng.standard_normal((b * hkv * span, d)).astype(np.float32), numerics.DT_FP8)
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    ref = oatt.compact_decode_attention(q, ck, cv, base, live)
+    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (4, 512))
+    qd, ckd, cvd = from_values(q, numerics.DT_BF16), from_values(ck, numerics.DT_FP8), from_values(cv, numerics.DT_FP8)
+    assert ca.mfma_attention_path(qd, ckd, g)
+    if paged:
+        # page p of span (b, h) is physical page perm[...]: same rows, permuted pages
+        npg = span // page
+        perm = rng.permutation(b * hkv * npg).astype(np.int32)
+        table = perm.reshape(b, hkv, npg)
+        ckp, cvp = np.empty_like(ck), np.empty_like(cv)
+        for bi in range(b):
+            for h in range(hkv):
+                for pg in range(npg):
+                    src = slice(int(base[bi, h]) + pg * page, int(base[bi, h]) + (pg + 1) * page)
+                    dst = slice(int(table[bi, h, pg]) * page, (int(table[bi, h, pg]) + 1) * page)
+                    ckp[dst], cvp[dst] = ck[src], cv[src]
+        outs = [ca.compact_decode_attention_paged(qd, from_values(ckp, numerics.DT_FP8),
+                                                  from_values(cvp, numerics.DT_FP8), torch.from_numpy(table).cuda(),
+                                                  torch.from_numpy(live).cuda(), page_size=page, max_live_count=1600)
+                for _ in range(2)]
+    else:
+        outs = [ca.compact_decode_attention(qd, ckd, cvd, torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda(),
+                                            max_live_count=1600) for _ in range(2)]
+    torch.cuda.synchronize()
+    for out in outs:
+        assert _rel_err(values_of(out), ref) <= TOL_LOWP
 
 
 def test_split_count_does_not_change_fp32_result(monkeypatch):
