@@ -38,6 +38,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_rope_inplace": "pillliipllpp",
     "fdms_store_compact_kvcache": "ppillllppilplliiip",
     "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpp",
+    "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",

@@ -970,23 +970,45 @@ constexpr int kVtStride = 20;  // dwords per dim row of the transposed V tile (1
 
 }  // namespace
 
-template <int D, int NW, bool PAGED>
+// Inputs of the decode preprocess fused in front of the attention (the
+// reference's fused_dms_rope_store_compact_decode, compact_attention.py:67-209):
+// raw k / v rows of the step, RoPE table and positions, append slots, DMS
+// decision output and threshold.
+struct DecodePre {
+  const bf16_t* k;
+  int64_t ks_b, ks_h;
+  const bf16_t* v;
+  int64_t vs_b, vs_h;
+  const float* cos_sin;
+  int64_t cs_p, cs_d;
+  const int64_t* positions;
+  const int32_t* slot;
+  int64_t sm_b, sm_h;
+  uint8_t* evict_out;
+  int64_t ev_b, ev_h;
+  float alpha_scale, alpha_offset, threshold;
+  int positive_scale;
+};
+
+template <int D, int NW, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
-    const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, const uint8_t* __restrict__ ck,
-    const uint8_t* __restrict__ cv, int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b,
+    const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, uint8_t* __restrict__ ck,
+    uint8_t* __restrict__ cv, int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b,
     int64_t bo_h, const int32_t* __restrict__ block_tables, int64_t bt_b, int64_t bt_h, int page_shift, int paged,
     const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
     int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int group_size,
     int num_pairs, int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
-    int64_t rcs_d, const int64_t* __restrict__ rope_pos) {
+    int64_t rcs_d, const int64_t* __restrict__ rope_pos, const DecodePre pre) {
   constexpr int NT = NW * kWave;
+  constexpr int NWX = FUSED ? NW + 1 : NW;  // combine slots: the waves (+ the appended token)
   constexpr int KW = MfmaGroup<D>::kW;
   constexpr int VW = KW / 4;    // V words per token slice
   constexpr int NA = D / 64;    // accumulator quads per lane
   __shared__ __attribute__((aligned(16))) uint16_t s_q[4][D];  // bf16 q, heads >= G zero
   __shared__ __attribute__((aligned(16))) uint32_t s_vt[NW][D * kVtStride];
-  __shared__ float s_wm[NW][4], s_wl[NW][4];
-  __shared__ __attribute__((aligned(16))) float s_wacc[NW][4][D];
+  __shared__ float s_wm[NWX][4], s_wl[NWX][4];
+  __shared__ __attribute__((aligned(16))) float s_wacc[NWX][4][D];
+  __shared__ float s_knew[FUSED ? D : 1], s_vnew[FUSED ? D : 1];  // appended row as stored (FP8 values)
   __shared__ int s_last;
 
   const int lin = blockIdx.x;
@@ -1022,8 +1044,20 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   if (split >= ns) return;  // uniform per workgroup
   const int per = (((live + ns - 1) / ns) + 63) & ~63;
   const int t0 = min(live, split * per);
-  const int t1 = min(live, t0 + per);
-  const int ngroups = (t1 - t0 + 63) >> 6;
+  int t1 = min(live, t0 + per);
+  // Fused preprocess: the step's token is rank live - 1 (slot >= 0); its row is
+  // being written by this launch, so no workgroup reads it back -- the split
+  // holding that rank adds the token from the values it computes itself.
+  int32_t app_slot = -1;
+  bool new_tok = false;
+  if constexpr (FUSED) {
+    app_slot = pre.slot[b * pre.sm_b + h * pre.sm_h];
+    if (app_slot >= 0 && live > 0) {
+      new_tok = t0 < live && t1 == live;
+      t1 = min(t1, live - 1);
+    }
+  }
+  const int ngroups = max(0, (t1 - t0 + 63) >> 6);
 
   const uint8_t* kspan = PAGED ? ck : ck + bo * c_s;  // flat: the span's first row
   const uint8_t* vspan = PAGED ? cv : cv + bo * c_s;
@@ -1031,7 +1065,55 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   int gi = wave;
   if (gi < ngroups) mfma_load_group<D, PAGED>(cur, kspan, vspan, c_s, addr, b, h, t0 + gi * 64, t1, lane);
 
-  if (rope_pos) {
+  if constexpr (FUSED) {
+    // decode preprocess: q pairs (decision lane read, then zeroed), the key
+    // pair j and the value element d of the step's row; the workgroup of split
+    // 0 writes the decision and appends the FP8 row at the slot
+    constexpr int half = D / 2;
+    const int64_t pos = pre.positions[b];
+    const float* cs = pre.cos_sin + pos * pre.cs_p;
+    for (int i = tid; i < 5 * half + D; i += NT) {
+      if (i < 4 * half) {
+        const int g = i / half, jx = i - g * half;
+        uint32_t y1b = 0u, y2b = 0u;
+        if (g < G) {
+          const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
+          const float x1 = ld<bf16_t>(qh + jx);
+          float x2 = ld<bf16_t>(qh + jx + half);
+          if (g == 0 && jx == half - 1) {
+            if (split == 0)
+              pre.evict_out[b * pre.ev_b + h * pre.ev_h] =
+                  dms_decide(x2, pre.alpha_scale, pre.alpha_offset, pre.threshold, pre.positive_scale) ? 1 : 0;
+            x2 = 0.0f;
+          }
+          float y1, y2;
+          rope_f32(x1, x2, cs[(int64_t)jx * pre.cs_d], cs[(int64_t)(jx + half) * pre.cs_d], &y1, &y2);
+          y1b = f32_to_bf16(y1);
+          y2b = f32_to_bf16(y2);
+        }
+        s_q[g][jx] = (uint16_t)y1b;
+        s_q[g][jx + half] = (uint16_t)y2b;
+      } else if (i < 5 * half) {
+        const int jx = i - 4 * half;
+        const bf16_t* kh = pre.k + b * pre.ks_b + h * pre.ks_h;
+        float y1, y2;
+        rope_f32(ld<bf16_t>(kh + jx), ld<bf16_t>(kh + jx + half), cs[(int64_t)jx * pre.cs_d],
+                 cs[(int64_t)(jx + half) * pre.cs_d], &y1, &y2);
+        const uint32_t k1 = f32_to_fp8(y1), k2 = f32_to_fp8(y2);
+        s_knew[jx] = fp8_to_f32(k1);
+        s_knew[jx + half] = fp8_to_f32(k2);
+        if (split == 0 && app_slot >= 0) {
+          ck[(int64_t)app_slot * c_s + jx] = (uint8_t)k1;
+          ck[(int64_t)app_slot * c_s + jx + half] = (uint8_t)k2;
+        }
+      } else {
+        const int d = i - 5 * half;
+        const uint32_t v8 = f32_to_fp8(ld<bf16_t>(pre.v + b * pre.vs_b + h * pre.vs_h + d));
+        s_vnew[d] = fp8_to_f32(v8);
+        if (split == 0 && app_slot >= 0) cv[(int64_t)app_slot * c_s + d] = (uint8_t)v8;
+      }
+    }
+  } else if (rope_pos) {
     // rotate q here (decision lane zeroed), rounded to bf16 like a stored q
     constexpr int half = D / 2;
     const int64_t pos = rope_pos[b];
@@ -1140,6 +1222,28 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   };
   for (; gi < ngroups; gi += NW) process(cur, gi);  // wave-uniform
 
+  if constexpr (FUSED) {
+    // the appended token as one more partial: m = its score, l = 1, acc = v
+    if (wave == NW - 1) {
+      float sg[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float part = 0.0f;
+#pragma unroll
+        for (int d = lane; d < D; d += kWave) part += bf16_to_f32(s_q[g][d]) * s_knew[d];
+        sg[g] = wave_sum(part);
+      }
+      if (lane < 4) {
+        const float sl = lane == 0 ? sg[0] : lane == 1 ? sg[1] : lane == 2 ? sg[2] : sg[3];
+        s_wm[NW][lane] = new_tok ? sl * qscale : -INFINITY;
+        s_wl[NW][lane] = 1.0f;
+      }
+#pragma unroll
+      for (int d = lane; d < D; d += kWave)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) s_wacc[NW][g][d] = s_vnew[d];
+    }
+  }
   // per wave: max, denominator, accumulators -> LDS; combine the waves
   const float lw = blocks_sum(l_j);
   if (lane < 4) {
@@ -1158,10 +1262,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     const int og = o / D, od = o - og * D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][og]);
+    for (int w = 0; w < NWX; ++w) M = fmaxf(M, s_wm[w][og]);
     float L = 0.0f, A = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
+    for (int w = 0; w < NWX; ++w) {
       const float mw = s_wm[w][og];
       const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       L += s_wl[w][og] * f;
@@ -1286,12 +1390,12 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
 #define FDMS_MFMA_ARGS                                                                                          \
-  (const bf16_t*)q, qs_b, qs_h, (const uint8_t*)compact_k, (const uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, \
+  (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h,             \
       block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h, (bf16_t*)out, os_b, os_h, workspace,     \
       counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, rope_cos_sin, rcs_p, rcs_d,        \
-      rope_positions
+      rope_positions, DecodePre{}
 #define FDMS_MFMA_LAUNCH(DD, NWV, PG)                                                                       \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, false>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
                      (hipStream_t)stream, FDMS_MFMA_ARGS)
     if (head_dim == 64) {
       const char* ew = std::getenv("FASTDMS_AMD_ATTN_WAVES");
@@ -1335,6 +1439,50 @@ FDMS_EXPORT int fdms_compact_decode_attention(
                          bo_b, bo_h, block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h, (QT*)out,
                          os_b, os_h, workspace, counters, num_kv_heads, group_size, head_dim, num_splits, scale,
                          rope_cos_sin, rcs_p, rcs_d, rope_positions)));
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Decode preprocess + attention in one launch: the reference's
+// fused_dms_rope_store_compact_decode(store_q=False, store_transient_k=False)
+// followed by compact_decode_attention with in-kernel q RoPE
+// (compact_attention.py:67-209, 418-534, 1010-1336; llama.py:112-134).  q, k,
+// v are the step's raw rows; q and k are not written back.  The appended token
+// is rank live-1 of span (b, h) (prepare_decode_metadata: slot = base + live,
+// then live += 1).  Matrix-core path only: bf16 q/k/v, FP8 flat spans,
+// group_size <= 4, head_dim 64 / 128, 16-byte aligned rows.
+FDMS_EXPORT int fdms_fused_decode_attention(
+    const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+    const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+    float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
+    int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
+    int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
+    int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, void* stream) {
+  if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4) return (int)hipErrorInvalidValue;
+  if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
+    return (int)hipErrorInvalidValue;
+  if (batch == 0) return 0;
+  if (!q || !k || !v || !cos_sin || !positions || !slot_mapping || !evict_out || !compact_k || !compact_v ||
+      !base_offsets || !live_counts || !out)
+    return (int)hipErrorInvalidValue;
+  if (c_s % 16 || ((uintptr_t)compact_k % 16) || ((uintptr_t)compact_v % 16)) return (int)hipErrorInvalidValue;
+  if (num_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
+  const int pairs = batch * num_kv_heads;
+  if (pairs > 65535) return (int)hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
+                      slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
+                      positive_scale};
+#define FDMS_FUSED_LAUNCH(DD)                                                                                    \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 8, false, true>), dim3((unsigned)blocks), dim3(8 * kWave), 0, \
+                     (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,   \
+                     c_s, base_offsets, bo_b, bo_h, nullptr, 0, 0, 0, 0, live_counts, lc_b, lc_h, (bf16_t*)out,     \
+                     os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, \
+                     nullptr, 0, 0, nullptr, pre)
+  if (head_dim == 64) FDMS_FUSED_LAUNCH(64); else FDMS_FUSED_LAUNCH(128);
+#undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;
 }

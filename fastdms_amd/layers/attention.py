@@ -13,7 +13,8 @@ from torch import nn
 
 from .. import _native as nat
 from ..utils.context import get_context
-from .compact_attention import compact_decode_attention, store_compact_kvcache
+from .compact_attention import (compact_decode_attention, fused_dms_rope_store_compact_decode_attention,
+                                store_compact_kvcache)
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
@@ -68,3 +69,15 @@ class Attention(nn.Module):
                                         max_live_count=ctx.compact_max_live_count,
                                         q_rope_positions=positions if compact_q_rope else None,
                                         q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None)
+
+    def forward_fused_decode(self, q, k, v, positions, cos_sin_cache, evict_out, alpha_scale, alpha_offset):
+        """Decode step of this layer in one launch: DMS decision, RoPE, FP8
+        append of k / v and compact attention (q / k / v raw from qkv_proj)."""
+        ctx = get_context()
+        base, live, slot = ctx.compact_base_offsets, ctx.compact_live_counts, ctx.compact_slot_mapping
+        if base.ndim == 3:
+            base, live, slot = base[self.layer_id], live[self.layer_id], slot[self.layer_id]
+        return fused_dms_rope_store_compact_decode_attention(
+            q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, slot, evict_out, positions, base,
+            live, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
+            scale=self.scale, max_live_count=ctx.compact_max_live_count)

@@ -321,6 +321,76 @@ def fused_dms_rope_store_compact_decode(q: torch.Tensor, k: torch.Tensor, v: tor
              int(bool(store_transient_k)), nat.stream())
 
 
+def fused_decode_attention_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                     compact_k: torch.Tensor) -> bool:
+    """True when fused_dms_rope_store_compact_decode_attention can run: the
+    matrix-core attention path with bf16 q/k/v rows."""
+    group = q.shape[1] // max(1, k.shape[1])
+    return (mfma_attention_path(q, compact_k, group) and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+            and q.stride(2) == 1 and k.stride(2) == 1 and v.stride(2) == 1 and compact_k.stride(1) == 1
+            and os.environ.get("FASTDMS_AMD_FUSED_DECODE_ATTN", "1").strip() != "0")
+
+
+def fused_dms_rope_store_compact_decode_attention(
+        q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos_sin_cache: torch.Tensor, compact_k: torch.Tensor,
+        compact_v: torch.Tensor, slot_mapping: torch.Tensor, evict_out: torch.Tensor, positions: torch.Tensor,
+        base_offsets: torch.Tensor, live_counts: torch.Tensor, *, num_kv_heads: int, alpha_scale: float,
+        alpha_offset: float, scale: float | None = None, max_live_count: int | None = None,
+        out: torch.Tensor | None = None) -> torch.Tensor:
+    """One launch for fused_dms_rope_store_compact_decode(store_q=False,
+    store_transient_k=False) followed by compact_decode_attention with the q
+    RoPE done in the kernel (the reference's inline-q-RoPE decode order,
+    llama.py:112-134).  q, k, v are the raw rows of the step and are not
+    modified; ``live_counts`` already counts the appended token (rank
+    live - 1, stored at ``slot_mapping``).  Returns the attention output."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
+        raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
+    batch, num_q_heads, head_dim = q.shape
+    if k.shape != (batch, num_kv_heads, head_dim) or num_q_heads % num_kv_heads:
+        raise ValueError(f"q/k shape mismatch: q={tuple(q.shape)}, k={tuple(k.shape)}, num_kv_heads={num_kv_heads}")
+    group = num_q_heads // num_kv_heads
+    for name, t in (("slot_mapping", slot_mapping), ("evict_out", evict_out), ("base_offsets", base_offsets),
+                    ("live_counts", live_counts)):
+        if tuple(t.shape) != (batch, num_kv_heads):
+            raise ValueError(f"expected {name} {(batch, num_kv_heads)}, got {tuple(t.shape)}")
+    if evict_out.dtype != torch.bool:
+        raise ValueError("evict_out must be bool")
+    if positions.shape != (batch,):
+        raise ValueError(f"expected positions {(batch,)}, got {tuple(positions.shape)}")
+    if cos_sin_cache.ndim != 3 or cos_sin_cache.shape[2] != head_dim or cos_sin_cache.dtype != torch.float32:
+        raise ValueError(f"expected an fp32 cos_sin_cache [positions, 1, {head_dim}]")
+    if not fused_decode_attention_supported(q, k, v, compact_k):
+        raise ValueError("fused decode attention needs bf16 q/k/v, FP8 16-byte compact rows, group <= 4, "
+                         "head_dim 64 or 128")
+    nat.require_cuda(q, k, v, compact_k, compact_v, positions, what="fused decode attention")
+    if max_live_count is None:
+        max_live_count = int(live_counts.max().item())
+    if scale is None:
+        scale = head_dim ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    if out.stride(2) != 1:
+        raise ValueError("out needs a contiguous head_dim axis")
+    pairs = batch * num_kv_heads
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True)
+    ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
+    slot_mapping = slot_mapping.to(dtype=torch.int32)
+    live_counts = live_counts.to(dtype=torch.int32)
+    base_offsets = base_offsets.to(dtype=torch.int32)
+    positions = positions.to(dtype=torch.int64)
+    s_, off, thr, positive = dms_threshold_args(alpha_scale, alpha_offset)
+    ev = evict_out.view(torch.uint8)
+    nat.call("fdms_fused_decode_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+             k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0),
+             cos_sin_cache.stride(2), positions.data_ptr(), slot_mapping.data_ptr(), slot_mapping.stride(0),
+             slot_mapping.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), s_, off, thr, positive,
+             compact_k.data_ptr(), compact_v.data_ptr(), compact_k.stride(0), base_offsets.data_ptr(),
+             base_offsets.stride(0), base_offsets.stride(1), live_counts.data_ptr(), live_counts.stride(0),
+             live_counts.stride(1), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), counters.data_ptr(),
+             batch, num_kv_heads, group, head_dim, splits, split_rows, float(scale), nat.stream())
+    return out
+
+
 def _expiry(incremental: bool, *, positions_per_lh, evict_per_lh, live_counts, base_offsets, compact_k, compact_v,
             current_positions, window_size):
     num_seqs, num_kv_heads, max_capacity = positions_per_lh.shape

@@ -18,7 +18,7 @@ from ..layers.activation import silu_and_mul
 from ..layers.attention import Attention
 from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled, compact_attention_splitk_enabled,
                                         dms_decode_store_transient_k_enabled, dms_fused_decode_preprocess_enabled,
-                                        fused_dms_rope_store_compact_decode)
+                                        fused_decode_attention_supported, fused_dms_rope_store_compact_decode)
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm, rms_norm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
@@ -114,6 +114,16 @@ class LlamaAttention(nn.Module):
             evict_out = None
             if ctx.dms_layer_evictions_buffer is not None:
                 evict_out = ctx.dms_layer_evictions_buffer[layer_id]
+            if (can_fuse and not dms_decode_store_transient_k_enabled()
+                    and fused_decode_attention_supported(q, k, v, self.attn.compact_k_cache)):
+                # decision + RoPE + append + attention in one launch
+                if evict_out is None:
+                    evict_out = torch.empty((q.shape[0], self.num_kv_heads), device=q.device, dtype=torch.bool)
+                o = self.attn.forward_fused_decode(q, k, v, positions, self.rotary_emb.cos_sin_cache, evict_out,
+                                                   ctx.dms_alpha_scale, ctx.dms_alpha_offset)
+                if ctx.dms_layer_evictions is not None:
+                    ctx.dms_layer_evictions[layer_id] = evict_out
+                return o.view(o.shape[0], -1)
             if can_fuse:
                 inline_q_rope = (compact_attention_inline_q_rope_enabled() and compact_attention_splitk_enabled()
                                  and q.shape[0] == 1 and self.head_dim % 2 == 0 and self.head_dim >= 32)

@@ -144,6 +144,27 @@ int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int6
                                   int num_splits, int split_rows, float scale, const float* rope_cos_sin,
                                   int64_t rcs_p, int64_t rcs_d, const int64_t* rope_positions, void* stream);
 
+/* A9 + B2-B5 — decode preprocess and attention in one launch: the reference's
+ * fused_dms_rope_store_compact_decode(store_q=False, store_transient_k=False)
+ * (compact_attention.py:67-209, 1010-1113) followed by compact_decode_attention
+ * with in-kernel q RoPE (418-534, 1116-1336), as llama.py:112-134 sequences them.
+ * q / k / v are the step's raw bf16 rows (not written back).  The DMS decision
+ * goes to evict_out, RoPE(k) and v are appended as FP8 at slot_mapping[b,h]
+ * (skipped when < 0), and the appended token is rank live-1 of the flat span
+ * (prepare_decode_metadata has already counted it).  Matrix-core path only:
+ * FP8 compact K/V with 16-byte rows, group_size <= 4, head_dim 64 / 128.
+ * Workspace, counters and split_rows as for fdms_compact_decode_attention. */
+int fdms_fused_decode_attention(const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b,
+                                int64_t ks_h, const void* v, int64_t vs_b, int64_t vs_h, const float* cos_sin,
+                                int64_t cs_p, int64_t cs_d, const int64_t* positions, const int32_t* slot_mapping,
+                                int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+                                float alpha_scale, float alpha_offset, float threshold, int positive_scale,
+                                void* compact_k, void* compact_v, int64_t c_s, const int32_t* base_offsets,
+                                int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b, int64_t lc_h,
+                                void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
+                                int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows,
+                                float scale, void* stream);
+
 /* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
  * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /
  * dms_expiry_incremental_one_layer (compact_attention.py:690-965) and the

@@ -334,6 +334,23 @@ class Emulator:
                 cvf[cv0 + r * c_s + torch.arange(D)] = tmp
         return 0
 
+    def fused_decode_attention(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
+                               slot, sm_b, sm_h, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv, c_s, base,
+                               bo_b, bo_h, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
+                               split_rows, scale, stream):
+        """The documented composition: preprocess (store_q = store_transient_k =
+        0) then attention with in-kernel q RoPE over the span incl. the append."""
+        if B == 0:
+            return 0
+        if G > 4 or D not in (64, 128):
+            return 1
+        self.dms_rope_store_compact_decode(q, DT_BF16, qs_b, qs_h, k, v, DT_BF16, ks_b, ks_h, vs_b, vs_h, cos_sin,
+                                           cs_p, cs_d, ck, cv, DT_FP8, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h,
+                                           positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, stream)
+        return self.compact_decode_attention(q, DT_BF16, qs_b, qs_h, ck, cv, DT_FP8, c_s, base, bo_b, bo_h, None, 0,
+                                             0, 0, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D,
+                                             splits, split_rows, scale, cos_sin, cs_p, cs_d, positions, stream)
+
     def store_compact_kvcache(self, key, value, kvdt, ks_b, ks_h, vs_b, vs_h, ck, cv, cdt, c_s, slot, sm_b, sm_h,
                               B, H, D, stream):
         if B == 0:

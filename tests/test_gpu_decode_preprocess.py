@@ -137,3 +137,65 @@ def test_prefill_rope_matches_apply_rotary_emb():
     rope_inplace(kd, torch.from_numpy(pos).cuda(), dev_cache)
     torch.cuda.synchronize()
     assert np.array_equal(values_of(qd), qe) and np.array_equal(values_of(kd), ke)
+
+
+@pytest.mark.parametrize("d,split_rows", [(64, None), (128, None), (64, 256)])
+def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows):
+    """One-launch decode preprocess + attention (fdms_fused_decode_attention) on
+    Llama / Qwen3 head shapes with q/k/v as views of one qkv row: the decision
+    and the appended FP8 rows bit-exact vs the oracle's preprocess (store_q off),
+    q / k untouched, the output within 2e-2 of the oracle's attention over the
+    span incl. the appended token; split_rows=256 splits long spans so the
+    appended token lands in the last split."""
+    require_gpu()
+    import fastdms_amd.layers.compact_attention as ca
+    if split_rows is not None:
+        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (8, split_rows))
+    rng = np.random.default_rng(d + (split_rows or 0))
+    b, hq, hkv = 8, 32, 8
+    g = hq // hkv
+    cap = 1600
+    live_prev = rng.integers(0, 1500, (b, hkv)).astype(np.int32)
+    live_prev[0, 0] = 0
+    live_prev[1, 2] = 63
+    live_prev[2, 5] = 255
+    base = (np.arange(b * hkv).reshape(b, hkv) * cap).astype(np.int32)
+    slot = base + live_prev
+    live_prev[3, 1] = 700
+    slot[3, 1] = -1  # no append for this pair: its span is read as is
+    live = live_prev + (slot >= 0)
+    qkv = numerics.cast(rng.standard_normal((b, (hq + 2 * hkv) * d)).astype(np.float32), numerics.DT_BF16)
+    q = qkv[:, :hq * d].reshape(b, hq, d).copy()
+    k = qkv[:, hq * d:(hq + hkv) * d].reshape(b, hkv, d).copy()
+    v = qkv[:, (hq + hkv) * d:].reshape(b, hkv, d).copy()
+    positions = rng.integers(2000, 8192, b)
+    cache = oatt.rope_cos_sin_cache(d, 8192, 500000.0)
+    ck = numerics.to_storage(rng.standard_normal((b * hkv * cap, d)).astype(np.float32), numerics.DT_FP8)
+    cv = numerics.to_storage(rng.standard_normal((b * hkv * cap, d)).astype(np.float32), numerics.DT_FP8)
+    qo, ko, cko, cvo = q.copy(), k.copy(), ck.copy(), cv.copy()
+    ev = oatt.fused_dms_rope_store_compact_decode(q=qo, k=ko, v=v, cos_sin_cache=cache, compact_k=cko, compact_v=cvo,
+                                                  slot_mapping=slot, positions=positions, num_kv_heads=hkv,
+                                                  alpha_scale=10.0, alpha_offset=5.0, q_dtype_code=numerics.DT_BF16,
+                                                  k_dtype_code=numerics.DT_BF16, compact_dtype_code=numerics.DT_FP8,
+                                                  store_q=True, store_transient_k=False)
+    ref = oatt.compact_decode_attention(qo, numerics.from_storage(cko, numerics.DT_FP8),
+                                        numerics.from_storage(cvo, numerics.DT_FP8), base, live)
+    qkv_d = from_values(qkv, numerics.DT_BF16)
+    qd = qkv_d[:, :hq * d].view(b, hq, d)
+    kd = qkv_d[:, hq * d:(hq + hkv) * d].view(b, hkv, d)
+    vd = qkv_d[:, (hq + hkv) * d:].view(b, hkv, d)
+    ckd = torch.from_numpy(ck).cuda().view(torch.float8_e4m3fn)
+    cvd = torch.from_numpy(cv).cuda().view(torch.float8_e4m3fn)
+    evd = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
+    assert ca.fused_decode_attention_supported(qd, kd, vd, ckd)
+    out = ca.fused_dms_rope_store_compact_decode_attention(
+        qd, kd, vd, torch.from_numpy(cache).cuda(), ckd, cvd, torch.from_numpy(slot).cuda(), evd,
+        torch.from_numpy(positions).cuda(), torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda(),
+        num_kv_heads=hkv, alpha_scale=10.0, alpha_offset=5.0, max_live_count=cap)
+    torch.cuda.synchronize()
+    assert np.array_equal(evd.cpu().numpy(), ev)
+    assert np.array_equal(storage_of(ckd), cko) and np.array_equal(storage_of(cvd), cvo)
+    assert np.array_equal(values_of(qd), q) and np.array_equal(values_of(kd), k)
+    got = values_of(out)
+    assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= 2e-2
+    assert g == 4
