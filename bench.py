@@ -51,58 +51,164 @@ def parse_args():
 
 
 def attention_roofline(llm, seqs, replays: int):
-    """Average duration and algorithmic HBM bytes of the compact decode attention
-    kernel on the live decode state: one graph holds the kernel of every layer
-    with the exact decode-step arguments; HIP events bracket `replays` replays."""
+    """Average duration and algorithmic HBM bytes of the decode attention kernel
+    the step runs, on the live decode state: one graph holds the kernel of
+    every layer with the decode step's arguments; HIP events on the capture
+    stream bracket `replays` replays.  With the fused decode path this is
+    fdms_fused_decode_attention (DMS decision + RoPE + FP8 append + attention;
+    each replay re-appends the step's row at rank live-1), else the plain
+    compact attention.  Bytes per launch: FP8 K/V rows read from the spans,
+    q / k / v rows read (bf16), the appended FP8 rows and the output written,
+    and the int32 / int64 metadata."""
     import torch
     from fastdms_amd.layers.compact_attention import (attention_split_plan, compact_decode_attention,
+                                                      fused_decode_attention_supported,
+                                                      fused_dms_rope_store_compact_decode_attention,
                                                       mfma_attention_path)
 
     runner = llm.model_runner
     mgr = runner.compact_kv_manager
     cfg = llm.config.hf_config
+    md = runner.dms_metadata
     states = [mgr.seq_states[s.seq_id] for s in seqs]
     start = mgr._contiguous_active_slot_start(states)
     b = len(seqs)
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     base = mgr.layer_major_base_offsets[:, start:start + b]
     live = mgr.layer_major_live_counts[:, start:start + b]
+    slot = (base + live - 1).contiguous()  # the row the last decode step appended
     hint = runner.attention_hint(seqs)  # the bound (and so the split count) the decode step uses
-    q = torch.randn((b, cfg.num_attention_heads, cfg.head_dim), device="cuda").to(torch.bfloat16)
+    gen = torch.Generator(device="cpu").manual_seed(1)
+    qkv = (torch.randn((b, (hq + 2 * hkv) * d), generator=gen) * 4).to(device="cuda", dtype=torch.bfloat16)
+    q = qkv[:, :hq * d].view(b, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+    positions = torch.tensor([len(s) - 1 for s in seqs], device="cuda", dtype=torch.int64)
+    evict = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
     layers = list(range(cfg.num_hidden_layers))
     arenas = [(mgr.compact_k_per_layer[l], mgr.compact_v_per_layer[l]) for l in layers]
-    g = torch.cuda.CUDAGraph()
-    with torch.inference_mode():  # the engine's tensors are inference tensors
-        for l in layers:  # warm-up outside capture
+    cos_sin = runner.model.model.layers[0].self_attn.rotary_emb.cos_sin_cache
+    fused = fused_decode_attention_supported(q, k, v, arenas[0][0])
+    out = torch.empty_like(q)
+
+    def launch(l):
+        if fused:
+            fused_dms_rope_store_compact_decode_attention(
+                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions, base[l], live[l],
+                num_kv_heads=hkv, alpha_scale=md.alpha_scale, alpha_offset=md.alpha_offset, max_live_count=hint,
+                out=out)
+        else:
             compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.inference_mode(), torch.cuda.stream(s):  # the engine's tensors are inference tensors
+        for l in layers:  # warm-up outside capture
+            launch(l)
         torch.cuda.synchronize()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):
             for l in layers:
-                compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
-    g.replay()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(replays):
+                launch(l)
         g.replay()
-    t1.record()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(s)
+        for _ in range(replays):
+            g.replay()
+        t1.record(s)
+        torch.cuda.synchronize()
     per_launch_s = t0.elapsed_time(t1) / 1e3 / (replays * len(layers))
     lv = live.to(torch.int64).cpu()
-    kv_bytes = int(lv.sum()) * cfg.head_dim * 2 * arenas[0][0].element_size()   # K and V rows read
-    qo_bytes = 2 * b * cfg.num_attention_heads * cfg.head_dim * 2                # q read + out write (bf16)
-    meta_bytes = 2 * 4 * b * cfg.num_key_value_heads * len(layers)               # base + live (int32)
-    bytes_per_launch = (kv_bytes + qo_bytes * len(layers) + meta_bytes) / len(layers)
-    mfma = mfma_attention_path(q, arenas[0][0], cfg.num_attention_heads // cfg.num_key_value_heads)
-    splits, split_rows = attention_split_plan(q.device, b * cfg.num_key_value_heads, hint, mfma)
+    elem = arenas[0][0].element_size()
+    nl = len(layers)
+    if fused:
+        kv_bytes = int((lv - 1).clamp(min=0).sum()) * d * 2 * elem     # span rows read (all but the appended one)
+        io_bytes = nl * b * ((hq + 2 * hkv) * d * 2                     # raw q, k, v rows (bf16)
+                             + 2 * hkv * d * elem                        # appended K and V rows (FP8)
+                             + hq * d * 2                                # output (bf16)
+                             + hkv * (3 * 4 + 1) + 8 + d * 4)            # base/live/slot, evict, position, cos/sin
+    else:
+        kv_bytes = int(lv.sum()) * d * 2 * elem
+        io_bytes = nl * b * (2 * hq * d * 2 + 2 * 4 * hkv)
+    bytes_per_launch = (kv_bytes + io_bytes) / nl
+    mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
+    splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
     if split_rows:  # per-pair split counts, as the kernel derives them
         splits = int(((lv + split_rows - 1) // split_rows).clamp(1, splits).max())
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel",
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic(),
+            "kernel": ("decode_attn_mfma_kernel<fused>" if fused else
+                       "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel"),
             "avg_launch_us": round(per_launch_s * 1e6, 3),
-            "bytes_per_launch": int(bytes_per_launch), "splits": splits,
-            "live_tokens_mean_per_head": round(float(lv.float().mean()), 1)}
+            "bytes_per_launch": int(bytes_per_launch), "max_splits_per_pair": splits,
+            "live_tokens_per_head": {"mean": round(float(lv.float().mean()), 1), "max": int(lv.max()),
+                                     "p99": int(lv.float().quantile(0.99))}}
+
+
+def _pmc_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the factor the same counter
+    reads for the plain copy kernel), or None when it is absent."""
+    path = ROOT / "profiles" / "decode_attention_pmc_traffic.json"
+    try:
+        return json.loads(path.read_text())["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def compaction_roofline(replays: int = 50):
+    """Prefill compaction (A4 + A5): per-chunk keep counts / offsets and the
+    fused rank scatter of one 8192-token sequence (8 KV heads, D = 64, bf16
+    K/V -> FP8 span), keep = last 256 tokens + 1/8 of the older ones.  HIP
+    events bracket `replays` graph replays of the two launches.  Bytes: the
+    scatter reads T*H*(2*D*2 + 1) and writes live*(2*D + 4 + 1); the prepare
+    reads T*H evict bytes and writes the counts / offsets."""
+    import torch
+    from fastdms_amd.engine import compact_kv as ckv
+
+    t_len, h, d, window = 8192, 8, 64, 256
+    gen = torch.Generator(device="cpu").manual_seed(2)
+    k = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
+    v = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
+    evict = (torch.rand((t_len, h), generator=gen) >= 0.125).to("cuda")
+    cap = t_len
+    ck = torch.zeros((h * cap, d), device="cuda", dtype=torch.float8_e4m3fn)
+    cv = torch.zeros_like(ck)
+    pos = torch.full((h, cap), -1, device="cuda", dtype=torch.int32)
+    em = torch.zeros((h, cap), device="cuda", dtype=torch.bool)
+    base = (torch.arange(h, device="cuda", dtype=torch.int32) * cap)
+    live_out = {}
+
+    def run():
+        live, offsets = ckv._streaming_pack_fused_rank_prepare(seq_evict=evict, seq_len=t_len, window_size=window)
+        ckv._streaming_pack_rank_scatter_hip(k=k, v=v, seq_evict=evict, block_offsets=offsets, compact_k=ck,
+                                             compact_v=cv, token_positions=pos, evict_mask=em, base_offsets=base,
+                                             start=0, seq_len=t_len, window_size=window)
+        live_out["live"] = live
+
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.stream(s):
+        run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            run()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(replays):
+            g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    step_s = e0.elapsed_time(e1) / 1e3 / replays
+    live = int(live_out["live"].sum())
+    nbytes = t_len * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + t_len * h + h * 4 * (1 + -(-t_len // 256))
+    achieved = nbytes / step_s / 1e9
+    return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "us_per_pack": round(step_s * 1e6, 2), "bytes": nbytes, "tokens": t_len, "live_rows": live}
 
 
 def hbm_copy_gbps(nbytes: int = 1 << 30) -> float:
@@ -207,11 +313,12 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     value = args.batch * args.steps / dt
-    roof = attention_roofline(llm, seqs, args.attn_replays)
-    copy_bw = hbm_copy_gbps()
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline:  # before the roofline replays re-append rows
         cpu = cpu_baseline(llm, seqs, args.cpu_seconds)
+    roof = attention_roofline(llm, seqs, args.attn_replays)
+    pack = compaction_roofline()
+    copy_bw = hbm_copy_gbps()
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -223,6 +330,7 @@ def main():
                    "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager},
         "prefill_tok_s": round(sum(lens) / prefill_s, 1),
         "roofline": roof,
+        "compaction_roofline": pack,
         "hbm_copy_gbps": round(copy_bw, 1),
         "cpu_baseline": cpu,
     }

@@ -31,6 +31,8 @@
 // workgroups: each split publishes its fragment with agent-scope atomic stores
 // and the last split of a strip to arrive (device-scope ticket) sums them and
 // runs the epilogue, then resets its ticket.  HBM-bound on W.
+#include <cstdlib>
+
 #include "fdms_vec.h"
 
 using namespace fdms;
@@ -571,7 +573,11 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
   if (k % k_splits) return (int)hipErrorInvalidValue;
-  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
+    const int v = std::atoi(e);
+    if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
+  }
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;  // whole k-blocks per wave
   const int wsz = w_dtype == kFP8 ? 1 : 2;
   auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
@@ -656,7 +662,11 @@ FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int 
   if (n % 16 || k_splits < 1 || k_splits > 64 || k % k_splits) return (int)hipErrorInvalidValue;
   if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
-  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
+    const int v = std::atoi(e);
+    if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
+  }
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
   const int wsz = w_dtype == kFP8 ? 1 : 2;
   if (((uintptr_t)x % 16) || ((uintptr_t)w % 16) || (x_stride * 2) % 16 || (w_stride * wsz) % 16 ||
@@ -784,7 +794,11 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
   if (k_splits < 1 || k_splits > 64 || k % k_splits || (k_splits > 1 && (!workspace || !counters)))
     return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
-  const int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
+    const int v = std::atoi(e);
+    if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
+  }
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
   if (((uintptr_t)x % 16) || ((uintptr_t)w_packed % 8) || (x_stride * 2) % 16 || w_stride_bytes % 8 ||
       x_stride < k || w_stride_bytes * 2 < k || (epilogue != 2 && y_stride < n_out))
