@@ -1035,6 +1035,37 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     qraw[x] = (i < 4 * D && g < G) ? (uint32_t)q[b * qs_b + (int64_t)(h * G + g) * qs_h + d].bits : 0u;
   }
 
+  // fused preprocess: this thread's raw q pair, k pair or v element and the
+  // step's position, loaded before anything they do not depend on
+  constexpr int kHalf = D / 2;
+  float fx1 = 0.0f, fx2 = 0.0f, fc = 0.0f, fsn = 0.0f;  // raw pair / element, RoPE cos and sin
+  if constexpr (FUSED) {
+    static_assert(NT >= 5 * kHalf + D, "one preprocess item per thread");
+    // the RoPE table row goes out with the raw rows, ahead of the span loads,
+    // so waiting for it never waits for those
+    const int64_t fpos = pre.positions[b];
+    if (tid < 5 * kHalf) {
+      const int jx = tid % kHalf;
+      const float* cs = pre.cos_sin + fpos * pre.cs_p;
+      fc = cs[(int64_t)jx * pre.cs_d];
+      fsn = cs[(int64_t)(jx + kHalf) * pre.cs_d];
+    }
+    if (tid < 4 * kHalf) {
+      const int g = tid / kHalf, jx = tid - g * kHalf;
+      if (g < G) {
+        const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
+        fx1 = ld<bf16_t>(qh + jx);
+        fx2 = ld<bf16_t>(qh + jx + kHalf);
+      }
+    } else if (tid < 5 * kHalf) {
+      const bf16_t* kh = pre.k + b * pre.ks_b + h * pre.ks_h;
+      fx1 = ld<bf16_t>(kh + tid - 4 * kHalf);
+      fx2 = ld<bf16_t>(kh + tid - 4 * kHalf + kHalf);
+    } else if (tid < 5 * kHalf + D) {
+      fx1 = ld<bf16_t>(pre.v + b * pre.vs_b + h * pre.vs_h + (tid - 5 * kHalf));
+    }
+  }
+
   const int live = live_counts[b * lc_b + h * lc_h];
   const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
   const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
@@ -1069,49 +1100,40 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     // decode preprocess: q pairs (decision lane read, then zeroed), the key
     // pair j and the value element d of the step's row; the workgroup of split
     // 0 writes the decision and appends the FP8 row at the slot
-    constexpr int half = D / 2;
-    const int64_t pos = pre.positions[b];
-    const float* cs = pre.cos_sin + pos * pre.cs_p;
-    for (int i = tid; i < 5 * half + D; i += NT) {
-      if (i < 4 * half) {
-        const int g = i / half, jx = i - g * half;
-        uint32_t y1b = 0u, y2b = 0u;
-        if (g < G) {
-          const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
-          const float x1 = ld<bf16_t>(qh + jx);
-          float x2 = ld<bf16_t>(qh + jx + half);
-          if (g == 0 && jx == half - 1) {
-            if (split == 0)
-              pre.evict_out[b * pre.ev_b + h * pre.ev_h] =
-                  dms_decide(x2, pre.alpha_scale, pre.alpha_offset, pre.threshold, pre.positive_scale) ? 1 : 0;
-            x2 = 0.0f;
-          }
-          float y1, y2;
-          rope_f32(x1, x2, cs[(int64_t)jx * pre.cs_d], cs[(int64_t)(jx + half) * pre.cs_d], &y1, &y2);
-          y1b = f32_to_bf16(y1);
-          y2b = f32_to_bf16(y2);
+    if (tid < 4 * kHalf) {
+      const int g = tid / kHalf, jx = tid - g * kHalf;
+      uint32_t y1b = 0u, y2b = 0u;
+      if (g < G) {
+        float x2 = fx2;
+        if (g == 0 && jx == kHalf - 1) {
+          if (split == 0)
+            pre.evict_out[b * pre.ev_b + h * pre.ev_h] =
+                dms_decide(x2, pre.alpha_scale, pre.alpha_offset, pre.threshold, pre.positive_scale) ? 1 : 0;
+          x2 = 0.0f;
         }
-        s_q[g][jx] = (uint16_t)y1b;
-        s_q[g][jx + half] = (uint16_t)y2b;
-      } else if (i < 5 * half) {
-        const int jx = i - 4 * half;
-        const bf16_t* kh = pre.k + b * pre.ks_b + h * pre.ks_h;
         float y1, y2;
-        rope_f32(ld<bf16_t>(kh + jx), ld<bf16_t>(kh + jx + half), cs[(int64_t)jx * pre.cs_d],
-                 cs[(int64_t)(jx + half) * pre.cs_d], &y1, &y2);
-        const uint32_t k1 = f32_to_fp8(y1), k2 = f32_to_fp8(y2);
-        s_knew[jx] = fp8_to_f32(k1);
-        s_knew[jx + half] = fp8_to_f32(k2);
-        if (split == 0 && app_slot >= 0) {
-          ck[(int64_t)app_slot * c_s + jx] = (uint8_t)k1;
-          ck[(int64_t)app_slot * c_s + jx + half] = (uint8_t)k2;
-        }
-      } else {
-        const int d = i - 5 * half;
-        const uint32_t v8 = f32_to_fp8(ld<bf16_t>(pre.v + b * pre.vs_b + h * pre.vs_h + d));
-        s_vnew[d] = fp8_to_f32(v8);
-        if (split == 0 && app_slot >= 0) cv[(int64_t)app_slot * c_s + d] = (uint8_t)v8;
+        rope_f32(fx1, x2, fc, fsn, &y1, &y2);
+        y1b = f32_to_bf16(y1);
+        y2b = f32_to_bf16(y2);
       }
+      s_q[g][jx] = (uint16_t)y1b;
+      s_q[g][jx + kHalf] = (uint16_t)y2b;
+    } else if (tid < 5 * kHalf) {
+      const int jx = tid - 4 * kHalf;
+      float y1, y2;
+      rope_f32(fx1, fx2, fc, fsn, &y1, &y2);
+      const uint32_t k1 = f32_to_fp8(y1), k2 = f32_to_fp8(y2);
+      s_knew[jx] = fp8_to_f32(k1);
+      s_knew[jx + kHalf] = fp8_to_f32(k2);
+      if (split == 0 && app_slot >= 0) {
+        ck[(int64_t)app_slot * c_s + jx] = (uint8_t)k1;
+        ck[(int64_t)app_slot * c_s + jx + kHalf] = (uint8_t)k2;
+      }
+    } else if (tid < 5 * kHalf + D) {
+      const int d = tid - 5 * kHalf;
+      const uint32_t v8 = f32_to_fp8(fx1);
+      s_vnew[d] = fp8_to_f32(v8);
+      if (split == 0 && app_slot >= 0) cv[(int64_t)app_slot * c_s + d] = (uint8_t)v8;
     }
   } else if (rope_pos) {
     // rotate q here (decision lane zeroed), rounded to bf16 like a stored q
@@ -1143,6 +1165,29 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   __syncthreads();
 
   const float qscale = scale * kLog2e;
+  if constexpr (FUSED) {
+    // the appended token as one more partial (m = its score, l = 1, acc = v),
+    // by the last wave, which has the fewest groups
+    if (wave == NW - 1) {
+      float sg[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float part = 0.0f;
+#pragma unroll
+        for (int d = lane; d < D; d += kWave) part += bf16_to_f32(s_q[g][d]) * s_knew[d];
+        sg[g] = wave_sum(part);
+      }
+      if (lane < 4) {
+        const float sl = lane == 0 ? sg[0] : lane == 1 ? sg[1] : lane == 2 ? sg[2] : sg[3];
+        s_wm[NW][lane] = new_tok ? sl * qscale : -INFINITY;
+        s_wl[NW][lane] = 1.0f;
+      }
+#pragma unroll
+      for (int d = lane; d < D; d += kWave)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) s_wacc[NW][g][d] = s_vnew[d];
+    }
+  }
   float m_j = -INFINITY;  // running max of head jj (same in every lane of that head)
   float l_j = 0.0f;       // this lane's share of the denominator of head jj
   v4f32_t acc[NA][2];  // even / odd P.V steps (two independent chains)
@@ -1222,28 +1267,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   };
   for (; gi < ngroups; gi += NW) process(cur, gi);  // wave-uniform
 
-  if constexpr (FUSED) {
-    // the appended token as one more partial: m = its score, l = 1, acc = v
-    if (wave == NW - 1) {
-      float sg[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float part = 0.0f;
-#pragma unroll
-        for (int d = lane; d < D; d += kWave) part += bf16_to_f32(s_q[g][d]) * s_knew[d];
-        sg[g] = wave_sum(part);
-      }
-      if (lane < 4) {
-        const float sl = lane == 0 ? sg[0] : lane == 1 ? sg[1] : lane == 2 ? sg[2] : sg[3];
-        s_wm[NW][lane] = new_tok ? sl * qscale : -INFINITY;
-        s_wl[NW][lane] = 1.0f;
-      }
-#pragma unroll
-      for (int d = lane; d < D; d += kWave)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) s_wacc[NW][g][d] = s_vnew[d];
-    }
-  }
   // per wave: max, denominator, accumulators -> LDS; combine the waves
   const float lw = blocks_sum(l_j);
   if (lane < 4) {

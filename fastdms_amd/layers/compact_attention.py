@@ -122,6 +122,9 @@ def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: 
     the batch's live bound.  Other kernels: choose_num_splits, even splits."""
     if mfma:
         rows = 2048 if pairs >= 32 else 512
+        env = os.environ.get("FASTDMS_AMD_ATTN_SPLIT_ROWS", "").strip()
+        if env.isdigit() and int(env) >= 64:  # tuning override
+            rows = int(env)
         return int(min(_MFMA_CAP_SPLITS, max(1, -(-int(max_live) // rows)))), rows
     return choose_num_splits(device, pairs, max_live), 0
 
