@@ -1,13 +1,16 @@
 #!/usr/bin/env python3
 """Compact-DMS decode throughput on one MI355X.
 
-Workload: Llama-3.2-1B-shaped model with random bf16
-weights, DMS window 256 / threshold 0.5 (~1/8 of tokens outside the window
-survive), FP8 compact KV; 8 requests with prompt lengths uniform in
-[4096, 8192] and uniform-random token ids, 128 greedy tokens each.  The 8
-prompts are prefilled together (untimed), then one "step" is one decode step of
-the 8-sequence batch: expiry policy, DMS decision + RoPE + FP8 append, compact
-attention and the full model forward, greedy argmax and decision recording.
+Default workload (--config l1b-c8): Llama-3.2-1B-shaped
+model with random bf16 weights, DMS window 256 / threshold 0.5 (~1/8 of tokens
+outside the window survive), FP8 compact KV; 8 requests with prompt lengths
+uniform in [4096, 8192] and uniform-random token ids, 128 greedy tokens each.
+--config l1b-c1 and q8b-c8 (configs[3], Qwen3-8B shape) run the
+same harness.  After a warm-up generation of the same prompt lengths, the
+prompts are prefilled together (timed separately as prefill_tok_s), then one
+"step" is one decode step of the batch: expiry policy, DMS decision + RoPE +
+FP8 append, compact attention and the full model forward, greedy argmax and
+decision recording.
 
 Prints one JSON line:
   value            decode tok/s over the K timed steps (inputs resident in HBM)
@@ -31,6 +34,24 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E bandwidth
 
+# BASELINE.json configs[1..3]: model preset, sequences, prompt-length range
+CONFIGS = {
+    "l1b-c1": ("llama-3.2-1b", 1, 8192, 8192,
+               "BASELINE configs[1]: Llama-3.2-1B shape, c=1, one 8192-token prompt, 128 greedy tokens, "
+               "DMS window 256 thr 0.5"),
+    "l1b-c8": ("llama-3.2-1b", 8, 4096, 8192,
+               "BASELINE configs[2]: Llama-3.2-1B shape, c=8 ragged prompts U[4096,8192], 128 greedy tokens, "
+               "DMS window 256 thr 0.5"),
+    "q8b-c8": ("qwen3-8b", 8, 8192, 8192,
+               "BASELINE configs[3]: Qwen3-8B shape (QK-norm), c=8, 8192-token prompts, 128 greedy tokens, "
+               "DMS window 256 thr 0.5"),
+}
+
+
+def progress(msg: str) -> None:
+    """One progress line on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
 
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -38,11 +59,13 @@ def parse_args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--batch", type=int, default=8)
-    p.add_argument("--min-prompt", type=int, default=4096)
-    p.add_argument("--max-prompt", type=int, default=8192)
+    p.add_argument("--config", choices=sorted(CONFIGS), default="l1b-c8",
+                   help="BASELINE workload preset (model, batch, prompt lengths)")
+    p.add_argument("--batch", type=int, default=None)
+    p.add_argument("--min-prompt", type=int, default=None)
+    p.add_argument("--max-prompt", type=int, default=None)
     p.add_argument("--gen", type=int, default=128)
-    p.add_argument("--model", default="llama-3.2-1b")
+    p.add_argument("--model", default=None)
     p.add_argument("--attn-replays", type=int, default=50)
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -289,34 +312,55 @@ def main():
     import torch
     from fastdms_amd import LLM, SamplingParams
 
+    model, batch, lo, hi, workload = CONFIGS[args.config]
+    args.model = args.model or model
+    args.batch = args.batch or batch
+    args.min_prompt = args.min_prompt or lo
+    args.max_prompt = args.max_prompt or hi
     if args.warmup + args.steps > args.gen - 1:
         sys.exit(f"warmup + steps must be <= gen - 1 = {args.gen - 1}")
     rng = np.random.default_rng(args.seed)
     lens = rng.integers(args.min_prompt, args.max_prompt + 1, args.batch).tolist()
+    progress(f"{args.config}: building {args.model}, prompts {lens}")
     llm = LLM(args.model, max_model_len=args.max_prompt + args.gen, max_num_seqs=args.batch,
               max_num_batched_tokens=sum(lens), dms_window_size=256, dms_alpha_scale=10.0, dms_alpha_offset=5.0,
               kv_cache_dtype="float8_e4m3fn", seed=args.seed, enforce_eager=args.eager)
     vocab = llm.config.hf_config.vocab_size
+    # warm-up generation of the same prompt lengths (first-call library set-up,
+    # graph capture), then freed; the reference times post-warm-up as well
+    progress("warm-up generation")
+    wrng = np.random.default_rng(args.seed + 1)
+    warm_sp = SamplingParams(temperature=0.0, max_tokens=2, ignore_eos=True)
+    for n in lens:
+        llm.add_request(wrng.integers(0, vocab, n).tolist(), warm_sp)
+    while not llm.is_finished():
+        llm.step()
     sp = SamplingParams(temperature=0.0, max_tokens=args.gen, ignore_eos=True)
     seqs = [llm.add_request(rng.integers(0, vocab, n).tolist(), sp) for n in lens]
     torch.cuda.synchronize()
+    progress("prefill")
     t0 = time.perf_counter()
-    llm.step()  # prefill of all 8 prompts
+    llm.step()  # prefill of all prompts
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     for _ in range(args.warmup):
         llm.step()
     torch.cuda.synchronize()
+    progress(f"timing {args.steps} decode steps")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         llm.step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     value = args.batch * args.steps / dt
+    progress(f"decode {value:.1f} tok/s")
     cpu = None
     if not args.no_cpu_baseline:  # before the roofline replays re-append rows
+        progress("cpu baseline")
         cpu = cpu_baseline(llm, seqs, args.cpu_seconds)
+    progress("attention roofline")
     roof = attention_roofline(llm, seqs, args.attn_replays)
+    progress("compaction roofline")
     pack = compaction_roofline()
     copy_bw = hbm_copy_gbps()
     out = {
@@ -324,8 +368,7 @@ def main():
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16 activations/weights, fp8_e4m3 compact KV", "data": "synthetic",
-        "config": {"workload": "BASELINE configs[2]: Llama-3.2-1B shape, c=8 ragged prompts U[4096,8192], "
-                               "128 greedy tokens, DMS window 256 thr 0.5",
+        "config": {"workload": workload,
                    "model": args.model, "global_batch": args.batch, "seq_len": int(max(lens)),
                    "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager},
         "prefill_tok_s": round(sum(lens) / prefill_s, 1),

@@ -53,6 +53,25 @@ __device__ __forceinline__ uint32_t f32_to_fp8(float x) {
   return sign | (uint32_t)__builtin_rintf(f);  // 0..8, half-to-even
 }
 
+// f32_to_fp8 of four values packed into one dword (byte i = value i), on the
+// gfx950 converter v_cvt_pk_fp8_f32.  The converter rounds to nearest even
+// but turns out-of-range values into NaN, so inputs are clamped to +-448 first
+// (saturation, as above); a NaN input is then re-encoded as sign | 0x7F.  Equal
+// to f32_to_fp8 on every bf16 bit pattern and on random / tie / subnormal f32
+// inputs (checked on the device against the scalar routine).
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+  const float ca = __builtin_amdgcn_fmed3f(a, -448.0f, 448.0f);
+  const float cb = __builtin_amdgcn_fmed3f(b, -448.0f, 448.0f);
+  const float cc = __builtin_amdgcn_fmed3f(c, -448.0f, 448.0f);
+  const float cd = __builtin_amdgcn_fmed3f(d, -448.0f, 448.0f);
+  uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false);
+  r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(cc, cd, (int)r, true);
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
+    r = f32_to_fp8(a) | (f32_to_fp8(b) << 8) | (f32_to_fp8(c) << 16) | (f32_to_fp8(d) << 24);
+  }
+  return r;
+}
+
 // ---------------------------------------------------------------- bf16
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

@@ -3,6 +3,8 @@
 // that every source and destination address is VEC*sizeof aligned.
 #pragma once
 
+#include <type_traits>
+
 #include "fdms_common.h"
 
 namespace fdms {
@@ -12,13 +14,27 @@ struct alignas(sizeof(T) * N) Vec {
   T v[N];
 };
 
+// Element-wise dtype conversion of a vector; conversions into FP8 go four
+// values at a time through f32x4_to_fp8x4.
+template <typename TI, typename TO, int N>
+__device__ __forceinline__ Vec<TO, N> convert_vec(const Vec<TI, N>& in) {
+  Vec<TO, N> out;
+  if constexpr (std::is_same<TO, fp8_t>::value && !std::is_same<TI, fp8_t>::value && N % 4 == 0) {
+    uint32_t* o = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+      o[i] = f32x4_to_fp8x4(ld<TI>(&in.v[4 * i]), ld<TI>(&in.v[4 * i + 1]), ld<TI>(&in.v[4 * i + 2]),
+                            ld<TI>(&in.v[4 * i + 3]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) Copy<TI, TO>::run(&out.v[i], &in.v[i]);
+  }
+  return out;
+}
+
 template <typename TI, typename TO, int N>
 __device__ __forceinline__ void copy_vec(TO* __restrict__ dst, const TI* __restrict__ src) {
-  const Vec<TI, N> in = *reinterpret_cast<const Vec<TI, N>*>(src);
-  Vec<TO, N> out;
-#pragma unroll
-  for (int i = 0; i < N; ++i) Copy<TI, TO>::run(&out.v[i], &in.v[i]);
-  *reinterpret_cast<Vec<TO, N>*>(dst) = out;
+  *reinterpret_cast<Vec<TO, N>*>(dst) = convert_vec<TI, TO, N>(*reinterpret_cast<const Vec<TI, N>*>(src));
 }
 
 // Byte-level moves for same-dtype arenas (expiry): N bytes per call.

@@ -38,6 +38,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   constexpr int kMaxPer = 4;  // hidden <= 8192
   float vals[kMaxPer][V];
   float ss = 0.0f;
+  // the norm weight does not depend on the row sum: its loads go out with x's
+  Vec<bf16_t, V> wv[kMaxPer];
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = (threadIdx.x + j * kThreads) * V;
+    if (c < hidden) wv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + c);
+  }
 #pragma unroll
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
@@ -66,12 +73,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
     if (c < hidden) {
-      const Vec<bf16_t, V> wv = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + c);
       Vec<bf16_t, V> o;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float xn = bf16_to_f32(f32_to_bf16(vals[j][i] * inv));
-        o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv.v[i].bits));
+        o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv[j].v[i].bits));
       }
       *reinterpret_cast<Vec<bf16_t, V>*>(out + row * out_stride + c) = o;
     }

@@ -62,41 +62,64 @@ __device__ __forceinline__ SeqSpan seq_span(const int32_t* cu, int b, int single
 // One block per (seq, head): chunk keep counts -> exclusive chunk offsets and
 // live count (compact_kv.py:140-165 + the torch scan at 294-295).  Optionally
 // resets the (seq, head) metadata row to (-1, False) first (compact_kv.py:1031-1032).
+// The evict bytes of kPrepBatch chunks are loaded together (one memory round
+// trip per batch, not per chunk); each wave counts its 64 tokens of every
+// chunk with a ballot, and the running offset is accumulated uniformly.
+constexpr int kPrepBatch = 32;
+
 __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     const uint8_t* __restrict__ evict, int64_t es_t, int64_t es_h, const int32_t* __restrict__ cu,
     int single_len, int window, int num_kv_heads, int max_chunks, int32_t* __restrict__ live_out, int64_t lo_b,
     int64_t lo_h, int32_t* __restrict__ offsets, int64_t of_b, int64_t of_h, int64_t of_c,
     int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta, const int32_t* __restrict__ meta_rows,
     int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap) {
-  __shared__ int s_wave[kChunk / kWave];
+  __shared__ int s_cnt[kPrepBatch][kChunk / kWave];
   const int h = blockIdx.x % num_kv_heads;
   const int b = blockIdx.x / num_kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const SeqSpan sp = seq_span(cu, b, 0, single_len);
   const int thresh = max(0, sp.len - 1 - window);
   if (positions) {
     const int64_t row = meta_rows ? meta_rows[b] : b;
     int32_t* pr = positions + row * tp_b + h * tp_h;
     uint8_t* er = evict_meta + row * em_b + h * em_h;
-    for (int s = threadIdx.x; s < meta_cap; s += kChunk) {
+    for (int s = tid; s < meta_cap; s += kChunk) {
       pr[s] = -1;
       er[s] = 0;
     }
   }
-  const int nchunks = (sp.len + kChunk - 1) / kChunk;
+  const uint8_t* ev = evict + sp.ev0 * es_t + h * es_h;
   int running = 0;
-  for (int c = 0; c < max_chunks; ++c) {
-    int total = 0;
-    if (c < nchunks) {
-      const int t = c * kChunk + threadIdx.x;
-      bool keep = false;
-      if (t < sp.len) keep = (evict[(sp.ev0 + t) * es_t + h * es_h] == 0) || (t >= thresh);
-      block_rank(keep, s_wave, &total);
+  for (int c0 = 0; c0 < max_chunks; c0 += kPrepBatch) {
+    // branch-free loads from clamped rows (a select on a predicated load would
+    // wait for it on the spot); rows past the end are masked in the ballot
+    uint8_t e[kPrepBatch];
+    if (sp.len > 0) {
+#pragma unroll
+      for (int j = 0; j < kPrepBatch; ++j) {
+        const int t = min((c0 + j) * kChunk + tid, sp.len - 1);
+        e[j] = ev[(int64_t)t * es_t];
+      }
     }
-    if (threadIdx.x == 0) offsets[b * of_b + h * of_h + c * of_c] = running;
-    running += total;
+#pragma unroll
+    for (int j = 0; j < kPrepBatch; ++j) {
+      const int t = (c0 + j) * kChunk + tid;
+      const bool keep = t < sp.len && (e[j] == 0 || t >= thresh);
+      const uint64_t m = __ballot(keep);
+      if (lane == 0) s_cnt[j][wave] = __popcll(m);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPrepBatch; ++j) {
+      int tot = 0;
+#pragma unroll
+      for (int w = 0; w < kChunk / kWave; ++w) tot += s_cnt[j][w];
+      if (tid == j && c0 + j < max_chunks) offsets[b * of_b + h * of_h + (c0 + j) * of_c] = running;
+      running += tot;
+    }
     __syncthreads();
   }
-  if (threadIdx.x == 0) live_out[b * lo_b + h * lo_h] = running;
+  if (tid == 0) live_out[b * lo_b + h * lo_h] = running;
 }
 
 template <typename TI, typename TO, int VEC, bool FUSED>
@@ -117,6 +140,10 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
   const int b = blockIdx.y / num_kv_heads;
   const SeqSpan sp = seq_span(cu, b, single_start, single_len);
   if (c * kChunk >= sp.len) return;  // uniform per block
+  // per-block scalars first: their loads overlap the evict load
+  const int64_t row = meta_rows ? meta_rows[b] : b;
+  const int64_t span0 = base[b * bs_b + h * bs_h];
+  const int chunk0 = FUSED ? block_offsets[b * bo_b + h * bo_h + c * bo_c] : 0;
   const int t = c * kChunk + threadIdx.x;
   const bool valid = t < sp.len;
   uint8_t e = 0;
@@ -129,29 +156,43 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
   }
   int total = 0;
   const int local = block_rank(keep, s_wave, &total);
+  int64_t rank = 0;
   if (keep) {
-    int64_t rank;
-    if (FUSED) {
-      rank = (int64_t)block_offsets[b * bo_b + h * bo_h + c * bo_c] + local;
-    } else {
-      rank = rank_in[(int64_t)t * rk_t + h * rk_h];
-    }
-    const int64_t row = meta_rows ? meta_rows[b] : b;
-    positions[row * tp_b + h * tp_h + rank * tp_s] = t;
-    evict_meta[row * em_b + h * em_h + rank * em_s] = e;
+    rank = FUSED ? (int64_t)chunk0 + local : (int64_t)rank_in[(int64_t)t * rk_t + h * rk_h];
     s_src[local] = sp.tok0 + t;
-    s_dst[local] = (int64_t)base[b * bs_b + h * bs_h] + rank;
+    s_dst[local] = span0 + rank;
   }
   __syncthreads();
+  // metadata stores after the barrier, so the barrier does not wait for them
+  if (keep) {
+    positions[row * tp_b + h * tp_h + rank * tp_s] = t;
+    evict_meta[row * em_b + h * em_h + rank * em_s] = e;
+  }
+  // kU vectors of K and of V per thread are loaded before any is stored, so a
+  // chunk of kept rows moves in one memory round trip per batch
+  constexpr int kU = 8;
   const int units = head_dim / VEC;
   const int n = total * units;
-  for (int u = threadIdx.x; u < n; u += kChunk) {
-    const int r = u / units;
-    const int j = (u - r * units) * VEC;
-    const int64_t src = s_src[r];
-    const int64_t dst = s_dst[r] * cs_s + j;
-    copy_vec<TI, TO, VEC>(ck + dst, k + src * ks_t + h * ks_h + j);
-    copy_vec<TI, TO, VEC>(cv + dst, v + src * vs_t + h * vs_h + j);
+  for (int u0 = threadIdx.x; u0 < n; u0 += kChunk * kU) {
+    Vec<TI, VEC> kr[kU], vr[kU];
+    int64_t dst[kU];
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      const int u = min(u0 + i * kChunk, n - 1);  // clamped: loads stay unpredicated
+      const int r = u / units;
+      const int j = (u - r * units) * VEC;
+      const int64_t src = s_src[r];
+      dst[i] = s_dst[r] * cs_s + j;
+      kr[i] = *reinterpret_cast<const Vec<TI, VEC>*>(k + src * ks_t + h * ks_h + j);
+      vr[i] = *reinterpret_cast<const Vec<TI, VEC>*>(v + src * vs_t + h * vs_h + j);
+    }
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      if (u0 + i * kChunk < n) {
+        *reinterpret_cast<Vec<TO, VEC>*>(ck + dst[i]) = convert_vec<TI, TO, VEC>(kr[i]);
+        *reinterpret_cast<Vec<TO, VEC>*>(cv + dst[i]) = convert_vec<TI, TO, VEC>(vr[i]);
+      }
+    }
   }
 }
 
