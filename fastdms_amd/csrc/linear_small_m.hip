@@ -322,6 +322,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
           const uint32_t q[4] = {b.nw[u][h].x, b.nw[u][h].y, b.nw[u][h].z, b.nw[u][h].w};
           const uint32_t rs[4] = {b.r[u][h].x, b.r[u][h].y, b.r[u][h].z, b.r[u][h].w};
           uint32_t o[4];
+          float f[8];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float lo = bf_lo(v[i]), hi = bf_hi(v[i]);
@@ -329,11 +330,18 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
               lo = rbf(rbf((lo + bf_lo(rs[i])) * inv) * bf_lo(q[i]));
               hi = rbf(rbf((hi + bf_hi(rs[i])) * inv) * bf_hi(q[i]));
             }
-            if (QX) {  // fp8 quantised activation, exact in bf16
-              lo = fp8_to_f32(f32_to_fp8(lo * xsc));
-              hi = fp8_to_f32(f32_to_fp8(hi * xsc));
-            }
+            f[2 * i] = lo;
+            f[2 * i + 1] = hi;
             o[i] = pack2(lo, hi);
+          }
+          if (QX) {  // fp8 quantised activation (exact in bf16), four values per conversion
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              const uint32_t q8 = f32x4_to_fp8x4(f[4 * i] * xsc, f[4 * i + 1] * xsc, f[4 * i + 2] * xsc,
+                                                 f[4 * i + 3] * xsc);
+              o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, false));
+              o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, true));
+            }
           }
           bo[h] = uint4{o[0], o[1], o[2], o[3]};
         }
@@ -733,9 +741,12 @@ __global__ __launch_bounds__(256) void fp8_rerank_topk_kernel(const bf16_t* __re
         load_sum8(xr + k, nullptr, f);
         load_sum8(xr + k + 8, nullptr, f + 8);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float xq = fp8_to_f32(f32_to_fp8(f[i] * xs));
-          acc += xq * fp8_to_f32((ww[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const uint32_t q8 = f32x4_to_fp8x4(f[4 * i4] * xs, f[4 * i4 + 1] * xs, f[4 * i4 + 2] * xs,
+                                             f[4 * i4 + 3] * xs);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc += fp8_to_f32((q8 >> (8 * i)) & 0xFFu) * fp8_to_f32((ww[i4] >> (8 * i)) & 0xFFu);
         }
       }
       score = wave_sum(acc) * xsi * w_scale_inv[id];
@@ -936,7 +947,13 @@ __global__ __launch_bounds__(256) void quantize_fp8_rows_kernel(const TI* __rest
   // torch's tensor expression 448 / amax is reciprocal(amax) * 448 (two roundings)
   const float sc = amax > 0.0f ? (torch_form ? (1.0f / amax) * kFp8Max : kFp8Max / amax) : 1.0f;
   uint8_t* o = out + row * out_s;
-  for (int j = threadIdx.x; j < k; j += 256) o[j] = (uint8_t)f32_to_fp8(ld<TI>(r + j) * sc);
+  if (k % 4 == 0 && (reinterpret_cast<uintptr_t>(o) & 3) == 0) {  // four codes per converter call
+    for (int j = 4 * threadIdx.x; j < k; j += 4 * 256)
+      *reinterpret_cast<uint32_t*>(o + j) = f32x4_to_fp8x4(ld<TI>(r + j) * sc, ld<TI>(r + j + 1) * sc,
+                                                           ld<TI>(r + j + 2) * sc, ld<TI>(r + j + 3) * sc);
+  } else {
+    for (int j = threadIdx.x; j < k; j += 256) o[j] = (uint8_t)f32_to_fp8(ld<TI>(r + j) * sc);
+  }
   if (threadIdx.x == 0) scale_inv[row] = 1.0f / sc;
 }
 
