@@ -180,35 +180,42 @@ def _pmc_traffic():
         return None
 
 
-def compaction_roofline(replays: int = 50):
+def compaction_roofline(replays: int = 20, seqs: int = 16):
     """Prefill compaction (A4 + A5): per-chunk keep counts / offsets and the
-    fused rank scatter of one 8192-token sequence (8 KV heads, D = 64, bf16
-    K/V -> FP8 span), keep = last 256 tokens + 1/8 of the older ones.  HIP
-    events bracket `replays` graph replays of the two launches.  Bytes: the
-    scatter reads T*H*(2*D*2 + 1) and writes live*(2*D + 4 + 1); the prepare
-    reads T*H evict bytes and writes the counts / offsets."""
+    fused rank scatter of an 8192-token sequence (8 KV heads, D = 64, bf16
+    K/V -> FP8 span), keep = last 256 tokens + 1/8 of the older ones.  One HIP
+    graph packs `seqs` sequences with their own K/V and spans (268 MB of K/V in
+    all, more than the 256 MB MALL, so every pack reads from HBM as a prefill
+    does); HIP events bracket `replays` replays.  Bytes per pack (SURVEY
+    formula): T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written + the prepare's
+    evict bytes and counts; the scatter itself reads only the kept rows."""
     import torch
     from fastdms_amd.engine import compact_kv as ckv
 
     t_len, h, d, window = 8192, 8, 64, 256
     gen = torch.Generator(device="cpu").manual_seed(2)
-    k = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
-    v = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
-    evict = (torch.rand((t_len, h), generator=gen) >= 0.125).to("cuda")
-    cap = t_len
-    ck = torch.zeros((h * cap, d), device="cuda", dtype=torch.float8_e4m3fn)
-    cv = torch.zeros_like(ck)
-    pos = torch.full((h, cap), -1, device="cuda", dtype=torch.int32)
-    em = torch.zeros((h, cap), device="cuda", dtype=torch.bool)
-    base = (torch.arange(h, device="cuda", dtype=torch.int32) * cap)
-    live_out = {}
+    sets = []
+    for _ in range(seqs):
+        k = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
+        v = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
+        evict = (torch.rand((t_len, h), generator=gen) >= 0.125).to("cuda")
+        ck = torch.zeros((h * t_len, d), device="cuda", dtype=torch.float8_e4m3fn)
+        cv = torch.zeros_like(ck)
+        pos = torch.full((h, t_len), -1, device="cuda", dtype=torch.int32)
+        em = torch.zeros((h, t_len), device="cuda", dtype=torch.bool)
+        sets.append((k, v, evict, ck, cv, pos, em))
+    base = (torch.arange(h, device="cuda", dtype=torch.int32) * t_len)
+    lives = []
 
     def run():
-        live, offsets = ckv._streaming_pack_fused_rank_prepare(seq_evict=evict, seq_len=t_len, window_size=window)
-        ckv._streaming_pack_rank_scatter_hip(k=k, v=v, seq_evict=evict, block_offsets=offsets, compact_k=ck,
-                                             compact_v=cv, token_positions=pos, evict_mask=em, base_offsets=base,
-                                             start=0, seq_len=t_len, window_size=window)
-        live_out["live"] = live
+        lives.clear()
+        for k, v, evict, ck, cv, pos, em in sets:
+            live, offsets = ckv._streaming_pack_fused_rank_prepare(seq_evict=evict, seq_len=t_len,
+                                                                   window_size=window)
+            ckv._streaming_pack_rank_scatter_hip(k=k, v=v, seq_evict=evict, block_offsets=offsets, compact_k=ck,
+                                                 compact_v=cv, token_positions=pos, evict_mask=em,
+                                                 base_offsets=base, start=0, seq_len=t_len, window_size=window)
+            lives.append(live)
 
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
@@ -225,13 +232,15 @@ def compaction_roofline(replays: int = 50):
             g.replay()
         e1.record(s)
         torch.cuda.synchronize()
-    step_s = e0.elapsed_time(e1) / 1e3 / replays
-    live = int(live_out["live"].sum())
+    pack_s = e0.elapsed_time(e1) / 1e3 / (replays * seqs)
+    live = sum(int(x.sum()) for x in lives) / seqs
     nbytes = t_len * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + t_len * h + h * 4 * (1 + -(-t_len // 256))
-    achieved = nbytes / step_s / 1e9
+    achieved = nbytes / pack_s / 1e9
+    del sets
     return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "us_per_pack": round(step_s * 1e6, 2), "bytes": nbytes, "tokens": t_len, "live_rows": live}
+            "us_per_pack": round(pack_s * 1e6, 2), "bytes": int(nbytes), "tokens": t_len,
+            "live_rows": round(live, 1), "packs_per_graph": seqs}
 
 
 def hbm_copy_gbps(nbytes: int = 1 << 30) -> float:

@@ -24,20 +24,35 @@ FDMS_EXPORT int fdms_copy_bytes(const void* src, void* dst, int64_t nbytes, int 
   return 0;
 }
 
+// Thread i converts elements [4i, 4i + 4) with the vector conversion the row
+// kernels use (convert_vec: the FP8 encoder four values at a time), and the
+// last n % 4 elements one by one, so a test over this entry point checks the
+// kernels' own rounding.
 template <typename TI, typename TO>
 __global__ void convert_kernel(const TI* __restrict__ src, TO* __restrict__ dst, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) Copy<TI, TO>::run(dst + i, src + i);
+  const int64_t n4 = n / 4;
+  if (i < n4) {
+    *reinterpret_cast<Vec<TO, 4>*>(dst + 4 * i) =
+        convert_vec<TI, TO, 4>(*reinterpret_cast<const Vec<TI, 4>*>(src + 4 * i));
+  } else if (i < n4 + (n & 3)) {
+    const int64_t j = 4 * n4 + (i - n4);
+    Copy<TI, TO>::run(dst + j, src + j);
+  }
 }
 
-// Element-wise dtype conversion with the library's rounding (RNE, fp8 saturating).
+// Element-wise dtype conversion with the library's rounding (RNE, fp8
+// saturating).  src / dst aligned to four elements.
 FDMS_EXPORT int fdms_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream) {
   if (!src || !dst || n < 0) return (int)hipErrorInvalidValue;
   if (n == 0) return 0;
-  const int64_t grid = (n + 255) / 256;
+  const int64_t threads = n / 4 + (n & 3);
+  const int64_t grid = (threads + 255) / 256;
   if (grid > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   FDMS_DISPATCH_DTYPE(src_dtype, TI,
     FDMS_DISPATCH_DTYPE(dst_dtype, TO,
+      if (reinterpret_cast<uintptr_t>(src) % (4 * sizeof(TI)) || reinterpret_cast<uintptr_t>(dst) % (4 * sizeof(TO)))
+        return (int)hipErrorInvalidValue;
       hipLaunchKernelGGL((convert_kernel<TI, TO>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
                          (const TI*)src, (TO*)dst, n)));
   FDMS_LAUNCH_CHECK();

@@ -35,7 +35,9 @@ int fdms_copy_bytes(const void* src, void* dst, int64_t nbytes, int num_blocks, 
 
 /* Element-wise dtype conversion with the library's store rounding (no
  * reference counterpart: exposes the cast the reference's Triton stores apply,
- * compact_kv.py:243-252, for exhaustive tests). */
+ * compact_kv.py:243-252, for exhaustive tests).  Runs the row kernels' vector
+ * conversion (FP8 encoded four values at a time); src and dst must be aligned
+ * to four elements. */
 int fdms_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 
 /* Decode n (multiple of 4) FP8 e4m3fn bytes to fp32 with the hardware
