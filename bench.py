@@ -169,53 +169,69 @@ def attention_roofline(llm, seqs, replays: int):
                                      "p99": int(lv.float().quantile(0.99))}}
 
 
-def _pmc_traffic():
-    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary
+def _pmc_traffic(name: str = "decode_attention_pmc_traffic.json"):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE, each scaled by the factor the same counter
     reads for the plain copy kernel), or None when it is absent."""
-    path = ROOT / "profiles" / "decode_attention_pmc_traffic.json"
+    path = ROOT / "profiles" / name
     try:
         return json.loads(path.read_text())["traffic_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
 
 
-def compaction_roofline(replays: int = 20, seqs: int = 16):
-    """Prefill compaction (A4 + A5): per-chunk keep counts / offsets and the
-    fused rank scatter of an 8192-token sequence (8 KV heads, D = 64, bf16
-    K/V -> FP8 span), keep = last 256 tokens + 1/8 of the older ones.  One HIP
-    graph packs `seqs` sequences with their own K/V and spans (268 MB of K/V in
-    all, more than the 256 MB MALL, so every pack reads from HBM as a prefill
-    does); HIP events bracket `replays` replays.  Bytes per pack (SURVEY
-    formula): T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written + the prepare's
-    evict bytes and counts; the scatter itself reads only the kept rows."""
+def compaction_roofline(lens, replays: int = 20, layers: int = 16):
+    """Prefill compaction (A4 + A5) as the engine runs it for one layer of a
+    prefill batch (streaming_pack_layer): one pack-prepare launch over every
+    sequence (keep counts, chunk offsets, metadata rows reset to (-1, False))
+    and one rank-scatter launch (bf16 K/V -> FP8 spans + positions / evict
+    metadata), for the bench's prompt lengths, 8 KV heads, D = 64, keep = last
+    256 tokens + 1/8 of the older ones.  One HIP graph packs `layers` layers
+    with their own K/V, spans and metadata (more than the 256 MB MALL); HIP
+    events bracket `replays` replays.  Algorithmic bytes per layer: the evict
+    bytes (T*H), the kept K/V rows (live*2*D*2), their FP8 rows and metadata
+    (live*(2*D + 5)), the metadata reset (S*H*cap*5) and the counts / offsets.
+    The SURVEY formula, which also counts the evicted rows' K/V as read, is
+    reported beside it (bytes_survey)."""
+    import numpy as np
     import torch
-    from fastdms_amd.engine import compact_kv as ckv
+    from fastdms_amd import _native as nat
 
-    t_len, h, d, window = 8192, 8, 64, 256
-    gen = torch.Generator(device="cpu").manual_seed(2)
-    sets = []
-    for _ in range(seqs):
-        k = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
-        v = torch.randn((t_len, h, d), generator=gen).to(device="cuda", dtype=torch.bfloat16)
-        evict = (torch.rand((t_len, h), generator=gen) >= 0.125).to("cuda")
-        ck = torch.zeros((h * t_len, d), device="cuda", dtype=torch.float8_e4m3fn)
+    h, d, window = 8, 64, 256
+    nseq = len(lens)
+    t_tot = int(sum(lens))
+    cap = int(max(lens))
+    chunks = -(-cap // 256)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    keep_old = 0.125
+    per_layer = []
+    for _ in range(layers):
+        k = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
+        v = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
+        evict = (torch.rand((t_tot, h), generator=gen, device="cuda") >= keep_old).view(torch.uint8)
+        ck = torch.zeros((nseq * h * cap, d), device="cuda", dtype=torch.float8_e4m3fn)
         cv = torch.zeros_like(ck)
-        pos = torch.full((h, t_len), -1, device="cuda", dtype=torch.int32)
-        em = torch.zeros((h, t_len), device="cuda", dtype=torch.bool)
-        sets.append((k, v, evict, ck, cv, pos, em))
-    base = (torch.arange(h, device="cuda", dtype=torch.int32) * t_len)
-    lives = []
+        pos = torch.zeros((nseq, h, cap), device="cuda", dtype=torch.int32)
+        em = torch.zeros((nseq, h, cap), device="cuda", dtype=torch.uint8)
+        live = torch.empty((nseq, h), device="cuda", dtype=torch.int32)
+        offs = torch.empty((nseq, h, chunks), device="cuda", dtype=torch.int32)
+        per_layer.append((k, v, evict, ck, cv, pos, em, live, offs))
+    base = (torch.arange(nseq * h, device="cuda", dtype=torch.int32) * cap).view(nseq, h)
+    rows = torch.arange(nseq, device="cuda", dtype=torch.int32)
 
     def run():
-        lives.clear()
-        for k, v, evict, ck, cv, pos, em in sets:
-            live, offsets = ckv._streaming_pack_fused_rank_prepare(seq_evict=evict, seq_len=t_len,
-                                                                   window_size=window)
-            ckv._streaming_pack_rank_scatter_hip(k=k, v=v, seq_evict=evict, block_offsets=offsets, compact_k=ck,
-                                                 compact_v=cv, token_positions=pos, evict_mask=em,
-                                                 base_offsets=base, start=0, seq_len=t_len, window_size=window)
-            lives.append(live)
+        for k, v, ev, ck, cv, pos, em, live, offs in per_layer:
+            nat.call("fdms_streaming_pack_prepare", ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), 0, nseq,
+                     window, h, chunks, live.data_ptr(), live.stride(0), live.stride(1), offs.data_ptr(),
+                     offs.stride(0), offs.stride(1), offs.stride(2), pos.data_ptr(), em.data_ptr(), rows.data_ptr(),
+                     pos.stride(0), pos.stride(1), em.stride(0), em.stride(1), cap, nat.stream())
+            nat.call("fdms_streaming_pack_rank_scatter", k.data_ptr(), v.data_ptr(), nat.DT_BF16, k.stride(0),
+                     k.stride(1), v.stride(0), v.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(),
+                     0, 0, nseq, offs.data_ptr(), offs.stride(0), offs.stride(1), offs.stride(2), base.data_ptr(),
+                     base.stride(0), base.stride(1), ck.data_ptr(), cv.data_ptr(), nat.DT_FP8, ck.stride(0),
+                     pos.data_ptr(), em.data_ptr(), rows.data_ptr(), pos.stride(0), pos.stride(1), pos.stride(2),
+                     em.stride(0), em.stride(1), em.stride(2), window, h, d, chunks, 8, nat.stream())
 
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
@@ -232,15 +248,19 @@ def compaction_roofline(replays: int = 20, seqs: int = 16):
             g.replay()
         e1.record(s)
         torch.cuda.synchronize()
-    pack_s = e0.elapsed_time(e1) / 1e3 / (replays * seqs)
-    live = sum(int(x.sum()) for x in lives) / seqs
-    nbytes = t_len * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + t_len * h + h * 4 * (1 + -(-t_len // 256))
-    achieved = nbytes / pack_s / 1e9
-    del sets
-    return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel", "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "us_per_pack": round(pack_s * 1e6, 2), "bytes": int(nbytes), "tokens": t_len,
-            "live_rows": round(live, 1), "packs_per_graph": seqs}
+    layer_s = e0.elapsed_time(e1) / 1e3 / (replays * layers)
+    live = sum(int(x[7].sum()) for x in per_layer) / layers
+    meta = nseq * h * (1 + chunks) * 4
+    nbytes = t_tot * h + live * 2 * d * 2 + live * (2 * d + 5) + nseq * h * cap * 5 + meta
+    survey = t_tot * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + meta
+    achieved = nbytes / layer_s / 1e9
+    del per_layer
+    return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel (one prefill layer, all sequences)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("compaction_pmc_traffic.json"),
+            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(nbytes), "tokens": t_tot,
+            "live_rows": round(live, 1), "bytes_survey": int(survey),
+            "achieved_survey": round(survey / layer_s / 1e9, 1)}
 
 
 def hbm_copy_gbps(nbytes: int = 1 << 30) -> float:
@@ -370,7 +390,7 @@ def main():
     progress("attention roofline")
     roof = attention_roofline(llm, seqs, args.attn_replays)
     progress("compaction roofline")
-    pack = compaction_roofline()
+    pack = compaction_roofline(lens)
     copy_bw = hbm_copy_gbps()
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
       if (tid == j && c0 + j < max_chunks) offsets[b * of_b + h * of_h + (c0 + j) * of_c] = running;
       running += tot;
     }
-    __syncthreads();
+    if (c0 + kPrepBatch < max_chunks) __syncthreads();  // s_cnt is reused by the next batch
   }
   if (tid == 0) live_out[b * lo_b + h * lo_h] = running;
 }
