@@ -3,7 +3,8 @@
 Every ``*.hip`` file is compiled for gfx950 with hipcc into an object under
 ``fastdms_amd/_build`` (in parallel), then linked into
 ``fastdms_amd/_lib/libfastdms_amd.so``.  Packed-FP32 instruction selection is
-disabled for all device code (``-packed-fp32-ops``).
+disabled for all device code (``-packed-fp32-ops``); FILE_FLAGS adds
+per-file code-generation options.
 """
 from __future__ import annotations
 
@@ -30,11 +31,17 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
+# Per-file flags.  The prefill attention kernel feeds its MFMA results straight
+# into VALU softmax / masking: with the results in AGPRs (the compiler's
+# default there) every block copies them out and back.
+FILE_FLAGS = {
+    "prefill_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-I", str(HERE), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(HERE), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

@@ -14,6 +14,8 @@
 // S^T's C layout gives lane l the scores of query l%16 for keys
 // 16t + 4*(l/16) + r, which is directly the A operand of P.V once the key
 // order inside each 32-key MFMA step is permuted the same way for V.
+#include <cstdlib>
+
 #include "fdms_common.h"
 
 using namespace fdms;
@@ -38,11 +40,28 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return f32_to_bf16(a) | (f32_to_bf16(b) << 16);
 }
 
+// Two fp32 -> bf16 (round to nearest even) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 }  // namespace
+
+// FASTDMS_AMD_PREFILL_GQA=0 selects the per-head kernel for every shape
+// (comparison / testing).
+static bool fdms_prefill_gqa_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("FASTDMS_AMD_PREFILL_GQA");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
@@ -189,6 +208,242 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
   }
 }
 
+// GQA-packed variant for group sizes 1, 2 and 4: a workgroup takes P = 128/G
+// query positions of one KV head for all G query heads that share it, so one
+// staged K/V block feeds 128 query rows (wave w: head w % G, positions
+// 32*(w / G) .. +31, two 16-row MFMA tiles).  K/V blocks of 64 keys are
+// double-buffered in LDS: the next block's global loads are in flight while
+// the current one is computed, and one barrier separates blocks.  V is
+// transposed in registers (4 keys x 8 dims per thread, byte permutes) so the
+// LDS stores are 8-byte vectors.  Every K fragment read from LDS feeds both
+// query tiles of a wave, as does every V fragment.  Softmax rescaling is lazy:
+// the running max only moves (and O / l are rescaled) when a block raises it
+// by more than 8 in the log2 domain, so p = exp2(s - m) stays below 256.
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
+    int64_t ks_h, const bf16_t* __restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t* __restrict__ out, int64_t os_t,
+    int64_t os_h, const int32_t* __restrict__ cu_seqlens, float scale_log2) {
+  constexpr int P = 128 / G;        // query positions per workgroup
+  constexpr int KPAD = D + 8;       // sK row stride (bf16)
+  constexpr int VPAD = kKeys + 8;   // sVt row stride (bf16)
+  constexpr int UNITS = 4 * D;      // staging units per block: 2D V quads (4 keys x 8 dims) + 2D K quads (4 chunks)
+  constexpr int UPT = UNITS / kThreads;
+  static_assert(UNITS % kThreads == 0, "staging units must divide over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeys * KPAD];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][D * VPAD];
+
+  const int seq = blockIdx.z;
+  const int kvh = blockIdx.y;
+  const int start = cu_seqlens[seq];
+  const int len = cu_seqlens[seq + 1] - start;
+  const int nqb = (len + P - 1) / P;
+  if ((int)blockIdx.x >= nqb) return;
+  const int q0 = (nqb - 1 - (int)blockIdx.x) * P;  // heaviest (diagonal-last) blocks first
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lg = lane >> 4;
+  const int lc = lane & 15;
+  const int qh = kvh * G + wave % G;
+  const int wq0 = q0 + (wave / G) * 32;            // first position of this wave
+  const int wq_last = min(wq0 + 31, len - 1);      // last valid position of this wave
+  const int my_q0 = wq0 + lc, my_q1 = wq0 + 16 + lc;
+
+  bf16x8 qop[2][D / 32];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qrow = min(wq0 + 16 * qt + lc, len - 1);
+    const bf16_t* qp = q + (int64_t)(start + qrow) * qs_t + (int64_t)qh * qs_h;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) qop[qt][j] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 * j + 8 * lg));
+  }
+
+  const bf16_t* kb_base = k + (int64_t)start * ks_t + (int64_t)kvh * ks_h;
+  const bf16_t* vb_base = v + (int64_t)start * vs_t + (int64_t)kvh * vs_h;
+  uint4 stage[UPT][4];
+  // unit u < 2D: V quad (keys 4*(u / (D/8)) .. +3, dims 8*(u % (D/8)) .. +7);
+  // u >= 2D: K chunks 4*(u - 2D) .. +3 (chunk c = key * (D/8) + dim / 8).
+  // Row r of unit i is key k0 + krow[i][r] at element offset koff[i][r] +
+  // key * stride; rows past the sequence end are clamped (their scores are
+  // masked).
+  int krow[UPT][4], koff[UPT][4];
+  const bf16_t* kvp[UPT];
+  int64_t kvs[UPT];
+#pragma unroll
+  for (int i = 0; i < UPT; ++i) {
+    const int u = tid + i * kThreads;
+    const bool is_v = u < 2 * D;
+    kvp[i] = is_v ? vb_base : kb_base;
+    kvs[i] = is_v ? vs_t : ks_t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = 4 * (u - 2 * D) + r;
+      krow[i][r] = is_v ? 4 * (u / (D / 8)) + r : c / (D / 8);
+      koff[i][r] = is_v ? 8 * (u % (D / 8)) : 8 * (c % (D / 8));
+    }
+  }
+  auto load_block = [&](int k0) {
+    const bool tail = k0 + kKeys > len;  // uniform
+#pragma unroll
+    for (int i = 0; i < UPT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = tail ? min(k0 + krow[i][r], len - 1) : k0 + krow[i][r];
+        stage[i][r] = *reinterpret_cast<const uint4*>(kvp[i] + (int64_t)key * kvs[i] + koff[i][r]);
+      }
+  };
+  auto store_block = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = tid + i * kThreads;
+      if (u < 2 * D) {
+        const int kq = u / (D / 8), dc = u % (D / 8);
+        const uint32_t w0[4] = {stage[i][0].x, stage[i][0].y, stage[i][0].z, stage[i][0].w};
+        const uint32_t w1[4] = {stage[i][1].x, stage[i][1].y, stage[i][1].z, stage[i][1].w};
+        const uint32_t w2[4] = {stage[i][2].x, stage[i][2].y, stage[i][2].z, stage[i][2].w};
+        const uint32_t w3[4] = {stage[i][3].x, stage[i][3].y, stage[i][3].z, stage[i][3].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          uint2 t;
+          t.x = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);  // keys 4kq, 4kq+1 of dim 8dc+e
+          t.y = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);  // keys 4kq+2, 4kq+3
+          *reinterpret_cast<uint2*>(&sVt[buf][(8 * dc + e) * VPAD + 4 * kq]) = t;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = 4 * (u - 2 * D) + r;
+          *reinterpret_cast<uint4*>(&sK[buf][(c / (D / 8)) * KPAD + 8 * (c % (D / 8))]) = stage[i][r];
+        }
+      }
+    }
+  };
+
+  float m_run[2] = {-INFINITY, -INFINITY};  // raw-score running max of query lc of each tile
+  float l_part[2] = {0.0f, 0.0f};
+  f32x4 o[2][D / 16];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) o[qt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kend = min(len, q0 + P);  // keys 0 .. kend-1 are visible to some row of the workgroup
+  const int nkb = (kend + kKeys - 1) / kKeys;
+  load_block(0);
+  store_block(0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * kKeys;
+    const int buf = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) load_block(k0 + kKeys);
+    if (k0 <= wq_last) {  // wave-uniform: this block holds keys visible to the wave
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[0][t] = acc[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) {
+          const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&sK[buf][(16 * t + lc) * KPAD + 32 * j + 8 * lg]));
+          acc[0][t] = mfma16x16x32(a, qop[0][j], acc[0][t]);
+          acc[1][t] = mfma16x16x32(a, qop[1][j], acc[1][t]);
+        }
+      }
+      const bool masked = k0 + kKeys - 1 > wq0 || k0 + kKeys > len;  // wave-uniform
+      if (masked) {
+        const int lim0 = min(my_q0, len - 1), lim1 = min(my_q1, len - 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 16 * t + 4 * lg + r;
+            acc[0][t][r] = key > lim0 ? -INFINITY : acc[0][t][r];
+            acc[1][t][r] = key > lim1 ? -INFINITY : acc[1][t][r];
+          }
+      }
+      uint4 pa[2][2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, acc[qt][t][r]);
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        // lazy rescale: move the max only when it grows by more than 2^8 in p
+        const bool grow = m_run[qt] == -INFINITY ? bmax > -INFINITY : (bmax - m_run[qt]) * scale_log2 > 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
+          const float m_new = fmaxf(m_run[qt], bmax);
+          const float alpha = m_run[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * scale_log2);
+          m_run[qt] = m_new;
+          l_part[qt] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * lg + r);
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) o[qt][c][r] *= ar;
+          }
+        }
+        const float mb = m_run[qt] * scale_log2;
+        float psum = 0.0f;
+        float p[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[qt][t][r], scale_log2, -mb));
+            psum += p[t][r];
+          }
+        l_part[qt] += psum;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          pa[qt][st].x = cvt_pk_bf16(p[2 * st][0], p[2 * st][1]);
+          pa[qt][st].y = cvt_pk_bf16(p[2 * st][2], p[2 * st][3]);
+          pa[qt][st].z = cvt_pk_bf16(p[2 * st + 1][0], p[2 * st + 1][1]);
+          pa[qt][st].w = cvt_pk_bf16(p[2 * st + 1][2], p[2 * st + 1][3]);
+        }
+      }
+      // O += P.V; k index i of lane group lg = key 32*st + 16*(i/4) + 4*lg + i%4
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int key_a = 32 * st + 4 * lg;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const uint16_t* vr = &sVt[buf][(16 * c + lc) * VPAD];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + key_a);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + key_a + 16);
+          const bf16x8 b = as_bf16x8(uint4{lo.x, lo.y, hi.x, hi.y});
+          o[0][c] = mfma16x16x32(as_bf16x8(pa[0][st]), b, o[0][c]);
+          o[1][c] = mfma16x16x32(as_bf16x8(pa[1][st]), b, o[1][c]);
+        }
+      }
+    }
+    if (more) store_block(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float l_tot = l_part[qt];
+    l_tot += __shfl_xor(l_tot, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    const float inv_l = 1.0f / l_tot;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float inv = __shfl(inv_l, 4 * lg + r);
+      const int row = wq0 + 16 * qt + 4 * lg + r;
+      if (row < len) {
+        bf16_t* op = out + (int64_t)(start + row) * os_t + (int64_t)qh * os_h;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) op[16 * c + lc].bits = (uint16_t)f32_to_bf16(o[qt][c][r] * inv);
+      }
+    }
+  }
+}
+
 FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t,
                                        int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h, void* out,
                                        int64_t os_t, int64_t os_h, const int32_t* cu_seqlens, int num_seqs,
@@ -198,9 +453,25 @@ FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h
   if (num_seqs == 0 || max_seqlen <= 0) return 0;
   if (!q || !k || !v || !out || !cu_seqlens) return (int)hipErrorInvalidValue;
   if (num_seqs > 65535 || num_q_heads > 65535) return (int)hipErrorInvalidValue;
-  const dim3 grid((max_seqlen + kQRows - 1) / kQRows, num_q_heads, num_seqs);
   const float sl2 = scale * 1.4426950408889634f;
   const int group = num_q_heads / num_kv_heads;
+  if ((group == 1 || group == 2 || group == 4) && (head_dim == 64 || head_dim == 128) &&
+      fdms_prefill_gqa_enabled()) {
+    const dim3 ggrid((max_seqlen + 128 / group - 1) / (128 / group), num_kv_heads, num_seqs);
+#define FDMS_PREFILL_GQA(DD, GG)                                                                                   \
+  hipLaunchKernelGGL((prefill_attn_gqa_kernel<DD, GG>), ggrid, dim3(kThreads), 0, (hipStream_t)stream,              \
+                     (const bf16_t*)q, qs_t, qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h,       \
+                     (bf16_t*)out, os_t, os_h, cu_seqlens, sl2)
+    if (head_dim == 64) {
+      if (group == 1) FDMS_PREFILL_GQA(64, 1); else if (group == 2) FDMS_PREFILL_GQA(64, 2); else FDMS_PREFILL_GQA(64, 4);
+    } else {
+      if (group == 1) FDMS_PREFILL_GQA(128, 1); else if (group == 2) FDMS_PREFILL_GQA(128, 2); else FDMS_PREFILL_GQA(128, 4);
+    }
+#undef FDMS_PREFILL_GQA
+    FDMS_LAUNCH_CHECK();
+    return 0;
+  }
+  const dim3 grid((max_seqlen + kQRows - 1) / kQRows, num_q_heads, num_seqs);
   if (head_dim == 64) {
     hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)q, qs_t,
                        qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h, (bf16_t*)out, os_t, os_h,

@@ -121,16 +121,28 @@ def test_argmax_rows_matches_torch(dtype):
     assert out.cpu().tolist()[1:7] == [5000, 0, 77, 600, n - 1, 0]
 
 
-@pytest.mark.parametrize("d,lens", [(64, [1, 63, 64, 65, 200, 517]), (128, [129, 700, 2])])
-def test_prefill_attention_vs_oracle(d, lens):
+@pytest.mark.parametrize("d,lens,hq,hkv,ramp", [
+    (64, [1, 63, 64, 65, 200, 517], 8, 2, 0.0),
+    (128, [129, 700, 2], 8, 2, 0.0),
+    (64, [31, 160, 1500], 4, 4, 0.0),      # G = 1 (packed kernel, 128 positions per workgroup)
+    (128, [95, 300], 8, 4, 0.0),           # G = 2
+    (64, [77, 400], 6, 2, 0.0),            # G = 3 (per-head kernel)
+    (64, [2100, 130], 8, 2, 3.0),          # keys scaled up along the sequence: the running max keeps growing
+    (128, [900], 8, 2, 3.0),
+])
+def test_prefill_attention_vs_oracle(d, lens, hq, hkv, ramp):
     """Causal varlen attention (flash_attn_varlen_func semantics, attention.py:85-92)
-    on q/k/v that are strided views of fused qkv rows, GQA 8/2."""
+    on q/k/v that are strided views of fused qkv rows, GQA hq/hkv.  ramp > 0
+    scales key t of each sequence by 1 + ramp * t / len, so later blocks raise
+    the softmax max (the kernel's rescale path)."""
     require_gpu()
     from fastdms_amd.layers.attention import prefill_attention
-    hq, hkv = 8, 2
     t = sum(lens)
-    rng = np.random.default_rng(d)
+    rng = np.random.default_rng(d + 7 * hq + hkv)
     qkv = rng.standard_normal((t, (hq + 2 * hkv) * d)).astype(np.float32)
+    if ramp:
+        pos = np.concatenate([np.arange(n) / n for n in lens]).astype(np.float32)
+        qkv[:, hq * d:(hq + hkv) * d] *= (1.0 + ramp * pos)[:, None]
     qkv_b = _bf16(qkv)
     qkv_v = qkv_b.float().numpy()
     q = qkv_v[:, :hq * d].reshape(t, hq, d)
