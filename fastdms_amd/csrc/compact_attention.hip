@@ -881,16 +881,12 @@ __device__ __forceinline__ v4f16_t fp8x4_to_f16x4(uint32_t w) {
 __device__ __forceinline__ float blocks_sum(float v) {
   v += dpp_f<0x128>(v);  // row_ror:8
   v += dpp_f<0x124>(v);  // row_ror:4
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return rows_sum(v);    // lanes l^16, l^32
 }
 __device__ __forceinline__ float blocks_max(float v) {
   v = fmaxf(v, dpp_f<0x128>(v));
   v = fmaxf(v, dpp_f<0x124>(v));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  return rows_max(v);
 }
 // value of lane (l & ~3) + I (quad broadcast)
 template <int I>

@@ -113,15 +113,45 @@ template <typename T> struct Copy<T, T> {
 };
 
 // ---------------------------------------------------------------- wave helpers
+// DPP move within 16-lane rows (CTRL e.g. 0x120 + n = row_ror:n).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the
+// gfx950 row-swap permutes: permlane16_swap(x, x) yields (even rows, odd rows)
+// of x in every row pair and permlane32_swap(x, x) (low half, high half), so
+// combining the two results reduces over xor 16 then xor 32 without an LDS
+// round trip.  Every lane gets the same bits (the combines are commutative).
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Whole-wave max / sum: rotations by 8, 4, 2, 1 inside each row (DPP), then
+// across rows.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp_mov_f<0x128>(v));
+  v = fmaxf(v, dpp_mov_f<0x124>(v));
+  v = fmaxf(v, dpp_mov_f<0x122>(v));
+  v = fmaxf(v, dpp_mov_f<0x121>(v));
+  return rows_max(v);
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp_mov_f<0x128>(v);
+  v += dpp_mov_f<0x124>(v);
+  v += dpp_mov_f<0x122>(v);
+  v += dpp_mov_f<0x121>(v);
+  return rows_sum(v);
 }
 
 // torch.argmax order: NaN beats every number (lowest NaN index wins), ties go

@@ -371,8 +371,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, acc[qt][t][r]);
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = rows_max(bmax);
         // lazy rescale: move the max only when it grows by more than 2^8 in p
         const bool grow = m_run[qt] == -INFINITY ? bmax > -INFINITY : (bmax - m_run[qt]) * scale_log2 > 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
@@ -427,9 +426,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
 
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float l_tot = l_part[qt];
-    l_tot += __shfl_xor(l_tot, 16);
-    l_tot += __shfl_xor(l_tot, 32);
+    const float l_tot = rows_sum(l_part[qt]);
     const float inv_l = 1.0f / l_tot;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
