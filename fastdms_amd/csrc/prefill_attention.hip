@@ -216,8 +216,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 // the current one is computed, and one barrier separates blocks.  V is
 // transposed in registers (4 keys x 8 dims per thread, byte permutes) so the
 // LDS stores are 8-byte vectors.  Every K fragment read from LDS feeds both
-// query tiles of a wave, as does every V fragment.  Softmax rescaling is lazy:
-// the running max only moves (and O / l are rescaled) when a block raises it
+// query tiles of a wave, as does every V fragment.  The softmax row sums come
+// from the matrix cores (P . 1, an extra output tile).  Softmax rescaling is
+// lazy: the running max only moves (and O / the sums are rescaled) when a block raises it
 // by more than 8 in the log2 domain, so p = exp2(s - m) stays below 256.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
@@ -226,7 +227,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     int64_t os_h, const int32_t* __restrict__ cu_seqlens, float scale_log2) {
   constexpr int P = 128 / G;        // query positions per workgroup
   constexpr int KPAD = D + 8;       // sK row stride (bf16)
-  constexpr int VPAD = kKeys + 8;   // sVt row stride (bf16)
+  // sVt row stride (bf16): 136 B = 34 dwords, so the 16 lanes of one 8-byte
+  // B-operand read (rows 16c + lc) land on 16 distinct bank pairs
+  constexpr int VPAD = kKeys + 4;
   constexpr int UNITS = 4 * D;      // staging units per block: 2D V quads (4 keys x 8 dims) + 2D K quads (4 chunks)
   constexpr int UPT = UNITS / kThreads;
   static_assert(UNITS % kThreads == 0, "staging units must divide over the workgroup");
@@ -262,8 +265,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   const bf16_t* kb_base = k + (int64_t)start * ks_t + (int64_t)kvh * ks_h;
   const bf16_t* vb_base = v + (int64_t)start * vs_t + (int64_t)kvh * vs_h;
   uint4 stage[UPT][4];
-  // unit u < 2D: V quad (keys 4*(u / (D/8)) .. +3, dims 8*(u % (D/8)) .. +7);
-  // u >= 2D: K chunks 4*(u - 2D) .. +3 (chunk c = key * (D/8) + dim / 8).
+  // unit u < 2D: V quad (keys 4*(u % 16) .. +3, dims 8*(u / 16) .. +7: the 16
+  // lanes of a row store 128 contiguous bytes of one transposed row);
+  // u >= 2D: K chunks (u - 2D) + 2D*r, r = 0..3 (chunk c = key * (D/8) + dim / 8:
+  // consecutive lanes move consecutive 16-byte chunks).
   // Row r of unit i is key k0 + krow[i][r] at element offset koff[i][r] +
   // key * stride; rows past the sequence end are clamped (their scores are
   // masked).
@@ -278,9 +283,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     kvs[i] = is_v ? vs_t : ks_t;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int c = 4 * (u - 2 * D) + r;
-      krow[i][r] = is_v ? 4 * (u / (D / 8)) + r : c / (D / 8);
-      koff[i][r] = is_v ? 8 * (u % (D / 8)) : 8 * (c % (D / 8));
+      const int c = (u - 2 * D) + 2 * D * r;
+      krow[i][r] = is_v ? 4 * (u % 16) + r : c / (D / 8);
+      koff[i][r] = is_v ? 8 * (u / 16) : 8 * (c % (D / 8));
     }
   }
   auto load_block = [&](int k0) {
@@ -298,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     for (int i = 0; i < UPT; ++i) {
       const int u = tid + i * kThreads;
       if (u < 2 * D) {
-        const int kq = u / (D / 8), dc = u % (D / 8);
+        const int kq = u % 16, dc = u / 16;
         const uint32_t w0[4] = {stage[i][0].x, stage[i][0].y, stage[i][0].z, stage[i][0].w};
         const uint32_t w1[4] = {stage[i][1].x, stage[i][1].y, stage[i][1].z, stage[i][1].w};
         const uint32_t w2[4] = {stage[i][2].x, stage[i][2].y, stage[i][2].z, stage[i][2].w};
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int c = 4 * (u - 2 * D) + r;
+          const int c = (u - 2 * D) + 2 * D * r;
           *reinterpret_cast<uint4*>(&sK[buf][(c / (D / 8)) * KPAD + 8 * (c % (D / 8))]) = stage[i][r];
         }
       }
@@ -322,12 +327,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   };
 
   float m_run[2] = {-INFINITY, -INFINITY};  // raw-score running max of query lc of each tile
-  float l_part[2] = {0.0f, 0.0f};
-  f32x4 o[2][D / 16];
+  // o[qt][D/16] accumulates P . 1 on the matrix cores: column-replicated row
+  // sums of the same bf16 P as the numerator, in the O layout (no shuffles)
+  f32x4 o[2][D / 16 + 1];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) o[qt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c <= D / 16; ++c) o[qt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bf16x8 ones = as_bf16x8(uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
   const int kend = min(len, q0 + P);  // keys 0 .. kend-1 are visible to some row of the workgroup
   const int nkb = (kend + kKeys - 1) / kKeys;
@@ -378,25 +385,19 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
           const float m_new = fmaxf(m_run[qt], bmax);
           const float alpha = m_run[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * scale_log2);
           m_run[qt] = m_new;
-          l_part[qt] *= alpha;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float ar = __shfl(alpha, 4 * lg + r);
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) o[qt][c][r] *= ar;
+            for (int c = 0; c <= D / 16; ++c) o[qt][c][r] *= ar;
           }
         }
         const float mb = m_run[qt] * scale_log2;
-        float psum = 0.0f;
         float p[4][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[qt][t][r], scale_log2, -mb));
-            psum += p[t][r];
-          }
-        l_part[qt] += psum;
+          for (int r = 0; r < 4; ++r) p[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[qt][t][r], scale_log2, -mb));
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
           pa[qt][st].x = cvt_pk_bf16(p[2 * st][0], p[2 * st][1]);
@@ -418,6 +419,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
           o[0][c] = mfma16x16x32(as_bf16x8(pa[0][st]), b, o[0][c]);
           o[1][c] = mfma16x16x32(as_bf16x8(pa[1][st]), b, o[1][c]);
         }
+        o[0][D / 16] = mfma16x16x32(as_bf16x8(pa[0][st]), ones, o[0][D / 16]);
+        o[1][D / 16] = mfma16x16x32(as_bf16x8(pa[1][st]), ones, o[1][D / 16]);
       }
     }
     if (more) store_block(buf ^ 1);
@@ -426,11 +429,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
 
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const float l_tot = rows_sum(l_part[qt]);
-    const float inv_l = 1.0f / l_tot;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float inv = __shfl(inv_l, 4 * lg + r);
+      const float inv = 1.0f / o[qt][D / 16][r];  // row sum of query 4*lg + r
       const int row = wq0 + 16 * qt + 4 * lg + r;
       if (row < len) {
         bf16_t* op = out + (int64_t)(start + row) * os_t + (int64_t)qh * os_h;
