@@ -47,6 +47,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_prefill_attention": "pllpllpllpllpiiiiifp",
     "fdms_rmsnorm": "pllippplplifp",
     "fdms_silu_mul": "pplip",
+    "fdms_rmsnorm_partials": "pilppplplifp",
     "fdms_quantize_fp8_rows": "pilliplpip",
     "fdms_linear_small_m": "pliipilppiipfplpliiippplp",
     "fdms_linear_argmax_small_m": "pliipilppiiiipppppp",

@@ -17,6 +17,9 @@
 // and the output may go through a fused epilogue:
 //   EPI = 1: the weight holds [gate; up] (n = 2 * n_out rows, gate_up_proj) and
 //            the output is bf16(silu(bf16 gate) * bf16 up) (activation.py:8-11).
+//   EPI = 3: bf16 weights, no bias: each K split writes its fp32 partial sums
+//            to workspace[split][m][n] and the consumer adds them in split
+//            order (the merge of EPI 0, moved into the next kernel).
 //
 // MI355X mapping: one workgroup per 16-column output strip (per gate/up strip
 // pair for EPI 1) and K split; its NW waves split the workgroup's K range.  A
@@ -400,6 +403,15 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       t[a][3] += o[3];
     }
   }
+  if (EPI == 3) {
+    // split partials for the consumer to sum (no merge here): ws[ks][m][n]
+    const int mm = lane & 15;
+    if (mm < M) {
+      float* dst = ws + ((int64_t)ks * M + mm) * n_out + n0 + 4 * (lane >> 4);
+      *reinterpret_cast<f32x4*>(dst) = t[0];
+    }
+    return;
+  }
   if (ksplit > 1) {
     // split-K: publish this split's fragments (agent-coherent stores), the last
     // split of the strip to arrive sums them all
@@ -563,8 +575,10 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
                                     void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue,
                                     int k_splits, float* workspace, int* counters, void* y, int64_t y_stride,
                                     void* stream) {
-  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 || epilogue > 1 ||
-      quantize_x < 0 || quantize_x > 2)
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 ||
+      (epilogue > 1 && epilogue != 3) || quantize_x < 0 || quantize_x > 2)
+    return (int)hipErrorInvalidValue;
+  if (epilogue == 3 && (w_dtype != kBF16 || prologue != 0 || quantize_x != 0 || bias || !workspace))
     return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
   if (!x || !w || !y || (prologue == 1 && !norm_weight)) return (int)hipErrorInvalidValue;
@@ -578,7 +592,7 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   const int n_out = epilogue == 1 ? n / 2 : n;
   if (n_out % 16 || (epilogue == 1 && n % 2)) return (int)hipErrorInvalidValue;
   if (k_splits < 1 || k_splits > 64) return (int)hipErrorInvalidValue;
-  if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
+  if (k_splits > 1 && epilogue != 3 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
   if (k % k_splits) return (int)hipErrorInvalidValue;
   int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
@@ -604,7 +618,9 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
             res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, nullptr,
             nullptr};
   a.qx_torch = quantize_x == 2;
-  if (w_dtype == kFP8) {
+  if (epilogue == 3) {
+    launch_linear<bf16_t, 0, false, 3>(nw, grid, (hipStream_t)stream, a);
+  } else if (w_dtype == kFP8) {
     dispatch_linear<fp8_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
   } else {
     dispatch_linear<bf16_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);

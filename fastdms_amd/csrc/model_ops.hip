@@ -25,14 +25,19 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
 
 // x_out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w), where x = in (+ residual
 // in fp32, and residual_out = bf16(x)) — layernorm.py:19-40.
+// PART: the input is the fp32 split-K partial sums of the preceding linear,
+// part[s * split_stride + row * hidden + c], s < k_splits, and x = bf16 of
+// their sum taken in split order (the linear kernel's own merge).
+template <bool PART>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restrict__ in, const bf16_t* residual,
                                                            const bf16_t* __restrict__ weight, bf16_t* __restrict__ out,
                                                            bf16_t* residual_out, int hidden, int64_t in_stride,
                                                            int64_t in_head_stride, int heads, int64_t out_stride,
-                                                           float eps) {
+                                                           float eps, const float* __restrict__ part, int k_splits,
+                                                           int64_t split_stride) {
   __shared__ float s_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
-  const bf16_t* x = in + (row / heads) * in_stride + (row % heads) * in_head_stride;
+  const bf16_t* x = PART ? nullptr : in + (row / heads) * in_stride + (row % heads) * in_head_stride;
   const bf16_t* rs = residual ? residual + row * (int64_t)hidden : nullptr;
   constexpr int V = 8;
   constexpr int kMaxPer = 4;  // hidden <= 8192
@@ -49,12 +54,27 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
     if (c < hidden) {
-      const Vec<bf16_t, V> xv = *reinterpret_cast<const Vec<bf16_t, V>*>(x + c);
+      float xf[V];
+      if constexpr (PART) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xf[i] = 0.0f;
+        for (int sp = 0; sp < k_splits; ++sp) {
+          const Vec<float, V> pv = *reinterpret_cast<const Vec<float, V>*>(part + sp * split_stride + row * hidden + c);
+#pragma unroll
+          for (int i = 0; i < V; ++i) xf[i] += pv.v[i];
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(f32_to_bf16(xf[i]));
+      } else {
+        const Vec<bf16_t, V> xv = *reinterpret_cast<const Vec<bf16_t, V>*>(x + c);
+#pragma unroll
+        for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(xv.v[i].bits);
+      }
       Vec<bf16_t, V> rv;
       if (rs) rv = *reinterpret_cast<const Vec<bf16_t, V>*>(rs + c);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        float f = bf16_to_f32(xv.v[i].bits);
+        float f = xf[i];
         if (rs) f += bf16_to_f32(rv.v[i].bits);
         vals[j][i] = f;
         ss += f * f;
@@ -95,9 +115,28 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   if (heads > 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   if (!in || !weight || !out || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
                      (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,
-                     (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps);
+                     (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps, nullptr, 0,
+                     (int64_t)0);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// RMSNorm (+ residual) of x = bf16(sum of the k_splits fp32 partials
+// partials[s * split_stride + r * hidden + c]) -- the consumer side of
+// fdms_linear_small_m's epilogue 3.  residual / residual_out contiguous rows.
+FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64_t split_stride,
+                                      const void* residual, const void* weight, void* out, int64_t out_stride,
+                                      void* residual_out, int64_t rows, int hidden, float eps, void* stream) {
+  if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 8 * kThreads * 4 || k_splits < 1) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!partials || !weight || !out || rows > 0x7FFFFFFF || split_stride < rows * (int64_t)hidden)
+    return (int)hipErrorInvalidValue;
+  if ((uintptr_t)partials % 32 || split_stride % 8) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                     nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out, (bf16_t*)residual_out,
+                     hidden, (int64_t)0, (int64_t)0, 1, out_stride, eps, partials, k_splits, split_stride);
   FDMS_LAUNCH_CHECK();
   return 0;
 }

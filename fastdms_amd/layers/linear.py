@@ -21,7 +21,7 @@ from .. import _native as nat
 from . import quant_env as qe
 
 PRO_NONE, PRO_RMSNORM = 0, 1
-EPI_NONE, EPI_SILU_MUL = 0, 1
+EPI_NONE, EPI_SILU_MUL, EPI_PARTIALS = 0, 1, 3
 QX_NONE, QX_DIVIDE, QX_TORCH = 0, 1, 2   # activation quantisation: none / 448/amax / reciprocal(amax)*448
 SMALL_M_MAX_ROWS = 16
 _MAX_K_SPLITS = 8
@@ -66,6 +66,65 @@ def choose_k_splits(device: torch.device, strips: int, k: int) -> int:
     return s
 
 
+def choose_partial_splits(device: torch.device, strips: int, k: int) -> int:
+    """K splits of a linear whose merge the consumer does (no merge cost in the
+    linear): enough workgroups to cover the CUs, each split a whole number of
+    512-column slices.  FASTDMS_AMD_PARTIAL_SPLITS overrides (tuning)."""
+    env = os.environ.get("FASTDMS_AMD_PARTIAL_SPLITS", "").strip()
+    if env.isdigit() and int(env) >= 1 and k % (int(env) * 256) == 0:
+        return int(env)
+    s = 1
+    cus = _num_cus(device)
+    while s * 2 <= _MAX_K_SPLITS and strips * s < cus and k % (s * 2 * 512) == 0:
+        s *= 2
+    return s
+
+
+class SplitPartials:
+    """fp32 split-K partial sums [k_splits, rows, n] of a decode linear whose
+    merge is left to the consuming RMSNorm (``rms_norm`` accepts this in place
+    of x): x = bf16(sum over splits, in split order)."""
+
+    def __init__(self, data: torch.Tensor):
+        self.data = data
+
+    @property
+    def shape(self):
+        return self.data.shape[1:]
+
+
+_PARTIALS: dict[int, torch.Tensor] = {}
+
+
+def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None = None) -> SplitPartials:
+    """y = x @ W^T (bf16 W [N, K], no bias, at most 16 rows) as fp32 split
+    partials (fdms_linear_small_m epilogue 3).  The partials live in a per-device
+    buffer that the next call overwrites: consume them before the next
+    linear_partials call."""
+    if weight.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+        raise ValueError("linear_partials expects bf16 activations and bf16 weights")
+    n, k = weight.shape
+    rows = x.shape[0]
+    if not small_m_supported(rows, k, n) or x.shape[1] != k:
+        raise ValueError(f"linear_partials does not support rows={rows}, K={k}, N={n}")
+    if k_splits is None:
+        k_splits = choose_partial_splits(x.device, n // 16, k)
+    need = k_splits * rows * n
+    idx = _device_index(x.device)
+    buf = _PARTIALS.get(idx)
+    if buf is None or buf.numel() < need:
+        if buf is not None:
+            _RETIRED.append(buf)
+        buf = torch.empty(max(need, SMALL_M_MAX_ROWS * 4096 * 4), device=x.device, dtype=torch.float32)
+        _PARTIALS[idx] = buf
+    part = buf[:need].view(k_splits, rows, n)
+    nat.require_cuda(x, weight, what="linear_partials")
+    nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(), nat.DT_BF16,
+             weight.stride(0), None, None, n, PRO_NONE, None, 0.0, None, 0, None, 0, QX_NONE, EPI_PARTIALS,
+             int(k_splits), part.data_ptr(), None, part.data_ptr(), n, nat.stream())
+    return SplitPartials(part)
+
+
 def linear_workspace(device: torch.device, n_floats: int, n_counters: int):
     idx = _device_index(device)
     entry = _WS.setdefault(idx, [None, None])
@@ -81,8 +140,15 @@ def linear_workspace(device: torch.device, n_floats: int, n_counters: int):
 
 
 def reserve_linear_workspace(device: torch.device, max_out_features: int) -> None:
-    """Size the split-K workspace for any linear of at most max_out_features
-    output columns (call before graph capture)."""
+    """Size the split-K workspace (and the split-partials buffer) for any
+    linear of at most max_out_features output columns (call before graph
+    capture)."""
+    idx = _device_index(device)
+    need = _MAX_K_SPLITS * SMALL_M_MAX_ROWS * max_out_features
+    if idx not in _PARTIALS or _PARTIALS[idx].numel() < need:
+        if idx in _PARTIALS:
+            _RETIRED.append(_PARTIALS[idx])
+        _PARTIALS[idx] = torch.empty(need, device=device, dtype=torch.float32)
     strips = max_out_features // 16
     linear_workspace(device, strips * _MAX_K_SPLITS * 512, strips)
 

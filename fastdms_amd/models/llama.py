@@ -8,6 +8,7 @@ pack of post-RoPE k / v into compact spans (prefill) -> attention -> o_proj.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 
 import torch
@@ -23,7 +24,7 @@ from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm, rms_norm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
                              QKVParallelLinear, RowParallelLinear, linear_argmax_small_m, linear_int4_small_m,
-                             linear_small_m, small_m_supported)
+                             linear_partials, linear_small_m, small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -65,6 +66,21 @@ def _fused_linear(lin: LinearBase, x: torch.Tensor, prologue: int, norm: RMSNorm
     return linear_small_m(x, lin.weight, lin.bias, prologue=prologue,
                           norm_weight=None if norm is None else norm.weight, eps=1e-6 if norm is None else norm.eps,
                           residual=residual, residual_out=residual_out, epilogue=epilogue)
+
+
+def _deferred_linear(lin: LinearBase, x: torch.Tensor):
+    """A linear whose only consumer is an RMSNorm: on the bf16 decode path its
+    split-K merge moves into that RMSNorm (SplitPartials), which saves the
+    linear's merge round trips; other paths return the finished tensor."""
+    rows = x.shape[0]
+    if (_defer_splitk_enabled() and lin.bias is None and lin.route(rows)[0] == "bf16"
+            and small_m_supported(rows, lin.input_size, lin.output_size) and x.stride(-1) == 1):
+        return linear_partials(x, lin.weight)
+    return _fused_linear(lin, x, PRO_NONE)
+
+
+def _defer_splitk_enabled() -> bool:
+    return os.environ.get("FASTDMS_AMD_DEFER_SPLITK", "1").strip() != "0"
 
 
 class LlamaAttention(nn.Module):
@@ -226,10 +242,10 @@ class LlamaModel(nn.Module):
             else:
                 h, res = layer.input_layernorm(x, res)
             qkv = _fused_linear(attn.qkv_proj, h, PRO_NONE)
-            o = _fused_linear(attn.o_proj, attn.attend(positions, qkv), PRO_NONE)
+            o = _deferred_linear(attn.o_proj, attn.attend(positions, qkv))
             h, res = layer.post_attention_layernorm(o, res)
             act = _fused_linear(mlp.gate_up_proj, h, PRO_NONE, epilogue=EPI_SILU_MUL)
-            x = _fused_linear(mlp.down_proj, act, PRO_NONE)
+            x = _deferred_linear(mlp.down_proj, act)
         h, _ = self.norm(x, res)
         if greedy_out is not None:
             lm_head.greedy_into(h, greedy_out)

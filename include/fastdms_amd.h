@@ -226,6 +226,16 @@ int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int 
 /* out = silu(x[:, :F]) * x[:, F:], bf16 (fastdms/layers/activation.py:8-11). */
 int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
 
+/* RMSNorm (+ residual) whose input row r is bf16(sum over s < k_splits of
+ * partials[s * split_stride + r * hidden + c]) in split order: the merge of a
+ * split-K fdms_linear_small_m (epilogue 3) done by its consumer, as the
+ * reference's RMSNorm(down_proj / o_proj output, residual) sequence
+ * (layernorm.py:19-40; llama.py:248-266).  partials 32-byte aligned,
+ * split_stride a multiple of 8; residual / residual_out contiguous rows. */
+int fdms_rmsnorm_partials(const float* partials, int k_splits, int64_t split_stride, const void* residual,
+                          const void* weight, void* out, int64_t out_stride, void* residual_out, int64_t rows,
+                          int hidden, float eps, void* stream);
+
 /* Row argmax, ties to the lowest index (fastdms/layers/embed_head.py:142, 160,
  * and the torch argmax of ParallelLMHead.greedy_token_ids, 491-543). */
 int fdms_argmax_rows(const void* x, int dtype, int64_t stride, int64_t rows, int n, int64_t* out, void* stream);
@@ -253,7 +263,10 @@ int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int6
  * w_dtype bf16.  prologue 1 = RMSNorm of x (+ residual, fp32 sum; the bf16 sum
  * goes to residual_out, written by one workgroup; layernorm.py:19-40).
  * epilogue 1 = W is [gate; up] (n rows), the output has n/2 columns
- * bf16(silu(gate) * up) (activation.py:8-11).  k_splits > 1 splits K over
+ * bf16(silu(gate) * up) (activation.py:8-11).  epilogue 3 (bf16 weights, no
+ * bias, no prologue) = no merge: split s writes its fp32 partial sums to
+ * workspace[(s * m + row) * n + col] and y is not written; the consumer
+ * (fdms_rmsnorm_partials) adds the splits in order.  k_splits > 1 splits K over
  * workgroups: workspace holds (n_out/16) * k_splits * 256 floats (x2 for
  * epilogue 1) and counters n_out/16 ints, zero before the first call and left
  * zero.  k / k_splits a multiple of 256, n_out of 16, 16-byte aligned rows; y

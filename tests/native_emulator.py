@@ -537,6 +537,28 @@ class Emulator:
         self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
         return 0
 
+    def rmsnorm_partials(self, partials, k_splits, split_stride, residual, weight, out, out_stride, residual_out,
+                         rows, hidden, eps, stream):
+        if rows < 0 or hidden <= 0 or hidden % 8 or hidden > 8192 or k_splits < 1 or split_stride < rows * hidden:
+            return 1
+        if rows == 0:
+            return 0
+        part = self.view(partials, torch.float32, (k_splits, rows, hidden), (split_stride, hidden, 1), "partials")
+        acc = torch.zeros((rows, hidden), dtype=torch.float32)
+        for s in range(k_splits):
+            acc = acc + part[s]
+        f = acc.to(torch.bfloat16).float()
+        if residual:
+            f = f + self.view(residual, torch.bfloat16, (rows, hidden), (hidden, 1), "residual").float()
+        if residual_out:
+            self.view(residual_out, torch.bfloat16, (rows, hidden), (hidden, 1), "residual_out").copy_(
+                f.to(torch.bfloat16))
+        w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
+        inv = 1.0 / torch.sqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
+        xn = (f * inv).to(torch.bfloat16).float()
+        self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
+        return 0
+
     def silu_mul(self, x, out, rows, f, stream):
         if rows == 0:
             return 0
@@ -566,6 +588,15 @@ class Emulator:
         n_out = n // 2 if epilogue == 1 else n
         if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1):
             return 1
+        if epilogue == 3:  # split partials: all of the fp32 sum in split 0, zeros in the others
+            if w_dtype != DT_BF16 or prologue or qx or bias or not ws:
+                return 1
+            part = self.view(ws, torch.float32, (k_splits, m, n), (m * n, n, 1), "partials")
+            xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
+            wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float()
+            part.zero_()
+            part[0].copy_(xv @ wv.T)
+            return 0
         if k_splits > 1:
             strips = n_out // 16
             self.view(ws, torch.float32, (strips * k_splits * 256 * (2 if epilogue else 1),), (1,), "workspace")

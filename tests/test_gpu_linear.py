@@ -134,6 +134,35 @@ def test_linear_small_m_split_k_is_consistent(splits):
                 f"silu split {splits}", ulps=2.0, atol=2e-3)
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(8, 2048, 8192, 2), (8, 2048, 2048, 2), (3, 512, 4096, 4),
+                                          (16, 256, 2048, 1), (1, 2048, 8192, 8)])
+def test_linear_partials_sum_to_the_merged_linear(m, n, k, splits):
+    """Epilogue 3 (split partials, merge left to the consumer): the fp32
+    partials summed in split order and rounded to bf16 equal the merged
+    split-K linear bit for bit; the RMSNorm of the partials (+ residual) equals
+    the RMSNorm of that bf16 tensor bit for bit."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    from fastdms_amd.layers.linear import SplitPartials, linear_partials, linear_small_m
+    g = torch.Generator().manual_seed(m * 31 + splits)
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    merged = linear_small_m(x, w, k_splits=splits)
+    part = linear_partials(x, w, k_splits=splits)
+    assert tuple(part.data.shape) == (splits, m, n)
+    acc = torch.zeros((m, n), device="cuda", dtype=torch.float32)
+    for s in range(splits):
+        acc = acc + part.data[s]
+    assert torch.equal(acc.to(torch.bfloat16), merged), "partials do not sum to the merged linear"
+    _close_bf16(merged, _ref_linear(x.cpu(), w.cpu(), None), f"partials split {splits}")
+    nw = (1.0 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16).cuda()
+    res = _bf16((m, n), g).cuda()
+    want_h, want_res = rms_norm(merged, nw, 1e-5, residual=res)
+    got_h, got_res = rms_norm(SplitPartials(part.data), nw, 1e-5, residual=res)
+    torch.cuda.synchronize()
+    assert torch.equal(got_res, want_res) and torch.equal(got_h, want_h)
+    assert torch.equal(rms_norm(SplitPartials(part.data), nw, 1e-5), rms_norm(merged, nw, 1e-5))
+
+
 @pytest.mark.parametrize("quantize_x", [0, 1, 2])
 @pytest.mark.parametrize("m,n,k", [(1, 3072, 2048), (8, 2048, 8192), (5, 512, 256)])
 def test_linear_small_m_fp8_matches_oracle(quantize_x, m, n, k):
