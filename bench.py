@@ -69,6 +69,7 @@ def parse_args():
     p.add_argument("--attn-replays", type=int, default=50)
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-scaling", action="store_true", help="skip the attention batch-scaling points")
     p.add_argument("--eager", action="store_true", help="decode without HIP graphs")
     return p.parse_args()
 
@@ -167,6 +168,82 @@ def attention_roofline(llm, seqs, replays: int):
             "bytes_per_launch": int(bytes_per_launch), "max_splits_per_pair": splits,
             "live_tokens_per_head": {"mean": round(float(lv.float().mean()), 1), "max": int(lv.max()),
                                      "p99": int(lv.float().quantile(0.99))}}
+
+
+def attention_scaling(llm, seqs, batches=(8, 32, 128), layers: int = 8, replays: int = 20):
+    """The same fused decode attention kernel at larger batches: per-(seq, head)
+    live counts resampled from the bench's own decode state (layer-major), one
+    arena per layer (distinct memory, more than the MALL at the larger sizes),
+    HIP events over graph replays of `layers` launches.  Shows how the kernel's
+    HBM rate grows once a launch carries more than the c=8 step's few MB."""
+    import torch
+    from fastdms_amd.layers.compact_attention import fused_dms_rope_store_compact_decode_attention
+
+    runner = llm.model_runner
+    mgr = runner.compact_kv_manager
+    cfg = llm.config.hf_config
+    md = runner.dms_metadata
+    states = [mgr.seq_states[s.seq_id] for s in seqs]
+    start = mgr._contiguous_active_slot_start(states)
+    pool = mgr.layer_major_live_counts[:, start:start + len(seqs)].reshape(-1).to(torch.int64).cpu()
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    cos_sin = runner.model.model.layers[0].self_attn.rotary_emb.cos_sin_cache
+    dt = mgr.compact_k_per_layer[0].dtype
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    rows = []
+    for b in batches:
+        live = pool[torch.randint(0, pool.numel(), (layers, b, hkv), generator=gen)].to(torch.int32)
+        cap = int(live.max()) + 1
+        base = (torch.arange(b * hkv, dtype=torch.int32) * cap).view(1, b, hkv).expand(layers, b, hkv).contiguous()
+        arenas = [(torch.randint(0, 120, (b * hkv * cap, d), dtype=torch.uint8, device="cuda").view(dt),
+                   torch.randint(0, 120, (b * hkv * cap, d), dtype=torch.uint8, device="cuda").view(dt))
+                  for _ in range(layers)]
+        live_d, base_d = live.cuda(), base.cuda()
+        slot = (base_d + live_d - 1).contiguous()
+        qkv = (torch.randn((b, (hq + 2 * hkv) * d), generator=gen) * 4).to(device="cuda", dtype=torch.bfloat16)
+        q = qkv[:, :hq * d].view(b, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+        positions = torch.full((b,), 8300, device="cuda", dtype=torch.int64)
+        evict = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
+        out = torch.empty_like(q)
+        hint = (int(live.max()) // 256 + 1) * 256
+
+        def launch(l):
+            fused_dms_rope_store_compact_decode_attention(
+                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions, base_d[l], live_d[l],
+                num_kv_heads=hkv, alpha_scale=md.alpha_scale, alpha_offset=md.alpha_offset, max_live_count=hint,
+                out=out)
+
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        with torch.inference_mode(), torch.cuda.stream(s):
+            for l in range(layers):
+                launch(l)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                for l in range(layers):
+                    launch(l)
+            g.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(s)
+            for _ in range(replays):
+                g.replay()
+            t1.record(s)
+            torch.cuda.synchronize()
+        per_launch_s = t0.elapsed_time(t1) / 1e3 / (replays * layers)
+        elem = arenas[0][0].element_size()
+        kv_bytes = int((live.to(torch.int64) - 1).clamp(min=0).sum()) * d * 2 * elem / layers
+        io_bytes = b * ((hq + 2 * hkv) * d * 2 + 2 * hkv * d * elem + hq * d * 2 + hkv * 13 + 8 + d * 4)
+        nbytes = kv_bytes + io_bytes
+        achieved = nbytes / per_launch_s / 1e9
+        rows.append({"batch": b, "pairs": b * hkv, "bytes_per_launch": int(nbytes),
+                     "avg_launch_us": round(per_launch_s * 1e6, 2), "achieved": round(achieved, 1),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4)})
+        del arenas
+    return {"kernel": "decode_attn_mfma_kernel<fused>", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
+            "live_counts": "resampled from this run's decode state", "points": rows}
 
 
 def _pmc_traffic(name: str = "decode_attention_pmc_traffic.json"):
@@ -389,6 +466,8 @@ def main():
         cpu = cpu_baseline(llm, seqs, args.cpu_seconds)
     progress("attention roofline")
     roof = attention_roofline(llm, seqs, args.attn_replays)
+    progress("attention scaling")
+    scaling = attention_scaling(llm, seqs) if not args.no_scaling else None
     progress("compaction roofline")
     pack = compaction_roofline(lens)
     copy_bw = hbm_copy_gbps()
@@ -402,6 +481,7 @@ def main():
                    "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager},
         "prefill_tok_s": round(sum(lens) / prefill_s, 1),
         "roofline": roof,
+        "roofline_scaling": scaling,
         "compaction_roofline": pack,
         "hbm_copy_gbps": round(copy_bw, 1),
         "cpu_baseline": cpu,

@@ -1494,13 +1494,25 @@ FDMS_EXPORT int fdms_fused_decode_attention(
   const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                       slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                       positive_scale};
-#define FDMS_FUSED_LAUNCH(DD)                                                                                    \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 8, false, true>), dim3((unsigned)blocks), dim3(8 * kWave), 0, \
+  // waves per workgroup: 8 when few (seq, head) pairs must fill the chip, 4
+  // (head_dim 64) once there are several pairs per CU, so each wave runs more
+  // 64-row groups per workgroup prologue / combine
+  int nw = (head_dim == 64 && pairs >= 256) ? 4 : 8;
+  if (const char* e = std::getenv("FASTDMS_AMD_FUSED_WAVES")) {  // tuning override
+    const int v = std::atoi(e);
+    if (v == 8 || (v == 4 && head_dim == 64)) nw = v;
+  }
+#define FDMS_FUSED_LAUNCH(DD, NWV)                                                                                \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, false, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
                      (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,   \
                      c_s, base_offsets, bo_b, bo_h, nullptr, 0, 0, 0, 0, live_counts, lc_b, lc_h, (bf16_t*)out,     \
                      os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, \
                      nullptr, 0, 0, nullptr, pre)
-  if (head_dim == 64) FDMS_FUSED_LAUNCH(64); else FDMS_FUSED_LAUNCH(128);
+  if (head_dim == 64) {
+    if (nw == 4) FDMS_FUSED_LAUNCH(64, 4); else FDMS_FUSED_LAUNCH(64, 8);
+  } else {
+    FDMS_FUSED_LAUNCH(128, 8);
+  }
 #undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;
