@@ -49,6 +49,17 @@ class Config:
     seed: int = 0
     dms_survive_fraction: float = 0.125
     compact_decode_cudagraph: bool = True
+    # What happens when a prefill's compact spans do not fit (the reference
+    # raises from the allocator, compact_kv.py:715-718): "defer" puts the
+    # prefill back at the head of the queue until a running sequence finishes;
+    # "preempt" frees the most recently admitted running sequences (re-admitted
+    # later by re-prefilling their tokens) until it fits.
+    compact_admission: str = "defer"
+    # Decode rows reserved per compact span after the pack.  None reserves
+    # max_tokens (the reference's sizing: decode never runs out); a smaller
+    # number overcommits the KV memory: a full span grows during decode and,
+    # when no range is free, the youngest running sequence is preempted.
+    compact_decode_reserve_tokens: int | None = None
     # LM-head GEMV fused with the greedy argmax (no logits materialised);
     # FASTDMS_GREEDY_FUSED_ARGMAX, default on (embed_head.py:62-63)
     fused_greedy_head: bool = field(default_factory=lambda: _env_flag("FASTDMS_GREEDY_FUSED_ARGMAX", True))
@@ -56,6 +67,11 @@ class Config:
     def __post_init__(self):
         from .models.synthetic import model_config
         assert self.kvcache_block_size % 256 == 0
+        if self.compact_admission not in ("defer", "preempt"):
+            raise ValueError(f"compact_admission must be 'defer' or 'preempt', got {self.compact_admission!r}")
+        if self.compact_decode_reserve_tokens is not None and (
+                self.compact_admission != "preempt" or self.compact_decode_reserve_tokens < 1):
+            raise ValueError("compact_decode_reserve_tokens needs compact_admission='preempt' and a positive value")
         if self.tensor_parallel_size != 1:
             raise ValueError("this build runs on one GPU (tensor_parallel_size must be 1)")
         assert self.kv_cache_dtype in _KV_CACHE_DTYPES, f"kv_cache_dtype must be one of {sorted(_KV_CACHE_DTYPES)}"

@@ -158,6 +158,15 @@ class CompactKVSequenceState:
     # device syncs: exact after the prefill pack, +1 per appended token,
     # never below the true value (expiry only lowers it on the device)
     live_upper_bound: int = 0
+    # host lower bound of min over (layer, head) of range capacity - live count
+    # (free rows for decode appends): exact after the pack or a sync, -1 per
+    # appended token
+    decode_slack: int = 1 << 30
+
+
+class CompactCapacityExhausted(RuntimeError):
+    """No free range of a layer can hold a span (compact_kv.py:715-718 raises a
+    plain RuntimeError here; the subclass lets the engine preempt or defer)."""
 
 
 class CompactKVManager:
@@ -167,7 +176,8 @@ class CompactKVManager:
                  device: torch.device | str, target_live_tokens_per_seq: int | None = None,
                  head_dim: int | None = None, compact_dtype: torch.dtype | None = None,
                  per_layer_storage: bool = False, layer_major_metadata: bool = False,
-                 max_active_seqs: int | None = None, preallocate: bool = False):
+                 max_active_seqs: int | None = None, preallocate: bool = False,
+                 decode_reserve_tokens: int | None = None):
         if capacity_tokens <= 0:
             raise ValueError(f"capacity_tokens must be positive, got {capacity_tokens}")
         self.num_layers = num_layers
@@ -176,6 +186,11 @@ class CompactKVManager:
         self.max_model_len = max_model_len
         self.device = torch.device(device)
         self.per_layer_storage = per_layer_storage
+        # decode rows reserved per span after the pack: max_tokens (the
+        # reference's sizing, compact_kv.py:830-857) or, overcommitting, at most
+        # this many (spans then grow during decode, grow_for_decode)
+        self.decode_reserve_tokens = decode_reserve_tokens
+        self.num_span_moves = 0
         self.head_dim = head_dim
         self.compact_dtype = compact_dtype
         self.layer_major_metadata = layer_major_metadata
@@ -295,8 +310,8 @@ class CompactKVManager:
             else:
                 free[idx] = (start + length, available - length)
             return start
-        raise RuntimeError(f"compact KV capacity exhausted in layer {layer_id}: requested {length}, "
-                           f"free {self.free_tokens_in_layer(layer_id)}")
+        raise CompactCapacityExhausted(f"compact KV capacity exhausted in layer {layer_id}: requested {length}, "
+                                       f"free {self.free_tokens_in_layer(layer_id)}")
 
     def _free_range(self, layer_id: int, start: int, length: int) -> None:
         if length <= 0:
@@ -356,9 +371,14 @@ class CompactKVManager:
             ev = torch.zeros((L, H, cap), device=self.device, dtype=torch.bool)
         state = CompactKVSequenceState(seq_id=seq.seq_id, base_offsets=base, range_capacity=rcap, live_counts=live,
                                        token_positions=pos, evict_mask=ev, active_slot=active_slot,
-                                       max_capacity_per_lh=cap, decode_headroom=int(seq.max_tokens))
+                                       max_capacity_per_lh=cap, decode_headroom=self._decode_headroom(seq))
         self.seq_states[seq.seq_id] = state
         return state
+
+    def _decode_headroom(self, seq: Sequence) -> int:
+        if self.decode_reserve_tokens is None:
+            return int(seq.max_tokens)
+        return max(1, min(int(seq.max_tokens), int(self.decode_reserve_tokens)))
 
     def _layer_range_sizes(self, state: CompactKVSequenceState, live_per_head: list[int]) -> list[int]:
         return [max(min(int(x) + int(state.decode_headroom), state.max_capacity_per_lh), 1) for x in live_per_head]
@@ -453,14 +473,23 @@ class CompactKVManager:
         # host first-fit allocation, all sequences of the batch (reference order)
         all_bases, all_sizes = [], []
         high_water = 0
-        for i, st in enumerate(states):
-            if lens[i] > 0:
-                bases, sizes = self._alloc_layer_ranges_host(st, layer_id, live_host[i])
-            else:
-                bases, sizes = [-1] * H, [0] * H
-            all_bases.append(bases)
-            all_sizes.append(sizes)
-            high_water = max(high_water, max(b + s for b, s in zip(bases, sizes)))
+        try:
+            for i, st in enumerate(states):
+                if lens[i] > 0:
+                    bases, sizes = self._alloc_layer_ranges_host(st, layer_id, live_host[i])
+                else:
+                    bases, sizes = [-1] * H, [0] * H
+                all_bases.append(bases)
+                all_sizes.append(sizes)
+                high_water = max(high_water, max(b + s for b, s in zip(bases, sizes)))
+        except CompactCapacityExhausted:
+            # this layer's ranges of the earlier sequences are not recorded in
+            # their states yet: give them back before the caller frees the rest
+            for bases, sizes in zip(all_bases, all_sizes):
+                for b, n in zip(bases, sizes):
+                    if b >= 0 and n > 0:
+                        self._free_range(layer_id, b, n)
+            raise
             if lens[i] > 0 and max(live_host[i]) > st.max_capacity_per_lh:
                 raise RuntimeError(f"streaming pack live count {max(live_host[i])} exceeds metadata capacity "
                                    f"{st.max_capacity_per_lh} (layer {layer_id}, seq {st.seq_id})")
@@ -507,11 +536,104 @@ class CompactKVManager:
         for i, st in enumerate(states):
             if lens[i] > 0:
                 st.live_upper_bound = max(st.live_upper_bound, max(live_host[i]))
+                st.decode_slack = min(st.decode_slack, min(sz - lv for sz, lv in zip(all_sizes[i], live_host[i])))
 
     def _meta_rows(self, states) -> torch.Tensor | None:
         if not self.layer_major_metadata:
             return None
         return torch.tensor([st.active_slot for st in states], dtype=torch.int32).to(self.device, non_blocking=True)
+
+    # -- decode growth of overcommitted spans (a build extension) ----------------
+    def decode_room_needed(self, seq: Sequence) -> bool:
+        """True when some (layer, head) span of ``seq`` has no free row for the
+        next decode append.  Host-only while the slack bound allows; otherwise
+        one small device->host copy of the sequence's live counts refreshes the
+        bounds (expiry may have freed rows)."""
+        st = self.seq_states[seq.seq_id]
+        if st.decode_slack >= 1:
+            return False
+        live = st.live_counts.cpu()
+        cap = st.range_capacity.cpu()
+        st.decode_slack = int((cap - live).min())
+        st.live_upper_bound = int(live.max())
+        return st.decode_slack < 1
+
+    def grow_for_decode(self, seq: Sequence) -> None:
+        """Move every full (layer, head) span of ``seq`` to a new range of
+        live + the decode reserve rows (first fit), copying its K / V rows; the
+        rank-indexed positions / evict metadata do not move.  Raises
+        CompactCapacityExhausted when a layer has no such range (spans moved
+        before that stay valid)."""
+        st = self.seq_states[seq.seq_id]
+        live = st.live_counts.cpu().tolist()
+        cap = st.range_capacity.cpu().tolist()
+        base = st.base_offsets.cpu().tolist()
+        try:
+            for layer_id in range(self.num_layers):
+                ck, cv = self._layer_arena(layer_id)
+                for h in range(self.num_kv_heads):
+                    n, old_base, old_size = int(live[layer_id][h]), int(base[layer_id][h]), int(cap[layer_id][h])
+                    if old_size - n >= 1:
+                        continue
+                    new_size = min(n + max(int(st.decode_headroom), 1), st.max_capacity_per_lh)
+                    if new_size <= old_size:
+                        raise RuntimeError(f"sequence {seq.seq_id} reached its metadata capacity "
+                                           f"{st.max_capacity_per_lh} in layer {layer_id}")
+                    new_base = self._alloc_range(layer_id, new_size)
+                    if n:
+                        ck[new_base:new_base + n].copy_(ck[old_base:old_base + n])
+                        cv[new_base:new_base + n].copy_(cv[old_base:old_base + n])
+                    self._free_range(layer_id, old_base, old_size)
+                    self.num_span_moves += 1
+                    st.base_offsets[layer_id, h] = new_base
+                    st.range_capacity[layer_id, h] = new_size
+                    base[layer_id][h], cap[layer_id][h] = new_base, new_size
+        finally:
+            st.decode_slack = min(int(c) - int(v) for cr, lr in zip(cap, live) for c, v in zip(cr, lr))
+
+    def _bind_slot_views(self, state: CompactKVSequenceState, slot: int) -> None:
+        cap = state.max_capacity_per_lh
+        state.active_slot = slot
+        state.base_offsets = self.layer_major_base_offsets[:, slot, :]
+        state.range_capacity = self.layer_major_range_capacity[:, slot, :]
+        state.live_counts = self.layer_major_live_counts[:, slot, :]
+        state.token_positions = self.layer_major_token_positions[:, slot, :, :cap]
+        state.evict_mask = self.layer_major_evict_mask[:, slot, :, :cap]
+
+    def pack_active_slots(self, states) -> None:
+        """Move the layer-major metadata rows of ``states`` (every active
+        sequence, in decode order) to slots 0 .. len-1 in that order, so one
+        decode launch covers them.  Sequences that finish or are preempted leave
+        holes; the reference then processes the batch sequence by sequence
+        (compact_kv.py:1162-1172), this build moves the rows (5 small device
+        copies per moved sequence) and keeps one launch.  Spans, arenas and the
+        allocator are untouched."""
+        if not self.layer_major_metadata:
+            return
+        if len(states) != len(self.active_slot_by_seq):
+            raise RuntimeError("slot packing needs every active sequence in the batch")
+        tensors = (self.layer_major_base_offsets, self.layer_major_range_capacity, self.layer_major_live_counts,
+                   self.layer_major_token_positions, self.layer_major_evict_mask)
+        fills = (-1, 0, 0, -1, False)
+        target = {st.seq_id: i for i, st in enumerate(states)}
+        moving = [st for st in states if st.active_slot != target[st.seq_id]]
+        if not moving:
+            return
+        # rows of the moving sequences are copied out first, so cycles need no
+        # staging slot; vacated slots that nobody moves into are reset
+        saved = {st.seq_id: [t[:, st.active_slot].clone() for t in tensors] for st in moving}
+        vacated = {st.active_slot for st in moving} - {target[st.seq_id] for st in moving}
+        for st in moving:
+            new = target[st.seq_id]
+            for t, rows in zip(tensors, saved[st.seq_id]):
+                t[:, new].copy_(rows)
+            self._bind_slot_views(st, new)
+            self.active_slot_by_seq[st.seq_id] = new
+        for slot in vacated:
+            for t, f in zip(tensors, fills):
+                t[:, slot].fill_(f)
+        used = set(self.active_slot_by_seq.values())
+        self.free_active_slots = [i for i in range(self.max_active_seqs) if i not in used]
 
     def _contiguous_active_slot_start(self, states) -> int | None:
         """compact_kv.py:1162-1172."""

@@ -6,6 +6,7 @@ from dataclasses import fields
 
 from ..config import Config
 from ..sampling_params import SamplingParams
+from .compact_kv import CompactCapacityExhausted
 from .model_runner import ModelRunner
 from .scheduler import Scheduler
 from .sequence import Sequence
@@ -28,10 +29,69 @@ class LLMEngine:
         self.scheduler.add(seq)
         return seq
 
+    def _free_preempted(self) -> None:
+        freed = self.scheduler.consume_freed_seq_ids()
+        if freed:
+            self.model_runner.free_compact(freed)
+
+    def _run_prefill_admitting(self, seqs):
+        """Run a prefill batch; when its compact spans do not fit, preempt
+        running sequences (compact_admission="preempt") or defer the batch.
+        Returns (the sequences prefilled, their sampled tokens), or (None, None)
+        when the batch was deferred."""
+        while True:
+            try:
+                return seqs, self.model_runner.run(seqs, True)
+            except CompactCapacityExhausted:
+                self.model_runner.free_compact([s.seq_id for s in seqs])  # spans of the failed attempt
+                victim = None
+                if self.config.compact_admission == "preempt":
+                    victim = self.scheduler.preemption_victim(seqs)
+                if victim is not None:
+                    self.scheduler.preempt(victim)
+                    self._free_preempted()
+                    continue
+                if len(seqs) > 1:  # retry the head of the batch alone, the rest waits
+                    self.scheduler.defer_prefill(seqs[1:])
+                    self.scheduler.admission_blocked = False
+                    seqs = seqs[:1]
+                    continue
+                if not any(s is not seqs[0] for s in self.scheduler.running):
+                    raise  # nothing runs that could free space: the request never fits
+                self.scheduler.defer_prefill(seqs)
+                return None, None
+
+    def _make_decode_room(self, seqs):
+        """Before a decode step: grow the full spans of overcommitted sequences
+        (oldest first), preempting the youngest running sequence -- possibly
+        the one that needs room -- when no range is free.  Returns the batch
+        without the preempted sequences."""
+        mgr = self.model_runner.compact_kv_manager
+        for seq in sorted(seqs, key=lambda s: s.seq_id):
+            while seq in self.scheduler.running and mgr.decode_room_needed(seq):
+                try:
+                    mgr.grow_for_decode(seq)
+                except CompactCapacityExhausted:
+                    victim = self.scheduler.preemption_victim([seq], include_self=True)
+                    self.scheduler.preempt(victim)
+                    self._free_preempted()
+        return [s for s in seqs if s in self.scheduler.running]
+
     def step(self):
         seqs, is_prefill = self.scheduler.schedule()
         t0 = time.perf_counter()
-        token_ids = self.model_runner.run(seqs, is_prefill)
+        if is_prefill:
+            done, token_ids = self._run_prefill_admitting(seqs)
+            if done is None:  # deferred: run a decode step of the running batch instead
+                seqs, is_prefill = self.scheduler.schedule()
+                if is_prefill:
+                    raise RuntimeError("prefill admission is paused but the scheduler chose a prefill")
+            else:
+                seqs = done
+        if not is_prefill:
+            if self.config.compact_decode_reserve_tokens is not None:
+                seqs = self._make_decode_room(seqs)
+            token_ids = self.model_runner.run(seqs, False) if seqs else []
         dt = time.perf_counter() - t0
         self.scheduler.postprocess(seqs, token_ids, is_prefill)
         freed = self.scheduler.consume_freed_seq_ids()

@@ -137,7 +137,8 @@ class ModelRunner:
             max_model_len=c.max_model_len, device=self.device,
             target_live_tokens_per_seq=c.compact_kv_target_live_tokens_per_seq, head_dim=self.head_dim,
             compact_dtype=self.kv_dtype, per_layer_storage=True, layer_major_metadata=True,
-            max_active_seqs=self.max_num_seqs, preallocate=True)
+            max_active_seqs=self.max_num_seqs, preallocate=True,
+            decode_reserve_tokens=c.compact_decode_reserve_tokens)
         attn_modules = []
         for layer_id, layer in enumerate(self.model.model.layers):
             layer.self_attn.attn.layer_id = layer_id
@@ -161,7 +162,10 @@ class ModelRunner:
         cu_t = torch.tensor(cu, dtype=torch.int32, pin_memory=True).to(self.device, non_blocking=True)
         pack_ids = []
         for seq in seqs:
-            if min(seq.num_cached_tokens + seq.num_scheduled_tokens, seq.num_tokens) < seq.num_tokens:
+            done = min(seq.num_cached_tokens + seq.num_scheduled_tokens, seq.num_tokens)
+            # a re-prefill after preemption stops one token short: the next
+            # decode step appends the last token
+            if done < seq.num_tokens and not (seq.reprefill and done == seq.num_tokens - 1):
                 raise NotImplementedError("chunked DMS prefill is not supported (the reference packs only "
                                           "completed prompts, model_runner.py:652-659)")
             self.compact_kv_manager.allocate(seq)
@@ -176,7 +180,11 @@ class ModelRunner:
     @torch.inference_mode()
     def run_prefill(self, seqs: list[Sequence]) -> list[int]:
         ids, pos = self.prepare_prefill(seqs)
-        hidden = self.model(ids, pos)
+        try:
+            hidden = self.model(ids, pos)
+        except BaseException:
+            reset_context()  # e.g. CompactCapacityExhausted from a layer's pack: the engine frees and retries
+            raise
         head = self.model.lm_head
         if self.config.fused_greedy_head:
             tokens = self.model.compute_greedy_token_ids(hidden)
@@ -254,6 +262,9 @@ class ModelRunner:
         mgr = self.compact_kv_manager
         batch = len(seqs)
         positions = [len(seq) - 1 for seq in seqs]
+        # finished / preempted sequences leave holes in the layer-major slots:
+        # move the batch's rows to slots 0 .. batch-1 (one launch per step)
+        mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
         stats = mgr.apply_dms_evictions(seqs, positions, window_size=self.dms_metadata.window_size, sync_stats=False)
         self.last_dms_decode_stats = [dict(stats, phase="expire")]
         states = [mgr.seq_states[s.seq_id] for s in seqs]
@@ -262,6 +273,7 @@ class ModelRunner:
             raise RuntimeError("decode batch must occupy contiguous active slots")
         for st in states:
             st.live_upper_bound += 1
+            st.decode_slack -= 1
         hint = self.attention_hint(seqs)
         for i, seq in enumerate(seqs):
             self.pinned_ids[i] = seq.last_token

@@ -35,6 +35,10 @@ class Sequence:
         self.temperature = sampling_params.temperature
         self.max_tokens = sampling_params.max_tokens
         self.ignore_eos = sampling_params.ignore_eos
+        # set when a preempted sequence with generated tokens waits for its
+        # re-prefill: every token but the last is prefilled again, and the
+        # next decode step appends the last one
+        self.reprefill = False
 
     def __len__(self):
         return self.num_tokens
