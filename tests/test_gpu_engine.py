@@ -217,3 +217,54 @@ def test_quantized_weights_graph_equals_eager(monkeypatch, env):
         del llm
         torch.cuda.synchronize()
     assert outs[0] == outs[1] == outs[2]
+
+
+@pytest.mark.parametrize("admission,reserve,cap", [("defer", None, 260), ("preempt", 4, 300)])
+def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, cap):
+    """Capped compact KV on the GPU (graphs on): deferred prefills, spans that
+    grow during decode and preempted sequences re-admitted by re-prefill.  Every
+    request completes, every span returns to the allocator, a rerun is token-
+    for-token identical (deterministic across preemptions), and the tokens each
+    sequence produced before its first preemption equal an uncapped run's."""
+    require_gpu()
+    from fastdms_amd import LLM, SamplingParams
+    monkeypatch.setenv("FASTDMS_DMS_EXPIRY_TRITON", "1")
+    monkeypatch.setenv("FASTDMS_DMS_EXPIRY_INTERVAL", "1")
+    gen = 30
+
+    def run(capped):
+        llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096,
+                  fused_greedy_head=True, compact_kv_capacity_tokens=cap if capped else 0,
+                  compact_admission=admission, compact_decode_reserve_tokens=reserve if capped else None, **DMS)
+        rng = np.random.default_rng(11)
+        sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+        seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in (300, 200)]
+        for _ in range(5):
+            llm.step()
+        seqs.append(llm.add_request(rng.integers(0, 512, 160).tolist(), sp))
+        steps = 0
+        while not llm.is_finished():
+            llm.step()
+            steps += 1
+            assert steps < 400, "the engine stopped making progress"
+        mgr = llm.model_runner.compact_kv_manager
+        assert not mgr.seq_states and mgr.free_tokens == mgr.capacity_tokens * mgr.num_layers
+        first = {}
+        for sid, g in llm.scheduler.preemption_log:
+            first.setdefault(sid, g)
+        out = ([list(s.completion_token_ids) for s in seqs], [first.get(s.seq_id, gen) for s in seqs],
+               llm.scheduler.num_deferrals, mgr.num_span_moves)
+        llm.exit()
+        torch.cuda.synchronize()
+        return out
+
+    toks, first, deferrals, moves = run(True)
+    assert all(len(t) == gen for t in toks)
+    if admission == "defer":
+        assert deferrals >= 1 and all(g == gen for g in first)
+    else:
+        assert any(g < gen for g in first) and moves >= 1
+    assert run(True)[0] == toks
+    free_toks = run(False)[0]
+    for t, f, g in zip(toks, free_toks, first):
+        assert t[:g] == f[:g]
