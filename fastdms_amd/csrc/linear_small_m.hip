@@ -363,7 +363,44 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   Buf cur, nxt;
   if (kw0 < kend) load(kw0, cur);  // the first weight group is in flight during the stats pass
 
-  if (PRO == 1 || QX) {
+  if (PRO == 0 && QX) {
+    // per-row 448/amax of x: the whole workgroup reads every row at once,
+    // thread t the 8-column chunks t, t + NT, ... (one pass of loads, then a
+    // wave reduction per row and one across the waves)
+    constexpr int NT = NW * 64;
+    __shared__ float s_am[kMaxM][NW];
+    float am[kMaxM];
+#pragma unroll
+    for (int mm = 0; mm < kMaxM; ++mm) am[mm] = 0.0f;
+    for (int c = tid * 8; c < K; c += NT * 8) {
+      uint4 xv[kMaxM];
+#pragma unroll
+      for (int mm = 0; mm < kMaxM; ++mm)
+        xv[mm] = *reinterpret_cast<const uint4*>(x + (int64_t)min(mm, M - 1) * x_s + c);  // clamped row
+#pragma unroll
+      for (int mm = 0; mm < kMaxM; ++mm) {
+        const uint32_t w4[4] = {xv[mm].x, xv[mm].y, xv[mm].z, xv[mm].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) am[mm] = fmaxf(am[mm], fmaxf(fabsf(bf_lo(w4[i])), fabsf(bf_hi(w4[i]))));
+      }
+    }
+#pragma unroll
+    for (int mm = 0; mm < kMaxM; ++mm) {
+      if (mm >= M) break;
+      const float w = wave_max(am[mm]);
+      if (lane == 0) s_am[mm][wave] = w;
+    }
+    __syncthreads();
+    if (tid < M) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) a = fmaxf(a, s_am[tid][w2]);
+      // 448 / amax: the Triton kernels divide; torch's tensor expression
+      // (_fp8_linear) multiplies the reciprocal of amax by 448 (two roundings)
+      s_xs[tid] = a > 0.0f ? (qx_torch ? (1.0f / a) * kFp8Max : kFp8Max / a) : 1.0f;
+    }
+    __syncthreads();
+  } else if (PRO == 1 || QX) {
     for (int m = wave; m < M; m += NW) {
       float inv, xs;
       row_stats<PRO, QX>(x + (int64_t)m * x_s, (PRO == 1 && res) ? res + (int64_t)m * res_s : nullptr, norm_w, K,
@@ -538,7 +575,9 @@ struct LinArgs {
 template <typename WT, int PRO, bool QX, int EPI>
 void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   const WT* w = (const WT*)a.w;
-  constexpr int U = (PRO == 1 || QX) ? 2 : 4;  // k-blocks per double-buffered group (register budget)
+  // k-blocks per double-buffered group (register budget: the RMSNorm prologue
+  // also holds the residual and norm weight of each k-block)
+  constexpr int U = PRO == 1 ? 2 : 4;
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
                       a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
                       a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores
