@@ -14,6 +14,8 @@ and one device->host copy of the token ids.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from .. import _native as nat
@@ -99,6 +101,12 @@ class ModelRunner:
         self.last_compact_prefill_stats: dict = {}
         self.last_dms_decode_stats: list = []
         self.compact_live_tokens_peak = 0
+        fp8 = getattr(torch, "float8_e4m3fn", None)
+        group = hf.num_attention_heads // hf.num_key_value_heads
+        self._static_attention_bound = (
+            os.environ.get("FASTDMS_AMD_ATTN_MFMA", "1").strip() != "0"
+            and os.environ.get("FASTDMS_AMD_ATTN_GENERIC", "0").strip() != "1"
+            and self.kv_dtype == fp8 and group <= 4 and hf.head_dim in (64, 128))
 
     # -- setup -----------------------------------------------------------------
     def _dms_metadata(self) -> DMSMetadata:
@@ -251,10 +259,16 @@ class ModelRunner:
 
     def attention_hint(self, seqs: list[Sequence]) -> int:
         """Bound on the live count of every (layer, seq, kv head) of the batch,
-        which sets the attention split count.  It is the host's upper bound
-        rounded up to the next 256-token bucket, so eager and graph-replayed
-        steps use the same split count (bit-identical results) and one graph
-        serves up to 256 steps."""
+        which sets the attention split count.  On the matrix-core path a pair's
+        split count follows its own live count and the bound only caps it, so
+        the static bound max_model_len serves every step (one decode graph per
+        batch shape, never recaptured as the spans grow).  Other kernels split
+        evenly by the bound: there it is the host's upper bound rounded up to
+        the next 256-token bucket, so eager and graph-replayed steps use the
+        same split count (bit-identical results) and one graph serves up to
+        256 steps."""
+        if self._static_attention_bound:
+            return (self.config.max_model_len // 256 + 1) * 256
         return (self.compact_kv_manager.max_live_upper_bound(seqs) // 256 + 1) * 256
 
     @torch.inference_mode()
@@ -301,7 +315,7 @@ class ModelRunner:
             self.model.lm_head.last_logits = entry[3]
         else:
             self.model.lm_head.last_logits = self._decode_body(start, batch, hint)
-        self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, hint)
+        self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
         return self.static_tokens[:batch].tolist()
 
     def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
