@@ -506,6 +506,9 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+    # the engine steps one token at a time here (value); the device-side
+    # greedy loop is timed separately on the same batch (decode_fast_loop)
+    os.environ.setdefault("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
     import numpy as np
     import torch
     from fastdms_amd import LLM, SamplingParams
@@ -554,6 +557,17 @@ def main():
     dt = time.perf_counter() - t0
     value = args.batch * args.steps / dt
     progress(f"decode {value:.1f} tok/s")
+    fast = None
+    left = min(s.max_tokens - s.num_completion_tokens for s in seqs)
+    if left >= 8:  # the device-side greedy loop over the rest of the generation
+        progress(f"greedy fast loop, {left} steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        llm.model_runner.run_compact_greedy_decode_loop(seqs, left)
+        fast_dt = time.perf_counter() - t0
+        fast = {"tok_s": round(args.batch * left / fast_dt, 2), "ms_per_step": round(fast_dt / left * 1e3, 4),
+                "steps": left}
+        progress(f"fast loop {fast['tok_s']:.1f} tok/s")
     cpu = None
     if not args.no_cpu_baseline:  # before the roofline replays re-append rows
         progress("cpu baseline")
@@ -574,6 +588,7 @@ def main():
                    "model": args.model, "global_batch": args.batch, "seq_len": int(max(lens)),
                    "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager},
         "prefill_tok_s": round(sum(lens) / prefill_s, 1),
+        "decode_fast_loop": fast,
         "roofline": roof,
         "roofline_scaling": scaling,
         "compaction_roofline": pack,

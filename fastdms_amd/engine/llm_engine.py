@@ -7,9 +7,9 @@ from dataclasses import fields
 from ..config import Config
 from ..sampling_params import SamplingParams
 from .compact_kv import CompactCapacityExhausted
-from .model_runner import ModelRunner
+from .model_runner import ModelRunner, compact_greedy_fast_loop_enabled
 from .scheduler import Scheduler
-from .sequence import Sequence
+from .sequence import Sequence, SequenceStatus
 
 
 class LLMEngine:
@@ -94,6 +94,7 @@ class LLMEngine:
             token_ids = self.model_runner.run(seqs, False) if seqs else []
         dt = time.perf_counter() - t0
         self.scheduler.postprocess(seqs, token_ids, is_prefill)
+        fast = self._greedy_fast_loop(seqs) if is_prefill else None
         freed = self.scheduler.consume_freed_seq_ids()
         if freed:
             self.model_runner.free_compact(freed)
@@ -101,8 +102,35 @@ class LLMEngine:
         num_tokens = sum(seq.num_scheduled_tokens or len(seq) for seq in seqs) if is_prefill else len(seqs)
         if is_prefill:
             num_tokens = sum(len(s.prompt_token_ids) for s in seqs)
-        self.last_step_stats = {"is_prefill": is_prefill, "seconds": dt, "tokens": num_tokens}
+        self.last_step_stats = {"is_prefill": is_prefill, "seconds": dt, "tokens": num_tokens, "fast_loop": fast}
         return outputs, (num_tokens if is_prefill else -len(seqs))
+
+    def _greedy_fast_loop(self, seqs):
+        """llm_engine.py:55-74: a lone greedy ignore_eos sequence that has just
+        been prefilled decodes its whole tail in one device-side loop.  Besides
+        the reference's conditions it must be the only running sequence (the
+        loop packs the active slots) and hold its full span reservation.
+        Returns {"tokens", "seconds"} of the loop, or None when not taken."""
+        cfg = self.config
+        if not (compact_greedy_fast_loop_enabled() and len(seqs) == 1 and list(self.scheduler.running) == seqs
+                and cfg.fused_greedy_head and cfg.compact_decode_cudagraph and not cfg.enforce_eager
+                and cfg.compact_decode_reserve_tokens is None):
+            return None
+        seq = seqs[0]
+        if not (seq.temperature <= 1e-10 and seq.ignore_eos and seq.status == SequenceStatus.RUNNING
+                and seq.num_cached_tokens == seq.num_tokens):
+            return None
+        remaining = seq.max_tokens - seq.num_completion_tokens
+        if remaining <= 0:
+            return None
+        t0 = time.perf_counter()
+        self.model_runner.run_compact_greedy_decode_loop([seq], remaining)
+        dt = time.perf_counter() - t0
+        if seq.is_finished:
+            self.scheduler.freed_seq_ids.append(seq.seq_id)
+            self.scheduler.running.remove(seq)
+            self.scheduler.admission_blocked = False
+        return {"tokens": remaining, "seconds": dt}
 
     def is_finished(self) -> bool:
         return self.scheduler.is_finished()

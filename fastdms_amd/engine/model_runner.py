@@ -27,7 +27,12 @@ from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
 from .compact_kv import CompactKVManager
 from .dms import DMSMetadata, load_dms_metadata
-from .sequence import Sequence
+from .sequence import Sequence, SequenceStatus
+
+
+def compact_greedy_fast_loop_enabled() -> bool:
+    """FASTDMS_COMPACT_GREEDY_FAST_LOOP (default on), model_runner.py:30-32."""
+    return os.environ.get("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "1").strip().lower() not in ("0", "false", "no", "off")
 
 
 def convert_model_weights(model) -> tuple[int, bool, bool]:
@@ -272,13 +277,11 @@ class ModelRunner:
         return (self.compact_kv_manager.max_live_upper_bound(seqs) // 256 + 1) * 256
 
     @torch.inference_mode()
-    def run_decode(self, seqs: list[Sequence]) -> list[int]:
+    def _begin_decode_step(self, seqs: list[Sequence], positions: list[int]) -> tuple[int, int]:
+        """Host side of one decode step: the expiry launch the policy picks for
+        these positions and the live bounds; returns (start slot, attention
+        bound).  The batch occupies slots start .. start + len - 1."""
         mgr = self.compact_kv_manager
-        batch = len(seqs)
-        positions = [len(seq) - 1 for seq in seqs]
-        # finished / preempted sequences leave holes in the layer-major slots:
-        # move the batch's rows to slots 0 .. batch-1 (one launch per step)
-        mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
         stats = mgr.apply_dms_evictions(seqs, positions, window_size=self.dms_metadata.window_size, sync_stats=False)
         self.last_dms_decode_stats = [dict(stats, phase="expire")]
         states = [mgr.seq_states[s.seq_id] for s in seqs]
@@ -288,16 +291,17 @@ class ModelRunner:
         for st in states:
             st.live_upper_bound += 1
             st.decode_slack -= 1
-        hint = self.attention_hint(seqs)
-        for i, seq in enumerate(seqs):
-            self.pinned_ids[i] = seq.last_token
-            self.pinned_pos[i] = positions[i]
-        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
-        self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
+        return start, self.attention_hint(seqs)
+
+    def _replay_decode(self, start: int, batch: int, hint: int) -> None:
+        """One decode step on the static buffers: the captured graph of this
+        batch shape (captured on its second use; the first runs eagerly so the
+        library GEMMs pick their kernels outside capture)."""
+        mgr = self.compact_kv_manager
         use_graph = self.config.compact_decode_cudagraph and not self.config.enforce_eager
         key = (start, batch)
         if use_graph and key not in self._warm:
-            self._warm.add(key)  # first step of a shape runs eagerly: library GEMMs pick kernels outside capture
+            self._warm.add(key)
             use_graph = False
         if use_graph:
             entry = self.graphs.get(key)
@@ -315,8 +319,73 @@ class ModelRunner:
             self.model.lm_head.last_logits = entry[3]
         else:
             self.model.lm_head.last_logits = self._decode_body(start, batch, hint)
+
+    @torch.inference_mode()
+    def run_decode(self, seqs: list[Sequence]) -> list[int]:
+        mgr = self.compact_kv_manager
+        batch = len(seqs)
+        positions = [len(seq) - 1 for seq in seqs]
+        # finished / preempted sequences leave holes in the layer-major slots:
+        # move the batch's rows to slots 0 .. batch-1 (one launch per step)
+        mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
+        start, hint = self._begin_decode_step(seqs, positions)
+        for i, seq in enumerate(seqs):
+            self.pinned_ids[i] = seq.last_token
+            self.pinned_pos[i] = positions[i]
+        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+        self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
+        self._replay_decode(start, batch, hint)
         self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
         return self.static_tokens[:batch].tolist()
+
+    @torch.inference_mode()
+    def run_compact_greedy_decode_loop(self, seqs: list[Sequence], max_steps: int):
+        """Greedy decode of ``max_steps`` tokens for the batch with no host
+        sync between steps (model_runner.py:971-1053, which does batch size 1):
+        each step's sampled ids feed the next step on the device, positions come
+        from a pinned host table filled up front, the expiry policy is decided
+        on the host from the positions alone, and one copy of all the tokens
+        ends the loop.  Requires the fused greedy head, ignore_eos sequences
+        (no EOS check until the end) and the full span reservation.  Returns
+        the tokens of a single sequence (the reference's form) or one list per
+        sequence."""
+        if max_steps <= 0:
+            return [] if len(seqs) == 1 else [[] for _ in seqs]
+        if not self.config.fused_greedy_head:
+            raise RuntimeError("compact greedy fast loop requires the fused greedy argmax path")
+        if self.config.compact_decode_reserve_tokens is not None:
+            raise RuntimeError("compact greedy fast loop requires the full decode reservation")
+        if any(not s.ignore_eos or s.temperature > 0 for s in seqs):
+            raise RuntimeError("compact greedy fast loop requires greedy, ignore_eos sequences")
+        if any(s.num_completion_tokens + max_steps > s.max_tokens for s in seqs):
+            raise RuntimeError("compact greedy fast loop would run past max_tokens")
+        mgr = self.compact_kv_manager
+        batch = len(seqs)
+        mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
+        base_pos = [len(seq) - 1 for seq in seqs]
+        pos_table = torch.tensor([[p + step for p in base_pos] for step in range(max_steps)], dtype=torch.int64,
+                                 pin_memory=True)
+        for i, seq in enumerate(seqs):
+            self.pinned_ids[i] = seq.last_token
+        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+        tokens = torch.empty((max_steps, batch), device=self.device, dtype=torch.int64)
+        for step in range(max_steps):
+            start, hint = self._begin_decode_step(seqs, pos_table[step].tolist())
+            self.static_positions[:batch].copy_(pos_table[step], non_blocking=True)
+            if step:
+                self.static_input_ids[:batch].copy_(self.static_tokens[:batch])
+            self._replay_decode(start, batch, hint)
+            tokens[step].copy_(self.static_tokens[:batch])
+        out = tokens.t().contiguous().cpu().tolist()  # the loop's one host sync
+        for seq, toks in zip(seqs, out):
+            for t in toks:
+                seq.append_token(t)
+                seq.num_cached_tokens += 1
+            seq.num_scheduled_tokens = 0
+            if seq.num_completion_tokens >= seq.max_tokens:
+                seq.status = SequenceStatus.FINISHED
+        self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
+        return out[0] if batch == 1 else out
 
     def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
         return self.run_prefill(seqs) if is_prefill else self.run_decode(seqs)

@@ -84,3 +84,94 @@ def _run(model, lens, gen, fused_head):
                 assert np.abs(got - want).max() <= 2, f"live counts at step {step}: {got} vs {want}"
         assert "fdms_dms_expiry" in emu.calls
         llm.exit()
+
+
+@pytest.mark.parametrize("lens,gen", [([300], 14), ([300, 64, 517], 10)])
+def test_greedy_fast_loop_matches_the_oracle_tokens(lens, gen):
+    """The device-side greedy loop (model_runner.py:971-1053) takes the whole
+    decode tail after prefill: its tokens are the oracle's greedy tokens, the
+    sequences end FINISHED with consistent counters, and their compact state
+    follows the oracle's."""
+    from oracle.model import OracleModel, weights_from_model
+    with cpu_engine():
+        from fastdms_amd import LLM, SamplingParams
+        from fastdms_amd.engine.sequence import SequenceStatus
+        llm = LLM("tiny-llama", max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384,
+                  enforce_eager=True, fused_greedy_head=True, **DMS)
+        runner = llm.model_runner
+        orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
+                          alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
+                          max_model_len=llm.config.max_model_len)
+        rng = np.random.default_rng(5)
+        sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+        seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in lens]
+        llm.step()
+        ids = [s.seq_id for s in seqs]
+        want = [[int(t)] for t in orc.prefill([(s.seq_id, s.prompt_token_ids, gen) for s in seqs])]
+        assert [s.completion_token_ids for s in seqs] == want, "prefill tokens"
+        got = runner.run_compact_greedy_decode_loop(seqs, gen - 1)
+        if len(seqs) == 1:
+            got = [got]
+        for _ in range(gen - 1):
+            toks = orc.decode(ids, [w[-1] for w in want], [len(s.prompt_token_ids) + len(w) - 1
+                                                             for s, w in zip(seqs, want)])
+            for w, t in zip(want, toks):
+                w.append(int(t))
+        assert [w[1:] for w in want] == got
+        mgr = runner.compact_kv_manager
+        for s, w in zip(seqs, want):
+            assert s.completion_token_ids == w and s.last_token == w[-1]
+            assert s.status == SequenceStatus.FINISHED and s.num_cached_tokens == s.num_tokens
+            live = np.array(mgr.seq_states[s.seq_id].live_counts.tolist())
+            o_live = np.array(orc.mgr.seq_states[s.seq_id].live_counts.tolist())
+            assert (live[0] == o_live[0]).all() and np.abs(live - o_live).max() <= 2
+        with pytest.raises(RuntimeError, match="max_tokens"):
+            runner.run_compact_greedy_decode_loop(seqs, 1)
+        llm.exit()
+
+
+def test_engine_takes_the_greedy_fast_loop_only_for_a_lone_greedy_sequence(monkeypatch):
+    """llm_engine.py:55-74: after a prefill, a lone greedy ignore_eos sequence
+    (the only one running) hands its decode tail to the device-side loop, which
+    finishes it and frees its compact state.  The loop itself is stubbed here
+    (graph replay is GPU-only); its tokens are pinned by the test above."""
+    with cpu_engine():
+        from fastdms_amd import LLM, SamplingParams
+        from fastdms_amd.engine.sequence import SequenceStatus
+        llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096,
+                  enforce_eager=True, fused_greedy_head=True, **DMS)
+        calls = []
+
+        def loop(seqs, n):
+            calls.append((list(seqs), n))
+            for s in seqs:
+                for _ in range(n):
+                    s.append_token(7)
+                    s.num_cached_tokens += 1
+                s.status = SequenceStatus.FINISHED
+            return [7] * n
+
+        monkeypatch.setattr(llm.model_runner, "run_compact_greedy_decode_loop", loop)
+        llm.config.enforce_eager = False  # the reference takes the loop only with decode graphs
+        greedy = SamplingParams(temperature=0.0, max_tokens=9, ignore_eos=True)
+        a = llm.add_request(list(range(40)), greedy)
+        outputs, _ = llm.step()
+        assert calls == [([a], 8)] and a.is_finished and outputs == [(a.seq_id, a.completion_token_ids)]
+        assert a.seq_id not in llm.model_runner.compact_kv_manager.seq_states and llm.is_finished()
+        assert llm.last_step_stats["fast_loop"]["tokens"] == 8
+        # not taken: two sequences prefilled together, a sampled sequence, or the switch off
+        for prompts, sp, env in (([list(range(30)), list(range(50))], greedy, "1"),
+                                 ([list(range(30))], SamplingParams(temperature=0.7, max_tokens=9, ignore_eos=True),
+                                  "1"),
+                                 ([list(range(30))], greedy, "0")):
+            monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", env)
+            calls.clear()
+            for p in prompts:
+                llm.add_request(p, sp)
+            llm.step()  # the prefill, with the gate evaluated under decode graphs
+            assert calls == [] and llm.last_step_stats["fast_loop"] is None
+            llm.config.enforce_eager = True  # decode steps run eagerly on the CPU
+            while not llm.is_finished():
+                llm.step()
+            llm.config.enforce_eager = False
+        llm.exit()

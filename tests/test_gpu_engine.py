@@ -179,6 +179,43 @@ def test_fused_greedy_head_equals_logits_argmax(model, lens):
     assert outs[0] == outs[1]
 
 
+@pytest.mark.parametrize("lens", [[1500], [300, 517, 800, 64]])
+def test_greedy_fast_loop_equals_per_step_decode(monkeypatch, lens):
+    """The device-side greedy loop (model_runner.py:971-1053) gives the tokens
+    of per-step graph decode.  A lone sequence takes it from the engine step
+    after its prefill (llm_engine.py:55-74); a batch calls it on the runner."""
+    require_gpu()
+    from fastdms_amd import SamplingParams
+    rng = np.random.default_rng(8)
+    prompts = _prompts(rng, lens, 512)
+    gen = 48
+    sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+    monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
+    llm = _llm("tiny-llama")
+    want = [o["token_ids"] for o in llm.generate(prompts, sp)]
+    llm.exit()
+    del llm
+    torch.cuda.synchronize()
+    monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "1")
+    llm = _llm("tiny-llama")
+    if len(lens) == 1:
+        got = [o["token_ids"] for o in llm.generate(prompts, sp)]
+        assert llm.last_step_stats["fast_loop"] == {"tokens": gen - 1,
+                                                    "seconds": llm.last_step_stats["fast_loop"]["seconds"]}
+    else:
+        seqs = [llm.add_request(p, sp) for p in prompts]
+        llm.step()
+        assert llm.last_step_stats["fast_loop"] is None
+        first = [s.completion_token_ids[0] for s in seqs]
+        tail = llm.model_runner.run_compact_greedy_decode_loop(seqs, gen - 1)
+        got = [[f] + t for f, t in zip(first, tail)]
+        assert all(s.is_finished for s in seqs)
+    assert got == want
+    llm.exit()
+    del llm
+    torch.cuda.synchronize()
+
+
 _QUANT_ENVS = {
     "fp8_all": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "1"},
     "fp8_mlp_int4": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "mlp_lm_head",
