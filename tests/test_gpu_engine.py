@@ -267,6 +267,9 @@ def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, ca
     from fastdms_amd import LLM, SamplingParams
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_TRITON", "1")
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_INTERVAL", "1")
+    # a sequence admitted alone would otherwise finish inside its prefill step
+    # (the greedy fast loop), and no decode would meet a deferred admission
+    monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
     gen = 30
 
     def run(capped):
