@@ -45,6 +45,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_argmax_rows": "pillipp",
     "fdms_mfma_probe": "pppp",
     "fdms_prefill_attention": "pllpllpllpllpiiiiifp",
+    "fdms_prefill_attention_varlen": "pllpllpllpllppiiiiifp",
     "fdms_rmsnorm": "pllippplplifp",
     "fdms_silu_mul": "pplip",
     "fdms_rmsnorm_partials": "pilppplplifp",

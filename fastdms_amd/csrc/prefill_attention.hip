@@ -1,6 +1,9 @@
 // Dense causal prefill attention over a ragged batch (the reference calls
-// flash_attn_varlen_func(q, k, v, cu_seqlens, causal=True), attention.py:85-92:
-// evictions act only at pack time, so prefill attends to the full prompt).
+// flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, causal=True),
+// attention.py:85-92: evictions act only at pack time, so prefill attends to
+// the full prompt).  A sequence's query rows are the last of its keys
+// (flash-attn's bottom-right causal alignment): a chunk of a long prompt
+// attends to the retained earlier chunks plus itself.
 //
 // bf16 in/out, fp32 softmax, GQA.  One workgroup = 64 query rows of one query
 // head (4 waves x 16 rows); key/value blocks of 64 tokens are staged in LDS
@@ -67,7 +70,8 @@ template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
     const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
     int64_t ks_h, const bf16_t* __restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t* __restrict__ out, int64_t os_t,
-    int64_t os_h, const int32_t* __restrict__ cu_seqlens, int group, float scale_log2) {
+    int64_t os_h, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int group,
+    float scale_log2) {
   constexpr int KPAD = D + 8;       // sK row stride (bf16)
   constexpr int VPAD = kKeys + 8;   // sVt row stride (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t sK[kKeys * KPAD];
@@ -76,8 +80,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
   const int seq = blockIdx.z;
   const int qh = blockIdx.y;
   const int kvh = qh / group;
-  const int start = cu_seqlens[seq];
-  const int len = cu_seqlens[seq + 1] - start;
+  // query rows are the last qlen of the sequence's klen keys (bottom-right
+  // causal alignment): row i is position off + i and sees keys 0 .. off + i
+  const int start = cu_q[seq];
+  const int len = cu_q[seq + 1] - start;
+  const int kstart = cu_k[seq];
+  const int klen = cu_k[seq + 1] - kstart;
+  const int off = klen - len;
+  if (off < 0) return;  // rejected: more queries than keys
   const int nqb = (len + kQRows - 1) / kQRows;
   if ((int)blockIdx.x >= nqb) return;
   const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest (diagonal-last) blocks first
@@ -104,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nkb = min((len + kKeys - 1) / kKeys, qb + 1);
+  const int nkb = min((klen + kKeys - 1) / kKeys, (off + q0 + kQRows - 1) / kKeys + 1);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * kKeys;
     __syncthreads();
@@ -113,9 +123,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
       const int key = u / (D / 8);
       const int d0 = (u - key * (D / 8)) * 8;
       uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (k0 + key < len) {
-        kv = *reinterpret_cast<const uint4*>(k + (int64_t)(start + k0 + key) * ks_t + (int64_t)kvh * ks_h + d0);
-        vv = *reinterpret_cast<const uint4*>(v + (int64_t)(start + k0 + key) * vs_t + (int64_t)kvh * vs_h + d0);
+      if (k0 + key < klen) {
+        kv = *reinterpret_cast<const uint4*>(k + (int64_t)(kstart + k0 + key) * ks_t + (int64_t)kvh * ks_h + d0);
+        vv = *reinterpret_cast<const uint4*>(v + (int64_t)(kstart + k0 + key) * vs_t + (int64_t)kvh * vs_h + d0);
       }
       *reinterpret_cast<uint4*>(&sK[key * KPAD + d0]) = kv;
       const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vv);
@@ -137,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = k0 + 16 * t + 4 * lg + r;
-        const bool ok = key <= my_q && key < len;
+        const bool ok = key <= off + my_q && key < klen;
         s[t][r] = ok ? acc[r] * scale_log2 : -INFINITY;
       }
     }
@@ -224,7 +234,7 @@ template <int D, int G>
 __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
     int64_t ks_h, const bf16_t* __restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t* __restrict__ out, int64_t os_t,
-    int64_t os_h, const int32_t* __restrict__ cu_seqlens, float scale_log2) {
+    int64_t os_h, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, float scale_log2) {
   constexpr int P = 128 / G;        // query positions per workgroup
   constexpr int KPAD = D + 8;       // sK row stride (bf16)
   // sVt row stride (bf16): 136 B = 34 dwords, so the 16 lanes of one 8-byte
@@ -238,8 +248,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
 
   const int seq = blockIdx.z;
   const int kvh = blockIdx.y;
-  const int start = cu_seqlens[seq];
-  const int len = cu_seqlens[seq + 1] - start;
+  // query rows are the last len of the klen keys (bottom-right causal
+  // alignment, as the per-head kernel); positions below are query rows
+  const int start = cu_q[seq];
+  const int len = cu_q[seq + 1] - start;
+  const int kstart = cu_k[seq];
+  const int klen = cu_k[seq + 1] - kstart;
+  const int off = klen - len;
+  if (off < 0) return;  // rejected: more queries than keys
   const int nqb = (len + P - 1) / P;
   if ((int)blockIdx.x >= nqb) return;
   const int q0 = (nqb - 1 - (int)blockIdx.x) * P;  // heaviest (diagonal-last) blocks first
@@ -262,8 +278,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     for (int j = 0; j < D / 32; ++j) qop[qt][j] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 * j + 8 * lg));
   }
 
-  const bf16_t* kb_base = k + (int64_t)start * ks_t + (int64_t)kvh * ks_h;
-  const bf16_t* vb_base = v + (int64_t)start * vs_t + (int64_t)kvh * vs_h;
+  const bf16_t* kb_base = k + (int64_t)kstart * ks_t + (int64_t)kvh * ks_h;
+  const bf16_t* vb_base = v + (int64_t)kstart * vs_t + (int64_t)kvh * vs_h;
   uint4 stage[UPT][4];
   // unit u < 2D: V quad (keys 4*(u % 16) .. +3, dims 8*(u / 16) .. +7: the 16
   // lanes of a row store 128 contiguous bytes of one transposed row);
@@ -289,12 +305,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     }
   }
   auto load_block = [&](int k0) {
-    const bool tail = k0 + kKeys > len;  // uniform
+    const bool tail = k0 + kKeys > klen;  // uniform
 #pragma unroll
     for (int i = 0; i < UPT; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = tail ? min(k0 + krow[i][r], len - 1) : k0 + krow[i][r];
+        const int key = tail ? min(k0 + krow[i][r], klen - 1) : k0 + krow[i][r];
         stage[i][r] = *reinterpret_cast<const uint4*>(kvp[i] + (int64_t)key * kvs[i] + koff[i][r]);
       }
   };
@@ -336,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     for (int c = 0; c <= D / 16; ++c) o[qt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16x8 ones = as_bf16x8(uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
-  const int kend = min(len, q0 + P);  // keys 0 .. kend-1 are visible to some row of the workgroup
+  const int kend = min(klen, off + q0 + P);  // keys 0 .. kend-1 are visible to some row of the workgroup
   const int nkb = (kend + kKeys - 1) / kKeys;
   load_block(0);
   store_block(0);
@@ -346,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     const int buf = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) load_block(k0 + kKeys);
-    if (k0 <= wq_last) {  // wave-uniform: this block holds keys visible to the wave
+    if (k0 <= off + wq_last) {  // wave-uniform: this block holds keys visible to the wave
       f32x4 acc[2][4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -358,9 +374,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
           acc[1][t] = mfma16x16x32(a, qop[1][j], acc[1][t]);
         }
       }
-      const bool masked = k0 + kKeys - 1 > wq0 || k0 + kKeys > len;  // wave-uniform
+      const bool masked = k0 + kKeys - 1 > off + wq0 || k0 + kKeys > klen;  // wave-uniform
       if (masked) {
-        const int lim0 = min(my_q0, len - 1), lim1 = min(my_q1, len - 1);
+        const int lim0 = off + min(my_q0, len - 1), lim1 = off + min(my_q1, len - 1);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -442,24 +458,27 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   }
 }
 
-FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t,
-                                       int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h, void* out,
-                                       int64_t os_t, int64_t os_h, const int32_t* cu_seqlens, int num_seqs,
-                                       int max_seqlen, int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                                       void* stream) {
+FDMS_EXPORT int fdms_prefill_attention_varlen(const void* q, int64_t qs_t, int64_t qs_h, const void* k,
+                                              int64_t ks_t, int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h,
+                                              void* out, int64_t os_t, int64_t os_h, const int32_t* cu_seqlens_q,
+                                              const int32_t* cu_seqlens_k, int num_seqs, int max_seqlen_q,
+                                              int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                                              void* stream) {
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return (int)hipErrorInvalidValue;
-  if (num_seqs == 0 || max_seqlen <= 0) return 0;
-  if (!q || !k || !v || !out || !cu_seqlens) return (int)hipErrorInvalidValue;
+  if (num_seqs == 0 || max_seqlen_q <= 0) return 0;
+  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k) return (int)hipErrorInvalidValue;
   if (num_seqs > 65535 || num_q_heads > 65535) return (int)hipErrorInvalidValue;
   const float sl2 = scale * 1.4426950408889634f;
   const int group = num_q_heads / num_kv_heads;
+  const int32_t* cq = cu_seqlens_q;
+  const int32_t* ck = cu_seqlens_k;
   if ((group == 1 || group == 2 || group == 4) && (head_dim == 64 || head_dim == 128) &&
       fdms_prefill_gqa_enabled()) {
-    const dim3 ggrid((max_seqlen + 128 / group - 1) / (128 / group), num_kv_heads, num_seqs);
+    const dim3 ggrid((max_seqlen_q + 128 / group - 1) / (128 / group), num_kv_heads, num_seqs);
 #define FDMS_PREFILL_GQA(DD, GG)                                                                                   \
   hipLaunchKernelGGL((prefill_attn_gqa_kernel<DD, GG>), ggrid, dim3(kThreads), 0, (hipStream_t)stream,              \
                      (const bf16_t*)q, qs_t, qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h,       \
-                     (bf16_t*)out, os_t, os_h, cu_seqlens, sl2)
+                     (bf16_t*)out, os_t, os_h, cq, ck, sl2)
     if (head_dim == 64) {
       if (group == 1) FDMS_PREFILL_GQA(64, 1); else if (group == 2) FDMS_PREFILL_GQA(64, 2); else FDMS_PREFILL_GQA(64, 4);
     } else {
@@ -469,20 +488,30 @@ FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h
     FDMS_LAUNCH_CHECK();
     return 0;
   }
-  const dim3 grid((max_seqlen + kQRows - 1) / kQRows, num_q_heads, num_seqs);
+  const dim3 grid((max_seqlen_q + kQRows - 1) / kQRows, num_q_heads, num_seqs);
   if (head_dim == 64) {
     hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)q, qs_t,
                        qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h, (bf16_t*)out, os_t, os_h,
-                       cu_seqlens, group, sl2);
+                       cq, ck, group, sl2);
   } else if (head_dim == 128) {
     hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)q,
                        qs_t, qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h, (bf16_t*)out, os_t,
-                       os_h, cu_seqlens, group, sl2);
+                       os_h, cq, ck, group, sl2);
   } else {
     return (int)hipErrorInvalidValue;
   }
   FDMS_LAUNCH_CHECK();
   return 0;
+}
+
+FDMS_EXPORT int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t,
+                                       int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h, void* out,
+                                       int64_t os_t, int64_t os_h, const int32_t* cu_seqlens, int num_seqs,
+                                       int max_seqlen, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                                       void* stream) {
+  return fdms_prefill_attention_varlen(q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu_seqlens,
+                                       cu_seqlens, num_seqs, max_seqlen, num_q_heads, num_kv_heads, head_dim, scale,
+                                       stream);
 }
 
 // One v_mfma_f32_16x16x32_bf16 of a 16x32 A and a 32x16 B (row-major bf16)

@@ -25,6 +25,7 @@ from ..layers import quant_env as qe
 from ..layers.linear import convert_linear_modules_to_fp8, reserve_linear_workspace
 from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
+from .chunked_prefill import ChunkPlan, PromptStage
 from .compact_kv import CompactKVManager
 from .dms import DMSMetadata, load_dms_metadata
 from .sequence import Sequence, SequenceStatus
@@ -98,6 +99,7 @@ class ModelRunner:
         self.static_slot = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads), device=self.device,
                                        dtype=torch.int32)
         self.static_tokens = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        self.prompt_stages: dict[int, PromptStage] = {}  # long prompts between their chunks
         self.pinned_ids = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         self.graphs: dict[tuple, tuple] = {}
@@ -174,21 +176,53 @@ class ModelRunner:
         pos_t = torch.tensor(positions, dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
         cu_t = torch.tensor(cu, dtype=torch.int32, pin_memory=True).to(self.device, non_blocking=True)
         pack_ids = []
-        for seq in seqs:
-            done = min(seq.num_cached_tokens + seq.num_scheduled_tokens, seq.num_tokens)
+        chunk = None
+        for i, seq in enumerate(seqs):
             # a re-prefill after preemption stops one token short: the next
             # decode step appends the last token
-            if done < seq.num_tokens and not (seq.reprefill and done == seq.num_tokens - 1):
-                raise NotImplementedError("chunked DMS prefill is not supported (the reference packs only "
-                                          "completed prompts, model_runner.py:652-659)")
+            target = seq.num_tokens - 1 if seq.reprefill else seq.num_tokens
+            start = seq.num_cached_tokens
+            done = min(start + seq.num_scheduled_tokens, target)
+            if start > 0 or done < target:  # a chunk of a prompt longer than the step's budget
+                if i != 0:
+                    raise RuntimeError("only the first sequence of a prefill batch may be chunked")
+                chunk = self._plan_chunk(seq, start, seq.num_scheduled_tokens, target)
+                if chunk.final:
+                    self.compact_kv_manager.allocate(seq)
+                continue
             self.compact_kv_manager.allocate(seq)
             pack_ids.append(seq.seq_id)
+        if chunk is not None:
+            rest = cu[1:]
+            chunk.rest_ids = pack_ids
+            chunk.cu_rest_host = [c - chunk.rows for c in rest]
+            chunk.max_rest = max((rest[j + 1] - rest[j] for j in range(len(rest) - 1)), default=0)
+            chunk.cu_rest = (torch.tensor(chunk.cu_rest_host, dtype=torch.int32, pin_memory=True)
+                             .to(self.device, non_blocking=True)) if pack_ids else None
+            pack_ids = pack_ids + ([chunk.seq_id] if chunk.final else [])
         md = self.dms_metadata
         set_context(True, cu_t, cu_t, max_q, max_q, dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale,
                     dms_alpha_offset=md.alpha_offset, dms_layer_evictions={},
                     streaming_pack_manager=self.compact_kv_manager, streaming_pack_seq_ids=pack_ids,
-                    streaming_pack_window_size=md.window_size, cu_seqlens_q_host=cu)
+                    streaming_pack_window_size=md.window_size, cu_seqlens_q_host=cu, prefill_chunk=chunk)
         return ids_t, pos_t
+
+    def _plan_chunk(self, seq: Sequence, start: int, rows: int, target: int) -> ChunkPlan:
+        """The stage and launch metadata of one chunk of a long prompt: the
+        prompt's dense stage is made at its first chunk (a restarted prompt,
+        e.g. a re-prefill, starts a new one) and must hold exactly the chunks
+        before this one."""
+        stage = self.prompt_stages.get(seq.seq_id)
+        if start == 0 or stage is None or stage.total != target:
+            stage = PromptStage(self.num_layers, target, self.num_kv_heads, self.head_dim, self.device)
+            self.prompt_stages[seq.seq_id] = stage
+        if stage.filled != start or start + rows > target:
+            raise RuntimeError(f"prompt chunk {start}..{start + rows} of seq {seq.seq_id} does not follow the "
+                               f"{stage.filled} staged tokens")
+        end = start + rows
+        dev = lambda v: torch.tensor(v, dtype=torch.int32, pin_memory=True).to(self.device, non_blocking=True)
+        return ChunkPlan(seq.seq_id, stage, start, rows, end == target, dev([0, rows]), dev([0, end]), [], None,
+                         None, 0)
 
     @torch.inference_mode()
     def run_prefill(self, seqs: list[Sequence]) -> list[int]:
@@ -211,7 +245,12 @@ class ModelRunner:
         ctx = get_context()
         total = sum(e.numel() for e in ctx.dms_layer_evictions.values())
         true = sum(e.sum() for e in ctx.dms_layer_evictions.values())
+        chunk = ctx.prefill_chunk
         reset_context()
+        if chunk is not None:  # the chunk is staged; a completed prompt is packed and its stage dropped
+            chunk.stage.filled = chunk.end
+            if chunk.final:
+                self.prompt_stages.pop(chunk.seq_id, None)
         out = tokens.tolist()
         self.last_compact_prefill_stats = {"eviction_decisions_total": total,
                                            "eviction_decisions_true": int(true) if total else 0}

@@ -71,9 +71,11 @@ class Scheduler:
                 seq.num_cached_tokens = min(seq.num_cached_tokens + seq.num_scheduled_tokens, seq.num_tokens)
                 if seq.num_cached_tokens < seq.num_tokens or seq.num_completion_tokens > 0:
                     # chunked prefill, or re-prefill after preemption (its sampled
-                    # token is dropped: the next decode step recomputes it)
+                    # token is dropped: the next decode step recomputes it); a
+                    # re-prefill stays one until its last chunk
                     seq.num_scheduled_tokens = 0
-                    seq.reprefill = False
+                    if seq.num_cached_tokens >= seq.num_tokens - 1:
+                        seq.reprefill = False
                     continue
             seq.append_token(token_id)
             seq.num_cached_tokens += 1

@@ -18,8 +18,12 @@ from .compact_attention import (compact_decode_attention, fused_dms_rope_store_c
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
-                      max_seqlen: int, scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Causal varlen attention: q [T, Hq, D], k/v [T, Hkv, D] bf16 -> [T, Hq, D]."""
+                      max_seqlen: int, scale: float, out: torch.Tensor | None = None,
+                      cu_seqlens_k: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal varlen attention: q [T, Hq, D], k/v [Tk, Hkv, D] bf16 -> [T, Hq, D].
+    With ``cu_seqlens_k`` a sequence's queries are the last of its keys
+    (bottom-right causal alignment, flash_attn_varlen_func's): a prompt chunk
+    attending to the retained earlier chunks and itself."""
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("prefill attention expects bf16 q/k/v")
     t, hq, d = q.shape
@@ -32,9 +36,17 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seql
     if out is None:
         out = torch.empty((t, hq, d), device=q.device, dtype=q.dtype)
     cu = cu_seqlens.to(torch.int32)
-    nat.call("fdms_prefill_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+    if cu_seqlens_k is None:
+        nat.call("fdms_prefill_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                 k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                 cu.data_ptr(), cu.numel() - 1, int(max_seqlen), hq, hkv, d, float(scale), nat.stream())
+        return out
+    cuk = cu_seqlens_k.to(torch.int32)
+    if cuk.numel() != cu.numel():
+        raise ValueError("cu_seqlens and cu_seqlens_k must describe the same sequences")
+    nat.call("fdms_prefill_attention_varlen", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
              k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
-             cu.data_ptr(), cu.numel() - 1, int(max_seqlen), hq, hkv, d, float(scale), nat.stream())
+             cu.data_ptr(), cuk.data_ptr(), cu.numel() - 1, int(max_seqlen), hq, hkv, d, float(scale), nat.stream())
     return out
 
 

@@ -14,6 +14,7 @@ from dataclasses import dataclass, field
 import torch
 from torch import nn
 
+from ..engine.chunked_prefill import attend_and_pack
 from ..engine.dms import extract_dms_eviction_decisions
 from ..layers.activation import silu_and_mul
 from ..layers.attention import Attention
@@ -119,6 +120,7 @@ class LlamaAttention(nn.Module):
         ctx = get_context()
         fused = False
         inline_q_rope = False
+        evict_mask = None
         layer_id = self.attn.layer_id
         if ctx.dms_capture_enabled:
             can_fuse = (dms_fused_decode_preprocess_enabled() and not ctx.is_prefill and ctx.compact_kv_enabled
@@ -163,6 +165,9 @@ class LlamaAttention(nn.Module):
                 ctx.dms_layer_evictions[layer_id] = evict_mask
         if not fused:
             q, k = self.rotary_emb(positions, q, k)
+        if ctx.is_prefill and ctx.prefill_chunk is not None:  # a long prompt's chunk over its retained prefix
+            o = attend_and_pack(self.attn, layer_id, q, k, v, evict_mask, ctx, self.attn.scale)
+            return o.view(o.shape[0], -1)
         if (ctx.is_prefill and ctx.streaming_pack_manager is not None and ctx.streaming_pack_seq_ids
                 and ctx.dms_capture_enabled):
             ctx.streaming_pack_manager.streaming_pack_layer(

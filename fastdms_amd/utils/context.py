@@ -35,6 +35,8 @@ class Context:
     streaming_pack_window_size: int = 0
     # host copy of cu_seqlens_q (saves a device sync in the streaming pack)
     cu_seqlens_q_host: list | None = None
+    # a chunk of a long prompt in this prefill batch (engine.chunked_prefill.ChunkPlan)
+    prefill_chunk: object | None = None
 
 
 _CONTEXT = Context()
@@ -49,13 +51,14 @@ def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0
                 compact_base_offsets=None, compact_live_counts=None, compact_slot_mapping=None,
                 compact_max_live_count=0, dms_capture_enabled=False, dms_alpha_scale=100.0, dms_alpha_offset=5.0,
                 dms_layer_evictions=None, dms_layer_evictions_buffer=None, streaming_pack_manager=None,
-                streaming_pack_seq_ids=None, streaming_pack_window_size=0, cu_seqlens_q_host=None) -> None:
+                streaming_pack_seq_ids=None, streaming_pack_window_size=0, cu_seqlens_q_host=None,
+                prefill_chunk=None) -> None:
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping,
                        context_lens, block_tables, compact_kv_enabled, compact_base_offsets, compact_live_counts,
                        compact_slot_mapping, compact_max_live_count, dms_capture_enabled, dms_alpha_scale,
                        dms_alpha_offset, dms_layer_evictions, dms_layer_evictions_buffer, streaming_pack_manager,
-                       streaming_pack_seq_ids, streaming_pack_window_size, cu_seqlens_q_host)
+                       streaming_pack_seq_ids, streaming_pack_window_size, cu_seqlens_q_host, prefill_chunk)
 
 
 def reset_context() -> None:

@@ -211,6 +211,21 @@ int fdms_prefill_attention(const void* q, int64_t qs_t, int64_t qs_h, const void
                            const int32_t* cu_seqlens, int num_seqs, int max_seqlen, int num_q_heads,
                            int num_kv_heads, int head_dim, float scale, void* stream);
 
+/* B1 with separate query and key ranges (the reference's
+ * flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, causal=True),
+ * attention.py:85-92): sequence s has query rows cu_seqlens_q[s] ..
+ * cu_seqlens_q[s+1]-1 of q / out and keys cu_seqlens_k[s] .. cu_seqlens_k[s+1]-1
+ * of k / v, the queries being the last of the keys (bottom-right causal
+ * alignment: query i of n attends to keys 0 .. klen - n + i).  A chunk of a
+ * long prompt passes the retained earlier chunks' K/V plus its own.  Needs
+ * klen >= qlen for every sequence (a sequence with fewer keys than queries is
+ * skipped and its rows are not written); max_seqlen_q bounds the grid. */
+int fdms_prefill_attention_varlen(const void* q, int64_t qs_t, int64_t qs_h, const void* k, int64_t ks_t,
+                                  int64_t ks_h, const void* v, int64_t vs_t, int64_t vs_h, void* out, int64_t os_t,
+                                  int64_t os_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads, int head_dim,
+                                  float scale, void* stream);
+
 /* One v_mfma_f32_16x16x32_bf16 with the operand layout the attention kernels
  * assume (no reference counterpart: a lane-layout self-check for tests). */
 int fdms_mfma_probe(const void* a, const void* b, float* c, void* stream);

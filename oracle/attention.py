@@ -197,12 +197,17 @@ def compact_decode_attention_paged(q, kv_k, kv_v, block_tables, live_counts, pag
     return out
 
 
-def causal_prefill_attention(q, k, v, cu_seqlens, scale=None):
+def causal_prefill_attention(q, k, v, cu_seqlens, scale=None, cu_seqlens_k=None):
     """Dense causal softmax attention per sequence (attention.py:85-92;
-    flash_attn_varlen_func semantics with causal=True, q_len == k_len).
+    flash_attn_varlen_func semantics with causal=True).
 
-    q [T, Hq, D], k/v [T, Hkv, D] float values; returns float64 [T, Hq, D].
+    q [T, Hq, D], k/v [Tk, Hkv, D] float values; returns float64 [T, Hq, D].
+    With cu_seqlens_k the sequence's queries are the last of its keys
+    (flash-attn's bottom-right alignment: query i of n sees keys 0 ..
+    klen - n + i); without it q_len == k_len.
     """
+    if cu_seqlens_k is not None:
+        return _causal_prefill_varlen(q, k, v, cu_seqlens, cu_seqlens_k, scale)
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -223,4 +228,29 @@ def causal_prefill_attention(q, k, v, cu_seqlens, scale=None):
             s = s - s.max(axis=1, keepdims=True)
             p = np.exp(s)
             out[s0:s1, qh] = (p @ v[s0:s1, h]) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+def _causal_prefill_varlen(q, k, v, cu_q, cu_k, scale):
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    hq, d = q.shape[1], q.shape[2]
+    g = hq // k.shape[1]
+    scale = d ** -0.5 if scale is None else scale
+    out = np.zeros_like(q)
+    cq, ck = [int(x) for x in cu_q], [int(x) for x in cu_k]
+    for i in range(len(cq) - 1):
+        s0, s1, k0, k1 = cq[i], cq[i + 1], ck[i], ck[i + 1]
+        n, nk = s1 - s0, k1 - k0
+        if nk < n:
+            raise ValueError("a sequence has fewer keys than queries")
+        mask = np.tril(np.ones((n, nk), dtype=bool), nk - n)
+        for qh in range(hq):
+            h = qh // g
+            sc = q[s0:s1, qh] @ k[k0:k1, h].T * scale
+            sc = np.where(mask, sc, -np.inf)
+            sc = sc - sc.max(axis=1, keepdims=True)
+            p = np.exp(sc)
+            out[s0:s1, qh] = (p @ v[k0:k1, h]) / p.sum(axis=1, keepdims=True)
     return out

@@ -735,26 +735,35 @@ class Emulator:
 
     def prefill_attention(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, num_seqs,
                           max_seqlen, hq, hkv, d, scale, stream):
+        return self.prefill_attention_varlen(q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, cu,
+                                             num_seqs, max_seqlen, hq, hkv, d, scale, stream)
+
+    def prefill_attention_varlen(self, q, qs_t, qs_h, k, ks_t, ks_h, v, vs_t, vs_h, out, os_t, os_h, cu, cuk,
+                                 num_seqs, max_seqlen, hq, hkv, d, scale, stream):
+        """Causal softmax in float64, queries aligned to the end of their keys."""
         if num_seqs == 0 or max_seqlen <= 0:
             return 0
-        c = self.view(cu, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens").tolist()
-        t = c[-1]
+        c = self.view(cu, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens_q").tolist()
+        ck = self.view(cuk, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens_k").tolist()
+        t, tk = c[-1], ck[-1]
         if max(c[i + 1] - c[i] for i in range(num_seqs)) > max_seqlen:
             raise OutOfBounds(f"{self.name}: a sequence is longer than max_seqlen (rows would be skipped)")
+        if any(ck[i + 1] - ck[i] < c[i + 1] - c[i] for i in range(num_seqs)):
+            raise OutOfBounds(f"{self.name}: a sequence has fewer keys than queries")
         qv = self.view(q, torch.bfloat16, (t, hq, d), (qs_t, qs_h, 1), "q").float()
-        kv_ = self.view(k, torch.bfloat16, (t, hkv, d), (ks_t, ks_h, 1), "k").float()
-        vv = self.view(v, torch.bfloat16, (t, hkv, d), (vs_t, vs_h, 1), "v").float()
+        kv_ = self.view(k, torch.bfloat16, (tk, hkv, d), (ks_t, ks_h, 1), "k").float()
+        vv = self.view(v, torch.bfloat16, (tk, hkv, d), (vs_t, vs_h, 1), "v").float()
         ov = self.view(out, torch.bfloat16, (t, hq, d), (os_t, os_h, 1), "out")
         g = hq // hkv
         res = torch.empty((t, hq, d), dtype=torch.float32)
         for i in range(num_seqs):
-            s0, s1 = c[i], c[i + 1]
-            n = s1 - s0
-            mask = torch.ones(n, n, dtype=torch.bool).tril()
+            s0, s1, k0, k1 = c[i], c[i + 1], ck[i], ck[i + 1]
+            n, nk = s1 - s0, k1 - k0
+            mask = torch.ones(n, nk, dtype=torch.bool).tril(nk - n)
             for h in range(hq):
-                sc = (qv[s0:s1, h].double() @ kv_[s0:s1, h // g].double().T) * scale
+                sc = (qv[s0:s1, h].double() @ kv_[k0:k1, h // g].double().T) * scale
                 sc = sc.masked_fill(~mask, float("-inf"))
-                res[s0:s1, h] = (torch.softmax(sc, -1) @ vv[s0:s1, h // g].double()).float()
+                res[s0:s1, h] = (torch.softmax(sc, -1) @ vv[k0:k1, h // g].double()).float()
         ov.copy_(res.to(torch.bfloat16))
         return 0
 

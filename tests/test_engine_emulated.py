@@ -175,3 +175,77 @@ def test_engine_takes_the_greedy_fast_loop_only_for_a_lone_greedy_sequence(monke
                 llm.step()
             llm.config.enforce_eager = False
         llm.exit()
+
+
+def _generate(lens, gen, budget, seed=9, max_model_len=2048):
+    """Greedy generation of random prompts with a per-step token budget."""
+    from fastdms_amd import LLM, SamplingParams
+    llm = LLM("tiny-llama", max_model_len=max_model_len, max_num_seqs=4, max_num_batched_tokens=budget,
+              enforce_eager=True, fused_greedy_head=True, **DMS)
+    rng = np.random.default_rng(seed)
+    sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+    seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in lens]
+    while not llm.is_finished():
+        llm.step()
+    return llm, [list(s.completion_token_ids) for s in seqs]
+
+
+@pytest.mark.parametrize("budget", [128, 200])
+def test_chunked_prefill_equals_the_unchunked_prefill(budget):
+    """Prompts longer than the step's token budget are prefilled in chunks
+    over a dense-retained prefix (each chunk attends to the staged earlier
+    chunks plus itself; the completing chunk packs the whole prompt).  The
+    reference's semantics are dense causal attention over the whole prompt
+    with evictions at pack time (attention.py:85-92), so the generation must
+    equal the unchunked one token for token, and the first tokens the CPU
+    model oracle's."""
+    from oracle.model import OracleModel, weights_from_model
+    lens, gen = [300, 517, 64], 6
+    with cpu_engine() as emu:
+        llm_c, chunked = _generate(lens, gen, budget)
+        assert emu.calls.count("fdms_prefill_attention_varlen") > 0
+        assert not llm_c.model_runner.prompt_stages, "stages of completed prompts are dropped"
+        runner = llm_c.model_runner
+        orc = OracleModel(weights_from_model(runner.model), llm_c.config.hf_config, window_size=32,
+                          alpha_scale=10.0, alpha_offset=5.0, capacity_tokens=1 << 16,
+                          max_model_len=llm_c.config.max_model_len)
+        rng = np.random.default_rng(9)
+        prompts = [rng.integers(0, 512, n).tolist() for n in lens]
+        first = orc.prefill([(i, p, gen) for i, p in enumerate(prompts)])
+        assert [t[0] for t in chunked] == [int(x) for x in first]
+        llm_c.exit()
+        llm_u, whole = _generate(lens, gen, 4096)
+        llm_u.exit()
+    assert chunked == whole
+
+
+def test_chunked_prefill_state_equals_the_unchunked_state():
+    """After a chunked prefill the compact state (live counts, token
+    positions, FP8 rows of every span) is the unchunked prefill's, byte for
+    byte."""
+    from fastdms_amd import LLM, SamplingParams
+    states = []
+    with cpu_engine():
+        for budget in (96, 4096):
+            llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=2, max_num_batched_tokens=budget,
+                      enforce_eager=True, fused_greedy_head=True, **DMS)
+            sp = SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True)
+            seq = llm.add_request(np.random.default_rng(2).integers(0, 512, 333).tolist(), sp)
+            while seq.num_completion_tokens == 0:
+                llm.step()
+            mgr = llm.model_runner.compact_kv_manager
+            st = mgr.seq_states[seq.seq_id]
+            live = st.live_counts.clone()
+            rows = []
+            for layer in range(mgr.num_layers):
+                for h in range(mgr.num_kv_heads):
+                    b, n = int(st.base_offsets[layer, h]), int(live[layer, h])
+                    rows.append((mgr.compact_k_per_layer[layer][b:b + n].view(torch.uint8).clone(),
+                                 mgr.compact_v_per_layer[layer][b:b + n].view(torch.uint8).clone(),
+                                 st.token_positions[layer, h, :n].clone()))
+            states.append((live, rows, seq.completion_token_ids[0]))
+            llm.exit()
+    (lc, rc, tc), (lu, ru, tu) = states
+    assert torch.equal(lc, lu) and tc == tu
+    for (kc, vc, pc), (ku, vu, pu) in zip(rc, ru):
+        assert torch.equal(kc, ku) and torch.equal(vc, vu) and torch.equal(pc, pu)

@@ -216,6 +216,43 @@ def test_greedy_fast_loop_equals_per_step_decode(monkeypatch, lens):
     torch.cuda.synchronize()
 
 
+def test_chunked_prefill_matches_the_unchunked_prefill():
+    """A prompt longer than the step's token budget, prefilled in chunks over
+    its dense-retained prefix: the prefill logits equal the unchunked
+    prefill's to bf16 noise, layer 0's compact live counts match exactly (its
+    decisions see only the embedding) and deeper layers within a decision or
+    two; generation then runs to completion from the chunked state."""
+    require_gpu()
+    from fastdms_amd import LLM, SamplingParams
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, 512, 1500).tolist()
+    sp = SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True)
+    res = []
+    for budget in (256, 4096):
+        llm = LLM("tiny-llama", max_model_len=2048, max_num_seqs=2, max_num_batched_tokens=budget,
+                  fused_greedy_head=False, **DMS)
+        seq = llm.add_request(prompt, sp)
+        steps = 0
+        while seq.num_completion_tokens == 0:
+            llm.step()
+            steps += 1
+        logits = llm.model_runner.model.lm_head.last_logits.float().cpu()
+        live = llm.model_runner.compact_kv_manager.seq_states[seq.seq_id].live_counts.cpu().clone()
+        while not llm.is_finished():
+            llm.step()
+        res.append((steps, logits, live, len(seq.completion_token_ids)))
+        assert not llm.model_runner.prompt_stages
+        llm.exit()
+        del llm
+        torch.cuda.synchronize()
+    (sc, lc, vc, nc), (su, lu, vu, nu) = res
+    assert sc == 6 and su == 1, "1500 tokens in 256-token chunks"
+    scale = max(1.0, float(lu.abs().max()))
+    assert float((lc - lu).abs().max()) <= 2e-2 * scale
+    assert torch.equal(vc[0], vu[0]) and int((vc - vu).abs().max()) <= 2
+    assert nc == nu == 24
+
+
 _QUANT_ENVS = {
     "fp8_all": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "1"},
     "fp8_mlp_int4": {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "mlp_lm_head",

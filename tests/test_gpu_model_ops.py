@@ -163,6 +163,44 @@ def test_prefill_attention_vs_oracle(d, lens, hq, hkv, ramp):
     assert np.mean(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
 
 
+@pytest.mark.parametrize("d,lens,cuts,hq,hkv", [
+    (64, [300, 517, 64], [128, 100, 0], 8, 2),     # G = 4, prefix a multiple of 64 / not / none
+    (128, [700, 129], [511, 128], 8, 2),
+    (64, [1500, 90], [1499, 37], 4, 4),           # G = 1, a one-row chunk
+    (128, [400], [3], 8, 4),                      # G = 2
+    (64, [333, 200], [200, 1], 6, 2),             # G = 3 (per-head kernel)
+])
+def test_prefill_attention_chunk_over_retained_prefix(d, lens, cuts, hq, hkv):
+    """A prompt chunk attending to the retained earlier chunks plus itself
+    (flash_attn_varlen_func with cu_seqlens_k, queries aligned to the end of
+    the keys): equal to the oracle's varlen form, and to the same rows of the
+    unchunked prefill to bf16 rounding."""
+    require_gpu()
+    from fastdms_amd.layers.attention import prefill_attention
+    rng = np.random.default_rng(d + hq + sum(cuts))
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    t = int(cu[-1])
+    q = _bf16(rng.standard_normal((t, hq, d)).astype(np.float32))
+    k = _bf16(rng.standard_normal((t, hkv, d)).astype(np.float32))
+    v = _bf16(rng.standard_normal((t, hkv, d)).astype(np.float32))
+    rows = np.concatenate([np.arange(cu[i] + cuts[i], cu[i + 1]) for i in range(len(lens))])
+    cq = np.concatenate([[0], np.cumsum([n - c for n, c in zip(lens, cuts)])]).astype(np.int32)
+    qc = q[torch.from_numpy(rows)].contiguous()
+    want = oatt.causal_prefill_attention(qc.float().numpy(), k.float().numpy(), v.float().numpy(), cq,
+                                         cu_seqlens_k=cu)
+    out = prefill_attention(qc.cuda(), k.cuda(), v.cuda(), torch.from_numpy(cq).cuda(),
+                            int(max(n - c for n, c in zip(lens, cuts))), d ** -0.5,
+                            cu_seqlens_k=torch.from_numpy(cu).cuda())
+    full = prefill_attention(q.cuda(), k.cuda(), v.cuda(), torch.from_numpy(cu).cuda(), max(lens), d ** -0.5)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err <= 2e-2, f"max-abs-rel error {err:.3g}"
+    assert np.mean(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
+    same = np.abs(got - full.float().cpu().numpy()[rows])
+    assert np.mean(same <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
+
+
 def test_prepare_decode_metadata_strided_slot_output():
     """slot_out as a [:, :B] view of a wider [L, max_seqs, H] buffer (the decode
     graph's static buffer): only the view's elements are written."""

@@ -77,6 +77,28 @@ def test_causal_prefill_matches_torch_sdpa():
         np.testing.assert_allclose(out[s0:s1], ref.numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_chunked_prefill_rows_equal_the_full_prompt_rows():
+    """A chunk's queries aligned to the end of their keys (the retained
+    earlier chunks + the chunk) give the same rows as the unchunked causal
+    attention over the whole prompt; a wrong alignment offset fails."""
+    rng = np.random.default_rng(3)
+    lens = [23, 40, 9]
+    hq, hkv, d = 4, 2, 16
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    q = rng.standard_normal((cu[-1], hq, d))
+    k = rng.standard_normal((cu[-1], hkv, d))
+    v = rng.standard_normal((cu[-1], hkv, d))
+    full = oatt.causal_prefill_attention(q, k, v, cu)
+    for cut in ([10, 17, 0], [22, 1, 8], [0, 39, 3]):
+        rows = [np.arange(cu[i] + cut[i], cu[i + 1]) for i in range(3)]
+        cq = np.concatenate([[0], np.cumsum([len(r) for r in rows])])
+        out = oatt.causal_prefill_attention(q[np.concatenate(rows)], k, v, cq, cu_seqlens_k=cu)
+        np.testing.assert_allclose(out, full[np.concatenate(rows)], rtol=1e-12, atol=1e-12)
+        # queries aligned to the start of the keys instead see too few keys
+        assert not np.allclose(out[:3], oatt.causal_prefill_attention(q[np.concatenate(rows)][:3], k[:3], v[:3],
+                                                                       [0, 3])) or cut[0] == 0
+
+
 def test_rope_table_and_rotation_match_reference_formula():
     cache = oatt.rope_cos_sin_cache(64, 32, 500000.0)
     inv = 1.0 / (500000.0 ** (torch.arange(0, 64, 2, dtype=torch.float) / 64))
