@@ -35,6 +35,7 @@
 // and the last split of a strip to arrive (device-scope ticket) sums them and
 // runs the epilogue, then resets its ticket.  HBM-bound on W.
 #include <cstdlib>
+#include <type_traits>
 
 #include "fdms_vec.h"
 
@@ -44,6 +45,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kKB = 64;       // k-block: columns per lane group step
 constexpr int kMaxM = 16;
@@ -240,6 +242,12 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     const bf16_t* __restrict__ g_scale, const bf16_t* __restrict__ g_zero, int group, int64_t g_s, int qx_torch,
     int bf16_scores) {
   constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
+  // FP8 weights with the quantised activation run on the FP8 matrix cores
+  // (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales): 128-column k-blocks,
+  // lane group g holding columns 32g .. 32g + 31 of both operands, no
+  // per-element conversion of the weights
+  constexpr bool F8 = is_fp8<WT>() && QX && PRO == 0;
+  constexpr int KB = F8 ? 2 * kKB : kKB;
   __shared__ float s_inv[kMaxM], s_xs[kMaxM];
   __shared__ f32x4 s_acc[NA][NW][64];
   __shared__ int s_last;
@@ -277,8 +285,32 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     uint4 x[U][2];
     uint4 r[U][2];   // residual (PRO 1)
     uint4 nw[U][2];  // norm weight (PRO 1)
+    uint4 w8[NA][U][2];  // F8: 32 weight bytes per lane per k-block
+    uint4 x8[U][4];      // F8: 32 bf16 activations per lane per k-block
   };
   auto load = [&](int kb0, Buf& b) {
+    if constexpr (F8) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb0 + u * KB + 32 * g;
+        if (kb0 + u * KB < kend) {
+          // branch-free: a last half block (64 columns) has nothing for lane
+          // groups 2 and 3, whose loads are clamped in bounds and whose values
+          // (and those of rows >= M, read from row 0) are zeroed in compute
+          const int kl = min(k, kend - 32);
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            const uint4* p = reinterpret_cast<const uint4*>(wrow[a] + kl);
+            b.w8[a][u][0] = p[0];
+            b.w8[a][u][1] = p[1];
+          }
+          const uint4* xp = reinterpret_cast<const uint4*>(xrow + kl);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) b.x8[u][i] = xp[i];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = kb0 + u * kKB + 16 * g;
@@ -312,6 +344,56 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   };
   auto compute = [&](int kb0, const Buf& b) {
+    if constexpr (F8) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB >= kend) break;
+        const bool gv = kb0 + u * KB + 32 * g < kend;  // this lane group's columns exist
+        // x * x_s quantised to e4m3fn, four columns per word (the hardware
+        // RNE-saturating conversion; a NaN anywhere in the block takes the
+        // software encoder, one branch per block)
+        float f[32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t v[4] = {b.x8[u][i].x, b.x8[u][i].y, b.x8[u][i].z, b.x8[u][i].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f[8 * i + 2 * e] = bf_lo(v[e]) * xsc;
+            f[8 * i + 2 * e + 1] = bf_hi(v[e]) * xsc;
+          }
+        }
+        uint32_t q[8];
+        bool nan = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float c0 = __builtin_amdgcn_fmed3f(f[4 * j], -kFp8Max, kFp8Max);
+          const float c1 = __builtin_amdgcn_fmed3f(f[4 * j + 1], -kFp8Max, kFp8Max);
+          const float c2 = __builtin_amdgcn_fmed3f(f[4 * j + 2], -kFp8Max, kFp8Max);
+          const float c3 = __builtin_amdgcn_fmed3f(f[4 * j + 3], -kFp8Max, kFp8Max);
+          uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false);
+          q[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, (int)r, true);
+          nan |= (f[4 * j] != f[4 * j]) | (f[4 * j + 1] != f[4 * j + 1]) | (f[4 * j + 2] != f[4 * j + 2]) |
+                 (f[4 * j + 3] != f[4 * j + 3]);
+        }
+        if (__builtin_expect(nan, 0)) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            q[j] = f32_to_fp8(f[4 * j]) | (f32_to_fp8(f[4 * j + 1]) << 8) | (f32_to_fp8(f[4 * j + 2]) << 16) |
+                   (f32_to_fp8(f[4 * j + 3]) << 24);
+        }
+        const bool xv = gv && has_row;
+        const i32x8 bx = i32x8{xv ? (int)q[0] : 0, xv ? (int)q[1] : 0, xv ? (int)q[2] : 0, xv ? (int)q[3] : 0,
+                               xv ? (int)q[4] : 0, xv ? (int)q[5] : 0, xv ? (int)q[6] : 0, xv ? (int)q[7] : 0};
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint4 w0 = b.w8[a][u][0], w1 = b.w8[a][u][1];
+          const i32x8 aw = i32x8{gv ? (int)w0.x : 0, gv ? (int)w0.y : 0, gv ? (int)w0.z : 0, gv ? (int)w0.w : 0,
+                                 gv ? (int)w1.x : 0, gv ? (int)w1.y : 0, gv ? (int)w1.z : 0, gv ? (int)w1.w : 0};
+          acc[a] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aw, bx, acc[a], 0, 0, 0, 127, 0, 127);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (kb0 + u * kKB >= kend) break;
@@ -415,9 +497,9 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
 
   if (PRO == 1 && has_row) inv = s_inv[c];
   if (QX && has_row) xsc = s_xs[c];
-  for (int kb0 = kw0; kb0 < kend; kb0 += U * kKB) {
-    const bool more = kb0 + U * kKB < kend;
-    if (more) load(kb0 + U * kKB, nxt);  // next group in flight while this one computes
+  for (int kb0 = kw0; kb0 < kend; kb0 += U * KB) {
+    const bool more = kb0 + U * KB < kend;
+    if (more) load(kb0 + U * KB, nxt);  // next group in flight while this one computes
     compute(kb0, cur);
     if (more) cur = nxt;
   }
@@ -577,7 +659,7 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   const WT* w = (const WT*)a.w;
   // k-blocks per double-buffered group (register budget: the RMSNorm prologue
   // also holds the residual and norm weight of each k-block)
-  constexpr int U = PRO == 1 ? 2 : 4;
+  constexpr int U = (PRO == 1 || (std::is_same<WT, fp8_t>::value && QX && PRO == 0)) ? 2 : 4;
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
                       a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
                       a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores
