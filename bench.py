@@ -166,7 +166,7 @@ def parse_args():
     return p.parse_args()
 
 
-def attention_roofline(llm, seqs, replays: int):
+def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     """Average duration and algorithmic HBM bytes of the decode attention kernel
     the step runs, on the live decode state: one graph holds the kernel of
     every layer with the decode step's arguments; HIP events on the capture
@@ -253,7 +253,7 @@ def attention_roofline(llm, seqs, replays: int):
         splits = int(((lv + split_rows - 1) // split_rows).clamp(1, splits).max())
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic(),
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("decode_attention_pmc_traffic.json", config),
             "kernel": ("decode_attn_mfma_kernel<fused>" if fused else
                        "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel"),
             "avg_launch_us": round(per_launch_s * 1e6, 3),
@@ -338,18 +338,20 @@ def attention_scaling(llm, seqs, batches=(8, 32, 128), layers: int = 8, replays:
             "live_counts": "resampled from this run's decode state", "points": rows}
 
 
-def _pmc_traffic(name: str = "decode_attention_pmc_traffic.json"):
+def _pmc_traffic(name: str, config: str):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE, each scaled by the factor the same counter
-    reads for the plain copy kernel), or None when it is absent."""
+    reads for the plain copy kernel), or None when it is absent or was taken
+    on another bench config."""
     path = ROOT / "profiles" / name
     try:
-        return json.loads(path.read_text())["traffic_bytes_per_launch"]
+        d = json.loads(path.read_text())
+        return d["traffic_bytes_per_launch"] if d.get("config") == config else None
     except (OSError, KeyError, ValueError):
         return None
 
 
-def compaction_roofline(lens, replays: int = 20, layers: int = 16):
+def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str = "l1b-c8"):
     """Prefill compaction (A4 + A5) as the engine runs it for one layer of a
     prefill batch (streaming_pack_layer): one pack-prepare launch over every
     sequence (keep counts, chunk offsets, metadata rows reset to (-1, False))
@@ -426,7 +428,7 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16):
     del per_layer
     return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel (one prefill layer, all sequences)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("compaction_pmc_traffic.json"),
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("compaction_pmc_traffic.json", config),
             "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(nbytes), "tokens": t_tot,
             "live_rows": round(live, 1), "bytes_survey": int(survey),
             "achieved_survey": round(survey / layer_s / 1e9, 1)}
@@ -573,11 +575,11 @@ def main():
         progress("cpu baseline")
         cpu = cpu_baseline(llm, seqs, args.cpu_seconds)
     progress("attention roofline")
-    roof = attention_roofline(llm, seqs, args.attn_replays)
+    roof = attention_roofline(llm, seqs, args.attn_replays, args.config)
     progress("attention scaling")
     scaling = attention_scaling(llm, seqs) if not args.no_scaling else None
     progress("compaction roofline")
-    pack = compaction_roofline(lens)
+    pack = compaction_roofline(lens, config=args.config)
     copy_bw = hbm_copy_gbps()
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",
