@@ -28,7 +28,13 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
 // PART: the input is the fp32 split-K partial sums of the preceding linear,
 // part[s * split_stride + row * hidden + c], s < k_splits, and x = bf16 of
 // their sum taken in split order (the linear kernel's own merge).
-template <bool PART>
+// PART: the input is the fp32 split-K partials; KS > 0 is their count known
+// at compile time, KS = 0 reads k_splits at run time.  PER = 8-column chunks
+// per thread (hidden <= PER * 8 * kThreads).  Every load of the row goes out
+// before the first use, with addresses clamped in bounds instead of loads
+// under a condition (a conditional load makes the compiler wait for it at
+// the end of its block, one memory round trip per load).
+template <bool PART, int KS, int PER>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restrict__ in, const bf16_t* residual,
                                                            const bf16_t* __restrict__ weight, bf16_t* __restrict__ out,
                                                            bf16_t* residual_out, int hidden, int64_t in_stride,
@@ -38,59 +44,70 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   __shared__ float s_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const bf16_t* x = PART ? nullptr : in + (row / heads) * in_stride + (row % heads) * in_head_stride;
-  const bf16_t* rs = residual ? residual + row * (int64_t)hidden : nullptr;
+  const bool has_res = residual != nullptr;  // uniform
+  const bf16_t* rs = has_res ? residual + row * (int64_t)hidden : weight;  // a valid address either way
   constexpr int V = 8;
-  constexpr int kMaxPer = 4;  // hidden <= 8192
-  float vals[kMaxPer][V];
-  float ss = 0.0f;
-  // the norm weight does not depend on the row sum: its loads go out with x's
-  Vec<bf16_t, V> wv[kMaxPer];
+  constexpr int NS = KS > 0 ? KS : 1;
+  Vec<bf16_t, V> wv[PER], xv[PER], rv[PER];
+  Vec<float, V> pv[PER][NS];
 #pragma unroll
-  for (int j = 0; j < kMaxPer; ++j) {
-    const int c = (threadIdx.x + j * kThreads) * V;
-    if (c < hidden) wv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + c);
+  for (int j = 0; j < PER; ++j) {
+    const int cc = min((threadIdx.x + j * kThreads) * V, hidden - V);
+    wv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + cc);
+    if constexpr (PART && KS > 0) {
+#pragma unroll
+      for (int sp = 0; sp < KS; ++sp)
+        pv[j][sp] = *reinterpret_cast<const Vec<float, V>*>(part + sp * split_stride + row * hidden + cc);
+    }
+    if constexpr (!PART) xv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(x + cc);
+    rv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(rs + cc);
   }
+  float vals[PER][V];
+  float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kMaxPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
-    if (c < hidden) {
-      float xf[V];
-      if constexpr (PART) {
+    const bool valid = c < hidden;
+    float xf[V];
+    if constexpr (PART) {
 #pragma unroll
-        for (int i = 0; i < V; ++i) xf[i] = 0.0f;
+      for (int i = 0; i < V; ++i) xf[i] = 0.0f;
+      if constexpr (KS > 0) {
+#pragma unroll
+        for (int sp = 0; sp < KS; ++sp)
+#pragma unroll
+          for (int i = 0; i < V; ++i) xf[i] += pv[j][sp].v[i];
+      } else if (valid) {
         for (int sp = 0; sp < k_splits; ++sp) {
-          const Vec<float, V> pv = *reinterpret_cast<const Vec<float, V>*>(part + sp * split_stride + row * hidden + c);
+          const Vec<float, V> p = *reinterpret_cast<const Vec<float, V>*>(part + sp * split_stride + row * hidden + c);
 #pragma unroll
-          for (int i = 0; i < V; ++i) xf[i] += pv.v[i];
+          for (int i = 0; i < V; ++i) xf[i] += p.v[i];
         }
-#pragma unroll
-        for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(f32_to_bf16(xf[i]));
-      } else {
-        const Vec<bf16_t, V> xv = *reinterpret_cast<const Vec<bf16_t, V>*>(x + c);
-#pragma unroll
-        for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(xv.v[i].bits);
       }
-      Vec<bf16_t, V> rv;
-      if (rs) rv = *reinterpret_cast<const Vec<bf16_t, V>*>(rs + c);
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        float f = xf[i];
-        if (rs) f += bf16_to_f32(rv.v[i].bits);
-        vals[j][i] = f;
-        ss += f * f;
-      }
-      if (residual_out) {
-        Vec<bf16_t, V> ro;
+      for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(f32_to_bf16(xf[i]));
+    } else {
 #pragma unroll
-        for (int i = 0; i < V; ++i) ro.v[i].bits = (uint16_t)f32_to_bf16(vals[j][i]);
-        *reinterpret_cast<Vec<bf16_t, V>*>(residual_out + row * (int64_t)hidden + c) = ro;
-      }
+      for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(xv[j].v[i].bits);
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float f = xf[i];
+      if (has_res) f += bf16_to_f32(rv[j].v[i].bits);
+      vals[j][i] = f;
+      ss += valid ? f * f : 0.0f;
+    }
+    if (residual_out && valid) {
+      Vec<bf16_t, V> ro;
+#pragma unroll
+      for (int i = 0; i < V; ++i) ro.v[i].bits = (uint16_t)f32_to_bf16(vals[j][i]);
+      *reinterpret_cast<Vec<bf16_t, V>*>(residual_out + row * (int64_t)hidden + c) = ro;
     }
   }
   const float total = block_sum(ss, s_red);
   const float inv = 1.0f / sqrtf(total / (float)hidden + eps);
 #pragma unroll
-  for (int j = 0; j < kMaxPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
     if (c < hidden) {
       Vec<bf16_t, V> o;
@@ -115,10 +132,16 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   if (heads > 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   if (!in || !weight || !out || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,
-                     (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps, nullptr, 0,
-                     (int64_t)0);
+#define FDMS_RMSNORM(PERV)                                                                                      \
+  hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                  \
+                     (hipStream_t)stream, (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight,        \
+                     (bf16_t*)out, (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps, \
+                     nullptr, 0, (int64_t)0)
+  const int per = (hidden + 8 * kThreads - 1) / (8 * kThreads);
+  if (per == 1) FDMS_RMSNORM(1);
+  else if (per == 2) FDMS_RMSNORM(2);
+  else FDMS_RMSNORM(4);
+#undef FDMS_RMSNORM
   FDMS_LAUNCH_CHECK();
   return 0;
 }
@@ -134,9 +157,27 @@ FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64
   if (!partials || !weight || !out || rows > 0x7FFFFFFF || split_stride < rows * (int64_t)hidden)
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)partials % 32 || split_stride % 8) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
-                     nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out, (bf16_t*)residual_out,
-                     hidden, (int64_t)0, (int64_t)0, 1, out_stride, eps, partials, k_splits, split_stride);
+#define FDMS_RMSNORM_PART(KSV, PERV)                                                                              \
+  hipLaunchKernelGGL((rmsnorm_kernel<true, KSV, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                   \
+                     (hipStream_t)stream, nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,      \
+                     (bf16_t*)residual_out, hidden, (int64_t)0, (int64_t)0, 1, out_stride, eps, partials, k_splits,   \
+                     split_stride)
+#define FDMS_RMSNORM_PART_PER(PERV)                   \
+  if (k_splits == 1) FDMS_RMSNORM_PART(1, PERV);      \
+  else if (k_splits == 2) FDMS_RMSNORM_PART(2, PERV); \
+  else if (k_splits == 4) FDMS_RMSNORM_PART(4, PERV); \
+  else if (k_splits == 8) FDMS_RMSNORM_PART(8, PERV); \
+  else FDMS_RMSNORM_PART(0, PERV)
+  const int per = (hidden + 8 * kThreads - 1) / (8 * kThreads);
+  if (per == 1) {
+    FDMS_RMSNORM_PART_PER(1);
+  } else if (per == 2) {
+    FDMS_RMSNORM_PART_PER(2);
+  } else {
+    FDMS_RMSNORM_PART_PER(4);
+  }
+#undef FDMS_RMSNORM_PART_PER
+#undef FDMS_RMSNORM_PART
   FDMS_LAUNCH_CHECK();
   return 0;
 }
