@@ -761,12 +761,24 @@ __global__ __launch_bounds__(1024) void argmax_partials_kernel(const float* __re
   const int64_t row = blockIdx.x;
   float bv = 0.0f;
   int bi = kNone;
-  for (int j = threadIdx.x; j < strips; j += 1024) {
-    const float v = pval[row * strips + j];
-    const int i = pidx[row * strips + j];
-    if (bi == kNone || argmax_better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
+  // kU strips per thread per pass, all loads issued before the first compare
+  // (clamped to the last strip; the duplicates cannot change the argmax)
+  constexpr int kU = 8;
+  for (int j0 = threadIdx.x; j0 < strips; j0 += 1024 * kU) {
+    float v[kU];
+    int ix[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int j = min(j0 + u * 1024, strips - 1);
+      v[u] = pval[row * strips + j];
+      ix[u] = pidx[row * strips + j];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (bi == kNone || argmax_better(v[u], ix[u], bv, bi)) {
+        bv = v[u];
+        bi = ix[u];
+      }
     }
   }
 #pragma unroll
