@@ -160,10 +160,11 @@ def test_engine_takes_the_greedy_fast_loop_only_for_a_lone_greedy_sequence(monke
         assert a.seq_id not in llm.model_runner.compact_kv_manager.seq_states and llm.is_finished()
         assert llm.last_step_stats["fast_loop"]["tokens"] == 8
         # not taken: two sequences prefilled together, a sampled sequence, or the switch off
-        for prompts, sp, env in (([list(range(30)), list(range(50))], greedy, "1"),
-                                 ([list(range(30))], SamplingParams(temperature=0.7, max_tokens=9, ignore_eos=True),
+        short = SamplingParams(temperature=0.0, max_tokens=3, ignore_eos=True)
+        for prompts, sp, env in (([list(range(30)), list(range(50))], short, "1"),
+                                 ([list(range(30))], SamplingParams(temperature=0.7, max_tokens=3, ignore_eos=True),
                                   "1"),
-                                 ([list(range(30))], greedy, "0")):
+                                 ([list(range(30))], short, "0")):
             monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", env)
             calls.clear()
             for p in prompts:
