@@ -196,6 +196,13 @@ __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
 #define FDMS_EXPORT extern "C" __attribute__((visibility("default")))
 
+// True when every non-null pointer is 16-byte aligned (host-side argument check
+// for kernels that move rows as 16-byte vectors).
+template <typename... P>
+inline bool fdms_aligned16(const P*... p) {
+  return ((((uintptr_t)p) % 16 == 0) && ...);
+}
+
 // Dispatch a runtime dtype code to a C++ storage type.
 #define FDMS_DISPATCH_DTYPE(code, T, ...)                     \
   switch (code) {                                             \

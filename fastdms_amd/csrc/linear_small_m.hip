@@ -189,7 +189,7 @@ __device__ __forceinline__ void row_stats(const bf16_t* xr, const bf16_t* rr, co
       }
     }
     ss = wave_sum(ss);
-    inv = 1.0f / sqrtf(ss / (float)K + eps);
+    inv = rsqrtf(ss / (float)K + eps);  // torch.rsqrt (layernorm.py:24, 38)
   }
   float amax = 0.0f;
   if (QX) {

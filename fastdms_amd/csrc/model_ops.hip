@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
     }
   }
   const float total = block_sum(ss, s_red);
-  const float inv = 1.0f / sqrtf(total / (float)hidden + eps);
+  const float inv = rsqrtf(total / (float)hidden + eps);  // torch.rsqrt (layernorm.py:24, 38)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
@@ -132,6 +132,9 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   if (heads > 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   if (!in || !weight || !out || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  // rows move as 16-byte vectors
+  if (!fdms_aligned16(in, weight, out, residual, residual_out) || (in_stride | in_head_stride | out_stride) % 8)
+    return (int)hipErrorInvalidValue;
 #define FDMS_RMSNORM(PERV)                                                                                      \
   hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                  \
                      (hipStream_t)stream, (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight,        \
@@ -157,6 +160,7 @@ FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64
   if (!partials || !weight || !out || rows > 0x7FFFFFFF || split_stride < rows * (int64_t)hidden)
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)partials % 32 || split_stride % 8) return (int)hipErrorInvalidValue;
+  if (!fdms_aligned16(weight, out, residual, residual_out) || out_stride % 8) return (int)hipErrorInvalidValue;
 #define FDMS_RMSNORM_PART(KSV, PERV)                                                                              \
   hipLaunchKernelGGL((rmsnorm_kernel<true, KSV, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                   \
                      (hipStream_t)stream, nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,      \

@@ -470,6 +470,13 @@ class CompactKVManager:
                     st.token_positions[layer_id].fill_(-1)
                     st.evict_mask[layer_id].fill_(False)
         live_host = live.tolist()  # the one host sync of this layer
+        # a span holds at most max_capacity_per_lh rows: a larger live count
+        # would scatter past it (compact_kv.py:1018-1023), so fail before any
+        # range of this layer is allocated
+        for i, st in enumerate(states):
+            if lens[i] > 0 and max(live_host[i]) > st.max_capacity_per_lh:
+                raise RuntimeError(f"streaming pack live count {max(live_host[i])} exceeds metadata capacity "
+                                   f"{st.max_capacity_per_lh} (layer {layer_id}, seq {st.seq_id})")
         # host first-fit allocation, all sequences of the batch (reference order)
         all_bases, all_sizes = [], []
         high_water = 0
@@ -490,9 +497,6 @@ class CompactKVManager:
                     if b >= 0 and n > 0:
                         self._free_range(layer_id, b, n)
             raise
-            if lens[i] > 0 and max(live_host[i]) > st.max_capacity_per_lh:
-                raise RuntimeError(f"streaming pack live count {max(live_host[i])} exceeds metadata capacity "
-                                   f"{st.max_capacity_per_lh} (layer {layer_id}, seq {st.seq_id})")
         if self.per_layer_storage:
             self._ensure_layer_storage(layer_id, high_water)
         compact_k, compact_v = self._layer_arena(layer_id)

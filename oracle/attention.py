@@ -14,6 +14,7 @@ from __future__ import annotations
 import math
 
 import numpy as np
+import torch
 
 from . import numerics
 from .dms import dms_decide
@@ -204,53 +205,36 @@ def causal_prefill_attention(q, k, v, cu_seqlens, scale=None, cu_seqlens_k=None)
     q [T, Hq, D], k/v [Tk, Hkv, D] float values; returns float64 [T, Hq, D].
     With cu_seqlens_k the sequence's queries are the last of its keys
     (flash-attn's bottom-right alignment: query i of n sees keys 0 ..
-    klen - n + i); without it q_len == k_len.
+    klen - n + i); without it q_len == k_len and cu_seqlens_k = cu_seqlens.
+    Evaluated in float64 with torch CPU matmuls (multi-threaded), 512 query
+    rows of one KV head's query group at a time.
     """
-    if cu_seqlens_k is not None:
-        return _causal_prefill_varlen(q, k, v, cu_seqlens, cu_seqlens_k, scale)
-    q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
-    t, hq, d = q.shape
+    q = torch.from_numpy(np.ascontiguousarray(q, np.float64))
+    k = torch.from_numpy(np.ascontiguousarray(k, np.float64))
+    v = torch.from_numpy(np.ascontiguousarray(v, np.float64))
+    hq, d = q.shape[1], q.shape[2]
     hkv = k.shape[1]
     g = hq // hkv
     scale = d ** -0.5 if scale is None else scale
-    out = np.zeros_like(q)
-    cu = [int(x) for x in cu_seqlens]
-    for i in range(len(cu) - 1):
-        s0, s1 = cu[i], cu[i + 1]
-        n = s1 - s0
-        mask = np.tril(np.ones((n, n), dtype=bool))
-        for qh in range(hq):
-            h = qh // g
-            s = q[s0:s1, qh] @ k[s0:s1, h].T * scale
-            s = np.where(mask, s, -np.inf)
-            s = s - s.max(axis=1, keepdims=True)
-            p = np.exp(s)
-            out[s0:s1, qh] = (p @ v[s0:s1, h]) / p.sum(axis=1, keepdims=True)
-    return out
-
-
-def _causal_prefill_varlen(q, k, v, cu_q, cu_k, scale):
-    q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
-    hq, d = q.shape[1], q.shape[2]
-    g = hq // k.shape[1]
-    scale = d ** -0.5 if scale is None else scale
-    out = np.zeros_like(q)
-    cq, ck = [int(x) for x in cu_q], [int(x) for x in cu_k]
+    out = torch.zeros_like(q)
+    cq = [int(x) for x in cu_seqlens]
+    ck = cq if cu_seqlens_k is None else [int(x) for x in cu_seqlens_k]
     for i in range(len(cq) - 1):
         s0, s1, k0, k1 = cq[i], cq[i + 1], ck[i], ck[i + 1]
         n, nk = s1 - s0, k1 - k0
         if nk < n:
             raise ValueError("a sequence has fewer keys than queries")
-        mask = np.tril(np.ones((n, nk), dtype=bool), nk - n)
-        for qh in range(hq):
-            h = qh // g
-            sc = q[s0:s1, qh] @ k[k0:k1, h].T * scale
-            sc = np.where(mask, sc, -np.inf)
-            sc = sc - sc.max(axis=1, keepdims=True)
-            p = np.exp(sc)
-            out[s0:s1, qh] = (p @ v[k0:k1, h]) / p.sum(axis=1, keepdims=True)
-    return out
+        for r0 in range(0, n, 512):
+            r1 = min(n, r0 + 512)
+            # query row r sees keys 0 .. nk - n + r
+            qi = torch.arange(r0, r1).unsqueeze(1) + (nk - n)
+            mask = torch.arange(nk).unsqueeze(0) <= qi
+            for h in range(hkv):
+                qs = q[s0 + r0:s0 + r1, h * g:(h + 1) * g].transpose(0, 1)  # [g, rows, d]
+                sc = (qs @ k[k0:k1, h].T) * scale
+                sc = sc.masked_fill(~mask, -float("inf"))
+                sc = sc - sc.amax(dim=-1, keepdim=True)
+                p = torch.exp(sc)
+                o = (p @ v[k0:k1, h]) / p.sum(dim=-1, keepdim=True)
+                out[s0 + r0:s0 + r1, h * g:(h + 1) * g] = o.transpose(0, 1)
+    return out.numpy()

@@ -59,7 +59,7 @@ class OracleModel:
             x = x + residual
             residual = bf16(x)
         var = (x * x).mean(dim=-1, keepdim=True)
-        xn = bf16(x * (1.0 / torch.sqrt(var + eps)))
+        xn = bf16(x * torch.rsqrt(var + eps))  # layernorm.py:24, 37-38
         return bf16(xn * weight), residual
 
     def linear(self, x, name, bias=True):
@@ -91,7 +91,7 @@ class OracleModel:
         gu = self.linear(h, f"model.layers.{layer}.mlp.gate_up_proj", bias=False)
         f = gu.shape[1] // 2
         g, u = gu[:, :f], gu[:, f:]
-        act = bf16((g / (1.0 + torch.exp(-g))) * u)
+        act = bf16(torch.nn.functional.silu(g) * u)  # activation.py:8-11, one rounding (compiled)
         return self.linear(act, f"model.layers.{layer}.mlp.down_proj", bias=False)
 
     def logits(self, x):

@@ -532,7 +532,7 @@ class Emulator:
             self.view(residual_out, torch.bfloat16, (rows, hidden), (hidden, 1), "residual_out").copy_(
                 f.to(torch.bfloat16))
         w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
-        inv = 1.0 / torch.sqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
+        inv = torch.rsqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
         xn = (f * inv).to(torch.bfloat16).float()
         self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
         return 0
@@ -554,7 +554,7 @@ class Emulator:
             self.view(residual_out, torch.bfloat16, (rows, hidden), (hidden, 1), "residual_out").copy_(
                 f.to(torch.bfloat16))
         w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
-        inv = 1.0 / torch.sqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
+        inv = torch.rsqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
         xn = (f * inv).to(torch.bfloat16).float()
         self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
         return 0
@@ -609,7 +609,7 @@ class Emulator:
             if res_out:
                 self.view(res_out, torch.bfloat16, (m, k), (ro_s, 1), "residual_out").copy_(f.to(torch.bfloat16))
             var = (f * f).mean(dim=-1, keepdim=True)
-            a = (f * (1.0 / torch.sqrt(var + eps))).to(torch.bfloat16).float()
+            a = (f * torch.rsqrt(var + eps)).to(torch.bfloat16).float()
             nw = self.view(norm_w, torch.bfloat16, (k,), (1,), "norm_weight").float()
             a = (a * nw).to(torch.bfloat16).float()
         else:

@@ -91,3 +91,22 @@ def test_a_request_that_can_never_fit_raises():
         llm.add_request(list(range(300)), SamplingParams(temperature=0.0, max_tokens=8, ignore_eos=True))
         with pytest.raises(CompactCapacityExhausted):
             llm.step()
+
+
+def test_streaming_pack_rejects_a_live_count_above_the_span_capacity():
+    """compact_kv.py:1018-1023: with the per-sequence target capped below a
+    prompt's live count, the pack raises before it allocates or scatters
+    (a span of max_capacity_per_lh rows cannot hold the survivors)."""
+    with cpu_engine():
+        from fastdms_amd import LLM, SamplingParams
+        llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=2, max_num_batched_tokens=4096,
+                  enforce_eager=True, compact_kv_target_live_tokens_per_seq=64, **DMS)
+        rng = np.random.default_rng(5)
+        sp = SamplingParams(temperature=0.0, max_tokens=8, ignore_eos=True)
+        for n in (500, 400):
+            llm.add_request(rng.integers(0, 512, n).tolist(), sp)
+        mgr = llm.model_runner.compact_kv_manager
+        free_before = [list(r) for r in mgr.free_ranges_per_layer]
+        with pytest.raises(RuntimeError, match="exceeds metadata capacity"):
+            llm.step()
+        assert [list(r) for r in mgr.free_ranges_per_layer] == free_before
