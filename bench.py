@@ -249,15 +249,19 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     bytes_per_launch = (kv_bytes + io_bytes) / nl
     mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
     splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
-    if split_rows:  # per-pair split counts, as the kernel derives them
-        splits = int(((lv + split_rows - 1) // split_rows).clamp(1, splits).max())
+    if mfma:  # per-pair split counts, as the kernel derives them (layer 0)
+        splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma,
+                                                  waves=4 if (d == 64 or not fused) else 8)
+        per_pair = ((lv[0] + split_rows - 1) // split_rows).clamp(1, splits)
+        splits = {"rows_per_split": split_rows, "bound": splits, "workgroups": int(per_pair.sum()),
+                  "max_per_pair": int(per_pair.max())}
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("decode_attention_pmc_traffic.json", config),
             "kernel": ("decode_attn_mfma_kernel<fused>" if fused else
                        "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel"),
             "avg_launch_us": round(per_launch_s * 1e6, 3),
-            "bytes_per_launch": int(bytes_per_launch), "max_splits_per_pair": splits,
+            "bytes_per_launch": int(bytes_per_launch), "partition": splits,
             "live_tokens_per_head": {"mean": round(float(lv.float().mean()), 1), "max": int(lv.max()),
                                      "p99": int(lv.float().quantile(0.99))}}
 
@@ -402,7 +406,7 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
                      0, 0, nseq, offs.data_ptr(), offs.stride(0), offs.stride(1), offs.stride(2), base.data_ptr(),
                      base.stride(0), base.stride(1), ck.data_ptr(), cv.data_ptr(), nat.DT_FP8, ck.stride(0),
                      pos.data_ptr(), em.data_ptr(), rows.data_ptr(), pos.stride(0), pos.stride(1), pos.stride(2),
-                     em.stride(0), em.stride(1), em.stride(2), window, h, d, chunks, 8, nat.stream())
+                     em.stride(0), em.stride(1), em.stride(2), window, h, d, chunks, 8, None, None, nat.stream())
 
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()

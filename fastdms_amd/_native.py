@@ -32,13 +32,13 @@ SIGNATURES: dict[str, str] = {
     "fdms_fp8_decode_hw": "pplp",
     "fdms_extract_dms_decisions": "pilllpllliiifffip",
     "fdms_streaming_pack_prepare": "pllpiiiiipllplllpppllllip",
-    "fdms_streaming_pack_rank_scatter": "ppillllpllpiiiplllpllppilppplllllliiiiip",
-    "fdms_streaming_pack_scatter": "ppillllpllpllpllplppilpllplliiiiip",
-    "fdms_dms_rope_store_compact_decode": "pillppillllpllppilpllpllpiiiifffiiip",
+    "fdms_streaming_pack_rank_scatter": "ppillllpllpiiiplllpllppilppplllllliiiiippp",
+    "fdms_streaming_pack_scatter": "ppillllpllpllpllplppilpllplliiiiippp",
+    "fdms_dms_rope_store_compact_decode": "pillppillllpllppilpllpllpiiiifffiiippp",
     "fdms_rope_inplace": "pillliipllpp",
-    "fdms_store_compact_kvcache": "ppillllppilplliiip",
-    "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpp",
-    "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifp",
+    "fdms_store_compact_kvcache": "ppillllppilplliiippp",
+    "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpppp",
+    "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifppp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",

@@ -49,6 +49,10 @@ class Config:
     seed: int = 0
     dms_survive_fraction: float = 0.125
     compact_decode_cudagraph: bool = True
+    # Per-(layer, kv head) FP8 KV scales (no reference counterpart; the
+    # reference stores K/V with a bare cast): "unit" = none (the reference's
+    # numerics), "calibrate" = set from each layer's first prefill (amax / 224)
+    compact_kv_fp8_scales: str = "unit"
     # What happens when a prefill's compact spans do not fit (the reference
     # raises from the allocator, compact_kv.py:715-718): "defer" puts the
     # prefill back at the head of the queue until a running sequence finishes;

@@ -57,6 +57,29 @@ struct SpanAddr {
   }
 };
 
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-merge handoff of a workgroup (handoff_release / handoff_acquire in
+// fdms_common.h): every thread's partials (relaxed agent-scope atomic stores)
+// have completed before one thread takes the pair's ticket; the workgroup that
+// takes ticket n-1 (the last of the pair's n workgroups) orders its partial
+// loads (relaxed agent-scope atomic loads) after it.  Correct wherever the
+// pair's workgroups run (any XCD).
+__device__ __forceinline__ bool take_last_ticket(int* counter, int n, int* s_flag) {
+  handoff_release();
+  __syncthreads();
+  if (threadIdx.x == 0) *s_flag = ticket_add(counter) == n - 1;
+  __syncthreads();
+  const bool last = *s_flag;
+  if (last) handoff_acquire();
+  return last;
+}
+
 }  // namespace
 
 template <typename QT, typename KT>
@@ -200,20 +223,15 @@ __global__ __launch_bounds__(kThreads) void decode_attn_generic_kernel(
   const int64_t stride = (int64_t)G * (D + 2);
   float* mine = ws + ((int64_t)pair * num_splits + split) * stride;
   if (tid < G) {
-    mine[tid] = s_m[tid];
-    mine[G + tid] = s_l[tid];
+    store_agent(mine + tid, s_m[tid]);
+    store_agent(mine + G + tid, s_l[tid]);
   }
 #pragma unroll
   for (int k = 0; k < kMaxG; ++k) {
     const int o = tid + k * kThreads;
-    if (o < n_out) mine[2 * G + o] = acc[k];
+    if (o < n_out) store_agent(mine + 2 * G + o, acc[k]);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == num_splits - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!take_last_ticket(&counters[pair], num_splits, &s_last)) return;
   const float* all = ws + (int64_t)pair * num_splits * stride;
 #pragma unroll
   for (int k = 0; k < kMaxG; ++k) {
@@ -221,20 +239,20 @@ __global__ __launch_bounds__(kThreads) void decode_attn_generic_kernel(
     if (o < n_out) {
       const int g = o / D;
       float M = -INFINITY;
-      for (int s = 0; s < num_splits; ++s) M = fmaxf(M, (all + s * stride + g)[0]);
+      for (int s = 0; s < num_splits; ++s) M = fmaxf(M, load_agent(all + s * stride + g));
       float L = 0.0f, A = 0.0f;
       for (int s = 0; s < num_splits; ++s) {
         const float* ps = all + s * stride;
-        const float ms = (ps + g)[0];
+        const float ms = load_agent(ps + g);
         const float wgt = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-        L += (ps + G + g)[0] * wgt;
-        A += (ps + 2 * G + o)[0] * wgt;
+        L += load_agent(ps + G + g) * wgt;
+        A += load_agent(ps + 2 * G + o) * wgt;
       }
       const int d = o - g * D;
       st<QT>(out + b * os_b + (int64_t)(h * G + g) * os_h + d, A / L);
     }
   }
-  if (tid == 0) counters[pair] = 0;
+  if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -491,35 +509,30 @@ __global__ __launch_bounds__(kThreads) void decode_attn_tiled_kernel(
   constexpr int64_t kStride = (int64_t)G * (D + 2);
   float* mine = ws + ((int64_t)pair * num_splits + split) * kStride;
   if (tid < G) {
-    mine[tid] = s_m[tid];
-    mine[G + tid] = s_l[tid];
+    store_agent(mine + tid, s_m[tid]);
+    store_agent(mine + G + tid, s_l[tid]);
   }
   if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) mine[2 * G + pv_g * D + pv_d0 + i] = tot[i];
+    for (int i = 0; i < DPL; ++i) store_agent(mine + 2 * G + pv_g * D + pv_d0 + i, tot[i]);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == num_splits - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!take_last_ticket(&counters[pair], num_splits, &s_last)) return;
   const float* all = ws + (int64_t)pair * num_splits * kStride;
   for (int o = tid; o < G * D; o += kThreads) {
     const int g = o / D;
     float M = -INFINITY;
-    for (int s2 = 0; s2 < num_splits; ++s2) M = fmaxf(M, all[s2 * kStride + g]);
+    for (int s2 = 0; s2 < num_splits; ++s2) M = fmaxf(M, load_agent(all + s2 * kStride + g));
     float L = 0.0f, A = 0.0f;
     for (int s2 = 0; s2 < num_splits; ++s2) {
       const float* ps = all + s2 * kStride;
-      const float ms = ps[g];
+      const float ms = load_agent(ps + g);
       const float wgt = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-      L += ps[G + g] * wgt;
-      A += ps[2 * G + o] * wgt;
+      L += load_agent(ps + G + g) * wgt;
+      A += load_agent(ps + 2 * G + o) * wgt;
     }
     out[b * os_b + (int64_t)(h * G + g) * os_h + (o - g * D)].bits = (uint16_t)f32_to_bf16(A / L);
   }
-  if (tid == 0) counters[pair] = 0;
+  if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -561,12 +574,6 @@ __device__ __forceinline__ float same_chunk_row_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 }  // namespace
 
@@ -791,12 +798,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_wave_kernel(
       for (int r = 0; r < kRows16; ++r) A += s_buf[w][r][cidx][g][e];
     store_agent(mine + 2 * G + o, A);
   }
-  // every partial store has completed (device-coherent) before the ticket
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == num_splits - 1);
-  __syncthreads();
-  if (!s_last) return;
+  if (!take_last_ticket(&counters[pair], num_splits, &s_last)) return;
   const float* all = ws + (int64_t)pair * num_splits * kStride;
   for (int o = tid; o < kOut; o += kThreads) {
     const int g = o / D;
@@ -994,7 +996,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
     int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int group_size,
     int num_pairs, int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
-    int64_t rcs_d, const int64_t* __restrict__ rope_pos, const DecodePre pre) {
+    int64_t rcs_d, const int64_t* __restrict__ rope_pos, const DecodePre pre, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
   constexpr int NT = NW * kWave;
   constexpr int NWX = FUSED ? NW + 1 : NW;  // combine slots: the waves (+ the appended token)
   constexpr int KW = MfmaGroup<D>::kW;
@@ -1007,11 +1010,16 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   __shared__ float s_knew[FUSED ? D : 1], s_vnew[FUSED ? D : 1];  // appended row as stored (FP8 values)
   __shared__ int s_last;
 
+  // Work split: workgroup (pair, split) with the splits of a pair consecutive
+  // on one XCD (block ids are dispatched round-robin over the 8 XCDs, so the
+  // pair's partials meet in that XCD's L2).  Pair (b, h) takes ns = ceil(live
+  // / split_rows) splits (at most num_splits, the host's bound for the batch)
+  // of at most split_rows rows each; workgroups past ns exit after one load.
   const int lin = blockIdx.x;
   const int xcd = lin % kXcds;
-  const int slot = lin / kXcds;
-  const int pair = (slot / num_splits) * kXcds + xcd;
-  const int split = slot - (slot / num_splits) * num_splits;
+  const int slot_id = lin / kXcds;
+  const int pair = (slot_id / num_splits) * kXcds + xcd;
+  const int split = slot_id - (slot_id / num_splits) * num_splits;
   if (pair >= num_pairs) return;  // uniform per workgroup
   const int b = pair / num_kv_heads;
   const int h = pair - b * num_kv_heads;
@@ -1065,9 +1073,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   const int live = live_counts[b * lc_b + h * lc_h];
   const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
   const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
-  // this pair's split count: ceil(live / split_rows) (at most num_splits) when
-  // split_rows > 0, else num_splits; workgroups past it have nothing to do
-  const int ns = split_rows > 0 ? min(num_splits, max(1, (live + split_rows - 1) / split_rows)) : num_splits;
+  const int ns = min(num_splits, max(1, (live + split_rows - 1) / split_rows));
   if (split >= ns) return;  // uniform per workgroup
   const int per = (((live + ns - 1) / ns) + 63) & ~63;
   const int t0 = min(live, split * per);
@@ -1118,7 +1124,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
       const int jx = tid - 4 * kHalf;
       float y1, y2;
       rope_f32(fx1, fx2, fc, fsn, &y1, &y2);
-      const uint32_t k1 = f32_to_fp8(y1), k2 = f32_to_fp8(y2);
+      const float km = k_scale ? 1.0f / k_scale[h] : 1.0f;  // per-head FP8 scale: stored = x / scale
+      const uint32_t k1 = f32_to_fp8(y1 * km), k2 = f32_to_fp8(y2 * km);
       s_knew[jx] = fp8_to_f32(k1);
       s_knew[jx + kHalf] = fp8_to_f32(k2);
       if (split == 0 && app_slot >= 0) {
@@ -1127,7 +1134,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
       }
     } else if (tid < 5 * kHalf + D) {
       const int d = tid - 5 * kHalf;
-      const uint32_t v8 = f32_to_fp8(fx1);
+      const uint32_t v8 = f32_to_fp8(fx1 * (v_scale ? 1.0f / v_scale[h] : 1.0f));
       s_vnew[d] = fp8_to_f32(v8);
       if (split == 0 && app_slot >= 0) cv[(int64_t)app_slot * c_s + d] = (uint8_t)v8;
     }
@@ -1160,7 +1167,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   }
   __syncthreads();
 
-  const float qscale = scale * kLog2e;
+  // FP8 dequant in registers: the per-head K scale folds into the score scale,
+  // the V scale multiplies the output
+  const float qscale = scale * kLog2e * (k_scale ? k_scale[h] : 1.0f);
+  const float oscale = v_scale ? v_scale[h] : 1.0f;
   if constexpr (FUSED) {
     // the appended token as one more partial (m = its score, l = 1, acc = v),
     // by the last wave, which has the fewest groups
@@ -1291,7 +1301,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
       A += s_wacc[w][og][od] * f;
     }
     if (ns == 1) {
-      out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(A / L);
+      out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(A / L * oscale);
     } else {
       store_agent(mine + 2 * G + o, A);
       if (od == 0) {
@@ -1301,11 +1311,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     }
   }
   if (ns == 1) return;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&counters[pair], 1) == ns - 1);
-  __syncthreads();
-  if (!s_last) return;
+  if (!take_last_ticket(&counters[pair], ns, &s_last)) return;
   const float* all = ws + (int64_t)pair * num_splits * stride;
   for (int o = tid; o < n_out; o += NT) {
     const int og = o / D, od = o - og * D;
@@ -1337,7 +1343,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
       }
       M = bm;
     }
-    out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(Acc / L);
+    out[b * os_b + (int64_t)(h * G + og) * os_h + od].bits = (uint16_t)f32_to_bf16(Acc / L * oscale);
   }
   if (tid == 0) __hip_atomic_store(&counters[pair], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1380,7 +1386,7 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     int64_t bt_b, int64_t bt_h, int page_size, const int32_t* live_counts, int64_t lc_b, int64_t lc_h, void* out,
     int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads, int group_size,
     int head_dim, int num_splits, int split_rows, float scale, const float* rope_cos_sin, int64_t rcs_p,
-    int64_t rcs_d, const int64_t* rope_positions, void* stream) {
+    int64_t rcs_d, const int64_t* rope_positions, const float* k_scale, const float* v_scale, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > kMaxG) return (int)hipErrorInvalidValue;
   if (head_dim <= 0 || head_dim > kMaxD || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
     return (int)hipErrorInvalidValue;
@@ -1406,31 +1412,31 @@ FDMS_EXPORT int fdms_compact_decode_attention(
                         group_size == 4 || group_size == 8) && !fdms_force_generic_attention();
   const bool mfma_ok = tiled_ok && kv_dtype == kFP8 && group_size <= 4 && fdms_mfma_attention_enabled();
   if (mfma_ok) {
+    // split_rows: rows per split (rounded up to 64; 0 = one 64-row group per wave)
+    const int nw = 4;
+    const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
     const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
 #define FDMS_MFMA_ARGS                                                                                          \
   (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h,             \
       block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h, (bf16_t*)out, os_b, os_h, workspace,     \
-      counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, rope_cos_sin, rcs_p, rcs_d,        \
-      rope_positions, DecodePre{}
-#define FDMS_MFMA_LAUNCH(DD, NWV, PG)                                                                       \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, false>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
+      counters, num_kv_heads, group_size, pairs, num_splits, rows, scale, rope_cos_sin, rcs_p, rcs_d,              \
+      rope_positions, DecodePre{}, k_scale, v_scale
+#define FDMS_MFMA_LAUNCH(DD, PG)                                                                            \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
                      (hipStream_t)stream, FDMS_MFMA_ARGS)
     if (head_dim == 64) {
-      const char* ew = std::getenv("FASTDMS_AMD_ATTN_WAVES");
-      if (ew && ew[0] == '1' && ew[1] == '6') {
-        if (paged) FDMS_MFMA_LAUNCH(64, 16, true); else FDMS_MFMA_LAUNCH(64, 16, false);
-      } else {
-        if (paged) FDMS_MFMA_LAUNCH(64, 8, true); else FDMS_MFMA_LAUNCH(64, 8, false);
-      }
+      if (paged) FDMS_MFMA_LAUNCH(64, true); else FDMS_MFMA_LAUNCH(64, false);
     } else {
-      if (paged) FDMS_MFMA_LAUNCH(128, 8, true); else FDMS_MFMA_LAUNCH(128, 8, false);
+      if (paged) FDMS_MFMA_LAUNCH(128, true); else FDMS_MFMA_LAUNCH(128, false);
     }
 #undef FDMS_MFMA_LAUNCH
 #undef FDMS_MFMA_ARGS
     FDMS_LAUNCH_CHECK();
     return 0;
   }
+  // per-head FP8 scales: matrix-core kernel only
+  if (k_scale || v_scale) return (int)hipErrorInvalidValue;
   if (tiled_ok) {
     const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
@@ -1470,14 +1476,15 @@ FDMS_EXPORT int fdms_compact_decode_attention(
 // is rank live-1 of span (b, h) (prepare_decode_metadata: slot = base + live,
 // then live += 1).  Matrix-core path only: bf16 q/k/v, FP8 flat spans,
 // group_size <= 4, head_dim 64 / 128, 16-byte aligned rows.
-FDMS_EXPORT int fdms_fused_decode_attention(
+static int fused_decode_attention(
     const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
     int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
     const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
     float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
     int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
     int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
-    int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, void* stream) {
+    int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
+    const float* v_scale, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4) return (int)hipErrorInvalidValue;
   if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
     return (int)hipErrorInvalidValue;
@@ -1489,31 +1496,40 @@ FDMS_EXPORT int fdms_fused_decode_attention(
   if (num_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int pairs = batch * num_kv_heads;
   if (pairs > 65535) return (int)hipErrorInvalidValue;
-  const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
-  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                       slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                       positive_scale};
-  // waves per workgroup: 8 when few (seq, head) pairs must fill the chip, 4
-  // (head_dim 64) once there are several pairs per CU, so each wave runs more
-  // 64-row groups per workgroup prologue / combine
-  int nw = (head_dim == 64 && pairs >= 256) ? 4 : 8;
-  if (const char* e = std::getenv("FASTDMS_AMD_FUSED_WAVES")) {  // tuning override
-    const int v = std::atoi(e);
-    if (v == 8 || (v == 4 && head_dim == 64)) nw = v;
-  }
+  // 4 waves, 8 for head_dim 128 (the preprocess needs 2.5 * head_dim threads);
+  // split_rows as for fdms_compact_decode_attention
+  const int nw = head_dim == 64 ? 4 : 8;
+  const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
+  const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
 #define FDMS_FUSED_LAUNCH(DD, NWV)                                                                                \
   hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, false, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
                      (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,   \
                      c_s, base_offsets, bo_b, bo_h, nullptr, 0, 0, 0, 0, live_counts, lc_b, lc_h, (bf16_t*)out,     \
-                     os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, split_rows, scale, \
-                     nullptr, 0, 0, nullptr, pre)
-  if (head_dim == 64) {
-    if (nw == 4) FDMS_FUSED_LAUNCH(64, 4); else FDMS_FUSED_LAUNCH(64, 8);
-  } else {
-    FDMS_FUSED_LAUNCH(128, 8);
-  }
+                     os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, rows, scale,       \
+                     nullptr, 0, 0, nullptr, pre, k_scale, v_scale)
+  if (head_dim == 64) FDMS_FUSED_LAUNCH(64, 4); else FDMS_FUSED_LAUNCH(128, 8);
 #undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;
 }
+
+FDMS_EXPORT int fdms_fused_decode_attention(
+    const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+    const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+    float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
+    int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
+    int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
+    int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
+    const float* v_scale, void* stream) {
+  return fused_decode_attention(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
+                                slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
+                                positive_scale, compact_k, compact_v, c_s, base_offsets, bo_b, bo_h, live_counts, lc_b,
+                                lc_h, out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
+                                num_splits, split_rows, scale, k_scale, v_scale, stream);
+}
+

@@ -20,7 +20,8 @@ __global__ void dms_rope_store_kernel(QT* __restrict__ q, KT* __restrict__ k, co
                                       int64_t cs_d, int64_t c_s, int64_t sm_b, int64_t sm_h, int64_t ev_b,
                                       int64_t ev_h, int num_kv_heads, int group_size, int head_dim,
                                       float alpha_scale, float alpha_offset, float threshold, int positive_scale,
-                                      int store_q, int store_transient_k) {
+                                      int store_q, int store_transient_k, const float* __restrict__ k_scale,
+                                      const float* __restrict__ v_scale) {
   const int h = blockIdx.x % num_kv_heads;
   const int b = blockIdx.x / num_kv_heads;
   const int half = head_dim / 2;
@@ -58,13 +59,21 @@ __global__ void dms_rope_store_kernel(QT* __restrict__ q, KT* __restrict__ k, co
   }
   const int32_t slot = slot_mapping[b * sm_b + h * sm_h];
   if (slot >= 0) {
+    // per-head FP8 scales: stored = x * (1 / scale) (none: x)
     CT* dk = ck + (int64_t)slot * c_s;
     CT* dv = cv + (int64_t)slot * c_s;
-    st<CT>(dk + j, y1);
-    st<CT>(dk + j + half, y2);
+    const float km = inv_scale(k_scale, h);
+    st<CT>(dk + j, y1 * km);
+    st<CT>(dk + j + half, y2 * km);
     const KT* vh = v + b * vs_b + h * vs_h;
-    Copy<KT, CT>::run(dv + j, vh + j);
-    Copy<KT, CT>::run(dv + j + half, vh + j + half);
+    if (v_scale) {
+      const float vm = inv_scale(v_scale, h);
+      st<CT>(dv + j, ld<KT>(vh + j) * vm);
+      st<CT>(dv + j + half, ld<KT>(vh + j + half) * vm);
+    } else {
+      Copy<KT, CT>::run(dv + j, vh + j);
+      Copy<KT, CT>::run(dv + j + half, vh + j + half);
+    }
   }
 }
 
@@ -74,8 +83,9 @@ FDMS_EXPORT int fdms_dms_rope_store_compact_decode(
     void* compact_v, int compact_dtype, int64_t c_s, const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h,
     uint8_t* evict_out, int64_t ev_b, int64_t ev_h, const int64_t* positions, int batch, int num_kv_heads,
     int group_size, int head_dim, float alpha_scale, float alpha_offset, float threshold, int positive_scale,
-    int store_q, int store_transient_k, void* stream) {
+    int store_q, int store_transient_k, const float* k_scale, const float* v_scale, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || head_dim <= 0 || head_dim % 2) return (int)hipErrorInvalidValue;
+  if ((k_scale || v_scale) && compact_dtype != kFP8) return (int)hipErrorInvalidValue;
   if (head_dim > 512) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
   if (!q || !k || !v || !cos_sin || !compact_k || !compact_v || !slot_mapping || !evict_out || !positions)
@@ -88,7 +98,8 @@ FDMS_EXPORT int fdms_dms_rope_store_compact_decode(
                            (hipStream_t)stream, (QT*)q, (KT*)k, (const KT*)v, cos_sin, (CT*)compact_k,
                            (CT*)compact_v, slot_mapping, evict_out, positions, qs_b, qs_h, ks_b, ks_h, vs_b, vs_h,
                            cs_p, cs_d, c_s, sm_b, sm_h, ev_b, ev_h, num_kv_heads, group_size, head_dim, alpha_scale,
-                           alpha_offset, threshold, positive_scale, store_q, store_transient_k))));
+                           alpha_offset, threshold, positive_scale, store_q, store_transient_k, k_scale,
+                           v_scale))));
   FDMS_LAUNCH_CHECK();
   return 0;
 }
@@ -98,14 +109,21 @@ template <typename KT, typename CT>
 __global__ void store_compact_kernel(const KT* __restrict__ key, const KT* __restrict__ value, CT* __restrict__ ck,
                                      CT* __restrict__ cv, const int32_t* __restrict__ slot_mapping, int64_t ks_b,
                                      int64_t ks_h, int64_t vs_b, int64_t vs_h, int64_t c_s, int64_t sm_b,
-                                     int64_t sm_h, int num_kv_heads, int head_dim) {
+                                     int64_t sm_h, int num_kv_heads, int head_dim, const float* __restrict__ k_scale,
+                                     const float* __restrict__ v_scale) {
   const int h = blockIdx.x % num_kv_heads;
   const int b = blockIdx.x / num_kv_heads;
   const int32_t slot = slot_mapping[b * sm_b + h * sm_h];
   if (slot < 0) return;
+  const float km = inv_scale(k_scale, h), vm = inv_scale(v_scale, h);
   for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
-    Copy<KT, CT>::run(ck + (int64_t)slot * c_s + d, key + b * ks_b + h * ks_h + d);
-    Copy<KT, CT>::run(cv + (int64_t)slot * c_s + d, value + b * vs_b + h * vs_h + d);
+    if (k_scale || v_scale) {  // per-head FP8 scales: stored = x * (1 / scale)
+      st<CT>(ck + (int64_t)slot * c_s + d, ld<KT>(key + b * ks_b + h * ks_h + d) * km);
+      st<CT>(cv + (int64_t)slot * c_s + d, ld<KT>(value + b * vs_b + h * vs_h + d) * vm);
+    } else {
+      Copy<KT, CT>::run(ck + (int64_t)slot * c_s + d, key + b * ks_b + h * ks_h + d);
+      Copy<KT, CT>::run(cv + (int64_t)slot * c_s + d, value + b * vs_b + h * vs_h + d);
+    }
   }
 }
 
@@ -113,15 +131,18 @@ FDMS_EXPORT int fdms_store_compact_kvcache(const void* key, const void* value, i
                                            int64_t ks_h, int64_t vs_b, int64_t vs_h, void* compact_k,
                                            void* compact_v, int compact_dtype, int64_t c_s,
                                            const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, int batch,
-                                           int num_kv_heads, int head_dim, void* stream) {
+                                           int num_kv_heads, int head_dim, const float* k_scale,
+                                           const float* v_scale, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0) return (int)hipErrorInvalidValue;
+  if ((k_scale || v_scale) && compact_dtype != kFP8) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
   if (!key || !value || !compact_k || !compact_v || !slot_mapping) return (int)hipErrorInvalidValue;
   FDMS_DISPATCH_DTYPE(kv_dtype, KT,
     FDMS_DISPATCH_DTYPE(compact_dtype, CT,
       hipLaunchKernelGGL((store_compact_kernel<KT, CT>), dim3(batch * num_kv_heads), dim3(64), 0,
                          (hipStream_t)stream, (const KT*)key, (const KT*)value, (CT*)compact_k, (CT*)compact_v,
-                         slot_mapping, ks_b, ks_h, vs_b, vs_h, c_s, sm_b, sm_h, num_kv_heads, head_dim)));
+                         slot_mapping, ks_b, ks_h, vs_b, vs_h, c_s, sm_b, sm_h, num_kv_heads, head_dim, k_scale,
+                         v_scale)));
   FDMS_LAUNCH_CHECK();
   return 0;
 }

@@ -184,6 +184,35 @@ __device__ __forceinline__ void rope_f32(float x1, float x2, float c, float s, f
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Cross-workgroup handoff of split partials.  On gfx942 / gfx950 an
+// agent-scope fence writes back and invalidates the whole L2 of the XCD
+// (buffer_wbl2 sc1 / buffer_inv sc1), which costs microseconds per call; the
+// split kernels instead keep the handoff coherent through the accesses
+// themselves and order it with workgroup-scope fences, the protocol AMD's
+// rocPRIM look-back scan uses on these chips:
+//   producer: partials written with relaxed agent-scope atomic stores (sc1:
+//     they bypass the non-coherent cache levels), then handoff_release()
+//     (workgroup release fence + wait until every vector-memory operation of
+//     the thread has completed), then the ticket, a relaxed agent-scope
+//     atomic add performed at the device coherence point;
+//   consumer (the workgroup that takes the last ticket): handoff_acquire()
+//     (wait for the ticket + workgroup acquire fence, so no later load is
+//     issued before it), then relaxed agent-scope atomic loads (sc1: served
+//     from the coherence point, never a stale cache line).
+// The stores have completed at the coherence point before the ticket is
+// taken, and the loads are issued after the last ticket returned.
+__device__ __forceinline__ void handoff_release() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+}
+__device__ __forceinline__ void handoff_acquire() {
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+__device__ __forceinline__ int ticket_add(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
 }  // namespace fdms

@@ -539,10 +539,12 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int r = 0; r < 4; ++r) store_agent(mine + a * 256 + lane * 4 + r, t[a][r]);
-    __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) s_last = (atomicAdd(&counters[strip], 1) == ksplit - 1);
+    // handoff (fdms_common.h): stores completed before the ticket, loads after it
+    handoff_release();
+    if (lane == 0) s_last = (ticket_add(&counters[strip]) == ksplit - 1);
     __builtin_amdgcn_wave_barrier();
     if (!s_last) return;
+    handoff_acquire();
     const float* all = ws + (int64_t)strip * ksplit * (NA * 256);
 #pragma unroll
     for (int a = 0; a < NA; ++a) t[a] = f32x4{0.f, 0.f, 0.f, 0.f};

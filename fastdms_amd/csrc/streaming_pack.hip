@@ -131,7 +131,8 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
     int64_t rk_t, int64_t rk_h, const int32_t* __restrict__ base, int64_t bs_b, int64_t bs_h, TO* __restrict__ ck,
     TO* __restrict__ cv, int64_t cs_s, int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta,
     const int32_t* __restrict__ meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s, int64_t em_b, int64_t em_h,
-    int64_t em_s, int window, int num_kv_heads, int head_dim) {
+    int64_t em_s, int window, int num_kv_heads, int head_dim, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale) {
   __shared__ int s_wave[kChunk / kWave];
   __shared__ int64_t s_src[kChunk];
   __shared__ int64_t s_dst[kChunk];
@@ -143,6 +144,7 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
   // per-block scalars first: their loads overlap the evict load
   const int64_t row = meta_rows ? meta_rows[b] : b;
   const int64_t span0 = base[b * bs_b + h * bs_h];
+  const float kmul = inv_scale(k_scale, h), vmul = inv_scale(v_scale, h);
   const int chunk0 = FUSED ? block_offsets[b * bo_b + h * bo_h + c * bo_c] : 0;
   const int t = c * kChunk + threadIdx.x;
   const bool valid = t < sp.len;
@@ -189,8 +191,8 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
       if (u0 + i * kChunk < n) {
-        *reinterpret_cast<Vec<TO, VEC>*>(ck + dst[i]) = convert_vec<TI, TO, VEC>(kr[i]);
-        *reinterpret_cast<Vec<TO, VEC>*>(cv + dst[i]) = convert_vec<TI, TO, VEC>(vr[i]);
+        *reinterpret_cast<Vec<TO, VEC>*>(ck + dst[i]) = convert_vec_scaled<TI, TO, VEC>(kr[i], kmul);
+        *reinterpret_cast<Vec<TO, VEC>*>(cv + dst[i]) = convert_vec_scaled<TI, TO, VEC>(vr[i], vmul);
       }
     }
   }
@@ -223,7 +225,7 @@ static int launch_scatter(const void* k, const void* v, int kv_dtype, int64_t ks
                           int64_t bs_h, void* ck, void* cv, int compact_dtype, int64_t cs_s, int32_t* positions,
                           uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s,
                           int64_t em_b, int64_t em_h, int64_t em_s, int window, int num_kv_heads, int head_dim,
-                          int max_chunks, int vec, void* stream) {
+                          int max_chunks, int vec, const float* k_scale, const float* v_scale, void* stream) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_chunks <= 0) return (int)hipErrorInvalidValue;
   if (vec <= 0 || head_dim % vec != 0) return (int)hipErrorInvalidValue;
   if (!k || !v || !evict || !base || !ck || !cv || !positions || !evict_meta) return (int)hipErrorInvalidValue;
@@ -235,7 +237,7 @@ static int launch_scatter(const void* k, const void* v, int kv_dtype, int64_t ks
                            (const TI*)k, (const TI*)v, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
                            single_len, bo, bo_b, bo_h, bo_c, keep, kp_t, kp_h, rank, rk_t, rk_h, base, bs_b, bs_h,
                            (TO*)ck, (TO*)cv, cs_s, positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h,
-                           em_s, window, num_kv_heads, head_dim))));
+                           em_s, window, num_kv_heads, head_dim, k_scale, v_scale))));
   FDMS_LAUNCH_CHECK();
   return 0;
 }
@@ -247,13 +249,13 @@ FDMS_EXPORT int fdms_streaming_pack_rank_scatter(
     int64_t bs_b, int64_t bs_h, void* compact_k, void* compact_v, int compact_dtype, int64_t cs_s,
     int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s,
     int64_t em_b, int64_t em_h, int64_t em_s, int window, int num_kv_heads, int head_dim, int max_chunks, int vec,
-    void* stream) {
+    const float* k_scale, const float* v_scale, void* stream) {
   if (!block_offsets) return (int)hipErrorInvalidValue;
   return launch_scatter<true>(k, v, kv_dtype, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu_seqlens, single_start,
                               single_len, num_seqs, block_offsets, bo_b, bo_h, bo_c, nullptr, 0, 0, nullptr, 0, 0,
                               base, bs_b, bs_h, compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta,
                               meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s, window, num_kv_heads, head_dim,
-                              max_chunks, vec, stream);
+                              max_chunks, vec, k_scale, v_scale, stream);
 }
 
 FDMS_EXPORT int fdms_streaming_pack_scatter(
@@ -262,12 +264,13 @@ FDMS_EXPORT int fdms_streaming_pack_scatter(
     const uint8_t* seq_evict, int64_t es_t, int64_t es_h, const int32_t* base, int64_t bs_h, void* compact_k,
     void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions, int64_t tp_h, int64_t tp_s,
     uint8_t* evict_meta, int64_t em_h, int64_t em_s, int start, int seq_len, int num_kv_heads, int head_dim, int vec,
-    void* stream) {
+    const float* k_scale, const float* v_scale, void* stream) {
   if (!keep || !rank) return (int)hipErrorInvalidValue;
   if (seq_len <= 0) return 0;
   const int max_chunks = (seq_len + kChunk - 1) / kChunk;
   return launch_scatter<false>(k, v, kv_dtype, ks_t, ks_h, vs_t, vs_h, seq_evict, es_t, es_h, nullptr, start,
                                seq_len, 1, nullptr, 0, 0, 0, keep, kp_t, kp_h, rank, rk_t, rk_h, base, 0, bs_h,
                                compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta, nullptr, 0, tp_h,
-                               tp_s, 0, em_h, em_s, 0, num_kv_heads, head_dim, max_chunks, vec, stream);
+                               tp_s, 0, em_h, em_s, 0, num_kv_heads, head_dim, max_chunks, vec, k_scale, v_scale,
+                               stream);
 }

@@ -78,8 +78,10 @@ def _pack_vec(k, v, compact_k, head_dim):
 
 
 def _streaming_pack_rank_scatter_hip(*, k, v, seq_evict, block_offsets, compact_k, compact_v, token_positions,
-                                     evict_mask, base_offsets, start: int, seq_len: int, window_size: int) -> None:
-    """compact_kv.py:299-361 (fused rank scatter of one sequence)."""
+                                     evict_mask, base_offsets, start: int, seq_len: int, window_size: int,
+                                     k_scale=None, v_scale=None) -> None:
+    """compact_kv.py:299-361 (fused rank scatter of one sequence); optional
+    per-kv-head FP8 scales [Hkv] (stored = x / scale; no reference counterpart)."""
     if seq_len <= 0:
         return
     num_kv_heads, head_dim = k.shape[1], k.shape[2]
@@ -97,11 +99,12 @@ def _streaming_pack_rank_scatter_hip(*, k, v, seq_evict, block_offsets, compact_
              base_offsets.data_ptr(), 0, base_offsets.stride(0), compact_k.data_ptr(), compact_v.data_ptr(),
              nat.dtype_code(compact_k.dtype), compact_k.stride(0), token_positions.data_ptr(), em.data_ptr(), None,
              0, token_positions.stride(0), token_positions.stride(1), 0, em.stride(0), em.stride(1),
-             int(window_size), num_kv_heads, head_dim, chunks, _pack_vec(k, v, compact_k, head_dim), nat.stream())
+             int(window_size), num_kv_heads, head_dim, chunks, _pack_vec(k, v, compact_k, head_dim),
+             nat.ptr(k_scale), nat.ptr(v_scale), nat.stream())
 
 
 def _streaming_pack_scatter_hip(*, k, v, keep, rank, seq_evict, compact_k, compact_v, token_positions, evict_mask,
-                                base_offsets, start: int, seq_len: int) -> None:
+                                base_offsets, start: int, seq_len: int, k_scale=None, v_scale=None) -> None:
     """compact_kv.py:364-423 (scatter with precomputed keep / rank)."""
     if seq_len <= 0:
         return
@@ -119,7 +122,7 @@ def _streaming_pack_scatter_hip(*, k, v, keep, rank, seq_evict, compact_k, compa
              base_offsets.stride(0), compact_k.data_ptr(), compact_v.data_ptr(), nat.dtype_code(compact_k.dtype),
              compact_k.stride(0), token_positions.data_ptr(), token_positions.stride(0), token_positions.stride(1),
              em.data_ptr(), em.stride(0), em.stride(1), int(start), int(seq_len), num_kv_heads, head_dim,
-             _pack_vec(k, v, compact_k, head_dim), nat.stream())
+             _pack_vec(k, v, compact_k, head_dim), nat.ptr(k_scale), nat.ptr(v_scale), nat.stream())
 
 
 # ---------------------------------------------------------------------------
@@ -177,7 +180,7 @@ class CompactKVManager:
                  head_dim: int | None = None, compact_dtype: torch.dtype | None = None,
                  per_layer_storage: bool = False, layer_major_metadata: bool = False,
                  max_active_seqs: int | None = None, preallocate: bool = False,
-                 decode_reserve_tokens: int | None = None):
+                 decode_reserve_tokens: int | None = None, fp8_scales: str = "unit"):
         if capacity_tokens <= 0:
             raise ValueError(f"capacity_tokens must be positive, got {capacity_tokens}")
         self.num_layers = num_layers
@@ -226,6 +229,21 @@ class CompactKVManager:
         self.compact_v: torch.Tensor | None = None
         self._layer_ptrs: tuple[torch.Tensor, torch.Tensor] | None = None
         self.storage_version = 0
+        # Per-(layer, kv head) FP8 scales (no reference counterpart; the
+        # reference stores with a bare cast, i.e. scale 1): kv_scales[l, 0] for
+        # K and [l, 1] for V, stored = x / scale, dequantised in the attention
+        # kernels.  "unit": no tables (the reference's numerics); "calibrate":
+        # each layer's scales are set at its first prefill pack from the prompt's
+        # post-RoPE K / V (amax / 224, i.e. twice the range seen), then frozen.
+        if fp8_scales not in ("unit", "calibrate"):
+            raise ValueError(f"fp8_scales must be 'unit' or 'calibrate', got {fp8_scales!r}")
+        self.fp8_scales = fp8_scales
+        self.kv_scales: torch.Tensor | None = None
+        self._scales_calibrated = [False] * num_layers
+        if fp8_scales != "unit":
+            if compact_dtype != getattr(torch, "float8_e4m3fn", None):
+                raise ValueError("per-head KV scales need FP8 compact storage")
+            self.kv_scales = torch.ones((num_layers, 2, num_kv_heads), device=self.device, dtype=torch.float32)
         if preallocate and per_layer_storage:
             for layer_id in range(num_layers):
                 self._ensure_layer_storage(layer_id, capacity_tokens)
@@ -244,6 +262,36 @@ class CompactKVManager:
             if self.compact_k_per_layer[layer_id] is not None:
                 module.compact_k_cache = self.compact_k_per_layer[layer_id]
                 module.compact_v_cache = self.compact_v_per_layer[layer_id]
+            module.compact_k_scale, module.compact_v_scale = self.layer_kv_scales(layer_id)
+
+    def layer_kv_scales(self, layer_id: int) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+        """(K scales, V scales) [Hkv] of a layer, or (None, None) without tables."""
+        if self.kv_scales is None:
+            return None, None
+        return self.kv_scales[layer_id, 0], self.kv_scales[layer_id, 1]
+
+    def set_kv_scales(self, scales: torch.Tensor) -> None:
+        """Set every layer's FP8 scales ([num_layers, 2, num_kv_heads], > 0)
+        before any sequence is packed; the tables keep their storage, so captured
+        graphs stay valid."""
+        if self.kv_scales is None:
+            raise RuntimeError("the manager was built without KV scale tables (fp8_scales='unit')")
+        if self.seq_states:
+            raise RuntimeError("KV scales must be set before any sequence is packed")
+        if tuple(scales.shape) != tuple(self.kv_scales.shape):
+            raise ValueError(f"expected scales {tuple(self.kv_scales.shape)}, got {tuple(scales.shape)}")
+        self.kv_scales.copy_(scales.to(device=self.device, dtype=torch.float32))
+        self._scales_calibrated = [True] * self.num_layers
+
+    def _calibrate_layer_scales(self, layer_id: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """First pack of a layer in "calibrate" mode: scale = amax / 224 per
+        kv head (on the device, no host sync); an all-zero head keeps 1."""
+        if self.fp8_scales != "calibrate" or self._scales_calibrated[layer_id]:
+            return
+        for i, x in enumerate((k, v)):
+            amax = x.detach().abs().amax(dim=(0, 2)).float()
+            self.kv_scales[layer_id, i].copy_(torch.where(amax > 0, amax / 224.0, torch.ones_like(amax)))
+        self._scales_calibrated[layer_id] = True
 
     def _ensure_layer_storage(self, layer_id: int, min_tokens: int):
         """compact_kv.py:661-695: grow to a 256-token multiple, keep old rows."""
@@ -511,6 +559,8 @@ class CompactKVManager:
                 st.base_offsets[layer_id].copy_(bases_t[i])
                 st.range_capacity[layer_id].copy_(sizes_t[i])
         vec = _pack_vec(k, v, compact_k, D)
+        self._calibrate_layer_scales(layer_id, k, v)
+        ks, vs = self.layer_kv_scales(layer_id)
         if rows is not None:
             pos_l = self.layer_major_token_positions[layer_id]
             ev_l = self.layer_major_evict_mask[layer_id].view(torch.uint8)
@@ -521,7 +571,7 @@ class CompactKVManager:
                      compact_k.data_ptr(), compact_v.data_ptr(), nat.dtype_code(compact_k.dtype),
                      compact_k.stride(0), pos_l.data_ptr(), ev_l.data_ptr(), rows.data_ptr(), pos_l.stride(0),
                      pos_l.stride(1), pos_l.stride(2), ev_l.stride(0), ev_l.stride(1), ev_l.stride(2),
-                     int(window_size), H, D, max_chunks, vec, nat.stream())
+                     int(window_size), H, D, max_chunks, vec, nat.ptr(ks), nat.ptr(vs), nat.stream())
             self.layer_major_live_counts[layer_id].index_copy_(0, rows_l, live)
         else:
             for i, st in enumerate(states):
@@ -535,7 +585,7 @@ class CompactKVManager:
                          offsets.stride(2), bases_t[i].data_ptr(), 0, 1, compact_k.data_ptr(), compact_v.data_ptr(),
                          nat.dtype_code(compact_k.dtype), compact_k.stride(0), pos.data_ptr(), em.data_ptr(), None,
                          0, pos.stride(0), pos.stride(1), 0, em.stride(0), em.stride(1), int(window_size), H, D,
-                         -(-lens[i] // PACK_CHUNK), vec, nat.stream())
+                         -(-lens[i] // PACK_CHUNK), vec, nat.ptr(ks), nat.ptr(vs), nat.stream())
                 st.live_counts[layer_id].copy_(live[i])
         for i, st in enumerate(states):
             if lens[i] > 0:

@@ -153,7 +153,7 @@ class ModelRunner:
             target_live_tokens_per_seq=c.compact_kv_target_live_tokens_per_seq, head_dim=self.head_dim,
             compact_dtype=self.kv_dtype, per_layer_storage=True, layer_major_metadata=True,
             max_active_seqs=self.max_num_seqs, preallocate=True,
-            decode_reserve_tokens=c.compact_decode_reserve_tokens)
+            decode_reserve_tokens=c.compact_decode_reserve_tokens, fp8_scales=c.compact_kv_fp8_scales)
         attn_modules = []
         for layer_id, layer in enumerate(self.model.model.layers):
             layer.self_attn.attn.layer_id = layer_id

@@ -60,6 +60,8 @@ class Attention(nn.Module):
         self.num_kv_heads = num_kv_heads
         self.k_cache = self.v_cache = torch.tensor([])
         self.compact_k_cache = self.compact_v_cache = torch.tensor([])
+        # per-kv-head FP8 scales of this layer's arenas ([Hkv] fp32 views) or None
+        self.compact_k_scale = self.compact_v_scale = None
         self.layer_id = -1
 
     def forward(self, q, k, v, *, compact_append_stored: bool = False, compact_q_rope: bool = False,
@@ -76,11 +78,13 @@ class Attention(nn.Module):
             base, live = base[self.layer_id], live[self.layer_id]
             slot = None if slot is None else slot[self.layer_id]
         if slot is not None and not compact_append_stored:
-            store_compact_kvcache(k, v, self.compact_k_cache, self.compact_v_cache, slot)
+            store_compact_kvcache(k, v, self.compact_k_cache, self.compact_v_cache, slot,
+                                  k_scale=self.compact_k_scale, v_scale=self.compact_v_scale)
         return compact_decode_attention(q, self.compact_k_cache, self.compact_v_cache, base, live, scale=self.scale,
                                         max_live_count=ctx.compact_max_live_count,
                                         q_rope_positions=positions if compact_q_rope else None,
-                                        q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None)
+                                        q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None,
+                                        k_scale=self.compact_k_scale, v_scale=self.compact_v_scale)
 
     def forward_fused_decode(self, q, k, v, positions, cos_sin_cache, evict_out, alpha_scale, alpha_offset):
         """Decode step of this layer in one launch: DMS decision, RoPE, FP8
@@ -92,4 +96,5 @@ class Attention(nn.Module):
         return fused_dms_rope_store_compact_decode_attention(
             q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, slot, evict_out, positions, base,
             live, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
-            scale=self.scale, max_live_count=ctx.compact_max_live_count)
+            scale=self.scale, max_live_count=ctx.compact_max_live_count, k_scale=self.compact_k_scale,
+            v_scale=self.compact_v_scale)

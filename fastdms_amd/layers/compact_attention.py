@@ -92,8 +92,22 @@ def attention_workspace(device: torch.device, n_floats: int, n_counters: int):
 _MFMA_CAP_SPLITS = 64
 
 
-def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size: int, head_dim: int) -> None:
-    """Allocate the split workspace for the largest split count choose_num_splits
+def mfma_split_rows(pairs: int, waves: int = 4) -> int:
+    """Rows per split of the matrix-core kernel (measured on MI355X over
+    8 / 32 / 128 sequences x 8 KV heads, fused decode kernel): with at most
+    128 (seq, kv head) pairs two 64-row groups per wave (a decode step there
+    is a chain of memory round trips and more, smaller splits only add merge
+    work), beyond that 2048 rows, about one workgroup per pair, since every
+    split pays a fixed metadata / q / combine / merge chain of several
+    microseconds."""
+    if pairs <= 128:
+        return 128 * waves
+    return 2048
+
+
+def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size: int, head_dim: int,
+                                max_live: int = 1 << 17) -> None:
+    """Allocate the split workspace for the largest split count attention_split_plan
     can return for up to max_pairs (seq, kv head) pairs."""
     target = _TARGET_BLOCKS_PER_CU * _num_cus(device)
     worst = max(p * max(min(1024, -(-target // p)), _MFMA_CAP_SPLITS) for p in range(1, max_pairs + 1))
@@ -112,16 +126,17 @@ def mfma_attention_path(q: torch.Tensor, kv: torch.Tensor, group: int) -> bool:
             and kv.stride(0) % 16 == 0 and kv.data_ptr() % 16 == 0)
 
 
-def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: bool) -> tuple[int, int]:
+def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: bool,
+                         waves: int = 4) -> tuple[int, int]:
     """(num_splits, split_rows) for fdms_compact_decode_attention.
 
-    Matrix-core kernel: a pair gets one workgroup per `split_rows` live rows
-    (2048 with >= 32 pairs, 512 with fewer), decided per pair inside the
-    kernel, because merging splits costs three memory round trips while the
-    per-pair work at decode sizes is small; num_splits only bounds it from
-    the batch's live bound.  Other kernels: choose_num_splits, even splits."""
+    Matrix-core kernel: a pair gets one workgroup per split_rows live rows
+    (mfma_split_rows), decided per pair inside the kernel from the step's live
+    count, so a captured graph stays valid as spans grow; num_splits only
+    bounds it from the batch's live bound (at most 64).  Other kernels:
+    choose_num_splits, even splits."""
     if mfma:
-        rows = 2048 if pairs >= 32 else 512
+        rows = mfma_split_rows(pairs, waves)
         env = os.environ.get("FASTDMS_AMD_ATTN_SPLIT_ROWS", "").strip()
         if env.isdigit() and int(env) >= 64:  # tuning override
             rows = int(env)
@@ -139,19 +154,34 @@ def choose_num_splits(device: torch.device, pairs: int, max_live: int) -> int:
     return int(min(s, 1024))
 
 
+def _scale_table(t, num_kv_heads: int, what: str):
+    """A per-kv-head FP8 scale table [Hkv] fp32 (contiguous) or None."""
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or t.shape != (num_kv_heads,) or t.stride(0) != 1:
+        raise ValueError(f"{what} must be a contiguous float32 [{num_kv_heads}] tensor")
+    return t
+
+
 def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, live_counts, scale, max_live,
-                      rope_positions=None, rope_cache=None, out=None):
+                      rope_positions=None, rope_cache=None, out=None, k_scale=None, v_scale=None):
     batch, num_q_heads, head_dim = q.shape
     num_kv_heads = live_counts.shape[1]
     group = num_q_heads // num_kv_heads
     if out is None:
         out = torch.empty_like(q)
     pairs = batch * num_kv_heads
-    splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma_attention_path(q, kv_k, group))
+    mfma = mfma_attention_path(q, kv_k, group)
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma)
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     if q.stride(2) != 1 or kv_k.stride(1) != 1 or out.stride(2) != 1:
         raise ValueError("compact attention needs a contiguous head_dim axis")
     bt = block_tables
+    k_scale = _scale_table(k_scale, num_kv_heads, "k_scale")
+    v_scale = _scale_table(v_scale, num_kv_heads, "v_scale")
+    if (k_scale is not None or v_scale is not None) and not mfma:
+        raise ValueError("per-head FP8 KV scales need the matrix-core path (bf16 q, FP8 K/V, group <= 4, "
+                         "head_dim 64 / 128)")
     nat.call("fdms_compact_decode_attention", q.data_ptr(), nat.dtype_code(q.dtype), q.stride(0), q.stride(1),
              kv_k.data_ptr(), kv_v.data_ptr(), nat.dtype_code(kv_k.dtype), kv_k.stride(0),
              nat.ptr(base_offsets), 0 if base_offsets is None else base_offsets.stride(0),
@@ -160,7 +190,8 @@ def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, l
              live_counts.data_ptr(), live_counts.stride(0), live_counts.stride(1), out.data_ptr(), out.stride(0),
              out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads, group, head_dim, splits,
              split_rows, float(scale), nat.ptr(rope_cache), 0 if rope_cache is None else rope_cache.stride(0),
-             0 if rope_cache is None else rope_cache.stride(2), nat.ptr(rope_positions), nat.stream())
+             0 if rope_cache is None else rope_cache.stride(2), nat.ptr(rope_positions), nat.ptr(k_scale),
+             nat.ptr(v_scale), nat.stream())
     return out
 
 
@@ -168,8 +199,11 @@ def compact_decode_attention(q: torch.Tensor, compact_k: torch.Tensor, compact_v
                              base_offsets: torch.Tensor, live_counts: torch.Tensor, scale: float | None = None,
                              max_live_count: int | None = None, block_n: int = 128, grouped: bool = True,
                              q_rope_positions: torch.Tensor | None = None,
-                             q_rope_cos_sin_cache: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode attention over flat compact K/V spans (compact_attention.py:1116-1336)."""
+                             q_rope_cos_sin_cache: torch.Tensor | None = None, *, k_scale: torch.Tensor | None = None,
+                             v_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention over flat compact K/V spans (compact_attention.py:1116-1336).
+    k_scale / v_scale: optional per-kv-head FP8 scales [Hkv] (K = fp8 * k_scale,
+    V = fp8 * v_scale; no reference counterpart, the reference casts bare)."""
     if q.ndim != 3:
         raise ValueError(f"expected q as [batch, q_heads, head_dim], got {q.shape}")
     if compact_k.shape != compact_v.shape:
@@ -219,13 +253,14 @@ def compact_decode_attention(q: torch.Tensor, compact_k: torch.Tensor, compact_v
     return _attention_launch(q, compact_k, compact_v, base_offsets=base_offsets, block_tables=None, page_size=0,
                              live_counts=live_counts, scale=scale, max_live=max_live_count,
                              rope_positions=q_rope_positions if inline else None,
-                             rope_cache=q_rope_cos_sin_cache if inline else None)
+                             rope_cache=q_rope_cos_sin_cache if inline else None, k_scale=k_scale, v_scale=v_scale)
 
 
 def compact_decode_attention_paged(q: torch.Tensor, kv_k: torch.Tensor, kv_v: torch.Tensor,
                                    block_tables: torch.Tensor, live_counts: torch.Tensor, page_size: int,
                                    scale: float | None = None, max_live_count: int | None = None,
-                                   out: torch.Tensor | None = None) -> torch.Tensor:
+                                   out: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+                                   v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """Same attention over paged compact storage: rank r of (b, h) lives at
     block_tables[b, h, r // page_size] * page_size + r % page_size.
     (No reference counterpart: the reference stores flat spans.)"""
@@ -245,12 +280,14 @@ def compact_decode_attention_paged(q: torch.Tensor, kv_k: torch.Tensor, kv_v: to
         block_tables = block_tables.contiguous()
     return _attention_launch(q, kv_k, kv_v, base_offsets=None, block_tables=block_tables, page_size=page_size,
                              live_counts=live_counts.to(dtype=torch.int32), scale=scale, max_live=max_live_count,
-                             out=out)
+                             out=out, k_scale=k_scale, v_scale=v_scale)
 
 
 def store_compact_kvcache(key: torch.Tensor, value: torch.Tensor, compact_k: torch.Tensor, compact_v: torch.Tensor,
-                          slot_mapping: torch.Tensor) -> None:
-    """compact[slot] = key/value for slot >= 0 (compact_attention.py:968-1007)."""
+                          slot_mapping: torch.Tensor, *, k_scale: torch.Tensor | None = None,
+                          v_scale: torch.Tensor | None = None) -> None:
+    """compact[slot] = key/value for slot >= 0 (compact_attention.py:968-1007);
+    with per-kv-head FP8 scales the stored value is x / scale."""
     if key.shape != value.shape:
         raise ValueError(f"key/value shape mismatch: {key.shape} != {value.shape}")
     if key.ndim != 3:
@@ -269,7 +306,9 @@ def store_compact_kvcache(key: torch.Tensor, value: torch.Tensor, compact_k: tor
     nat.call("fdms_store_compact_kvcache", key.data_ptr(), value.data_ptr(), nat.dtype_code(key.dtype),
              key.stride(0), key.stride(1), value.stride(0), value.stride(1), compact_k.data_ptr(),
              compact_v.data_ptr(), nat.dtype_code(compact_k.dtype), compact_k.stride(0), slot_mapping.data_ptr(),
-             slot_mapping.stride(0), slot_mapping.stride(1), batch, num_kv_heads, head_dim, nat.stream())
+             slot_mapping.stride(0), slot_mapping.stride(1), batch, num_kv_heads, head_dim,
+             nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
 
 
 def fused_dms_rope_store_compact_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -277,8 +316,10 @@ def fused_dms_rope_store_compact_decode(q: torch.Tensor, k: torch.Tensor, v: tor
                                         compact_v: torch.Tensor, slot_mapping: torch.Tensor,
                                         evict_out: torch.Tensor, positions: torch.Tensor, *, num_kv_heads: int,
                                         alpha_scale: float, alpha_offset: float, store_q: bool = True,
-                                        store_transient_k: bool = True) -> None:
-    """Decode DMS extraction + RoPE + compact append (compact_attention.py:1010-1113)."""
+                                        store_transient_k: bool = True, k_scale: torch.Tensor | None = None,
+                                        v_scale: torch.Tensor | None = None) -> None:
+    """Decode DMS extraction + RoPE + compact append (compact_attention.py:1010-1113);
+    with per-kv-head FP8 scales the appended rows are x / scale."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError("expected q/k/v as [batch, heads, head_dim]")
     if k.shape != v.shape:
@@ -321,7 +362,8 @@ def fused_dms_rope_store_compact_decode(q: torch.Tensor, k: torch.Tensor, v: tor
              slot_mapping.data_ptr(), slot_mapping.stride(0), slot_mapping.stride(1), evict_out.data_ptr(),
              evict_out.stride(0), evict_out.stride(1), positions.data_ptr(), batch, num_kv_heads,
              num_q_heads // num_kv_heads, head_dim, scale, offset, thr, positive, int(bool(store_q)),
-             int(bool(store_transient_k)), nat.stream())
+             int(bool(store_transient_k)), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
 
 
 def fused_decode_attention_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -339,13 +381,16 @@ def fused_dms_rope_store_compact_decode_attention(
         compact_v: torch.Tensor, slot_mapping: torch.Tensor, evict_out: torch.Tensor, positions: torch.Tensor,
         base_offsets: torch.Tensor, live_counts: torch.Tensor, *, num_kv_heads: int, alpha_scale: float,
         alpha_offset: float, scale: float | None = None, max_live_count: int | None = None,
-        out: torch.Tensor | None = None) -> torch.Tensor:
+        out: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
+        v_scale: torch.Tensor | None = None) -> torch.Tensor:
     """One launch for fused_dms_rope_store_compact_decode(store_q=False,
     store_transient_k=False) followed by compact_decode_attention with the q
     RoPE done in the kernel (the reference's inline-q-RoPE decode order,
     llama.py:112-134).  q, k, v are the raw rows of the step and are not
     modified; ``live_counts`` already counts the appended token (rank
-    live - 1, stored at ``slot_mapping``).  Returns the attention output."""
+    live - 1, stored at ``slot_mapping``).  k_scale / v_scale: optional
+    per-kv-head FP8 scales [Hkv] for the append and the dequant.  Returns the
+    attention output."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
         raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
     batch, num_q_heads, head_dim = q.shape
@@ -375,7 +420,8 @@ def fused_dms_rope_store_compact_decode_attention(
     if out.stride(2) != 1:
         raise ValueError("out needs a contiguous head_dim axis")
     pairs = batch * num_kv_heads
-    splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True)
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True,
+                                              waves=4 if head_dim == 64 else 8)
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     slot_mapping = slot_mapping.to(dtype=torch.int32)
     live_counts = live_counts.to(dtype=torch.int32)
@@ -390,7 +436,9 @@ def fused_dms_rope_store_compact_decode_attention(
              compact_k.data_ptr(), compact_v.data_ptr(), compact_k.stride(0), base_offsets.data_ptr(),
              base_offsets.stride(0), base_offsets.stride(1), live_counts.data_ptr(), live_counts.stride(0),
              live_counts.stride(1), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), counters.data_ptr(),
-             batch, num_kv_heads, group, head_dim, splits, split_rows, float(scale), nat.stream())
+             batch, num_kv_heads, group, head_dim, splits, split_rows, float(scale),
+             nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
     return out
 
 

@@ -85,6 +85,8 @@ class ParallelLMHead(VocabParallelEmbedding, LinearBase):
     """The LM head as a bias-free linear [vocab, hidden] (LinearBase's FP8 /
     INT4 weights and kernels) that also serves as the tied embedding table."""
 
+    is_lm_head = True
+
     def __init__(self, num_embeddings: int, embedding_dim: int, bias: bool = False):
         assert not bias
         LinearBase.__init__(self, embedding_dim, num_embeddings, bias=False)

@@ -535,7 +535,9 @@ def convert_linear_modules_to_fp8(module: nn.Module) -> int:
     full = qe.fp8_attention_full_enabled()
     converted = 0
     for name, child in module.named_modules():
-        if not isinstance(child, LinearBase):
+        # the LM head is not a LinearBase in the reference (embed_head.py:450):
+        # it is converted only by FASTDMS_FP8_LM_HEAD (model_runner.py:76-93)
+        if not isinstance(child, LinearBase) or getattr(child, "is_lm_head", False):
             continue
         is_attn = ".self_attn." in name
         use_shadow = shadow and is_attn and not full

@@ -52,6 +52,10 @@ class ModelConfig:
     qk_norm: bool = False
     hidden_act: str = "silu"
     dtype: str = "bfloat16"
+    # synthetic-weights option (no checkpoint counterpart): > 0 plants a token
+    # successor table in an untied LM head, so that greedy decisions carry a
+    # wide logit margin (see models/synthetic.py)
+    successor_margin: float = 0.0
 
 
 def _fused_linear(lin: LinearBase, x: torch.Tensor, prologue: int, norm: RMSNorm | None = None,
@@ -154,7 +158,8 @@ class LlamaAttention(nn.Module):
                     q, k, v, self.rotary_emb.cos_sin_cache, self.attn.compact_k_cache, self.attn.compact_v_cache,
                     slot, evict_out, positions, num_kv_heads=self.num_kv_heads, alpha_scale=ctx.dms_alpha_scale,
                     alpha_offset=ctx.dms_alpha_offset, store_q=not inline_q_rope,
-                    store_transient_k=dms_decode_store_transient_k_enabled())
+                    store_transient_k=dms_decode_store_transient_k_enabled(), k_scale=self.attn.compact_k_scale,
+                    v_scale=self.attn.compact_v_scale)
                 evict_mask = evict_out
                 fused = True
             else:

@@ -13,7 +13,14 @@
  *   - bool tensors are uint8_t (0/1);
  *   - `stream` is a hipStream_t; kernels are enqueued on it and never
  *     synchronise, allocate or call hipMemset, so every call is capturable in a
- *     HIP graph.
+ *     HIP graph;
+ *   - k_scale / v_scale (where taken): optional per-kv-head FP8 scale tables
+ *     [num_kv_heads] fp32 of the layer (NULL = none, the reference's bare
+ *     cast).  Stores write e4m3(x * fp32(1 / scale)); the matrix-core
+ *     attention kernel dequantises in registers (K scale folded into the score
+ *     scale, V scale on the output).  No reference counterpart: the reference
+ *     casts K/V to FP8 without a scale (compact_kv.py:243-252,
+ *     compact_attention.py:387, 399).  Only FP8 arenas take scales.
  *
  * Reference citations are path:line in shisa-ai/FastDMS.
  */
@@ -26,7 +33,8 @@
 extern "C" {
 #endif
 
-/* ABI version of this header (1). */
+/* ABI version of this header (2: per-kv-head FP8 scale tables on the pack,
+ * append and attention entry points). */
 int fdms_abi_version(void);
 
 /* Plain 16-byte-vector copy used to calibrate HBM byte counters and the copy
@@ -83,7 +91,8 @@ int fdms_streaming_pack_rank_scatter(const void* k, const void* v, int kv_dtype,
                                      void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions,
                                      uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h,
                                      int64_t tp_s, int64_t em_b, int64_t em_h, int64_t em_s, int window,
-                                     int num_kv_heads, int head_dim, int max_chunks, int vec, void* stream);
+                                     int num_kv_heads, int head_dim, int max_chunks, int vec, const float* k_scale,
+                                     const float* v_scale, void* stream);
 
 /* A6 — scatter with precomputed keep/rank.  Replaces _streaming_pack_scatter_kernel
  * / _streaming_pack_scatter_triton (compact_kv.py:38-137, 364-423). */
@@ -93,7 +102,8 @@ int fdms_streaming_pack_scatter(const void* k, const void* v, int kv_dtype, int6
                                 int64_t es_t, int64_t es_h, const int32_t* base, int64_t bs_h, void* compact_k,
                                 void* compact_v, int compact_dtype, int64_t cs_s, int32_t* positions, int64_t tp_h,
                                 int64_t tp_s, uint8_t* evict_meta, int64_t em_h, int64_t em_s, int start,
-                                int seq_len, int num_kv_heads, int head_dim, int vec, void* stream);
+                                int seq_len, int num_kv_heads, int head_dim, int vec, const float* k_scale,
+                                const float* v_scale, void* stream);
 
 /* A9 — fused decode DMS decision + RoPE + compact append.  Replaces
  * _dms_rope_store_compact_decode_kernel / fused_dms_rope_store_compact_decode
@@ -106,7 +116,8 @@ int fdms_dms_rope_store_compact_decode(void* q, int q_dtype, int64_t qs_b, int64
                                        int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
                                        const int64_t* positions, int batch, int num_kv_heads, int group_size,
                                        int head_dim, float alpha_scale, float alpha_offset, float threshold,
-                                       int positive_scale, int store_q, int store_transient_k, void* stream);
+                                       int positive_scale, int store_q, int store_transient_k, const float* k_scale,
+                                       const float* v_scale, void* stream);
 
 /* B8 — prefill RoPE in place on a [tokens, heads, D] view.  Replaces
  * RotaryEmbedding.forward / apply_rotary_emb (fastdms/layers/rotary_embedding.py:7-15,
@@ -120,7 +131,8 @@ int fdms_rope_inplace(void* x, int dtype, int64_t xs_t, int64_t xs_h, int64_t nu
 int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype, int64_t ks_b, int64_t ks_h,
                                int64_t vs_b, int64_t vs_h, void* compact_k, void* compact_v, int compact_dtype,
                                int64_t c_s, const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, int batch,
-                               int num_kv_heads, int head_dim, void* stream);
+                               int num_kv_heads, int head_dim, const float* k_scale, const float* v_scale,
+                               void* stream);
 
 /* B2/B3/B5 — split-K GQA decode attention over compact spans with the split
  * merge fused into the same launch.  Replaces compact_decode_attention and its
@@ -132,11 +144,13 @@ int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype,
  * leaves them zero).  Calls that share counters must not overlap in time.
  * rope_positions != NULL rotates q in-kernel with the decision lane zeroed
  * (B4, _compact_decode_grouped_splitk_partial_qrope_kernel, compact_attention.py:418-534).
- * split_rows == 0 divides every pair's live span evenly over num_splits; with
- * split_rows > 0 the matrix-core kernel (bf16 q, FP8 K/V, group_size <= 4,
- * head_dim 64 / 128) gives each pair ceil(live / split_rows) splits, at most
- * num_splits, and a pair with one split skips the merge (other kernels ignore
- * split_rows). */
+ * The matrix-core kernel (bf16 q, FP8 K/V, group_size <= 4, head_dim 64 /
+ * 128) gives each pair ceil(live / split_rows) splits (split_rows rounded up
+ * to 64; 0 = one 64-row group per wave of the workgroup), at most num_splits,
+ * and a pair with one split skips the merge; the other kernels ignore
+ * split_rows and divide every pair's live span evenly over num_splits.  Split
+ * partials are handed over with agent-scope atomic stores / loads ordered
+ * around the ticket (no L2 write-back or invalidate). */
 int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int64_t qs_h, const void* compact_k,
                                   const void* compact_v, int kv_dtype, int64_t c_s, const int32_t* base_offsets,
                                   int64_t bo_b, int64_t bo_h, const int32_t* block_tables, int64_t bt_b,
@@ -144,7 +158,8 @@ int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int6
                                   int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace,
                                   int* counters, int batch, int num_kv_heads, int group_size, int head_dim,
                                   int num_splits, int split_rows, float scale, const float* rope_cos_sin,
-                                  int64_t rcs_p, int64_t rcs_d, const int64_t* rope_positions, void* stream);
+                                  int64_t rcs_p, int64_t rcs_d, const int64_t* rope_positions, const float* k_scale,
+                                  const float* v_scale, void* stream);
 
 /* A9 + B2-B5 — decode preprocess and attention in one launch: the reference's
  * fused_dms_rope_store_compact_decode(store_q=False, store_transient_k=False)
@@ -165,7 +180,7 @@ int fdms_fused_decode_attention(const void* q, int64_t qs_b, int64_t qs_h, const
                                 int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b, int64_t lc_h,
                                 void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
                                 int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows,
-                                float scale, void* stream);
+                                float scale, const float* k_scale, const float* v_scale, void* stream);
 
 /* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
  * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /

@@ -75,7 +75,8 @@ def apply_rotary_emb(x, cos, sin, out_dtype_code: int):
 
 def fused_dms_rope_store_compact_decode(*, q, k, v, cos_sin_cache, compact_k, compact_v, slot_mapping,
                                         positions, num_kv_heads, alpha_scale, alpha_offset, q_dtype_code,
-                                        k_dtype_code, compact_dtype_code, store_q=True, store_transient_k=True):
+                                        k_dtype_code, compact_dtype_code, store_q=True, store_transient_k=True,
+                                        k_scale=None, v_scale=None):
     """compact_attention.py:67-209, in place on numpy arrays; returns evict [B, Hkv].
 
     q [B, Hq, D], k/v [B, Hkv, D] float32 values; compact_* storage arrays;
@@ -107,8 +108,13 @@ def fused_dms_rope_store_compact_decode(*, q, k, v, cos_sin_cache, compact_k, co
                 k[bi, h] = numerics.cast(krot, k_dtype_code)
             slot = int(slot_mapping[bi, h])
             if slot >= 0:
+                vrow = np.asarray(v[bi, h], np.float32)
+                if k_scale is not None:  # per-kv-head FP8 scale: stored = x * fp32(1 / scale)
+                    krot = (krot * (np.float32(1.0) / np.float32(k_scale[h]))).astype(np.float32)
+                if v_scale is not None:
+                    vrow = (vrow * (np.float32(1.0) / np.float32(v_scale[h]))).astype(np.float32)
                 compact_k[slot] = numerics.to_storage(krot, compact_dtype_code)
-                compact_v[slot] = numerics.to_storage(np.asarray(v[bi, h], np.float32), compact_dtype_code)
+                compact_v[slot] = numerics.to_storage(vrow, compact_dtype_code)
     return evict
 
 
@@ -130,11 +136,14 @@ def _attend(q, keys, values, scale):
     return (p @ values) / p.sum()
 
 
-def compact_decode_attention(q, compact_k, compact_v, base_offsets, live_counts, scale=None):
+def compact_decode_attention(q, compact_k, compact_v, base_offsets, live_counts, scale=None, k_scale=None,
+                             v_scale=None):
     """compact_attention.py:1339-1364 in float64.
 
     q [B, Hq, D] float values; compact_* float values [slots, D];
     base_offsets/live_counts [B, Hkv].  Returns float64 [B, Hq, D].
+    k_scale / v_scale [Hkv]: per-kv-head dequant of stored FP8 values
+    (K = stored * k_scale; no reference counterpart).
     """
     q = np.asarray(q, dtype=np.float64)
     b, hq, d = q.shape
@@ -144,15 +153,18 @@ def compact_decode_attention(q, compact_k, compact_v, base_offsets, live_counts,
     ck = np.asarray(compact_k, dtype=np.float64)
     cv = np.asarray(compact_v, dtype=np.float64)
     out = np.zeros((b, hq, d), dtype=np.float64)
+    ksc = np.ones(hkv) if k_scale is None else np.asarray(k_scale, np.float64)
+    vsc = np.ones(hkv) if v_scale is None else np.asarray(v_scale, np.float64)
     for bi in range(b):
         for qh in range(hq):
             h = qh // g
             base, live = int(base_offsets[bi, h]), int(live_counts[bi, h])
-            out[bi, qh] = _attend(q[bi, qh], ck[base:base + live], cv[base:base + live], scale)
+            out[bi, qh] = _attend(q[bi, qh], ck[base:base + live] * ksc[h], cv[base:base + live] * vsc[h], scale)
     return out
 
 
-def compact_decode_attention_storage(q, ck_storage, cv_storage, dtype_code, base_offsets, live_counts, scale=None):
+def compact_decode_attention_storage(q, ck_storage, cv_storage, dtype_code, base_offsets, live_counts, scale=None,
+                                     k_scale=None, v_scale=None):
     """compact_decode_attention over arena *storage* arrays, decoding only the
     live span of each (b, kv head)."""
     q = np.asarray(q, dtype=np.float64)
@@ -166,6 +178,10 @@ def compact_decode_attention_storage(q, ck_storage, cv_storage, dtype_code, base
             base, live = int(base_offsets[bi, h]), int(live_counts[bi, h])
             keys = numerics.from_storage(ck_storage[base:base + live], dtype_code).astype(np.float64)
             vals = numerics.from_storage(cv_storage[base:base + live], dtype_code).astype(np.float64)
+            if k_scale is not None:
+                keys = keys * float(k_scale[h])
+            if v_scale is not None:
+                vals = vals * float(v_scale[h])
             s = q[bi, h * g:(h + 1) * g] @ keys.T * scale
             s = s - s.max(axis=1, keepdims=True)
             p = np.exp(s)
@@ -179,7 +195,8 @@ def paged_rows(block_table_row, live: int, page_size: int) -> np.ndarray:
     return np.asarray(block_table_row, dtype=np.int64)[r // page_size] * page_size + r % page_size
 
 
-def compact_decode_attention_paged(q, kv_k, kv_v, block_tables, live_counts, page_size, scale=None):
+def compact_decode_attention_paged(q, kv_k, kv_v, block_tables, live_counts, page_size, scale=None, k_scale=None,
+                                   v_scale=None):
     """Same math as compact_decode_attention, K/V addressed through a
     block table [B, Hkv, max_pages] of page_size-token pages."""
     q = np.asarray(q, dtype=np.float64)
@@ -194,7 +211,9 @@ def compact_decode_attention_paged(q, kv_k, kv_v, block_tables, live_counts, pag
         for qh in range(hq):
             h = qh // g
             rows = paged_rows(block_tables[bi, h], int(live_counts[bi, h]), page_size)
-            out[bi, qh] = _attend(q[bi, qh], ck[rows], cv[rows], scale)
+            ks = 1.0 if k_scale is None else float(k_scale[h])
+            vs = 1.0 if v_scale is None else float(v_scale[h])
+            out[bi, qh] = _attend(q[bi, qh], ck[rows] * ks, cv[rows] * vs, scale)
     return out
 
 

@@ -54,8 +54,14 @@ def streaming_pack_fused_rank_prepare(seq_evict, seq_len: int, window_size: int)
     return live, offsets
 
 
+def inv_scales(scale) -> np.ndarray:
+    """fp32 1 / scale per kv head (an IEEE division, as the kernels compute it)."""
+    s = np.asarray(scale, np.float32)
+    return (np.float32(1.0) / s).astype(np.float32)
+
+
 def streaming_pack_scatter(*, k, v, keep, rank, seq_evict, compact_k, compact_v, token_positions,
-                           evict_mask, base_offsets, start: int, seq_len: int, dtype_code: int):
+                           evict_mask, base_offsets, start: int, seq_len: int, dtype_code: int, k_scale=None, v_scale=None):
     """compact_kv.py:38-137 (precomputed keep/rank) — in place on numpy arrays.
 
     k, v: float32 values [T_total, Hkv, D]; compact_*: storage [slots, D];
@@ -66,14 +72,21 @@ def streaming_pack_scatter(*, k, v, keep, rank, seq_evict, compact_k, compact_v,
     t_idx, h_idx = np.nonzero(keep)
     dst_rank = rank[t_idx, h_idx]
     dst = np.asarray(base_offsets, dtype=np.int64)[h_idx] + dst_rank
-    compact_k[dst] = numerics.to_storage(np.asarray(k)[start + t_idx, h_idx], dtype_code)
-    compact_v[dst] = numerics.to_storage(np.asarray(v)[start + t_idx, h_idx], dtype_code)
+    kv = np.asarray(k, np.float32)[start + t_idx, h_idx]
+    vv = np.asarray(v, np.float32)[start + t_idx, h_idx]
+    if k_scale is not None:  # per-kv-head FP8 scale: stored = x * fp32(1 / scale)
+        kv = (kv * inv_scales(k_scale)[h_idx, None]).astype(np.float32)
+    if v_scale is not None:
+        vv = (vv * inv_scales(v_scale)[h_idx, None]).astype(np.float32)
+    compact_k[dst] = numerics.to_storage(kv, dtype_code)
+    compact_v[dst] = numerics.to_storage(vv, dtype_code)
     token_positions[h_idx, dst_rank] = t_idx.astype(np.int32)
     evict_mask[h_idx, dst_rank] = np.asarray(seq_evict, dtype=bool)[t_idx, h_idx]
 
 
 def streaming_pack_rank_scatter(*, k, v, seq_evict, compact_k, compact_v, token_positions, evict_mask,
-                                base_offsets, start: int, seq_len: int, window_size: int, dtype_code: int):
+                                base_offsets, start: int, seq_len: int, window_size: int, dtype_code: int,
+                                k_scale=None, v_scale=None):
     """compact_kv.py:168-262 fused count/rank scatter; rank = stable order of
     kept tokens (cumsum(keep) - 1), so it equals the precomputed-rank form."""
     if seq_len <= 0:
@@ -83,7 +96,8 @@ def streaming_pack_rank_scatter(*, k, v, seq_evict, compact_k, compact_v, token_
     rank = np.cumsum(keep.astype(np.int64), axis=0) - 1
     streaming_pack_scatter(k=k, v=v, keep=keep, rank=rank, seq_evict=seq_evict, compact_k=compact_k,
                            compact_v=compact_v, token_positions=token_positions, evict_mask=evict_mask,
-                           base_offsets=base_offsets, start=start, seq_len=seq_len, dtype_code=dtype_code)
+                           base_offsets=base_offsets, start=start, seq_len=seq_len, dtype_code=dtype_code,
+                           k_scale=k_scale, v_scale=v_scale)
     return keep.sum(axis=0).astype(np.int32)
 
 
@@ -321,8 +335,10 @@ class OracleCompactKVManager:
         self.compact_k_per_layer[layer_id] = nk
         self.compact_v_per_layer[layer_id] = nv
 
-    def streaming_pack_layer(self, *, layer_id, k, v, evict_mask, cu_seqlens_q, seq_ids, window_size):
-        """compact_kv.py:915-1099 (per-layer storage branch)."""
+    def streaming_pack_layer(self, *, layer_id, k, v, evict_mask, cu_seqlens_q, seq_ids, window_size,
+                             k_scale=None, v_scale=None):
+        """compact_kv.py:915-1099 (per-layer storage branch); optional
+        per-kv-head FP8 scales of the layer (no reference counterpart)."""
         cu = [int(x) for x in cu_seqlens_q]
         lives = {}
         high = 0
@@ -359,7 +375,8 @@ class OracleCompactKVManager:
                                         token_positions=st.token_positions[layer_id],
                                         evict_mask=st.evict_mask[layer_id],
                                         base_offsets=st.base_offsets[layer_id], start=cu[i], seq_len=n,
-                                        window_size=window_size, dtype_code=self.dtype_code)
+                                        window_size=window_size, dtype_code=self.dtype_code, k_scale=k_scale,
+                                        v_scale=v_scale)
             st.live_counts[layer_id] = live
 
     # -- decode metadata (compact_kv.py:1727-1770) --

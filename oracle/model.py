@@ -34,7 +34,9 @@ class OracleModel:
 
     def __init__(self, weights: dict, cfg, *, window_size: int, alpha_scale: float, alpha_offset: float,
                  capacity_tokens: int, max_model_len: int, kv_code: int = numerics.DT_FP8,
-                 manager: ock.OracleCompactKVManager | None = None, fp8_linear: dict | None = None):
+                 manager: ock.OracleCompactKVManager | None = None, fp8_linear: dict | None = None,
+                 fp8_torch_form_min_rows: int | None = None, int4_linear: dict | None = None,
+                 int4_max_rows: int = 0, embed_fp8: tuple | None = None, route=None, fp8_scales: str = "unit"):
         self.w = weights
         self.cfg = cfg
         self.window = int(window_size)
@@ -49,7 +51,25 @@ class OracleModel:
                                                cfg.rope_scaling)
         self.mgr = manager or ock.OracleCompactKVManager(self.L, self.Hkv, capacity_tokens, max_model_len,
                                                          head_dim=self.D, dtype_code=kv_code)
+        # name -> (W8^T e4m3 bits [K, N], scale_inv [1, N]); rows at or above
+        # fp8_torch_form_min_rows quantise the activation in _fp8_linear's torch
+        # form (linear.py:652-654), fewer rows as the Triton kernels do
         self.fp8_linear = fp8_linear or {}
+        self.fp8_torch_form_min_rows = fp8_torch_form_min_rows
+        # name -> dequantised INT4 weight [N, K] (bf16 values), used for calls
+        # of at most int4_max_rows rows (linear.py:855-870)
+        self.int4_linear = int4_linear or {}
+        self.int4_max_rows = int(int4_max_rows)
+        # (e4m3 bits [V, D], scale_inv [V]): the FP8 token table (embed_head.py:424-434)
+        self.embed_fp8 = embed_fp8
+        # optional (name, rows) -> "int4" | "fp8" | "fp8_torch" | "bf16": the
+        # dispatch decision of LinearBase._linear (linear.py:855-926) for a
+        # module with several weight forms; None = the defaults above
+        self.route = route
+        # per-(layer, kv head) FP8 KV scales (the manager's "calibrate" mode:
+        # amax / 224 of the layer's first packed K / V, fp32), None = unit
+        self.kv_scales = None if fp8_scales == "unit" else np.ones((self.L, 2, self.Hkv), np.float32)
+        self._calibrated = [False] * self.L
 
     # -- building blocks ------------------------------------------------------
     def rmsnorm(self, x, weight, residual=None):
@@ -62,15 +82,43 @@ class OracleModel:
         xn = bf16(x * torch.rsqrt(var + eps))  # layernorm.py:24, 37-38
         return bf16(xn * weight), residual
 
+    def embed(self, ids):
+        """embed_head.py:424-434: with an FP8 table, bf16(fp8 row) * bf16(scale_inv)."""
+        ids = torch.as_tensor(ids)
+        if self.embed_fp8 is None:
+            return self.w["model.embed_tokens.weight"][ids]
+        codes, sinv = self.embed_fp8
+        rows = torch.from_numpy(numerics.e4m3fn_decode(codes[ids.numpy()]).astype(np.float32))
+        s = torch.from_numpy(np.asarray(sinv, np.float32).reshape(-1)[ids.numpy()]).reshape(-1, 1)
+        return bf16(bf16(rows) * bf16(s))
+
     def linear(self, x, name, bias=True):
-        if name in self.fp8_linear:
-            w8_t, scale_inv = self.fp8_linear[name]
-            y = torch.from_numpy(olin.fp8_linear(x.numpy(), w8_t, scale_inv, quantize_x=True).astype(np.float32))
+        """bf16 F.linear: one rounding of the fp32 sum incl. the bias (the GEMM
+        epilogue adds it); the FP8 and INT4 paths round the matmul to bf16 and
+        add the bias in bf16 (linear.py:475-477, 659-661)."""
+        quantised = True
+        rows = x.shape[0]
+        if self.route is not None:
+            path = self.route(name, rows)
+        elif name in self.int4_linear and rows <= self.int4_max_rows:
+            path = "int4"
+        elif name in self.fp8_linear:
+            tf = self.fp8_torch_form_min_rows is not None and rows >= self.fp8_torch_form_min_rows
+            path = "fp8_torch" if tf else "fp8"
         else:
+            path = "bf16"
+        if path == "int4":
+            y = bf16(x @ self.int4_linear[name].T)
+        elif path in ("fp8", "fp8_torch"):
+            w8_t, scale_inv = self.fp8_linear[name]
+            y = bf16(torch.from_numpy(olin.fp8_linear(x.numpy(), w8_t, scale_inv, quantize_x=True,
+                                                      torch_form=path == "fp8_torch").astype(np.float32)))
+        else:
+            quantised = False
             y = x @ self.w[name + ".weight"].T
         b = self.w.get(name + ".bias") if bias else None
         if b is not None:
-            y = y + b
+            y = y + (bf16(b) if quantised else b)
         return bf16(y)
 
     def qkv_split(self, qkv):
@@ -104,6 +152,17 @@ class OracleModel:
         self.last_logits = self.logits(x)
         return olin.argmax_lowest(self.last_logits.numpy())
 
+    def _layer_scales(self, layer, k=None, v=None):
+        if self.kv_scales is None:
+            return None, None
+        if not self._calibrated[layer] and k is not None:
+            for i, x in enumerate((k, v)):
+                amax = np.abs(np.asarray(x, np.float32)).max(axis=(0, 2))
+                self.kv_scales[layer, i] = np.where(amax > 0, (amax / np.float32(224.0)).astype(np.float32),
+                                                    np.float32(1.0))
+            self._calibrated[layer] = True
+        return self.kv_scales[layer, 0], self.kv_scales[layer, 1]
+
     # -- prefill (model_runner.py:594-679, llama.py:87-202) --------------------
     def prefill(self, seqs: list[tuple[int, list[int], int]]) -> list[int]:
         """seqs: (seq_id, prompt token ids, max_tokens).  Returns each sequence's first token."""
@@ -114,7 +173,7 @@ class OracleModel:
         pos = np.concatenate([np.arange(len(p)) for _, p, _ in seqs])
         cs = self.cos_sin[pos][:, None, 0]
         cos, sin = cs[..., :self.D // 2], cs[..., self.D // 2:]
-        x = self.w["model.embed_tokens.weight"][ids]
+        x = self.embed(ids)
         residual = None
         for layer in range(self.L):
             pre = f"model.layers.{layer}."
@@ -131,8 +190,10 @@ class OracleModel:
             qr = oatt.apply_rotary_emb(qn, cos, sin, numerics.DT_BF16)
             kr = oatt.apply_rotary_emb(k.numpy(), cos, sin, numerics.DT_BF16)
             vn = v.numpy()
+            ks, vs = self._layer_scales(layer, kr, vn)
             self.mgr.streaming_pack_layer(layer_id=layer, k=kr, v=vn, evict_mask=evict, cu_seqlens_q=cu,
-                                          seq_ids=[s for s, _, _ in seqs], window_size=self.window)
+                                          seq_ids=[s for s, _, _ in seqs], window_size=self.window, k_scale=ks,
+                                          v_scale=vs)
             att = numerics.bf16_round(oatt.causal_prefill_attention(qr, kr, vn, cu).astype(np.float32))
             o = self.linear(torch.from_numpy(att.reshape(att.shape[0], -1)), pre + "self_attn.o_proj", bias=False)
             h, residual = self.rmsnorm(o, self.w[pre + "post_attention_layernorm.weight"], residual)
@@ -146,7 +207,7 @@ class OracleModel:
         self.mgr.apply_dms_evictions(seq_ids, positions, window_size=self.window, triton_mode=expiry_mode)
         base, live, slot, _ = self.mgr.prepare_decode_metadata(seq_ids)
         b = len(seq_ids)
-        x = self.w["model.embed_tokens.weight"][torch.tensor(last_tokens)]
+        x = self.embed(last_tokens)
         residual = None
         pos = np.asarray(positions)
         evict_all = np.zeros((self.L, b, self.Hkv), dtype=bool)
@@ -165,8 +226,11 @@ class OracleModel:
                 q=qn, k=kn, v=v.numpy(), cos_sin_cache=self.cos_sin, compact_k=ck, compact_v=cv,
                 slot_mapping=slot[layer], positions=pos, num_kv_heads=self.Hkv, alpha_scale=self.alpha_scale,
                 alpha_offset=self.alpha_offset, q_dtype_code=numerics.DT_BF16, k_dtype_code=numerics.DT_BF16,
-                compact_dtype_code=self.kv_code, store_q=True, store_transient_k=False)
-            att = oatt.compact_decode_attention_storage(qn, ck, cv, self.kv_code, base[layer], live[layer])
+                compact_dtype_code=self.kv_code, store_q=True, store_transient_k=False,
+                k_scale=self._layer_scales(layer)[0], v_scale=self._layer_scales(layer)[1])
+            ks, vs = self._layer_scales(layer)
+            att = oatt.compact_decode_attention_storage(qn, ck, cv, self.kv_code, base[layer], live[layer],
+                                                        k_scale=ks, v_scale=vs)
             att = numerics.bf16_round(att.astype(np.float32))
             o = self.linear(torch.from_numpy(att.reshape(b, -1)), pre + "self_attn.o_proj", bias=False)
             h, residual = self.rmsnorm(o, self.w[pre + "post_attention_layernorm.weight"], residual)

@@ -174,6 +174,18 @@ class Emulator:
         lane.zero_()
         return 0
 
+    def _inv_scales(self, scale, H, what):
+        """fp32 1 / scale[h] per kv head (the kernels' IEEE division), ones without a table."""
+        if not scale:
+            return torch.ones(H, dtype=torch.float32)
+        s = self.view(scale, torch.float32, (H,), (1,), what).clone()
+        return (torch.ones(H, dtype=torch.float32) / s).float()
+
+    def _scales(self, scale, H, what):
+        if not scale:
+            return torch.ones(H, dtype=torch.float32)
+        return self.view(scale, torch.float32, (H,), (1,), what).clone()
+
     def _seq_spans(self, cu, single_start, single_len, num_seqs):
         if cu:
             c = self.view(cu, torch.int32, (num_seqs + 1,), (1,), "cu_seqlens").tolist()
@@ -218,9 +230,10 @@ class Emulator:
     def streaming_pack_rank_scatter(self, k, v, kvdt, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
                                     single_len, num_seqs, bo, bo_b, bo_h, bo_c, base, bs_b, bs_h, ck, cv, cdt, cs_s,
                                     positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s, window, H,
-                                    D, max_chunks, vec, stream):
+                                    D, max_chunks, vec, k_scale, v_scale, stream):
         if num_seqs <= 0 or H <= 0 or D <= 0 or max_chunks <= 0 or vec <= 0 or D % vec:
             return 1
+        kinv, vinv = self._inv_scales(k_scale, H, "k_scale"), self._inv_scales(v_scale, H, "v_scale")
         spans = self._seq_spans(cu, single_start, single_len, num_seqs)
         rows = list(range(num_seqs))
         if meta_rows:
@@ -259,6 +272,8 @@ class Emulator:
                 self.gather_idx(cvf, cv0 + didx, "compact_v")
                 kvals = self.load(kview[src, h], kvdt)
                 vvals = self.load(vview[src, h], kvdt)
+                if k_scale or v_scale:  # stored = x * (1 / scale), one fp32 rounding
+                    kvals, vvals = (kvals * kinv[h]).float(), (vvals * vinv[h]).float()
                 tmp = torch.empty(didx.shape, dtype=_TORCH[cdt])
                 self.store(tmp, kvals, cdt)
                 ckf[ck0 + didx] = tmp
@@ -293,9 +308,10 @@ class Emulator:
 
     def dms_rope_store_compact_decode(self, q, qdt, qs_b, qs_h, k, v, kvdt, ks_b, ks_h, vs_b, vs_h, cos_sin, cs_p,
                                       cs_d, ck, cv, cdt, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h, positions, B, H,
-                                      G, D, a_s, a_o, thr, pos_scale, store_q, store_tk, stream):
+                                      G, D, a_s, a_o, thr, pos_scale, store_q, store_tk, k_scale, v_scale, stream):
         if B == 0:
             return 0
+        kinv, vinv = self._inv_scales(k_scale, H, "k_scale"), self._inv_scales(v_scale, H, "v_scale")
         qv = self.view(q, _TORCH[qdt], (B, H * G, D), (qs_b, qs_h, 1), "q")
         kv_ = self.view(k, _TORCH[kvdt], (B, H, D), (ks_b, ks_h, 1), "k")
         vv = self.view(v, _TORCH[kvdt], (B, H, D), (vs_b, vs_h, 1), "v")
@@ -328,16 +344,16 @@ class Emulator:
                 idx = self.gather_idx(ckf, ck0 + r * c_s + torch.arange(D), "compact_k slot")
                 self.gather_idx(cvf, cv0 + r * c_s + torch.arange(D), "compact_v slot")
                 tmp = torch.empty(D, dtype=_TORCH[cdt])
-                self.store(tmp, krot[b, h], cdt)
+                self.store(tmp, (krot[b, h] * kinv[h]).float(), cdt)
                 ckf[idx] = tmp
-                self.store(tmp, vf[b, h], cdt)
+                self.store(tmp, (vf[b, h] * vinv[h]).float() if v_scale else vf[b, h], cdt)
                 cvf[cv0 + r * c_s + torch.arange(D)] = tmp
         return 0
 
     def fused_decode_attention(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                                slot, sm_b, sm_h, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv, c_s, base,
                                bo_b, bo_h, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
-                               split_rows, scale, stream):
+                               split_rows, scale, k_scale, v_scale, stream):
         """The documented composition: preprocess (store_q = store_transient_k =
         0) then attention with in-kernel q RoPE over the span incl. the append."""
         if B == 0:
@@ -346,15 +362,18 @@ class Emulator:
             return 1
         self.dms_rope_store_compact_decode(q, DT_BF16, qs_b, qs_h, k, v, DT_BF16, ks_b, ks_h, vs_b, vs_h, cos_sin,
                                            cs_p, cs_d, ck, cv, DT_FP8, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h,
-                                           positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, stream)
+                                           positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, k_scale, v_scale,
+                                           stream)
         return self.compact_decode_attention(q, DT_BF16, qs_b, qs_h, ck, cv, DT_FP8, c_s, base, bo_b, bo_h, None, 0,
                                              0, 0, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D,
-                                             splits, split_rows, scale, cos_sin, cs_p, cs_d, positions, stream)
+                                             splits, split_rows, scale, cos_sin, cs_p, cs_d, positions, k_scale,
+                                             v_scale, stream)
 
     def store_compact_kvcache(self, key, value, kvdt, ks_b, ks_h, vs_b, vs_h, ck, cv, cdt, c_s, slot, sm_b, sm_h,
-                              B, H, D, stream):
+                              B, H, D, k_scale, v_scale, stream):
         if B == 0:
             return 0
+        kinv, vinv = self._inv_scales(k_scale, H, "k_scale"), self._inv_scales(v_scale, H, "v_scale")
         kv_ = self.load(self.view(key, _TORCH[kvdt], (B, H, D), (ks_b, ks_h, 1), "key"), kvdt)
         vv = self.load(self.view(value, _TORCH[kvdt], (B, H, D), (vs_b, vs_h, 1), "value"), kvdt)
         sl = self.view(slot, torch.int32, (B, H), (sm_b, sm_h), "slot_mapping")
@@ -368,17 +387,18 @@ class Emulator:
                 idx = self.gather_idx(ckf, ck0 + r * c_s + torch.arange(D), "compact_k slot")
                 self.gather_idx(cvf, cv0 + r * c_s + torch.arange(D), "compact_v slot")
                 tmp = torch.empty(D, dtype=_TORCH[cdt])
-                self.store(tmp, kv_[b, h], cdt)
+                self.store(tmp, (kv_[b, h] * kinv[h]).float() if k_scale or v_scale else kv_[b, h], cdt)
                 ckf[idx] = tmp
-                self.store(tmp, vv[b, h], cdt)
+                self.store(tmp, (vv[b, h] * vinv[h]).float() if k_scale or v_scale else vv[b, h], cdt)
                 cvf[cv0 + r * c_s + torch.arange(D)] = tmp
         return 0
 
     def compact_decode_attention(self, q, qdt, qs_b, qs_h, ck, cv, kvdt, c_s, base, bo_b, bo_h, bt, bt_b, bt_h,
                                  page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
-                                 split_rows, scale, rope_cs, rcs_p, rcs_d, rope_pos, stream):
+                                 split_rows, scale, rope_cs, rcs_p, rcs_d, rope_pos, k_scale, v_scale, stream):
         if B == 0:
             return 0
+        ksc, vsc = self._scales(k_scale, H, "k_scale"), self._scales(v_scale, H, "v_scale")
         if splits > 1:
             self.view(ws, torch.float32, (B * H * splits * G * (D + 2),), (1,), "workspace")
             cnt = self.view(counters, torch.int32, (B * H,), (1,), "counters")
@@ -417,9 +437,9 @@ class Emulator:
                 kk = self.load(ckf[self.gather_idx(ckf, ck0 + idx, "compact_k span")], kvdt).double()
                 vv = self.load(cvf[self.gather_idx(cvf, cv0 + idx, "compact_v span")], kvdt).double()
                 qq = qf[b, h * G:(h + 1) * G].double()
-                sc = qq @ kk.T * scale
+                sc = qq @ (kk * float(ksc[h])).T * scale  # dequant: fp8 value * scale
                 p = torch.softmax(sc, dim=-1)
-                res[b, h * G:(h + 1) * G] = (p @ vv).float()
+                res[b, h * G:(h + 1) * G] = (p @ (vv * float(vsc[h]))).float()
         self.store(ov, res, qdt)
         return 0
 
@@ -564,7 +584,7 @@ class Emulator:
             return 0
         xv = self.view(x, torch.bfloat16, (rows, 2 * f), (2 * f, 1), "x").float()
         g, u = xv[:, :f], xv[:, f:]
-        self.view(out, torch.bfloat16, (rows, f), (f, 1), "out").copy_((g / (1.0 + torch.exp(-g)) * u)
+        self.view(out, torch.bfloat16, (rows, f), (f, 1), "out").copy_((torch.nn.functional.silu(g) * u)
                                                                          .to(torch.bfloat16))
         return 0
 
@@ -630,7 +650,7 @@ class Emulator:
             out = out.to(torch.bfloat16).float()
         if epilogue == 1:  # gate_up -> SiluAndMul, the oracle model's mlp expression
             g, u = out[:, :n_out], out[:, n_out:]
-            out = (g / (1.0 + torch.exp(-g))) * u
+            out = torch.nn.functional.silu(g) * u
         self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
         return 0
 
@@ -729,7 +749,7 @@ class Emulator:
             return 0
         if epilogue == 1:
             g, u = out[:, :n_out], out[:, n_out:]
-            out = (g / (1.0 + torch.exp(-g))) * u
+            out = torch.nn.functional.silu(g) * u
         self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
         return 0
 

@@ -22,7 +22,7 @@ def _rel_err(got, ref):
 
 def _force_splits(monkeypatch, n):
     import fastdms_amd.layers.compact_attention as ca
-    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (n, 0))
+    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, **kw: (n, 0))
 
 
 @pytest.mark.parametrize("splits", [None, 1, 2, 3, 20])
@@ -142,7 +142,7 @@ def test_matrix_core_per_pair_splits(monkeypatch, d, paged):
     cv = numerics.cast(rng.standard_normal((b * hkv * span, d)).astype(np.float32), numerics.DT_FP8)
     q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
     ref = oatt.compact_decode_attention(q, ck, cv, base, live)
-    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (4, 512))
+    monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, **kw: (4, 512))
     qd, ckd, cvd = from_values(q, numerics.DT_BF16), from_values(ck, numerics.DT_FP8), from_values(cv, numerics.DT_FP8)
     assert ca.mfma_attention_path(qd, ckd, g)
     if paged:
@@ -354,3 +354,51 @@ def test_tiled_paged_and_inline_rope(d):
                                    q_rope_cos_sin_cache=torch.from_numpy(cache).cuda())
     torch.cuda.synchronize()
     assert _rel_err(values_of(out), ref) <= TOL_LOWP
+
+
+@pytest.mark.parametrize("b,fused", [(80, False), (80, True), (3, False)])
+def test_matrix_core_heavy_tail_splits(monkeypatch, b, fused):
+    """The matrix-core kernel's per-pair splits over a heavy-tailed batch
+    (live counts from 1 to 6000, a few pairs holding most rows) at several
+    split bounds with the default rows per split: 640 pairs at b = 80, a tiny
+    batch at b = 3, twice in a row (the tickets are reused), vs the float64
+    oracle."""
+    require_gpu()
+    import fastdms_amd.layers.compact_attention as ca
+    rng = np.random.default_rng(b * 7 + fused)
+    hkv, g, d = 8, 4, 64
+    live = np.minimum(rng.pareto(1.2, (b, hkv)) * 120 + 1, 6000).astype(np.int32)
+    live[0, 0] = 6000
+    live[-1, -1] = 1
+    cap = int(live.max()) + 1
+    base = (np.arange(b * hkv).reshape(b, hkv) * cap).astype(np.int32)
+    rows = b * hkv * cap
+    ck = numerics.to_storage(rng.standard_normal((rows, d)).astype(np.float32), numerics.DT_FP8)
+    cv = numerics.to_storage(rng.standard_normal((rows, d)).astype(np.float32), numerics.DT_FP8)
+    q = numerics.cast(rng.standard_normal((b, hkv * g, d)).astype(np.float32), numerics.DT_BF16)
+    qd = from_values(q, numerics.DT_BF16)
+    ckd = torch.from_numpy(ck).cuda().view(torch.float8_e4m3fn)
+    cvd = torch.from_numpy(cv).cuda().view(torch.float8_e4m3fn)
+    base_d, live_d = torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda()
+    qr = q.copy()
+    if fused:  # position 0: RoPE is the identity, only the decision lane is zeroed
+        qr.reshape(b, hkv, g, d)[:, :, 0, d - 1] = 0.0
+    ref = oatt.compact_decode_attention(qr, numerics.from_storage(ck, numerics.DT_FP8),
+                                        numerics.from_storage(cv, numerics.DT_FP8), base, live)
+    for target in (1, 8, 24):
+        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, waves=4, t=target: (t, 0))
+        if fused:
+            # no append (slot -1): the fused kernel attends over the stored span
+            kq = qd[:, :hkv].contiguous()
+            pos = torch.zeros(b, dtype=torch.int64, device="cuda")
+            cache = torch.from_numpy(oatt.rope_cos_sin_cache(d, 16, 500000.0)).cuda()
+            slot = torch.full((b, hkv), -1, dtype=torch.int32, device="cuda")
+            ev = torch.empty((b, hkv), dtype=torch.bool, device="cuda")
+            outs = [ca.fused_dms_rope_store_compact_decode_attention(
+                qd, kq, kq, cache, ckd, cvd, slot, ev, pos, base_d, live_d, num_kv_heads=hkv, alpha_scale=10.0,
+                alpha_offset=5.0, max_live_count=cap) for _ in range(2)]
+        else:
+            outs = [ca.compact_decode_attention(qd, ckd, cvd, base_d, live_d, max_live_count=cap) for _ in range(2)]
+        torch.cuda.synchronize()
+        for out in outs:
+            assert _rel_err(values_of(out), ref) <= TOL_LOWP, target

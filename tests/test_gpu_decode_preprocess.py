@@ -150,7 +150,7 @@ def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows):
     require_gpu()
     import fastdms_amd.layers.compact_attention as ca
     if split_rows is not None:
-        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma: (8, split_rows))
+        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, **kw: (8, split_rows))
     rng = np.random.default_rng(d + (split_rows or 0))
     b, hq, hkv = 8, 32, 8
     g = hq // hkv
