@@ -39,6 +39,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_store_compact_kvcache": "ppillllppilplliiippp",
     "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpppp",
     "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifppp",
+    "fdms_fused_decode_attention_noalloc": "pllpllpllpllppllpllfffipplpllpllplliiiiiifppp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",

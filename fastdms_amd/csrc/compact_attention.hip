@@ -15,6 +15,7 @@
 // its ticket to 0 so the next call (or graph replay) starts clean.  Softmax is
 // computed in the log2 domain (q pre-scaled by scale*log2 e, exp2).
 #include <cstdlib>
+#include <mutex>
 
 #include "fdms_common.h"
 
@@ -1533,3 +1534,89 @@ FDMS_EXPORT int fdms_fused_decode_attention(
                                 num_splits, split_rows, scale, k_scale, v_scale, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free variant of fdms_fused_decode_attention: the split partials
+// and tickets live in the library's own device array `scratch` (one copy per
+// GPU, held until the process ends), so a caller that cannot allocate (HIP
+// graph capture, a serving loop that forbids hipMalloc) passes only inputs and
+// outputs.  Host code must never pass the array's name to a kernel (in host
+// code it is a stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, once per device with that device current, and is kept
+// per device.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kScratchFloats = int64_t(2) << 20;  // 8 MiB of split partials
+constexpr int kScratchCounters = 16384;                // tickets (ints) after the partials
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) float scratch[kScratchFloats + kScratchCounters];
+
+__global__ void zero_ints_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up and its tickets
+// zeroed on the first call there); nullptr with *err set on failure.
+static float* scratch_on_current_device(hipStream_t stream, int* err) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = (int)e;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = (int)hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    // the tickets must start at zero (every call leaves them zero); a fill
+    // kernel, not hipMemsetAsync, so a first call under graph capture is fine
+    hipLaunchKernelGGL(zero_ints_kernel, dim3(16), dim3(256), 0, stream,
+                       reinterpret_cast<int*>(static_cast<float*>(p) + kScratchFloats), kScratchCounters);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      *err = (int)e;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+FDMS_EXPORT int fdms_fused_decode_attention_noalloc(
+    const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+    const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+    float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
+    int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
+    int64_t lc_h, void* out, int64_t os_b, int64_t os_h, int batch, int num_kv_heads, int group_size, int head_dim,
+    int num_splits, int split_rows, float scale, const float* k_scale, const float* v_scale, void* stream) {
+  if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4 || num_splits <= 0)
+    return (int)hipErrorInvalidValue;
+  // the scratch limit: pairs * num_splits * group_size * (head_dim + 2)
+  // partial floats and one ticket per pair
+  const int64_t pairs = (int64_t)batch * num_kv_heads;
+  if (pairs * num_splits * group_size * (int64_t)(head_dim + 2) > kScratchFloats || pairs > kScratchCounters)
+    return (int)hipErrorInvalidValue;
+  if (batch == 0) return 0;
+  int err = 0;
+  float* ws = scratch_on_current_device((hipStream_t)stream, &err);
+  if (!ws) return err;
+  return fused_decode_attention(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
+                                slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
+                                positive_scale, compact_k, compact_v, c_s, base_offsets, bo_b, bo_h, live_counts, lc_b,
+                                lc_h, out, os_b, os_h, ws, reinterpret_cast<int*>(ws + kScratchFloats), batch,
+                                num_kv_heads, group_size, head_dim, num_splits, split_rows, scale, k_scale, v_scale,
+                                stream);
+}

@@ -182,6 +182,28 @@ int fdms_fused_decode_attention(const void* q, int64_t qs_b, int64_t qs_h, const
                                 int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows,
                                 float scale, const float* k_scale, const float* v_scale, void* stream);
 
+/* Allocation-free fdms_fused_decode_attention (no reference counterpart): for
+ * callers that cannot allocate (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  Same arguments minus workspace / counters: the split
+ * partials and tickets live in the library's own device array (one per GPU,
+ * held until the process ends; looked up with hipGetSymbolAddress on the first
+ * call on a device).  Limit: batch * num_kv_heads * num_splits * group_size *
+ * (head_dim + 2) <= 2^21 floats and batch * num_kv_heads <= 16384, else
+ * hipErrorInvalidValue.  Every call on a GPU shares that array and leaves its
+ * tickets zero: calls that overlap in time on one GPU (other streams, other
+ * threads) race and must not be issued. */
+int fdms_fused_decode_attention_noalloc(const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b,
+                                        int64_t ks_h, const void* v, int64_t vs_b, int64_t vs_h,
+                                        const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+                                        const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out,
+                                        int64_t ev_b, int64_t ev_h, float alpha_scale, float alpha_offset,
+                                        float threshold, int positive_scale, void* compact_k, void* compact_v,
+                                        int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h,
+                                        const int32_t* live_counts, int64_t lc_b, int64_t lc_h, void* out,
+                                        int64_t os_b, int64_t os_h, int batch, int num_kv_heads, int group_size,
+                                        int head_dim, int num_splits, int split_rows, float scale,
+                                        const float* k_scale, const float* v_scale, void* stream);
+
 /* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
  * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /
  * dms_expiry_incremental_one_layer (compact_attention.py:690-965) and the
