@@ -178,6 +178,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     and the int32 / int64 metadata."""
     import torch
     from fastdms_amd.layers.compact_attention import (attention_split_plan, compact_decode_attention,
+                                                      compact_decode_attention_paged,
                                                       fused_decode_attention_supported,
                                                       fused_dms_rope_store_compact_decode_attention,
                                                       mfma_attention_path)
@@ -190,9 +191,17 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     start = mgr._contiguous_active_slot_start(states)
     b = len(seqs)
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    base = mgr.layer_major_base_offsets[:, start:start + b]
     live = mgr.layer_major_live_counts[:, start:start + b]
-    slot = (base + live - 1).contiguous()  # the row the last decode step appended
+    if mgr.paged:  # the row the last decode step appended: rank live-1 through the block table
+        bt = mgr.block_tables[:, start:start + b]
+        last = (live - 1).long().clamp(min=0)
+        page = torch.gather(bt, 3, (last // 16).unsqueeze(-1)).squeeze(-1)
+        slot = (page * 16 + last % 16).to(torch.int32).contiguous()
+        base = None
+    else:
+        bt = None
+        base = mgr.layer_major_base_offsets[:, start:start + b]
+        slot = (base + live - 1).contiguous()
     hint = runner.attention_hint(seqs)  # the bound (and so the split count) the decode step uses
     gen = torch.Generator(device="cpu").manual_seed(1)
     qkv = (torch.randn((b, (hq + 2 * hkv) * d), generator=gen) * 4).to(device="cuda", dtype=torch.bfloat16)
@@ -210,9 +219,12 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     def launch(l):
         if fused:
             fused_dms_rope_store_compact_decode_attention(
-                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions, base[l], live[l],
-                num_kv_heads=hkv, alpha_scale=md.alpha_scale, alpha_offset=md.alpha_offset, max_live_count=hint,
-                out=out)
+                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions,
+                None if base is None else base[l], live[l], num_kv_heads=hkv, alpha_scale=md.alpha_scale,
+                alpha_offset=md.alpha_offset, max_live_count=hint, out=out,
+                block_tables=None if bt is None else bt[l])
+        elif bt is not None:
+            compact_decode_attention_paged(q, arenas[l][0], arenas[l][1], bt[l], live[l], 16, max_live_count=hint)
         else:
             compact_decode_attention(q, arenas[l][0], arenas[l][1], base[l], live[l], max_live_count=hint)
 
@@ -237,15 +249,18 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     lv = live.to(torch.int64).cpu()
     elem = arenas[0][0].element_size()
     nl = len(layers)
+    # paged: one int32 block-table entry per 16-row page read in place of the
+    # span's base offset
+    meta = 4 * int(((lv + 15) // 16).sum()) if bt is not None else 4 * nl * b * hkv
     if fused:
         kv_bytes = int((lv - 1).clamp(min=0).sum()) * d * 2 * elem     # span rows read (all but the appended one)
         io_bytes = nl * b * ((hq + 2 * hkv) * d * 2                     # raw q, k, v rows (bf16)
                              + 2 * hkv * d * elem                        # appended K and V rows (FP8)
                              + hq * d * 2                                # output (bf16)
-                             + hkv * (3 * 4 + 1) + 8 + d * 4)            # base/live/slot, evict, position, cos/sin
+                             + hkv * (2 * 4 + 1) + 8 + d * 4) + meta     # live/slot, evict, position, cos/sin
     else:
         kv_bytes = int(lv.sum()) * d * 2 * elem
-        io_bytes = nl * b * (2 * hq * d * 2 + 2 * 4 * hkv)
+        io_bytes = nl * b * (2 * hq * d * 2 + 4 * hkv) + meta
     bytes_per_launch = (kv_bytes + io_bytes) / nl
     mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
     splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
@@ -260,6 +275,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("decode_attention_pmc_traffic.json", config),
             "kernel": ("decode_attn_mfma_kernel<fused>" if fused else
                        "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel"),
+            "layout": "paged (16-row pages)" if bt is not None else "span",
             "avg_launch_us": round(per_launch_s * 1e6, 3),
             "bytes_per_launch": int(bytes_per_launch), "partition": splits,
             "live_tokens_per_head": {"mean": round(float(lv.float().mean()), 1), "max": int(lv.max()),
@@ -289,13 +305,26 @@ def attention_scaling(llm, seqs, batches=(8, 32, 128), layers: int = 8, replays:
     rows = []
     for b in batches:
         live = pool[torch.randint(0, pool.numel(), (layers, b, hkv), generator=gen)].to(torch.int32)
-        cap = int(live.max()) + 1
-        base = (torch.arange(b * hkv, dtype=torch.int32) * cap).view(1, b, hkv).expand(layers, b, hkv).contiguous()
-        arenas = [(torch.randint(0, 120, (b * hkv * cap, d), dtype=torch.uint8, device="cuda").view(dt),
-                   torch.randint(0, 120, (b * hkv * cap, d), dtype=torch.uint8, device="cuda").view(dt))
+        # the engine's paged layout: every span ceil(live / 16) pages, page ids
+        # a random permutation of each layer's pool
+        npg = (live.to(torch.int64) + 15) // 16
+        maxp = int(npg.max())
+        bt = torch.full((layers, b, hkv, maxp), -1, dtype=torch.int32)
+        for l in range(layers):
+            ids = torch.randperm(int(npg[l].sum()), generator=gen).to(torch.int32)
+            at = 0
+            for i in range(b):
+                for h in range(hkv):
+                    n = int(npg[l, i, h])
+                    bt[l, i, h, :n] = ids[at:at + n]
+                    at += n
+        rows_per_layer = int(npg.sum(dim=(1, 2)).max()) * 16
+        arenas = [(torch.randint(0, 120, (rows_per_layer, d), dtype=torch.uint8, device="cuda").view(dt),
+                   torch.randint(0, 120, (rows_per_layer, d), dtype=torch.uint8, device="cuda").view(dt))
                   for _ in range(layers)]
-        live_d, base_d = live.cuda(), base.cuda()
-        slot = (base_d + live_d - 1).contiguous()
+        live_d, bt_d = live.cuda(), bt.cuda()
+        last = (live_d - 1).long()
+        slot = (torch.gather(bt_d, 3, (last // 16).unsqueeze(-1)).squeeze(-1) * 16 + last % 16).to(torch.int32)
         qkv = (torch.randn((b, (hq + 2 * hkv) * d), generator=gen) * 4).to(device="cuda", dtype=torch.bfloat16)
         q = qkv[:, :hq * d].view(b, hq, d)
         k = qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d)
@@ -307,9 +336,9 @@ def attention_scaling(llm, seqs, batches=(8, 32, 128), layers: int = 8, replays:
 
         def launch(l):
             fused_dms_rope_store_compact_decode_attention(
-                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions, base_d[l], live_d[l],
+                q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions, None, live_d[l],
                 num_kv_heads=hkv, alpha_scale=md.alpha_scale, alpha_offset=md.alpha_offset, max_live_count=hint,
-                out=out)
+                out=out, block_tables=bt_d[l])
 
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
@@ -331,15 +360,17 @@ def attention_scaling(llm, seqs, batches=(8, 32, 128), layers: int = 8, replays:
         per_launch_s = t0.elapsed_time(t1) / 1e3 / (replays * layers)
         elem = arenas[0][0].element_size()
         kv_bytes = int((live.to(torch.int64) - 1).clamp(min=0).sum()) * d * 2 * elem / layers
-        io_bytes = b * ((hq + 2 * hkv) * d * 2 + 2 * hkv * d * elem + hq * d * 2 + hkv * 13 + 8 + d * 4)
+        io_bytes = (b * ((hq + 2 * hkv) * d * 2 + 2 * hkv * d * elem + hq * d * 2 + hkv * 9 + 8 + d * 4)
+                    + 4 * int(npg.sum()) / layers)
         nbytes = kv_bytes + io_bytes
         achieved = nbytes / per_launch_s / 1e9
         rows.append({"batch": b, "pairs": b * hkv, "bytes_per_launch": int(nbytes),
                      "avg_launch_us": round(per_launch_s * 1e6, 2), "achieved": round(achieved, 1),
                      "frac": round(achieved / HBM_PEAK_GBPS, 4)})
         del arenas
-    return {"kernel": "decode_attn_mfma_kernel<fused>", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
-            "live_counts": "resampled from this run's decode state", "points": rows}
+    return {"kernel": "decode_attn_mfma_kernel<fused>", "layout": "paged (16-row pages, permuted ids)",
+            "unit": "GB/s", "peak": HBM_PEAK_GBPS, "live_counts": "resampled from this run's decode state",
+            "points": rows}
 
 
 def _pmc_traffic(name: str, config: str):
@@ -474,14 +505,26 @@ def cpu_baseline(llm, seqs, budget_s: float):
     md = runner.dms_metadata
     om = ock.OracleCompactKVManager(mgr.num_layers, mgr.num_kv_heads, mgr.capacity_tokens, mgr.max_model_len,
                                     head_dim=mgr.head_dim, dtype_code=numerics.DT_FP8)
-    om.free_ranges_per_layer = [list(r) for r in mgr.free_ranges_per_layer]
-    om.compact_k_per_layer = [t.view(torch.uint8).cpu().numpy() for t in mgr.compact_k_per_layer]
-    om.compact_v_per_layer = [t.view(torch.uint8).cpu().numpy() for t in mgr.compact_v_per_layer]
-    for s in seqs:
+    arenas_k = [t.view(torch.uint8).cpu().numpy() for t in mgr.compact_k_per_layer]
+    arenas_v = [t.view(torch.uint8).cpu().numpy() for t in mgr.compact_v_per_layer]
+    if mgr.paged:  # the oracle keeps flat spans: gather each span from its pages in rank order
+        slots = [mgr.seq_states[s.seq_id].active_slot for s in seqs]
+        caps = [mgr.seq_states[s.seq_id].max_capacity_per_lh for s in seqs]
+        live_all = mgr.layer_major_live_counts.cpu().numpy()
+        arenas_k, arenas_v, bases = ock.spans_from_pages(arenas_k, arenas_v, mgr.block_tables.cpu().numpy(),
+                                                         live_all, slots, caps)
+        om.free_ranges_per_layer = [[] for _ in range(mgr.num_layers)]
+    else:
+        om.free_ranges_per_layer = [list(r) for r in mgr.free_ranges_per_layer]
+    om.compact_k_per_layer, om.compact_v_per_layer = arenas_k, arenas_v
+    for i, s in enumerate(seqs):
         st = mgr.seq_states[s.seq_id]
+        if mgr.paged:
+            base, rcap = bases[i], np.full_like(bases[i], caps[i])
+        else:
+            base, rcap = st.base_offsets.cpu().numpy().copy(), st.range_capacity.cpu().numpy().copy()
         om.seq_states[s.seq_id] = ock.SeqState(
-            s.seq_id, st.base_offsets.cpu().numpy().copy(), st.range_capacity.cpu().numpy().copy(),
-            st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
+            s.seq_id, base, rcap, st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
             st.evict_mask.cpu().numpy().copy(), st.max_capacity_per_lh, st.decode_headroom,
             st.dms_initial_expiry_done, st.last_dms_expiry_position)
     orc = OracleModel(weights_from_model(runner.model), cfg, window_size=md.window_size, alpha_scale=md.alpha_scale,

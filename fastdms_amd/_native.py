@@ -56,6 +56,12 @@ SIGNATURES: dict[str, str] = {
     "fdms_linear_int4_small_m": "pliiplppilpiiipppppplp",
     "fdms_quantize_int4_groups": "pilliiiplpplp",
     "fdms_fp8_rerank_topk": "pliiplpipipp",
+    "fdms_paged_pack_prepare": "pllpiiiipllplllpppllllippppllpllipp",
+    "fdms_paged_pack_scatter": "ppillllpllpiplllppilpppllllllplliiiiippp",
+    "fdms_paged_prepare_decode": "plllplllplllplllplpipiiip",
+    "fdms_paged_free": "piplllplllplllplpiip",
+    "fdms_paged_expiry": "iplllplllplllplllplllplpppllpiiiip",
+    "fdms_fused_decode_attention_paged": "pllpllpllpllppllpllfffipplpllipllpllppiiiiiifppp",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

@@ -46,6 +46,12 @@ class Config:
     compact_kv_budget_bytes: int | None = None
     compact_kv_target_live_tokens_per_seq: int | None = None
     compact_kv_layer_major_metadata: bool = True
+    # Where the compact K/V rows live (no reference counterpart; the reference
+    # stores flat spans from a host first-fit allocator, compact_kv.py:697-857):
+    # "paged" = 16-row pages from a device-resident free-page pool (pack,
+    # decode append, expiry and free allocate on the device, no host sync per
+    # prefill layer); "span" = the reference's flat spans
+    compact_kv_layout: str = "paged"
     seed: int = 0
     dms_survive_fraction: float = 0.125
     compact_decode_cudagraph: bool = True
@@ -71,6 +77,8 @@ class Config:
     def __post_init__(self):
         from .models.synthetic import model_config
         assert self.kvcache_block_size % 256 == 0
+        if self.compact_kv_layout not in ("paged", "span"):
+            raise ValueError(f"compact_kv_layout must be 'paged' or 'span', got {self.compact_kv_layout!r}")
         if self.compact_admission not in ("defer", "preempt"):
             raise ValueError(f"compact_admission must be 'defer' or 'preempt', got {self.compact_admission!r}")
         if self.compact_decode_reserve_tokens is not None and (

@@ -932,10 +932,25 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* 
   const uint4* ksrc;
   const uint4* vsrc[4];
   if constexpr (PAGED) {
-    ksrc = reinterpret_cast<const uint4*>(kspan + span_row<true>(addr, b, h, 0, min(g0 + s + 16 * q, end - 1)) * c_s);
+    // A group starts 64-row aligned and pages hold >= 16 rows (the host
+    // checks), so each 16-row quarter of the group lies in one page: its id
+    // is a wave-uniform value, read through the scalar cache (the tables are
+    // not written during the launch), instead of a table load per lane.
+    using const_i32 = const __attribute__((address_space(4))) int32_t;
+    const_i32* trow = (const_i32*)(addr.table + b * addr.tb_b + h * addr.tb_h);
+    const int last = end - 1;
+    const int mask = (1 << addr.page_shift) - 1;
+    int64_t qrow[4];  // physical row of the first row of each quarter's page
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int r0 = __builtin_amdgcn_readfirstlane(min(g0 + 16 * kk, last));
+      qrow[kk] = (int64_t)trow[r0 >> addr.page_shift] << addr.page_shift;
+    }
+    const int64_t kq = q == 0 ? qrow[0] : q == 1 ? qrow[1] : q == 2 ? qrow[2] : qrow[3];
+    ksrc = reinterpret_cast<const uint4*>(kspan + (kq + (min(g0 + s + 16 * q, last) & mask)) * c_s);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + span_row<true>(addr, b, h, 0, min(g0 + s + 16 * kk, end - 1)) * c_s +
+      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + (qrow[kk] + (min(g0 + s + 16 * kk, last) & mask)) * c_s +
                                                 q * (D / 4));
   } else {
     const uint32_t cs = (uint32_t)c_s;
@@ -1072,7 +1087,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   }
 
   const int live = live_counts[b * lc_b + h * lc_h];
-  const int64_t bo = paged ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
+  const int64_t bo = PAGED ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
   const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
   const int ns = min(num_splits, max(1, (live + split_rows - 1) / split_rows));
   if (split >= ns) return;  // uniform per workgroup
@@ -1411,7 +1426,10 @@ FDMS_EXPORT int fdms_compact_decode_attention(
                         (c_s * kv_size) % 16 == 0 && ((uintptr_t)compact_k % 16) == 0 &&
                         ((uintptr_t)compact_v % 16) == 0 && (group_size == 1 || group_size == 2 ||
                         group_size == 4 || group_size == 8) && !fdms_force_generic_attention();
-  const bool mfma_ok = tiled_ok && kv_dtype == kFP8 && group_size <= 4 && fdms_mfma_attention_enabled();
+  // matrix-core path: pages (if any) of at least 16 rows, so a 64-row group's
+  // quarters each lie in one page
+  const bool mfma_ok = tiled_ok && kv_dtype == kFP8 && group_size <= 4 && fdms_mfma_attention_enabled() &&
+                       (!paged || page_shift >= 4);
   if (mfma_ok) {
     // split_rows: rows per split (rounded up to 64; 0 = one 64-row group per wave)
     const int nw = 4;
@@ -1485,14 +1503,23 @@ static int fused_decode_attention(
     int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
     int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
     int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
-    const float* v_scale, void* stream) {
+    const float* v_scale, void* stream, const int32_t* block_tables = nullptr, int64_t bt_b = 0, int64_t bt_h = 0,
+    int page_size = 0) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4) return (int)hipErrorInvalidValue;
   if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
     return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
   if (!q || !k || !v || !cos_sin || !positions || !slot_mapping || !evict_out || !compact_k || !compact_v ||
-      !base_offsets || !live_counts || !out)
+      !live_counts || !out)
     return (int)hipErrorInvalidValue;
+  int page_shift = 0;
+  if (block_tables) {  // pages of at least 16 rows (see mfma_load_group)
+    if (page_size < 16 || (page_size & (page_size - 1))) return (int)hipErrorInvalidValue;
+    while ((1 << page_shift) < page_size) ++page_shift;
+  } else if (!base_offsets) {
+    return (int)hipErrorInvalidValue;
+  }
+  const int paged = block_tables ? 1 : 0;
   if (c_s % 16 || ((uintptr_t)compact_k % 16) || ((uintptr_t)compact_v % 16)) return (int)hipErrorInvalidValue;
   if (num_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int pairs = batch * num_kv_heads;
@@ -1506,13 +1533,17 @@ static int fused_decode_attention(
   const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
   const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-#define FDMS_FUSED_LAUNCH(DD, NWV)                                                                                \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, false, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
-                     (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,   \
-                     c_s, base_offsets, bo_b, bo_h, nullptr, 0, 0, 0, 0, live_counts, lc_b, lc_h, (bf16_t*)out,     \
-                     os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, rows, scale,       \
-                     nullptr, 0, 0, nullptr, pre, k_scale, v_scale)
-  if (head_dim == 64) FDMS_FUSED_LAUNCH(64, 4); else FDMS_FUSED_LAUNCH(128, 8);
+#define FDMS_FUSED_LAUNCH(DD, NWV, PG)                                                                               \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0,     \
+                     (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,     \
+                     c_s, base_offsets, bo_b, bo_h, block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b,   \
+                     lc_h, (bf16_t*)out, os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, \
+                     rows, scale, nullptr, 0, 0, nullptr, pre, k_scale, v_scale)
+  if (head_dim == 64) {
+    if (paged) FDMS_FUSED_LAUNCH(64, 4, true); else FDMS_FUSED_LAUNCH(64, 4, false);
+  } else {
+    if (paged) FDMS_FUSED_LAUNCH(128, 8, true); else FDMS_FUSED_LAUNCH(128, 8, false);
+  }
 #undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;
@@ -1532,6 +1563,29 @@ FDMS_EXPORT int fdms_fused_decode_attention(
                                 positive_scale, compact_k, compact_v, c_s, base_offsets, bo_b, bo_h, live_counts, lc_b,
                                 lc_h, out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
                                 num_splits, split_rows, scale, k_scale, v_scale, stream);
+}
+
+// Paged-layout fused decode attention (no reference counterpart: the reference
+// reads flat spans): fdms_fused_decode_attention with rank r of (b, h) at row
+// block_tables[b, h, r / page_size] * page_size + r % page_size instead of
+// base_offsets[b, h] + r; slot_mapping holds the appended token's row (from
+// fdms_paged_prepare_decode).
+FDMS_EXPORT int fdms_fused_decode_attention_paged(
+    const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+    const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+    float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
+    int64_t c_s, const int32_t* block_tables, int64_t bt_b, int64_t bt_h, int page_size, const int32_t* live_counts,
+    int64_t lc_b, int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
+    int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
+    const float* v_scale, void* stream) {
+  if (!block_tables) return (int)hipErrorInvalidValue;
+  return fused_decode_attention(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
+                                slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
+                                positive_scale, compact_k, compact_v, c_s, nullptr, 0, 0, live_counts, lc_b, lc_h,
+                                out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
+                                num_splits, split_rows, scale, k_scale, v_scale, stream, block_tables, bt_b, bt_h,
+                                page_size);
 }
 
 // ---------------------------------------------------------------------------

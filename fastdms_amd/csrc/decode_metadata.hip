@@ -73,3 +73,120 @@ FDMS_EXPORT int fdms_record_dms_decisions(int32_t* positions, int64_t p_l, int64
   FDMS_LAUNCH_CHECK();
   return 0;
 }
+
+// ---------------------------------------------------------------------------
+// Paged compact KV (no reference counterpart: the reference appends into flat
+// spans, slot = base + live, compact_kv.py:1727-1770).  Per layer l the pool
+// holds free page ids stack[l * stack_stride + 0 .. top[l]); span (l, b, h)
+// owns pages bt[l, b, h, 0 .. held[l, b, h]) of 16 rows each.
+// ---------------------------------------------------------------------------
+constexpr int kPagedShift = 4;
+
+// Decode append slot with on-demand pages: when the span's pages are full
+// (live == 16 * held) one page is popped from the layer's stack (atomic,
+// distinct per thread) and appended to the span's table; then slot = the
+// physical row of rank live, and live += 1.  A pool that is short gives slot
+// -1 (no append) and sets *overflow.
+__global__ void paged_prepare_decode_kernel(int32_t* __restrict__ live, int64_t l_l, int64_t l_b, int64_t l_h,
+                                            int32_t* __restrict__ slot, int64_t s_l, int64_t s_b, int64_t s_h,
+                                            int32_t* __restrict__ bt, int64_t bt_l, int64_t bt_b, int64_t bt_h,
+                                            int32_t* __restrict__ held, int64_t hd_l, int64_t hd_b, int64_t hd_h,
+                                            const int32_t* __restrict__ stack, int64_t stack_stride,
+                                            int32_t* __restrict__ top, int max_pages, int32_t* __restrict__ overflow,
+                                            int num_seqs, int num_kv_heads, int total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int h = i % num_kv_heads;
+  const int b = (i / num_kv_heads) % num_seqs;
+  const int l = i / (num_kv_heads * num_seqs);
+  int32_t* lp = live + l * l_l + b * l_b + h * l_h;
+  int32_t* hp = held + l * hd_l + b * hd_b + h * hd_h;
+  int32_t* btr = bt + l * bt_l + b * bt_b + h * bt_h;
+  int32_t* sp = slot + l * s_l + b * s_b + h * s_h;
+  const int32_t n = *lp;
+  int32_t np = *hp;
+  if (n >= (np << kPagedShift)) {
+    int32_t got = -1;
+    if (np < max_pages) {
+      const int32_t t = atomicSub(top + l, 1);
+      if (t > 0) {
+        got = stack[l * stack_stride + t - 1];
+      } else {
+        atomicAdd(top + l, 1);
+      }
+    }
+    if (got < 0) {
+      atomicExch(overflow, 1);
+      *sp = -1;
+      return;
+    }
+    btr[np] = got;
+    *hp = ++np;
+  }
+  *sp = (btr[n >> kPagedShift] << kPagedShift) + (n & ((1 << kPagedShift) - 1));
+  *lp = n + 1;
+}
+
+FDMS_EXPORT int fdms_paged_prepare_decode(int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out,
+                                          int64_t s_l, int64_t s_b, int64_t s_h, int32_t* block_table, int64_t bt_l,
+                                          int64_t bt_b, int64_t bt_h, int32_t* pages_held, int64_t hd_l,
+                                          int64_t hd_b, int64_t hd_h, const int32_t* page_stack,
+                                          int64_t stack_stride, int32_t* page_top, int max_pages, int32_t* overflow,
+                                          int num_layers, int num_seqs, int num_kv_heads, void* stream) {
+  if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0 || max_pages <= 0) return (int)hipErrorInvalidValue;
+  const int total = num_layers * num_seqs * num_kv_heads;
+  if (total == 0) return 0;
+  if (!live || !slot_out || !block_table || !pages_held || !page_stack || !page_top || !overflow)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(paged_prepare_decode_kernel, dim3((total + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     live, l_l, l_b, l_h, slot_out, s_l, s_b, s_h, block_table, bt_l, bt_b, bt_h, pages_held, hd_l,
+                     hd_b, hd_h, page_stack, stack_stride, page_top, max_pages, overflow, num_seqs, num_kv_heads,
+                     total);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Return every page of the spans of rows[0 .. num_rows) (all layers, all kv
+// heads) to the layers' stacks and clear their tables (the sequence-free of
+// the paged layout; the span layout's is the host free list).  One thread per
+// (layer, row, head); pushes take distinct stack ranges with an atomic add.
+__global__ void paged_free_kernel(const int32_t* __restrict__ rows, int num_rows, int32_t* __restrict__ bt,
+                                  int64_t bt_l, int64_t bt_b, int64_t bt_h, int32_t* __restrict__ held, int64_t hd_l,
+                                  int64_t hd_b, int64_t hd_h, int32_t* __restrict__ live, int64_t l_l, int64_t l_b,
+                                  int64_t l_h, int32_t* __restrict__ stack, int64_t stack_stride,
+                                  int32_t* __restrict__ top, int num_kv_heads, int total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int h = i % num_kv_heads;
+  const int r = (i / num_kv_heads) % num_rows;
+  const int l = i / (num_kv_heads * num_rows);
+  const int64_t row = rows[r];
+  int32_t* hp = held + l * hd_l + row * hd_b + h * hd_h;
+  int32_t* btr = bt + l * bt_l + row * bt_b + h * bt_h;
+  const int32_t n = *hp;
+  if (n > 0) {
+    const int32_t at = atomicAdd(top + l, n);
+    for (int j = 0; j < n; ++j) {
+      stack[l * stack_stride + at + j] = btr[j];
+      btr[j] = -1;
+    }
+  }
+  *hp = 0;
+  live[l * l_l + row * l_b + h * l_h] = 0;
+}
+
+FDMS_EXPORT int fdms_paged_free(const int32_t* rows, int num_rows, int32_t* block_table, int64_t bt_l, int64_t bt_b,
+                                int64_t bt_h, int32_t* pages_held, int64_t hd_l, int64_t hd_b, int64_t hd_h,
+                                int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h, int32_t* page_stack,
+                                int64_t stack_stride, int32_t* page_top, int num_layers, int num_kv_heads,
+                                void* stream) {
+  if (num_layers <= 0 || num_rows < 0 || num_kv_heads <= 0) return (int)hipErrorInvalidValue;
+  const int total = num_layers * num_rows * num_kv_heads;
+  if (total == 0) return 0;
+  if (!rows || !block_table || !pages_held || !live || !page_stack || !page_top) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(paged_free_kernel, dim3((total + 255) / 256), dim3(256), 0, (hipStream_t)stream, rows, num_rows,
+                     block_table, bt_l, bt_b, bt_h, pages_held, hd_l, hd_b, hd_h, live, l_l, l_b, l_h, page_stack,
+                     stack_stride, page_top, num_kv_heads, total);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}

@@ -46,9 +46,15 @@ __device__ __forceinline__ int block_rank(bool keep, int* s_wave, int* total) {
 
 // Copy n_moves rows (src slot s_src[i] -> dst slot s_dst[i], both relative to
 // the span base) for K and V, in passes that read everything before writing.
+// Physical arena row of span slot r: base + r (flat spans) or, paged,
+// table[r >> 4] * 16 + (r & 15).
+__device__ __forceinline__ int64_t slot_row(int64_t base, const int32_t* table, int r) {
+  return table ? ((int64_t)table[r >> 4] << 4) + (r & 15) : base + r;
+}
+
 template <int UNIT>
 __device__ void move_rows(uint8_t* ck, uint8_t* cv, int64_t base, int64_t c_s_bytes, int64_t row_bytes,
-                          const int* s_src, const int* s_dst, int n_moves) {
+                          const int* s_src, const int* s_dst, int n_moves, const int32_t* table) {
   const int units_per_row = (int)(row_bytes / UNIT);
   const int total = n_moves * units_per_row * 2;
   for (int p0 = 0; p0 < total; p0 += kThreads * kUnitsPerThread) {
@@ -65,9 +71,10 @@ __device__ void move_rows(uint8_t* ck, uint8_t* cv, int64_t base, int64_t c_s_by
         const int r = uu / units_per_row;
         const int64_t off = (int64_t)(uu - r * units_per_row) * UNIT;
         uint8_t* arena = which ? cv : ck;
-        buf[j] = *reinterpret_cast<const Vec<uint8_t, UNIT>*>(arena + (base + s_src[r]) * c_s_bytes + off);
+        buf[j] = *reinterpret_cast<const Vec<uint8_t, UNIT>*>(arena + slot_row(base, table, s_src[r]) * c_s_bytes +
+                                                              off);
         dst_arena[j] = arena;
-        dst_off[j] = (base + s_dst[r]) * c_s_bytes + off;
+        dst_off[j] = slot_row(base, table, s_dst[r]) * c_s_bytes + off;
       }
     }
     __syncthreads();
@@ -76,6 +83,32 @@ __device__ void move_rows(uint8_t* ck, uint8_t* cv, int64_t base, int64_t c_s_by
       if (dst_arena[j]) *reinterpret_cast<Vec<uint8_t, UNIT>*>(dst_arena[j] + dst_off[j]) = buf[j];
     }
     __syncthreads();
+  }
+}
+
+// Paged spans of the expiry launch (table == nullptr: flat spans).  After the
+// re-compaction a span keeps ceil(live / 16) pages; the rest go back to the
+// layer's free stack (atomic add: distinct ranges).
+struct PagedSpans {
+  int32_t* table;
+  int64_t bt_l, bt_s, bt_h;
+  int32_t* held;
+  int64_t hd_l, hd_s, hd_h;
+  int32_t* stack;
+  int64_t stack_stride;
+  int32_t* top;
+};
+
+__device__ void release_pages(const PagedSpans& pg, int l, int32_t* table, int32_t* held, int live_after) {
+  const int keep = (live_after + 15) >> 4;
+  const int n = *held;
+  if (n > keep) {
+    const int32_t at = atomicAdd(pg.top + l, n - keep);
+    for (int j = keep; j < n; ++j) {
+      pg.stack[l * pg.stack_stride + at + (j - keep)] = table[j];
+      table[j] = -1;
+    }
+    *held = keep;
   }
 }
 
@@ -88,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
     int64_t lc_h, const int32_t* __restrict__ base_offsets, int64_t bo_l, int64_t bo_s, int64_t bo_h,
     uint8_t* compact_k, uint8_t* compact_v, const uint64_t* __restrict__ layer_k, const uint64_t* __restrict__ layer_v,
     int64_t row_bytes, int64_t c_s_bytes, const int64_t* __restrict__ current_positions, int num_kv_heads,
-    int window) {
+    int window, const PagedSpans pg) {
   __shared__ int s_wave[kThreads / kWave];
   __shared__ int s_wave_mv[kThreads / kWave];
   __shared__ int s_src[kThreads];
@@ -101,7 +134,9 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
   int32_t* pos = positions + l * ps_l + s * ps_s + h * ps_h;
   uint8_t* ev = evict + l * es_l + s * es_s + h * es_h;
   int32_t* live_p = live_counts + l * lc_l + s * lc_s + h * lc_h;
-  const int64_t base = base_offsets[l * bo_l + s * bo_s + h * bo_h];
+  const int64_t base = pg.table ? 0 : base_offsets[l * bo_l + s * bo_s + h * bo_h];
+  int32_t* table = pg.table ? pg.table + l * pg.bt_l + s * pg.bt_s + h * pg.bt_h : nullptr;
+  int32_t* held = pg.table ? pg.held + l * pg.hd_l + s * pg.hd_s + h * pg.hd_h : nullptr;
   uint8_t* ck = layer_k ? reinterpret_cast<uint8_t*>(layer_k[l]) : compact_k;
   uint8_t* cv = layer_v ? reinterpret_cast<uint8_t*>(layer_v[l]) : compact_v;
   const int64_t cur = current_positions[s];
@@ -144,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
           ev[r] = e;
         }
         __syncthreads();
-        if (nmv) move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, nmv);
+        if (nmv) move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, nmv, table);
       }
       running += total;
       __syncthreads();
@@ -153,7 +188,10 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
       pos[slot] = -1;
       ev[slot] = 0;
     }
-    if (tid == 0) *live_p = running;
+    if (tid == 0) {
+      *live_p = running;
+      if (table) release_pages(pg, l, table, held, running);
+    }
     return;
   }
 
@@ -193,25 +231,27 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
       pos[slot] = p;
       ev[slot] = e;
     }
-    move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, n);
+    move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, n, table);
   }
   if (tid == 0) {
     pos[live - 1] = -1;
     ev[live - 1] = 0;
     *live_p = live - 1;
+    if (table) release_pages(pg, l, table, held, live - 1);
   }
 }
 
-FDMS_EXPORT int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h,
-                                uint8_t* evict, int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts,
-                                int64_t lc_l, int64_t lc_s, int64_t lc_h, const int32_t* base_offsets, int64_t bo_l,
-                                int64_t bo_s, int64_t bo_h, void* compact_k, void* compact_v, const uint64_t* layer_k,
-                                const uint64_t* layer_v, int64_t row_bytes, int64_t c_s_bytes,
-                                const int64_t* current_positions, int num_layers, int num_seqs, int num_kv_heads,
-                                int window, void* stream) {
+static int launch_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h,
+                         uint8_t* evict, int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts,
+                         int64_t lc_l, int64_t lc_s, int64_t lc_h, const int32_t* base_offsets, int64_t bo_l,
+                         int64_t bo_s, int64_t bo_h, void* compact_k, void* compact_v, const uint64_t* layer_k,
+                         const uint64_t* layer_v, int64_t row_bytes, int64_t c_s_bytes,
+                         const int64_t* current_positions, int num_layers, int num_seqs, int num_kv_heads,
+                         int window, void* stream, const PagedSpans pg) {
   if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0 || row_bytes <= 0) return (int)hipErrorInvalidValue;
   if (num_seqs == 0) return 0;
-  if (!positions || !evict || !live_counts || !base_offsets || !current_positions) return (int)hipErrorInvalidValue;
+  if (!positions || !evict || !live_counts || !current_positions) return (int)hipErrorInvalidValue;
+  if (pg.table ? (!pg.held || !pg.stack || !pg.top) : !base_offsets) return (int)hipErrorInvalidValue;
   if (!(layer_k && layer_v) && !(compact_k && compact_v)) return (int)hipErrorInvalidValue;
   if ((int64_t)num_seqs * num_kv_heads > 0x7FFFFFFF || num_layers > 65535) return (int)hipErrorInvalidValue;
   const dim3 grid(num_seqs * num_kv_heads, num_layers);
@@ -222,7 +262,7 @@ FDMS_EXPORT int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_
   hipLaunchKernelGGL((dms_expiry_kernel<U, INC>), grid, dim3(kThreads), 0, (hipStream_t)stream, positions, ps_l, \
                      ps_s, ps_h, evict, es_l, es_s, es_h, live_counts, lc_l, lc_s, lc_h, base_offsets, bo_l, bo_s, \
                      bo_h, (uint8_t*)compact_k, (uint8_t*)compact_v, layer_k, layer_v, row_bytes, c_s_bytes,       \
-                     current_positions, num_kv_heads, window)
+                     current_positions, num_kv_heads, window, pg)
   if (incremental) {
     if (unit == 16) FDMS_EXPIRY_LAUNCH(16, true);
     else if (unit == 4) FDMS_EXPIRY_LAUNCH(4, true);
@@ -235,4 +275,36 @@ FDMS_EXPORT int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_
 #undef FDMS_EXPIRY_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;
+}
+
+FDMS_EXPORT int fdms_dms_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h,
+                                uint8_t* evict, int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts,
+                                int64_t lc_l, int64_t lc_s, int64_t lc_h, const int32_t* base_offsets, int64_t bo_l,
+                                int64_t bo_s, int64_t bo_h, void* compact_k, void* compact_v, const uint64_t* layer_k,
+                                const uint64_t* layer_v, int64_t row_bytes, int64_t c_s_bytes,
+                                const int64_t* current_positions, int num_layers, int num_seqs, int num_kv_heads,
+                                int window, void* stream) {
+  return launch_expiry(incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live_counts, lc_l, lc_s,
+                       lc_h, base_offsets, bo_l, bo_s, bo_h, compact_k, compact_v, layer_k, layer_v, row_bytes,
+                       c_s_bytes, current_positions, num_layers, num_seqs, num_kv_heads, window, stream, PagedSpans{});
+}
+
+// Paged-layout expiry (no reference counterpart: the reference re-compacts
+// flat spans, compact_attention.py:690-965): the same re-compaction with span
+// slot r at row block_table[l, s, h, r >> 4] * 16 + (r & 15), after which each
+// span keeps ceil(live / 16) pages and returns the rest to its layer's free
+// stack (page_stack[l * stack_stride ...], page_top[l]).
+FDMS_EXPORT int fdms_paged_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h,
+                                  uint8_t* evict, int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts,
+                                  int64_t lc_l, int64_t lc_s, int64_t lc_h, int32_t* block_table, int64_t bt_l,
+                                  int64_t bt_s, int64_t bt_h, int32_t* pages_held, int64_t hd_l, int64_t hd_s,
+                                  int64_t hd_h, int32_t* page_stack, int64_t stack_stride, int32_t* page_top,
+                                  const uint64_t* layer_k, const uint64_t* layer_v, int64_t row_bytes,
+                                  int64_t c_s_bytes, const int64_t* current_positions, int num_layers, int num_seqs,
+                                  int num_kv_heads, int window, void* stream) {
+  if (!block_table || !layer_k || !layer_v) return (int)hipErrorInvalidValue;
+  const PagedSpans pg{block_table, bt_l, bt_s, bt_h, pages_held, hd_l, hd_s, hd_h, page_stack, stack_stride, page_top};
+  return launch_expiry(incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live_counts, lc_l, lc_s,
+                       lc_h, nullptr, 0, 0, 0, nullptr, nullptr, layer_k, layer_v, row_bytes, c_s_bytes,
+                       current_positions, num_layers, num_seqs, num_kv_heads, window, stream, pg);
 }

@@ -67,13 +67,31 @@ __device__ __forceinline__ SeqSpan seq_span(const int32_t* cu, int b, int single
 // chunk with a ballot, and the running offset is accumulated uniformly.
 constexpr int kPrepBatch = 32;
 
+// Page pool of one layer (paged compact KV): the free page ids are
+// stack[0 .. *top); a (seq, head) span owns pages bt[row * bt_b + h * bt_h + j],
+// j < held[row * hd_b + h * hd_h], rank r living at row bt[r >> 4] * 16 + (r & 15).
+struct PagePool {
+  int32_t* stack;
+  int32_t* top;
+  int32_t* budget;  // pages this launch may still take (debited before the stack), or nullptr
+  int32_t* bt;
+  int64_t bt_b, bt_h;
+  int32_t* held;
+  int64_t hd_b, hd_h;
+  int max_pages;
+  int32_t* overflow;  // set to 1 when a pop finds the pool short (the pop is undone)
+};
+constexpr int kPageShift = 4;  // 16-row pages
+
+template <bool PAGED>
 __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     const uint8_t* __restrict__ evict, int64_t es_t, int64_t es_h, const int32_t* __restrict__ cu,
     int single_len, int window, int num_kv_heads, int max_chunks, int32_t* __restrict__ live_out, int64_t lo_b,
     int64_t lo_h, int32_t* __restrict__ offsets, int64_t of_b, int64_t of_h, int64_t of_c,
     int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta, const int32_t* __restrict__ meta_rows,
-    int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap) {
+    int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap, const PagePool pool) {
   __shared__ int s_cnt[kPrepBatch][kChunk / kWave];
+  __shared__ int s_p0;
   const int h = blockIdx.x % num_kv_heads;
   const int b = blockIdx.x / num_kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -120,9 +138,44 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     if (c0 + kPrepBatch < max_chunks) __syncthreads();  // s_cnt is reused by the next batch
   }
   if (tid == 0) live_out[b * lo_b + h * lo_h] = running;
+  if constexpr (PAGED) {
+    // ceil(live / 16) pages from the layer's free stack: one atomic pop per
+    // (seq, head) (distinct ranges), then the span's block-table row
+    const int64_t row = meta_rows ? meta_rows[b] : b;
+    const int n = (running + (1 << kPageShift) - 1) >> kPageShift;
+    if (tid == 0) {
+      int p0 = -1;
+      if (n > 0 && n <= pool.max_pages) {
+        bool ok = true;
+        if (pool.budget && atomicSub(pool.budget, n) < n) {
+          atomicAdd(pool.budget, n);
+          ok = false;
+        }
+        if (ok) {
+          p0 = atomicSub(pool.top, n) - n;
+          if (p0 < 0) {
+            atomicAdd(pool.top, n);
+            if (pool.budget) atomicAdd(pool.budget, n);
+            p0 = -1;
+          }
+        }
+      }
+      if (p0 < 0 && n > 0) {
+        // no pages: the span is left empty (live 0) and the launch flagged
+        atomicExch(pool.overflow, 1);
+        live_out[b * lo_b + h * lo_h] = 0;
+      }
+      s_p0 = p0;
+    }
+    __syncthreads();
+    const int p0 = s_p0;
+    int32_t* btr = pool.bt + row * pool.bt_b + h * pool.bt_h;
+    for (int j = tid; j < pool.max_pages; j += kChunk) btr[j] = (p0 >= 0 && j < n) ? pool.stack[p0 + j] : -1;
+    if (tid == 0) pool.held[row * pool.hd_b + h * pool.hd_h] = p0 >= 0 ? n : 0;
+  }
 }
 
-template <typename TI, typename TO, int VEC, bool FUSED>
+template <typename TI, typename TO, int VEC, bool FUSED, bool PAGED>
 __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
     const TI* __restrict__ k, const TI* __restrict__ v, int64_t ks_t, int64_t ks_h, int64_t vs_t, int64_t vs_h,
     const uint8_t* __restrict__ evict, int64_t es_t, int64_t es_h, const int32_t* __restrict__ cu, int single_start,
@@ -132,7 +185,7 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
     TO* __restrict__ cv, int64_t cs_s, int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta,
     const int32_t* __restrict__ meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s, int64_t em_b, int64_t em_h,
     int64_t em_s, int window, int num_kv_heads, int head_dim, const float* __restrict__ k_scale,
-    const float* __restrict__ v_scale) {
+    const float* __restrict__ v_scale, const int32_t* __restrict__ bt, int64_t bt_b, int64_t bt_h) {
   __shared__ int s_wave[kChunk / kWave];
   __shared__ int64_t s_src[kChunk];
   __shared__ int64_t s_dst[kChunk];
@@ -143,7 +196,8 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
   if (c * kChunk >= sp.len) return;  // uniform per block
   // per-block scalars first: their loads overlap the evict load
   const int64_t row = meta_rows ? meta_rows[b] : b;
-  const int64_t span0 = base[b * bs_b + h * bs_h];
+  const int64_t span0 = PAGED ? 0 : base[b * bs_b + h * bs_h];
+  const int32_t* btr = PAGED ? bt + row * bt_b + h * bt_h : nullptr;
   const float kmul = inv_scale(k_scale, h), vmul = inv_scale(v_scale, h);
   const int chunk0 = FUSED ? block_offsets[b * bo_b + h * bo_h + c * bo_c] : 0;
   const int t = c * kChunk + threadIdx.x;
@@ -162,7 +216,12 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
   if (keep) {
     rank = FUSED ? (int64_t)chunk0 + local : (int64_t)rank_in[(int64_t)t * rk_t + h * rk_h];
     s_src[local] = sp.tok0 + t;
-    s_dst[local] = span0 + rank;
+    if constexpr (PAGED) {
+      const int32_t page = btr[rank >> kPageShift];  // -1: the span got no pages (pool short)
+      s_dst[local] = page < 0 ? -1 : ((int64_t)page << kPageShift) + (rank & ((1 << kPageShift) - 1));
+    } else {
+      s_dst[local] = span0 + rank;
+    }
   }
   __syncthreads();
   // metadata stores after the barrier, so the barrier does not wait for them
@@ -184,13 +243,13 @@ __global__ __launch_bounds__(kChunk) void pack_scatter_kernel(
       const int r = u / units;
       const int j = (u - r * units) * VEC;
       const int64_t src = s_src[r];
-      dst[i] = s_dst[r] * cs_s + j;
+      dst[i] = s_dst[r] < 0 ? -1 : s_dst[r] * cs_s + j;
       kr[i] = *reinterpret_cast<const Vec<TI, VEC>*>(k + src * ks_t + h * ks_h + j);
       vr[i] = *reinterpret_cast<const Vec<TI, VEC>*>(v + src * vs_t + h * vs_h + j);
     }
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
-      if (u0 + i * kChunk < n) {
+      if (u0 + i * kChunk < n && dst[i] >= 0) {
         *reinterpret_cast<Vec<TO, VEC>*>(ck + dst[i]) = convert_vec_scaled<TI, TO, VEC>(kr[i], kmul);
         *reinterpret_cast<Vec<TO, VEC>*>(cv + dst[i]) = convert_vec_scaled<TI, TO, VEC>(vr[i], vmul);
       }
@@ -208,15 +267,15 @@ FDMS_EXPORT int fdms_streaming_pack_prepare(const uint8_t* evict, int64_t es_t, 
   if (num_seqs <= 0 || num_kv_heads <= 0 || max_chunks < 0) return (int)hipErrorInvalidValue;
   if (!evict || !live_out || (max_chunks > 0 && !block_offsets)) return (int)hipErrorInvalidValue;
   if (positions && !evict_meta) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(pack_prepare_kernel, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0, (hipStream_t)stream,
-                     evict, es_t, es_h, cu_seqlens, single_len, window, num_kv_heads, max_chunks, live_out, lo_b,
-                     lo_h, block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
-                     meta_cap);
+  hipLaunchKernelGGL(pack_prepare_kernel<false>, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0,
+                     (hipStream_t)stream, evict, es_t, es_h, cu_seqlens, single_len, window, num_kv_heads, max_chunks,
+                     live_out, lo_b, lo_h, block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b,
+                     tp_h, em_b, em_h, meta_cap, PagePool{});
   FDMS_LAUNCH_CHECK();
   return 0;
 }
 
-template <bool FUSED>
+template <bool FUSED, bool PAGED = false>
 static int launch_scatter(const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t,
                           int64_t vs_h, const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu,
                           int single_start, int single_len, int num_seqs, const int32_t* bo, int64_t bo_b,
@@ -225,19 +284,21 @@ static int launch_scatter(const void* k, const void* v, int kv_dtype, int64_t ks
                           int64_t bs_h, void* ck, void* cv, int compact_dtype, int64_t cs_s, int32_t* positions,
                           uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h, int64_t tp_s,
                           int64_t em_b, int64_t em_h, int64_t em_s, int window, int num_kv_heads, int head_dim,
-                          int max_chunks, int vec, const float* k_scale, const float* v_scale, void* stream) {
+                          int max_chunks, int vec, const float* k_scale, const float* v_scale, void* stream,
+                          const int32_t* bt = nullptr, int64_t bt_b = 0, int64_t bt_h = 0) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_chunks <= 0) return (int)hipErrorInvalidValue;
   if (vec <= 0 || head_dim % vec != 0) return (int)hipErrorInvalidValue;
-  if (!k || !v || !evict || !base || !ck || !cv || !positions || !evict_meta) return (int)hipErrorInvalidValue;
+  if (!k || !v || !evict || !ck || !cv || !positions || !evict_meta) return (int)hipErrorInvalidValue;
+  if (PAGED ? !bt : !base) return (int)hipErrorInvalidValue;
   const dim3 grid(max_chunks, num_seqs * num_kv_heads);
   FDMS_DISPATCH_DTYPE(kv_dtype, TI,
     FDMS_DISPATCH_DTYPE(compact_dtype, TO,
       FDMS_DISPATCH_VEC(vec, V,
-        hipLaunchKernelGGL((pack_scatter_kernel<TI, TO, V, FUSED>), grid, dim3(kChunk), 0, (hipStream_t)stream,
+        hipLaunchKernelGGL((pack_scatter_kernel<TI, TO, V, FUSED, PAGED>), grid, dim3(kChunk), 0, (hipStream_t)stream,
                            (const TI*)k, (const TI*)v, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
                            single_len, bo, bo_b, bo_h, bo_c, keep, kp_t, kp_h, rank, rk_t, rk_h, base, bs_b, bs_h,
                            (TO*)ck, (TO*)cv, cs_s, positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h,
-                           em_s, window, num_kv_heads, head_dim, k_scale, v_scale))));
+                           em_s, window, num_kv_heads, head_dim, k_scale, v_scale, bt, bt_b, bt_h))));
   FDMS_LAUNCH_CHECK();
   return 0;
 }
@@ -273,4 +334,57 @@ FDMS_EXPORT int fdms_streaming_pack_scatter(
                                compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta, nullptr, 0, tp_h,
                                tp_s, 0, em_h, em_s, 0, num_kv_heads, head_dim, max_chunks, vec, k_scale, v_scale,
                                stream);
+}
+
+// Paged compact KV, prefill side (no reference counterpart: the reference packs
+// into flat spans from a host first-fit allocator, compact_kv.py:830-857,
+// 955-1099).  Prepare = fdms_streaming_pack_prepare plus the page pop of every
+// (seq, head): ceil(live / 16) pages from the layer's free stack into the
+// span's block-table row (other entries -1) and held[row, h].  With
+// page_budget (one counter per layer) the pops of the launch also debit it
+// first, so pages kept for other sequences' decode appends stay on the stack.
+// A span whose pages do not fit (budget or stack short) gets none and live 0,
+// and *overflow is set: the caller then gives up the batch (frees its spans).
+// One layer per call; pops use atomics, so which page ids a span gets depends
+// on the order the workgroups run in (the rows a rank lands in follow the
+// table).
+FDMS_EXPORT int fdms_paged_pack_prepare(const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens,
+                                        int num_seqs, int window, int num_kv_heads, int max_chunks,
+                                        int32_t* live_out, int64_t lo_b, int64_t lo_h, int32_t* block_offsets,
+                                        int64_t of_b, int64_t of_h, int64_t of_c, int32_t* positions,
+                                        uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b, int64_t tp_h,
+                                        int64_t em_b, int64_t em_h, int meta_cap, int32_t* page_stack,
+                                        int32_t* page_top, int32_t* page_budget, int32_t* block_table,
+                                        int64_t bt_b, int64_t bt_h, int32_t* pages_held, int64_t hd_b, int64_t hd_h,
+                                        int max_pages, int32_t* overflow, void* stream) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || max_chunks <= 0 || max_pages <= 0) return (int)hipErrorInvalidValue;
+  if (!evict || !cu_seqlens || !live_out || !block_offsets || !positions || !evict_meta) return (int)hipErrorInvalidValue;
+  if (!page_stack || !page_top || !block_table || !pages_held || !overflow) return (int)hipErrorInvalidValue;
+  const PagePool pool{page_stack, page_top, page_budget, block_table, bt_b, bt_h, pages_held, hd_b, hd_h, max_pages,
+                      overflow};
+  hipLaunchKernelGGL(pack_prepare_kernel<true>, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0, (hipStream_t)stream,
+                     evict, es_t, es_h, cu_seqlens, 0, window, num_kv_heads, max_chunks, live_out, lo_b, lo_h,
+                     block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
+                     meta_cap, pool);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Paged compact KV, prefill side: fdms_streaming_pack_rank_scatter with rank r
+// of (seq, head) stored at row block_table[row, h, r >> 4] * 16 + (r & 15)
+// (the table written by fdms_paged_pack_prepare).
+FDMS_EXPORT int fdms_paged_pack_scatter(
+    const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t, int64_t vs_h,
+    const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens, int num_seqs,
+    const int32_t* block_offsets, int64_t bo_b, int64_t bo_h, int64_t bo_c, void* compact_k, void* compact_v,
+    int compact_dtype, int64_t cs_s, int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows, int64_t tp_b,
+    int64_t tp_h, int64_t tp_s, int64_t em_b, int64_t em_h, int64_t em_s, const int32_t* block_table, int64_t bt_b,
+    int64_t bt_h, int window, int num_kv_heads, int head_dim, int max_chunks, int vec, const float* k_scale,
+    const float* v_scale, void* stream) {
+  if (!block_offsets || !cu_seqlens) return (int)hipErrorInvalidValue;
+  return launch_scatter<true, true>(k, v, kv_dtype, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu_seqlens, 0, 0,
+                                    num_seqs, block_offsets, bo_b, bo_h, bo_c, nullptr, 0, 0, nullptr, 0, 0, nullptr,
+                                    0, 0, compact_k, compact_v, compact_dtype, cs_s, positions, evict_meta, meta_rows,
+                                    tp_b, tp_h, tp_s, em_b, em_h, em_s, window, num_kv_heads, head_dim, max_chunks,
+                                    vec, k_scale, v_scale, stream, block_table, bt_b, bt_h);
 }

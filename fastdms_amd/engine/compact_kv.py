@@ -175,6 +175,8 @@ class CompactCapacityExhausted(RuntimeError):
 class CompactKVManager:
     """Per-(layer, sequence, kv head) compact spans (compact_kv.py:554-1795)."""
 
+    paged = False  # flat spans; engine.paged_kv.PagedCompactKVManager stores pages
+
     def __init__(self, *, num_layers: int, num_kv_heads: int, capacity_tokens: int, max_model_len: int,
                  device: torch.device | str, target_live_tokens_per_seq: int | None = None,
                  head_dim: int | None = None, compact_dtype: torch.dtype | None = None,
@@ -666,9 +668,7 @@ class CompactKVManager:
             return
         if len(states) != len(self.active_slot_by_seq):
             raise RuntimeError("slot packing needs every active sequence in the batch")
-        tensors = (self.layer_major_base_offsets, self.layer_major_range_capacity, self.layer_major_live_counts,
-                   self.layer_major_token_positions, self.layer_major_evict_mask)
-        fills = (-1, 0, 0, -1, False)
+        tensors, fills = self._slot_tables()
         target = {st.seq_id: i for i, st in enumerate(states)}
         moving = [st for st in states if st.active_slot != target[st.seq_id]]
         if not moving:
@@ -688,6 +688,19 @@ class CompactKVManager:
                 t[:, slot].fill_(f)
         used = set(self.active_slot_by_seq.values())
         self.free_active_slots = [i for i in range(self.max_active_seqs) if i not in used]
+
+    def _slot_tables(self) -> tuple[tuple, tuple]:
+        """The layer-major tables indexed [layer, slot, ...] and the value of
+        an empty slot in each (what pack_active_slots moves)."""
+        return ((self.layer_major_base_offsets, self.layer_major_range_capacity, self.layer_major_live_counts,
+                 self.layer_major_token_positions, self.layer_major_evict_mask), (-1, 0, 0, -1, False))
+
+    def note_decode_step(self, states) -> None:
+        """Host bookkeeping of one decode append per sequence (no device work):
+        the live-count upper bound grows by one, the free-row bound shrinks."""
+        for st in states:
+            st.live_upper_bound += 1
+            st.decode_slack -= 1
 
     def _contiguous_active_slot_start(self, states) -> int | None:
         """compact_kv.py:1162-1172."""

@@ -77,6 +77,22 @@ class LLMEngine:
                     self._free_preempted()
         return [s for s in seqs if s in self.scheduler.running]
 
+    def _make_page_room(self, seqs):
+        """Paged layout, before a decode step: while the next append of every
+        running sequence may not fit the page pool (one sync of the page
+        counts decides), preempt the youngest running sequence.  With the full
+        decode reservation admission already guarantees the room.  Returns
+        the batch without the preempted sequences."""
+        mgr = self.model_runner.compact_kv_manager
+        while seqs and not mgr.decode_pages_fit():
+            victim = self.scheduler.preemption_victim([min(seqs, key=lambda s: s.seq_id)], include_self=True)
+            if victim is None:
+                raise CompactCapacityExhausted("paged compact KV: no page for the next decode step")
+            self.scheduler.preempt(victim)
+            self._free_preempted()
+            seqs = [s for s in seqs if s in self.scheduler.running]
+        return seqs
+
     def step(self):
         seqs, is_prefill = self.scheduler.schedule()
         t0 = time.perf_counter()
@@ -89,7 +105,9 @@ class LLMEngine:
             else:
                 seqs = done
         if not is_prefill:
-            if self.config.compact_decode_reserve_tokens is not None:
+            if self.model_runner.compact_kv_manager.paged:
+                seqs = self._make_page_room(seqs)
+            elif self.config.compact_decode_reserve_tokens is not None:
                 seqs = self._make_decode_room(seqs)
             token_ids = self.model_runner.run(seqs, False) if seqs else []
         dt = time.perf_counter() - t0

@@ -27,6 +27,7 @@ from ..models.synthetic import build_synthetic_model
 from ..utils.context import get_context, reset_context, set_context
 from .chunked_prefill import ChunkPlan, PromptStage
 from .compact_kv import CompactKVManager
+from .paged_kv import PagedCompactKVManager
 from .dms import DMSMetadata, load_dms_metadata
 from .sequence import Sequence, SequenceStatus
 
@@ -147,13 +148,20 @@ class ModelRunner:
             cap = self.max_num_seqs * self.num_kv_heads * c.max_model_len
         if cap <= 0:
             raise ValueError("compact KV capacity must be positive")
-        self.compact_kv_manager = CompactKVManager(
-            num_layers=self.num_layers, num_kv_heads=self.num_kv_heads, capacity_tokens=cap,
-            max_model_len=c.max_model_len, device=self.device,
-            target_live_tokens_per_seq=c.compact_kv_target_live_tokens_per_seq, head_dim=self.head_dim,
-            compact_dtype=self.kv_dtype, per_layer_storage=True, layer_major_metadata=True,
-            max_active_seqs=self.max_num_seqs, preallocate=True,
-            decode_reserve_tokens=c.compact_decode_reserve_tokens, fp8_scales=c.compact_kv_fp8_scales)
+        if c.compact_kv_layout == "paged":
+            self.compact_kv_manager = PagedCompactKVManager(
+                num_layers=self.num_layers, num_kv_heads=self.num_kv_heads, capacity_tokens=cap,
+                max_model_len=c.max_model_len, device=self.device, head_dim=self.head_dim,
+                compact_dtype=self.kv_dtype, max_active_seqs=self.max_num_seqs,
+                decode_reserve_tokens=c.compact_decode_reserve_tokens, fp8_scales=c.compact_kv_fp8_scales)
+        else:
+            self.compact_kv_manager = CompactKVManager(
+                num_layers=self.num_layers, num_kv_heads=self.num_kv_heads, capacity_tokens=cap,
+                max_model_len=c.max_model_len, device=self.device,
+                target_live_tokens_per_seq=c.compact_kv_target_live_tokens_per_seq, head_dim=self.head_dim,
+                compact_dtype=self.kv_dtype, per_layer_storage=True, layer_major_metadata=True,
+                max_active_seqs=self.max_num_seqs, preallocate=True,
+                decode_reserve_tokens=c.compact_decode_reserve_tokens, fp8_scales=c.compact_kv_fp8_scales)
         attn_modules = []
         for layer_id, layer in enumerate(self.model.model.layers):
             layer.self_attn.attn.layer_id = layer_id
@@ -200,6 +208,8 @@ class ModelRunner:
             chunk.cu_rest = (torch.tensor(chunk.cu_rest_host, dtype=torch.int32, pin_memory=True)
                              .to(self.device, non_blocking=True)) if pack_ids else None
             pack_ids = pack_ids + ([chunk.seq_id] if chunk.final else [])
+        if self.compact_kv_manager.paged:
+            self.compact_kv_manager.begin_prefill()
         md = self.dms_metadata
         set_context(True, cu_t, cu_t, max_q, max_q, dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale,
                     dms_alpha_offset=md.alpha_offset, dms_layer_evictions={},
@@ -246,12 +256,18 @@ class ModelRunner:
         total = sum(e.numel() for e in ctx.dms_layer_evictions.values())
         true = sum(e.sum() for e in ctx.dms_layer_evictions.values())
         chunk = ctx.prefill_chunk
+        packed = list(ctx.streaming_pack_seq_ids or [])
         reset_context()
+        mgr = self.compact_kv_manager
+        if mgr.paged:
+            mgr.stage_prefill_check(packed)
+        out = tokens.tolist()
+        if mgr.paged:
+            mgr.finish_prefill_check()  # CompactCapacityExhausted when the batch's pages did not fit
         if chunk is not None:  # the chunk is staged; a completed prompt is packed and its stage dropped
             chunk.stage.filled = chunk.end
             if chunk.final:
                 self.prompt_stages.pop(chunk.seq_id, None)
-        out = tokens.tolist()
         self.last_compact_prefill_stats = {"eviction_decisions_total": total,
                                            "eviction_decisions_true": int(true) if total else 0}
         return out
@@ -262,17 +278,22 @@ class ModelRunner:
         logits tensor (graph-owned under capture: each replay refreshes it)."""
         mgr = self.compact_kv_manager
         L, H = self.num_layers, self.num_kv_heads
-        base = mgr.layer_major_base_offsets[:, start:start + batch]
-        live = mgr.layer_major_live_counts[:, start:start + batch]
         slot = self.static_slot[:, :batch]
-        nat.call("fdms_prepare_decode_metadata", base.data_ptr(), base.stride(0), base.stride(1), base.stride(2),
-                 live.data_ptr(), live.stride(0), live.stride(1), live.stride(2), slot.data_ptr(), slot.stride(0),
-                 slot.stride(1), slot.stride(2), L, batch, H, nat.stream())
+        if mgr.paged:
+            bt, live = mgr.paged_prepare_decode(start, batch, slot)
+            base = None
+        else:
+            bt = None
+            base = mgr.layer_major_base_offsets[:, start:start + batch]
+            live = mgr.layer_major_live_counts[:, start:start + batch]
+            nat.call("fdms_prepare_decode_metadata", base.data_ptr(), base.stride(0), base.stride(1),
+                     base.stride(2), live.data_ptr(), live.stride(0), live.stride(1), live.stride(2),
+                     slot.data_ptr(), slot.stride(0), slot.stride(1), slot.stride(2), L, batch, H, nat.stream())
         md = self.dms_metadata
         evict = self.evict_buffer[:, :batch]
-        set_context(False, compact_kv_enabled=True, compact_base_offsets=base, compact_live_counts=live,
-                    compact_slot_mapping=slot, compact_max_live_count=max_live_hint, dms_capture_enabled=True,
-                    dms_alpha_scale=md.alpha_scale, dms_alpha_offset=md.alpha_offset,
+        set_context(False, block_tables=bt, compact_kv_enabled=True, compact_base_offsets=base,
+                    compact_live_counts=live, compact_slot_mapping=slot, compact_max_live_count=max_live_hint,
+                    dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale, dms_alpha_offset=md.alpha_offset,
                     dms_layer_evictions_buffer=evict)
         ids = self.static_input_ids[:batch]
         pos = self.static_positions[:batch]
@@ -327,9 +348,7 @@ class ModelRunner:
         start = mgr._contiguous_active_slot_start(states)
         if start is None:
             raise RuntimeError("decode batch must occupy contiguous active slots")
-        for st in states:
-            st.live_upper_bound += 1
-            st.decode_slack -= 1
+        mgr.note_decode_step(states)
         return start, self.attention_hint(seqs)
 
     def _replay_decode(self, start: int, batch: int, hint: int) -> None:
@@ -375,7 +394,12 @@ class ModelRunner:
         self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
         self._replay_decode(start, batch, hint)
         self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
-        return self.static_tokens[:batch].tolist()
+        if mgr.paged:
+            mgr.stage_overflow_check()
+        out = self.static_tokens[:batch].tolist()
+        if mgr.paged:
+            mgr.check_overflow(sync=False)
+        return out
 
     @torch.inference_mode()
     def run_compact_greedy_decode_loop(self, seqs: list[Sequence], max_steps: int):
@@ -401,6 +425,8 @@ class ModelRunner:
         mgr = self.compact_kv_manager
         batch = len(seqs)
         mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
+        if mgr.paged and not mgr.decode_pages_fit(max_steps):
+            raise RuntimeError(f"compact greedy fast loop: {max_steps} appends do not fit the page pool")
         base_pos = [len(seq) - 1 for seq in seqs]
         pos_table = torch.tensor([[p + step for p in base_pos] for step in range(max_steps)], dtype=torch.int64,
                                  pin_memory=True)
@@ -415,7 +441,11 @@ class ModelRunner:
                 self.static_input_ids[:batch].copy_(self.static_tokens[:batch])
             self._replay_decode(start, batch, hint)
             tokens[step].copy_(self.static_tokens[:batch])
+        if mgr.paged:
+            mgr.stage_overflow_check()
         out = tokens.t().contiguous().cpu().tolist()  # the loop's one host sync
+        if mgr.paged:
+            mgr.check_overflow(sync=False)
         for seq, toks in zip(seqs, out):
             for t in toks:
                 seq.append_token(t)

@@ -13,8 +13,10 @@ from torch import nn
 
 from .. import _native as nat
 from ..utils.context import get_context
-from .compact_attention import (compact_decode_attention, fused_dms_rope_store_compact_decode_attention,
-                                store_compact_kvcache)
+from .compact_attention import (compact_decode_attention, compact_decode_attention_paged,
+                                fused_dms_rope_store_compact_decode_attention, store_compact_kvcache)
+
+PAGE_SIZE = 16  # rows per page of the paged compact layout (engine.paged_kv)
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
@@ -71,30 +73,41 @@ class Attention(nn.Module):
             return prefill_attention(q, k, v, ctx.cu_seqlens_q, ctx.max_seqlen_q, self.scale, out=out)
         if not ctx.compact_kv_enabled:
             raise RuntimeError("dense paged decode is not part of this build; enable compact KV")
-        if ctx.compact_base_offsets is None or ctx.compact_live_counts is None:
-            raise RuntimeError("compact KV decode requires compact_base_offsets and compact_live_counts")
-        base, live, slot = ctx.compact_base_offsets, ctx.compact_live_counts, ctx.compact_slot_mapping
-        if base.ndim == 3:
-            base, live = base[self.layer_id], live[self.layer_id]
-            slot = None if slot is None else slot[self.layer_id]
+        base, bt, live, slot = self._layer_metadata(ctx)
         if slot is not None and not compact_append_stored:
             store_compact_kvcache(k, v, self.compact_k_cache, self.compact_v_cache, slot,
                                   k_scale=self.compact_k_scale, v_scale=self.compact_v_scale)
+        rope = dict(q_rope_positions=positions if compact_q_rope else None,
+                    q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None)
+        if bt is not None:
+            return compact_decode_attention_paged(q, self.compact_k_cache, self.compact_v_cache, bt, live, PAGE_SIZE,
+                                                  scale=self.scale, max_live_count=ctx.compact_max_live_count,
+                                                  k_scale=self.compact_k_scale, v_scale=self.compact_v_scale, **rope)
         return compact_decode_attention(q, self.compact_k_cache, self.compact_v_cache, base, live, scale=self.scale,
-                                        max_live_count=ctx.compact_max_live_count,
-                                        q_rope_positions=positions if compact_q_rope else None,
-                                        q_rope_cos_sin_cache=cos_sin_cache if compact_q_rope else None,
-                                        k_scale=self.compact_k_scale, v_scale=self.compact_v_scale)
+                                        max_live_count=ctx.compact_max_live_count, k_scale=self.compact_k_scale,
+                                        v_scale=self.compact_v_scale, **rope)
+
+    def _layer_metadata(self, ctx):
+        """This layer's (base offsets or None, block tables or None, live
+        counts, append slots) from the step's [layers, batch, kv heads] context
+        (block tables: the paged layout, [layers, batch, kv heads, pages])."""
+        base, bt, live, slot = (ctx.compact_base_offsets, ctx.block_tables, ctx.compact_live_counts,
+                                ctx.compact_slot_mapping)
+        if live is None or (base is None and bt is None):
+            raise RuntimeError("compact KV decode requires live counts and base offsets or block tables")
+        if live.ndim == 3:
+            live = live[self.layer_id]
+            slot = None if slot is None else slot[self.layer_id]
+            base = None if base is None else base[self.layer_id]
+            bt = None if bt is None else bt[self.layer_id]
+        return base, bt, live, slot
 
     def forward_fused_decode(self, q, k, v, positions, cos_sin_cache, evict_out, alpha_scale, alpha_offset):
         """Decode step of this layer in one launch: DMS decision, RoPE, FP8
         append of k / v and compact attention (q / k / v raw from qkv_proj)."""
-        ctx = get_context()
-        base, live, slot = ctx.compact_base_offsets, ctx.compact_live_counts, ctx.compact_slot_mapping
-        if base.ndim == 3:
-            base, live, slot = base[self.layer_id], live[self.layer_id], slot[self.layer_id]
+        base, bt, live, slot = self._layer_metadata(get_context())
         return fused_dms_rope_store_compact_decode_attention(
             q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, slot, evict_out, positions, base,
             live, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
-            scale=self.scale, max_live_count=ctx.compact_max_live_count, k_scale=self.compact_k_scale,
-            v_scale=self.compact_v_scale)
+            scale=self.scale, max_live_count=get_context().compact_max_live_count, k_scale=self.compact_k_scale,
+            v_scale=self.compact_v_scale, block_tables=bt, page_size=PAGE_SIZE)

@@ -171,7 +171,8 @@ def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, l
     if out is None:
         out = torch.empty_like(q)
     pairs = batch * num_kv_heads
-    mfma = mfma_attention_path(q, kv_k, group)
+    # the matrix-core kernel reads pages of at least 16 rows
+    mfma = mfma_attention_path(q, kv_k, group) and (block_tables is None or page_size >= 16)
     splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma)
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     if q.stride(2) != 1 or kv_k.stride(1) != 1 or out.stride(2) != 1:
@@ -260,7 +261,9 @@ def compact_decode_attention_paged(q: torch.Tensor, kv_k: torch.Tensor, kv_v: to
                                    block_tables: torch.Tensor, live_counts: torch.Tensor, page_size: int,
                                    scale: float | None = None, max_live_count: int | None = None,
                                    out: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
-                                   v_scale: torch.Tensor | None = None) -> torch.Tensor:
+                                   v_scale: torch.Tensor | None = None,
+                                   q_rope_positions: torch.Tensor | None = None,
+                                   q_rope_cos_sin_cache: torch.Tensor | None = None) -> torch.Tensor:
     """Same attention over paged compact storage: rank r of (b, h) lives at
     block_tables[b, h, r // page_size] * page_size + r % page_size.
     (No reference counterpart: the reference stores flat spans.)"""
@@ -278,9 +281,15 @@ def compact_decode_attention_paged(q: torch.Tensor, kv_k: torch.Tensor, kv_v: to
     block_tables = block_tables.to(dtype=torch.int32)
     if block_tables.stride(2) != 1:
         block_tables = block_tables.contiguous()
+    if (q_rope_positions is None) != (q_rope_cos_sin_cache is None):
+        raise ValueError("inline q RoPE requires both positions and cos_sin_cache")
+    if q_rope_positions is not None:
+        q_rope_positions = q_rope_positions.to(dtype=torch.int64).contiguous()
+        q_rope_cos_sin_cache = q_rope_cos_sin_cache.to(dtype=torch.float32)
     return _attention_launch(q, kv_k, kv_v, base_offsets=None, block_tables=block_tables, page_size=page_size,
                              live_counts=live_counts.to(dtype=torch.int32), scale=scale, max_live=max_live_count,
-                             out=out, k_scale=k_scale, v_scale=v_scale)
+                             out=out, k_scale=k_scale, v_scale=v_scale, rope_positions=q_rope_positions,
+                             rope_cache=q_rope_cos_sin_cache)
 
 
 def store_compact_kvcache(key: torch.Tensor, value: torch.Tensor, compact_k: torch.Tensor, compact_v: torch.Tensor,
@@ -382,24 +391,29 @@ def fused_dms_rope_store_compact_decode_attention(
         base_offsets: torch.Tensor, live_counts: torch.Tensor, *, num_kv_heads: int, alpha_scale: float,
         alpha_offset: float, scale: float | None = None, max_live_count: int | None = None,
         out: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
-        v_scale: torch.Tensor | None = None) -> torch.Tensor:
+        v_scale: torch.Tensor | None = None, block_tables: torch.Tensor | None = None,
+        page_size: int = 16) -> torch.Tensor:
     """One launch for fused_dms_rope_store_compact_decode(store_q=False,
     store_transient_k=False) followed by compact_decode_attention with the q
     RoPE done in the kernel (the reference's inline-q-RoPE decode order,
     llama.py:112-134).  q, k, v are the raw rows of the step and are not
     modified; ``live_counts`` already counts the appended token (rank
     live - 1, stored at ``slot_mapping``).  k_scale / v_scale: optional
-    per-kv-head FP8 scales [Hkv] for the append and the dequant.  Returns the
-    attention output."""
+    per-kv-head FP8 scales [Hkv] for the append and the dequant.  With
+    ``block_tables`` [B, Hkv, pages] the storage is paged (rank r at row
+    block_tables[b, h, r // page_size] * page_size + r % page_size) and
+    ``base_offsets`` is ignored (may be None).  Returns the attention output."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
         raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
     batch, num_q_heads, head_dim = q.shape
     if k.shape != (batch, num_kv_heads, head_dim) or num_q_heads % num_kv_heads:
         raise ValueError(f"q/k shape mismatch: q={tuple(q.shape)}, k={tuple(k.shape)}, num_kv_heads={num_kv_heads}")
     group = num_q_heads // num_kv_heads
-    for name, t in (("slot_mapping", slot_mapping), ("evict_out", evict_out), ("base_offsets", base_offsets),
+    paged = block_tables is not None
+    for name, t in (("slot_mapping", slot_mapping), ("evict_out", evict_out),
+                    ("block_tables" if paged else "base_offsets", block_tables if paged else base_offsets),
                     ("live_counts", live_counts)):
-        if tuple(t.shape) != (batch, num_kv_heads):
+        if tuple(t.shape[:2] if paged and name == "block_tables" else t.shape) != (batch, num_kv_heads):
             raise ValueError(f"expected {name} {(batch, num_kv_heads)}, got {tuple(t.shape)}")
     if evict_out.dtype != torch.bool:
         raise ValueError("evict_out must be bool")
@@ -425,10 +439,26 @@ def fused_dms_rope_store_compact_decode_attention(
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     slot_mapping = slot_mapping.to(dtype=torch.int32)
     live_counts = live_counts.to(dtype=torch.int32)
-    base_offsets = base_offsets.to(dtype=torch.int32)
     positions = positions.to(dtype=torch.int64)
     s_, off, thr, positive = dms_threshold_args(alpha_scale, alpha_offset)
     ev = evict_out.view(torch.uint8)
+    if paged:
+        if block_tables.ndim != 3 or block_tables.dtype != torch.int32 or block_tables.stride(2) != 1:
+            raise ValueError("block_tables must be int32 [batch, kv_heads, pages] with contiguous pages")
+        if page_size < 16 or page_size & (page_size - 1):
+            raise ValueError("fused paged decode attention needs a power-of-two page_size >= 16")
+        nat.call("fdms_fused_decode_attention_paged", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                 k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos_sin_cache.data_ptr(),
+                 cos_sin_cache.stride(0), cos_sin_cache.stride(2), positions.data_ptr(), slot_mapping.data_ptr(),
+                 slot_mapping.stride(0), slot_mapping.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), s_, off,
+                 thr, positive, compact_k.data_ptr(), compact_v.data_ptr(), compact_k.stride(0),
+                 block_tables.data_ptr(), block_tables.stride(0), block_tables.stride(1), int(page_size),
+                 live_counts.data_ptr(), live_counts.stride(0), live_counts.stride(1), out.data_ptr(), out.stride(0),
+                 out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads, group, head_dim, splits,
+                 split_rows, float(scale), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+                 nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
+        return out
+    base_offsets = base_offsets.to(dtype=torch.int32)
     nat.call("fdms_fused_decode_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
              k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0),
              cos_sin_cache.stride(2), positions.data_ptr(), slot_mapping.data_ptr(), slot_mapping.stride(0),

@@ -374,6 +374,86 @@ int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int6
                               int asymmetric, void* out_packed, int64_t out_stride, void* group_scale,
                               void* group_zero, int64_t g_stride, void* stream);
 
+/* Paged compact KV (16-row pages from a device free stack per layer; no
+ * reference counterpart: the reference packs into flat spans from a host
+ * first-fit allocator, compact_kv.py:830-857, 955-1099).  Prefill side, one
+ * layer: fdms_streaming_pack_prepare plus the page pop of every (seq, head):
+ * ceil(live / 16) ids from page_stack[page_top - n .. page_top) (one atomic pop
+ * per span) into block_table[row, h, 0 .. n) (other entries -1), n into
+ * pages_held[row, h].  page_budget (optional, one int of device memory):
+ * the launch's pops debit it first and fail when it is short, which keeps
+ * pages on the stack for other sequences.  A span whose pages do not fit gets
+ * none and live_out 0, and *overflow is set to 1 (the caller frees the
+ * batch's spans and retries it later). */
+int fdms_paged_pack_prepare(const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens,
+                            int num_seqs, int window, int num_kv_heads, int max_chunks, int32_t* live_out,
+                            int64_t lo_b, int64_t lo_h, int32_t* block_offsets, int64_t of_b, int64_t of_h,
+                            int64_t of_c, int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows,
+                            int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap,
+                            int32_t* page_stack, int32_t* page_top, int32_t* page_budget, int32_t* block_table,
+                            int64_t bt_b, int64_t bt_h, int32_t* pages_held, int64_t hd_b, int64_t hd_h,
+                            int max_pages, int32_t* overflow, void* stream);
+
+/* Paged prefill scatter: fdms_streaming_pack_rank_scatter with rank r of (seq,
+ * head) stored at row block_table[row, h, r >> 4] * 16 + (r & 15). */
+int fdms_paged_pack_scatter(const void* k, const void* v, int kv_dtype, int64_t ks_t, int64_t ks_h, int64_t vs_t,
+                            int64_t vs_h, const uint8_t* evict, int64_t es_t, int64_t es_h,
+                            const int32_t* cu_seqlens, int num_seqs, const int32_t* block_offsets, int64_t bo_b,
+                            int64_t bo_h, int64_t bo_c, void* compact_k, void* compact_v, int compact_dtype,
+                            int64_t cs_s, int32_t* positions, uint8_t* evict_meta, const int32_t* meta_rows,
+                            int64_t tp_b, int64_t tp_h, int64_t tp_s, int64_t em_b, int64_t em_h, int64_t em_s,
+                            const int32_t* block_table, int64_t bt_b, int64_t bt_h, int window, int num_kv_heads,
+                            int head_dim, int max_chunks, int vec, const float* k_scale, const float* v_scale,
+                            void* stream);
+
+/* Paged decode append slots, all layers: when a span's pages are full (live ==
+ * 16 * held) one page is popped from its layer's stack (page_stack[l *
+ * stack_stride ...], page_top[l]) into the next table entry; then slot =
+ * physical row of rank live and live += 1 (prepare_decode_metadata,
+ * compact_kv.py:1727-1770, on pages).  A short pool gives slot -1 and sets
+ * *overflow. */
+int fdms_paged_prepare_decode(int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out, int64_t s_l,
+                              int64_t s_b, int64_t s_h, int32_t* block_table, int64_t bt_l, int64_t bt_b,
+                              int64_t bt_h, int32_t* pages_held, int64_t hd_l, int64_t hd_b, int64_t hd_h,
+                              const int32_t* page_stack, int64_t stack_stride, int32_t* page_top, int max_pages,
+                              int32_t* overflow, int num_layers, int num_seqs, int num_kv_heads, void* stream);
+
+/* Paged sequence free: every page of the spans of rows[0 .. num_rows) (all
+ * layers and kv heads) back to its layer's stack; tables -1, held and live 0
+ * (the reference frees host ranges, compact_kv.py:1772-1795). */
+int fdms_paged_free(const int32_t* rows, int num_rows, int32_t* block_table, int64_t bt_l, int64_t bt_b,
+                    int64_t bt_h, int32_t* pages_held, int64_t hd_l, int64_t hd_b, int64_t hd_h, int32_t* live,
+                    int64_t l_l, int64_t l_b, int64_t l_h, int32_t* page_stack, int64_t stack_stride,
+                    int32_t* page_top, int num_layers, int num_kv_heads, void* stream);
+
+/* Paged decode expiry (A12 / A13 on pages): fdms_dms_expiry's re-compaction
+ * with span slot r at row block_table[l, s, h, r >> 4] * 16 + (r & 15); each
+ * span then keeps ceil(live / 16) pages and returns the rest to its layer's
+ * stack. */
+int fdms_paged_expiry(int incremental, int32_t* positions, int64_t ps_l, int64_t ps_s, int64_t ps_h, uint8_t* evict,
+                      int64_t es_l, int64_t es_s, int64_t es_h, int32_t* live_counts, int64_t lc_l, int64_t lc_s,
+                      int64_t lc_h, int32_t* block_table, int64_t bt_l, int64_t bt_s, int64_t bt_h,
+                      int32_t* pages_held, int64_t hd_l, int64_t hd_s, int64_t hd_h, int32_t* page_stack,
+                      int64_t stack_stride, int32_t* page_top, const uint64_t* layer_k, const uint64_t* layer_v,
+                      int64_t row_bytes, int64_t c_s_bytes, const int64_t* current_positions, int num_layers,
+                      int num_seqs, int num_kv_heads, int window, void* stream);
+
+/* Paged fused decode attention: fdms_fused_decode_attention with rank r of (b,
+ * h) at row block_tables[b, h, r / page_size] * page_size + r % page_size
+ * (no base offsets); slot_mapping holds the appended token's row. */
+int fdms_fused_decode_attention_paged(const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b,
+                                      int64_t ks_h, const void* v, int64_t vs_b, int64_t vs_h, const float* cos_sin,
+                                      int64_t cs_p, int64_t cs_d, const int64_t* positions,
+                                      const int32_t* slot_mapping, int64_t sm_b, int64_t sm_h, uint8_t* evict_out,
+                                      int64_t ev_b, int64_t ev_h, float alpha_scale, float alpha_offset,
+                                      float threshold, int positive_scale, void* compact_k, void* compact_v,
+                                      int64_t c_s, const int32_t* block_tables, int64_t bt_b, int64_t bt_h,
+                                      int page_size, const int32_t* live_counts, int64_t lc_b, int64_t lc_h,
+                                      void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters,
+                                      int batch, int num_kv_heads, int group_size, int head_dim, int num_splits,
+                                      int split_rows, float scale, const float* k_scale, const float* v_scale,
+                                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,6 +209,36 @@ def expiry_incremental(*, positions, evict, live, base, compact_k, compact_v, cu
 # stateful manager (A7, A8, A11, A14, A15) — first-fit per-layer ranges
 # ---------------------------------------------------------------------------
 
+def spans_from_pages(arenas_k, arenas_v, block_tables, live_counts, slots, caps, page_size=16):
+    """Flat spans of paged compact KV (no reference counterpart: the reference
+    stores flat spans only).  arenas_*: per-layer [rows, row_bytes] storage;
+    block_tables [L, S, H, pages]; live_counts [L, S, H]; slots / caps: the
+    metadata row and span capacity of each sequence.  Span (l, slots[i], h) is
+    copied in rank order (rank r from row table[r // P] * P + r % P) to rows
+    base .. base + live of a new arena, spans laid out one after another with
+    caps[i] rows each.  Returns (new_k, new_v, bases) with bases[i] [L, H]."""
+    L, _, H, _ = block_tables.shape
+    width = arenas_k[0].shape[1]
+    total = int(sum(caps)) * H
+    new_k = [np.zeros((total, width), arenas_k[0].dtype) for _ in range(L)]
+    new_v = [np.zeros((total, width), arenas_v[0].dtype) for _ in range(L)]
+    bases = []
+    at = 0
+    for slot, cap in zip(slots, caps):
+        base = np.zeros((L, H), np.int32)
+        for h in range(H):
+            base[:, h] = at
+            for l in range(L):
+                n = int(live_counts[l, slot, h])
+                r = np.arange(n)
+                rows = block_tables[l, slot, h][r // page_size].astype(np.int64) * page_size + r % page_size
+                new_k[l][at:at + n] = arenas_k[l][rows]
+                new_v[l][at:at + n] = arenas_v[l][rows]
+            at += int(cap)
+        bases.append(base)
+    return new_k, new_v, bases
+
+
 @dataclass
 class SeqState:
     seq_id: int

@@ -230,7 +230,7 @@ class Emulator:
     def streaming_pack_rank_scatter(self, k, v, kvdt, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, single_start,
                                     single_len, num_seqs, bo, bo_b, bo_h, bo_c, base, bs_b, bs_h, ck, cv, cdt, cs_s,
                                     positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s, window, H,
-                                    D, max_chunks, vec, k_scale, v_scale, stream):
+                                    D, max_chunks, vec, k_scale, v_scale, stream, _table=None):
         if num_seqs <= 0 or H <= 0 or D <= 0 or max_chunks <= 0 or vec <= 0 or D % vec:
             return 1
         kinv, vinv = self._inv_scales(k_scale, H, "k_scale"), self._inv_scales(v_scale, H, "v_scale")
@@ -239,7 +239,7 @@ class Emulator:
         if meta_rows:
             rows = self.view(meta_rows, torch.int32, (num_seqs,), (1,), "meta_rows").tolist()
         offs = self.view(bo, torch.int32, (num_seqs, H, max_chunks), (bo_b, bo_h, bo_c), "block_offsets")
-        bases = self.view(base, torch.int32, (num_seqs, H), (bs_b, bs_h), "base")
+        bases = None if _table else self.view(base, torch.int32, (num_seqs, H), (bs_b, bs_h), "base")
         ckf, ck0 = self.flat_at(ck, _TORCH[cdt], "compact_k")
         cvf, cv0 = self.flat_at(cv, _TORCH[cdt], "compact_v")
         pflat, poff = self.flat_at(positions, torch.int32, "positions")
@@ -266,7 +266,15 @@ class Emulator:
                 eidx = self.gather_idx(eflat, eoff + rows[b] * em_b + h * em_h + rank * em_s, "evict_meta")
                 pflat[pidx] = src.to(torch.int32)
                 eflat[eidx] = e[src]
-                dst_rows = int(bases[b, h]) + rank
+                if _table:  # paged: rank r at row table[row, h, r >> 4] * 16 + (r & 15); no page -> not stored
+                    bt, bt_b, bt_h = _table
+                    btf, bt0 = self.flat_at(bt, torch.int32, "block_table")
+                    pg = btf[self.gather_idx(btf, bt0 + rows[b] * bt_b + h * bt_h + rank // 16, "block_table")]
+                    ok = pg >= 0
+                    src, rank, pg = src[ok], rank[ok], pg[ok]
+                    dst_rows = pg.to(torch.int64) * 16 + rank % 16
+                else:
+                    dst_rows = int(bases[b, h]) + rank
                 didx = dst_rows[:, None] * cs_s + torch.arange(D)[None, :]
                 self.gather_idx(ckf, ck0 + didx, "compact_k")
                 self.gather_idx(cvf, cv0 + didx, "compact_v")
@@ -445,12 +453,12 @@ class Emulator:
 
     def dms_expiry(self, incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live, lc_l, lc_s, lc_h,
                    base, bo_l, bo_s, bo_h, ck, cv, layer_k, layer_v, row_bytes, c_s_bytes, cur, L, S, H, window,
-                   stream):
+                   stream, _paged=None):
         from oracle import compact_kv as ock
         if S == 0:
             return 0
         lv = self.view(live, torch.int32, (L, S, H), (lc_l, lc_s, lc_h), "live_counts")
-        bv = self.view(base, torch.int32, (L, S, H), (bo_l, bo_s, bo_h), "base_offsets")
+        bv = None if _paged else self.view(base, torch.int32, (L, S, H), (bo_l, bo_s, bo_h), "base_offsets")
         cp = self.view(cur, torch.int64, (S,), (1,), "current_positions")
         pflat, poff = self.flat_at(positions, torch.int32, "positions")
         eflat, eoff = self.flat_at(evict, torch.uint8, "evict")
@@ -469,8 +477,11 @@ class Emulator:
                         continue
                     pi = self.gather_idx(pflat, poff + l * ps_l + s_ * ps_s + h * ps_h + torch.arange(n), "positions")
                     ei = self.gather_idx(eflat, eoff + l * es_l + s_ * es_s + h * es_h + torch.arange(n), "evict")
-                    b0 = int(bv[l, s_, h])
-                    rows_b = (b0 + torch.arange(n))[:, None] * c_s_bytes + torch.arange(row_bytes)[None, :]
+                    if _paged:
+                        span_rows = self._page_rows(_paged, l, s_, h, n)
+                    else:
+                        span_rows = int(bv[l, s_, h]) + torch.arange(n)
+                    rows_b = span_rows[:, None] * c_s_bytes + torch.arange(row_bytes)[None, :]
                     self.gather_idx(kf, k0 + rows_b, "compact_k rows")
                     self.gather_idx(vf, v0 + rows_b, "compact_v rows")
                     pos_row = pflat[pi].numpy().copy()
@@ -485,7 +496,182 @@ class Emulator:
                     kf[k0 + rows_b] = torch.from_numpy(krows)
                     vf[v0 + rows_b] = torch.from_numpy(vrows)
                     lv[l, s_, h] = new_live
+                    if _paged:
+                        self._release_pages(_paged, l, s_, h, new_live)
         return 0
+
+    # -- paged layout --------------------------------------------------------------
+    def _page_rows(self, pg, l, s_, h, n):
+        """Physical rows of ranks 0 .. n-1 of span (l, s, h) through its table."""
+        btf, bt0 = self.flat_at(pg["bt"], torch.int32, "block_table")
+        r = torch.arange(n)
+        idx = self.gather_idx(btf, bt0 + l * pg["bt_l"] + s_ * pg["bt_s"] + h * pg["bt_h"] + r // 16,
+                              "block_table")
+        pages = btf[idx].to(torch.int64)
+        if n and int(pages.min()) < 0:
+            raise OutOfBounds(f"{self.name}: span (l={l}, s={s_}, h={h}) reads a rank without a page")
+        return pages * 16 + r % 16
+
+    def _push_pages(self, stack, stack_stride, top, l, pages):
+        tf, t0 = self.flat_at(top, torch.int32, "page_top")
+        ti = self.gather_idx(tf, [t0 + l], "page_top")
+        at = int(tf[ti][0])
+        sf, s0 = self.flat_at(stack, torch.int32, "page_stack")
+        si = self.gather_idx(sf, s0 + l * stack_stride + at + torch.arange(len(pages)), "page_stack")
+        sf[si] = torch.as_tensor(pages, dtype=torch.int32)
+        tf[ti] = at + len(pages)
+
+    def _pop_pages(self, stack, stack_stride, top, l, n):
+        """n page ids off layer l's stack, or None (pool short, nothing taken)."""
+        tf, t0 = self.flat_at(top, torch.int32, "page_top")
+        ti = self.gather_idx(tf, [t0 + l], "page_top")
+        at = int(tf[ti][0])
+        if n > at:
+            return None
+        sf, s0 = self.flat_at(stack, torch.int32, "page_stack")
+        si = self.gather_idx(sf, s0 + l * stack_stride + at - n + torch.arange(n), "page_stack")
+        tf[ti] = at - n
+        return sf[si].clone()
+
+    def _release_pages(self, pg, l, s_, h, live_after):
+        keep = (live_after + 15) // 16
+        hf, h0 = self.flat_at(pg["held"], torch.int32, "pages_held")
+        hi = self.gather_idx(hf, [h0 + l * pg["hd_l"] + s_ * pg["hd_s"] + h * pg["hd_h"]], "pages_held")
+        n = int(hf[hi][0])
+        if n <= keep:
+            return
+        btf, bt0 = self.flat_at(pg["bt"], torch.int32, "block_table")
+        idx = self.gather_idx(btf, bt0 + l * pg["bt_l"] + s_ * pg["bt_s"] + h * pg["bt_h"] + torch.arange(keep, n),
+                              "block_table")
+        self._push_pages(pg["stack"], pg["stack_stride"], pg["top"], l, btf[idx].clone())
+        btf[idx] = -1
+        hf[hi] = keep
+
+    def paged_pack_prepare(self, evict, es_t, es_h, cu, num_seqs, window, H, max_chunks, live_out, lo_b, lo_h,
+                           offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
+                           meta_cap, page_stack, page_top, page_budget, bt, bt_b, bt_h, held, hd_b, hd_h, max_pages,
+                           overflow, stream):
+        if num_seqs <= 0 or H <= 0 or max_chunks <= 0 or max_pages <= 0:
+            return 1
+        rc = self.streaming_pack_prepare(evict, es_t, es_h, cu, 0, num_seqs, window, H, max_chunks, live_out, lo_b,
+                                         lo_h, offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b,
+                                         tp_h, em_b, em_h, meta_cap, stream)
+        if rc:
+            return rc
+        live = self.view(live_out, torch.int32, (num_seqs, H), (lo_b, lo_h), "live_out")
+        rows = list(range(num_seqs))
+        if meta_rows:
+            rows = self.view(meta_rows, torch.int32, (num_seqs,), (1,), "meta_rows").tolist()
+        ov = self.view(overflow, torch.int32, (1,), (1,), "overflow")
+        for b in range(num_seqs):
+            for h in range(H):
+                n = (int(live[b, h]) + 15) // 16
+                got = None
+                if 0 < n <= max_pages:
+                    budget = self.view(page_budget, torch.int32, (1,), (1,), "page_budget") if page_budget else None
+                    if budget is None or int(budget[0]) >= n:
+                        got = self._pop_pages(page_stack, 0, page_top, 0, n)
+                        if got is not None and budget is not None:
+                            budget[0] -= n
+                if got is None and n > 0:
+                    ov[0] = 1
+                    live[b, h] = 0
+                table = self.view_at(bt, torch.int32, rows[b] * bt_b + h * bt_h, (max_pages,), (1,), "block_table")
+                table.fill_(-1)
+                if got is not None:
+                    table[:n] = got
+                self.view_at(held, torch.int32, rows[b] * hd_b + h * hd_h, (1,), (1,), "pages_held")[0] = \
+                    n if got is not None else 0
+        return 0
+
+    def paged_pack_scatter(self, k, v, kvdt, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, num_seqs, bo, bo_b,
+                           bo_h, bo_c, ck, cv, cdt, cs_s, positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b,
+                           em_h, em_s, bt, bt_b, bt_h, window, H, D, max_chunks, vec, k_scale, v_scale, stream):
+        if not bo or not cu or not bt:
+            return 1
+        return self.streaming_pack_rank_scatter(k, v, kvdt, ks_t, ks_h, vs_t, vs_h, evict, es_t, es_h, cu, 0, 0,
+                                                num_seqs, bo, bo_b, bo_h, bo_c, None, 0, 0, ck, cv, cdt, cs_s,
+                                                positions, evict_meta, meta_rows, tp_b, tp_h, tp_s, em_b, em_h, em_s,
+                                                window, H, D, max_chunks, vec, k_scale, v_scale, stream,
+                                                _table=(bt, bt_b, bt_h))
+
+    def paged_prepare_decode(self, live, l_l, l_b, l_h, slot, s_l, s_b, s_h, bt, bt_l, bt_b, bt_h, held, hd_l, hd_b,
+                             hd_h, stack, stack_stride, top, max_pages, overflow, L, B, H, stream):
+        if L <= 0 or B < 0 or H <= 0 or max_pages <= 0:
+            return 1
+        if B == 0:
+            return 0
+        lv = self.view(live, torch.int32, (L, B, H), (l_l, l_b, l_h), "live")
+        sv = self.view(slot, torch.int32, (L, B, H), (s_l, s_b, s_h), "slot_out")
+        hv = self.view(held, torch.int32, (L, B, H), (hd_l, hd_b, hd_h), "pages_held")
+        ov = self.view(overflow, torch.int32, (1,), (1,), "overflow")
+        for l in range(L):
+            for b in range(B):
+                for h in range(H):
+                    n, np_ = int(lv[l, b, h]), int(hv[l, b, h])
+                    table = self.view_at(bt, torch.int32, l * bt_l + b * bt_b + h * bt_h, (max_pages,), (1,),
+                                         "block_table")
+                    if n >= 16 * np_:
+                        got = self._pop_pages(stack, stack_stride, top, l, 1) if np_ < max_pages else None
+                        if got is None:
+                            ov[0] = 1
+                            sv[l, b, h] = -1
+                            continue
+                        table[np_] = got[0]
+                        np_ += 1
+                        hv[l, b, h] = np_
+                    sv[l, b, h] = int(table[n // 16]) * 16 + n % 16
+                    lv[l, b, h] = n + 1
+        return 0
+
+    def paged_free(self, rows, num_rows, bt, bt_l, bt_b, bt_h, held, hd_l, hd_b, hd_h, live, l_l, l_b, l_h, stack,
+                   stack_stride, top, L, H, stream):
+        if L <= 0 or num_rows < 0 or H <= 0:
+            return 1
+        if num_rows == 0:
+            return 0
+        rv = self.view(rows, torch.int32, (num_rows,), (1,), "rows").tolist()
+        for l in range(L):
+            for r in rv:
+                for h in range(H):
+                    hp = self.view_at(held, torch.int32, l * hd_l + r * hd_b + h * hd_h, (1,), (1,), "pages_held")
+                    n = int(hp[0])
+                    if n > 0:
+                        table = self.view_at(bt, torch.int32, l * bt_l + r * bt_b + h * bt_h, (n,), (1,),
+                                             "block_table")
+                        self._push_pages(stack, stack_stride, top, l, table.clone())
+                        table.fill_(-1)
+                    hp[0] = 0
+                    self.view_at(live, torch.int32, l * l_l + r * l_b + h * l_h, (1,), (1,), "live")[0] = 0
+        return 0
+
+    def paged_expiry(self, incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live, lc_l, lc_s, lc_h,
+                     bt, bt_l, bt_s, bt_h, held, hd_l, hd_s, hd_h, stack, stack_stride, top, layer_k, layer_v,
+                     row_bytes, c_s_bytes, cur, L, S, H, window, stream):
+        if not bt or not layer_k or not layer_v:
+            return 1
+        pg = dict(bt=bt, bt_l=bt_l, bt_s=bt_s, bt_h=bt_h, held=held, hd_l=hd_l, hd_s=hd_s, hd_h=hd_h, stack=stack,
+                  stack_stride=stack_stride, top=top)
+        return self.dms_expiry(incremental, positions, ps_l, ps_s, ps_h, evict, es_l, es_s, es_h, live, lc_l, lc_s,
+                               lc_h, None, 0, 0, 0, None, None, layer_k, layer_v, row_bytes, c_s_bytes, cur, L, S, H,
+                               window, stream, _paged=pg)
+
+    def fused_decode_attention_paged(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d,
+                                     positions, slot, sm_b, sm_h, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv,
+                                     c_s, bt, bt_b, bt_h, page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters,
+                                     B, H, G, D, splits, split_rows, scale, k_scale, v_scale, stream):
+        if B == 0:
+            return 0
+        if G > 4 or D not in (64, 128) or not bt:
+            return 1
+        self.dms_rope_store_compact_decode(q, DT_BF16, qs_b, qs_h, k, v, DT_BF16, ks_b, ks_h, vs_b, vs_h, cos_sin,
+                                           cs_p, cs_d, ck, cv, DT_FP8, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h,
+                                           positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, k_scale, v_scale,
+                                           stream)
+        return self.compact_decode_attention(q, DT_BF16, qs_b, qs_h, ck, cv, DT_FP8, c_s, None, 0, 0, bt, bt_b, bt_h,
+                                             page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D,
+                                             splits, split_rows, scale, cos_sin, cs_p, cs_d, positions, k_scale,
+                                             v_scale, stream)
 
     def prepare_decode_metadata(self, base, b_l, b_b, b_h, live, l_l, l_b, l_h, slot, s_l, s_b, s_h, L, B, H,
                                 stream):

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from native_emulator import cpu_engine
+from paged_invariants import check_page_invariants
 from oracle import linear as olin
 
 DMS = dict(dms_window_size=32, dms_alpha_scale=10.0, dms_alpha_offset=5.0)
@@ -28,11 +29,12 @@ def _check_logits(got: torch.Tensor, want: torch.Tensor, what: str):
     assert err <= 2e-2 * scale, f"{what}: max |logit diff| {err:.4g} (scale {scale:.3g})"
 
 
+@pytest.mark.parametrize("layout", ["paged", "span"])
 @pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 800, 64], 40),
                                             ("tiny-qwen3", [129, 700], 12),
                                             ("tiny-llama", [40], 6)])
-def test_engine_glue_matches_oracle(model, lens, gen):
-    _run(model, lens, gen, fused_head=False)
+def test_engine_glue_matches_oracle(model, lens, gen, layout):
+    _run(model, lens, gen, fused_head=False, layout=layout)
 
 
 @pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 64], 12), ("tiny-qwen3", [129, 700], 8)])
@@ -42,12 +44,12 @@ def test_engine_fused_greedy_head_matches_oracle_tokens(model, lens, gen):
     _run(model, lens, gen, fused_head=True)
 
 
-def _run(model, lens, gen, fused_head):
+def _run(model, lens, gen, fused_head, layout="paged"):
     from oracle.model import OracleModel, weights_from_model
     with cpu_engine() as emu:
         from fastdms_amd import LLM, SamplingParams
         llm = LLM(model, max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384, enforce_eager=True,
-                  fused_greedy_head=fused_head, **DMS)
+                  fused_greedy_head=fused_head, compact_kv_layout=layout, **DMS)
         runner = llm.model_runner
         orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
                           alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
@@ -82,7 +84,9 @@ def _run(model, lens, gen, fused_head):
                 want = np.array(orc.mgr.seq_states[s.seq_id].live_counts.tolist())
                 assert (got[0] == want[0]).all(), f"layer-0 live counts at step {step}: {got[0]} vs {want[0]}"
                 assert np.abs(got - want).max() <= 2, f"live counts at step {step}: {got} vs {want}"
-        assert "fdms_dms_expiry" in emu.calls
+            if layout == "paged":
+                check_page_invariants(mgr)
+        assert ("fdms_paged_expiry" if layout == "paged" else "fdms_dms_expiry") in emu.calls
         llm.exit()
 
 

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 from native_emulator import cpu_engine
+from paged_invariants import check_page_invariants
 
 DMS = dict(dms_window_size=32, dms_alpha_scale=10.0, dms_alpha_offset=5.0)
 GEN = 30
@@ -47,15 +48,20 @@ def _replay_alone(runner, llm, seq, preempted_at):
     return got, want
 
 
-@pytest.mark.parametrize("admission,reserve,cap", [("defer", None, 260), ("preempt", 4, 300)])
-def test_admission_and_preemption_follow_the_oracle(monkeypatch, admission, reserve, cap):
+@pytest.mark.parametrize("admission,reserve,cap,layout", [
+    ("defer", None, 260, "paged"), ("defer", None, 260, "span"),
+    # the paged pool admits the second prompt only once both fit (23 pages of
+    # 16 rows); their decode growth then forces a preemption
+    ("preempt", 4, 368, "paged"), ("preempt", 4, 300, "span")])
+def test_admission_and_preemption_follow_the_oracle(monkeypatch, admission, reserve, cap, layout):
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_TRITON", "1")
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_INTERVAL", "1")
     with cpu_engine():
         from fastdms_amd import LLM, SamplingParams
         llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096,
                   enforce_eager=True, fused_greedy_head=True, compact_kv_capacity_tokens=cap,
-                  compact_admission=admission, compact_decode_reserve_tokens=reserve, **DMS)
+                  compact_admission=admission, compact_decode_reserve_tokens=reserve, compact_kv_layout=layout,
+                  **DMS)
         runner = llm.model_runner
         rng = np.random.default_rng(11)
         sp = SamplingParams(temperature=0.0, max_tokens=GEN, ignore_eos=True)
@@ -73,9 +79,14 @@ def test_admission_and_preemption_follow_the_oracle(monkeypatch, admission, rese
         assert all(len(s.completion_token_ids) == GEN for s in seqs)
         if admission == "defer":
             assert sched.num_deferrals >= 1 and sched.num_preemptions == 0
+        else:  # spans grow by moving to a larger range; pages grow in place
+            assert sched.num_preemptions >= 1 and (layout == "paged" or mgr.num_span_moves >= 1)
+        assert not mgr.seq_states
+        if layout == "span":
+            assert mgr.free_tokens == cap * mgr.num_layers  # every span came back
         else:
-            assert sched.num_preemptions >= 1 and mgr.num_span_moves >= 1
-        assert not mgr.seq_states and mgr.free_tokens == cap * mgr.num_layers  # every span came back
+            check_page_invariants(mgr)  # every page came back: the whole pool is on the free stacks
+            assert mgr.page_top.tolist() == [mgr.num_pages] * mgr.num_layers
         for s in seqs:
             at = [g for sid, g in sched.preemption_log if sid == s.seq_id]
             got, want = _replay_alone(runner, llm, s, at)
@@ -100,7 +111,7 @@ def test_streaming_pack_rejects_a_live_count_above_the_span_capacity():
     with cpu_engine():
         from fastdms_amd import LLM, SamplingParams
         llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=2, max_num_batched_tokens=4096,
-                  enforce_eager=True, compact_kv_target_live_tokens_per_seq=64, **DMS)
+                  enforce_eager=True, compact_kv_target_live_tokens_per_seq=64, compact_kv_layout="span", **DMS)
         rng = np.random.default_rng(5)
         sp = SamplingParams(temperature=0.0, max_tokens=8, ignore_eos=True)
         for n in (500, 400):

@@ -7,6 +7,9 @@ import numpy as np
 import pytest
 import torch
 
+from oracle_sync import sync_oracle_state
+from paged_invariants import check_page_invariants
+
 from helpers import require_gpu
 
 pytestmark = pytest.mark.gpu
@@ -53,18 +56,7 @@ def _fp32_linear(x, w, b=None):
 def _sync_oracle_state(orc, mgr, seqs):
     """Give the oracle the GPU's compact state (arenas, spans, live counts,
     positions, decisions), so its next decode step starts from the same KV."""
-    from oracle import compact_kv as ock
-    om = orc.mgr
-    om.free_ranges_per_layer = [list(r) for r in mgr.free_ranges_per_layer]
-    om.compact_k_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_k_per_layer]
-    om.compact_v_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_v_per_layer]
-    for s in seqs:
-        st = mgr.seq_states[s.seq_id]
-        om.seq_states[s.seq_id] = ock.SeqState(
-            s.seq_id, st.base_offsets.cpu().numpy().copy(), st.range_capacity.cpu().numpy().copy(),
-            st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
-            st.evict_mask.cpu().numpy().copy(), st.max_capacity_per_lh, st.decode_headroom,
-            st.dms_initial_expiry_done, st.last_dms_expiry_position)
+    sync_oracle_state(orc, mgr, [s.seq_id for s in seqs])
 
 
 def _follow_oracle(model, lens, *, oracle_gemm: bool, gen: int = 40, sync_state: bool = False):
@@ -293,8 +285,13 @@ def test_quantized_weights_graph_equals_eager(monkeypatch, env):
     assert outs[0] == outs[1] == outs[2]
 
 
-@pytest.mark.parametrize("admission,reserve,cap", [("defer", None, 260), ("preempt", 4, 300)])
-def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, cap):
+@pytest.mark.parametrize("admission,reserve,cap,layout", [
+    ("defer", None, 260, "span"), ("preempt", 4, 300, "span"),
+    # 18 pages of 16 rows: the second prompt waits for the first.  (Preemption
+    # on the paged layout needs a pool sized to these prompts' DMS decisions;
+    # the CPU engine test pins it with the emulator's exact numerics.)
+    ("defer", None, 288, "paged")])
+def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, cap, layout):
     """Capped compact KV on the GPU (graphs on): deferred prefills, spans that
     grow during decode and preempted sequences re-admitted by re-prefill.  Every
     request completes, every span returns to the allocator, a rerun is token-
@@ -312,7 +309,8 @@ def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, ca
     def run(capped):
         llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096,
                   fused_greedy_head=True, compact_kv_capacity_tokens=cap if capped else 0,
-                  compact_admission=admission, compact_decode_reserve_tokens=reserve if capped else None, **DMS)
+                  compact_admission=admission, compact_decode_reserve_tokens=reserve if capped else None,
+                  compact_kv_layout=layout, **DMS)
         rng = np.random.default_rng(11)
         sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
         seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in (300, 200)]
@@ -326,6 +324,9 @@ def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, ca
             assert steps < 400, "the engine stopped making progress"
         mgr = llm.model_runner.compact_kv_manager
         assert not mgr.seq_states and mgr.free_tokens == mgr.capacity_tokens * mgr.num_layers
+        if layout == "paged":
+            check_page_invariants(mgr)
+            assert mgr.page_top.tolist() == [mgr.num_pages] * mgr.num_layers
         first = {}
         for sid, g in llm.scheduler.preemption_log:
             first.setdefault(sid, g)
@@ -340,7 +341,7 @@ def test_admission_and_preemption_on_the_gpu(monkeypatch, admission, reserve, ca
     if admission == "defer":
         assert deferrals >= 1 and all(g == gen for g in first)
     else:
-        assert any(g < gen for g in first) and moves >= 1
+        assert any(g < gen for g in first) and (layout == "paged" or moves >= 1)
     assert run(True)[0] == toks
     free_toks = run(False)[0]
     for t, f, g in zip(toks, free_toks, first):

@@ -35,6 +35,8 @@ import numpy as np
 import pytest
 import torch
 
+from oracle_sync import sync_oracle_state
+
 from helpers import require_gpu
 
 pytestmark = pytest.mark.gpu
@@ -108,20 +110,22 @@ QUANT_ENV = {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FAS
              "FASTDMS_INT4_ROW1_MAX_ROWS": "8"}
 
 
-def _run(model_cfg, lens, *, seed=0, quant=False):
+def _run(model_cfg, lens, *, seed=0, quant=False, layout="paged", with_oracle=True):
     from fastdms_amd import LLM, SamplingParams
     rng = np.random.default_rng(seed)
     prompts = [rng.integers(0, model_cfg.vocab_size, n).tolist() for n in lens]
     llm = LLM(model_cfg, max_model_len=max(lens) + GEN + 8, max_num_seqs=len(lens),
-              max_num_batched_tokens=sum(lens), seed=seed, **DMS)
+              max_num_batched_tokens=sum(lens), seed=seed, compact_kv_layout=layout, **DMS)
     sp = SamplingParams(temperature=0.0, max_tokens=GEN, ignore_eos=True)
     got = [o["token_ids"] for o in llm.generate(prompts, sp)]
-    orc = _oracle_for(llm.model_runner, llm.config, quant=quant)
+    orc = _oracle_for(llm.model_runner, llm.config, quant=quant) if with_oracle else None
     llm.exit()
     del llm
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     print(f"engine done: {len(lens)} prompts {lens}", flush=True)
+    if orc is None:
+        return got, None, None
 
     ids = list(range(len(lens)))
     toks = orc.prefill([(i, p, GEN) for i, p in zip(ids, prompts)])
@@ -158,18 +162,7 @@ def _check(got, want, gaps, what):
 def _sync_oracle_state(orc, mgr, seq_ids):
     """Give the oracle the GPU's compact state (arenas, spans, live counts,
     positions, decisions), so its next decode step starts from the same KV."""
-    from oracle import compact_kv as ock
-    om = orc.mgr
-    om.free_ranges_per_layer = [list(r) for r in mgr.free_ranges_per_layer]
-    om.compact_k_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_k_per_layer]
-    om.compact_v_per_layer = [t.view(torch.uint8).cpu().numpy().copy() for t in mgr.compact_v_per_layer]
-    for sid in seq_ids:
-        st = mgr.seq_states[sid]
-        om.seq_states[sid] = ock.SeqState(
-            sid, st.base_offsets.cpu().numpy().copy(), st.range_capacity.cpu().numpy().copy(),
-            st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
-            st.evict_mask.cpu().numpy().copy(), st.max_capacity_per_lh, st.decode_headroom,
-            st.dms_initial_expiry_done, st.last_dms_expiry_position)
+    sync_oracle_state(orc, mgr, seq_ids)
 
 
 def _follow(model_cfg, lens, *, seed=0, quant=False, steps=GEN - 1):
@@ -284,3 +277,17 @@ def test_first_32_greedy_tokens_match_the_oracle_at_baseline_shapes(monkeypatch,
     got, want, gaps = _run(cfg, lens, seed=1, quant=quant)
     _check(got, want, gaps, case)
     assert min(min(g) for g in gaps) >= 0.5, "the planted margin did not hold"
+
+
+@pytest.mark.parametrize("case", ["l1b_c8", "q8b4_c8"])
+def test_span_layout_gives_the_paged_layouts_tokens(case):
+    """The reference's flat-span layout and the paged layout hold the same
+    ranks, so the engine's first 32 greedy tokens agree token for token (and
+    with the oracle's)."""
+    require_gpu()
+    (name, layers), lens, quant = CASES[case]
+    cfg = replace(_model_config(name, layers), successor_margin=SUCCESSOR_MARGIN)
+    span, want, gaps = _run(cfg, lens, seed=1, quant=quant, layout="span")
+    _check(span, want, gaps, case + " span")
+    paged, _, _ = _run(cfg, lens, seed=1, quant=quant, layout="paged", with_oracle=False)
+    assert paged == span

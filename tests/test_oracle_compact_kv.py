@@ -277,3 +277,42 @@ def test_expiry_policy_branches():
     assert m.expiry_action([0, 1], [10, 10], 256) == "exact"  # B in {2, 3}
     assert m.expiry_action(ids4, [10, 10, 10, 10], 256, triton_mode="0") == "exact"
     assert m.expiry_action(ids4, [11, 10, 10, 10], 256) == "exact"  # not sequential
+
+
+def test_spans_from_pages_inverts_a_random_paging():
+    """oracle.compact_kv.spans_from_pages: spans of random lengths scattered
+    into 16-row pages under a random page permutation, then gathered back,
+    are the original spans, rank for rank (and rows past live stay zero)."""
+    rng = np.random.default_rng(3)
+    L, S, H, P, W = 2, 3, 2, 16, 8
+    live = rng.integers(0, 70, (L, S, H))
+    pages_needed = (live + P - 1) // P
+    npages = int(pages_needed.sum(axis=(1, 2)).max()) + 3
+    bt = np.full((L, S, H, 5), -1, np.int32)
+    spans = {}
+    arenas_k = [np.zeros((npages * P, W), np.uint8) for _ in range(L)]
+    arenas_v = [np.zeros((npages * P, W), np.uint8) for _ in range(L)]
+    for l in range(L):
+        ids = rng.permutation(npages)
+        at = 0
+        for s in range(S):
+            for h in range(H):
+                n, npg = int(live[l, s, h]), int(pages_needed[l, s, h])
+                bt[l, s, h, :npg] = ids[at:at + npg]
+                at += npg
+                vals = rng.integers(1, 255, (n, W)).astype(np.uint8)
+                spans[l, s, h] = vals
+                for r in range(n):
+                    row = bt[l, s, h, r // P] * P + r % P
+                    arenas_k[l][row] = vals[r]
+                    arenas_v[l][row] = 255 - vals[r]
+    slots, caps = [2, 0], [80, 75]
+    new_k, new_v, bases = ock.spans_from_pages(arenas_k, arenas_v, bt, live, slots, caps, P)
+    for i, (s, cap) in enumerate(zip(slots, caps)):
+        for l in range(L):
+            for h in range(H):
+                b, n = int(bases[i][l, h]), int(live[l, s, h])
+                assert np.array_equal(new_k[l][b:b + n], spans[l, s, h])
+                assert np.array_equal(new_v[l][b:b + n], 255 - spans[l, s, h])
+                assert not new_k[l][b + n:b + cap].any()
+    assert bases[1][0, 0] == caps[0] * H
