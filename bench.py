@@ -386,59 +386,10 @@ def _pmc_traffic(name: str, config: str):
         return None
 
 
-def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str = "l1b-c8"):
-    """Prefill compaction (A4 + A5) as the engine runs it for one layer of a
-    prefill batch (streaming_pack_layer): one pack-prepare launch over every
-    sequence (keep counts, chunk offsets, metadata rows reset to (-1, False))
-    and one rank-scatter launch (bf16 K/V -> FP8 spans + positions / evict
-    metadata), for the bench's prompt lengths, 8 KV heads, D = 64, keep = last
-    256 tokens + 1/8 of the older ones.  One HIP graph packs `layers` layers
-    with their own K/V, spans and metadata (more than the 256 MB MALL); HIP
-    events bracket `replays` replays.  Algorithmic bytes per layer: the evict
-    bytes (T*H), the kept K/V rows (live*2*D*2), their FP8 rows and metadata
-    (live*(2*D + 5)), the metadata reset (S*H*cap*5) and the counts / offsets.
-    The SURVEY formula, which also counts the evicted rows' K/V as read, is
-    reported beside it (bytes_survey)."""
-    import numpy as np
+def _graph_time(run, replays: int) -> float:
+    """Seconds per replay of a HIP graph of run()'s launches (HIP events on
+    the capture stream)."""
     import torch
-    from fastdms_amd import _native as nat
-
-    h, d, window = 8, 64, 256
-    nseq = len(lens)
-    t_tot = int(sum(lens))
-    cap = int(max(lens))
-    chunks = -(-cap // 256)
-    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device="cuda")
-    gen = torch.Generator(device="cuda").manual_seed(2)
-    keep_old = 0.125
-    per_layer = []
-    for _ in range(layers):
-        k = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
-        v = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
-        evict = (torch.rand((t_tot, h), generator=gen, device="cuda") >= keep_old).view(torch.uint8)
-        ck = torch.zeros((nseq * h * cap, d), device="cuda", dtype=torch.float8_e4m3fn)
-        cv = torch.zeros_like(ck)
-        pos = torch.zeros((nseq, h, cap), device="cuda", dtype=torch.int32)
-        em = torch.zeros((nseq, h, cap), device="cuda", dtype=torch.uint8)
-        live = torch.empty((nseq, h), device="cuda", dtype=torch.int32)
-        offs = torch.empty((nseq, h, chunks), device="cuda", dtype=torch.int32)
-        per_layer.append((k, v, evict, ck, cv, pos, em, live, offs))
-    base = (torch.arange(nseq * h, device="cuda", dtype=torch.int32) * cap).view(nseq, h)
-    rows = torch.arange(nseq, device="cuda", dtype=torch.int32)
-
-    def run():
-        for k, v, ev, ck, cv, pos, em, live, offs in per_layer:
-            nat.call("fdms_streaming_pack_prepare", ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), 0, nseq,
-                     window, h, chunks, live.data_ptr(), live.stride(0), live.stride(1), offs.data_ptr(),
-                     offs.stride(0), offs.stride(1), offs.stride(2), pos.data_ptr(), em.data_ptr(), rows.data_ptr(),
-                     pos.stride(0), pos.stride(1), em.stride(0), em.stride(1), cap, nat.stream())
-            nat.call("fdms_streaming_pack_rank_scatter", k.data_ptr(), v.data_ptr(), nat.DT_BF16, k.stride(0),
-                     k.stride(1), v.stride(0), v.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(),
-                     0, 0, nseq, offs.data_ptr(), offs.stride(0), offs.stride(1), offs.stride(2), base.data_ptr(),
-                     base.stride(0), base.stride(1), ck.data_ptr(), cv.data_ptr(), nat.DT_FP8, ck.stride(0),
-                     pos.data_ptr(), em.data_ptr(), rows.data_ptr(), pos.stride(0), pos.stride(1), pos.stride(2),
-                     em.stride(0), em.stride(1), em.stride(2), window, h, d, chunks, 8, None, None, nat.stream())
-
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
     with torch.inference_mode(), torch.cuda.stream(s):
@@ -454,19 +405,184 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
             g.replay()
         e1.record(s)
         torch.cuda.synchronize()
-    layer_s = e0.elapsed_time(e1) / 1e3 / (replays * layers)
-    live = sum(int(x[7].sum()) for x in per_layer) / layers
-    meta = nseq * h * (1 + chunks) * 4
-    nbytes = t_tot * h + live * 2 * d * 2 + live * (2 * d + 5) + nseq * h * cap * 5 + meta
+    return e0.elapsed_time(e1) / 1e3 / replays
+
+
+def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str = "l1b-c8"):
+    """Prefill compaction (A4 + A5) as the engine runs it for one layer of a
+    prefill batch on the paged layout (PagedCompactKVManager.streaming_pack_layer):
+    one count/scan launch that also pops each span's 16-row pages and writes
+    its block-table row, and one rank-scatter launch (bf16 K/V -> FP8 pages +
+    positions / evict metadata), for the bench's prompt lengths, 8 KV heads,
+    D = 64, keep = last 256 tokens + 1/8 of the older ones.  One HIP graph
+    packs `layers` layers with their own K/V, pools and metadata (more than the
+    256 MB MALL); HIP events bracket `replays` replays (each layer's pool holds
+    fresh pages for every replay).  Algorithmic bytes per layer (SURVEY
+    formula): T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written, plus the
+    counts / offsets and one table entry per page.  The kernels read only the
+    kept rows' K/V, so the bytes they must move (bytes_kept: evict bytes, kept
+    K/V rows, FP8 rows, metadata) are reported beside it."""
+    import numpy as np
+    import torch
+    from fastdms_amd import _native as nat
+
+    h, d, window = 8, 64, 256
+    nseq = len(lens)
+    t_tot = int(sum(lens))
+    cap = int(max(lens))
+    chunks = -(-cap // 256)
+    max_pages = -(-cap // 16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32).cuda()
+    gen = torch.Generator().manual_seed(2)
+    keep_old = 0.125
+    runs = replays + 3  # eager warm-up, capture (not run), first replay, timed replays
+    pool = runs * sum(-(-(window + int(n * keep_old * 1.3)) // 16) for n in lens) * h
+    per_layer = []
+    for _ in range(layers):
+        k = torch.randn((t_tot, h, d), generator=gen).to(torch.bfloat16).cuda()
+        v = torch.randn((t_tot, h, d), generator=gen).to(torch.bfloat16).cuda()
+        evict = (torch.rand((t_tot, h), generator=gen) >= keep_old).to(torch.uint8).cuda()
+        ck = torch.zeros((pool * 16, d), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+        cv = torch.zeros_like(ck)
+        stack = torch.arange(pool, dtype=torch.int32, device="cuda")
+        top = torch.full((1,), pool, dtype=torch.int32, device="cuda")
+        bt = torch.full((nseq, h, max_pages), -1, dtype=torch.int32, device="cuda")
+        held = torch.zeros((nseq, h), dtype=torch.int32, device="cuda")
+        pos = torch.full((nseq, h, cap), -1, dtype=torch.int32, device="cuda")
+        em = torch.zeros((nseq, h, cap), dtype=torch.uint8, device="cuda")
+        live = torch.empty((nseq, h), dtype=torch.int32, device="cuda")
+        offs = torch.empty((nseq, h, chunks), dtype=torch.int32, device="cuda")
+        per_layer.append((k, v, evict, ck, cv, stack, top, bt, held, pos, em, live, offs))
+    rows = torch.arange(nseq, dtype=torch.int32, device="cuda")
+    overflow = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def run():
+        for k, v, ev, ck, cv, stack, top, bt, held, pos, em, live, offs in per_layer:
+            nat.call("fdms_paged_pack_prepare", ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), nseq,
+                     window, h, chunks, live.data_ptr(), live.stride(0), live.stride(1), offs.data_ptr(),
+                     offs.stride(0), offs.stride(1), offs.stride(2), pos.data_ptr(), em.data_ptr(), rows.data_ptr(),
+                     pos.stride(0), pos.stride(1), em.stride(0), em.stride(1), 0, stack.data_ptr(), top.data_ptr(),
+                     None, bt.data_ptr(), bt.stride(0), bt.stride(1), held.data_ptr(), held.stride(0),
+                     held.stride(1), max_pages, overflow.data_ptr(), nat.stream())
+            nat.call("fdms_paged_pack_scatter", k.data_ptr(), v.data_ptr(), nat.DT_BF16, k.stride(0), k.stride(1),
+                     v.stride(0), v.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), nseq,
+                     offs.data_ptr(), offs.stride(0), offs.stride(1), offs.stride(2), ck.data_ptr(), cv.data_ptr(),
+                     nat.DT_FP8, ck.stride(0), pos.data_ptr(), em.data_ptr(), rows.data_ptr(), pos.stride(0),
+                     pos.stride(1), pos.stride(2), em.stride(0), em.stride(1), em.stride(2), bt.data_ptr(),
+                     bt.stride(0), bt.stride(1), window, h, d, chunks, 8, None, None, nat.stream())
+
+    layer_s = _graph_time(run, replays) / layers
+    if int(overflow.item()):
+        raise RuntimeError("compaction roofline: a page pool ran short")
+    live = sum(int(x[11].sum()) for x in per_layer) / layers
+    pages = sum(int(((x[11] + 15) // 16).sum()) for x in per_layer) / layers
+    meta = nseq * h * (1 + chunks) * 4 + pages * 4 * 2  # live + offsets; table entries and page ids
     survey = t_tot * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + meta
-    achieved = nbytes / layer_s / 1e9
+    kept = t_tot * h + live * 2 * d * 2 + live * (2 * d + 5) + meta
+    achieved = survey / layer_s / 1e9
     del per_layer
-    return {"bound": "hbm", "kernels": "pack_prepare_kernel + pack_scatter_kernel (one prefill layer, all sequences)",
+    return {"bound": "hbm", "layout": "paged (16-row pages)",
+            "kernels": "pack_prepare_kernel<paged> + pack_scatter_kernel<paged> (one prefill layer, all sequences)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("compaction_pmc_traffic.json", config),
-            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(nbytes), "tokens": t_tot,
-            "live_rows": round(live, 1), "bytes_survey": int(survey),
-            "achieved_survey": round(survey / layer_s / 1e9, 1)}
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": _pmc_traffic("compaction_pmc_traffic.json", config),
+            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(survey), "tokens": t_tot,
+            "live_rows": round(live, 1), "pages": round(pages, 1), "bytes_kept": int(kept),
+            "achieved_kept": round(kept / layer_s / 1e9, 1)}
+
+
+def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: int = 8, d: int = 64):
+    """Decode expiry A12 (the exact re-compaction the first decode step and
+    every window-th step run; fdms_paged_expiry, all layers in one launch) on
+    paged spans shaped like the bench's decode state: live ~ U[700, 1300] per
+    (layer, seq, head), the older ranks kept prefill survivors (evict 0), the
+    last 256 the in-window tokens (7/8 flagged), the step's position 64 past
+    the window, so the 64 oldest window tokens expire (about 56 of them are
+    flagged) and the rows after them move.  Each replay expires its own copy
+    of the state (`replays` copies in one graph).  Algorithmic bytes (SURVEY
+    formula): live_before * 5 metadata read + moved rows * 2 * D * 2 (K and V,
+    read + write) + live_after * 5 written, summed over the spans."""
+    import numpy as np
+    import torch
+    from fastdms_amd import _native as nat
+
+    window, cap = 256, 1400
+    rng = np.random.default_rng(4)
+    live = rng.integers(700, 1301, (layers, seqs, heads)).astype(np.int32)
+    cur = 8400
+    pos = np.full((layers, seqs, heads, cap), -1, np.int32)
+    ev = np.zeros((layers, seqs, heads, cap), np.uint8)
+    moved = kept = 0
+    for idx in np.ndindex(layers, seqs, heads):
+        n = int(live[idx])
+        old = np.sort(rng.choice(cur - window - 64, n - window, replace=False))
+        pos[idx][:n] = np.concatenate([old, np.arange(cur - window - 64, cur - 64)])
+        ev[idx][n - window:n] = rng.random(window) < 7 / 8
+        keep = ~((ev[idx][:n] == 1) & (pos[idx][:n] < cur - window))
+        first = int(np.argmin(keep)) if not keep.all() else n
+        moved += int(keep[first:].sum())
+        kept += int(keep.sum())
+    npg = (live.astype(np.int64) + 15) // 16
+    max_pages = int(npg.max())
+    pages_per_layer = int(npg.sum(axis=(1, 2)).max())
+    copies = []
+    for _ in range(replays + 2):
+        bt = np.full((layers, seqs, heads, max_pages), -1, np.int32)
+        for l in range(layers):
+            ids = rng.permutation(pages_per_layer).astype(np.int32)
+            at = 0
+            for b in range(seqs):
+                for h in range(heads):
+                    n = int(npg[l, b, h])
+                    bt[l, b, h, :n] = ids[at:at + n]
+                    at += n
+        arenas = [(torch.randint(0, 120, (pages_per_layer * 16, d), dtype=torch.uint8, device="cuda"),
+                   torch.randint(0, 120, (pages_per_layer * 16, d), dtype=torch.uint8, device="cuda"))
+                  for _ in range(layers)]
+        copies.append(dict(
+            pos=torch.from_numpy(pos).cuda(), ev=torch.from_numpy(ev).cuda(), live=torch.from_numpy(live).cuda(),
+            bt=torch.from_numpy(bt).cuda(), held=torch.from_numpy(npg.astype(np.int32)).cuda(),
+            stack=torch.zeros((layers, pages_per_layer), dtype=torch.int32, device="cuda"),
+            top=torch.zeros(layers, dtype=torch.int32, device="cuda"), arenas=arenas,
+            pk=torch.tensor([a[0].data_ptr() for a in arenas], dtype=torch.int64, device="cuda"),
+            pv=torch.tensor([a[1].data_ptr() for a in arenas], dtype=torch.int64, device="cuda")))
+    curs = torch.full((seqs,), cur, dtype=torch.int64, device="cuda")
+    it = iter(copies)
+
+    def run():
+        c = next(it)
+        p, e, lv, bt, hd = c["pos"], c["ev"], c["live"], c["bt"], c["held"]
+        nat.call("fdms_paged_expiry", 0, p.data_ptr(), p.stride(0), p.stride(1), p.stride(2), e.data_ptr(),
+                 e.stride(0), e.stride(1), e.stride(2), lv.data_ptr(), lv.stride(0), lv.stride(1), lv.stride(2),
+                 bt.data_ptr(), bt.stride(0), bt.stride(1), bt.stride(2), hd.data_ptr(), hd.stride(0),
+                 hd.stride(1), hd.stride(2), c["stack"].data_ptr(), c["stack"].stride(0), c["top"].data_ptr(),
+                 c["pk"].data_ptr(), c["pv"].data_ptr(), d, d, curs.data_ptr(), layers, seqs, heads, window,
+                 nat.stream())
+
+    run()  # warm-up on the first copy; each copy is expired once
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(replays + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        torch.cuda.synchronize()
+        t.append(e0.elapsed_time(e1) / 1e3)
+    launch_s = float(np.median(t[1:]))
+    lv_after = copies[-1]["live"].to(torch.int64).sum().item()
+    if lv_after != kept:
+        raise RuntimeError(f"expiry roofline: {lv_after} rows kept, expected {kept}")
+    nbytes = int(live.sum()) * 5 + moved * 2 * d * 2 + kept * 5
+    achieved = nbytes / launch_s / 1e9
+    del copies
+    return {"bound": "hbm", "layout": "paged (16-row pages)",
+            "kernel": "dms_expiry_kernel<exact> (fdms_paged_expiry, all layers one launch)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "avg_launch_us": round(launch_s * 1e6, 2),
+            "bytes": nbytes, "spans": layers * seqs * heads, "live_before": int(live.sum()),
+            "live_after": int(kept), "moved_rows": moved,
+            "timing": "HIP events around single launches (median of the timed ones)"}
 
 
 def hbm_copy_gbps(nbytes: int = 1 << 30) -> float:
@@ -627,6 +743,8 @@ def main():
     scaling = attention_scaling(llm, seqs) if not args.no_scaling else None
     progress("compaction roofline")
     pack = compaction_roofline(lens, config=args.config)
+    progress("expiry roofline")
+    expiry = expiry_roofline()
     copy_bw = hbm_copy_gbps()
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",
@@ -641,6 +759,7 @@ def main():
         "roofline": roof,
         "roofline_scaling": scaling,
         "compaction_roofline": pack,
+        "expiry_roofline": expiry,
         "hbm_copy_gbps": round(copy_bw, 1),
         "cpu_baseline": cpu,
     }

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_paged_free": "piplllplllplllplpiip",
     "fdms_paged_expiry": "iplllplllplllplllplllplpppllpiiiip",
     "fdms_fused_decode_attention_paged": "pllpllpllpllppllpllfffipplpllipllpllppiiiiiifppp",
+    "fdms_fp8_gemm": "plpplpppliiip",
 }
 
 _CT = {"p": _P, "i": _I, "l": _L, "f": _F}

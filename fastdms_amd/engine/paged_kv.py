@@ -294,7 +294,9 @@ class PagedCompactKVManager(CompactKVManager):
         pos_l = self.layer_major_token_positions[layer_id]
         ev_l = self.layer_major_evict_mask[layer_id].view(torch.uint8)
         bt_l, held_l = self.block_tables[layer_id], self.pages_held[layer_id]
-        meta_cap = max(st.max_capacity_per_lh for st in states)
+        # no metadata reset (meta_cap 0): allocate() and free() leave a slot's
+        # rows at (-1, False), and a slot is packed once between them
+        meta_cap = 0
         nat.call("fdms_paged_pack_prepare", ev.data_ptr(), ev.stride(0), ev.stride(1), cu_seqlens_q.data_ptr(), B,
                  int(window_size), H, max_chunks, live.data_ptr(), live.stride(0), live.stride(1),
                  offsets.data_ptr(), offsets.stride(0), offsets.stride(1), offsets.stride(2), pos_l.data_ptr(),

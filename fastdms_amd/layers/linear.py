@@ -319,19 +319,49 @@ def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
     return tok if greedy else y
 
 
+def fp8_gemm(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor,
+             bias: torch.Tensor | None = None, *, torch_form: bool = True,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """_fp8_linear for prefill row counts on the FP8 matrix cores
+    (linear.py:635-662): rows quantised per row (fdms_quantize_fp8_rows), then
+    fdms_fp8_gemm: y = bf16(sum_k xq * w8 * x_scale_inv * w_scale_inv), bias
+    added in bf16.  x [M, K] bf16 / fp32, weight_fp8 [N, K] e4m3fn, K a
+    multiple of 16."""
+    if x.dim() != 2 or weight_fp8.dim() != 2 or x.shape[1] != weight_fp8.shape[1]:
+        raise ValueError(f"fp8_gemm shape mismatch: x {tuple(x.shape)}, weight {tuple(weight_fp8.shape)}")
+    rows, k = x.shape
+    n = weight_fp8.shape[0]
+    if k % 16 or weight_fp8.stride(1) != 1 or weight_fp8.stride(0) % 16 or weight_fp8.data_ptr() % 16:
+        raise ValueError("fp8_gemm needs K a multiple of 16 and 16-byte aligned weight rows")
+    nat.require_cuda(x, weight_fp8, weight_scale_inv, what="fp8_gemm")
+    xq, xsi = quantize_fp8_rows(x.contiguous(), torch_form=torch_form)
+    sinv = weight_scale_inv.reshape(-1).float().contiguous()
+    if sinv.numel() != n:
+        raise ValueError(f"weight_scale_inv has {sinv.numel()} entries for {n} rows")
+    if out is None:
+        out = torch.empty((rows, n), device=x.device, dtype=torch.bfloat16)
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    nat.call("fdms_fp8_gemm", xq.data_ptr(), xq.stride(0), xsi.data_ptr(), weight_fp8.data_ptr(),
+             weight_fp8.stride(0), sinv.data_ptr(), nat.ptr(b), out.data_ptr(), out.stride(0), rows, n, k,
+             nat.stream())
+    return out
+
+
 def fp8_rows_gemm(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor,
                   bias: torch.Tensor | None, quantize_x: int) -> torch.Tensor:
     """FP8 linear for any row count, the reference's _fp8_linear semantics
     (linear.py:635-662; QX_TORCH) or its Triton kernels' (QX_DIVIDE / QX_NONE):
     y = bf16(sum_k xq*w8 / x_s * scale_inv), bias added in bf16.  Rows <= 16 of a
-    supported shape run fdms_linear_small_m; larger row counts quantise the rows
-    with fdms_quantize_fp8_rows and multiply the decoded FP8 values in fp32 (the
-    products of two e4m3 values are exact in fp32)."""
+    supported shape run fdms_linear_small_m; larger row counts run fp8_gemm (the
+    FP8 matrix cores).  Unquantised activations (QX_NONE) or K not a multiple
+    of 16 multiply the decoded FP8 values in fp32 with torch."""
     rows, k = x.shape
     n = weight_fp8.shape[0]
     if small_m_supported(rows, k, n):
         return linear_small_m(x.contiguous(), weight_fp8, bias, weight_scale_inv=weight_scale_inv,
                               quantize_x=quantize_x)
+    if quantize_x != QX_NONE and k % 16 == 0:
+        return fp8_gemm(x, weight_fp8, weight_scale_inv, bias, torch_form=quantize_x == QX_TORCH)
     sinv = weight_scale_inv.reshape(1, -1).float()
     w = weight_fp8.float()
     if quantize_x == QX_NONE:

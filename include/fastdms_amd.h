@@ -454,6 +454,15 @@ int fdms_fused_decode_attention_paged(const void* q, int64_t qs_b, int64_t qs_h,
                                       int split_rows, float scale, const float* k_scale, const float* v_scale,
                                       void* stream);
 
+/* FP8 GEMM for prefill row counts (replaces the torch._scaled_mm call of
+ * _fp8_linear, linear.py:635-662): y[m, n] = bf16((sum_k x[m, k] * w[n, k]) *
+ * x_inv[m] * w_inv[n]), then bf16(y + bias[n]) when bias is not NULL.  x [M, K]
+ * and w [N, K] e4m3fn rows with byte strides x_s / w_s (K, strides and
+ * pointers multiples of 16); x_inv [M], w_inv [N] fp32; y [M, N] bf16 with row
+ * stride y_s elements.  Runs on the FP8 matrix cores (fp32 accumulation). */
+int fdms_fp8_gemm(const void* x, int64_t x_s, const float* x_inv, const void* w, int64_t w_s, const float* w_inv,
+                  const void* bias, void* y, int64_t y_s, int M, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

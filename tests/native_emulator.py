@@ -785,6 +785,23 @@ class Emulator:
         self.view(scale_inv, torch.float32, (rows,), (1,), "scale_inv").copy_(torch.from_numpy(sinv))
         return 0
 
+    def fp8_gemm(self, x, x_s, x_inv, w, w_s, w_inv, bias, y, y_s, M, N, K, stream):
+        """y = bf16((xq . w8) * x_inv * w_inv) (+ bias in bf16), fp32 products."""
+        if M < 0 or N <= 0 or K <= 0 or K % 16 or x_s % 16 or w_s % 16:
+            return 1
+        if M == 0:
+            return 0
+        xq = torch.from_numpy(numerics.e4m3fn_decode(self.view(x, torch.uint8, (M, K), (x_s, 1), "x").numpy()))
+        wq = torch.from_numpy(numerics.e4m3fn_decode(self.view(w, torch.uint8, (N, K), (w_s, 1), "w").numpy()))
+        xi = self.view(x_inv, torch.float32, (M,), (1,), "x_inv")
+        wi = self.view(w_inv, torch.float32, (N,), (1,), "w_inv")
+        acc = (xq.float() @ wq.float().T) * xi.reshape(-1, 1) * wi.reshape(1, -1)
+        out = acc.to(torch.bfloat16)
+        if bias:
+            out = (out.float() + self.view(bias, torch.bfloat16, (N,), (1,), "bias").float()).to(torch.bfloat16)
+        self.view(y, torch.bfloat16, (M, N), (y_s, 1), "y").copy_(out)
+        return 0
+
     def linear_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, prologue, norm_w, eps, res, res_s,
                        res_out, ro_s, qx, epilogue, k_splits, ws, counters, y, y_s, stream):
         """Same expressions as oracle/model.py (rmsnorm, mlp, linear) and oracle/linear.py."""

@@ -20,12 +20,17 @@ def _bf16(shape, g, scale=1.0):
     return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
 
 
-def _close_bf16(got, want, what, ulps=1.0, atol=0.0):
+def _close_bf16(got, want, what, ulps=1.0, atol=0.0, mag=None):
     """Within `ulps` bf16 units of the larger of the two magnitudes (a value on
     a binade edge may round either way), plus fp32-accumulation noise relative
-    to the output's scale for values that cancel to near zero."""
+    to the output's scale for values that cancel to near zero.  ``mag``: the
+    magnitude of an intermediate rounded to bf16 before a final add (the
+    product before its bias), whose ulps then count too."""
     g, w = got.float().cpu(), want.float()
-    tol = torch.maximum(w.abs(), g.abs()) * (ulps * 2.0 ** -7) + atol + 1e-5 * float(w.abs().max())
+    m = torch.maximum(w.abs(), g.abs())
+    if mag is not None:
+        m = torch.maximum(m, mag.float().abs())
+    tol = m * (ulps * 2.0 ** -7) + atol + 1e-5 * float(w.abs().max())
     bad = (g - w).abs() > tol
     assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{bad.numel()} beyond {ulps} ulp; "
                                  f"max err {float((g - w).abs().max()):.4g}")
@@ -308,8 +313,31 @@ def test_fp8_rows_gemm_prefill_rows(m, n, k):
     y = fp8_rows_gemm(x.cuda(), w8, sinv.reshape(1, -1), bias.cuda(), QX_TORCH)
     w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
     acc = olin.fp8_linear(x.float().numpy(), w8_t, sref, quantize_x=True, torch_form=True)
-    want = (torch.from_numpy(numerics.bf16_round(acc.astype(np.float32))) + bias.float()).to(torch.bfloat16)
-    _close_bf16(y, want, "fp8 rows gemm", ulps=2.0, atol=1e-3)
+    pre = torch.from_numpy(numerics.bf16_round(acc.astype(np.float32)))
+    want = (pre + bias.float()).to(torch.bfloat16)
+    _close_bf16(y, want, "fp8 rows gemm", ulps=2.0, atol=1e-3, mag=pre)
+
+
+@pytest.mark.parametrize("m,n,k,bias", [(1000, 3072, 2048, False), (300, 202, 272, True), (129, 130, 160, True),
+                                         (17, 4096, 1024, False)])
+def test_fp8_gemm_matches_the_oracle(m, n, k, bias):
+    """fdms_fp8_gemm on the FP8 matrix cores (the _scaled_mm of _fp8_linear,
+    linear.py:635-662) at prefill row counts: full and partial 128 x 128 tiles,
+    a K tail (272 = 2 * 128 + 16), N not a multiple of 4 (per-element stores),
+    bias or none; within 2 bf16 ulps of the oracle (fp32 accumulation in a
+    different order)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import fp8_gemm, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    b = _bf16((n,), g, 0.1) if bias else None
+    w8, sinv = quantize_fp8_rows(w.cuda())
+    y = fp8_gemm(x.cuda(), w8, sinv.reshape(1, -1), None if b is None else b.cuda())
+    w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
+    acc = olin.fp8_linear(x.float().numpy(), w8_t, sref, quantize_x=True, torch_form=True)
+    pre = torch.from_numpy(numerics.bf16_round(acc.astype(np.float32)))
+    want = pre if b is None else pre + b.float()
+    _close_bf16(y, want.to(torch.bfloat16), "fp8 gemm", ulps=2.0, atol=1e-3, mag=pre)
 
 
 @pytest.mark.parametrize("m", [2, 8])
