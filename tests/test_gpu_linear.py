@@ -319,13 +319,15 @@ def test_fp8_rows_gemm_prefill_rows(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,bias", [(1000, 3072, 2048, False), (300, 202, 272, True), (129, 130, 160, True),
-                                         (17, 4096, 1024, False)])
+                                         (17, 4096, 1024, False), (4096, 4096, 1024, False),
+                                         (4100, 4098, 272, True)])
 def test_fp8_gemm_matches_the_oracle(m, n, k, bias):
     """fdms_fp8_gemm on the FP8 matrix cores (the _scaled_mm of _fp8_linear,
-    linear.py:635-662) at prefill row counts: full and partial 128 x 128 tiles,
-    a K tail (272 = 2 * 128 + 16), N not a multiple of 4 (per-element stores),
-    bias or none; within 2 bf16 ulps of the oracle (fp32 accumulation in a
-    different order)."""
+    linear.py:635-662) at prefill row counts: full and partial 128 x 128 tiles
+    and, from 256 tiles of 256 x 256 up, the LDS-staged kernel (full and
+    partial tiles); a K tail (272 = 2 * 128 + 16), N not a multiple of 4
+    (per-element stores), bias or none; within 2 bf16 ulps of the oracle
+    (fp32 accumulation in a different order)."""
     require_gpu()
     from fastdms_amd.layers.linear import fp8_gemm, quantize_fp8_rows
     g = torch.Generator().manual_seed(m * 7 + n + k)
