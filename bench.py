@@ -158,6 +158,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-scaling", action="store_true", help="skip the attention batch-scaling points")
+    p.add_argument("--no-fast-loop", action="store_true",
+                   help="skip the device-side greedy loop over the rest of the generation (counter runs)")
     p.add_argument("--requests", type=int, default=32, help="multitenant: number of requests")
     p.add_argument("--rate", type=float, default=4.0, help="multitenant: Poisson arrival rate (requests/s)")
     p.add_argument("--kv-cap-tokens", type=int, default=24000,
@@ -491,7 +493,8 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
             "achieved_kept": round(kept / layer_s / 1e9, 1)}
 
 
-def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: int = 8, d: int = 64):
+def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: int = 8, d: int = 64,
+                    config: str = "l1b-c8"):
     """Decode expiry A12 (the exact re-compaction the first decode step and
     every window-th step run; fdms_paged_expiry, all layers in one launch) on
     paged spans shaped like the bench's decode state: live ~ U[700, 1300] per
@@ -579,7 +582,8 @@ def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: i
     return {"bound": "hbm", "layout": "paged (16-row pages)",
             "kernel": "dms_expiry_kernel<exact> (fdms_paged_expiry, all layers one launch)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "avg_launch_us": round(launch_s * 1e6, 2),
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("expiry_pmc_traffic.json", config),
+            "avg_launch_us": round(launch_s * 1e6, 2),
             "bytes": nbytes, "spans": layers * seqs * heads, "live_before": int(live.sum()),
             "live_after": int(kept), "moved_rows": moved,
             "timing": "HIP events around single launches (median of the timed ones)"}
@@ -724,7 +728,7 @@ def main():
     progress(f"decode {value:.1f} tok/s")
     fast = None
     left = min(s.max_tokens - s.num_completion_tokens for s in seqs)
-    if left >= 8:  # the device-side greedy loop over the rest of the generation
+    if left >= 8 and not args.no_fast_loop:  # the device-side greedy loop over the rest of the generation
         progress(f"greedy fast loop, {left} steps")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -744,7 +748,7 @@ def main():
     progress("compaction roofline")
     pack = compaction_roofline(lens, config=args.config)
     progress("expiry roofline")
-    expiry = expiry_roofline()
+    expiry = expiry_roofline(config=args.config)
     copy_bw = hbm_copy_gbps()
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",

@@ -82,6 +82,12 @@ struct PagePool {
   int32_t* overflow;  // set to 1 when a pop finds the pool short (the pop is undone)
 };
 constexpr int kPageShift = 4;  // 16-row pages
+constexpr int kPackXcds = 8;
+
+// (seq, head) workgroups of the count / scan kernel, padded to whole XCD rounds
+inline dim3 prepare_grid(int num_seqs, int num_kv_heads) {
+  return dim3((unsigned)(((num_seqs + kPackXcds - 1) / kPackXcds) * kPackXcds * num_kv_heads));
+}
 
 template <bool PAGED>
 __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
@@ -89,11 +95,16 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     int single_len, int window, int num_kv_heads, int max_chunks, int32_t* __restrict__ live_out, int64_t lo_b,
     int64_t lo_h, int32_t* __restrict__ offsets, int64_t of_b, int64_t of_h, int64_t of_c,
     int32_t* __restrict__ positions, uint8_t* __restrict__ evict_meta, const int32_t* __restrict__ meta_rows,
-    int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap, const PagePool pool) {
+    int64_t tp_b, int64_t tp_h, int64_t em_b, int64_t em_h, int meta_cap, const PagePool pool, int num_seqs) {
   __shared__ int s_cnt[kPrepBatch][kChunk / kWave];
   __shared__ int s_p0;
-  const int h = blockIdx.x % num_kv_heads;
-  const int b = blockIdx.x / num_kv_heads;
+  // every kv head of a sequence on one XCD (block ids are dispatched round
+  // robin over the 8 XCDs): the heads read the same evict rows, which then
+  // come from HBM into one L2 instead of eight
+  const int xcd = blockIdx.x % kPackXcds, slot = blockIdx.x / kPackXcds;
+  const int b = xcd + kPackXcds * (slot / num_kv_heads);
+  const int h = slot - (slot / num_kv_heads) * num_kv_heads;
+  if (b >= num_seqs) return;  // uniform per workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const SeqSpan sp = seq_span(cu, b, 0, single_len);
   const int thresh = max(0, sp.len - 1 - window);
@@ -267,10 +278,10 @@ FDMS_EXPORT int fdms_streaming_pack_prepare(const uint8_t* evict, int64_t es_t, 
   if (num_seqs <= 0 || num_kv_heads <= 0 || max_chunks < 0) return (int)hipErrorInvalidValue;
   if (!evict || !live_out || (max_chunks > 0 && !block_offsets)) return (int)hipErrorInvalidValue;
   if (positions && !evict_meta) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(pack_prepare_kernel<false>, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0,
+  hipLaunchKernelGGL(pack_prepare_kernel<false>, prepare_grid(num_seqs, num_kv_heads), dim3(kChunk), 0,
                      (hipStream_t)stream, evict, es_t, es_h, cu_seqlens, single_len, window, num_kv_heads, max_chunks,
                      live_out, lo_b, lo_h, block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b,
-                     tp_h, em_b, em_h, meta_cap, PagePool{});
+                     tp_h, em_b, em_h, meta_cap, PagePool{}, num_seqs);
   FDMS_LAUNCH_CHECK();
   return 0;
 }
@@ -362,10 +373,11 @@ FDMS_EXPORT int fdms_paged_pack_prepare(const uint8_t* evict, int64_t es_t, int6
   if (!page_stack || !page_top || !block_table || !pages_held || !overflow) return (int)hipErrorInvalidValue;
   const PagePool pool{page_stack, page_top, page_budget, block_table, bt_b, bt_h, pages_held, hd_b, hd_h, max_pages,
                       overflow};
-  hipLaunchKernelGGL(pack_prepare_kernel<true>, dim3(num_seqs * num_kv_heads), dim3(kChunk), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(pack_prepare_kernel<true>, prepare_grid(num_seqs, num_kv_heads), dim3(kChunk), 0,
+                     (hipStream_t)stream,
                      evict, es_t, es_h, cu_seqlens, 0, window, num_kv_heads, max_chunks, live_out, lo_b, lo_h,
                      block_offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
-                     meta_cap, pool);
+                     meta_cap, pool, num_seqs);
   FDMS_LAUNCH_CHECK();
   return 0;
 }
