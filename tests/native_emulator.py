@@ -41,29 +41,39 @@ class _Registry:
         self.bases: list[int] = []
         self.entries: list[tuple[int, int, torch.UntypedStorage]] = []
 
-    def refresh(self):
+    def refresh(self, generation: int | None = None):
+        """Scan the garbage collector's objects for CPU tensors: all of them
+        (generation None: the cache is replaced, dropping freed storages), or
+        only one gc generation (new tensors sit in generation 0 until a
+        collection moves them on), whose storages are added to the cache."""
         seen = {}
+        objs = gc.get_objects() if generation is None else gc.get_objects(generation)
         with warnings.catch_warnings():
             warnings.simplefilter("ignore")
-            for o in gc.get_objects():
+            for o in objs:
+                if not isinstance(o, torch.Tensor):
+                    continue
                 try:
-                    if isinstance(o, torch.Tensor) and o.device.type == "cpu":
+                    if o.device.type == "cpu":
                         s = o.untyped_storage()
                         seen[s.data_ptr()] = (s.data_ptr(), s.nbytes(), s)
                 except Exception:  # noqa: BLE001 - fake/meta tensors
                     continue
+        if generation is not None:
+            for e in self.entries:
+                seen.setdefault(e[0], e)
         self.entries = sorted(seen.values(), key=lambda e: e[0])
         self.bases = [e[0] for e in self.entries]
 
     def find(self, ptr: int):
-        for attempt in range(2):
+        for attempt in (None, 0, 1, "all"):
+            if attempt is not None:
+                self.refresh(None if attempt == "all" else attempt)
             i = bisect.bisect_right(self.bases, ptr) - 1
             if i >= 0:
                 base, nbytes, s = self.entries[i]
                 if base <= ptr < base + max(nbytes, 1):
                     return base, nbytes, s
-            if attempt == 0:
-                self.refresh()
         return None
 
 
