@@ -62,7 +62,13 @@ def run_multitenant(args):
     "int4 shadow" is its INT4 weight path (used here), it has no int4 KV."""
     import numpy as np
     import torch
+    # the INT4 row-1 weights are applied by the FP8 weight conversion (as in
+    # model_runner.py:72-113): FP8 rows for prefill, INT4 for decode rows
+    os.environ.setdefault("FASTDMS_FP8_WEIGHTS", "1")
+    os.environ.setdefault("FASTDMS_FP8_WEIGHT_SCOPE", "all")
+    os.environ.setdefault("FASTDMS_FP8_LM_HEAD", "0")
     os.environ.setdefault("FASTDMS_INT4_ROW1_WEIGHTS", "1")
+    os.environ.setdefault("FASTDMS_INT4_ROW1_SCOPE", "all")
     os.environ.setdefault("FASTDMS_INT4_ROW1_GROUP_SIZE", "128")
     os.environ.setdefault("FASTDMS_INT4_ROW1_QUANT_MODE", "symmetric")
     os.environ.setdefault("FASTDMS_INT4_ROW1_MAX_ROWS", "16")
@@ -130,7 +136,9 @@ def run_multitenant(args):
         "wall_s": round(wall, 3), "generated_tokens": generated,
         "ttft_s": {"p50": round(float(np.percentile(ttft, 50)), 3), "p99": round(float(np.percentile(ttft, 99)), 3)},
         "preemptions": sched.num_preemptions, "deferred_prefills": sched.num_deferrals,
-        "span_moves": mgr.num_span_moves, "roofline": None, "cpu_baseline": None,
+        "span_moves": mgr.num_span_moves, "kv_layout": "paged" if mgr.paged else "span",
+        "int4_linears": sum(1 for m in llm.model_runner.model.modules() if getattr(m, "_int4_enabled", False)),
+        "roofline": None, "cpu_baseline": None,
     }
     print(json.dumps(out))
     llm.exit()
