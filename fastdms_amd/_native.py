@@ -47,11 +47,11 @@ SIGNATURES: dict[str, str] = {
     "fdms_mfma_probe": "pppp",
     "fdms_prefill_attention": "pllpllpllpllpiiiiifp",
     "fdms_prefill_attention_varlen": "pllpllpllpllppiiiiifp",
-    "fdms_rmsnorm": "pllippplplifp",
+    "fdms_rmsnorm": "pllippplplifpplip",
     "fdms_silu_mul": "pplip",
-    "fdms_rmsnorm_partials": "pilppplplifp",
+    "fdms_rmsnorm_partials": "pilppplplifpppplip",
     "fdms_quantize_fp8_rows": "pilliplpip",
-    "fdms_linear_small_m": "pliipilppiipfplpliiippplp",
+    "fdms_linear_small_m": "pliipilppiipfplpliiippplpilppip",
     "fdms_linear_argmax_small_m": "pliipilppiiiipppppp",
     "fdms_linear_int4_small_m": "pliiplppilpiiipppppplp",
     "fdms_quantize_int4_groups": "pilliiiplpplp",

@@ -154,6 +154,46 @@ __device__ __forceinline__ float wave_sum(float v) {
   return rows_sum(v);
 }
 
+// Row amax with NaN propagation, in the bit domain: for a float with its sign
+// cleared the unsigned order of the bits is the numeric order and every NaN
+// lies above +inf, so an unsigned max of abs_bits(x) is max |x| -- NaN when
+// any element is NaN, as torch's amax -- independent of the order of the
+// combines.
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, true));
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+// Per-row FP8 activation scale from the row amax (linear.py:386-388, 514-523,
+// 683-694): 448 / amax, 1 where amax > 0 fails (0 or NaN); torch_form rounds
+// as the reference's tensor expression (reciprocal, then times 448).
+__device__ __forceinline__ float fp8_row_scale(float amax, bool torch_form) {
+  return amax > 0.0f ? (torch_form ? (1.0f / amax) * 448.0f : 448.0f / amax) : 1.0f;
+}
+// True when every x * scale of the row is finite with |x * scale| <= 448 (1 +
+// 2^-22) (amax and scale finite): then the clamped hardware conversion below
+// equals f32_to_fp8 on the row, and no element needs the NaN re-encode.
+__device__ __forceinline__ bool fp8_row_finite(float amax, float scale) {
+  return amax <= 3.40282347e38f && scale <= 3.40282347e38f;
+}
+// f32x4_to_fp8x4 without the NaN re-encode, for values known to be finite.
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4_finite(float a, float b, float c, float d) {
+  const uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, -448.0f, 448.0f),
+                                                               __builtin_amdgcn_fmed3f(b, -448.0f, 448.0f), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, -448.0f, 448.0f),
+                                                   __builtin_amdgcn_fmed3f(d, -448.0f, 448.0f), (int)r, true);
+}
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4_sw(float a, float b, float c, float d) {
+  return f32_to_fp8(a) | (f32_to_fp8(b) << 8) | (f32_to_fp8(c) << 16) | (f32_to_fp8(d) << 24);
+}
+
 // torch.argmax order: NaN beats every number (lowest NaN index wins), ties go
 // to the lowest index.  True if (v, i) should replace the current best (bv, bi).
 __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {

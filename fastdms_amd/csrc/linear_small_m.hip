@@ -17,9 +17,13 @@
 // and the output may go through a fused epilogue:
 //   EPI = 1: the weight holds [gate; up] (n = 2 * n_out rows, gate_up_proj) and
 //            the output is bf16(silu(bf16 gate) * bf16 up) (activation.py:8-11).
-//   EPI = 3: bf16 weights, no bias: each K split writes its fp32 partial sums
-//            to workspace[split][m][n] and the consumer adds them in split
-//            order (the merge of EPI 0, moved into the next kernel).
+//   EPI = 3: no bias: each K split writes its fp32 partial sums to
+//            workspace[split][m][n]; the consumer adds them in split order and
+//            applies the row scale 1/x_s[m] and the FP8 column scale (the merge
+//            and scaling of EPI 0, moved into the next kernel).
+// The activation's per-row amax may come from its producer (x_amax: the
+// RMSNorm's output amax, or the per-strip output amax that EPI 0 / 1 writes to
+// amax_out) instead of a statistics pass over x.
 //
 // MI355X mapping: one workgroup per 16-column output strip (per gate/up strip
 // pair for EPI 1) and K split; its NW waves split the workgroup's K range.  A
@@ -232,7 +236,7 @@ __device__ __forceinline__ void row_stats(const bf16_t* xr, const bf16_t* rr, co
 // K split.  EPI 0: y = the finalised value.  EPI 1 (gate_up): the workgroup
 // computes gate strip n0 and up strip n0 + n_out and writes
 // bf16(silu(bf16 gate) * bf16 up) -- gate_up followed by SiluAndMul.
-template <typename WT, int PRO, bool QX, int EPI, int NW, int U>
+template <typename WT, int PRO, bool QX, int EPI, int NW, int U, bool XQ = false>
 __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     const bf16_t* __restrict__ x, int64_t x_s, int M, int K, const WT* __restrict__ w, int64_t w_s,
     const float* __restrict__ w_scale_inv, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ norm_w,
@@ -240,19 +244,26 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
     int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx,
     const bf16_t* __restrict__ g_scale, const bf16_t* __restrict__ g_zero, int group, int64_t g_s, int qx_torch,
-    int bf16_scores) {
+    int bf16_scores, const float* __restrict__ x_amax, int x_amax_n, int64_t x_amax_s, float* __restrict__ amax_out,
+    float* __restrict__ row_scale_out) {
   constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
   // FP8 weights with the quantised activation run on the FP8 matrix cores
   // (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales): 128-column k-blocks,
   // lane group g holding columns 32g .. 32g + 31 of both operands, no
   // per-element conversion of the weights
   constexpr bool F8 = is_fp8<WT>() && QX && PRO == 0;
+  // XQ: x already holds the e4m3fn codes of the quantised activation (its
+  // producer quantised it with the row amax it hands over in x_amax)
+  static_assert(!XQ || F8, "a pre-quantised activation needs FP8 weights");
   constexpr int KB = F8 ? 2 * kKB : kKB;
   __shared__ float s_inv[kMaxM], s_xs[kMaxM];
   __shared__ f32x4 s_acc[NA][NW][64];
   __shared__ int s_last;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // the wave index is uniform across the wave: saying so keeps the k-range
+  // tests below scalar branches (a divergent branch around a load makes the
+  // compiler wait for the load where the branches join)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   // XCD-aware (strip, split): the K splits of one strip run on the same XCD
   const int lin = blockIdx.x;
   const int xcd = lin % kXcds;
@@ -273,8 +284,10 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   if (EPI == 1) wrow[NA - 1] = w + (int64_t)(n0 + n_out + c) * w_s;
   const bool has_row = c < M;
   const bf16_t* xrow = x + (int64_t)(has_row ? c : 0) * x_s;
+  const uint8_t* xqrow = reinterpret_cast<const uint8_t*>(x) + (int64_t)(has_row ? c : 0) * x_s;  // XQ
   const bf16_t* rrow = (PRO == 1 && res) ? res + (int64_t)(has_row ? c : 0) * res_s : nullptr;
   float inv = 1.0f, xsc = 1.0f;  // row statistics, read after the stats pass below
+  bool xfin = true;               // F8: x * xsc of this lane's row is finite and in range
   f32x4 acc[NA];
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -290,23 +303,37 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   };
   auto load = [&](int kb0, Buf& b) {
     if constexpr (F8) {
+      // the group's activation loads go out before its weight loads: loads
+      // complete in issue order, so the activation (from L2) is quantised
+      // while the weights are still on their way from HBM.  Branch-free: a
+      // last half block (64 columns) has nothing for lane groups 2 and 3,
+      // whose loads are clamped in bounds and whose values (and those of rows
+      // >= M, read from row 0) are zeroed in compute
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int k = kb0 + u * KB + 32 * g;
         if (kb0 + u * KB < kend) {
-          // branch-free: a last half block (64 columns) has nothing for lane
-          // groups 2 and 3, whose loads are clamped in bounds and whose values
-          // (and those of rows >= M, read from row 0) are zeroed in compute
-          const int kl = min(k, kend - 32);
+          const int kl = min(kb0 + u * KB + 32 * g, kend - 32);
+          if constexpr (XQ) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xqrow + kl);
+            b.x8[u][0] = xp[0];
+            b.x8[u][1] = xp[1];
+          } else {
+            const uint4* xp = reinterpret_cast<const uint4*>(xrow + kl);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b.x8[u][i] = xp[i];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB < kend) {
+          const int kl = min(kb0 + u * KB + 32 * g, kend - 32);
 #pragma unroll
           for (int a = 0; a < NA; ++a) {
             const uint4* p = reinterpret_cast<const uint4*>(wrow[a] + kl);
             b.w8[a][u][0] = p[0];
             b.w8[a][u][1] = p[1];
           }
-          const uint4* xp = reinterpret_cast<const uint4*>(xrow + kl);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) b.x8[u][i] = xp[i];
         }
       }
       return;
@@ -345,13 +372,21 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   };
   auto compute = [&](int kb0, const Buf& b) {
     if constexpr (F8) {
+      // every block's activation quantised first (it arrives before the
+      // weights), then the MFMAs
+      uint32_t qx[U][8];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (kb0 + u * KB >= kend) break;
-        const bool gv = kb0 + u * KB + 32 * g < kend;  // this lane group's columns exist
-        // x * x_s quantised to e4m3fn, four columns per word (the hardware
-        // RNE-saturating conversion; a NaN anywhere in the block takes the
-        // software encoder, one branch per block)
+        if constexpr (XQ) {
+          const uint4 a0 = b.x8[u][0], a1 = b.x8[u][1];
+          qx[u][0] = a0.x; qx[u][1] = a0.y; qx[u][2] = a0.z; qx[u][3] = a0.w;
+          qx[u][4] = a1.x; qx[u][5] = a1.y; qx[u][6] = a1.z; qx[u][7] = a1.w;
+          continue;
+        }
+        // x * x_s quantised to e4m3fn, four columns per word: the clamped
+        // hardware RNE conversion, or the software encoder for a row whose
+        // amax or scale is not finite (NaN / inf elements)
         float f[32];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -362,25 +397,20 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
             f[8 * i + 2 * e + 1] = bf_hi(v[e]) * xsc;
           }
         }
-        uint32_t q[8];
-        bool nan = false;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float c0 = __builtin_amdgcn_fmed3f(f[4 * j], -kFp8Max, kFp8Max);
-          const float c1 = __builtin_amdgcn_fmed3f(f[4 * j + 1], -kFp8Max, kFp8Max);
-          const float c2 = __builtin_amdgcn_fmed3f(f[4 * j + 2], -kFp8Max, kFp8Max);
-          const float c3 = __builtin_amdgcn_fmed3f(f[4 * j + 3], -kFp8Max, kFp8Max);
-          uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false);
-          q[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, (int)r, true);
-          nan |= (f[4 * j] != f[4 * j]) | (f[4 * j + 1] != f[4 * j + 1]) | (f[4 * j + 2] != f[4 * j + 2]) |
-                 (f[4 * j + 3] != f[4 * j + 3]);
-        }
-        if (__builtin_expect(nan, 0)) {
+        if (__builtin_expect(xfin, 1)) {
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            q[j] = f32_to_fp8(f[4 * j]) | (f32_to_fp8(f[4 * j + 1]) << 8) | (f32_to_fp8(f[4 * j + 2]) << 16) |
-                   (f32_to_fp8(f[4 * j + 3]) << 24);
+            qx[u][j] = f32x4_to_fp8x4_finite(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qx[u][j] = f32x4_to_fp8x4_sw(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
         }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB >= kend) break;
+        const bool gv = kb0 + u * KB + 32 * g < kend;  // this lane group's columns exist
+        const uint32_t* q = qx[u];
         const bool xv = gv && has_row;
         const i32x8 bx = i32x8{xv ? (int)q[0] : 0, xv ? (int)q[1] : 0, xv ? (int)q[2] : 0, xv ? (int)q[3] : 0,
                                xv ? (int)q[4] : 0, xv ? (int)q[5] : 0, xv ? (int)q[6] : 0, xv ? (int)q[7] : 0};
@@ -442,44 +472,108 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   };
 
-  Buf cur, nxt;
-  if (kw0 < kend) load(kw0, cur);  // the first weight group is in flight during the stats pass
+  // 448 / amax: the Triton kernels divide; torch's tensor expression
+  // (_fp8_linear) multiplies the reciprocal of amax by 448 (two roundings)
+  auto x_scale = [&](float a) { return fp8_row_scale(a, qx_torch != 0); };
 
+  // Activation statistics (PRO 0 with QX): their loads go out before the
+  // weight loads -- loads complete in issue order, so the statistics wait for
+  // their own loads only -- and the first two weight groups are in flight
+  // while the statistics are reduced.  Maxima are taken over abs_bits (NaN
+  // propagates, as in the producers' amax).
+  constexpr int NT = NW * 64;
+  constexpr int kRowsPerWave = (kMaxM + NW - 1) / NW;
+  __shared__ uint32_t s_am[kMaxM][NW];
+  __shared__ float s_amax[kMaxM];
+  const bool amax_one = PRO == 0 && QX && x_amax && x_amax_n == 1;  // uniform
+  uint32_t a_one = 0;                // amax_one: row c's amax, one load per lane
+  uint32_t av[kRowsPerWave][8];      // x_amax partials: rows wave, wave + NW, ...
+  uint4 xv[kMaxM];                   // no x_amax: the first 8-column chunk of each row
   if (PRO == 0 && QX) {
-    // per-row 448/amax of x: the whole workgroup reads every row at once,
-    // thread t the 8-column chunks t, t + NT, ... (one pass of loads, then a
-    // wave reduction per row and one across the waves)
-    constexpr int NT = NW * 64;
-    __shared__ float s_am[kMaxM][NW];
-    float am[kMaxM];
+    if (amax_one) {
+      a_one = abs_bits(x_amax[(int64_t)min(c, M - 1) * x_amax_s]);
+    } else if (x_amax) {
+      // indices clamped in bounds: a repeated element cannot change a maximum
 #pragma unroll
-    for (int mm = 0; mm < kMaxM; ++mm) am[mm] = 0.0f;
-    for (int c = tid * 8; c < K; c += NT * 8) {
-      uint4 xv[kMaxM];
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const float* ap = x_amax + (int64_t)min(wave + rr * NW, M - 1) * x_amax_s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) av[rr][j] = abs_bits(ap[min(lane + 64 * j, x_amax_n - 1)]);
+      }
+    } else {
+      // the whole workgroup reads every row at once, thread t the 8-column
+      // chunks t, t + NT, ...; rows and columns clamped in bounds
+      const int c0 = min(tid * 8, K - 8);
+#pragma unroll
+      for (int mm = 0; mm < kMaxM; ++mm) xv[mm] = *reinterpret_cast<const uint4*>(x + (int64_t)min(mm, M - 1) * x_s + c0);
+    }
+  }
+
+  // with statistics to wait for, both first groups go out before them;
+  // otherwise the loop below issues group 1 right after group 0
+  constexpr bool kEarly2 = PRO == 0 && QX;
+  constexpr int G = U * KB;  // columns per group
+  Buf b0, b1;                // even / odd groups (no register copies between them)
+  if (kw0 < kend) load(kw0, b0);
+  if (kEarly2 && kw0 + G < kend) load(kw0 + G, b1);
+
+  // |bf16| of both halves of a word as abs_bits
+  auto bf_abs_max = [](uint32_t m, uint32_t w) { return max(m, max((w << 16) & 0x7FFFFFFFu, w & 0x7FFF0000u)); };
+  if (amax_one) {
+    const float a = __uint_as_float(a_one);
+    xsc = x_scale(a);
+    xfin = fp8_row_finite(a, xsc);
+    if (wave == 0 && lane < M) s_xs[lane] = xsc;  // the epilogue's copy (read after the reduction barrier)
+  } else if (PRO == 0 && QX && x_amax) {
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int mm = wave + rr * NW;
+      uint32_t a = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a = max(a, av[rr][j]);
+      const float* ap = x_amax + (int64_t)min(mm, M - 1) * x_amax_s;
+      for (int p = lane + 64 * 8; p < x_amax_n; p += 64) a = max(a, abs_bits(ap[p]));  // beyond 512 partials
+      a = wave_max_u32(a);
+      if (lane == 0 && mm < M) {
+        s_amax[mm] = __uint_as_float(a);
+        s_xs[mm] = x_scale(__uint_as_float(a));
+      }
+    }
+    __syncthreads();
+  } else if (PRO == 0 && QX) {
+    uint32_t am[kMaxM];
+#pragma unroll
+    for (int mm = 0; mm < kMaxM; ++mm) {
+      const uint32_t w4[4] = {xv[mm].x, xv[mm].y, xv[mm].z, xv[mm].w};
+      am[mm] = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) am[mm] = bf_abs_max(am[mm], w4[i]);
+    }
+    for (int cc = tid * 8 + NT * 8; cc < K; cc += NT * 8) {  // rows longer than one pass
+      uint4 xr[kMaxM];
 #pragma unroll
       for (int mm = 0; mm < kMaxM; ++mm)
-        xv[mm] = *reinterpret_cast<const uint4*>(x + (int64_t)min(mm, M - 1) * x_s + c);  // clamped row
+        xr[mm] = *reinterpret_cast<const uint4*>(x + (int64_t)min(mm, M - 1) * x_s + cc);
 #pragma unroll
       for (int mm = 0; mm < kMaxM; ++mm) {
-        const uint32_t w4[4] = {xv[mm].x, xv[mm].y, xv[mm].z, xv[mm].w};
+        const uint32_t w4[4] = {xr[mm].x, xr[mm].y, xr[mm].z, xr[mm].w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) am[mm] = fmaxf(am[mm], fmaxf(fabsf(bf_lo(w4[i])), fabsf(bf_hi(w4[i]))));
+        for (int i = 0; i < 4; ++i) am[mm] = bf_abs_max(am[mm], w4[i]);
       }
     }
 #pragma unroll
     for (int mm = 0; mm < kMaxM; ++mm) {
       if (mm >= M) break;
-      const float w = wave_max(am[mm]);
+      const uint32_t w = wave_max_u32(am[mm]);
       if (lane == 0) s_am[mm][wave] = w;
     }
     __syncthreads();
     if (tid < M) {
-      float a = 0.0f;
+      uint32_t a = 0;
 #pragma unroll
-      for (int w2 = 0; w2 < NW; ++w2) a = fmaxf(a, s_am[tid][w2]);
-      // 448 / amax: the Triton kernels divide; torch's tensor expression
-      // (_fp8_linear) multiplies the reciprocal of amax by 448 (two roundings)
-      s_xs[tid] = a > 0.0f ? (qx_torch ? (1.0f / a) * kFp8Max : kFp8Max / a) : 1.0f;
+      for (int w2 = 0; w2 < NW; ++w2) a = max(a, s_am[tid][w2]);
+      s_amax[tid] = __uint_as_float(a);
+      s_xs[tid] = x_scale(__uint_as_float(a));
     }
     __syncthreads();
   } else if (PRO == 1 || QX) {
@@ -496,12 +590,20 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   }
 
   if (PRO == 1 && has_row) inv = s_inv[c];
-  if (QX && has_row) xsc = s_xs[c];
-  for (int kb0 = kw0; kb0 < kend; kb0 += U * KB) {
-    const bool more = kb0 + U * KB < kend;
-    if (more) load(kb0 + U * KB, nxt);  // next group in flight while this one computes
-    compute(kb0, cur);
-    if (more) cur = nxt;
+  if (QX && has_row && !amax_one) {
+    xsc = s_xs[c];
+    if constexpr (F8) xfin = fp8_row_finite(s_amax[c], xsc);
+  }
+  // group i + 1 loads while group i computes
+  for (int kb0 = kw0; kb0 < kend; kb0 += 2 * G) {
+    const bool odd = kb0 + G < kend;
+    if (!kEarly2 && odd) load(kb0 + G, b1);
+    compute(kb0, b0);
+    if (kb0 + 2 * G < kend) load(kb0 + 2 * G, b0);
+    if (odd) {
+      compute(kb0 + G, b1);
+      if (kEarly2 && kb0 + 3 * G < kend) load(kb0 + 3 * G, b1);
+    }
   }
 
   // ---- reduce the waves' C fragments; lane l holds C[n = 4*(l/16) + r][m = l%16]
@@ -523,12 +625,15 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   }
   if (EPI == 3) {
-    // split partials for the consumer to sum (no merge here): ws[ks][m][n]
+    // split partials for the consumer to sum (no merge here): ws[ks][m][n]; the
+    // consumer applies the row scale 1/x_s[m] (one workgroup publishes it) and
+    // the weight's column scale after the sum, as the merge below does
     const int mm = lane & 15;
     if (mm < M) {
       float* dst = ws + ((int64_t)ks * M + mm) * n_out + n0 + 4 * (lane >> 4);
       *reinterpret_cast<f32x4*>(dst) = t[0];
     }
+    if (row_scale_out && strip == 0 && ks == 0 && lane < M) row_scale_out[lane] = QX ? 1.0f / s_xs[lane] : 1.0f;
     return;
   }
   if (ksplit > 1) {
@@ -617,8 +722,8 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
     return;
   }
-  if (m >= M) return;
-  const float xsi = QX ? 1.0f / s_xs[m] : 1.0f;
+  const bool row_ok = m < M;
+  const float xsi = (QX && row_ok) ? 1.0f / s_xs[m] : 1.0f;
   auto finalize = [&](float acc_v, int n) {
     float v;
     if (is_fp8<WT>() || is_int4<WT>() || QX) {  // matmul rounded to bf16, then the bias
@@ -631,6 +736,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
     return v;
   };
+  uint32_t vmax = 0;  // the row's max |output| over this strip, as abs_bits (rows >= M hold x = 0)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int n = n0 + 4 * (lane >> 4) + r;
@@ -642,7 +748,16 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     } else {
       v = finalize(t[0][r], n);
     }
-    y[(int64_t)m * y_s + n].bits = __builtin_bit_cast(uint16_t, (__bf16)v);
+    const __bf16 vb = (__bf16)v;
+    vmax = max(vmax, abs_bits((float)vb));
+    if (row_ok) y[(int64_t)m * y_s + n].bits = __builtin_bit_cast(uint16_t, vb);
+  }
+  if (EPI <= 1 && amax_out) {
+    // per-strip row amax (NaN propagating) for the consumer's activation
+    // quantisation: lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same row
+    vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 16));
+    vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 32));
+    if (lane < 16 && row_ok) amax_out[(int64_t)m * strips + strip] = __uint_as_float(vmax);
   }
 }
 
@@ -654,21 +769,25 @@ struct LinArgs {
   bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters; float* pval; int* pidx;
   const bf16_t* g_scale = nullptr; const bf16_t* g_zero = nullptr; int group = 1; int64_t g_s = 0;
   int qx_torch = 0; int bf16_scores = 1;
+  const float* x_amax = nullptr; int x_amax_n = 0; int64_t x_amax_s = 0; float* amax_out = nullptr;
+  float* row_scale_out = nullptr;
 };
 
-template <typename WT, int PRO, bool QX, int EPI>
+template <typename WT, int PRO, bool QX, int EPI, bool XQ = false>
 void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   const WT* w = (const WT*)a.w;
   // k-blocks per double-buffered group (register budget: the RMSNorm prologue
-  // also holds the residual and norm weight of each k-block)
-  constexpr int U = (PRO == 1 || (std::is_same<WT, fp8_t>::value && QX && PRO == 0)) ? 2 : 4;
+  // also holds the residual and norm weight of each k-block, the activation
+  // statistics hold their loads while both first groups are in flight)
+  constexpr int U = (PRO == 1 || (QX && PRO == 0)) ? 2 : 4;
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
                       a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
-                      a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores
+                      a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores, a.x_amax, a.x_amax_n, \
+                      a.x_amax_s, a.amax_out, a.row_scale_out
   if (nw == 8) {
-    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
+    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U, XQ>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
   } else {
-    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 4, U>), grid, dim3(256), 0, st, FDMS_LIN_ARGS);
+    hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 4, U, XQ>), grid, dim3(256), 0, st, FDMS_LIN_ARGS);
   }
 #undef FDMS_LIN_ARGS
 }
@@ -697,11 +816,19 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
                                     const void* norm_weight, float eps, const void* residual, int64_t res_stride,
                                     void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue,
                                     int k_splits, float* workspace, int* counters, void* y, int64_t y_stride,
-                                    void* stream) {
+                                    const float* x_amax, int x_amax_n, int64_t x_amax_stride, float* amax_out,
+                                    float* row_scale_out, int x_dtype, void* stream) {
   if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 ||
       (epilogue > 1 && epilogue != 3) || quantize_x < 0 || quantize_x > 2)
     return (int)hipErrorInvalidValue;
-  if (epilogue == 3 && (w_dtype != kBF16 || prologue != 0 || quantize_x != 0 || bias || !workspace))
+  if (epilogue == 3 && (prologue != 0 || bias || !workspace)) return (int)hipErrorInvalidValue;
+  // the producer's row amax replaces the activation statistics pass (no prologue)
+  if (x_amax && (prologue != 0 || quantize_x == 0 || x_amax_n < 1 || (m > 1 && x_amax_stride < x_amax_n)))
+    return (int)hipErrorInvalidValue;
+  if ((amax_out && epilogue > 1) || (row_scale_out && epilogue != 3)) return (int)hipErrorInvalidValue;
+  // an activation quantised by its producer: e4m3fn codes with their row amax
+  const bool xq = x_dtype == kFP8;
+  if ((x_dtype != kBF16 && !xq) || (xq && (w_dtype != kFP8 || quantize_x == 0 || !x_amax)))
     return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
   if (!x || !w || !y || (prologue == 1 && !norm_weight)) return (int)hipErrorInvalidValue;
@@ -726,7 +853,7 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;  // whole k-blocks per wave
   const int wsz = w_dtype == kFP8 ? 1 : 2;
   auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
-  if (!al16(x) || !al16(w) || (x_stride * 2) % 16 || (w_stride * wsz) % 16) return (int)hipErrorInvalidValue;
+  if (!al16(x) || !al16(w) || (x_stride * (xq ? 1 : 2)) % 16 || (w_stride * wsz) % 16) return (int)hipErrorInvalidValue;
   if (prologue == 1 && (!al16(norm_weight) || (residual && (!al16(residual) || (res_stride * 2) % 16)) ||
                         (residual_out && (!al16(residual_out) || (res_out_stride * 2) % 16))))
     return (int)hipErrorInvalidValue;
@@ -741,8 +868,20 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
             res_out_stride, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, nullptr,
             nullptr};
   a.qx_torch = quantize_x == 2;
-  if (epilogue == 3) {
-    launch_linear<bf16_t, 0, false, 3>(nw, grid, (hipStream_t)stream, a);
+  a.x_amax = x_amax;
+  a.x_amax_n = x_amax_n;
+  a.x_amax_s = x_amax_stride;
+  a.amax_out = amax_out;
+  a.row_scale_out = row_scale_out;
+  if (xq) {
+    if (epilogue == 3) launch_linear<fp8_t, 0, true, 3, true>(nw, grid, (hipStream_t)stream, a);
+    else if (epilogue == 1) launch_linear<fp8_t, 0, true, 1, true>(nw, grid, (hipStream_t)stream, a);
+    else launch_linear<fp8_t, 0, true, 0, true>(nw, grid, (hipStream_t)stream, a);
+  } else if (epilogue == 3) {
+    if (w_dtype == kFP8 && quantize_x) launch_linear<fp8_t, 0, true, 3>(nw, grid, (hipStream_t)stream, a);
+    else if (w_dtype == kFP8) launch_linear<fp8_t, 0, false, 3>(nw, grid, (hipStream_t)stream, a);
+    else if (quantize_x) launch_linear<bf16_t, 0, true, 3>(nw, grid, (hipStream_t)stream, a);
+    else launch_linear<bf16_t, 0, false, 3>(nw, grid, (hipStream_t)stream, a);
   } else if (w_dtype == kFP8) {
     dispatch_linear<fp8_t>(prologue, quantize_x, epilogue, nw, grid, (hipStream_t)stream, a);
   } else {

@@ -21,6 +21,17 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
   __syncthreads();
   return t;
 }
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, float* s_red) {
+  v = wave_max_u32(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) s_red[w] = __uint_as_float(v);
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) t = max(t, __float_as_uint(s_red[i]));
+  __syncthreads();
+  return t;
+}
 }  // namespace
 
 // x_out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w), where x = in (+ residual
@@ -29,7 +40,14 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
 // part[s * split_stride + row * hidden + c], s < k_splits, and x = bf16 of
 // their sum taken in split order (the linear kernel's own merge).
 // PART: the input is the fp32 split-K partials; KS > 0 is their count known
-// at compile time, KS = 0 reads k_splits at run time.  PER = 8-column chunks
+// at compile time, KS = 0 reads k_splits at run time.  With row_scale /
+// col_scale (an FP8 linear's 1/x_s[row] and weight scale_inv[c]) the input is
+// x = bf16(sum * row_scale[row] * col_scale[c]), the linear's own finalisation.
+// amax_out[row] (optional) = max |out[row, :]| (NaN if the row holds one), the
+// statistic the next FP8 linear's activation quantisation needs; q_out
+// (optional, with amax_out) receives that quantisation itself, e4m3fn(out *
+// s) with s = 448 / amax (q_mode 2: the torch rounding), and out may then be
+// null.  PER = 8-column chunks
 // per thread (hidden <= PER * 8 * kThreads).  Every load of the row goes out
 // before the first use, with addresses clamped in bounds instead of loads
 // under a condition (a conditional load makes the compiler wait for it at
@@ -40,7 +58,10 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
                                                            bf16_t* residual_out, int hidden, int64_t in_stride,
                                                            int64_t in_head_stride, int heads, int64_t out_stride,
                                                            float eps, const float* __restrict__ part, int k_splits,
-                                                           int64_t split_stride) {
+                                                           int64_t split_stride, const float* __restrict__ row_scale,
+                                                           const float* __restrict__ col_scale,
+                                                           float* __restrict__ amax_out, uint8_t* __restrict__ q_out,
+                                                           int64_t q_stride, int q_mode) {
   __shared__ float s_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const bf16_t* x = PART ? nullptr : in + (row / heads) * in_stride + (row % heads) * in_head_stride;
@@ -49,11 +70,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   constexpr int V = 8;
   constexpr int NS = KS > 0 ? KS : 1;
   Vec<bf16_t, V> wv[PER], xv[PER], rv[PER];
-  Vec<float, V> pv[PER][NS];
+  Vec<float, V> pv[PER][NS], cs[PER];
+  const float* csrc = (PART && col_scale) ? col_scale : part;  // a valid address either way (PART)
+  const float rscale = (PART && row_scale) ? row_scale[row] : 1.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int cc = min((threadIdx.x + j * kThreads) * V, hidden - V);
     wv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + cc);
+    if constexpr (PART) cs[j] = *reinterpret_cast<const Vec<float, V>*>(csrc + cc);
     if constexpr (PART && KS > 0) {
 #pragma unroll
       for (int sp = 0; sp < KS; ++sp)
@@ -84,6 +108,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
           for (int i = 0; i < V; ++i) xf[i] += p.v[i];
         }
       }
+      if (row_scale) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xf[i] *= rscale;
+      }
+      if (col_scale) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xf[i] *= cs[j].v[i];
+      }
 #pragma unroll
       for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(f32_to_bf16(xf[i]));
     } else {
@@ -106,17 +138,42 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   }
   const float total = block_sum(ss, s_red);
   const float inv = rsqrtf(total / (float)hidden + eps);  // torch.rsqrt (layernorm.py:24, 38)
+  uint32_t amax = 0;
+  float ov[PER][V];  // the bf16 outputs as fp32
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = (threadIdx.x + j * kThreads) * V;
-    if (c < hidden) {
-      Vec<bf16_t, V> o;
+    Vec<bf16_t, V> o;
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float xn = bf16_to_f32(f32_to_bf16(vals[j][i] * inv));
-        o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv[j].v[i].bits));
+    for (int i = 0; i < V; ++i) {
+      const float xn = bf16_to_f32(f32_to_bf16(vals[j][i] * inv));
+      o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv[j].v[i].bits));
+      ov[j][i] = bf16_to_f32(o.v[i].bits);
+      if (c < hidden) amax = max(amax, abs_bits(ov[j][i]));
+    }
+    if (out && c < hidden) *reinterpret_cast<Vec<bf16_t, V>*>(out + row * out_stride + c) = o;
+  }
+  if (amax_out) {  // uniform
+    amax = block_max_u32(amax, s_red);
+    const float a = __uint_as_float(amax);
+    if (threadIdx.x == 0) amax_out[row] = a;
+    if (q_out) {
+      const float qs = fp8_row_scale(a, q_mode == 2);
+      const bool finite = fp8_row_finite(a, qs);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int c = (threadIdx.x + j * kThreads) * V;
+        if (c < hidden) {
+          uint32_t w[V / 4];
+#pragma unroll
+          for (int i = 0; i < V / 4; ++i) {
+            const float* f = &ov[j][4 * i];
+            w[i] = finite ? f32x4_to_fp8x4_finite(f[0] * qs, f[1] * qs, f[2] * qs, f[3] * qs)
+                          : f32x4_to_fp8x4_sw(f[0] * qs, f[1] * qs, f[2] * qs, f[3] * qs);
+          }
+          *reinterpret_cast<uint2*>(q_out + row * q_stride + c) = uint2{w[0], w[1]};
+        }
       }
-      *reinterpret_cast<Vec<bf16_t, V>*>(out + row * out_stride + c) = o;
     }
   }
 }
@@ -127,11 +184,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
 // is at out + r * out_stride; residual / residual_out are contiguous rows.
 FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int heads,
                              const void* residual, const void* weight, void* out, int64_t out_stride,
-                             void* residual_out, int64_t rows, int hidden, float eps, void* stream) {
+                             void* residual_out, int64_t rows, int hidden, float eps, float* amax_out,
+                             void* q_out, int64_t q_stride, int q_mode, void* stream) {
   if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 8 * kThreads * 4 || heads <= 0) return (int)hipErrorInvalidValue;
   if (heads > 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
+  if (q_out && (!amax_out || q_mode < 1 || q_mode > 2 || q_stride < hidden || q_stride % 8 || (uintptr_t)q_out % 8))
+    return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
-  if (!in || !weight || !out || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if (!in || !weight || (!out && !q_out) || rows > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   // rows move as 16-byte vectors
   if (!fdms_aligned16(in, weight, out, residual, residual_out) || (in_stride | in_head_stride | out_stride) % 8)
     return (int)hipErrorInvalidValue;
@@ -139,7 +199,7 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                  \
                      (hipStream_t)stream, (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight,        \
                      (bf16_t*)out, (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps, \
-                     nullptr, 0, (int64_t)0)
+                     nullptr, 0, (int64_t)0, nullptr, nullptr, amax_out, (uint8_t*)q_out, q_stride, q_mode)
   const int per = (hidden + 8 * kThreads - 1) / (8 * kThreads);
   if (per == 1) FDMS_RMSNORM(1);
   else if (per == 2) FDMS_RMSNORM(2);
@@ -154,18 +214,22 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
 // fdms_linear_small_m's epilogue 3.  residual / residual_out contiguous rows.
 FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64_t split_stride,
                                       const void* residual, const void* weight, void* out, int64_t out_stride,
-                                      void* residual_out, int64_t rows, int hidden, float eps, void* stream) {
+                                      void* residual_out, int64_t rows, int hidden, float eps,
+                                      const float* row_scale, const float* col_scale, float* amax_out,
+                                      void* q_out, int64_t q_stride, int q_mode, void* stream) {
   if (rows < 0 || hidden <= 0 || hidden % 8 || hidden > 8 * kThreads * 4 || k_splits < 1) return (int)hipErrorInvalidValue;
-  if (rows == 0) return 0;
-  if (!partials || !weight || !out || rows > 0x7FFFFFFF || split_stride < rows * (int64_t)hidden)
+  if (q_out && (!amax_out || q_mode < 1 || q_mode > 2 || q_stride < hidden || q_stride % 8 || (uintptr_t)q_out % 8))
     return (int)hipErrorInvalidValue;
-  if ((uintptr_t)partials % 32 || split_stride % 8) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!partials || !weight || (!out && !q_out) || rows > 0x7FFFFFFF || split_stride < rows * (int64_t)hidden)
+    return (int)hipErrorInvalidValue;
+  if ((uintptr_t)partials % 32 || split_stride % 8 || (uintptr_t)col_scale % 32) return (int)hipErrorInvalidValue;
   if (!fdms_aligned16(weight, out, residual, residual_out) || out_stride % 8) return (int)hipErrorInvalidValue;
 #define FDMS_RMSNORM_PART(KSV, PERV)                                                                              \
   hipLaunchKernelGGL((rmsnorm_kernel<true, KSV, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                   \
                      (hipStream_t)stream, nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,      \
                      (bf16_t*)residual_out, hidden, (int64_t)0, (int64_t)0, 1, out_stride, eps, partials, k_splits,   \
-                     split_stride)
+                     split_stride, row_scale, col_scale, amax_out, (uint8_t*)q_out, q_stride, q_mode)
 #define FDMS_RMSNORM_PART_PER(PERV)                   \
   if (k_splits == 1) FDMS_RMSNORM_PART(1, PERV);      \
   else if (k_splits == 2) FDMS_RMSNORM_PART(2, PERV); \

@@ -83,10 +83,15 @@ def choose_partial_splits(device: torch.device, strips: int, k: int) -> int:
 class SplitPartials:
     """fp32 split-K partial sums [k_splits, rows, n] of a decode linear whose
     merge is left to the consuming RMSNorm (``rms_norm`` accepts this in place
-    of x): x = bf16(sum over splits, in split order)."""
+    of x): x = bf16(sum over splits, in split order), times ``row_scale[row]``
+    (an FP8 linear's 1/x_s) and ``col_scale[col]`` (its weight scale_inv) when
+    present."""
 
-    def __init__(self, data: torch.Tensor):
+    def __init__(self, data: torch.Tensor, row_scale: torch.Tensor | None = None,
+                 col_scale: torch.Tensor | None = None):
         self.data = data
+        self.row_scale = row_scale
+        self.col_scale = col_scale
 
     @property
     def shape(self):
@@ -94,19 +99,40 @@ class SplitPartials:
 
 
 _PARTIALS: dict[int, torch.Tensor] = {}
+_ROW_SCALES: dict[int, torch.Tensor] = {}
 
 
-def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None = None) -> SplitPartials:
-    """y = x @ W^T (bf16 W [N, K], no bias, at most 16 rows) as fp32 split
-    partials (fdms_linear_small_m epilogue 3).  The partials live in a per-device
-    buffer that the next call overwrites: consume them before the next
-    linear_partials call."""
-    if weight.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or x.stride(-1) != 1:
-        raise ValueError("linear_partials expects bf16 activations and bf16 weights")
+def _amax_args(x_amax: torch.Tensor | None, rows: int) -> tuple[int, int, int]:
+    """(pointer, partial maxima per row, row stride) of a producer's amax
+    [rows, n] fp32 (n = 1 for an RMSNorm's, the strips for a linear's)."""
+    if x_amax is None:
+        return 0, 0, 0
+    if x_amax.dtype != torch.float32 or x_amax.dim() != 2 or x_amax.shape[0] < rows or x_amax.stride(1) != 1:
+        raise ValueError("x_amax must be fp32 [rows, n] with a contiguous last axis")
+    return x_amax.data_ptr(), x_amax.shape[1], x_amax.stride(0)
+
+
+def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None = None, *,
+                    weight_scale_inv: torch.Tensor | None = None, quantize_x: int | None = None,
+                    x_amax: torch.Tensor | None = None) -> SplitPartials:
+    """y = x @ W^T (W [N, K] bf16, or FP8 e4m3fn with ``weight_scale_inv``; no
+    bias, at most 16 rows) as fp32 split partials (fdms_linear_small_m epilogue
+    3); for FP8 weights the row and column scales travel with them.  The
+    partials live in a per-device buffer that the next call overwrites: consume
+    them before the next linear_partials call."""
+    fp8 = weight.dtype == torch.float8_e4m3fn
+    if (weight.dtype != torch.bfloat16 and not fp8) or x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+        raise ValueError("linear_partials expects bf16 activations and bf16 or FP8 weights")
+    if fp8 and weight_scale_inv is None:
+        raise ValueError("FP8 weights need weight_scale_inv")
+    qx = (QX_DIVIDE if fp8 else QX_NONE) if quantize_x is None else int(quantize_x)
+    if qx not in (QX_NONE, QX_DIVIDE, QX_TORCH):
+        raise ValueError(f"quantize_x must be one of 0, 1, 2; got {quantize_x!r}")
     n, k = weight.shape
     rows = x.shape[0]
     if not small_m_supported(rows, k, n) or x.shape[1] != k:
         raise ValueError(f"linear_partials does not support rows={rows}, K={k}, N={n}")
+    am_ptr, am_n, am_s = _amax_args(x_amax if qx else None, rows)
     if k_splits is None:
         k_splits = choose_partial_splits(x.device, n // 16, k)
     need = k_splits * rows * n
@@ -118,11 +144,20 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None 
         buf = torch.empty(max(need, SMALL_M_MAX_ROWS * 4096 * 4), device=x.device, dtype=torch.float32)
         _PARTIALS[idx] = buf
     part = buf[:need].view(k_splits, rows, n)
+    sinv = row_scale = None
+    if fp8:
+        sinv = weight_scale_inv.reshape(-1)
+        row_scale = _ROW_SCALES.get(idx)
+        if row_scale is None:
+            row_scale = torch.empty(SMALL_M_MAX_ROWS, device=x.device, dtype=torch.float32)
+            _ROW_SCALES[idx] = row_scale
+        row_scale = row_scale[:rows]
     nat.require_cuda(x, weight, what="linear_partials")
-    nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(), nat.DT_BF16,
-             weight.stride(0), None, None, n, PRO_NONE, None, 0.0, None, 0, None, 0, QX_NONE, EPI_PARTIALS,
-             int(k_splits), part.data_ptr(), None, part.data_ptr(), n, nat.stream())
-    return SplitPartials(part)
+    nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
+             nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), None, n, PRO_NONE, None, 0.0,
+             None, 0, None, 0, qx if fp8 else QX_NONE, EPI_PARTIALS, int(k_splits), part.data_ptr(), None,
+             part.data_ptr(), n, am_ptr or None, am_n, am_s, None, nat.ptr(row_scale), nat.DT_BF16, nat.stream())
+    return SplitPartials(part, row_scale, sinv)
 
 
 def linear_workspace(device: torch.device, n_floats: int, n_counters: int):
@@ -178,21 +213,29 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
                    norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
                    residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
                    quantize_x: bool | int | None = None, epilogue: int = EPI_NONE, k_splits: int | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, x_amax: torch.Tensor | None = None,
+                   amax_out: torch.Tensor | None = None) -> torch.Tensor:
     """y = a @ W^T for at most 16 rows.  ``weight`` is [N, K] bf16, or FP8
     e4m3fn with ``weight_scale_inv`` [N] (or [1, N]).  ``a`` is x, or RMSNorm of
     x (+ residual) with ``norm_weight`` (prologue 1; the bf16 sum goes to
     ``residual_out``).  epilogue 1: W = [gate; up] and the result is
     silu(gate) * up, [rows, N/2].  quantize_x: QX_DIVIDE (True; the default for
     FP8 weights, the row-1 / small-M kernels), QX_TORCH (_fp8_linear's form) or
-    QX_NONE (False)."""
+    QX_NONE (False).  ``x_amax`` [rows, n]: x's row amax as partial maxima from
+    its producer (used with activation quantisation and no prologue; same
+    result, no pass over x).  ``amax_out`` [rows, N_out/16] receives the
+    per-strip max |y| for an FP8 consumer of y."""
     if weight.dim() != 2:
         raise ValueError("weight must be [out_features, in_features]")
     n, k = weight.shape
     rows = x.shape[0]
     fp8 = weight.dtype == torch.float8_e4m3fn
-    if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
-        raise ValueError("linear_small_m expects bf16 activations with a contiguous last axis")
+    x_fp8 = x.dtype == torch.float8_e4m3fn   # codes its producer quantised with x_amax
+    if (x.dtype != torch.bfloat16 and not x_fp8) or x.stride(-1) != 1:
+        raise ValueError("linear_small_m expects bf16 (or pre-quantised e4m3fn) activations with a contiguous "
+                         "last axis")
+    if x_fp8 and (not fp8 or x_amax is None or prologue != PRO_NONE or quantize_x in (False, QX_NONE)):
+        raise ValueError("e4m3fn activations need FP8 weights, x_amax and activation quantisation")
     if fp8 and weight_scale_inv is None:
         raise ValueError("FP8 weights need weight_scale_inv")
     if not fp8 and weight.dtype != torch.bfloat16:
@@ -214,12 +257,17 @@ def linear_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
     if k_splits > 1:
         ws, counters = linear_workspace(x.device, strips * k_splits * 256 * (2 if epilogue else 1), strips)
     sinv = None if weight_scale_inv is None else weight_scale_inv.reshape(-1)
+    am_ptr, am_n, am_s = _amax_args(x_amax if (qx and prologue == PRO_NONE) else None, rows)
+    if amax_out is not None and (amax_out.dtype != torch.float32 or not amax_out.is_contiguous()
+                                 or amax_out.numel() < rows * strips):
+        raise ValueError("amax_out must be contiguous fp32 [rows, N_out/16]")
     nat.require_cuda(x, weight, out, what="linear_small_m")
     nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
              nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), nat.ptr(bias), n, int(prologue),
              nat.ptr(norm_weight), float(eps), nat.ptr(residual), 0 if residual is None else residual.stride(0),
              nat.ptr(residual_out), 0 if residual_out is None else residual_out.stride(0), qx,
              int(epilogue), int(k_splits), nat.ptr(ws), nat.ptr(counters), out.data_ptr(), out.stride(0),
+             am_ptr or None, am_n, am_s, nat.ptr(amax_out), None, nat.DT_FP8 if x_fp8 else nat.DT_BF16,
              nat.stream())
     return out
 
@@ -486,23 +534,57 @@ class LinearBase(nn.Module):
             return "fp8", QX_TORCH
         return "bf16", QX_NONE
 
+    def small_m_fused(self, rows: int, epilogue: int = EPI_NONE) -> bool:
+        """True when a call of ``rows`` rows runs fdms_linear_small_m (bf16 or
+        FP8 route on a supported shape; contiguous rows assumed)."""
+        n_out = self.output_size // 2 if epilogue == EPI_SILU_MUL else self.output_size
+        return self.route(rows)[0] in ("bf16", "fp8") and small_m_supported(rows, self.input_size, n_out)
+
+    def x_quant_mode(self, rows: int) -> int:
+        """The activation quantisation (QX_DIVIDE / QX_TORCH) when this linear
+        quantises its activation on the small-M kernel -- its producer may then
+        hand over the row amax, or the quantised codes -- else QX_NONE."""
+        path, qx = self.route(rows)
+        if path == "fp8" and small_m_supported(rows, self.input_size, self.output_size):
+            return qx
+        return QX_NONE
+
+    def wants_x_amax(self, rows: int) -> bool:
+        return self.x_quant_mode(rows) != QX_NONE
+
+    def run_quantized(self, xq: torch.Tensor, x_amax: torch.Tensor, *, epilogue: int = EPI_NONE,
+                      amax_out: torch.Tensor | None = None) -> torch.Tensor:
+        """The small-M FP8 path on an activation its producer already quantised
+        (e4m3fn codes ``xq`` with the row amax ``x_amax``, as rms_norm's q_out
+        with q_mode = x_quant_mode(rows))."""
+        qx = self.x_quant_mode(xq.shape[0])
+        if qx == QX_NONE:
+            raise ValueError("run_quantized needs the small-M FP8 route with activation quantisation")
+        return linear_small_m(xq, self.weight_fp8, self.bias, weight_scale_inv=self.weight_scale_inv, quantize_x=qx,
+                              epilogue=epilogue, x_amax=x_amax, amax_out=amax_out)
+
     def run(self, x2: torch.Tensor, bias: torch.Tensor | None, *, epilogue: int = EPI_NONE,
-            route: tuple[str, int] | None = None) -> torch.Tensor:
+            route: tuple[str, int] | None = None, x_amax: torch.Tensor | None = None,
+            amax_out: torch.Tensor | None = None) -> torch.Tensor:
         """Execute ``route`` (default: self.route) on rows x2 [rows, K].  With
         epilogue EPI_SILU_MUL the weight is [gate; up] and the result is the
-        SiluAndMul of the linear's output (fused into the decode kernels)."""
+        SiluAndMul of the linear's output (fused into the decode kernels).
+        ``x_amax`` / ``amax_out`` as linear_small_m (small-M paths only;
+        amax_out on another path is an error)."""
         rows = x2.shape[0]
         path, qx = self.route(rows) if route is None else route
         n_out = self.output_size // 2 if epilogue == EPI_SILU_MUL else self.output_size
         fused = small_m_supported(rows, self.input_size, n_out) and x2.stride(-1) == 1
+        if amax_out is not None and not (fused and path in ("fp8", "bf16")):
+            raise ValueError("amax_out needs the small-M kernel path")
         if path == "int4":
             return linear_int4_small_m(x2.contiguous(), self.weight_int4, self.weight_int4_scale,
                                        self.weight_int4_zero, self._int4_group_size, bias, epilogue=epilogue)
         if path == "fp8" and fused:
             return linear_small_m(x2.contiguous(), self.weight_fp8, bias, weight_scale_inv=self.weight_scale_inv,
-                                  quantize_x=qx, epilogue=epilogue)
+                                  quantize_x=qx, epilogue=epilogue, x_amax=x_amax, amax_out=amax_out)
         if path == "bf16" and fused:
-            return linear_small_m(x2, self.weight, bias, epilogue=epilogue)
+            return linear_small_m(x2, self.weight, bias, epilogue=epilogue, amax_out=amax_out)
         if path == "fp8":
             y = fp8_rows_gemm(x2, self.weight_fp8, self.weight_scale_inv, bias, qx)
         elif path == "fp8_dequant":  # linear.py:645-647: the weight dequantised in the activation dtype

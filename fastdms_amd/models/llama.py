@@ -22,10 +22,9 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
                                         dms_decode_store_transient_k_enabled, dms_fused_decode_preprocess_enabled,
                                         fused_decode_attention_supported, fused_dms_rope_store_compact_decode)
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
-from ..layers.layernorm import RMSNorm, rms_norm
-from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, PRO_NONE, LinearBase, MergedColumnParallelLinear,
-                             QKVParallelLinear, RowParallelLinear, linear_argmax_small_m, linear_int4_small_m,
-                             linear_partials, linear_small_m, small_m_supported)
+from ..layers.layernorm import RMSNorm
+from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, LinearBase, MergedColumnParallelLinear, QKVParallelLinear,
+                             RowParallelLinear, linear_partials, small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -58,30 +57,53 @@ class ModelConfig:
     successor_margin: float = 0.0
 
 
-def _fused_linear(lin: LinearBase, x: torch.Tensor, prologue: int, norm: RMSNorm | None = None,
-                  residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
-                  epilogue: int = EPI_NONE) -> torch.Tensor:
-    """One decode-shaped linear launch on the path ``lin.route`` picks (the
-    reference's dispatch order), with the SiLU*up epilogue fused; the RMSNorm
-    prologue is fused for bf16 weights only."""
-    if prologue == PRO_NONE:
-        return lin.run(x, lin.bias, epilogue=epilogue)
-    if lin.route(x.shape[0])[0] != "bf16":
-        raise ValueError("the RMSNorm prologue is fused for bf16 weights only")
-    return linear_small_m(x, lin.weight, lin.bias, prologue=prologue,
-                          norm_weight=None if norm is None else norm.weight, eps=1e-6 if norm is None else norm.eps,
-                          residual=residual, residual_out=residual_out, epilogue=epilogue)
-
-
-def _deferred_linear(lin: LinearBase, x: torch.Tensor):
-    """A linear whose only consumer is an RMSNorm: on the bf16 decode path its
-    split-K merge moves into that RMSNorm (SplitPartials), which saves the
-    linear's merge round trips; other paths return the finished tensor."""
+def _deferred_linear(lin: LinearBase, x: torch.Tensor, x_amax: torch.Tensor | None = None):
+    """A linear whose only consumer is an RMSNorm: on the bf16 / FP8 small-M
+    decode path its split-K merge (and the FP8 row / column scaling) moves into
+    that RMSNorm (SplitPartials), which saves the linear's merge round trips;
+    other paths return the finished tensor.  ``x_amax``: x's row amax from its
+    producer, for an FP8 linear's activation quantisation."""
     rows = x.shape[0]
-    if (_defer_splitk_enabled() and lin.bias is None and lin.route(rows)[0] == "bf16"
+    path, qx = lin.route(rows)
+    if (_defer_splitk_enabled() and lin.bias is None and path in ("bf16", "fp8")
             and small_m_supported(rows, lin.input_size, lin.output_size) and x.stride(-1) == 1):
-        return linear_partials(x, lin.weight)
-    return _fused_linear(lin, x, PRO_NONE)
+        if path == "bf16":
+            return linear_partials(x, lin.weight)
+        return linear_partials(x, lin.weight_fp8, weight_scale_inv=lin.weight_scale_inv, quantize_x=qx,
+                               x_amax=x_amax)
+    return lin.run(x, lin.bias, x_amax=x_amax)
+
+
+def _norm_into(norm: RMSNorm, x, res: torch.Tensor | None, lin: LinearBase, rows: int):
+    """RMSNorm (+ residual add) whose output feeds ``lin``.  When ``lin``
+    quantises its activation to FP8 on the small-M kernel, the norm does that
+    quantisation once and hands over the e4m3fn codes and the row amax instead
+    of the bf16 rows (the linear's workgroups then skip quantising).  Returns
+    (activation, residual, row amax or None)."""
+    qx = lin.x_quant_mode(rows)
+    if not qx:
+        if res is None:
+            return norm(x), x, None
+        h, res = norm(x, res)
+        return h, res, None
+    dev = res.device if res is not None else x.device
+    am = torch.empty((rows, 1), device=dev, dtype=torch.float32)
+    q = torch.empty((rows, lin.input_size), device=dev, dtype=torch.float8_e4m3fn)
+    quant = dict(amax_out=am, q_out=q, q_mode=qx, bf16_out=False)
+    if res is None:
+        norm(x, **quant)
+        return q, x, am
+    _, res = norm(x, res, **quant)
+    return q, res, am
+
+
+def _linear_from_norm(lin: LinearBase, h: torch.Tensor, am: torch.Tensor | None, *, epilogue: int = EPI_NONE,
+                      amax_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The linear after _norm_into: on the pre-quantised codes when it handed
+    them over, else on the bf16 rows."""
+    if am is not None:
+        return lin.run_quantized(h, am, epilogue=epilogue, amax_out=amax_out)
+    return lin.run(h, lin.bias, epilogue=epilogue, amax_out=amax_out)
 
 
 def _defer_splitk_enabled() -> bool:
@@ -244,18 +266,22 @@ class LlamaModel(nn.Module):
         every workgroup would re-read and re-normalise the whole activation,
         which costs more at M <= 16 than the launch it saves.)"""
         x = self.embed_tokens(input_ids)
+        rows, dev = input_ids.shape[0], x.device
         res = None
         for layer in self.layers:
             attn, mlp = layer.self_attn, layer.mlp
-            if res is None:
-                h, res = layer.input_layernorm(x), x
-            else:
-                h, res = layer.input_layernorm(x, res)
-            qkv = _fused_linear(attn.qkv_proj, h, PRO_NONE)
+            # an FP8 linear's activation statistics come from its producer: the
+            # RMSNorms quantise qkv's / gate_up's input themselves, gate_up hands
+            # down_proj its per-strip output amax
+            h, res, am = _norm_into(layer.input_layernorm, x, res, attn.qkv_proj, rows)
+            qkv = _linear_from_norm(attn.qkv_proj, h, am)
             o = _deferred_linear(attn.o_proj, attn.attend(positions, qkv))
-            h, res = layer.post_attention_layernorm(o, res)
-            act = _fused_linear(mlp.gate_up_proj, h, PRO_NONE, epilogue=EPI_SILU_MUL)
-            x = _deferred_linear(mlp.down_proj, act)
+            h, res, am = _norm_into(layer.post_attention_layernorm, o, res, mlp.gate_up_proj, rows)
+            am_act = None
+            if mlp.down_proj.wants_x_amax(rows) and mlp.gate_up_proj.small_m_fused(rows, EPI_SILU_MUL):
+                am_act = torch.empty((rows, mlp.gate_up_proj.output_size // 32), device=dev, dtype=torch.float32)
+            act = _linear_from_norm(mlp.gate_up_proj, h, am, epilogue=EPI_SILU_MUL, amax_out=am_act)
+            x = _deferred_linear(mlp.down_proj, act, x_amax=am_act)
         h, _ = self.norm(x, res)
         if greedy_out is not None:
             lm_head.greedy_into(h, greedy_out)

@@ -34,7 +34,9 @@ extern "C" {
 #endif
 
 /* ABI version of this header (2: per-kv-head FP8 scale tables on the pack,
- * append and attention entry points). */
+ * append and attention entry points; 3: the paged compact-KV entry points, the
+ * FP8 GEMM, and the producer-side activation amax / FP8 split partials on
+ * fdms_linear_small_m and the RMSNorm entry points). */
 int fdms_abi_version(void);
 
 /* Plain 16-byte-vector copy used to calibrate HBM byte counters and the copy
@@ -270,10 +272,18 @@ int fdms_mfma_probe(const void* a, const void* b, float* c, void* stream);
 /* Residual-add + RMSNorm, bf16 (fastdms/layers/layernorm.py:16-40).  Row r of the
  * input is at in + (r/heads)*in_stride + (r%heads)*in_head_stride (heads > 1
  * normalises each head of a strided [tokens, heads, D] view, Qwen3 QK-norm,
- * qwen3.py:92-94). */
+ * qwen3.py:92-94).  amax_out (optional, fp32 [rows]) = max |out[r, :]| (NaN if
+ * the row holds a NaN): the row statistic of the consuming FP8 linear's
+ * activation quantisation (fdms_linear_small_m's x_amax), so that linear
+ * skips its own pass over x.  q_out (optional, with amax_out; e4m3fn [rows,
+ * q_stride], 8-byte aligned) = that quantisation done here once:
+ * e4m3fn(out * s), s = 448 / amax (1 if amax is 0 or NaN; q_mode 1 divides,
+ * 2 rounds as reciprocal(amax) * 448), RNE with saturation
+ * (linear.py:514-523, 683-694); the linear then reads the codes (x_dtype
+ * FP8).  out may be null when q_out is given. */
 int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int heads, const void* residual,
                  const void* weight, void* out, int64_t out_stride, void* residual_out, int64_t rows, int hidden,
-                 float eps, void* stream);
+                 float eps, float* amax_out, void* q_out, int64_t q_stride, int q_mode, void* stream);
 
 /* out = silu(x[:, :F]) * x[:, F:], bf16 (fastdms/layers/activation.py:8-11). */
 int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
@@ -282,11 +292,17 @@ int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
  * partials[s * split_stride + r * hidden + c]) in split order: the merge of a
  * split-K fdms_linear_small_m (epilogue 3) done by its consumer, as the
  * reference's RMSNorm(down_proj / o_proj output, residual) sequence
- * (layernorm.py:19-40; llama.py:248-266).  partials 32-byte aligned,
- * split_stride a multiple of 8; residual / residual_out contiguous rows. */
+ * (layernorm.py:19-40; llama.py:248-266).  For an FP8 linear, row_scale [rows]
+ * (its row_scale_out) and col_scale [hidden] (the weight's scale_inv) make the
+ * input bf16((sum * row_scale[r]) * col_scale[c]), the linear's own
+ * finalisation (either may be null: factor 1).  amax_out, q_out as
+ * fdms_rmsnorm.
+ * partials and col_scale 32-byte aligned, split_stride a multiple of 8;
+ * residual / residual_out contiguous rows. */
 int fdms_rmsnorm_partials(const float* partials, int k_splits, int64_t split_stride, const void* residual,
                           const void* weight, void* out, int64_t out_stride, void* residual_out, int64_t rows,
-                          int hidden, float eps, void* stream);
+                          int hidden, float eps, const float* row_scale, const float* col_scale, float* amax_out,
+                          void* q_out, int64_t q_stride, int q_mode, void* stream);
 
 /* Row argmax, ties to the lowest index (fastdms/layers/embed_head.py:142, 160,
  * and the torch argmax of ParallelLMHead.greedy_token_ids, 491-543). */
@@ -315,10 +331,20 @@ int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int6
  * w_dtype bf16.  prologue 1 = RMSNorm of x (+ residual, fp32 sum; the bf16 sum
  * goes to residual_out, written by one workgroup; layernorm.py:19-40).
  * epilogue 1 = W is [gate; up] (n rows), the output has n/2 columns
- * bf16(silu(gate) * up) (activation.py:8-11).  epilogue 3 (bf16 weights, no
- * bias, no prologue) = no merge: split s writes its fp32 partial sums to
- * workspace[(s * m + row) * n + col] and y is not written; the consumer
- * (fdms_rmsnorm_partials) adds the splits in order.  k_splits > 1 splits K over
+ * bf16(silu(gate) * up) (activation.py:8-11).  epilogue 3 (no bias, no
+ * prologue) = no merge: split s writes its fp32 partial sums (before the FP8
+ * scales) to workspace[(s * m + row) * n + col] and y is not written; the
+ * consumer (fdms_rmsnorm_partials) adds the splits in order and applies
+ * row_scale_out[row] (written here when given: 1/x_s, or 1 without activation
+ * quantisation) and the weight's scale_inv.  x_amax (optional, prologue 0 with
+ * quantize_x): row r's amax is the max of x_amax[r * x_amax_stride + p], p <
+ * x_amax_n, supplied by x's producer (fdms_rmsnorm's amax_out, or this
+ * function's amax_out) in place of the pass over x; the result is the same
+ * (the amax must propagate NaN, as torch's does).  x_dtype FP8 (FP8 weights,
+ * quantize_x 1 / 2, x_amax required): x holds the e4m3fn codes of the
+ * quantised activation (fdms_rmsnorm's q_out, same quantize_x form), row
+ * stride x_stride bytes.  amax_out (optional, epilogues 0 / 1) = per-strip max
+ * |y|: amax_out[row * (n_out/16) + strip].  k_splits > 1 splits K over
  * workgroups: workspace holds (n_out/16) * k_splits * 256 floats (x2 for
  * epilogue 1) and counters n_out/16 ints, zero before the first call and left
  * zero.  k / k_splits a multiple of 256, n_out of 16, 16-byte aligned rows; y
@@ -327,7 +353,9 @@ int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const voi
                         int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int prologue,
                         const void* norm_weight, float eps, const void* residual, int64_t res_stride,
                         void* residual_out, int64_t res_out_stride, int quantize_x, int epilogue, int k_splits,
-                        float* workspace, int* counters, void* y, int64_t y_stride, void* stream);
+                        float* workspace, int* counters, void* y, int64_t y_stride, const float* x_amax,
+                        int x_amax_n, int64_t x_amax_stride, float* amax_out, float* row_scale_out, int x_dtype,
+                        void* stream);
 
 /* C7 — greedy LM head: token[m] = argmax_n a[m,:] . W[n,:] for m <= 16 rows,
  * ties to the lowest index, NaN first (torch.argmax order).  Replaces

@@ -733,8 +733,22 @@ class Emulator:
         self.view(out, torch.int64, (rows,), (1,), "out").copy_(first)
         return 0
 
+    def _store_row_amax(self, amax_out, out_rows, q_out=0, q_stride=0, q_mode=0):
+        """amax_out[r] = max |out[r]|; q_out = e4m3fn(out * 448/amax) (oracle/linear.py's row quantisation)."""
+        from oracle import linear as olin
+        rows, hidden = out_rows.shape
+        if q_out and (not amax_out or q_mode not in (1, 2) or q_stride < hidden):
+            raise OutOfBounds(f"{self.name}: bad q_out arguments")
+        if amax_out:
+            am = out_rows.float().abs().amax(dim=1)
+            self.view(amax_out, torch.float32, (rows,), (1,), "amax_out").copy_(am)
+            if q_out:
+                xs = olin.amax_to_scale(am.numpy(), torch_form=q_mode == 2)
+                codes = numerics.e4m3fn_encode((out_rows.float().numpy() * xs[:, None]).astype(np.float32))
+                self.view(q_out, torch.uint8, (rows, hidden), (q_stride, 1), "q_out").copy_(torch.from_numpy(codes))
+
     def rmsnorm(self, x, in_stride, in_head_stride, heads, residual, weight, out, out_stride, residual_out, rows,
-                hidden, eps, stream):
+                hidden, eps, amax_out, q_out, q_stride, q_mode, stream):
         if rows < 0 or hidden <= 0 or hidden % 8 or hidden > 8192 or heads <= 0:
             return 1
         if rows == 0:
@@ -750,11 +764,16 @@ class Emulator:
         w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
         inv = torch.rsqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
         xn = (f * inv).to(torch.bfloat16).float()
-        self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
+        o = (xn * w).to(torch.bfloat16)
+        if out:
+            self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_(o)
+        elif not q_out:
+            return 1
+        self._store_row_amax(amax_out, o, q_out, q_stride, q_mode)
         return 0
 
     def rmsnorm_partials(self, partials, k_splits, split_stride, residual, weight, out, out_stride, residual_out,
-                         rows, hidden, eps, stream):
+                         rows, hidden, eps, row_scale, col_scale, amax_out, q_out, q_stride, q_mode, stream):
         if rows < 0 or hidden <= 0 or hidden % 8 or hidden > 8192 or k_splits < 1 or split_stride < rows * hidden:
             return 1
         if rows == 0:
@@ -763,6 +782,10 @@ class Emulator:
         acc = torch.zeros((rows, hidden), dtype=torch.float32)
         for s in range(k_splits):
             acc = acc + part[s]
+        if row_scale:
+            acc = acc * self.view(row_scale, torch.float32, (rows,), (1,), "row_scale")[:, None]
+        if col_scale:
+            acc = acc * self.view(col_scale, torch.float32, (hidden,), (1,), "col_scale")[None, :]
         f = acc.to(torch.bfloat16).float()
         if residual:
             f = f + self.view(residual, torch.bfloat16, (rows, hidden), (hidden, 1), "residual").float()
@@ -772,7 +795,12 @@ class Emulator:
         w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
         inv = torch.rsqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
         xn = (f * inv).to(torch.bfloat16).float()
-        self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_((xn * w).to(torch.bfloat16))
+        o = (xn * w).to(torch.bfloat16)
+        if out:
+            self.view(out, torch.bfloat16, (rows, hidden), (out_stride, 1), "out").copy_(o)
+        elif not q_out:
+            return 1
+        self._store_row_amax(amax_out, o, q_out, q_stride, q_mode)
         return 0
 
     def silu_mul(self, x, out, rows, f, stream):
@@ -813,22 +841,63 @@ class Emulator:
         return 0
 
     def linear_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, prologue, norm_w, eps, res, res_s,
-                       res_out, ro_s, qx, epilogue, k_splits, ws, counters, y, y_s, stream):
-        """Same expressions as oracle/model.py (rmsnorm, mlp, linear) and oracle/linear.py."""
+                       res_out, ro_s, qx, epilogue, k_splits, ws, counters, y, y_s, x_amax, x_amax_n, x_amax_s,
+                       amax_out, row_scale_out, x_dtype, stream):
+        """Same expressions as oracle/model.py (rmsnorm, mlp, linear) and oracle/linear.py.
+        A producer's x_amax must equal x's own row amax (the kernel's contract);
+        x_dtype FP8: x holds the e4m3fn codes its producer quantised with that amax."""
         from oracle import linear as olin
         if m == 0 or n == 0:
             return 0
         n_out = n // 2 if epilogue == 1 else n
         if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1):
             return 1
+        if x_amax and (prologue or not qx or x_amax_n < 1 or (m > 1 and x_amax_s < x_amax_n)):
+            return 1
+        if (amax_out and epilogue > 1) or (row_scale_out and epilogue != 3):
+            return 1
+        xq_in = x_dtype == DT_FP8
+        if x_dtype not in (DT_BF16, DT_FP8) or (xq_in and (w_dtype != DT_FP8 or not qx or not x_amax)):
+            return 1
+        am = None
+        if x_amax:
+            self.calls.append("fdms_linear_small_m:x_amax" + (":fp8_x" if xq_in else ""))
+            am = self.view(x_amax, torch.float32, (m, x_amax_n), (x_amax_s, 1), "x_amax").amax(dim=1)
+            if not xq_in:
+                want = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float().abs().amax(dim=1)
+                if not torch.equal(am, want):
+                    raise AssertionError(f"{self.name}: x_amax {am.tolist()} is not x's row amax {want.tolist()}")
+
+        def quantised_x():
+            """(activation values after the FP8 row quantisation, 1 / x_s) as float64."""
+            if xq_in:
+                codes = self.view(x, torch.uint8, (m, k), (x_s, 1), "x").numpy()
+                xs = olin.amax_to_scale(am.numpy(), torch_form=qx == 2)
+                return numerics.e4m3fn_decode(codes).astype(np.float64), (np.float32(1.0) / xs).astype(np.float64)
+            xq, xs = olin.quantize_rows_fp8(self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float().numpy(),
+                                            torch_form=qx == 2)
+            return numerics.e4m3fn_decode(xq).astype(np.float64), (np.float32(1.0) / xs).astype(np.float64)
+
         if epilogue == 3:  # split partials: all of the fp32 sum in split 0, zeros in the others
-            if w_dtype != DT_BF16 or prologue or qx or bias or not ws:
+            if prologue or bias or not ws:
                 return 1
             part = self.view(ws, torch.float32, (k_splits, m, n), (m * n, n, 1), "partials")
-            xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
-            wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float()
+            if w_dtype == DT_FP8:
+                wv = numerics.e4m3fn_decode(self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy())
+            else:
+                wv = self.view(w, torch.bfloat16, (n, k), (w_s, 1), "weight").float().numpy()
+            if qx:
+                xv, inv = quantised_x()
+            else:
+                xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float().numpy()
+                inv = np.ones(m)
             part.zero_()
-            part[0].copy_(xv @ wv.T)
+            part[0].copy_(torch.from_numpy((xv.astype(np.float64) @ wv.astype(np.float64).T).astype(np.float32)))
+            if row_scale_out:
+                self.view(row_scale_out, torch.float32, (m,), (1,), "row_scale_out").copy_(
+                    torch.from_numpy(inv.astype(np.float32)))
+            if w_dtype == DT_FP8:
+                self.calls.append("fdms_linear_small_m:fp8_partials")
             return 0
         if k_splits > 1:
             strips = n_out // 16
@@ -836,8 +905,11 @@ class Emulator:
             cnt = self.view(counters, torch.int32, (strips,), (1,), "counters")
             if bool((cnt != 0).any()):
                 raise OutOfBounds(f"{self.name}: split-K counters are not zero before the launch")
-        xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
-        if prologue == 1:
+        bv = self.view(bias, torch.bfloat16, (n,), (1,), "bias").float() if bias else None
+        if xq_in:
+            a = None
+        elif prologue == 1:
+            xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
             f = xv + (self.view(res, torch.bfloat16, (m, k), (res_s, 1), "residual").float() if res else 0.0)
             if res_out:
                 self.view(res_out, torch.bfloat16, (m, k), (ro_s, 1), "residual_out").copy_(f.to(torch.bfloat16))
@@ -846,12 +918,16 @@ class Emulator:
             nw = self.view(norm_w, torch.bfloat16, (k,), (1,), "norm_weight").float()
             a = (a * nw).to(torch.bfloat16).float()
         else:
-            a = xv
-        bv = self.view(bias, torch.bfloat16, (n,), (1,), "bias").float() if bias else None
+            a = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
         if w_dtype == DT_FP8:
             w8 = self.view(w, torch.uint8, (n, k), (w_s, 1), "weight").numpy()
             si = self.view(wsi, torch.float32, (n,), (1,), "scale_inv").numpy()
-            acc = olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx), torch_form=qx == 2)
+            if xq_in:
+                xv, inv = quantised_x()
+                acc = (xv @ numerics.e4m3fn_decode(w8).astype(np.float64).T) * inv[:, None] * \
+                    si.astype(np.float64)[None, :]
+            else:
+                acc = olin.fp8_linear(a.numpy(), w8.T, si, quantize_x=bool(qx), torch_form=qx == 2)
             out = torch.from_numpy(acc.astype(np.float32)).to(torch.bfloat16).float()
             if bv is not None:
                 out = (out + bv).to(torch.bfloat16).float()
@@ -864,7 +940,12 @@ class Emulator:
         if epilogue == 1:  # gate_up -> SiluAndMul, the oracle model's mlp expression
             g, u = out[:, :n_out], out[:, n_out:]
             out = torch.nn.functional.silu(g) * u
-        self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(out.to(torch.bfloat16))
+        yb = out.to(torch.bfloat16)
+        self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(yb)
+        if amax_out:
+            strips = n_out // 16
+            self.view(amax_out, torch.float32, (m, strips), (strips, 1), "amax_out").copy_(
+                yb.float().abs().reshape(m, strips, 16).amax(dim=2))
         return 0
 
     def linear_argmax_small_m(self, x, x_s, m, k, w, w_dtype, w_s, wsi, bias, n, qx, bf16_scores, k_splits, ws,

@@ -44,16 +44,33 @@ def test_engine_fused_greedy_head_matches_oracle_tokens(model, lens, gen):
     _run(model, lens, gen, fused_head=True)
 
 
-def _run(model, lens, gen, fused_head, layout="paged"):
-    from oracle.model import OracleModel, weights_from_model
+FP8_ENV = {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "0"}
+
+
+def test_fp8_decode_glue_matches_the_quantised_oracle(monkeypatch):
+    """FP8 weights on every linear (the reference's FASTDMS_FP8_WEIGHTS=1 with
+    its attention-full default): prefill rows on the FP8 GEMM, decode rows on
+    the small-M kernel, which takes each activation's row amax from its
+    producer (the RMSNorms, which also quantise qkv's and gate_up's input;
+    gate_up for down_proj) and leaves o_proj's and down_proj's split merge and
+    FP8 scaling to the next RMSNorm.  Logits follow
+    the oracle holding the same FP8 weights and routes, and the emulator checks
+    that every amax handed to a linear is its activation's own."""
+    for k, v in FP8_ENV.items():
+        monkeypatch.setenv(k, v)
+    calls = _run("tiny-llama", [300, 517, 64], 8, fused_head=False, quant=True)
+    for tag in ("x_amax", "x_amax:fp8_x", "fp8_partials"):
+        assert "fdms_linear_small_m:" + tag in calls, tag
+
+
+def _run(model, lens, gen, fused_head, layout="paged", quant=False):
+    from engine_oracle import oracle_for
     with cpu_engine() as emu:
         from fastdms_amd import LLM, SamplingParams
         llm = LLM(model, max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384, enforce_eager=True,
                   fused_greedy_head=fused_head, compact_kv_layout=layout, **DMS)
         runner = llm.model_runner
-        orc = OracleModel(weights_from_model(runner.model), llm.config.hf_config, window_size=32, alpha_scale=10.0,
-                          alpha_offset=5.0, capacity_tokens=runner.compact_kv_manager.capacity_tokens,
-                          max_model_len=llm.config.max_model_len)
+        orc = oracle_for(runner, llm.config, quant=quant, dms=DMS)
         rng = np.random.default_rng(3)
         sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
         seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in lens]
@@ -88,6 +105,7 @@ def _run(model, lens, gen, fused_head, layout="paged"):
                 check_page_invariants(mgr)
         assert ("fdms_paged_expiry" if layout == "paged" else "fdms_dms_expiry") in emu.calls
         llm.exit()
+        return list(emu.calls)
 
 
 @pytest.mark.parametrize("lens,gen", [([300], 14), ([300, 64, 517], 10)])

@@ -35,6 +35,7 @@ import numpy as np
 import pytest
 import torch
 
+from engine_oracle import oracle_for
 from oracle_sync import sync_oracle_state
 
 from helpers import require_gpu
@@ -51,55 +52,8 @@ def _model_config(name: str, layers: int | None):
     return replace(cfg, num_hidden_layers=layers) if layers else replace(cfg)
 
 
-def _int4_weights(module):
-    """Dequantised INT4 shadow of a linear: bf16((q - 8) * scale + zero)."""
-    packed = module.weight_int4.cpu()
-    q = torch.stack([packed & 0xF, packed >> 4], dim=-1).reshape(packed.shape[0], -1).float()
-    g = module._int4_group_size
-    s = module.weight_int4_scale.float().cpu().repeat_interleave(g, dim=1)
-    z = module.weight_int4_zero.float().cpu().repeat_interleave(g, dim=1)
-    return ((q - 8.0) * s + z).to(torch.bfloat16).float()
-
-
 def _oracle_for(runner, config, *, quant: bool):
-    from oracle.model import OracleModel, weights_from_model
-    from fastdms_amd.layers import quant_env as qe
-    model = runner.model
-    kw = {}
-    if quant:
-        fp8, int4 = {}, {}
-        for name, mod in model.named_modules():
-            if getattr(mod, "_fp8_weight_enabled", False) and name != "lm_head":
-                fp8[name] = (mod.weight_fp8.t().contiguous().view(torch.uint8).cpu().numpy(),
-                             mod.weight_scale_inv.float().cpu().numpy())
-                if getattr(mod, "_int4_enabled", False):
-                    int4[name] = _int4_weights(mod)
-        emb = model.model.embed_tokens
-        if emb._fp8_embedding_enabled:
-            kw["embed_fp8"] = (emb._fp8_embedding_weight.view(torch.uint8).cpu().numpy(),
-                               emb._fp8_embedding_scale_inv.float().cpu().numpy().reshape(-1))
-        mods = dict(model.named_modules())
-        from fastdms_amd.layers.linear import QX_NONE, QX_TORCH
-
-        def route(name, rows):
-            # the module's own dispatch decision (linear.py:855-926, pinned on
-            # the CPU by tests/test_linear_dispatch.py)
-            mod = mods.get(name)
-            if mod is None or not getattr(mod, "_fp8_weight_enabled", False):
-                return "bf16"
-            path, qx = mod.route(rows)
-            if path == "fp8":
-                assert qx != QX_NONE, "unquantised FP8 activations are not modelled by the oracle"
-                return "fp8_torch" if qx == QX_TORCH else "fp8"
-            assert path in ("int4", "bf16"), path
-            return path
-
-        kw.update(fp8_linear=fp8, int4_linear=int4, route=route)
-    weights = weights_from_model(model)
-    return OracleModel(weights, config.hf_config, window_size=DMS["dms_window_size"],
-                       alpha_scale=DMS["dms_alpha_scale"], alpha_offset=DMS["dms_alpha_offset"],
-                       capacity_tokens=runner.compact_kv_manager.capacity_tokens,
-                       max_model_len=config.max_model_len, **kw)
+    return oracle_for(runner, config, quant=quant, dms=DMS)
 
 
 SUCCESSOR_MARGIN = 0.3
@@ -108,6 +62,16 @@ QUANT_ENV = {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FAS
              "FASTDMS_INT4_ROW1_WEIGHTS": "1", "FASTDMS_INT4_ROW1_SCOPE": "all",
              "FASTDMS_INT4_ROW1_GROUP_SIZE": "128", "FASTDMS_INT4_ROW1_QUANT_MODE": "symmetric",
              "FASTDMS_INT4_ROW1_MAX_ROWS": "8"}
+# FP8 weights on every linear (the reference's FASTDMS_FP8_WEIGHTS=1 with its
+# attention-full default): decode rows on the small-M FP8 kernel with dynamic
+# activation quantisation, prefill rows on the FP8 GEMM
+FP8_ENV = {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "0"}
+QUANT_ENVS = {"w4a16": QUANT_ENV, "fp8": FP8_ENV}
+
+
+def _set_quant_env(monkeypatch, quant):
+    for k, v in QUANT_ENVS.get(quant, {}).items():
+        monkeypatch.setenv(k, v)
 
 
 def _run(model_cfg, lens, *, seed=0, quant=False, layout="paged", with_oracle=True):
@@ -118,7 +82,7 @@ def _run(model_cfg, lens, *, seed=0, quant=False, layout="paged", with_oracle=Tr
               max_num_batched_tokens=sum(lens), seed=seed, compact_kv_layout=layout, **DMS)
     sp = SamplingParams(temperature=0.0, max_tokens=GEN, ignore_eos=True)
     got = [o["token_ids"] for o in llm.generate(prompts, sp)]
-    orc = _oracle_for(llm.model_runner, llm.config, quant=quant) if with_oracle else None
+    orc = _oracle_for(llm.model_runner, llm.config, quant=bool(quant)) if with_oracle else None
     llm.exit()
     del llm
     torch.cuda.synchronize()
@@ -129,9 +93,12 @@ def _run(model_cfg, lens, *, seed=0, quant=False, layout="paged", with_oracle=Tr
 
     ids = list(range(len(lens)))
     toks = orc.prefill([(i, p, GEN) for i, p in zip(ids, prompts)])
+    print("oracle prefill done", flush=True)
     want = [[t] for t in toks]
     gaps = [[_top2_gap(orc.last_logits[i])] for i in ids]
     for step in range(GEN - 1):
+        if step % 8 == 7:
+            print(f"oracle decode step {step + 1}", flush=True)
         pos = [len(p) + step for p in prompts]
         toks = orc.decode(ids, toks, pos)
         for i, t in enumerate(toks):
@@ -175,7 +142,7 @@ def _follow(model_cfg, lens, *, seed=0, quant=False, steps=GEN - 1):
     llm = LLM(model_cfg, max_model_len=max(lens) + GEN + 8, max_num_seqs=len(lens),
               max_num_batched_tokens=sum(lens), seed=seed, fused_greedy_head=False, **DMS)
     runner = llm.model_runner
-    orc = _oracle_for(runner, llm.config, quant=quant)
+    orc = _oracle_for(runner, llm.config, quant=bool(quant))
     sp = SamplingParams(temperature=0.0, max_tokens=steps + 1, ignore_eos=True)
     seqs = [llm.add_request(p, sp) for p in prompts]
     llm.step()  # prefill
@@ -221,7 +188,8 @@ CASES = {
     "l1b_c1": (L1B, [2048], False),
     "l1b_c8": (L1B, np.random.default_rng(2).integers(300, 900, 8).tolist(), False),
     "q8b4_c8": (Q8B4, np.random.default_rng(3).integers(300, 600, 8).tolist(), False),
-    "l1b_w4a16_c4": (L1B, np.random.default_rng(4).integers(300, 700, 4).tolist(), True),
+    "l1b_w4a16_c4": (L1B, np.random.default_rng(4).integers(300, 700, 4).tolist(), "w4a16"),
+    "l1b4_fp8_c4": (("llama-3.2-1b", 4), np.random.default_rng(5).integers(300, 600, 4).tolist(), "fp8"),
 }
 
 
@@ -238,6 +206,8 @@ CASES = {
 # activation that upstream rounding moved across an e4m3 rounding boundary
 # changes by a whole FP8 step (6-12 %), so its prefill logits get 10 % (2
 # layers) / 30 % (16 layers); its decode steps (INT4 rows) keep 1 % / 5 %.
+# With FP8 weights everywhere the decode rows quantise their activations too
+# and get the prefill's tolerance.
 LOGIT_CASES = {
     "l1b_c1": (CASES["l1b_c1"], 5e-2, None),
     "l1b_c8": (CASES["l1b_c8"], 5e-2, None),
@@ -246,6 +216,7 @@ LOGIT_CASES = {
     "l1b2_c8": ((("llama-3.2-1b", 2),) + CASES["l1b_c8"][1:], 1e-2, None),
     "q8b2_c8": ((("qwen3-8b", 2),) + CASES["q8b4_c8"][1:], 1e-2, None),
     "l1b2_w4a16_c4": ((("llama-3.2-1b", 2),) + CASES["l1b_w4a16_c4"][1:], 1e-2, 0.1),
+    "l1b2_fp8_c8": ((("llama-3.2-1b", 2),) + CASES["l1b_c8"][1:2] + ("fp8",), 0.1, 0.1),
 }
 
 
@@ -257,9 +228,7 @@ def test_logits_follow_the_oracle_at_baseline_shapes(monkeypatch, case):
     require_gpu()
     ((name, layers), lens, quant), tol, prefill_tol = LOGIT_CASES[case]
     monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
-    if quant:
-        for k, v in QUANT_ENV.items():
-            monkeypatch.setenv(k, v)
+    _set_quant_env(monkeypatch, quant)
     _check_logits(_follow(_model_config(name, layers), lens, seed=7, quant=quant), tol, prefill_tol)
 
 
@@ -270,9 +239,7 @@ def test_first_32_greedy_tokens_match_the_oracle_at_baseline_shapes(monkeypatch,
     sequence are the oracle's."""
     require_gpu()
     (name, layers), lens, quant = CASES[case]
-    if quant:
-        for k, v in QUANT_ENV.items():
-            monkeypatch.setenv(k, v)
+    _set_quant_env(monkeypatch, quant)
     cfg = replace(_model_config(name, layers), successor_margin=SUCCESSOR_MARGIN)
     got, want, gaps = _run(cfg, lens, seed=1, quant=quant)
     _check(got, want, gaps, case)

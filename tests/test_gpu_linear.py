@@ -191,6 +191,178 @@ def test_linear_small_m_fp8_matches_oracle(quantize_x, m, n, k):
     _close_bf16(y, want, "fp8", ulps=2.0, atol=1e-3 + 2.0 ** -7 * pre.abs())
 
 
+def _chunk_amax(x, cuts, pad=0):
+    """x's row amax as partial maxima over the column ranges between ``cuts``
+    (fp32 [rows, parts], row stride parts + pad), as a producer hands them on."""
+    edges = [0] + list(cuts) + [x.shape[1]]
+    parts = [x[:, a:b].float().abs().amax(dim=1) for a, b in zip(edges[:-1], edges[1:])]
+    buf = torch.zeros((x.shape[0], len(parts) + pad), device=x.device, dtype=torch.float32)
+    buf[:, :len(parts)] = torch.stack(parts, dim=1)
+    return buf[:, :len(parts)]
+
+
+@pytest.mark.parametrize("quantize_x", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(1, 3072, 2048), (8, 2048, 8192), (8, 16384, 2048), (5, 512, 256),
+                                   (16, 1024, 4096)])
+def test_fp8_producer_amax_gives_the_same_result(quantize_x, m, n, k):
+    """The activation's row amax handed in by its producer (one value per row,
+    or partial maxima over column ranges, strided rows) replaces the kernel's
+    pass over x without changing a bit of y; the same for split partials."""
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_partials, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m + n + k + quantize_x)
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    x[0, k // 3] = 40.0   # a dominant column: the amax must come from the right part
+    w8, sinv = quantize_fp8_rows(w)
+    want = linear_small_m(x, w8, weight_scale_inv=sinv, quantize_x=quantize_x)
+    for am in (x.float().abs().amax(dim=1, keepdim=True), _chunk_amax(x, [k // 4, k // 2, k // 2 + 16], pad=3),
+               _chunk_amax(x, list(range(8, k, 8)))):
+        got = linear_small_m(x, w8, weight_scale_inv=sinv, quantize_x=quantize_x, x_amax=am)
+        assert torch.equal(got, want), f"x_amax with {am.shape[1]} parts"
+    # the activation quantised by its producer (codes + row amax): same y
+    xq, _ = quantize_fp8_rows(x, torch_form=quantize_x == 2)
+    got = linear_small_m(xq, w8, weight_scale_inv=sinv, quantize_x=quantize_x, x_amax=_chunk_amax(x, [k // 2]))
+    assert torch.equal(got, want), "pre-quantised activation"
+    p_want = linear_partials(x, w8, weight_scale_inv=sinv, quantize_x=quantize_x)
+    p_want = (p_want.data.clone(), p_want.row_scale.clone())
+    p_got = linear_partials(x, w8, weight_scale_inv=sinv, quantize_x=quantize_x,
+                            x_amax=_chunk_amax(x, [k // 2]))
+    torch.cuda.synchronize()
+    assert torch.equal(p_got.data, p_want[0]) and torch.equal(p_got.row_scale, p_want[1])
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("epilogue", [0, 1])
+@pytest.mark.parametrize("m,n,k", [(8, 16384, 2048), (3, 512, 256), (16, 2048, 8192)])
+def test_strip_amax_output(fp8, epilogue, m, n, k):
+    """amax_out[row, strip] = max |y[row, 16 strip : 16 strip + 16]| of the
+    written output (gate_up's SiLU*up or a plain linear), split-K included."""
+    require_gpu()
+    from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m * 7 + n + epilogue + int(fp8))
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    n_out = n // 2 if epilogue == EPI_SILU_MUL else n
+    kw = {}
+    if fp8:
+        w, kw["weight_scale_inv"] = quantize_fp8_rows(w)
+    am = torch.full((m, n_out // 16), -1.0, device="cuda", dtype=torch.float32)
+    y = linear_small_m(x, w, epilogue=epilogue, amax_out=am, **kw)
+    want = y.float().abs().reshape(m, n_out // 16, 16).amax(dim=2)
+    torch.cuda.synchronize()
+    assert torch.equal(am, want)
+    assert torch.equal(linear_small_m(x, w, epilogue=epilogue, **kw), y), "amax_out changed y"
+
+
+@pytest.mark.parametrize("quantize_x", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k,splits", [(8, 2048, 8192, 2), (8, 2048, 2048, 2), (3, 512, 4096, 4),
+                                          (16, 256, 2048, 1), (1, 2048, 8192, 8)])
+def test_fp8_partials_through_the_rmsnorm_equal_the_merged_linear(quantize_x, m, n, k, splits):
+    """FP8 weights on epilogue 3: the consuming RMSNorm's sum of the partials
+    times the row scale (1/x_s) and the weight's scale_inv is the merged
+    linear's output bit for bit (same split count), and its residual sum,
+    output and output amax match the RMSNorm of that tensor bit for bit."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    from fastdms_amd.layers.linear import linear_partials, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m * 13 + splits + quantize_x)
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    w8, sinv = quantize_fp8_rows(w)
+    merged = linear_small_m(x, w8, weight_scale_inv=sinv, quantize_x=quantize_x, k_splits=splits)
+    part = linear_partials(x, w8, splits, weight_scale_inv=sinv, quantize_x=quantize_x)
+    nw = (1.0 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16).cuda()
+    res = _bf16((m, n), g).cuda()
+    am_want = torch.empty(m, device="cuda", dtype=torch.float32)
+    am_got = torch.empty(m, device="cuda", dtype=torch.float32)
+    want_h, want_res = rms_norm(merged, nw, 1e-5, residual=res, amax_out=am_want)
+    got_h, got_res = rms_norm(part, nw, 1e-5, residual=res, amax_out=am_got)
+    torch.cuda.synchronize()
+    assert torch.equal(got_res, want_res) and torch.equal(got_h, want_h)
+    assert torch.equal(am_got, am_want) and torch.equal(am_want, want_h.float().abs().amax(dim=1))
+    assert torch.equal(rms_norm(part, nw, 1e-5), rms_norm(merged, nw, 1e-5))
+
+
+@pytest.mark.parametrize("quantize_x", [1, 2])
+def test_fp8_rows_with_nan_or_inf(quantize_x):
+    """A row holding a NaN or an inf: its amax is NaN / inf (NaN propagates
+    through every amax), the scale follows the reference's where(amax > 0)
+    rule and the row's outputs are NaN, as the oracle's; the other rows are
+    unchanged.  Same through the statistics pass, a producer's amax and the
+    RMSNorm's quantised codes."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    from fastdms_amd.layers.linear import linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(40 + quantize_x)
+    m, n, k = 6, 512, 2048
+    x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
+    x[1, 100] = float("nan")
+    x[3, 7] = float("inf")
+    x[4, 9] = -float("inf")
+    w8, sinv = quantize_fp8_rows(w.cuda())
+    xc = x.cuda()
+    y = linear_small_m(xc, w8, weight_scale_inv=sinv, quantize_x=quantize_x).float().cpu()
+    w8_t, sinv_ref = olin.quantize_weight_to_fp8(w.float().numpy())
+    ref = olin.fp8_linear(x.float().numpy(), w8_t, sinv_ref, quantize_x=True, torch_form=quantize_x == 2)
+    bad = [1, 3, 4]
+    assert np.isnan(ref[bad]).all() and torch.isnan(y[bad]).all()
+    good = [0, 2, 5]
+    clean = linear_small_m(xc[good].contiguous(), w8, weight_scale_inv=sinv, quantize_x=quantize_x).float().cpu()
+    assert torch.equal(y[good], clean)
+    am = xc.float().abs().amax(dim=1, keepdim=True)
+    assert torch.isnan(am[1]).all() and torch.isinf(am[3]).all()
+    y2 = linear_small_m(xc, w8, weight_scale_inv=sinv, quantize_x=quantize_x, x_amax=am).float().cpu()
+    assert torch.isnan(y2[bad]).all() and torch.equal(y2[good], clean)
+    # through the RMSNorm: a NaN input row gives a NaN amax and NaN codes
+    nw = torch.ones(k, device="cuda", dtype=torch.bfloat16)
+    amn = torch.empty(m, device="cuda", dtype=torch.float32)
+    q = torch.empty((m, k), device="cuda", dtype=torch.float8_e4m3fn)
+    out = rms_norm(xc, nw, 1e-5, amax_out=amn, q_out=q, q_mode=quantize_x)
+    assert torch.isnan(amn[1]) and torch.isnan(out[1].float()).all()
+    y3 = linear_small_m(q, w8, weight_scale_inv=sinv, quantize_x=quantize_x, x_amax=amn.view(m, 1)).float().cpu()
+    y4 = linear_small_m(out, w8, weight_scale_inv=sinv, quantize_x=quantize_x).float().cpu()
+    assert torch.equal(torch.isnan(y3), torch.isnan(y4)) and torch.equal(y3.nan_to_num(), y4.nan_to_num())
+
+
+def test_rmsnorm_amax_output():
+    """fdms_rmsnorm's amax_out is each output row's max |value| (plain rows,
+    with a residual, and the per-head QK-norm view)."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    g = torch.Generator().manual_seed(5)
+    for rows, hidden in ((8, 2048), (1, 4096), (16, 8192), (3, 264)):
+        x, r = _bf16((rows, hidden), g).cuda(), _bf16((rows, hidden), g).cuda()
+        nw = (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).cuda()
+        am = torch.empty(rows, device="cuda", dtype=torch.float32)
+        out = rms_norm(x, nw, 1e-5, amax_out=am)
+        assert torch.equal(am, out.float().abs().amax(dim=1))
+        out, _ = rms_norm(x, nw, 1e-5, residual=r, amax_out=am)
+        assert torch.equal(am, out.float().abs().amax(dim=1))
+    # the quantised output: the codes and scale of quantize_fp8_rows on the
+    # bf16 output, bit for bit; bf16_out=False leaves only the codes
+    from fastdms_amd.layers.linear import SplitPartials, quantize_fp8_rows
+    for q_mode in (1, 2):
+        x, r = _bf16((8, 2048), g).cuda(), _bf16((8, 2048), g).cuda()
+        nw = (1.0 + 0.1 * torch.randn(2048, generator=g)).to(torch.bfloat16).cuda()
+        am = torch.empty(8, device="cuda", dtype=torch.float32)
+        codes = torch.empty((8, 2048), device="cuda", dtype=torch.float8_e4m3fn)
+        out, _ = rms_norm(x, nw, 1e-5, residual=r, amax_out=am, q_out=codes, q_mode=q_mode)
+        want, _ = quantize_fp8_rows(out, torch_form=q_mode == 2)
+        assert torch.equal(codes.view(torch.uint8), want.view(torch.uint8))
+        codes2 = torch.zeros_like(codes)
+        none, _ = rms_norm(x, nw, 1e-5, residual=r, amax_out=am, q_out=codes2, q_mode=q_mode, bf16_out=False)
+        assert none is None and torch.equal(codes2.view(torch.uint8), want.view(torch.uint8))
+        part = torch.randn((2, 8, 2048), generator=g).cuda()
+        codes3 = torch.empty_like(codes)
+        out3, _ = rms_norm(SplitPartials(part), nw, 1e-5, residual=r, amax_out=am, q_out=codes3, q_mode=q_mode)
+        want3, _ = quantize_fp8_rows(out3, torch_form=q_mode == 2)
+        assert torch.equal(codes3.view(torch.uint8), want3.view(torch.uint8))
+    q = _bf16((4, 6, 128), g).cuda()
+    view = q[:, 1:5]   # strided per-head rows
+    nw = (1.0 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).cuda()
+    am = torch.empty(16, device="cuda", dtype=torch.float32)
+    out = rms_norm(view, nw, 1e-6, amax_out=am)
+    assert torch.equal(am, out.float().abs().reshape(16, 128).amax(dim=1))
+
+
 def test_linear_small_m_argument_errors():
     require_gpu()
     from fastdms_amd.layers.linear import PRO_RMSNORM, linear_small_m
