@@ -250,6 +250,48 @@ FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64
   return 0;
 }
 
+// FP8 embedding rows: out[i, :] = bf16(e4m3fn(table[ids[i], :]) * bf16(scale_inv[ids[i]]))
+// (embed_head.py:422-432: the FP8 row and its scale_inv, each in bf16, then
+// multiplied).  One workgroup per id, 8 columns per thread; an id outside
+// [0, vocab) yields a row of NaN (the reference's index_select raises there)
+// and reads nothing.
+__global__ __launch_bounds__(kThreads) void embedding_fp8_kernel(const int64_t* __restrict__ ids,
+                                                                 const uint8_t* __restrict__ table, int64_t t_s,
+                                                                 const float* __restrict__ scale_inv, int64_t vocab,
+                                                                 bf16_t* __restrict__ out, int64_t o_s, int dim) {
+  const int64_t i = blockIdx.x;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  const float s = ok ? bf16_to_f32(f32_to_bf16(scale_inv[id])) : __builtin_nanf("");
+  const uint8_t* src = table + (ok ? id : 0) * t_s;
+  for (int c = threadIdx.x * 8; c < dim; c += kThreads * 8) {
+    const uint2 v = ok ? *reinterpret_cast<const uint2*>(src + c) : uint2{0u, 0u};
+    const uint32_t w[2] = {v.x, v.y};
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[h], false);  // exact
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[h], true);
+      o[2 * h] = f32_to_bf16(lo[0] * s) | (f32_to_bf16(lo[1] * s) << 16);
+      o[2 * h + 1] = f32_to_bf16(hi[0] * s) | (f32_to_bf16(hi[1] * s) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + i * o_s + c) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+FDMS_EXPORT int fdms_embedding_fp8(const int64_t* ids, int64_t n, const void* table, int64_t table_stride,
+                                   const float* scale_inv, int64_t vocab, void* out, int64_t out_stride, int dim,
+                                   void* stream) {
+  if (n < 0 || dim <= 0 || dim % 8 || vocab <= 0 || table_stride < dim || out_stride < dim) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  if (!ids || !table || !scale_inv || !out || n > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if ((uintptr_t)table % 8 || table_stride % 8 || !fdms_aligned16(out) || out_stride % 8) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(embedding_fp8_kernel, dim3((unsigned)n), dim3(kThreads), 0, (hipStream_t)stream, ids,
+                     (const uint8_t*)table, table_stride, scale_inv, vocab, (bf16_t*)out, out_stride, dim);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
 // out[r, j] = bf16(silu(x[r, j]) * x[r, F + j]) in fp32 (activation.py:8-11).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const bf16_t* __restrict__ x, bf16_t* __restrict__ out,
                                                             int64_t rows, int f) {

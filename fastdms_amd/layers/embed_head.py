@@ -52,12 +52,18 @@ class VocabParallelEmbedding(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self._fp8_embedding_enabled:
-            # embed_head.py:422-432: fp8 row and its scale_inv, each in the output dtype, multiplied
-            flat = x.reshape(-1).to(torch.long)
-            dt = self._fp8_embedding_dtype
-            y = (self._fp8_embedding_weight.index_select(0, flat).to(dt)
-                 * self._fp8_embedding_scale_inv.index_select(0, flat).to(dt))
-            return y.reshape(*x.shape, self._fp8_embedding_weight.shape[1])
+            # embed_head.py:422-432: fp8 row and its scale_inv, each in bf16,
+            # multiplied -- the fdms_embedding_fp8 gather
+            if self._fp8_embedding_dtype != torch.bfloat16:
+                raise ValueError("the FP8 embedding gather produces bf16 rows")
+            flat = x.reshape(-1).to(torch.long).contiguous()
+            w8 = self._fp8_embedding_weight
+            out = torch.empty((flat.numel(), w8.shape[1]), device=w8.device, dtype=torch.bfloat16)
+            nat.require_cuda(flat, w8, out, what="fp8 embedding")
+            nat.call("fdms_embedding_fp8", flat.data_ptr(), flat.numel(), w8.data_ptr(), w8.stride(0),
+                     self._fp8_embedding_scale_inv.data_ptr(), w8.shape[0], out.data_ptr(), out.stride(0),
+                     w8.shape[1], nat.stream())
+            return out.reshape(*x.shape, w8.shape[1])
         return F.embedding(x, self.weight)
 
 

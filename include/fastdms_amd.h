@@ -288,6 +288,14 @@ int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int 
 /* out = silu(x[:, :F]) * x[:, F:], bf16 (fastdms/layers/activation.py:8-11). */
 int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
 
+/* (f)2 — FP8 embedding gather: out[i, :] = bf16(e4m3fn(table[ids[i], :]) *
+ * bf16(scale_inv[ids[i]])), bf16 output [n, dim] (fastdms/layers/embed_head.py:
+ * 422-432, the table shared with or quantised like the FP8 LM head,
+ * 379-402).  ids int64 on the device; an id outside [0, vocab) gives a NaN
+ * row.  dim % 8 == 0, table rows 8-byte aligned, out 16-byte aligned. */
+int fdms_embedding_fp8(const int64_t* ids, int64_t n, const void* table, int64_t table_stride, const float* scale_inv,
+                       int64_t vocab, void* out, int64_t out_stride, int dim, void* stream);
+
 /* RMSNorm (+ residual) whose input row r is bf16(sum over s < k_splits of
  * partials[s * split_stride + r * hidden + c]) in split order: the merge of a
  * split-K fdms_linear_small_m (epilogue 3) done by its consumer, as the

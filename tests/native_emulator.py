@@ -803,6 +803,24 @@ class Emulator:
         self._store_row_amax(amax_out, o, q_out, q_stride, q_mode)
         return 0
 
+    def embedding_fp8(self, ids, n, table, t_s, scale_inv, vocab, out, o_s, dim, stream):
+        """bf16(bf16(e4m3fn row) * bf16(scale_inv)), NaN rows for ids outside [0, vocab)."""
+        if n < 0 or dim <= 0 or dim % 8 or vocab <= 0 or t_s < dim or o_s < dim:
+            return 1
+        if n == 0:
+            return 0
+        idv = self.view(ids, torch.int64, (n,), (1,), "ids")
+        ok = (idv >= 0) & (idv < vocab)
+        safe = torch.where(ok, idv, torch.zeros_like(idv))
+        tab = self.view(table, torch.uint8, (vocab, dim), (t_s, 1), "table")
+        rows = torch.from_numpy(numerics.e4m3fn_decode(tab[safe].numpy()).astype(np.float32))
+        s = self.view(scale_inv, torch.float32, (vocab,), (1,), "scale_inv")[safe]
+        s = s.to(torch.bfloat16).float().reshape(-1, 1)
+        y = (rows * s).to(torch.bfloat16)
+        y[~ok] = float("nan")
+        self.view(out, torch.bfloat16, (n, dim), (o_s, 1), "out").copy_(y)
+        return 0
+
     def silu_mul(self, x, out, rows, f, stream):
         if rows == 0:
             return 0

@@ -1,6 +1,7 @@
 """Kernels around the DMS path that the model runs every layer: MFMA operand
-layout, RMSNorm (+ residual, + per-head strided rows), SiLU*up, row argmax,
-dense causal prefill attention and the strided decode-slot preparation."""
+layout, RMSNorm (+ residual, + per-head strided rows), SiLU*up, the FP8
+embedding gather, row argmax, dense causal prefill attention and the strided
+decode-slot preparation."""
 import numpy as np
 import pytest
 import torch
@@ -95,6 +96,38 @@ def test_silu_mul(rows, f):
     xf = x.float()
     want = (torch.nn.functional.silu(xf[:, :f]) * xf[:, f:]).to(torch.bfloat16)
     _ulp_close(out, want, "silu_mul")
+
+
+@pytest.mark.parametrize("vocab,dim,n", [(128256, 2048, 8), (1000, 4096, 3000), (512, 264, 17)])
+def test_fp8_embedding_gather_matches_the_oracle(vocab, dim, n):
+    """(f)2: the FP8 embedding gather equals the oracle's rows bit for bit
+    (bf16(bf16(e4m3fn row) * bf16(scale_inv)), embed_head.py:422-432; the
+    table quantised by quantize_fp8_rows as the reference's FP8 table), for
+    repeated ids, the first and last rows and the LM-head-sized table; an id
+    outside the table gives a NaN row without touching memory outside it."""
+    require_gpu()
+    from fastdms_amd.layers.embed_head import VocabParallelEmbedding
+    from oracle import linear as olin
+    from oracle import numerics
+    g = torch.Generator().manual_seed(vocab + dim)
+    w = (torch.randn(vocab, dim, generator=g) * 0.05).to(torch.bfloat16)
+    emb = VocabParallelEmbedding(vocab, dim)
+    emb.weight.data = w.cuda()
+    emb.quantize_embedding_to_fp8()
+    ids = torch.randint(0, vocab, (n,), generator=g)
+    ids[0], ids[-1] = 0, vocab - 1
+    if n > 4:
+        ids[2] = ids[1]
+    got = emb(ids.cuda()).cpu()
+    codes, sinv = olin.quantize_weight_to_fp8(w.float().numpy())   # W8^T [dim, vocab], [1, vocab]
+    rows = numerics.e4m3fn_decode(codes.T[ids.numpy()]).astype(np.float32)
+    s = torch.from_numpy(sinv.reshape(-1)[ids.numpy()]).to(torch.bfloat16).float().reshape(-1, 1)
+    want = (torch.from_numpy(rows).to(torch.bfloat16).float() * s).to(torch.bfloat16)
+    assert torch.equal(got, want)
+    bad = torch.tensor([3, -1, vocab, 1], device="cuda")
+    y = emb(bad).cpu()
+    assert torch.isnan(y[1].float()).all() and torch.isnan(y[2].float()).all()
+    assert torch.equal(y[0], emb(torch.tensor([3], device="cuda")).cpu()[0])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
