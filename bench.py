@@ -173,6 +173,9 @@ def parse_args():
     p.add_argument("--kv-cap-tokens", type=int, default=24000,
                    help="multitenant: compact KV capacity per layer (tokens)")
     p.add_argument("--eager", action="store_true", help="decode without HIP graphs")
+    p.add_argument("--kv-scales", choices=["calibrate", "unit"], default="calibrate",
+                   help="per-(layer, kv head) FP8 KV scales (BASELINE configs[1]-[3]) or unit scales (the "
+                        "reference's bare cast)")
     return p.parse_args()
 
 
@@ -228,11 +231,12 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
 
     def launch(l):
         if fused:
+            ks, vs = mgr.layer_kv_scales(l)
             fused_dms_rope_store_compact_decode_attention(
                 q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions,
                 None if base is None else base[l], live[l], num_kv_heads=hkv, alpha_scale=md.alpha_scale,
                 alpha_offset=md.alpha_offset, max_live_count=hint, out=out,
-                block_tables=None if bt is None else bt[l])
+                block_tables=None if bt is None else bt[l], k_scale=ks, v_scale=vs)
         elif bt is not None:
             compact_decode_attention_paged(q, arenas[l][0], arenas[l][1], bt[l], live[l], 16, max_live_count=hint)
         else:
@@ -655,9 +659,14 @@ def cpu_baseline(llm, seqs, budget_s: float):
             s.seq_id, base, rcap, st.live_counts.cpu().numpy().copy(), st.token_positions.cpu().numpy().copy(),
             st.evict_mask.cpu().numpy().copy(), st.max_capacity_per_lh, st.decode_headroom,
             st.dms_initial_expiry_done, st.last_dms_expiry_position)
+    scaled = mgr.kv_scales is not None
     orc = OracleModel(weights_from_model(runner.model), cfg, window_size=md.window_size, alpha_scale=md.alpha_scale,
                       alpha_offset=md.alpha_offset, capacity_tokens=mgr.capacity_tokens,
-                      max_model_len=mgr.max_model_len, manager=om)
+                      max_model_len=mgr.max_model_len, manager=om,
+                      fp8_scales="calibrate" if scaled else "unit")
+    if scaled:  # the GPU's per-(layer, kv head) FP8 scales, already calibrated by the prefill
+        orc.kv_scales = mgr.kv_scales.cpu().numpy().copy()
+        orc._calibrated = [True] * mgr.num_layers
     ids = [s.seq_id for s in seqs]
     last = [s.last_token for s in seqs]
     pos = [len(s) - 1 for s in seqs]
@@ -704,7 +713,8 @@ def main():
     progress(f"{args.config}: building {args.model}, prompts {lens}")
     llm = LLM(args.model, max_model_len=args.max_prompt + args.gen, max_num_seqs=args.batch,
               max_num_batched_tokens=sum(lens), dms_window_size=256, dms_alpha_scale=10.0, dms_alpha_offset=5.0,
-              kv_cache_dtype="float8_e4m3fn", seed=args.seed, enforce_eager=args.eager)
+              kv_cache_dtype="float8_e4m3fn", seed=args.seed, enforce_eager=args.eager,
+              compact_kv_fp8_scales=args.kv_scales)
     vocab = llm.config.hf_config.vocab_size
     # warm-up generation of the same prompt lengths (first-call library set-up,
     # graph capture), then freed; the reference times post-warm-up as well
@@ -765,7 +775,10 @@ def main():
         "vs_baseline": None, "dtype": "bf16 activations/weights, fp8_e4m3 compact KV", "data": "synthetic",
         "config": {"workload": workload,
                    "model": args.model, "global_batch": args.batch, "seq_len": int(max(lens)),
-                   "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager},
+                   "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager,
+                   "kv_scales": "per (layer, kv head), calibrated" if args.kv_scales == "calibrate" else "unit",
+                   "linear_weights": "fp8_e4m3 (FASTDMS_FP8_WEIGHTS=1)" if os.environ.get(
+                       "FASTDMS_FP8_WEIGHTS", "0").strip().lower() in ("1", "true", "yes", "on") else "bf16"},
         "prefill_tok_s": round(sum(lens) / prefill_s, 1),
         "decode_fast_loop": fast,
         "roofline": roof,
