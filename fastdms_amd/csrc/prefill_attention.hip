@@ -218,10 +218,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
   }
 }
 
-// GQA-packed variant for group sizes 1, 2 and 4: a workgroup takes P = 128/G
-// query positions of one KV head for all G query heads that share it, so one
-// staged K/V block feeds 128 query rows (wave w: head w % G, positions
-// 32*(w / G) .. +31, two 16-row MFMA tiles).  K/V blocks of 64 keys are
+// GQA-packed variant for group sizes 1, 2 and 4: a workgroup takes P =
+// 64·QT/G query positions of one KV head for all G query heads that share it,
+// so one staged K/V block feeds 64·QT query rows (wave w: head w % G,
+// positions 16·QT·(w / G) .. +16·QT-1, QT 16-row MFMA tiles; QT = 2: QT = 4
+// halves the LDS reads per MFMA but costs an occupancy step and measured no
+// faster -- the loop is bound by its VALU work, the softmax).  K/V blocks of 64 keys are
 // double-buffered in LDS: the next block's global loads are in flight while
 // the current one is computed, and one barrier separates blocks.  V is
 // transposed in registers (4 keys x 8 dims per thread, byte permutes) so the
@@ -230,12 +232,13 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 // from the matrix cores (P . 1, an extra output tile).  Softmax rescaling is
 // lazy: the running max only moves (and O / the sums are rescaled) when a block raises it
 // by more than 8 in the log2 domain, so p = exp2(s - m) stays below 256.
-template <int D, int G>
+template <int D, int G, int QT>
 __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
     int64_t ks_h, const bf16_t* __restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t* __restrict__ out, int64_t os_t,
     int64_t os_h, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, float scale_log2) {
-  constexpr int P = 128 / G;        // query positions per workgroup
+  constexpr int RW = 16 * QT;       // query rows per wave (QT 16-row MFMA tiles)
+  constexpr int P = 4 * RW / G;     // query positions per workgroup
   constexpr int KPAD = D + 8;       // sK row stride (bf16)
   // sVt row stride (bf16): 136 B = 34 dwords, so the 16 lanes of one 8-byte
   // B-operand read (rows 16c + lc) land on 16 distinct bank pairs
@@ -265,13 +268,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   const int lg = lane >> 4;
   const int lc = lane & 15;
   const int qh = kvh * G + wave % G;
-  const int wq0 = q0 + (wave / G) * 32;            // first position of this wave
-  const int wq_last = min(wq0 + 31, len - 1);      // last valid position of this wave
-  const int my_q0 = wq0 + lc, my_q1 = wq0 + 16 + lc;
+  const int wq0 = q0 + (wave / G) * RW;            // first position of this wave
+  const int wq_last = min(wq0 + RW - 1, len - 1);  // last valid position of this wave
 
-  bf16x8 qop[2][D / 32];
+  bf16x8 qop[QT][D / 32];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qrow = min(wq0 + 16 * qt + lc, len - 1);
     const bf16_t* qp = q + (int64_t)(start + qrow) * qs_t + (int64_t)qh * qs_h;
 #pragma unroll
@@ -288,13 +290,16 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   // Row r of unit i is key k0 + krow[i][r] at element offset koff[i][r] +
   // key * stride; rows past the sequence end are clamped (their scores are
   // masked).
-  int krow[UPT][4], koff[UPT][4];
+  // Whether unit i is a V or a K unit is uniform per wave (2D is a multiple
+  // of 64), so a block's row base is a scalar and each lane adds a fixed
+  // 32-bit element offset: the loads of a block cost no vector address math.
+  int krow[UPT][4], koff[UPT][4], eoff[UPT][4];
   const bf16_t* kvp[UPT];
   int64_t kvs[UPT];
 #pragma unroll
   for (int i = 0; i < UPT; ++i) {
     const int u = tid + i * kThreads;
-    const bool is_v = u < 2 * D;
+    const bool is_v = __builtin_amdgcn_readfirstlane((int)(u < 2 * D)) != 0;
     kvp[i] = is_v ? vb_base : kb_base;
     kvs[i] = is_v ? vs_t : ks_t;
 #pragma unroll
@@ -302,17 +307,26 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
       const int c = (u - 2 * D) + 2 * D * r;
       krow[i][r] = is_v ? 4 * (u % 16) + r : c / (D / 8);
       koff[i][r] = is_v ? 8 * (u / 16) : 8 * (c % (D / 8));
+      eoff[i][r] = krow[i][r] * (int)kvs[i] + koff[i][r];  // < 64 rows: within int range for any real stride
     }
   }
   auto load_block = [&](int k0) {
-    const bool tail = k0 + kKeys > klen;  // uniform
+    if (k0 + kKeys <= klen) {  // uniform
 #pragma unroll
-    for (int i = 0; i < UPT; ++i)
+      for (int i = 0; i < UPT; ++i) {
+        const bf16_t* base = kvp[i] + (int64_t)k0 * kvs[i];  // scalar
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = tail ? min(k0 + krow[i][r], klen - 1) : k0 + krow[i][r];
-        stage[i][r] = *reinterpret_cast<const uint4*>(kvp[i] + (int64_t)key * kvs[i] + koff[i][r]);
+        for (int r = 0; r < 4; ++r) stage[i][r] = *reinterpret_cast<const uint4*>(base + eoff[i][r]);
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < UPT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = min(k0 + krow[i][r], klen - 1);  // rows past the end clamped (their scores are masked)
+          stage[i][r] = *reinterpret_cast<const uint4*>(kvp[i] + (int64_t)key * kvs[i] + koff[i][r]);
+        }
+    }
   };
   auto store_block = [&](int buf) {
 #pragma unroll
@@ -342,12 +356,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     }
   };
 
-  float m_run[2] = {-INFINITY, -INFINITY};  // raw-score running max of query lc of each tile
+  float m_run[QT];  // raw-score running max of query lc of each tile
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
   // o[qt][D/16] accumulates P . 1 on the matrix cores: column-replicated row
   // sums of the same bf16 P as the numerator, in the O layout (no shuffles)
-  f32x4 o[2][D / 16 + 1];
+  f32x4 o[QT][D / 16 + 1];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int c = 0; c <= D / 16; ++c) o[qt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16x8 ones = as_bf16x8(uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -363,32 +379,35 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     const bool more = kb + 1 < nkb;
     if (more) load_block(k0 + kKeys);
     if (k0 <= off + wq_last) {  // wave-uniform: this block holds keys visible to the wave
-      f32x4 acc[2][4];
+      f32x4 acc[QT][4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        acc[0][t] = acc[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) acc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < D / 32; ++j) {
           const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&sK[buf][(16 * t + lc) * KPAD + 32 * j + 8 * lg]));
-          acc[0][t] = mfma16x16x32(a, qop[0][j], acc[0][t]);
-          acc[1][t] = mfma16x16x32(a, qop[1][j], acc[1][t]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) acc[qt][t] = mfma16x16x32(a, qop[qt][j], acc[qt][t]);
         }
       }
       const bool masked = k0 + kKeys - 1 > off + wq0 || k0 + kKeys > klen;  // wave-uniform
       if (masked) {
-        const int lim0 = off + min(my_q0, len - 1), lim1 = off + min(my_q1, len - 1);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int qt = 0; qt < QT; ++qt) {
+          const int lim = off + min(wq0 + 16 * qt + lc, len - 1);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = k0 + 16 * t + 4 * lg + r;
-            acc[0][t][r] = key > lim0 ? -INFINITY : acc[0][t][r];
-            acc[1][t][r] = key > lim1 ? -INFINITY : acc[1][t][r];
-          }
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = k0 + 16 * t + 4 * lg + r;
+              acc[qt][t][r] = key > lim ? -INFINITY : acc[qt][t][r];
+            }
+        }
       }
-      uint4 pa[2][2];
+      uint4 pa[QT][2];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         float bmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -432,11 +451,11 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
           const uint2 lo = *reinterpret_cast<const uint2*>(vr + key_a);
           const uint2 hi = *reinterpret_cast<const uint2*>(vr + key_a + 16);
           const bf16x8 b = as_bf16x8(uint4{lo.x, lo.y, hi.x, hi.y});
-          o[0][c] = mfma16x16x32(as_bf16x8(pa[0][st]), b, o[0][c]);
-          o[1][c] = mfma16x16x32(as_bf16x8(pa[1][st]), b, o[1][c]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) o[qt][c] = mfma16x16x32(as_bf16x8(pa[qt][st]), b, o[qt][c]);
         }
-        o[0][D / 16] = mfma16x16x32(as_bf16x8(pa[0][st]), ones, o[0][D / 16]);
-        o[1][D / 16] = mfma16x16x32(as_bf16x8(pa[1][st]), ones, o[1][D / 16]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][D / 16] = mfma16x16x32(as_bf16x8(pa[qt][st]), ones, o[qt][D / 16]);
       }
     }
     if (more) store_block(buf ^ 1);
@@ -444,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
   }
 
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float inv = 1.0f / o[qt][D / 16][r];  // row sum of query 4*lg + r
@@ -468,21 +487,30 @@ FDMS_EXPORT int fdms_prefill_attention_varlen(const void* q, int64_t qs_t, int64
   if (num_seqs == 0 || max_seqlen_q <= 0) return 0;
   if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k) return (int)hipErrorInvalidValue;
   if (num_seqs > 65535 || num_q_heads > 65535) return (int)hipErrorInvalidValue;
+  // token strides in elements: 64 rows of either stay in 32-bit offsets
+  if (ks_t < 0 || vs_t < 0 || ks_t >= (1 << 24) || vs_t >= (1 << 24)) return (int)hipErrorInvalidValue;
   const float sl2 = scale * 1.4426950408889634f;
   const int group = num_q_heads / num_kv_heads;
   const int32_t* cq = cu_seqlens_q;
   const int32_t* ck = cu_seqlens_k;
   if ((group == 1 || group == 2 || group == 4) && (head_dim == 64 || head_dim == 128) &&
       fdms_prefill_gqa_enabled()) {
-    const dim3 ggrid((max_seqlen_q + 128 / group - 1) / (128 / group), num_kv_heads, num_seqs);
-#define FDMS_PREFILL_GQA(DD, GG)                                                                                   \
-  hipLaunchKernelGGL((prefill_attn_gqa_kernel<DD, GG>), ggrid, dim3(kThreads), 0, (hipStream_t)stream,              \
+    int qt = 2;  // 16-row query tiles per wave
+    if (const char* e = std::getenv("FASTDMS_AMD_PREFILL_QT")) {  // comparison / testing
+      if (e[0] == '4' && head_dim == 64) qt = 4;
+    }
+    const int pos = 64 * qt / group;  // query positions per workgroup
+    const dim3 ggrid((max_seqlen_q + pos - 1) / pos, num_kv_heads, num_seqs);
+#define FDMS_PREFILL_GQA(DD, GG, QQ)                                                                               \
+  hipLaunchKernelGGL((prefill_attn_gqa_kernel<DD, GG, QQ>), ggrid, dim3(kThreads), 0, (hipStream_t)stream,          \
                      (const bf16_t*)q, qs_t, qs_h, (const bf16_t*)k, ks_t, ks_h, (const bf16_t*)v, vs_t, vs_h,       \
                      (bf16_t*)out, os_t, os_h, cq, ck, sl2)
-    if (head_dim == 64) {
-      if (group == 1) FDMS_PREFILL_GQA(64, 1); else if (group == 2) FDMS_PREFILL_GQA(64, 2); else FDMS_PREFILL_GQA(64, 4);
+    if (head_dim == 64 && qt == 4) {
+      if (group == 1) FDMS_PREFILL_GQA(64, 1, 4); else if (group == 2) FDMS_PREFILL_GQA(64, 2, 4); else FDMS_PREFILL_GQA(64, 4, 4);
+    } else if (head_dim == 64) {
+      if (group == 1) FDMS_PREFILL_GQA(64, 1, 2); else if (group == 2) FDMS_PREFILL_GQA(64, 2, 2); else FDMS_PREFILL_GQA(64, 4, 2);
     } else {
-      if (group == 1) FDMS_PREFILL_GQA(128, 1); else if (group == 2) FDMS_PREFILL_GQA(128, 2); else FDMS_PREFILL_GQA(128, 4);
+      if (group == 1) FDMS_PREFILL_GQA(128, 1, 2); else if (group == 2) FDMS_PREFILL_GQA(128, 2, 2); else FDMS_PREFILL_GQA(128, 4, 2);
     }
 #undef FDMS_PREFILL_GQA
     FDMS_LAUNCH_CHECK();
