@@ -744,6 +744,10 @@ def main():
     dt = time.perf_counter() - t0
     value = args.batch * args.steps / dt
     progress(f"decode {value:.1f} tok/s")
+    # the engine launches a certain next decode step before reading back the
+    # current one (FASTDMS_AMD_DECODE_LOOKAHEAD): finish it before driving the
+    # runner directly
+    llm.drain()
     fast = None
     left = min(s.max_tokens - s.num_completion_tokens for s in seqs)
     if left >= 8 and not args.no_fast_loop:  # the device-side greedy loop over the rest of the generation

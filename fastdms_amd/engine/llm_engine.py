@@ -93,8 +93,21 @@ class LLMEngine:
             seqs = [s for s in seqs if s in self.scheduler.running]
         return seqs
 
-    def step(self):
-        seqs, is_prefill = self.scheduler.schedule()
+    def drain(self) -> None:
+        """Finish the decode step launched ahead, if any (one more step of the
+        running batch, launching nothing further), so that host and device
+        state agree before the runner is driven directly."""
+        if self.model_runner.lookahead_pending():
+            self.step(lookahead=False)
+
+    def step(self, lookahead: bool = True):
+        runner = self.model_runner
+        if runner.lookahead_pending():
+            # the decode step launched ahead by the previous step is in flight:
+            # this step is that decode (a new request's prefill comes next)
+            seqs, is_prefill = self.scheduler.schedule_running(), False
+        else:
+            seqs, is_prefill = self.scheduler.schedule()
         t0 = time.perf_counter()
         if is_prefill:
             done, token_ids = self._run_prefill_admitting(seqs)
@@ -105,11 +118,15 @@ class LLMEngine:
             else:
                 seqs = done
         if not is_prefill:
-            if self.model_runner.compact_kv_manager.paged:
+            if runner.lookahead_pending():
+                pass  # its room was checked when it was launched
+            elif runner.compact_kv_manager.paged:
                 seqs = self._make_page_room(seqs)
             elif self.config.compact_decode_reserve_tokens is not None:
                 seqs = self._make_decode_room(seqs)
-            token_ids = self.model_runner.run(seqs, False) if seqs else []
+            # the next step decodes this same batch when nothing waits to be
+            # admitted (and, checked by the runner, none of it finishes now)
+            token_ids = runner.run(seqs, False, lookahead=lookahead and not self.scheduler.waiting) if seqs else []
         dt = time.perf_counter() - t0
         self.scheduler.postprocess(seqs, token_ids, is_prefill)
         fast = self._greedy_fast_loop(seqs) if is_prefill else None

@@ -32,6 +32,12 @@ from .dms import DMSMetadata, load_dms_metadata
 from .sequence import Sequence, SequenceStatus
 
 
+def decode_lookahead_enabled() -> bool:
+    """FASTDMS_AMD_DECODE_LOOKAHEAD (default on): launch a certain next decode
+    step before reading back the current one's ids."""
+    return os.environ.get("FASTDMS_AMD_DECODE_LOOKAHEAD", "1").strip().lower() not in ("0", "false", "no", "off")
+
+
 def compact_greedy_fast_loop_enabled() -> bool:
     """FASTDMS_COMPACT_GREEDY_FAST_LOOP (default on), model_runner.py:30-32."""
     return os.environ.get("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "1").strip().lower() not in ("0", "false", "no", "off")
@@ -103,6 +109,12 @@ class ModelRunner:
         self.prompt_stages: dict[int, PromptStage] = {}  # long prompts between their chunks
         self.pinned_ids = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
+        # decode lookahead (run_decode): two pinned sets each for the sampled
+        # ids read back and the positions sent, alternating per staged step
+        self._tok_ring = [torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True) for _ in range(2)]
+        self._pos_ring = [torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True) for _ in range(2)]
+        self._ring = 0
+        self._lookahead: dict | None = None  # the decode step in flight ahead of the host
         self.graphs: dict[tuple, tuple] = {}
         self.graph_pool = None
         self._warm: set = set()
@@ -234,8 +246,13 @@ class ModelRunner:
         return ChunkPlan(seq.seq_id, stage, start, rows, end == target, dev([0, rows]), dev([0, end]), [], None,
                          None, 0)
 
+    def _no_step_in_flight(self, what: str) -> None:
+        if self._lookahead is not None:
+            raise RuntimeError(f"{what} while a decode step launched ahead is in flight (LLMEngine.drain() first)")
+
     @torch.inference_mode()
     def run_prefill(self, seqs: list[Sequence]) -> list[int]:
+        self._no_step_in_flight("prefill")
         ids, pos = self.prepare_prefill(seqs)
         try:
             hidden = self.model(ids, pos)
@@ -378,25 +395,77 @@ class ModelRunner:
         else:
             self.model.lm_head.last_logits = self._decode_body(start, batch, hint)
 
+    def lookahead_pending(self) -> bool:
+        """True while a decode step launched ahead of the host is in flight:
+        the engine's next step must be the decode of that same batch."""
+        return self._lookahead is not None
+
+    def _stage_tokens(self, batch: int):
+        """Queue the copies of the step's page-pool overflow flag and sampled
+        ids to pinned memory; return (id buffer, event marking both done)."""
+        if self.compact_kv_manager.paged:
+            self.compact_kv_manager.stage_overflow_check()
+        buf = self._tok_ring[self._ring]
+        self._ring ^= 1
+        buf[:batch].copy_(self.static_tokens[:batch], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return buf, ev
+
+    def _lookahead_ok(self, seqs: list[Sequence]) -> bool:
+        """The step after the one just launched is certain: greedy ids on the
+        device (fused head), ignore_eos sequences none of which finishes with
+        this step, paged KV with room for two more appends."""
+        mgr = self.compact_kv_manager
+        if not (decode_lookahead_enabled() and self.config.fused_greedy_head and mgr.paged):
+            return False
+        if any(s.temperature > 1e-10 or not s.ignore_eos or s.num_completion_tokens + 2 > s.max_tokens
+               for s in seqs):
+            return False
+        return mgr.decode_pages_fit(2)
+
     @torch.inference_mode()
-    def run_decode(self, seqs: list[Sequence]) -> list[int]:
+    def run_decode(self, seqs: list[Sequence], lookahead: bool = False) -> list[int]:
+        """One decode step of ``seqs``; returns its greedy / sampled ids.  With
+        ``lookahead`` (the engine knows the next step decodes the same batch)
+        the following step is launched before this one's ids are read back --
+        its input ids come from the device -- so the host's per-step work
+        overlaps the GPU; that step is then the one a later call returns."""
         mgr = self.compact_kv_manager
         batch = len(seqs)
-        positions = [len(seq) - 1 for seq in seqs]
-        # finished / preempted sequences leave holes in the layer-major slots:
-        # move the batch's rows to slots 0 .. batch-1 (one launch per step)
-        mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
-        start, hint = self._begin_decode_step(seqs, positions)
-        for i, seq in enumerate(seqs):
-            self.pinned_ids[i] = seq.last_token
-            self.pinned_pos[i] = positions[i]
-        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
-        self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
-        self._replay_decode(start, batch, hint)
-        self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
-        if mgr.paged:
-            mgr.stage_overflow_check()
-        out = self.static_tokens[:batch].tolist()
+        la, self._lookahead = self._lookahead, None
+        if la is not None:  # this step is already in flight
+            if la["ids"] != [s.seq_id for s in seqs]:
+                raise RuntimeError("the decode step in flight is for another batch")
+            host, done = la["host"], la["event"]
+        else:
+            positions = [len(seq) - 1 for seq in seqs]
+            # finished / preempted sequences leave holes in the layer-major slots:
+            # move the batch's rows to slots 0 .. batch-1 (one launch per step)
+            mgr.pack_active_slots([mgr.seq_states[s.seq_id] for s in seqs])
+            start, hint = self._begin_decode_step(seqs, positions)
+            for i, seq in enumerate(seqs):
+                self.pinned_ids[i] = seq.last_token
+                self.pinned_pos[i] = positions[i]
+            self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+            self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
+            self._replay_decode(start, batch, hint)
+            self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
+            host, done = self._stage_tokens(batch)
+        if lookahead and self._lookahead_ok(seqs):
+            positions = [len(seq) for seq in seqs]  # one past the step in flight
+            start, hint = self._begin_decode_step(seqs, positions)
+            pos = self._pos_ring[self._ring]
+            for i, p in enumerate(positions):
+                pos[i] = p
+            self.static_positions[:batch].copy_(pos[:batch], non_blocking=True)
+            self.static_input_ids[:batch].copy_(self.static_tokens[:batch])  # the ids of the step in flight
+            self._replay_decode(start, batch, hint)
+            self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs) + 1)
+            nhost, nev = self._stage_tokens(batch)
+            self._lookahead = {"ids": [s.seq_id for s in seqs], "host": nhost, "event": nev}
+        done.synchronize()
+        out = host[:batch].tolist()
         if mgr.paged:
             mgr.check_overflow(sync=False)
         return out
@@ -414,6 +483,7 @@ class ModelRunner:
         sequence."""
         if max_steps <= 0:
             return [] if len(seqs) == 1 else [[] for _ in seqs]
+        self._no_step_in_flight("the greedy fast loop")
         if not self.config.fused_greedy_head:
             raise RuntimeError("compact greedy fast loop requires the fused greedy argmax path")
         if self.config.compact_decode_reserve_tokens is not None:
@@ -456,10 +526,11 @@ class ModelRunner:
         self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
         return out[0] if batch == 1 else out
 
-    def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
-        return self.run_prefill(seqs) if is_prefill else self.run_decode(seqs)
+    def run(self, seqs: list[Sequence], is_prefill: bool, lookahead: bool = False) -> list[int]:
+        return self.run_prefill(seqs) if is_prefill else self.run_decode(seqs, lookahead)
 
     def free_compact(self, seq_ids: list[int]) -> None:
+        self._no_step_in_flight("freeing compact KV")
         for sid in seq_ids:
             self.compact_kv_manager.free(sid)
 

@@ -57,13 +57,18 @@ class Scheduler:
             batched += seq.num_scheduled_tokens
         if scheduled:
             return scheduled, True
+        return self.schedule_running(), False
+
+    def schedule_running(self) -> list[Sequence]:
+        """The decode batch: the first max_num_seqs running sequences."""
+        scheduled: list[Sequence] = []
         while self.running and len(scheduled) < self.max_num_seqs:
             seq = self.running.popleft()
             seq.num_scheduled_tokens = 1
             scheduled.append(seq)
         assert scheduled
         self.running.extendleft(reversed(scheduled))
-        return scheduled, False
+        return scheduled
 
     def postprocess(self, seqs: list[Sequence], token_ids: list[int], is_prefill: bool) -> None:
         for seq, token_id in zip(seqs, token_ids):

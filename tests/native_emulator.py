@@ -1100,6 +1100,22 @@ class Emulator:
         return 0
 
 
+class _HostEvent:
+    """torch.cuda.Event for the emulator, whose copies complete when issued."""
+
+    def __init__(self, *a, **k):
+        pass
+
+    def record(self, *a, **k):
+        pass
+
+    def synchronize(self):
+        pass
+
+    def query(self):
+        return True
+
+
 @contextmanager
 def cpu_engine():
     """Run fastdms_amd's engine on CPU tensors through the emulator.
@@ -1165,6 +1181,7 @@ def cpu_engine():
     patch(torch.cuda, "current_device", lambda: 0)
     patch(torch.cuda, "synchronize", lambda *a, **k: None)
     patch(torch.cuda, "is_available", lambda: True)
+    patch(torch.cuda, "Event", _HostEvent)
     patch(nat, "call", emu)
     patch(nat, "stream", lambda: 0)
     patch(nat, "require_cuda", lambda *a, **k: None)

@@ -38,10 +38,35 @@ def test_engine_glue_matches_oracle(model, lens, gen, layout):
 
 
 @pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 64], 12), ("tiny-qwen3", [129, 700], 8)])
-def test_engine_fused_greedy_head_matches_oracle_tokens(model, lens, gen):
+def test_engine_fused_greedy_head_matches_oracle_tokens(monkeypatch, model, lens, gen):
     """Decode with the LM-head GEMV fused with the argmax: no logits, tokens
-    equal to the oracle model's greedy tokens step for step."""
+    equal to the oracle model's greedy tokens step for step.  (The compact
+    state is compared after every step, so no step may run ahead.)"""
+    monkeypatch.setenv("FASTDMS_AMD_DECODE_LOOKAHEAD", "0")
     _run(model, lens, gen, fused_head=True)
+
+
+@pytest.mark.parametrize("layout", ["paged", "span"])
+def test_decode_lookahead_gives_the_oracle_tokens(layout):
+    """With the decode lookahead (the next step of a certain batch launched
+    before the current step's ids are read back; paged layout only) every
+    step still returns the oracle's greedy tokens -- those of the steps
+    launched ahead included, so their appends and expiry decisions are the
+    oracle's -- and the last step launches nothing ahead."""
+    calls = _run("tiny-llama", [300, 517, 64], 10, fused_head=True, layout=layout, lookahead=True)
+    assert calls.count("lookahead") == (8 if layout == "paged" else 0)
+
+
+def _lookahead_probe(runner, calls):
+    """Record each decode step that launched the next one ahead."""
+    orig = runner._lookahead_ok
+
+    def probe(seqs):
+        ok = orig(seqs)
+        if ok:
+            calls.append("lookahead")
+        return ok
+    runner._lookahead_ok = probe
 
 
 FP8_ENV = {"FASTDMS_FP8_WEIGHTS": "1", "FASTDMS_FP8_WEIGHT_SCOPE": "all", "FASTDMS_FP8_LM_HEAD": "0"}
@@ -63,13 +88,18 @@ def test_fp8_decode_glue_matches_the_quantised_oracle(monkeypatch):
         assert "fdms_linear_small_m:" + tag in calls, tag
 
 
-def _run(model, lens, gen, fused_head, layout="paged", quant=False):
+def _run(model, lens, gen, fused_head, layout="paged", quant=False, lookahead=False):
+    """lookahead: the decode lookahead runs (the compact state is then one
+    step ahead between steps and is compared once the sequences finish)."""
     from engine_oracle import oracle_for
+    probe: list[str] = []
     with cpu_engine() as emu:
         from fastdms_amd import LLM, SamplingParams
         llm = LLM(model, max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384, enforce_eager=True,
                   fused_greedy_head=fused_head, compact_kv_layout=layout, **DMS)
         runner = llm.model_runner
+        if lookahead:
+            _lookahead_probe(runner, probe)
         orc = oracle_for(runner, llm.config, quant=quant, dms=DMS)
         rng = np.random.default_rng(3)
         sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
@@ -94,6 +124,9 @@ def _run(model, lens, gen, fused_head, layout="paged", quant=False):
             # exactly; deeper layers' decisions see GEMM-order noise, and a
             # decision sitting on the threshold may flip
             mgr = runner.compact_kv_manager
+            if lookahead:  # the state runs a step ahead of the oracle's
+                assert runner.lookahead_pending() == (step < gen - 2 and layout == "paged"), step
+                continue
             for s in seqs:
                 if s.seq_id not in mgr.seq_states:  # finished and freed on the last step
                     continue
@@ -105,7 +138,7 @@ def _run(model, lens, gen, fused_head, layout="paged", quant=False):
                 check_page_invariants(mgr)
         assert ("fdms_paged_expiry" if layout == "paged" else "fdms_dms_expiry") in emu.calls
         llm.exit()
-        return list(emu.calls)
+        return list(emu.calls) + probe
 
 
 @pytest.mark.parametrize("lens,gen", [([300], 14), ([300, 64, 517], 10)])
