@@ -285,6 +285,51 @@ def test_quantized_weights_graph_equals_eager(monkeypatch, env):
     assert outs[0] == outs[1] == outs[2]
 
 
+@pytest.mark.parametrize("cap", [260, 300])
+def test_preempted_sequences_follow_the_oracle_on_the_gpu(monkeypatch, cap):
+    """(f)1 on the GPU: capped span KV with preemption (graphs on), on the
+    tiny-llama shape with a planted successor margin (greedy decisions a few
+    logits apart, so GPU and CPU rounding cannot flip them).  Every sequence's
+    tokens -- those after a re-admission included -- equal the CPU model
+    oracle replaying that sequence alone through the same history: prefill,
+    decode, free at each preemption, re-prefill of its tokens but the last,
+    decode (tests/test_engine_preemption.py's replay)."""
+    require_gpu()
+    from dataclasses import replace
+    from fastdms_amd import LLM, SamplingParams
+    from fastdms_amd.models.synthetic import PRESETS
+    from test_engine_preemption import GEN, _replay_alone
+    monkeypatch.setenv("FASTDMS_DMS_EXPIRY_TRITON", "1")
+    monkeypatch.setenv("FASTDMS_DMS_EXPIRY_INTERVAL", "1")
+    monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
+    cfg = replace(PRESETS["tiny-llama"], successor_margin=0.3)
+    llm = LLM(cfg, max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096, fused_greedy_head=True,
+              compact_kv_capacity_tokens=cap, compact_admission="preempt", compact_decode_reserve_tokens=4,
+              compact_kv_layout="span", **DMS)
+    rng = np.random.default_rng(11)
+    sp = SamplingParams(temperature=0.0, max_tokens=GEN, ignore_eos=True)
+    seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in (300, 200)]
+    for _ in range(5):
+        llm.step()
+    seqs.append(llm.add_request(rng.integers(0, 512, 160).tolist(), sp))
+    steps = 0
+    while not llm.is_finished():
+        llm.step()
+        steps += 1
+        assert steps < 400, "the engine stopped making progress"
+    sched = llm.scheduler
+    assert sched.num_preemptions >= 1, "no preemption: the test did not exercise re-admission"
+    torch.cuda.synchronize()
+    for s in seqs:
+        at = [g for sid, g in sched.preemption_log if sid == s.seq_id]
+        got, want = _replay_alone(llm.model_runner, llm, s, at)
+        assert got == want, f"seq {s.seq_id} (preempted at {at}): oracle {got} vs engine {want}"
+    print(f"cap {cap}: {sched.num_preemptions} preemptions {sched.preemption_log}", flush=True)
+    llm.exit()
+    del llm
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("admission,reserve,cap,layout", [
     ("defer", None, 260, "span"), ("preempt", 4, 300, "span"),
     # 18 pages of 16 rows: the second prompt waits for the first.  (Preemption
