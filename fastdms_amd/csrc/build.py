@@ -36,6 +36,11 @@ CFLAGS = [
 # default there) every block copies them out and back.
 FILE_FLAGS = {
     "prefill_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # The decode attention kernels take the arguments their first loads need
+    # first; preloading them into SGPRs at wave launch takes one scalar memory
+    # round trip off each workgroup's start (code objects carry a fallback
+    # prologue that loads them for firmware without preload support).
+    "compact_attention.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 

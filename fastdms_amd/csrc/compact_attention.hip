@@ -14,6 +14,7 @@
 // (device-scope atomic ticket) merges them and writes the output, then resets
 // its ticket to 0 so the next call (or graph replay) starts clean.  Softmax is
 // computed in the log2 domain (q pre-scaled by scale*log2 e, exp2).
+#include <climits>
 #include <cstdlib>
 #include <mutex>
 
@@ -27,6 +28,31 @@ static bool fdms_force_generic_attention() {
   const char* e = std::getenv("FASTDMS_AMD_ATTN_GENERIC");
   return e && e[0] == '1';
 }
+
+// Matrix-core kernel launch shape: FASTDMS_AMD_ATTN_NP = 64-row groups each
+// wave has in flight at the start (1 or 2, default 1: measured equal or
+// slower with 2 or 4, the loop being bound by the group arithmetic rather
+// than the load latency), FASTDMS_AMD_ATTN_WAVES = 4 or 8 waves per workgroup for the
+// fused head_dim-64 kernel (default: 8 for 17 to 128 (seq, kv head) pairs,
+// where a launch has few workgroups and each pair's rows go to more waves,
+// else 4: three workgroups fit per CU, and at 16 pairs or fewer smaller
+// splits spread the rows over more CUs).  Read per call; tuning switches
+// that change speed, never results.
+static int fdms_attn_np(int head_dim) {
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_NP");
+  int np = 1;
+  if (e && (e[0] == '1' || e[0] == '2') && !e[1]) np = e[0] - '0';
+  (void)head_dim;
+  return np;
+}
+static int fdms_attn_fused_waves(int head_dim, int pairs) {
+  if (head_dim == 128) return 8;  // the preprocess needs 2.5 * head_dim threads
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_WAVES");
+  if (e && (e[0] == '4' || e[0] == '8') && !e[1]) return e[0] - '0';
+  return (pairs > 16 && pairs <= 128) ? 8 : 4;
+}
+
+static bool fits_i32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
 
 // FASTDMS_AMD_ATTN_MFMA=0 keeps FP8 calls off the matrix-core kernel (read per
 // call; used to compare kernels on the same inputs).
@@ -921,16 +947,39 @@ __device__ __forceinline__ int64_t span_row(const SpanAddr& addr, int b, int h, 
 // instead, which keeps the wait counters exact across the loop.  Their
 // scores are masked to -inf, so their K and V never reach the output.
 // Flat spans address rows from the span's first row (kspan / vspan, uniform)
-// with 32-bit offsets; paged spans go through the block table per row.
+// with 32-bit offsets; paged spans go through the block table.  The address
+// step and the load step are separate so that the table reads of several
+// groups share one scalar-memory wait.
+template <int D>
+struct MfmaGroupAddr {
+  const uint4* k;
+  const uint4* v[4];
+};
+
+// Paged group with its quarters' page rows known (qrow[kk] = physical row of
+// the first row of the page holding rows g0 + 16 kk .. g0 + 16 kk + 15,
+// clamped to `end` - 1).
+template <int D>
+__device__ __forceinline__ void mfma_group_addr_paged(MfmaGroupAddr<D>& ga, const uint8_t* __restrict__ kspan,
+                                                      const uint8_t* __restrict__ vspan, int64_t c_s,
+                                                      const int64_t (&qrow)[4], int page_shift, int g0, int end,
+                                                      int lane) {
+  const int s = lane >> 2, q = lane & 3;
+  const int last = end - 1;
+  const int mask = (1 << page_shift) - 1;
+  const int64_t kq = q == 0 ? qrow[0] : q == 1 ? qrow[1] : q == 2 ? qrow[2] : qrow[3];
+  ga.k = reinterpret_cast<const uint4*>(kspan + (kq + (min(g0 + s + 16 * q, last) & mask)) * c_s);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    ga.v[kk] = reinterpret_cast<const uint4*>(vspan + (qrow[kk] + (min(g0 + s + 16 * kk, last) & mask)) * c_s +
+                                              q * (D / 4));
+}
+
 template <int D, bool PAGED>
-__device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* __restrict__ kspan,
+__device__ __forceinline__ void mfma_group_addr(MfmaGroupAddr<D>& ga, const uint8_t* __restrict__ kspan,
                                                 const uint8_t* __restrict__ vspan, int64_t c_s,
                                                 const SpanAddr& addr, int b, int h, int g0, int end, int lane) {
-  constexpr int KQ = D / 16;  // 16-byte chunks per K row
-  constexpr int VQ = D / 64;  // 16-byte chunks per V slice
   const int s = lane >> 2, q = lane & 3;
-  const uint4* ksrc;
-  const uint4* vsrc[4];
   if constexpr (PAGED) {
     // A group starts 64-row aligned and pages hold >= 16 rows (the host
     // checks), so each 16-row quarter of the group lies in one page: its id
@@ -939,30 +988,32 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* 
     using const_i32 = const __attribute__((address_space(4))) int32_t;
     const_i32* trow = (const_i32*)(addr.table + b * addr.tb_b + h * addr.tb_h);
     const int last = end - 1;
-    const int mask = (1 << addr.page_shift) - 1;
     int64_t qrow[4];  // physical row of the first row of each quarter's page
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int r0 = __builtin_amdgcn_readfirstlane(min(g0 + 16 * kk, last));
       qrow[kk] = (int64_t)trow[r0 >> addr.page_shift] << addr.page_shift;
     }
-    const int64_t kq = q == 0 ? qrow[0] : q == 1 ? qrow[1] : q == 2 ? qrow[2] : qrow[3];
-    ksrc = reinterpret_cast<const uint4*>(kspan + (kq + (min(g0 + s + 16 * q, last) & mask)) * c_s);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + (qrow[kk] + (min(g0 + s + 16 * kk, last) & mask)) * c_s +
-                                                q * (D / 4));
+    mfma_group_addr_paged<D>(ga, kspan, vspan, c_s, qrow, addr.page_shift, g0, end, lane);
+    (void)s;
+    (void)q;
   } else {
     const uint32_t cs = (uint32_t)c_s;
-    ksrc = reinterpret_cast<const uint4*>(kspan + __umul24((uint32_t)min(g0 + s + 16 * q, end - 1), cs));
+    ga.k = reinterpret_cast<const uint4*>(kspan + __umul24((uint32_t)min(g0 + s + 16 * q, end - 1), cs));
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      vsrc[kk] = reinterpret_cast<const uint4*>(vspan + (__umul24((uint32_t)min(g0 + s + 16 * kk, end - 1), cs) +
+      ga.v[kk] = reinterpret_cast<const uint4*>(vspan + (__umul24((uint32_t)min(g0 + s + 16 * kk, end - 1), cs) +
                                                          (uint32_t)(q * (D / 4))));
   }
+}
+
+template <int D>
+__device__ __forceinline__ void mfma_issue_group(MfmaGroup<D>& g, const MfmaGroupAddr<D>& ga) {
+  constexpr int KQ = D / 16;  // 16-byte chunks per K row
+  constexpr int VQ = D / 64;  // 16-byte chunks per V slice
 #pragma unroll
   for (int m = 0; m < KQ; ++m) {
-    const uint4 x = ksrc[m];
+    const uint4 x = ga.k[m];
     g.k[4 * m] = x.x;
     g.k[4 * m + 1] = x.y;
     g.k[4 * m + 2] = x.z;
@@ -972,12 +1023,21 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* 
   for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
     for (int m = 0; m < VQ; ++m) {
-      const uint4 x = vsrc[kk][m];
+      const uint4 x = ga.v[kk][m];
       g.v[kk][4 * m] = x.x;
       g.v[kk][4 * m + 1] = x.y;
       g.v[kk][4 * m + 2] = x.z;
       g.v[kk][4 * m + 3] = x.w;
     }
+}
+
+template <int D, bool PAGED>
+__device__ __forceinline__ void mfma_load_group(MfmaGroup<D>& g, const uint8_t* __restrict__ kspan,
+                                                const uint8_t* __restrict__ vspan, int64_t c_s,
+                                                const SpanAddr& addr, int b, int h, int g0, int end, int lane) {
+  MfmaGroupAddr<D> ga;
+  mfma_group_addr<D, PAGED>(ga, kspan, vspan, c_s, addr, b, h, g0, end, lane);
+  mfma_issue_group<D>(g, ga);
 }
 
 constexpr int kVtStride = 20;  // dwords per dim row of the transposed V tile (16 steps + pad)
@@ -1004,14 +1064,23 @@ struct DecodePre {
   int positive_scale;
 };
 
-template <int D, int NW, bool PAGED, bool FUSED>
+// The first nine arguments are what a workgroup needs before its first
+// loads (its pair, live count, and for the fused kernel the step's append
+// slot and position); this file is built with them preloaded into SGPRs at
+// wave launch (-amdgpu-kernarg-preload-count), which takes one scalar memory
+// round trip off that chain (the page table is read only after the live
+// count, by when the other arguments have landed).  Strides are int32 (the
+// hosts check the range).
+template <int D, int NW, bool PAGED, bool FUSED, int NP>
 __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
+    const int32_t* __restrict__ live_counts, int lc_b, int lc_h, const int32_t* __restrict__ fslot, int sm_b,
+    int sm_h, const int64_t* __restrict__ fpositions, int num_pairs, int num_kv_heads,
     const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, uint8_t* __restrict__ ck,
     uint8_t* __restrict__ cv, int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b,
-    int64_t bo_h, const int32_t* __restrict__ block_tables, int64_t bt_b, int64_t bt_h, int page_shift, int paged,
-    const int32_t* __restrict__ live_counts, int64_t lc_b, int64_t lc_h, bf16_t* __restrict__ out, int64_t os_b,
-    int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int num_kv_heads, int group_size,
-    int num_pairs, int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
+    int64_t bo_h, const int32_t* __restrict__ block_tables, int bt_b, int bt_h, int page_shift, int paged,
+    bf16_t* __restrict__ out, int64_t os_b,
+    int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int group_size,
+    int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
     int64_t rcs_d, const int64_t* __restrict__ rope_pos, const DecodePre pre, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale) {
   constexpr int NT = NW * kWave;
@@ -1026,16 +1095,19 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   __shared__ float s_knew[FUSED ? D : 1], s_vnew[FUSED ? D : 1];  // appended row as stored (FP8 values)
   __shared__ int s_last;
 
-  // Work split: workgroup (pair, split) with the splits of a pair consecutive
-  // on one XCD (block ids are dispatched round-robin over the 8 XCDs, so the
-  // pair's partials meet in that XCD's L2).  Pair (b, h) takes ns = ceil(live
-  // / split_rows) splits (at most num_splits, the host's bound for the batch)
-  // of at most split_rows rows each; workgroups past ns exit after one load.
+  // Work split: workgroup (pair, split), split-major: block ids are
+  // dispatched in order, so split 0 of every pair goes out first and the
+  // workgroups past a pair's split count (the grid holds the host's bound
+  // for the batch; they exit after one load) come last instead of between
+  // the working ones.  The padded pair count is a multiple of the 8 XCDs
+  // (block ids go round-robin over them), so all splits of a pair run on one
+  // XCD and their partials meet in its L2.  Pair (b, h) takes ns =
+  // ceil(live / split_rows) splits (at most num_splits) of at most
+  // split_rows rows each.
   const int lin = blockIdx.x;
-  const int xcd = lin % kXcds;
-  const int slot_id = lin / kXcds;
-  const int pair = (slot_id / num_splits) * kXcds + xcd;
-  const int split = slot_id - (slot_id / num_splits) * num_splits;
+  const int padded_pairs = ((num_pairs + kXcds - 1) / kXcds) * kXcds;
+  const int split = lin / padded_pairs;
+  const int pair = lin - split * padded_pairs;
   if (pair >= num_pairs) return;  // uniform per workgroup
   const int b = pair / num_kv_heads;
   const int h = pair - b * num_kv_heads;
@@ -1045,7 +1117,23 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   const int jj = lane & 3, ss = lane >> 2;
   const int G = group_size;
 
-  // q elements of this thread (issued before anything they do not depend on)
+  // Prologue order (each step issues what does not depend on the step after
+  // it, so the first K/V rows arrive after three memory latencies: live
+  // count, page ids, rows): the per-pair scalars (live count, the fused
+  // step's position and append slot), then the raw rows as bits (no use
+  // before the span loads are out), then the RoPE table row.
+  int64_t fpos = 0;
+  int32_t app_slot = -1;
+  if constexpr (FUSED) fpos = fpositions[b];
+  const int live = live_counts[(int64_t)b * lc_b + (int64_t)h * lc_h];
+  if constexpr (FUSED) {
+    app_slot = fslot[(int64_t)b * sm_b + (int64_t)h * sm_h];
+    // the three loads share one wait: keeps the position load from being
+    // sunk past the early exit below into a round trip of its own
+    asm volatile("" ::"s"(fpos), "s"(live), "s"(app_slot));
+  }
+
+  // q elements of this thread (non-fused path without RoPE)
   constexpr int QPT = (4 * D + NT - 1) / NT;  // q elements per thread
   uint32_t qraw[QPT];
 #pragma unroll
@@ -1055,38 +1143,40 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     qraw[x] = (i < 4 * D && g < G) ? (uint32_t)q[b * qs_b + (int64_t)(h * G + g) * qs_h + d].bits : 0u;
   }
 
-  // fused preprocess: this thread's raw q pair, k pair or v element and the
-  // step's position, loaded before anything they do not depend on
+  // fused preprocess: this thread's raw q pair, k pair or v element (bf16
+  // bits, from one load site so that no load waits for another) and its
+  // RoPE cos / sin
   constexpr int kHalf = D / 2;
-  float fx1 = 0.0f, fx2 = 0.0f, fc = 0.0f, fsn = 0.0f;  // raw pair / element, RoPE cos and sin
+  uint32_t fb1 = 0u, fb2 = 0u;  // raw pair / element
+  float fc = 0.0f, fsn = 0.0f;  // RoPE cos and sin
   if constexpr (FUSED) {
     static_assert(NT >= 5 * kHalf + D, "one preprocess item per thread");
-    // the RoPE table row goes out with the raw rows, ahead of the span loads,
-    // so waiting for it never waits for those
-    const int64_t fpos = pre.positions[b];
+    // threads without an item (and q heads past G) read the pair's first q
+    // element and ignore it
+    const bf16_t* src = q + b * qs_b + (int64_t)(h * G) * qs_h;
+    int second = 0;  // offset of the pair's second element (0: a v element, read twice)
+    if (tid < 4 * kHalf) {
+      const int g = tid / kHalf, jx = tid - g * kHalf;
+      if (g < G) {
+        src += (int64_t)g * qs_h + jx;
+        second = kHalf;
+      }
+    } else if (tid < 5 * kHalf) {
+      src = pre.k + b * pre.ks_b + h * pre.ks_h + (tid - 4 * kHalf);
+      second = kHalf;
+    } else if (tid < 5 * kHalf + D) {
+      src = pre.v + b * pre.vs_b + h * pre.vs_h + (tid - 5 * kHalf);
+    }
+    fb1 = src[0].bits;
+    fb2 = src[second].bits;
     if (tid < 5 * kHalf) {
       const int jx = tid % kHalf;
       const float* cs = pre.cos_sin + fpos * pre.cs_p;
       fc = cs[(int64_t)jx * pre.cs_d];
       fsn = cs[(int64_t)(jx + kHalf) * pre.cs_d];
     }
-    if (tid < 4 * kHalf) {
-      const int g = tid / kHalf, jx = tid - g * kHalf;
-      if (g < G) {
-        const bf16_t* qh = q + b * qs_b + (int64_t)(h * G + g) * qs_h;
-        fx1 = ld<bf16_t>(qh + jx);
-        fx2 = ld<bf16_t>(qh + jx + kHalf);
-      }
-    } else if (tid < 5 * kHalf) {
-      const bf16_t* kh = pre.k + b * pre.ks_b + h * pre.ks_h;
-      fx1 = ld<bf16_t>(kh + tid - 4 * kHalf);
-      fx2 = ld<bf16_t>(kh + tid - 4 * kHalf + kHalf);
-    } else if (tid < 5 * kHalf + D) {
-      fx1 = ld<bf16_t>(pre.v + b * pre.vs_b + h * pre.vs_h + (tid - 5 * kHalf));
-    }
   }
 
-  const int live = live_counts[b * lc_b + h * lc_h];
   const int64_t bo = PAGED ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
   const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
   const int ns = min(num_splits, max(1, (live + split_rows - 1) / split_rows));
@@ -1097,10 +1187,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   // Fused preprocess: the step's token is rank live - 1 (slot >= 0); its row is
   // being written by this launch, so no workgroup reads it back -- the split
   // holding that rank adds the token from the values it computes itself.
-  int32_t app_slot = -1;
   bool new_tok = false;
   if constexpr (FUSED) {
-    app_slot = pre.slot[b * pre.sm_b + h * pre.sm_h];
     if (app_slot >= 0 && live > 0) {
       new_tok = t0 < live && t1 == live;
       t1 = min(t1, live - 1);
@@ -1110,9 +1198,42 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
 
   const uint8_t* kspan = PAGED ? ck : ck + bo * c_s;  // flat: the span's first row
   const uint8_t* vspan = PAGED ? cv : cv + bo * c_s;
-  MfmaGroup<D> cur;
-  int gi = wave;
-  if (gi < ngroups) mfma_load_group<D, PAGED>(cur, kspan, vspan, c_s, addr, b, h, t0 + gi * 64, t1, lane);
+  // The wave's first NP groups (wave, wave + NW, ...) all go in flight now,
+  // so the split's rows arrive after one memory latency rather than one per
+  // group.  The loads are unconditional once the split has a group: a group
+  // past the end reads row t1 - 1 (live and finite) and is never processed,
+  // which keeps the wait counts exact.  Their page ids are read first, all
+  // under one scalar wait; the raw rows issued above are waited for before
+  // the span loads go out (they have had the live-count and page-id
+  // latencies to land), so the preprocess below never waits for span rows.
+  MfmaGroup<D> buf[NP];
+  MfmaGroupAddr<D> ga[NP];
+  int32_t pid = 0;  // paged: lane 4 j + kk reads the page id of quarter kk of group j
+  if constexpr (PAGED) {
+    static_assert(4 * NP <= kWave, "one page id per lane");
+    if (ngroups > 0 && lane < 4 * NP) {
+      const int r0 = min(t0 + (wave + (lane >> 2) * NW) * 64 + 16 * (lane & 3), t1 - 1);
+      pid = block_tables[(int64_t)b * bt_b + (int64_t)h * bt_h + (r0 >> page_shift)];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): raw rows, RoPE row and page ids have landed
+  if (ngroups > 0) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int g0 = t0 + (wave + j * NW) * 64;
+      if constexpr (PAGED) {
+        int64_t qrow[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) qrow[kk] = (int64_t)__builtin_amdgcn_readlane(pid, 4 * j + kk) << page_shift;
+        mfma_group_addr_paged<D>(ga[j], kspan, vspan, c_s, qrow, page_shift, g0, t1, lane);
+      } else {
+        mfma_group_addr<D, false>(ga[j], kspan, vspan, c_s, addr, b, h, g0, t1, lane);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NP; ++j) mfma_issue_group<D>(buf[j], ga[j]);
+  }
+  [[maybe_unused]] const float fx1 = __uint_as_float(fb1 << 16), fx2 = __uint_as_float(fb2 << 16);
 
   if constexpr (FUSED) {
     // decode preprocess: q pairs (decision lane read, then zeroed), the key
@@ -1217,8 +1338,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   for (int a = 0; a < NA; ++a) acc[a][0] = acc[a][1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
   uint32_t* vt = s_vt[wave];
 
-  // One group: QK^T, V -> transposed LDS tile, online softmax, P.V.
-  auto process = [&](MfmaGroup<D>& grp, int gidx) {
+  // One group: QK^T, V -> transposed LDS tile, online softmax, P.V.  With
+  // `reload`, the group gidx + NW goes in flight in grp's registers as soon
+  // as they are consumed.
+  auto process = [&](MfmaGroup<D>& grp, int gidx, bool reload) {
     // S^T for the group: register r of lane (s, j) = S[token s + 16r][head j]
     v4f32_t sq[2];  // two independent chains
     sq[0] = sq[1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
@@ -1242,7 +1365,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     }
     // the registers are free again: the wave's next group goes in flight now
     // and lands while the softmax and P.V below run
-    if (gidx + NW < ngroups)
+    if (reload && gidx + NW < ngroups)
       mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
     // scores, online softmax per head
     const int tb = t0 + gidx * 64 + ss;
@@ -1287,7 +1410,17 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
 #undef FDMS_PV_STEP
     __builtin_amdgcn_wave_barrier();  // reads done before the next group's writes
   };
-  for (; gi < ngroups; gi += NW) process(cur, gi);  // wave-uniform
+  // the first NP groups, straight-line (wave-uniform conditions)
+#pragma unroll
+  for (int j = 0; j < NP; ++j)
+    if (wave + j * NW < ngroups) process(buf[j], wave + j * NW, false);
+  // the rest (a split of more than NW * NP groups): one group in flight
+  // ahead of the one being processed
+  int gi = wave + NW * NP;
+  if (gi < ngroups) {
+    mfma_load_group<D, PAGED>(buf[0], kspan, vspan, c_s, addr, b, h, t0 + gi * 64, t1, lane);
+    for (; gi < ngroups; gi += NW) process(buf[0], gi, true);
+  }
 
   // per wave: max, denominator, accumulators -> LDS; combine the waves
   const float lw = blocks_sum(l_j);
@@ -1436,19 +1569,24 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
     const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h)) return (int)hipErrorInvalidValue;
 #define FDMS_MFMA_ARGS                                                                                          \
-  (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h,             \
-      block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b, lc_h, (bf16_t*)out, os_b, os_h, workspace,     \
-      counters, num_kv_heads, group_size, pairs, num_splits, rows, scale, rope_cos_sin, rcs_p, rcs_d,              \
-      rope_positions, DecodePre{}, k_scale, v_scale
-#define FDMS_MFMA_LAUNCH(DD, PG)                                                                            \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
+  live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h,    \
+      (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,   \
+      page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows, scale,         \
+      rope_cos_sin, rcs_p, rcs_d, rope_positions, DecodePre{}, k_scale, v_scale
+#define FDMS_MFMA_LAUNCH(DD, PG, NPV)                                                                            \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false, NPV>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
                      (hipStream_t)stream, FDMS_MFMA_ARGS)
+#define FDMS_MFMA_NP(DD, PG) \
+  if (np == 1) FDMS_MFMA_LAUNCH(DD, PG, 1); else FDMS_MFMA_LAUNCH(DD, PG, 2);
+    const int np = fdms_attn_np(head_dim);
     if (head_dim == 64) {
-      if (paged) FDMS_MFMA_LAUNCH(64, true); else FDMS_MFMA_LAUNCH(64, false);
+      if (paged) { FDMS_MFMA_NP(64, true) } else { FDMS_MFMA_NP(64, false) }
     } else {
-      if (paged) FDMS_MFMA_LAUNCH(128, true); else FDMS_MFMA_LAUNCH(128, false);
+      if (paged) { FDMS_MFMA_NP(128, true) } else { FDMS_MFMA_NP(128, false) }
     }
+#undef FDMS_MFMA_NP
 #undef FDMS_MFMA_LAUNCH
 #undef FDMS_MFMA_ARGS
     FDMS_LAUNCH_CHECK();
@@ -1527,23 +1665,34 @@ static int fused_decode_attention(
   const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                       slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                       positive_scale};
-  // 4 waves, 8 for head_dim 128 (the preprocess needs 2.5 * head_dim threads);
-  // split_rows as for fdms_compact_decode_attention
-  const int nw = head_dim == 64 ? 4 : 8;
+  // 4 waves (or 8), 8 for head_dim 128 (the preprocess needs 2.5 * head_dim
+  // threads); split_rows as for fdms_compact_decode_attention
+  const int nw = fdms_attn_fused_waves(head_dim, pairs);
+  const int np = fdms_attn_np(head_dim);
   const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
   const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-#define FDMS_FUSED_LAUNCH(DD, NWV, PG)                                                                               \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0,     \
-                     (hipStream_t)stream, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k, (uint8_t*)compact_v,     \
-                     c_s, base_offsets, bo_b, bo_h, block_tables, bt_b, bt_h, page_shift, paged, live_counts, lc_b,   \
-                     lc_h, (bf16_t*)out, os_b, os_h, workspace, counters, num_kv_heads, group_size, pairs, num_splits, \
-                     rows, scale, nullptr, 0, 0, nullptr, pre, k_scale, v_scale)
-  if (head_dim == 64) {
-    if (paged) FDMS_FUSED_LAUNCH(64, 4, true); else FDMS_FUSED_LAUNCH(64, 4, false);
+  if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h) || !fits_i32(sm_b) ||
+      !fits_i32(sm_h))
+    return (int)hipErrorInvalidValue;
+#define FDMS_FUSED_LAUNCH(DD, NWV, PG, NPV)                                                                          \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true, NPV>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
+                     (hipStream_t)stream, live_counts, (int)lc_b, (int)lc_h, slot_mapping, (int)sm_b, (int)sm_h,      \
+                     positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,               \
+                     (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,          \
+                     page_shift, paged, (bf16_t*)out, os_b, os_h,                                                     \
+                     workspace, counters, group_size, num_splits, rows, scale, nullptr, 0, 0, nullptr, pre, k_scale,   \
+                     v_scale)
+#define FDMS_FUSED_NP(DD, NWV, PG) \
+  if (np == 1) FDMS_FUSED_LAUNCH(DD, NWV, PG, 1); else FDMS_FUSED_LAUNCH(DD, NWV, PG, 2);
+  if (head_dim == 64 && nw == 4) {
+    if (paged) { FDMS_FUSED_NP(64, 4, true) } else { FDMS_FUSED_NP(64, 4, false) }
+  } else if (head_dim == 64) {
+    if (paged) { FDMS_FUSED_NP(64, 8, true) } else { FDMS_FUSED_NP(64, 8, false) }
   } else {
-    if (paged) FDMS_FUSED_LAUNCH(128, 8, true); else FDMS_FUSED_LAUNCH(128, 8, false);
+    if (paged) { FDMS_FUSED_NP(128, 8, true) } else { FDMS_FUSED_NP(128, 8, false) }
   }
+#undef FDMS_FUSED_NP
 #undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;

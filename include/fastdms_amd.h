@@ -152,7 +152,9 @@ int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype,
  * and a pair with one split skips the merge; the other kernels ignore
  * split_rows and divide every pair's live span evenly over num_splits.  Split
  * partials are handed over with agent-scope atomic stores / loads ordered
- * around the ticket (no L2 write-back or invalidate). */
+ * around the ticket (no L2 write-back or invalidate).  The matrix-core kernel
+ * takes the live-count and block-table strides (and, fused, the slot_mapping
+ * strides) as int32: larger ones are hipErrorInvalidValue. */
 int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int64_t qs_h, const void* compact_k,
                                   const void* compact_v, int kv_dtype, int64_t c_s, const int32_t* base_offsets,
                                   int64_t bo_b, int64_t bo_h, const int32_t* block_tables, int64_t bt_b,

@@ -386,7 +386,7 @@ def test_matrix_core_heavy_tail_splits(monkeypatch, b, fused):
     ref = oatt.compact_decode_attention(qr, numerics.from_storage(ck, numerics.DT_FP8),
                                         numerics.from_storage(cv, numerics.DT_FP8), base, live)
     for target in (1, 8, 24):
-        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, waves=4, t=target: (t, 0))
+        monkeypatch.setattr(ca, "attention_split_plan", lambda device, pairs, max_live, mfma, t=target, **kw: (t, 0))
         if fused:
             # no append (slot -1): the fused kernel attends over the stored span
             kq = qd[:, :hkv].contiguous()
