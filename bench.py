@@ -190,7 +190,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     q / k / v rows read (bf16), the appended FP8 rows and the output written,
     and the int32 / int64 metadata."""
     import torch
-    from fastdms_amd.layers.compact_attention import (attention_launch_shape, attention_split_plan,
+    from fastdms_amd.layers.compact_attention import (attention_split_plan, attention_waves,
                                                       compact_decode_attention,
                                                       compact_decode_attention_paged,
                                                       fused_decode_attention_supported,
@@ -280,9 +280,8 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
     splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
     if mfma:  # per-pair split counts, as the kernel derives them (layer 0)
-        waves, groups = attention_launch_shape(d, fused, b * hkv)
-        splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma, waves=waves,
-                                                  groups_in_flight=groups, head_dim=d)
+        splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma,
+                                                  waves=attention_waves(d, fused, b * hkv), head_dim=d)
         per_pair = ((lv[0] + split_rows - 1) // split_rows).clamp(1, splits)
         splits = {"rows_per_split": split_rows, "bound": splits, "workgroups": int(per_pair.sum()),
                   "max_per_pair": int(per_pair.max())}

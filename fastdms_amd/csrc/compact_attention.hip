@@ -29,22 +29,12 @@ static bool fdms_force_generic_attention() {
   return e && e[0] == '1';
 }
 
-// Matrix-core kernel launch shape: FASTDMS_AMD_ATTN_NP = 64-row groups each
-// wave has in flight at the start (1 or 2, default 1: measured equal or
-// slower with 2 or 4, the loop being bound by the group arithmetic rather
-// than the load latency), FASTDMS_AMD_ATTN_WAVES = 4 or 8 waves per workgroup for the
+// Matrix-core kernel launch shape: FASTDMS_AMD_ATTN_WAVES = 4 or 8 waves per workgroup for the
 // fused head_dim-64 kernel (default: 8 for 17 to 128 (seq, kv head) pairs,
 // where a launch has few workgroups and each pair's rows go to more waves,
 // else 4: three workgroups fit per CU, and at 16 pairs or fewer smaller
 // splits spread the rows over more CUs).  Read per call; tuning switches
 // that change speed, never results.
-static int fdms_attn_np(int head_dim) {
-  const char* e = std::getenv("FASTDMS_AMD_ATTN_NP");
-  int np = 1;
-  if (e && (e[0] == '1' || e[0] == '2') && !e[1]) np = e[0] - '0';
-  (void)head_dim;
-  return np;
-}
 static int fdms_attn_fused_waves(int head_dim, int pairs) {
   if (head_dim == 128) return 8;  // the preprocess needs 2.5 * head_dim threads
   const char* e = std::getenv("FASTDMS_AMD_ATTN_WAVES");
@@ -1071,8 +1061,12 @@ struct DecodePre {
 // round trip off that chain (the page table is read only after the live
 // count, by when the other arguments have landed).  Strides are int32 (the
 // hosts check the range).
-template <int D, int NW, bool PAGED, bool FUSED, int NP>
-__global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
+// Four waves per SIMD asked for (at most 128 VGPRs; met at head_dim 64, not
+// at 128, which stays at 130 without spilling): once a launch fills the chip
+// the kernel is bound by how many rows are in flight (7 % faster at 128
+// sequences than at the unconstrained 130 VGPRs).
+template <int D, int NW, bool PAGED, bool FUSED>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(
     const int32_t* __restrict__ live_counts, int lc_b, int lc_h, const int32_t* __restrict__ fslot, int sm_b,
     int sm_h, const int64_t* __restrict__ fpositions, int num_pairs, int num_kv_heads,
     const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, uint8_t* __restrict__ ck,
@@ -1198,40 +1192,34 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
 
   const uint8_t* kspan = PAGED ? ck : ck + bo * c_s;  // flat: the span's first row
   const uint8_t* vspan = PAGED ? cv : cv + bo * c_s;
-  // The wave's first NP groups (wave, wave + NW, ...) all go in flight now,
-  // so the split's rows arrive after one memory latency rather than one per
-  // group.  The loads are unconditional once the split has a group: a group
-  // past the end reads row t1 - 1 (live and finite) and is never processed,
-  // which keeps the wait counts exact.  Their page ids are read first, all
-  // under one scalar wait; the raw rows issued above are waited for before
-  // the span loads go out (they have had the live-count and page-id
-  // latencies to land), so the preprocess below never waits for span rows.
-  MfmaGroup<D> buf[NP];
-  MfmaGroupAddr<D> ga[NP];
-  int32_t pid = 0;  // paged: lane 4 j + kk reads the page id of quarter kk of group j
+  // The wave's first group goes in flight now.  Its loads are unconditional
+  // once the split has a group: a wave past the end reads row t1 - 1 (live
+  // and finite) and never processes it, which keeps the wait counts exact.
+  // Its four page ids are read first (lanes 0-3, one vector load); the raw
+  // rows issued above are waited for before the span loads go out (they have
+  // had the live-count and page-id latencies to land), so the preprocess
+  // below never waits for span rows.
+  MfmaGroup<D> cur;
+  int32_t pid = 0;  // paged: lane kk reads the page id of quarter kk
   if constexpr (PAGED) {
-    static_assert(4 * NP <= kWave, "one page id per lane");
-    if (ngroups > 0 && lane < 4 * NP) {
-      const int r0 = min(t0 + (wave + (lane >> 2) * NW) * 64 + 16 * (lane & 3), t1 - 1);
+    if (ngroups > 0 && lane < 4) {
+      const int r0 = min(t0 + wave * 64 + 16 * lane, t1 - 1);
       pid = block_tables[(int64_t)b * bt_b + (int64_t)h * bt_h + (r0 >> page_shift)];
     }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): raw rows, RoPE row and page ids have landed
   if (ngroups > 0) {
+    MfmaGroupAddr<D> ga;
+    const int g0 = t0 + wave * 64;
+    if constexpr (PAGED) {
+      int64_t qrow[4];
 #pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      const int g0 = t0 + (wave + j * NW) * 64;
-      if constexpr (PAGED) {
-        int64_t qrow[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) qrow[kk] = (int64_t)__builtin_amdgcn_readlane(pid, 4 * j + kk) << page_shift;
-        mfma_group_addr_paged<D>(ga[j], kspan, vspan, c_s, qrow, page_shift, g0, t1, lane);
-      } else {
-        mfma_group_addr<D, false>(ga[j], kspan, vspan, c_s, addr, b, h, g0, t1, lane);
-      }
+      for (int kk = 0; kk < 4; ++kk) qrow[kk] = (int64_t)__builtin_amdgcn_readlane(pid, kk) << page_shift;
+      mfma_group_addr_paged<D>(ga, kspan, vspan, c_s, qrow, page_shift, g0, t1, lane);
+    } else {
+      mfma_group_addr<D, false>(ga, kspan, vspan, c_s, addr, b, h, g0, t1, lane);
     }
-#pragma unroll
-    for (int j = 0; j < NP; ++j) mfma_issue_group<D>(buf[j], ga[j]);
+    mfma_issue_group<D>(cur, ga);
   }
   [[maybe_unused]] const float fx1 = __uint_as_float(fb1 << 16), fx2 = __uint_as_float(fb2 << 16);
 
@@ -1338,10 +1326,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
   for (int a = 0; a < NA; ++a) acc[a][0] = acc[a][1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
   uint32_t* vt = s_vt[wave];
 
-  // One group: QK^T, V -> transposed LDS tile, online softmax, P.V.  With
-  // `reload`, the group gidx + NW goes in flight in grp's registers as soon
+  // One group: QK^T, V -> transposed LDS tile, online softmax, P.V; the
+  // wave's next group (gidx + NW) goes in flight in grp's registers as soon
   // as they are consumed.
-  auto process = [&](MfmaGroup<D>& grp, int gidx, bool reload) {
+  auto process = [&](MfmaGroup<D>& grp, int gidx) {
     // S^T for the group: register r of lane (s, j) = S[token s + 16r][head j]
     v4f32_t sq[2];  // two independent chains
     sq[0] = sq[1] = v4f32_t{0.f, 0.f, 0.f, 0.f};
@@ -1365,7 +1353,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
     }
     // the registers are free again: the wave's next group goes in flight now
     // and lands while the softmax and P.V below run
-    if (reload && gidx + NW < ngroups)
+    if (gidx + NW < ngroups)
       mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
     // scores, online softmax per head
     const int tb = t0 + gidx * 64 + ss;
@@ -1410,17 +1398,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_mfma_kernel(
 #undef FDMS_PV_STEP
     __builtin_amdgcn_wave_barrier();  // reads done before the next group's writes
   };
-  // the first NP groups, straight-line (wave-uniform conditions)
-#pragma unroll
-  for (int j = 0; j < NP; ++j)
-    if (wave + j * NW < ngroups) process(buf[j], wave + j * NW, false);
-  // the rest (a split of more than NW * NP groups): one group in flight
-  // ahead of the one being processed
-  int gi = wave + NW * NP;
-  if (gi < ngroups) {
-    mfma_load_group<D, PAGED>(buf[0], kspan, vspan, c_s, addr, b, h, t0 + gi * 64, t1, lane);
-    for (; gi < ngroups; gi += NW) process(buf[0], gi, true);
-  }
+  for (int gi = wave; gi < ngroups; gi += NW) process(cur, gi);  // wave-uniform
 
   // per wave: max, denominator, accumulators -> LDS; combine the waves
   const float lw = blocks_sum(l_j);
@@ -1575,18 +1553,14 @@ FDMS_EXPORT int fdms_compact_decode_attention(
       (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,   \
       page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows, scale,         \
       rope_cos_sin, rcs_p, rcs_d, rope_positions, DecodePre{}, k_scale, v_scale
-#define FDMS_MFMA_LAUNCH(DD, PG, NPV)                                                                            \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false, NPV>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
+#define FDMS_MFMA_LAUNCH(DD, PG)                                                                            \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
                      (hipStream_t)stream, FDMS_MFMA_ARGS)
-#define FDMS_MFMA_NP(DD, PG) \
-  if (np == 1) FDMS_MFMA_LAUNCH(DD, PG, 1); else FDMS_MFMA_LAUNCH(DD, PG, 2);
-    const int np = fdms_attn_np(head_dim);
     if (head_dim == 64) {
-      if (paged) { FDMS_MFMA_NP(64, true) } else { FDMS_MFMA_NP(64, false) }
+      if (paged) FDMS_MFMA_LAUNCH(64, true); else FDMS_MFMA_LAUNCH(64, false);
     } else {
-      if (paged) { FDMS_MFMA_NP(128, true) } else { FDMS_MFMA_NP(128, false) }
+      if (paged) FDMS_MFMA_LAUNCH(128, true); else FDMS_MFMA_LAUNCH(128, false);
     }
-#undef FDMS_MFMA_NP
 #undef FDMS_MFMA_LAUNCH
 #undef FDMS_MFMA_ARGS
     FDMS_LAUNCH_CHECK();
@@ -1668,31 +1642,27 @@ static int fused_decode_attention(
   // 4 waves (or 8), 8 for head_dim 128 (the preprocess needs 2.5 * head_dim
   // threads); split_rows as for fdms_compact_decode_attention
   const int nw = fdms_attn_fused_waves(head_dim, pairs);
-  const int np = fdms_attn_np(head_dim);
   const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
   const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h) || !fits_i32(sm_b) ||
       !fits_i32(sm_h))
     return (int)hipErrorInvalidValue;
-#define FDMS_FUSED_LAUNCH(DD, NWV, PG, NPV)                                                                          \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true, NPV>), dim3((unsigned)blocks), dim3(NWV * kWave), 0, \
+#define FDMS_FUSED_LAUNCH(DD, NWV, PG)                                                                               \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0,     \
                      (hipStream_t)stream, live_counts, (int)lc_b, (int)lc_h, slot_mapping, (int)sm_b, (int)sm_h,      \
                      positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,               \
                      (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,          \
                      page_shift, paged, (bf16_t*)out, os_b, os_h,                                                     \
                      workspace, counters, group_size, num_splits, rows, scale, nullptr, 0, 0, nullptr, pre, k_scale,   \
                      v_scale)
-#define FDMS_FUSED_NP(DD, NWV, PG) \
-  if (np == 1) FDMS_FUSED_LAUNCH(DD, NWV, PG, 1); else FDMS_FUSED_LAUNCH(DD, NWV, PG, 2);
   if (head_dim == 64 && nw == 4) {
-    if (paged) { FDMS_FUSED_NP(64, 4, true) } else { FDMS_FUSED_NP(64, 4, false) }
+    if (paged) FDMS_FUSED_LAUNCH(64, 4, true); else FDMS_FUSED_LAUNCH(64, 4, false);
   } else if (head_dim == 64) {
-    if (paged) { FDMS_FUSED_NP(64, 8, true) } else { FDMS_FUSED_NP(64, 8, false) }
+    if (paged) FDMS_FUSED_LAUNCH(64, 8, true); else FDMS_FUSED_LAUNCH(64, 8, false);
   } else {
-    if (paged) { FDMS_FUSED_NP(128, 8, true) } else { FDMS_FUSED_NP(128, 8, false) }
+    if (paged) FDMS_FUSED_LAUNCH(128, 8, true); else FDMS_FUSED_LAUNCH(128, 8, false);
   }
-#undef FDMS_FUSED_NP
 #undef FDMS_FUSED_LAUNCH
   FDMS_LAUNCH_CHECK();
   return 0;

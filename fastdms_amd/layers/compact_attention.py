@@ -92,36 +92,34 @@ def attention_workspace(device: torch.device, n_floats: int, n_counters: int):
 _MFMA_CAP_SPLITS = 64
 
 
-def attention_launch_shape(head_dim: int, fused: bool, pairs: int) -> tuple[int, int]:
-    """(waves per workgroup, 64-row groups each wave has in flight at the
-    start) of the matrix-core kernel for a launch over `pairs` (seq, kv head)
-    pairs, the choice fdms_compact_decode_attention and
-    fdms_fused_decode_attention[_paged] make (FASTDMS_AMD_ATTN_WAVES and
-    FASTDMS_AMD_ATTN_NP override it; speed only, never results)."""
-    env = os.environ.get("FASTDMS_AMD_ATTN_NP", "").strip()
-    groups = int(env) if env in ("1", "2") else 1
+def attention_waves(head_dim: int, fused: bool, pairs: int) -> int:
+    """Waves per workgroup of the matrix-core kernel for a launch over `pairs`
+    (seq, kv head) pairs, the choice fdms_compact_decode_attention and
+    fdms_fused_decode_attention[_paged] make (FASTDMS_AMD_ATTN_WAVES = 4 or 8
+    overrides it for the fused head_dim-64 kernel; speed only, never
+    results)."""
     if not fused:
-        return 4, groups
+        return 4
     if head_dim == 128:
-        return 8, groups
+        return 8
     env = os.environ.get("FASTDMS_AMD_ATTN_WAVES", "").strip()
     if env in ("4", "8"):
-        return int(env), groups
-    return (8 if 16 < pairs <= 128 else 4), groups
+        return int(env)
+    return 8 if 16 < pairs <= 128 else 4
 
 
-def mfma_split_rows(pairs: int, waves: int = 4, groups_in_flight: int = 1, head_dim: int = 64) -> int:
+def mfma_split_rows(pairs: int, waves: int = 4, head_dim: int = 64) -> int:
     """Rows per split of the matrix-core kernel (measured on MI355X with the
     bench's own decode states, fused paged decode kernel): with at most 128
-    (seq, kv head) pairs, two 64-row groups per wave (or as many as the waves
-    have in flight at the start; a decode step there is a chain of memory
-    round trips and more, smaller splits only add merge work), beyond that
+    (seq, kv head) pairs, two 64-row groups per wave (a decode step there is
+    a chain of memory round trips and more, smaller splits only add merge
+    work), beyond that
     1024 rows at head_dim 64 (2048 was 10-20 % slower at 32 and 128
     sequences of the 1B shape: its heavy pairs' single workgroups set the
     launch time) and 2048 at head_dim 128 (the 8B shape's pairs hold ~1600
     rows: 1024-row splits made most of them pay a merge, 25 % slower)."""
     if pairs <= 128:
-        return 64 * waves * max(2, groups_in_flight)
+        return 128 * waves
     return 1024 if head_dim <= 64 else 2048
 
 
@@ -147,7 +145,7 @@ def mfma_attention_path(q: torch.Tensor, kv: torch.Tensor, group: int) -> bool:
 
 
 def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: bool,
-                         waves: int = 4, groups_in_flight: int = 1, head_dim: int = 64) -> tuple[int, int]:
+                         waves: int = 4, head_dim: int = 64) -> tuple[int, int]:
     """(num_splits, split_rows) for fdms_compact_decode_attention.
 
     Matrix-core kernel: a pair gets one workgroup per split_rows live rows
@@ -156,7 +154,7 @@ def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: 
     bounds it from the batch's live bound (at most 64).  Other kernels:
     choose_num_splits, even splits."""
     if mfma:
-        rows = mfma_split_rows(pairs, waves, groups_in_flight, head_dim)
+        rows = mfma_split_rows(pairs, waves, head_dim)
         env = os.environ.get("FASTDMS_AMD_ATTN_SPLIT_ROWS", "").strip()
         if env.isdigit() and int(env) >= 64:  # tuning override
             rows = int(env)
@@ -193,9 +191,8 @@ def _attention_launch(q, kv_k, kv_v, *, base_offsets, block_tables, page_size, l
     pairs = batch * num_kv_heads
     # the matrix-core kernel reads pages of at least 16 rows
     mfma = mfma_attention_path(q, kv_k, group) and (block_tables is None or page_size >= 16)
-    waves, groups = attention_launch_shape(head_dim, False, pairs)
-    splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma, waves=waves, groups_in_flight=groups,
-                                              head_dim=head_dim)
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live, mfma,
+                                              waves=attention_waves(head_dim, False, pairs), head_dim=head_dim)
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     if q.stride(2) != 1 or kv_k.stride(1) != 1 or out.stride(2) != 1:
         raise ValueError("compact attention needs a contiguous head_dim axis")
@@ -456,9 +453,8 @@ def fused_dms_rope_store_compact_decode_attention(
     if out.stride(2) != 1:
         raise ValueError("out needs a contiguous head_dim axis")
     pairs = batch * num_kv_heads
-    waves, groups = attention_launch_shape(head_dim, True, pairs)
-    splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True, waves=waves,
-                                              groups_in_flight=groups, head_dim=head_dim)
+    splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True,
+                                              waves=attention_waves(head_dim, True, pairs), head_dim=head_dim)
     ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     slot_mapping = slot_mapping.to(dtype=torch.int32)
     live_counts = live_counts.to(dtype=torch.int32)
