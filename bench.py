@@ -190,7 +190,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     q / k / v rows read (bf16), the appended FP8 rows and the output written,
     and the int32 / int64 metadata."""
     import torch
-    from fastdms_amd.layers.compact_attention import (attention_split_plan, attention_waves,
+    from fastdms_amd.layers.compact_attention import (attention_split_plan, attention_waves, mfma_heavy_rows,
                                                       compact_decode_attention,
                                                       compact_decode_attention_paged,
                                                       fused_decode_attention_supported,
@@ -282,7 +282,9 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     if mfma:  # per-pair split counts, as the kernel derives them (layer 0)
         splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma,
                                                   waves=attention_waves(d, fused, b * hkv), head_dim=d)
-        per_pair = ((lv[0] + split_rows - 1) // split_rows).clamp(1, splits)
+        heavy = mfma_heavy_rows(-(-split_rows // 64) * 64, d, b * hkv)
+        per_pair = torch.where(lv[0] <= split_rows, torch.ones_like(lv[0]),
+                               (lv[0] + heavy - 1) // heavy).clamp(1, splits)
         splits = {"rows_per_split": split_rows, "bound": splits, "workgroups": int(per_pair.sum()),
                   "max_per_pair": int(per_pair.max())}
     achieved = bytes_per_launch / per_launch_s / 1e9

@@ -14,6 +14,7 @@
 // (device-scope atomic ticket) merges them and writes the output, then resets
 // its ticket to 0 so the next call (or graph replay) starts clean.  Softmax is
 // computed in the log2 domain (q pre-scaled by scale*log2 e, exp2).
+#include <algorithm>
 #include <climits>
 #include <cstdlib>
 #include <mutex>
@@ -43,6 +44,20 @@ static int fdms_attn_fused_waves(int head_dim, int pairs) {
 }
 
 static bool fits_i32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
+
+// Rows per split of a pair longer than split_rows: split_rows / div rounded
+// up to 64, div = 2 at head_dim 64 with at most 128 (seq, kv head) pairs
+// (the launch time there is set by the heavy pairs, which pay the merge
+// chain: half-size splits shorten their loops, 9.45 -> 8.74 us at c = 8),
+// else 1 (measured slower: head_dim 128 19.9 vs 17.2 us, 128 sequences
+// 0.40 vs 0.42 of HBM).  FASTDMS_AMD_ATTN_SPLIT_DIV = 1, 2 or 4 overrides
+// (tuning only).
+static int fdms_attn_heavy_rows(int rows, int head_dim, int pairs) {
+  const char* e = std::getenv("FASTDMS_AMD_ATTN_SPLIT_DIV");
+  int div = (head_dim == 64 && pairs <= 128) ? 2 : 1;
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) div = e[0] - '0';
+  return std::max(64, ((rows / div) + 63) & ~63);
+}
 
 // FASTDMS_AMD_ATTN_MFMA=0 keeps FP8 calls off the matrix-core kernel (read per
 // call; used to compare kernels on the same inputs).
@@ -1074,7 +1089,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     int64_t bo_h, const int32_t* __restrict__ block_tables, int bt_b, int bt_h, int page_shift, int paged,
     bf16_t* __restrict__ out, int64_t os_b,
     int64_t os_h, float* __restrict__ ws, int* __restrict__ counters, int group_size,
-    int num_splits, int split_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
+    int num_splits, int split_rows, int heavy_rows, float scale, const float* __restrict__ rope_cs, int64_t rcs_p,
     int64_t rcs_d, const int64_t* __restrict__ rope_pos, const DecodePre pre, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale) {
   constexpr int NT = NW * kWave;
@@ -1173,7 +1188,10 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
 
   const int64_t bo = PAGED ? 0 : (int64_t)base_offsets[b * bo_b + h * bo_h];
   const SpanAddr addr{base_offsets, block_tables, bt_b, bt_h, page_shift, paged};
-  const int ns = min(num_splits, max(1, (live + split_rows - 1) / split_rows));
+  // a pair up to split_rows rows is one workgroup (no merge); a longer one
+  // takes splits of heavy_rows rows (<= split_rows), so the pairs that pay
+  // the merge chain get shorter loops
+  const int ns = live <= split_rows ? 1 : min(num_splits, (live + heavy_rows - 1) / heavy_rows);
   if (split >= ns) return;  // uniform per workgroup
   const int per = (((live + ns - 1) / ns) + 63) & ~63;
   const int t0 = min(live, split * per);
@@ -1551,7 +1569,8 @@ FDMS_EXPORT int fdms_compact_decode_attention(
 #define FDMS_MFMA_ARGS                                                                                          \
   live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h,    \
       (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,   \
-      page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows, scale,         \
+      page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows,              \
+      fdms_attn_heavy_rows(rows, head_dim, pairs), scale,                                                                            \
       rope_cos_sin, rcs_p, rcs_d, rope_positions, DecodePre{}, k_scale, v_scale
 #define FDMS_MFMA_LAUNCH(DD, PG)                                                                            \
   hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 4, PG, false>), dim3((unsigned)blocks), dim3(4 * kWave), 0, \
@@ -1643,6 +1662,7 @@ static int fused_decode_attention(
   // threads); split_rows as for fdms_compact_decode_attention
   const int nw = fdms_attn_fused_waves(head_dim, pairs);
   const int rows = split_rows > 0 ? ((split_rows + 63) & ~63) : nw * 64;
+  const int heavy = fdms_attn_heavy_rows(rows, head_dim, pairs);
   const int64_t blocks = (int64_t)((pairs + kXcds - 1) / kXcds) * kXcds * num_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
   if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h) || !fits_i32(sm_b) ||
@@ -1654,7 +1674,8 @@ static int fused_decode_attention(
                      positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,               \
                      (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,          \
                      page_shift, paged, (bf16_t*)out, os_b, os_h,                                                     \
-                     workspace, counters, group_size, num_splits, rows, scale, nullptr, 0, 0, nullptr, pre, k_scale,   \
+                     workspace, counters, group_size, num_splits, rows, heavy, scale, nullptr, 0, 0, nullptr, pre,     \
+                     k_scale,                                                                                          \
                      v_scale)
   if (head_dim == 64 && nw == 4) {
     if (paged) FDMS_FUSED_LAUNCH(64, 4, true); else FDMS_FUSED_LAUNCH(64, 4, false);

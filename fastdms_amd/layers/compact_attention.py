@@ -123,6 +123,16 @@ def mfma_split_rows(pairs: int, waves: int = 4, head_dim: int = 64) -> int:
     return 1024 if head_dim <= 64 else 2048
 
 
+def mfma_heavy_rows(rows: int, head_dim: int, pairs: int) -> int:
+    """Rows per split of a pair longer than `rows` (the matrix-core kernel's
+    choice: half of `rows` at head_dim 64 with at most 128 pairs, else
+    `rows`; FASTDMS_AMD_ATTN_SPLIT_DIV overrides), which bounds the launch's
+    split count."""
+    env = os.environ.get("FASTDMS_AMD_ATTN_SPLIT_DIV", "").strip()
+    div = int(env) if env in ("1", "2", "4") else (2 if head_dim == 64 and pairs <= 128 else 1)
+    return max(64, -(-(rows // div) // 64) * 64)
+
+
 def reserve_attention_workspace(device: torch.device, max_pairs: int, group_size: int, head_dim: int,
                                 max_live: int = 1 << 17) -> None:
     """Allocate the split workspace for the largest split count attention_split_plan
@@ -158,7 +168,8 @@ def attention_split_plan(device: torch.device, pairs: int, max_live: int, mfma: 
         env = os.environ.get("FASTDMS_AMD_ATTN_SPLIT_ROWS", "").strip()
         if env.isdigit() and int(env) >= 64:  # tuning override
             rows = int(env)
-        return int(min(_MFMA_CAP_SPLITS, max(1, -(-int(max_live) // rows)))), rows
+        heavy = mfma_heavy_rows(-(-rows // 64) * 64, head_dim, pairs)
+        return int(min(_MFMA_CAP_SPLITS, max(1, -(-int(max_live) // heavy)))), rows
     return choose_num_splits(device, pairs, max_live), 0
 
 

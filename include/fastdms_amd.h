@@ -147,9 +147,11 @@ int fdms_store_compact_kvcache(const void* key, const void* value, int kv_dtype,
  * rope_positions != NULL rotates q in-kernel with the decision lane zeroed
  * (B4, _compact_decode_grouped_splitk_partial_qrope_kernel, compact_attention.py:418-534).
  * The matrix-core kernel (bf16 q, FP8 K/V, group_size <= 4, head_dim 64 /
- * 128) gives each pair ceil(live / split_rows) splits (split_rows rounded up
- * to 64; 0 = one 64-row group per wave of the workgroup), at most num_splits,
- * and a pair with one split skips the merge; the other kernels ignore
+ * 128) runs a pair of at most split_rows live rows (rounded up to 64; 0 = one
+ * 64-row group per wave of the workgroup) as one workgroup with no merge and
+ * splits a longer one into ceil(live / h) workgroups, at most num_splits,
+ * with h = split_rows / 2 at head_dim 64 for at most 128 (seq, kv head) pairs
+ * and h = split_rows otherwise; the other kernels ignore
  * split_rows and divide every pair's live span evenly over num_splits.  Split
  * partials are handed over with agent-scope atomic stores / loads ordered
  * around the ticket (no L2 write-back or invalidate).  The matrix-core kernel
