@@ -845,7 +845,9 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   if (k_splits > 1 && epilogue != 3 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
   if (k % k_splits) return (int)hipErrorInvalidValue;
-  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  // four waves per workgroup (eight, the override, measured 5 % slower on
+  // the 8B decode shapes and 0.8 % on the 1B ones)
+  int nw = 4;
   if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
     const int v = std::atoi(e);
     if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
@@ -960,7 +962,9 @@ FDMS_EXPORT int fdms_linear_argmax_small_m(const void* x, int64_t x_stride, int 
   if (n % 16 || k_splits < 1 || k_splits > 64 || k % k_splits) return (int)hipErrorInvalidValue;
   if (k_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
-  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  // four waves per workgroup (eight, the override, measured 5 % slower on
+  // the 8B decode shapes and 0.8 % on the 1B ones)
+  int nw = 4;
   if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
     const int v = std::atoi(e);
     if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
@@ -1095,7 +1099,9 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
   if (k_splits < 1 || k_splits > 64 || k % k_splits || (k_splits > 1 && (!workspace || !counters)))
     return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
-  int nw = (kc % (kKB * 8) == 0 && kc >= 4096) ? 8 : 4;
+  // four waves per workgroup (eight, the override, measured 5 % slower on
+  // the 8B decode shapes and 0.8 % on the 1B ones)
+  int nw = 4;
   if (const char* e = std::getenv("FASTDMS_AMD_LIN_WAVES")) {  // tuning override
     const int v = std::atoi(e);
     if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
