@@ -38,8 +38,8 @@ SIGNATURES: dict[str, str] = {
     "fdms_rope_inplace": "pillliipllpp",
     "fdms_store_compact_kvcache": "ppillllppilplliiippp",
     "fdms_compact_decode_attention": "pillppilpllpllipllpllppiiiiiifpllpppp",
-    "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifppp",
-    "fdms_fused_decode_attention_noalloc": "pllpllpllpllppllpllfffipplpllpllplliiiiiifppp",
+    "fdms_fused_decode_attention": "pllpllpllpllppllpllfffipplpllpllpllppiiiiiifppppfp",
+    "fdms_fused_decode_attention_noalloc": "pllpllpllpllppllpllfffipplpllpllplliiiiiifppppfp",
     "fdms_dms_expiry": "iplllplllplllplllppppllpiiiip",
     "fdms_prepare_decode_metadata": "plllplllpllliiip",
     "fdms_record_dms_decisions": "pllllpllllplllplllpipiiiip",
@@ -62,7 +62,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_paged_prepare_decode": "plllplllplllplllplpipiiip",
     "fdms_paged_free": "piplllplllplllplpiip",
     "fdms_paged_expiry": "iplllplllplllplllplllplpppllpiiiip",
-    "fdms_fused_decode_attention_paged": "pllpllpllpllppllpllfffipplpllipllpllppiiiiiifppp",
+    "fdms_fused_decode_attention_paged": "pllpllpllpllppllpllfffipplpllipllpllppiiiiiifppppfp",
     "fdms_fp8_gemm": "plpplpppliiip",
 }
 

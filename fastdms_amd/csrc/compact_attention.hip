@@ -1067,7 +1067,21 @@ struct DecodePre {
   int64_t ev_b, ev_h;
   float alpha_scale, alpha_offset, threshold;
   int positive_scale;
+  // Qwen3 QK-norm (or NULL): q / k rows are RMS-normalised per head with
+  // these [head_dim] bf16 weights before the decision and RoPE
+  const bf16_t* q_norm;
+  const bf16_t* k_norm;
+  float norm_eps;
 };
+
+// Sum over aligned segments of N lanes (N = 32 or 64) of a wave; every lane
+// of the wave must call it.
+template <int N>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int o = N / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 
 // The first nine arguments are what a workgroup needs before its first
 // loads (its pair, live count, and for the fused kernel the step's append
@@ -1157,6 +1171,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   // RoPE cos / sin
   constexpr int kHalf = D / 2;
   uint32_t fb1 = 0u, fb2 = 0u;  // raw pair / element
+  uint32_t fw1 = 0u, fw2 = 0u;  // QK-norm weights of the pair (bf16 bits)
   float fc = 0.0f, fsn = 0.0f;  // RoPE cos and sin
   if constexpr (FUSED) {
     static_assert(NT >= 5 * kHalf + D, "one preprocess item per thread");
@@ -1183,6 +1198,11 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
       const float* cs = pre.cos_sin + fpos * pre.cs_p;
       fc = cs[(int64_t)jx * pre.cs_d];
       fsn = cs[(int64_t)(jx + kHalf) * pre.cs_d];
+      const bf16_t* nw = tid < 4 * kHalf ? pre.q_norm : pre.k_norm;
+      if (nw) {
+        fw1 = nw[jx].bits;
+        fw2 = nw[jx + kHalf].bits;
+      }
     }
   }
 
@@ -1239,7 +1259,22 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     }
     mfma_issue_group<D>(cur, ga);
   }
-  [[maybe_unused]] const float fx1 = __uint_as_float(fb1 << 16), fx2 = __uint_as_float(fb2 << 16);
+  [[maybe_unused]] float fx1 = __uint_as_float(fb1 << 16), fx2 = __uint_as_float(fb2 << 16);
+  if constexpr (FUSED) {
+    // QK-norm (layernorm.py:19-40 on each q / k head, qwen3.py:92-94, before
+    // the DMS extraction): x_out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w).
+    // A head's kHalf pair threads are an aligned lane segment; the sum runs
+    // on every lane (no divergent shuffles) and only q / k threads use it.
+    if (pre.q_norm || pre.k_norm) {
+      const float ss = segment_sum<kHalf>(fx1 * fx1 + fx2 * fx2);
+      const bool on = tid < 4 * kHalf ? pre.q_norm != nullptr : (tid < 5 * kHalf && pre.k_norm != nullptr);
+      if (on) {
+        const float inv = rsqrtf(ss / (float)D + pre.norm_eps);
+        fx1 = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(fx1 * inv)) * __uint_as_float(fw1 << 16)));
+        fx2 = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(fx2 * inv)) * __uint_as_float(fw2 << 16)));
+      }
+    }
+  }
 
   if constexpr (FUSED) {
     // decode preprocess: q pairs (decision lane read, then zeroed), the key
@@ -1634,8 +1669,8 @@ static int fused_decode_attention(
     int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
     int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
     int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
-    const float* v_scale, void* stream, const int32_t* block_tables = nullptr, int64_t bt_b = 0, int64_t bt_h = 0,
-    int page_size = 0) {
+    const float* v_scale, const void* q_norm, const void* k_norm, float norm_eps, void* stream,
+    const int32_t* block_tables = nullptr, int64_t bt_b = 0, int64_t bt_h = 0, int page_size = 0) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4) return (int)hipErrorInvalidValue;
   if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535 || split_rows < 0)
     return (int)hipErrorInvalidValue;
@@ -1655,9 +1690,11 @@ static int fused_decode_attention(
   if (num_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
   const int pairs = batch * num_kv_heads;
   if (pairs > 65535) return (int)hipErrorInvalidValue;
+  if ((q_norm && ((uintptr_t)q_norm & 1)) || (k_norm && ((uintptr_t)k_norm & 1)) || !(norm_eps >= 0.0f))
+    return (int)hipErrorInvalidValue;
   const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                       slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
-                      positive_scale};
+                      positive_scale, (const bf16_t*)q_norm, (const bf16_t*)k_norm, norm_eps};
   // 4 waves (or 8), 8 for head_dim 128 (the preprocess needs 2.5 * head_dim
   // threads); split_rows as for fdms_compact_decode_attention
   const int nw = fdms_attn_fused_waves(head_dim, pairs);
@@ -1697,12 +1734,12 @@ FDMS_EXPORT int fdms_fused_decode_attention(
     int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
     int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
     int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
-    const float* v_scale, void* stream) {
+    const float* v_scale, const void* q_norm, const void* k_norm, float norm_eps, void* stream) {
   return fused_decode_attention(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                                 slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                                 positive_scale, compact_k, compact_v, c_s, base_offsets, bo_b, bo_h, live_counts, lc_b,
                                 lc_h, out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
-                                num_splits, split_rows, scale, k_scale, v_scale, stream);
+                                num_splits, split_rows, scale, k_scale, v_scale, q_norm, k_norm, norm_eps, stream);
 }
 
 // Paged-layout fused decode attention (no reference counterpart: the reference
@@ -1718,14 +1755,14 @@ FDMS_EXPORT int fdms_fused_decode_attention_paged(
     int64_t c_s, const int32_t* block_tables, int64_t bt_b, int64_t bt_h, int page_size, const int32_t* live_counts,
     int64_t lc_b, int64_t lc_h, void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
     int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows, float scale, const float* k_scale,
-    const float* v_scale, void* stream) {
+    const float* v_scale, const void* q_norm, const void* k_norm, float norm_eps, void* stream) {
   if (!block_tables) return (int)hipErrorInvalidValue;
   return fused_decode_attention(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                                 slot_mapping, sm_b, sm_h, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                                 positive_scale, compact_k, compact_v, c_s, nullptr, 0, 0, live_counts, lc_b, lc_h,
                                 out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
-                                num_splits, split_rows, scale, k_scale, v_scale, stream, block_tables, bt_b, bt_h,
-                                page_size);
+                                num_splits, split_rows, scale, k_scale, v_scale, q_norm, k_norm, norm_eps, stream,
+                                block_tables, bt_b, bt_h, page_size);
 }
 
 // ---------------------------------------------------------------------------
@@ -1795,7 +1832,7 @@ FDMS_EXPORT int fdms_fused_decode_attention_noalloc(
     float alpha_scale, float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v,
     int64_t c_s, const int32_t* base_offsets, int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b,
     int64_t lc_h, void* out, int64_t os_b, int64_t os_h, int batch, int num_kv_heads, int group_size, int head_dim,
-    int num_splits, int split_rows, float scale, const float* k_scale, const float* v_scale, void* stream) {
+    int num_splits, int split_rows, float scale, const float* k_scale, const float* v_scale, const void* q_norm, const void* k_norm, float norm_eps, void* stream) {
   if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4 || num_splits <= 0)
     return (int)hipErrorInvalidValue;
   // the scratch limit: pairs * num_splits * group_size * (head_dim + 2)
@@ -1812,5 +1849,5 @@ FDMS_EXPORT int fdms_fused_decode_attention_noalloc(
                                 positive_scale, compact_k, compact_v, c_s, base_offsets, bo_b, bo_h, live_counts, lc_b,
                                 lc_h, out, os_b, os_h, ws, reinterpret_cast<int*>(ws + kScratchFloats), batch,
                                 num_kv_heads, group_size, head_dim, num_splits, split_rows, scale, k_scale, v_scale,
-                                stream);
+                                q_norm, k_norm, norm_eps, stream);
 }

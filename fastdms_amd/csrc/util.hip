@@ -5,7 +5,7 @@
 
 using namespace fdms;
 
-FDMS_EXPORT int fdms_abi_version() { return 3; }
+FDMS_EXPORT int fdms_abi_version() { return 4; }
 
 __global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
                                                      int64_t n16) {

@@ -102,12 +102,20 @@ class Attention(nn.Module):
             bt = None if bt is None else bt[self.layer_id]
         return base, bt, live, slot
 
-    def forward_fused_decode(self, q, k, v, positions, cos_sin_cache, evict_out, alpha_scale, alpha_offset):
+    def forward_fused_decode(self, q, k, v, positions, cos_sin_cache, evict_out, alpha_scale, alpha_offset,
+                             q_norm=None, k_norm=None):
         """Decode step of this layer in one launch: DMS decision, RoPE, FP8
-        append of k / v and compact attention (q / k / v raw from qkv_proj)."""
+        append of k / v and compact attention (q / k / v raw from qkv_proj;
+        q_norm / k_norm: Qwen3's per-head RMSNorm modules, applied in the
+        kernel)."""
         base, bt, live, slot = self._layer_metadata(get_context())
+        norms = {}
+        if q_norm is not None or k_norm is not None:
+            norms = dict(q_norm_weight=None if q_norm is None else q_norm.weight,
+                         k_norm_weight=None if k_norm is None else k_norm.weight,
+                         norm_eps=(q_norm if q_norm is not None else k_norm).eps)
         return fused_dms_rope_store_compact_decode_attention(
             q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, slot, evict_out, positions, base,
             live, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
             scale=self.scale, max_live_count=get_context().compact_max_live_count, k_scale=self.compact_k_scale,
-            v_scale=self.compact_v_scale, block_tables=bt, page_size=PAGE_SIZE)
+            v_scale=self.compact_v_scale, block_tables=bt, page_size=PAGE_SIZE, **norms)

@@ -422,7 +422,8 @@ def fused_dms_rope_store_compact_decode_attention(
         alpha_offset: float, scale: float | None = None, max_live_count: int | None = None,
         out: torch.Tensor | None = None, k_scale: torch.Tensor | None = None,
         v_scale: torch.Tensor | None = None, block_tables: torch.Tensor | None = None,
-        page_size: int = 16) -> torch.Tensor:
+        page_size: int = 16, q_norm_weight: torch.Tensor | None = None,
+        k_norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6) -> torch.Tensor:
     """One launch for fused_dms_rope_store_compact_decode(store_q=False,
     store_transient_k=False) followed by compact_decode_attention with the q
     RoPE done in the kernel (the reference's inline-q-RoPE decode order,
@@ -432,7 +433,10 @@ def fused_dms_rope_store_compact_decode_attention(
     per-kv-head FP8 scales [Hkv] for the append and the dequant.  With
     ``block_tables`` [B, Hkv, pages] the storage is paged (rank r at row
     block_tables[b, h, r // page_size] * page_size + r % page_size) and
-    ``base_offsets`` is ignored (may be None).  Returns the attention output."""
+    ``base_offsets`` is ignored (may be None).  q_norm_weight /
+    k_norm_weight (bf16 [head_dim]): Qwen3's QK-norm applied in the kernel
+    to the raw q / k heads first (RMSNorm with norm_eps, qwen3.py:92-94).
+    Returns the attention output."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
         raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
     batch, num_q_heads, head_dim = q.shape
@@ -463,6 +467,10 @@ def fused_dms_rope_store_compact_decode_attention(
         out = torch.empty_like(q)
     if out.stride(2) != 1:
         raise ValueError("out needs a contiguous head_dim axis")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.shape != (head_dim,) or not w.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous bf16 [{head_dim}] tensor")
+    norms = (nat.ptr(q_norm_weight), nat.ptr(k_norm_weight), float(norm_eps))
     pairs = batch * num_kv_heads
     splits, split_rows = attention_split_plan(q.device, pairs, max_live_count, True,
                                               waves=attention_waves(head_dim, True, pairs), head_dim=head_dim)
@@ -486,7 +494,7 @@ def fused_dms_rope_store_compact_decode_attention(
                  live_counts.data_ptr(), live_counts.stride(0), live_counts.stride(1), out.data_ptr(), out.stride(0),
                  out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads, group, head_dim, splits,
                  split_rows, float(scale), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
-                 nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
+                 nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), *norms, nat.stream())
         return out
     base_offsets = base_offsets.to(dtype=torch.int32)
     nat.call("fdms_fused_decode_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
@@ -498,7 +506,7 @@ def fused_dms_rope_store_compact_decode_attention(
              live_counts.stride(1), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), counters.data_ptr(),
              batch, num_kv_heads, group, head_dim, splits, split_rows, float(scale),
              nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
-             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.stream())
+             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), *norms, nat.stream())
     return out
 
 

@@ -140,17 +140,20 @@ class LlamaAttention(nn.Module):
         q = qkv[:, :self.q_size].view(-1, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size:self.q_size + self.kv_size].view(-1, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size:].view(-1, self.num_kv_heads, self.head_dim)
-        if self.qk_norm:  # Qwen3: QK-norm before DMS extraction (qwen3.py:92-94)
-            q = self.q_norm(q)
-            k = self.k_norm(k)
         ctx = get_context()
         fused = False
         inline_q_rope = False
         evict_mask = None
         layer_id = self.attn.layer_id
+        can_fuse = (ctx.dms_capture_enabled and dms_fused_decode_preprocess_enabled() and not ctx.is_prefill
+                    and ctx.compact_kv_enabled and ctx.compact_slot_mapping is not None
+                    and self.attn.compact_k_cache.numel() > 0)
+        one_launch = (can_fuse and not dms_decode_store_transient_k_enabled()
+                      and fused_decode_attention_supported(q, k, v, self.attn.compact_k_cache))
+        if self.qk_norm and not one_launch:  # Qwen3: QK-norm before DMS extraction (qwen3.py:92-94)
+            q = self.q_norm(q)
+            k = self.k_norm(k)
         if ctx.dms_capture_enabled:
-            can_fuse = (dms_fused_decode_preprocess_enabled() and not ctx.is_prefill and ctx.compact_kv_enabled
-                        and ctx.compact_slot_mapping is not None and self.attn.compact_k_cache.numel() > 0)
             if ctx.dms_layer_evictions is None and ctx.dms_layer_evictions_buffer is None and not can_fuse:
                 raise RuntimeError("DMS capture requires a layer eviction recorder")
             if layer_id < 0:
@@ -158,13 +161,13 @@ class LlamaAttention(nn.Module):
             evict_out = None
             if ctx.dms_layer_evictions_buffer is not None:
                 evict_out = ctx.dms_layer_evictions_buffer[layer_id]
-            if (can_fuse and not dms_decode_store_transient_k_enabled()
-                    and fused_decode_attention_supported(q, k, v, self.attn.compact_k_cache)):
-                # decision + RoPE + append + attention in one launch
+            if one_launch:
+                # (QK-norm +) decision + RoPE + append + attention in one launch
                 if evict_out is None:
                     evict_out = torch.empty((q.shape[0], self.num_kv_heads), device=q.device, dtype=torch.bool)
                 o = self.attn.forward_fused_decode(q, k, v, positions, self.rotary_emb.cos_sin_cache, evict_out,
-                                                   ctx.dms_alpha_scale, ctx.dms_alpha_offset)
+                                                   ctx.dms_alpha_scale, ctx.dms_alpha_offset,
+                                                   *((self.q_norm, self.k_norm) if self.qk_norm else ()))
                 if ctx.dms_layer_evictions is not None:
                     ctx.dms_layer_evictions[layer_id] = evict_out
                 return o.view(o.shape[0], -1)

@@ -36,7 +36,8 @@ extern "C" {
 /* ABI version of this header (2: per-kv-head FP8 scale tables on the pack,
  * append and attention entry points; 3: the paged compact-KV entry points, the
  * FP8 GEMM, and the producer-side activation amax / FP8 split partials on
- * fdms_linear_small_m and the RMSNorm entry points). */
+ * fdms_linear_small_m and the RMSNorm entry points; 4: the QK-norm weights on
+ * the fused decode attention entry points). */
 int fdms_abi_version(void);
 
 /* Plain 16-byte-vector copy used to calibrate HBM byte counters and the copy
@@ -176,7 +177,11 @@ int fdms_compact_decode_attention(const void* q, int q_dtype, int64_t qs_b, int6
  * (skipped when < 0), and the appended token is rank live-1 of the flat span
  * (prepare_decode_metadata has already counted it).  Matrix-core path only:
  * FP8 compact K/V with 16-byte rows, group_size <= 4, head_dim 64 / 128.
- * Workspace, counters and split_rows as for fdms_compact_decode_attention. */
+ * Workspace, counters and split_rows as for fdms_compact_decode_attention.
+ * q_norm / k_norm (bf16 [head_dim], or NULL): Qwen3's QK-norm, applied to each
+ * raw q / k head first, bf16(bf16(x * rsqrt(mean(x^2) + norm_eps)) * w) as
+ * the RMSNorm entry points compute it (qwen3.py:92-94, before the DMS
+ * extraction and RoPE), replacing the two RMSNorm launches before this one. */
 int fdms_fused_decode_attention(const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b,
                                 int64_t ks_h, const void* v, int64_t vs_b, int64_t vs_h, const float* cos_sin,
                                 int64_t cs_p, int64_t cs_d, const int64_t* positions, const int32_t* slot_mapping,
@@ -186,7 +191,8 @@ int fdms_fused_decode_attention(const void* q, int64_t qs_b, int64_t qs_h, const
                                 int64_t bo_b, int64_t bo_h, const int32_t* live_counts, int64_t lc_b, int64_t lc_h,
                                 void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch,
                                 int num_kv_heads, int group_size, int head_dim, int num_splits, int split_rows,
-                                float scale, const float* k_scale, const float* v_scale, void* stream);
+                                float scale, const float* k_scale, const float* v_scale, const void* q_norm,
+                                const void* k_norm, float norm_eps, void* stream);
 
 /* Allocation-free fdms_fused_decode_attention (no reference counterpart): for
  * callers that cannot allocate (code under HIP graph capture, serving loops
@@ -208,7 +214,8 @@ int fdms_fused_decode_attention_noalloc(const void* q, int64_t qs_b, int64_t qs_
                                         const int32_t* live_counts, int64_t lc_b, int64_t lc_h, void* out,
                                         int64_t os_b, int64_t os_h, int batch, int num_kv_heads, int group_size,
                                         int head_dim, int num_splits, int split_rows, float scale,
-                                        const float* k_scale, const float* v_scale, void* stream);
+                                        const float* k_scale, const float* v_scale, const void* q_norm,
+                                        const void* k_norm, float norm_eps, void* stream);
 
 /* A12/A13 — decode expiry, full (incremental = 0) or incremental (1).  Replaces
  * _dms_expiry_kernel / dms_expiry_one_layer and _dms_expiry_incremental_kernel /
@@ -492,7 +499,7 @@ int fdms_fused_decode_attention_paged(const void* q, int64_t qs_b, int64_t qs_h,
                                       void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters,
                                       int batch, int num_kv_heads, int group_size, int head_dim, int num_splits,
                                       int split_rows, float scale, const float* k_scale, const float* v_scale,
-                                      void* stream);
+                                      const void* q_norm, const void* k_norm, float norm_eps, void* stream);
 
 /* FP8 GEMM for prefill row counts (replaces the torch._scaled_mm call of
  * _fp8_linear, linear.py:635-662): y[m, n] = bf16((sum_k x[m, k] * w[n, k]) *

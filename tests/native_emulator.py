@@ -368,16 +368,36 @@ class Emulator:
                 cvf[cv0 + r * c_s + torch.arange(D)] = tmp
         return 0
 
+    def _qk_norm(self, q, qs_b, qs_h, k, ks_b, ks_h, B, H, G, D, q_norm, k_norm, eps):
+        """Qwen3's per-head QK-norm of the fused entry points, as the RMSNorm
+        entry point computes it: (q, qs_b, qs_h, k, ks_b, ks_h) of normalised
+        copies (the caller keeps self._keep alive for the call)."""
+        def norm(ptr, sb, sh, heads, wptr, what):
+            x = self.view(ptr, torch.bfloat16, (B, heads, D), (sb, sh, 1), what).float()
+            w = self.view(wptr, torch.bfloat16, (D,), (1,), what + "_norm").float()
+            inv = torch.rsqrt((x * x).sum(-1, keepdim=True) / D + eps)
+            o = ((x * inv).to(torch.bfloat16).float() * w).to(torch.bfloat16).contiguous()
+            self._keep.append(o)
+            return o.data_ptr(), heads * D, D
+        if q_norm:
+            q, qs_b, qs_h = norm(q, qs_b, qs_h, H * G, q_norm, "q")
+        if k_norm:
+            k, ks_b, ks_h = norm(k, ks_b, ks_h, H, k_norm, "k")
+        return q, qs_b, qs_h, k, ks_b, ks_h
+
     def fused_decode_attention(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                                slot, sm_b, sm_h, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv, c_s, base,
                                bo_b, bo_h, live, lc_b, lc_h, out, os_b, os_h, ws, counters, B, H, G, D, splits,
-                               split_rows, scale, k_scale, v_scale, stream):
-        """The documented composition: preprocess (store_q = store_transient_k =
-        0) then attention with in-kernel q RoPE over the span incl. the append."""
+                               split_rows, scale, k_scale, v_scale, q_norm, k_norm, eps, stream):
+        """The documented composition: (QK-norm,) preprocess (store_q =
+        store_transient_k = 0) then attention with in-kernel q RoPE over the
+        span incl. the append."""
         if B == 0:
             return 0
         if G > 4 or D not in (64, 128):
             return 1
+        self._keep = []
+        q, qs_b, qs_h, k, ks_b, ks_h = self._qk_norm(q, qs_b, qs_h, k, ks_b, ks_h, B, H, G, D, q_norm, k_norm, eps)
         self.dms_rope_store_compact_decode(q, DT_BF16, qs_b, qs_h, k, v, DT_BF16, ks_b, ks_h, vs_b, vs_h, cos_sin,
                                            cs_p, cs_d, ck, cv, DT_FP8, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h,
                                            positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, k_scale, v_scale,
@@ -669,11 +689,14 @@ class Emulator:
     def fused_decode_attention_paged(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d,
                                      positions, slot, sm_b, sm_h, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv,
                                      c_s, bt, bt_b, bt_h, page_size, live, lc_b, lc_h, out, os_b, os_h, ws, counters,
-                                     B, H, G, D, splits, split_rows, scale, k_scale, v_scale, stream):
+                                     B, H, G, D, splits, split_rows, scale, k_scale, v_scale, q_norm, k_norm, eps,
+                                     stream):
         if B == 0:
             return 0
         if G > 4 or D not in (64, 128) or not bt:
             return 1
+        self._keep = []
+        q, qs_b, qs_h, k, ks_b, ks_h = self._qk_norm(q, qs_b, qs_h, k, ks_b, ks_h, B, H, G, D, q_norm, k_norm, eps)
         self.dms_rope_store_compact_decode(q, DT_BF16, qs_b, qs_h, k, v, DT_BF16, ks_b, ks_h, vs_b, vs_h, cos_sin,
                                            cs_p, cs_d, ck, cv, DT_FP8, c_s, slot, sm_b, sm_h, ev_out, ev_b, ev_h,
                                            positions, B, H, G, D, a_s, a_o, thr, pos_scale, 0, 0, k_scale, v_scale,

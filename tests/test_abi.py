@@ -23,7 +23,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _native.lib()
     for name in header_signatures():
         assert hasattr(lib, name), name
-    assert lib.fdms_abi_version() == 3
+    assert lib.fdms_abi_version() == 4
 
 
 def test_rejected_arguments_return_invalid_value_without_launching():

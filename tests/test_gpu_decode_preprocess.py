@@ -139,14 +139,18 @@ def test_prefill_rope_matches_apply_rotary_emb():
     assert np.array_equal(values_of(qd), qe) and np.array_equal(values_of(kd), ke)
 
 
-@pytest.mark.parametrize("d,split_rows", [(64, None), (128, None), (64, 256)])
-def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows):
+@pytest.mark.parametrize("d,split_rows,qk_norm", [(64, None, False), (128, None, False), (64, 256, False),
+                                                  (64, None, True), (128, None, True)])
+def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows, qk_norm):
     """One-launch decode preprocess + attention (fdms_fused_decode_attention) on
     Llama / Qwen3 head shapes with q/k/v as views of one qkv row: the decision
     and the appended FP8 rows bit-exact vs the oracle's preprocess (store_q off),
     q / k untouched, the output within 2e-2 of the oracle's attention over the
     span incl. the appended token; split_rows=256 splits long spans so the
-    appended token lands in the last split."""
+    appended token lands in the last split.  qk_norm: Qwen3's per-head
+    RMSNorm of q and k done in the kernel from the raw rows, vs the oracle
+    fed the normalised rows (the per-head sums of squares add up in another
+    order, so at most two appended FP8 bytes may differ)."""
     require_gpu()
     import fastdms_amd.layers.compact_attention as ca
     if split_rows is not None:
@@ -172,7 +176,19 @@ def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows):
     cache = oatt.rope_cos_sin_cache(d, 8192, 500000.0)
     ck = numerics.to_storage(rng.standard_normal((b * hkv * cap, d)).astype(np.float32), numerics.DT_FP8)
     cv = numerics.to_storage(rng.standard_normal((b * hkv * cap, d)).astype(np.float32), numerics.DT_FP8)
+    qn_w = kn_w = None
     qo, ko, cko, cvo = q.copy(), k.copy(), ck.copy(), cv.copy()
+    if qk_norm:
+        qn_w = numerics.cast((1.0 + 0.25 * rng.standard_normal(d)).astype(np.float32), numerics.DT_BF16)
+        kn_w = numerics.cast((1.0 + 0.25 * rng.standard_normal(d)).astype(np.float32), numerics.DT_BF16)
+        eps = 1e-6
+
+        def head_norm(x, w):  # layernorm.py:19-40 on each head
+            xt = torch.from_numpy(x.astype(np.float32))
+            inv = torch.rsqrt(xt.pow(2).mean(-1, keepdim=True) + eps)
+            xn = (xt * inv).to(torch.bfloat16).float()
+            return (xn * torch.from_numpy(w.astype(np.float32))).to(torch.bfloat16).float().numpy()
+        qo, ko = head_norm(q, qn_w), head_norm(k, kn_w)
     ev = oatt.fused_dms_rope_store_compact_decode(q=qo, k=ko, v=v, cos_sin_cache=cache, compact_k=cko, compact_v=cvo,
                                                   slot_mapping=slot, positions=positions, num_kv_heads=hkv,
                                                   alpha_scale=10.0, alpha_offset=5.0, q_dtype_code=numerics.DT_BF16,
@@ -191,10 +207,15 @@ def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows):
     out = ca.fused_dms_rope_store_compact_decode_attention(
         qd, kd, vd, torch.from_numpy(cache).cuda(), ckd, cvd, torch.from_numpy(slot).cuda(), evd,
         torch.from_numpy(positions).cuda(), torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda(),
-        num_kv_heads=hkv, alpha_scale=10.0, alpha_offset=5.0, max_live_count=cap)
+        num_kv_heads=hkv, alpha_scale=10.0, alpha_offset=5.0, max_live_count=cap,
+        q_norm_weight=None if qn_w is None else from_values(qn_w, numerics.DT_BF16),
+        k_norm_weight=None if kn_w is None else from_values(kn_w, numerics.DT_BF16), norm_eps=1e-6)
     torch.cuda.synchronize()
     assert np.array_equal(evd.cpu().numpy(), ev)
-    assert np.array_equal(storage_of(ckd), cko) and np.array_equal(storage_of(cvd), cvo)
+    if qk_norm:
+        assert int((storage_of(ckd) != cko).sum()) <= 2 and np.array_equal(storage_of(cvd), cvo)
+    else:
+        assert np.array_equal(storage_of(ckd), cko) and np.array_equal(storage_of(cvd), cvo)
     assert np.array_equal(values_of(qd), q) and np.array_equal(values_of(kd), k)
     got = values_of(out)
     assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= 2e-2

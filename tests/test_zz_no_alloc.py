@@ -54,7 +54,7 @@ def _run(noalloc, case, hkv, g, d, scales, splits, split_rows):
             slotd.stride(0), slotd.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), s_, off, thr, positive,
             ckd.data_ptr(), cvd.data_ptr(), d, based.data_ptr(), based.stride(0), based.stride(1), lived.data_ptr(),
             lived.stride(0), lived.stride(1), out.data_ptr(), out.stride(0), out.stride(1)]
-    tail = [b, hkv, g, d, splits, split_rows, d ** -0.5, nat.ptr(ks), nat.ptr(vs), nat.stream()]
+    tail = [b, hkv, g, d, splits, split_rows, d ** -0.5, nat.ptr(ks), nat.ptr(vs), None, None, 0.0, nat.stream()]
     if noalloc:
         nat.call("fdms_fused_decode_attention_noalloc", *head, *tail)
     else:
@@ -94,5 +94,5 @@ def test_noalloc_rejects_sizes_beyond_its_scratch():
     args = [None, 0, 0, None, 0, 0, None, 0, 0, None, 0, 0, None, None, 0, 0, None, 0, 0, 1.0, 1.0, 1.0, 1,
             None, None, 64, None, 0, 0, None, 0, 0, None, 0, 0]
     # 512 sequences x 8 heads x 64 splits x 4 x 66 floats > 2^21
-    rc = fn(*args, 512, 8, 4, 64, 64, 256, 0.125, None, None, None)
+    rc = fn(*args, 512, 8, 4, 64, 64, 256, 0.125, None, None, None, None, 0.0, None)
     assert rc == 1  # hipErrorInvalidValue
