@@ -1074,14 +1074,6 @@ struct DecodePre {
   float norm_eps;
 };
 
-// Sum over aligned segments of N lanes (N = 32 or 64) of a wave; every lane
-// of the wave must call it.
-template <int N>
-__device__ __forceinline__ float segment_sum(float v) {
-#pragma unroll
-  for (int o = N / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 // The first nine arguments are what a workgroup needs before its first
 // loads (its pair, live count, and for the fused kernel the step's append

@@ -255,6 +255,15 @@ __device__ __forceinline__ int ticket_add(int* counter) {
 
 __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
+// Sum over aligned segments of N lanes (N a power of two <= 64) of a wave;
+// every lane of the wave must call it.
+template <int N>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int o = N / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 }  // namespace fdms
 
 #define FDMS_LAUNCH_CHECK()                         \

@@ -182,6 +182,47 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
 // (heads = 1 for plain rows; heads > 1 normalises every head of a strided
 // [tokens, heads, head_dim] view, as Qwen3's q_norm / k_norm do).  Output row r
 // is at out + r * out_stride; residual / residual_out are contiguous rows.
+// Short rows (hidden = 8 T, T = 4 .. 64 lanes, e.g. Qwen3's per-head q / k
+// norms at head_dim 128): T lanes per row, 256 / T rows per workgroup, the
+// row's sum of squares a segmented wave reduction; the same formula as
+// rmsnorm_kernel, without residual or quantised outputs.  (One 256-thread
+// workgroup per 128-element head row left 15 of 16 threads idle and launched
+// millions of workgroups per prefill layer.)
+template <int T>
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const bf16_t* __restrict__ in, int64_t in_stride,
+                                                                int64_t in_head_stride, int heads,
+                                                                const bf16_t* __restrict__ weight,
+                                                                bf16_t* __restrict__ out, int64_t out_stride,
+                                                                int64_t rows, float eps) {
+  constexpr int kRows = kThreads / T;
+  const int64_t r = (int64_t)blockIdx.x * kRows + threadIdx.x / T;
+  const int c = (threadIdx.x % T) * 8;
+  const bool ok = r < rows;
+  Vec<bf16_t, 8> xv{};
+  if (ok) {
+    const int64_t tok = r / heads, hd = r - tok * heads;
+    xv = *reinterpret_cast<const Vec<bf16_t, 8>*>(in + tok * in_stride + hd * in_head_stride + c);
+  }
+  float xf[8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xf[i] = bf16_to_f32(xv.v[i].bits);
+    ss += xf[i] * xf[i];
+  }
+  ss = segment_sum<T>(ss);  // every lane, rows past the end included
+  if (!ok) return;
+  const float inv = rsqrtf(ss / (float)(8 * T) + eps);  // torch.rsqrt (layernorm.py:24, 38)
+  const Vec<bf16_t, 8> wv = *reinterpret_cast<const Vec<bf16_t, 8>*>(weight + c);
+  Vec<bf16_t, 8> o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float xn = bf16_to_f32(f32_to_bf16(xf[i] * inv));
+    o.v[i].bits = (uint16_t)f32_to_bf16(xn * bf16_to_f32(wv.v[i].bits));
+  }
+  *reinterpret_cast<Vec<bf16_t, 8>*>(out + r * out_stride + c) = o;
+}
+
 FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_stride, int heads,
                              const void* residual, const void* weight, void* out, int64_t out_stride,
                              void* residual_out, int64_t rows, int hidden, float eps, float* amax_out,
@@ -195,6 +236,24 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   // rows move as 16-byte vectors
   if (!fdms_aligned16(in, weight, out, residual, residual_out) || (in_stride | in_head_stride | out_stride) % 8)
     return (int)hipErrorInvalidValue;
+  const int lanes = hidden / 8;
+  if (!residual && !residual_out && !amax_out && !q_out && hidden <= 512 && lanes >= 4 && !(lanes & (lanes - 1))) {
+    const int64_t blocks = (rows * lanes + kThreads - 1) / kThreads;
+#define FDMS_RMSNORM_ROWS(TV)                                                                                   \
+  hipLaunchKernelGGL((rmsnorm_rows_kernel<TV>), dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream,  \
+                     (const bf16_t*)in, in_stride, in_head_stride, heads, (const bf16_t*)weight, (bf16_t*)out,       \
+                     out_stride, rows, eps)
+    switch (lanes) {
+      case 4: FDMS_RMSNORM_ROWS(4); break;
+      case 8: FDMS_RMSNORM_ROWS(8); break;
+      case 16: FDMS_RMSNORM_ROWS(16); break;
+      case 32: FDMS_RMSNORM_ROWS(32); break;
+      default: FDMS_RMSNORM_ROWS(64); break;
+    }
+#undef FDMS_RMSNORM_ROWS
+    FDMS_LAUNCH_CHECK();
+    return 0;
+  }
 #define FDMS_RMSNORM(PERV)                                                                                      \
   hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                  \
                      (hipStream_t)stream, (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight,        \

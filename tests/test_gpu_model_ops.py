@@ -50,7 +50,7 @@ def _ulp_close(got: torch.Tensor, want: torch.Tensor, what: str):
     assert not bool(bad.any()), f"{what}: {int(bad.sum())} elements beyond 1 bf16 ulp"
 
 
-@pytest.mark.parametrize("rows,hidden", [(1, 2048), (37, 256), (9, 4096), (3, 8192)])
+@pytest.mark.parametrize("rows,hidden", [(1, 2048), (37, 256), (9, 4096), (3, 8192), (100, 64), (513, 128)])
 def test_rmsnorm(rows, hidden):
     require_gpu()
     from fastdms_amd.layers.layernorm import rms_norm
