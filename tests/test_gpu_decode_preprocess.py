@@ -220,3 +220,32 @@ def test_fused_decode_attention_matches_oracle(monkeypatch, d, split_rows, qk_no
     got = values_of(out)
     assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= 2e-2
     assert g == 4
+
+    # The same step on 16-row pages in a shuffled pool (the paged entry point,
+    # whose page ids of each split's first rows are read with the live
+    # count): the decisions, the appended rows (at their page) and the output
+    # equal the span launch's bit for bit.
+    npg = b * hkv * cap // 16
+    perm = rng.permutation(npg)
+    ckp, cvp = np.empty_like(ck), np.empty_like(cv)
+    ckp.reshape(npg, 16, d)[perm] = ck.reshape(npg, 16, d)
+    cvp.reshape(npg, 16, d)[perm] = cv.reshape(npg, 16, d)
+    table = perm[(base // 16)[..., None] + np.arange(cap // 16)].astype(np.int32)
+    lp = np.minimum(live_prev, cap - 1)
+    pslot = np.where(slot >= 0, np.take_along_axis(table, (lp // 16)[..., None], 2)[..., 0] * 16 + lp % 16,
+                     -1).astype(np.int32)
+    ckpd = torch.from_numpy(ckp).cuda().view(torch.float8_e4m3fn)
+    cvpd = torch.from_numpy(cvp).cuda().view(torch.float8_e4m3fn)
+    evpd = torch.empty((b, hkv), device="cuda", dtype=torch.bool)
+    outp = ca.fused_dms_rope_store_compact_decode_attention(
+        qd, kd, vd, torch.from_numpy(cache).cuda(), ckpd, cvpd, torch.from_numpy(pslot).cuda(), evpd,
+        torch.from_numpy(positions).cuda(), torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda(),
+        num_kv_heads=hkv, alpha_scale=10.0, alpha_offset=5.0, max_live_count=cap,
+        block_tables=torch.from_numpy(table).cuda(), page_size=16,
+        q_norm_weight=None if qn_w is None else from_values(qn_w, numerics.DT_BF16),
+        k_norm_weight=None if kn_w is None else from_values(kn_w, numerics.DT_BF16), norm_eps=1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(evpd.cpu().numpy(), evd.cpu().numpy())
+    assert np.array_equal(storage_of(ckpd).reshape(npg, 16, d)[perm], storage_of(ckd).reshape(npg, 16, d))
+    assert np.array_equal(storage_of(cvpd).reshape(npg, 16, d)[perm], storage_of(cvd).reshape(npg, 16, d))
+    assert np.array_equal(values_of(outp), got)
