@@ -434,8 +434,9 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
     D = 64, keep = last 256 tokens + 1/8 of the older ones.  One HIP graph
     packs `layers` layers with their own K/V, pools and metadata (more than the
     256 MB MALL); HIP events bracket `replays` replays (each layer's pool holds
-    fresh pages for every replay).  Algorithmic bytes per layer (SURVEY
-    formula): T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written, plus the
+    fresh pages for every replay).  Algorithmic bytes per layer (every
+    prompt row's K/V and decision read, each live row stored once):
+    T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written, plus the
     counts / offsets and one table entry per page.  The kernels read only the
     kept rows' K/V, so the bytes they must move (bytes_kept: evict bytes, kept
     K/V rows, FP8 rows, metadata) are reported beside it."""
@@ -494,16 +495,16 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
     live = sum(int(x[11].sum()) for x in per_layer) / layers
     pages = sum(int(((x[11] + 15) // 16).sum()) for x in per_layer) / layers
     meta = nseq * h * (1 + chunks) * 4 + pages * 4 * 2  # live + offsets; table entries and page ids
-    survey = t_tot * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + meta
+    algo = t_tot * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + meta
     kept = t_tot * h + live * 2 * d * 2 + live * (2 * d + 5) + meta
-    achieved = survey / layer_s / 1e9
+    achieved = algo / layer_s / 1e9
     del per_layer
     return {"bound": "hbm", "layout": "paged (16-row pages)",
             "kernels": "pack_prepare_kernel<paged> + pack_scatter_kernel<paged> (one prefill layer, all sequences)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": _pmc_traffic("compaction_pmc_traffic.json", config),
-            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(survey), "tokens": t_tot,
+            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(algo), "tokens": t_tot,
             "live_rows": round(live, 1), "pages": round(pages, 1), "bytes_kept": int(kept),
             "achieved_kept": round(kept / layer_s / 1e9, 1)}
 
@@ -517,8 +518,8 @@ def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: i
     last 256 the in-window tokens (7/8 flagged), the step's position 64 past
     the window, so the 64 oldest window tokens expire (about 56 of them are
     flagged) and the rows after them move.  Each replay expires its own copy
-    of the state (`replays` copies in one graph).  Algorithmic bytes (SURVEY
-    formula): live_before * 5 metadata read + moved rows * 2 * D * 2 (K and V,
+    of the state (`replays` copies in one graph).  Algorithmic bytes (the
+    metadata read once, each moved row read and written once): live_before * 5 metadata read + moved rows * 2 * D * 2 (K and V,
     read + write) + live_after * 5 written, summed over the spans."""
     import numpy as np
     import torch
