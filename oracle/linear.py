@@ -53,16 +53,17 @@ def quantize_rows_fp8(x, torch_form: bool = False):
     return xq, x_scale
 
 
-def fp8_linear(x, w8_t, scale_inv, quantize_x: bool = True, torch_form: bool = False):
+def fp8_linear(x, w8_t, scale_inv, quantize_x: bool = True, torch_form: bool = False, w_decoded=None):
     """y[m, n] = sum_k xq[m,k] w8[k,n] * (1/x_scale[m]) * scale_inv[n].
 
     Covers the row-1 (linear.py:492-578), small-M (665-719) and _scaled_mm
     (635-662, torch_form=True) paths, which share this closed form; with
     quantize_x=False the activation is used unquantised (linear.py:509-527
-    QUANTIZE_X=False).  Returns float64 [M, N].
+    QUANTIZE_X=False).  Returns float64 [M, N].  w_decoded: the float64
+    decode of w8_t, when the caller keeps it across calls.
     """
     x = np.atleast_2d(np.asarray(x, dtype=np.float32))
-    w = numerics.e4m3fn_decode(w8_t).astype(np.float64)
+    w = numerics.e4m3fn_decode(w8_t).astype(np.float64) if w_decoded is None else w_decoded
     if quantize_x:
         xq, xs = quantize_rows_fp8(x, torch_form=torch_form)
         xv = numerics.e4m3fn_decode(xq).astype(np.float64)

@@ -111,8 +111,12 @@ class OracleModel:
             y = bf16(x @ self.int4_linear[name].T)
         elif path in ("fp8", "fp8_torch"):
             w8_t, scale_inv = self.fp8_linear[name]
+            cache = self.__dict__.setdefault("_fp8_decoded", {})  # float64 weights, decoded once per name
+            if cache.get(name, (None,))[0] is not w8_t:
+                cache[name] = (w8_t, numerics.e4m3fn_decode(w8_t).astype(np.float64))
             y = bf16(torch.from_numpy(olin.fp8_linear(x.numpy(), w8_t, scale_inv, quantize_x=True,
-                                                      torch_form=path == "fp8_torch").astype(np.float32)))
+                                                      torch_form=path == "fp8_torch",
+                                                      w_decoded=cache[name][1]).astype(np.float32)))
         else:
             quantised = False
             y = x @ self.w[name + ".weight"].T
