@@ -7,6 +7,7 @@
 //          (the appended token's DMS decision, after the forward).
 // One thread per (layer, seq, head); one launch for all layers.  Launch-bound.
 #include "fdms_common.h"
+#include "fdms_pool.h"
 
 __global__ void prepare_decode_kernel(const int32_t* __restrict__ base, int64_t b_l, int64_t b_b, int64_t b_h,
                                       int32_t* __restrict__ live, int64_t l_l, int64_t l_b, int64_t l_h,
@@ -108,12 +109,8 @@ __global__ void paged_prepare_decode_kernel(int32_t* __restrict__ live, int64_t 
   if (n >= (np << kPagedShift)) {
     int32_t got = -1;
     if (np < max_pages) {
-      const int32_t t = atomicSub(top + l, 1);
-      if (t > 0) {
-        got = stack[l * stack_stride + t - 1];
-      } else {
-        atomicAdd(top + l, 1);
-      }
+      const int32_t t = fdms::claim_units(top + l, 1);  // compare-and-swap: a failed claim writes nothing
+      if (t >= 0) got = stack[l * stack_stride + t];
     }
     if (got < 0) {
       atomicExch(overflow, 1);

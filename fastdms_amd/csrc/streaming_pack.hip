@@ -11,6 +11,7 @@
 // elements per lane, so each row moves as whole 16-byte vectors.  HBM-bound:
 // only kept rows are read (2*D*in_bytes per kept token per head) and written
 // (2*D*out_bytes), plus one evict byte per token per head.
+#include "fdms_pool.h"
 #include "fdms_vec.h"
 
 using namespace fdms;
@@ -79,7 +80,7 @@ struct PagePool {
   int32_t* held;
   int64_t hd_b, hd_h;
   int max_pages;
-  int32_t* overflow;  // set to 1 when a pop finds the pool short (the pop is undone)
+  int32_t* overflow;  // set to 1 when a pop finds the pool short (nothing is taken)
 };
 constexpr int kPageShift = 4;  // 16-row pages
 constexpr int kPackXcds = 8;
@@ -157,18 +158,12 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     if (tid == 0) {
       int p0 = -1;
       if (n > 0 && n <= pool.max_pages) {
-        bool ok = true;
-        if (pool.budget && atomicSub(pool.budget, n) < n) {
-          atomicAdd(pool.budget, n);
-          ok = false;
-        }
+        // compare-and-swap claims: a claim that fails writes nothing, so it
+        // can neither hide pages from nor hand pages to a concurrent claim
+        const bool ok = !pool.budget || claim_units(pool.budget, n) >= 0;
         if (ok) {
-          p0 = atomicSub(pool.top, n) - n;
-          if (p0 < 0) {
-            atomicAdd(pool.top, n);
-            if (pool.budget) atomicAdd(pool.budget, n);
-            p0 = -1;
-          }
+          p0 = claim_units(pool.top, n);
+          if (p0 < 0 && pool.budget) atomicAdd(pool.budget, n);  // budget back; only a later claim can see it
         }
       }
       if (p0 < 0 && n > 0) {
