@@ -34,3 +34,35 @@ def test_rejected_arguments_return_invalid_value_without_launching():
     # unaligned / odd-sized copy and a bad dtype code are rejected before any launch
     assert lib.fdms_copy_bytes(None, None, 15, 1, None) == 1
     assert lib.fdms_convert(ctypes.c_void_p(16), 9, ctypes.c_void_p(16), 0, 4, None) == 1
+
+
+def _integration_python_blocks():
+    from pathlib import Path
+    import re
+    text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    return re.findall(r"```python\n(.*?)```", text, flags=re.S)
+
+
+def test_integration_stub_signatures_match_header():
+    """Every ctypes signature string and every library call in INTEGRATION.md's
+    reference-side stub agree with include/fastdms_amd.h (argument kinds and
+    the number of arguments passed)."""
+    import ast
+    header = header_signatures()
+    blocks = _integration_python_blocks()
+    assert blocks, "INTEGRATION.md has no python stub"
+    sigs, calls = {}, []
+    for code in blocks:
+        tree = ast.parse(code)
+        for node in ast.walk(tree):
+            if isinstance(node, ast.Assign) and any(isinstance(t, ast.Name) and t.id == "_SIG" for t in node.targets):
+                sigs.update(ast.literal_eval(node.value))
+            if (isinstance(node, ast.Call) and isinstance(node.func, ast.Attribute)
+                    and node.func.attr.startswith("fdms_")):
+                calls.append((node.func.attr, len(node.args)))
+    assert sigs and calls
+    for name, sig in sigs.items():
+        assert header.get(name) == sig, f"{name}: stub {sig!r} vs header {header.get(name)!r}"
+    for name, nargs in calls:
+        assert name in sigs, f"{name} is called in the stub without a _SIG entry"
+        assert nargs == len(header[name]), f"{name}: the stub passes {nargs} arguments, the header takes {len(header[name])}"
