@@ -434,12 +434,13 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
     D = 64, keep = last 256 tokens + 1/8 of the older ones.  One HIP graph
     packs `layers` layers with their own K/V, pools and metadata (more than the
     256 MB MALL); HIP events bracket `replays` replays (each layer's pool holds
-    fresh pages for every replay).  Algorithmic bytes per layer (every
-    prompt row's K/V and decision read, each live row stored once):
-    T*H*(2*D*2 + 1) read + live*(2*D + 4 + 1) written, plus the
-    counts / offsets and one table entry per page.  The kernels read only the
-    kept rows' K/V, so the bytes they must move (bytes_kept: evict bytes, kept
-    K/V rows, FP8 rows, metadata) are reported beside it."""
+    fresh pages for every replay).  Algorithmic bytes per layer, the
+    headline `bytes` / `achieved` / `frac`: what the kernels must move --
+    T*H evict bytes + live*2*D*2 kept bf16 K/V rows read + live*(2*D + 5) FP8
+    rows and metadata written + the counts / offsets and two int32 per page
+    (table entry, page id).  `survey_formula` gives the figure that counts
+    every prompt row's K/V as read (T*H*(2*D*2 + 1) + live*(2*D + 5) +
+    metadata), which the kernels never do (they read kept rows only)."""
     import numpy as np
     import torch
     from fastdms_amd import _native as nat
@@ -464,23 +465,24 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
         cv = torch.zeros_like(ck)
         stack = torch.arange(pool, dtype=torch.int32, device="cuda")
         top = torch.full((1,), pool, dtype=torch.int32, device="cuda")
+        budget = torch.full((1,), pool, dtype=torch.int32, device="cuda")  # the whole pool: nothing is reserved
         bt = torch.full((nseq, h, max_pages), -1, dtype=torch.int32, device="cuda")
         held = torch.zeros((nseq, h), dtype=torch.int32, device="cuda")
         pos = torch.full((nseq, h, cap), -1, dtype=torch.int32, device="cuda")
         em = torch.zeros((nseq, h, cap), dtype=torch.uint8, device="cuda")
         live = torch.empty((nseq, h), dtype=torch.int32, device="cuda")
         offs = torch.empty((nseq, h, chunks), dtype=torch.int32, device="cuda")
-        per_layer.append((k, v, evict, ck, cv, stack, top, bt, held, pos, em, live, offs))
+        per_layer.append((k, v, evict, ck, cv, stack, top, bt, held, pos, em, live, offs, budget))
     rows = torch.arange(nseq, dtype=torch.int32, device="cuda")
     overflow = torch.zeros(1, dtype=torch.int32, device="cuda")
 
     def run():
-        for k, v, ev, ck, cv, stack, top, bt, held, pos, em, live, offs in per_layer:
+        for k, v, ev, ck, cv, stack, top, bt, held, pos, em, live, offs, budget in per_layer:
             nat.call("fdms_paged_pack_prepare", ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), nseq,
                      window, h, chunks, live.data_ptr(), live.stride(0), live.stride(1), offs.data_ptr(),
                      offs.stride(0), offs.stride(1), offs.stride(2), pos.data_ptr(), em.data_ptr(), rows.data_ptr(),
                      pos.stride(0), pos.stride(1), em.stride(0), em.stride(1), 0, stack.data_ptr(), top.data_ptr(),
-                     None, bt.data_ptr(), bt.stride(0), bt.stride(1), held.data_ptr(), held.stride(0),
+                     budget.data_ptr(), bt.data_ptr(), bt.stride(0), bt.stride(1), held.data_ptr(), held.stride(0),
                      held.stride(1), max_pages, overflow.data_ptr(), nat.stream())
             nat.call("fdms_paged_pack_scatter", k.data_ptr(), v.data_ptr(), nat.DT_BF16, k.stride(0), k.stride(1),
                      v.stride(0), v.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), cu.data_ptr(), nseq,
@@ -497,16 +499,21 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
     meta = nseq * h * (1 + chunks) * 4 + pages * 4 * 2  # live + offsets; table entries and page ids
     algo = t_tot * h * (2 * d * 2 + 1) + live * (2 * d + 4 + 1) + meta
     kept = t_tot * h + live * 2 * d * 2 + live * (2 * d + 5) + meta
-    achieved = algo / layer_s / 1e9
+    achieved = kept / layer_s / 1e9
     del per_layer
     return {"bound": "hbm", "layout": "paged (16-row pages)",
             "kernels": "pack_prepare_kernel<paged> + pack_scatter_kernel<paged> (one prefill layer, all sequences)",
+            "basis": "bytes the kernels must move per layer (evict bytes, kept bf16 K/V rows read, FP8 rows and "
+                     "metadata written)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes": int(kept),
             "traffic": _pmc_traffic("compaction_pmc_traffic.json", config),
-            "us_per_layer": round(layer_s * 1e6, 2), "bytes": int(algo), "tokens": t_tot,
-            "live_rows": round(live, 1), "pages": round(pages, 1), "bytes_kept": int(kept),
-            "achieved_kept": round(kept / layer_s / 1e9, 1)}
+            "us_per_layer": round(layer_s * 1e6, 2), "tokens": t_tot,
+            "live_rows": round(live, 1), "pages": round(pages, 1),
+            "survey_formula": {"what": "every prompt row's bf16 K/V counted as read: T*H*(2*D*2+1) + "
+                                       "live*(2*D+5) + metadata", "bytes": int(algo),
+                               "achieved": round(algo / layer_s / 1e9, 1),
+                               "frac": round(algo / layer_s / 1e9 / HBM_PEAK_GBPS, 4)}}
 
 
 def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: int = 8, d: int = 64,

@@ -74,13 +74,13 @@ constexpr int kPrepBatch = 32;
 struct PagePool {
   int32_t* stack;
   int32_t* top;
-  int32_t* budget;  // pages this launch may still take (debited before the stack), or nullptr
+  int32_t* budget;  // pages this launch may still take (debited before the stack; at most the stack top)
   int32_t* bt;
   int64_t bt_b, bt_h;
   int32_t* held;
   int64_t hd_b, hd_h;
   int max_pages;
-  int32_t* overflow;  // set to 1 when a pop finds the pool short (nothing is taken)
+  int32_t* overflow;  // 1: a span's pages did not fit the budget; 2: the stack was short (broken pool)
 };
 constexpr int kPageShift = 4;  // 16-row pages
 constexpr int kPackXcds = 8;
@@ -157,18 +157,16 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
     const int n = (running + (1 << kPageShift) - 1) >> kPageShift;
     if (tid == 0) {
       int p0 = -1;
-      if (n > 0 && n <= pool.max_pages) {
-        // compare-and-swap claims: a claim that fails writes nothing, so it
-        // can neither hide pages from nor hand pages to a concurrent claim
-        const bool ok = !pool.budget || claim_units(pool.budget, n) >= 0;
-        if (ok) {
-          p0 = claim_units(pool.top, n);
-          if (p0 < 0 && pool.budget) atomicAdd(pool.budget, n);  // budget back; only a later claim can see it
-        }
+      int flag = 1;
+      if (n > 0 && n <= pool.max_pages && debit_budget(pool.budget, n, DeviceSub{}, DeviceAdd{})) {
+        // the debit fitted, so (budget <= top) the stack holds the pages
+        p0 = pop_pages(pool.top, n, DeviceSub{});
+        flag = 2;  // only reached with p0 < 0: the budget exceeded the stack
       }
       if (p0 < 0 && n > 0) {
         // no pages: the span is left empty (live 0) and the launch flagged
-        atomicExch(pool.overflow, 1);
+        // (1: the budget was short; 2: the pool's precondition was broken)
+        atomicMax(pool.overflow, flag);
         live_out[b * lo_b + h * lo_h] = 0;
       }
       s_p0 = p0;
@@ -346,11 +344,13 @@ FDMS_EXPORT int fdms_streaming_pack_scatter(
 // into flat spans from a host first-fit allocator, compact_kv.py:830-857,
 // 955-1099).  Prepare = fdms_streaming_pack_prepare plus the page pop of every
 // (seq, head): ceil(live / 16) pages from the layer's free stack into the
-// span's block-table row (other entries -1) and held[row, h].  With
-// page_budget (one counter per layer) the pops of the launch also debit it
-// first, so pages kept for other sequences' decode appends stay on the stack.
-// A span whose pages do not fit (budget or stack short) gets none and live 0,
-// and *overflow is set: the caller then gives up the batch (frees its spans).
+// span's block-table row (other entries -1) and held[row, h].  Each pop first
+// debits page_budget (one counter per layer, required, at most the stack top:
+// the pages not kept for other sequences' decode appends), then takes the
+// pages off the stack; neither is retried (fdms_pool.h).  A span whose pages
+// do not fit the budget gets none and live 0, and *overflow is raised to 1:
+// the caller then gives up the batch (frees its spans).  A stack shorter than
+// a fitted debit (budget > top: a caller error) raises it to 2.
 // One layer per call; pops use atomics, so which page ids a span gets depends
 // on the order the workgroups run in (the rows a rank lands in follow the
 // table).
@@ -365,7 +365,8 @@ FDMS_EXPORT int fdms_paged_pack_prepare(const uint8_t* evict, int64_t es_t, int6
                                         int max_pages, int32_t* overflow, void* stream) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || max_chunks <= 0 || max_pages <= 0) return (int)hipErrorInvalidValue;
   if (!evict || !cu_seqlens || !live_out || !block_offsets || !positions || !evict_meta) return (int)hipErrorInvalidValue;
-  if (!page_stack || !page_top || !block_table || !pages_held || !overflow) return (int)hipErrorInvalidValue;
+  if (!page_stack || !page_top || !page_budget || !block_table || !pages_held || !overflow)
+    return (int)hipErrorInvalidValue;
   const PagePool pool{page_stack, page_top, page_budget, block_table, bt_b, bt_h, pages_held, hd_b, hd_h, max_pages,
                       overflow};
   hipLaunchKernelGGL(pack_prepare_kernel<true>, prepare_grid(num_seqs, num_kv_heads), dim3(kChunk), 0,

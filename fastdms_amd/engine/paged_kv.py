@@ -164,7 +164,11 @@ class PagedCompactKVManager(CompactKVManager):
         later); otherwise the packed sequences' bounds become their exact page
         counts."""
         self._overflow_staged = False
-        if int(self._overflow_host[0]):
+        flag = int(self._overflow_host[0])
+        if flag >= 2:
+            raise RuntimeError("paged compact KV: a page pop found the stack shorter than the prefill's page budget "
+                               "(host page accounting failed)")
+        if flag:
             self.admission_denied_count += 1
             self.overflow.zero_()
             self._prefill_check = []

@@ -427,11 +427,14 @@ int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int6
  * layer: fdms_streaming_pack_prepare plus the page pop of every (seq, head):
  * ceil(live / 16) ids from page_stack[page_top - n .. page_top) (one atomic pop
  * per span) into block_table[row, h, 0 .. n) (other entries -1), n into
- * pages_held[row, h].  page_budget (optional, one int of device memory):
- * the launch's pops debit it first and fail when it is short, which keeps
- * pages on the stack for other sequences.  A span whose pages do not fit gets
- * none and live_out 0, and *overflow is set to 1 (the caller frees the
- * batch's spans and retries it later). */
+ * pages_held[row, h].  page_budget (required, one int of device memory, at
+ * most *page_top): the launch's pops debit it first and fail when it is
+ * short, which keeps pages on the stack for other sequences.  A span whose
+ * pages do not fit gets none and live_out 0, and *overflow is raised to 1
+ * (the caller frees the batch's spans and retries it later); 2 means the stack
+ * was shorter than a debit that fitted (page_budget > *page_top: the pool
+ * state is no longer valid).  Budget debits and stack pops are single atomic
+ * subtracts, never retried: concurrent spans do not serialise. */
 int fdms_paged_pack_prepare(const uint8_t* evict, int64_t es_t, int64_t es_h, const int32_t* cu_seqlens,
                             int num_seqs, int window, int num_kv_heads, int max_chunks, int32_t* live_out,
                             int64_t lo_b, int64_t lo_h, int32_t* block_offsets, int64_t of_b, int64_t of_h,

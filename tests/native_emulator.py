@@ -581,7 +581,7 @@ class Emulator:
                            offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b, tp_h, em_b, em_h,
                            meta_cap, page_stack, page_top, page_budget, bt, bt_b, bt_h, held, hd_b, hd_h, max_pages,
                            overflow, stream):
-        if num_seqs <= 0 or H <= 0 or max_chunks <= 0 or max_pages <= 0:
+        if num_seqs <= 0 or H <= 0 or max_chunks <= 0 or max_pages <= 0 or not page_budget:
             return 1
         rc = self.streaming_pack_prepare(evict, es_t, es_h, cu, 0, num_seqs, window, H, max_chunks, live_out, lo_b,
                                          lo_h, offsets, of_b, of_h, of_c, positions, evict_meta, meta_rows, tp_b,
@@ -596,15 +596,14 @@ class Emulator:
         for b in range(num_seqs):
             for h in range(H):
                 n = (int(live[b, h]) + 15) // 16
-                got = None
+                got, flag = None, 1
                 if 0 < n <= max_pages:
-                    budget = self.view(page_budget, torch.int32, (1,), (1,), "page_budget") if page_budget else None
-                    if budget is None or int(budget[0]) >= n:
-                        got = self._pop_pages(page_stack, 0, page_top, 0, n)
-                        if got is not None and budget is not None:
-                            budget[0] -= n
+                    budget = self.view(page_budget, torch.int32, (1,), (1,), "page_budget")
+                    if int(budget[0]) >= n:  # the debit fits; the stack must then hold the pages
+                        budget[0] -= n
+                        got, flag = self._pop_pages(page_stack, 0, page_top, 0, n), 2
                 if got is None and n > 0:
-                    ov[0] = 1
+                    ov[0] = max(int(ov[0]), flag)
                     live[b, h] = 0
                 table = self.view_at(bt, torch.int32, rows[b] * bt_b + h * bt_h, (max_pages,), (1,), "block_table")
                 table.fill_(-1)

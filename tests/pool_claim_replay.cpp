@@ -2,16 +2,17 @@
 // Built with g++ by tests/test_pool_claim.py; prints "ok" and exits 0 when
 // every check holds.
 //
-// 1. The interleaving in which a subtract-then-undo pop hands one page out
-//    twice (the scheme the pool used before claim_units): replayed step by
-//    step on that scheme it must show the double hand-out (a control that the
-//    replay can see the failure), and replayed on claim_units it must not.
+// 1. The interleaving in which a subtract-then-undo pop on the stack top
+//    hands one page out twice: replayed step by step on that scheme it must
+//    show the double hand-out (a control that the replay can see the
+//    failure); replayed on claim_units, and on debit_budget + pop_pages with
+//    the same requests, it must not.
 // 2. A compare-and-swap that finds the counter moved (another claim between
 //    the caller's read and its swap) retries with the value it found.
-// 3. Many host threads claiming from one counter with real atomics: the
-//    claimed ranges are disjoint and, with the counter's final value, cover
-//    the pool exactly; every refused claim asked for more than was left at
-//    some point.
+// 3. Many host threads claiming with real atomics, through claim_units and
+//    through debit_budget + pop_pages (budget <= top): the claimed ranges are
+//    disjoint and, with the counter's final value, cover the pool exactly;
+//    no pop after a fitted debit finds the stack short.
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -49,7 +50,7 @@ static bool take(std::vector<int>& owner, int lo, int n, int who) {
   return fresh;
 }
 
-// The ADVICE interleaving on a subtract-then-undo pop: A pops 4, B asks 8 and
+// An interleaving of subtract-then-undo pops: A pops 4, B asks 8 and
 // C asks 1 (both fail and leave their subtraction in place), B undoes, D pops
 // 5, C undoes.  Each step is one atomic operation of the old scheme.
 static void replay_subtract_undo() {
@@ -109,6 +110,35 @@ static void replay_interference() {
   CHECK(fdms::claim_units(&top, 3, 5, draining) == -1 && top == 1, "give up once fewer units are left");
 }
 
+// The same requests through the pack's scheme: each claimant debits the
+// budget (subtract; add back on failure), then pops the stack (subtract).
+// The budget starts equal to the stack top, the steps interleave as above.
+static void replay_debit_pop() {
+  int top = 10, budget = 10;
+  std::vector<int> owner(10, -1);
+  auto sub = [](int* p, int n) { const int o = *p; *p -= n; return o; };
+  auto add = [](int* p, int n) { const int o = *p; *p += n; return o; };
+  // A debits 4 and pops
+  CHECK(sub(&budget, 4) >= 4, "A debit");
+  const int a = fdms::pop_pages(&top, 4, sub);
+  // B (8) and C (1) subtract from the budget: both find it short
+  const bool b_ok = sub(&budget, 8) >= 8;
+  const bool c_ok = sub(&budget, 1) >= 1;  // refused while B's deficit is in flight
+  CHECK(!b_ok && !c_ok, "B refused for real, C refused while B is failing");
+  add(&budget, 8);  // B adds back
+  // D debits 5 and pops
+  CHECK(fdms::debit_budget(&budget, 5, sub, add), "D debit");
+  const int d = fdms::pop_pages(&top, 5, sub);
+  add(&budget, 1);  // C adds back
+  CHECK(a == 6 && d == 1 && top == 1 && budget == 1, "debit/pop replay values");
+  CHECK(take(owner, a, 4, 0) && take(owner, d, 5, 3), "debit/pop: no page twice");
+  CHECK(owner[0] < 0, "debit/pop: the page below top is still free");
+  // a pop with the stack shorter than the debit (budget > top: the caller's
+  // precondition broken) reports -1 and the caller flags the pool
+  int t2 = 2;
+  CHECK(fdms::pop_pages(&t2, 3, sub) == -1, "short stack reported");
+}
+
 struct AtomicCas {
   int operator()(int* p, int expected, int desired) const {
     __atomic_compare_exchange_n(p, &expected, desired, false, __ATOMIC_ACQ_REL, __ATOMIC_ACQUIRE);
@@ -149,11 +179,50 @@ static void stress() {
   for (int i = 0; i < top; ++i) CHECK(owner[i].load() < 0, "stress: the slots below top are free");
 }
 
+static void stress_debit_pop() {
+  constexpr int kPool = 20000, kBudget = 15000, kThreads = 8, kPerThread = 3000;
+  int top = kPool, budget = kBudget;
+  std::vector<std::atomic<int>> owner(kPool);
+  for (auto& o : owner) o.store(-1);
+  std::atomic<int> dup{0}, claimed{0}, short_pops{0};
+  auto sub = [](int* p, int n) { return __atomic_fetch_sub(p, n, __ATOMIC_ACQ_REL); };
+  auto add = [](int* p, int n) { return __atomic_fetch_add(p, n, __ATOMIC_ACQ_REL); };
+  std::vector<std::thread> ts;
+  for (int w = 0; w < kThreads; ++w) {
+    ts.emplace_back([&, w] {
+      std::mt19937 rng(777 + w);
+      std::uniform_int_distribution<int> size(1, 12);
+      for (int i = 0; i < kPerThread; ++i) {
+        const int n = size(rng);
+        if (!fdms::debit_budget(&budget, n, sub, add)) continue;
+        const int lo = fdms::pop_pages(&top, n, sub);
+        if (lo < 0) {
+          ++short_pops;
+          continue;
+        }
+        claimed += n;
+        for (int j = lo; j < lo + n; ++j) {
+          int expect = -1;
+          if (!owner[j].compare_exchange_strong(expect, w)) ++dup;
+        }
+      }
+    });
+  }
+  for (auto& t : ts) t.join();
+  CHECK(short_pops.load() == 0, "debit/pop stress: no pop after a fitted debit finds the stack short");
+  CHECK(dup.load() == 0, "debit/pop stress: no page handed out twice");
+  CHECK(claimed.load() <= kBudget, "debit/pop stress: never more than the budget");
+  CHECK(claimed.load() + top == kPool && claimed.load() + budget == kBudget, "debit/pop stress: counters agree");
+  for (int i = 0; i < top; ++i) CHECK(owner[i].load() < 0, "debit/pop stress: the slots below top are free");
+}
+
 int main() {
   replay_subtract_undo();
   replay_claim_units();
   replay_interference();
+  replay_debit_pop();
   stress();
+  stress_debit_pop();
   if (failures) return 1;
   std::printf("ok\n");
   return 0;

@@ -44,13 +44,13 @@ def _integration_python_blocks():
 
 
 def test_integration_stub_signatures_match_header():
-    """Every ctypes signature string and every library call in INTEGRATION.md's
-    reference-side stub agree with include/fastdms_amd.h (argument kinds and
-    the number of arguments passed)."""
+    """Every ctypes signature string and every library call in the integration
+    guide's reference-side stub (its python blocks) agree with
+    include/fastdms_amd.h (argument kinds and the number of arguments passed)."""
     import ast
     header = header_signatures()
     blocks = _integration_python_blocks()
-    assert blocks, "INTEGRATION.md has no python stub"
+    assert blocks, "the integration guide has no python stub"
     sigs, calls = {}, []
     for code in blocks:
         tree = ast.parse(code)
