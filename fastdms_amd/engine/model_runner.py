@@ -120,6 +120,7 @@ class ModelRunner:
         self._warm: set = set()
         self.last_compact_prefill_stats: dict = {}
         self.last_dms_decode_stats: list = []
+        self.last_decode_seq_ids: list[int] = []
         self.compact_live_tokens_peak = 0
         fp8 = getattr(torch, "float8_e4m3fn", None)
         group = hf.num_attention_heads // hf.num_key_value_heads
@@ -433,6 +434,7 @@ class ModelRunner:
         overlaps the GPU; that step is then the one a later call returns."""
         mgr = self.compact_kv_manager
         batch = len(seqs)
+        self.last_decode_seq_ids = [s.seq_id for s in seqs]  # the rows of this step's logits / ids
         la, self._lookahead = self._lookahead, None
         if la is not None:  # this step is already in flight
             if la["ids"] != [s.seq_id for s in seqs]:

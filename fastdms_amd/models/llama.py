@@ -51,9 +51,11 @@ class ModelConfig:
     qk_norm: bool = False
     hidden_act: str = "silu"
     dtype: str = "bfloat16"
-    # synthetic-weights option (no checkpoint counterpart): > 0 plants a token
-    # successor table in an untied LM head, so that greedy decisions carry a
-    # wide logit margin (see models/synthetic.py)
+    # synthetic-weights option (no checkpoint counterpart): > 0 plants a
+    # previous-token attention head and a successor table in an untied LM head
+    # (the greedy token at position p is succ[token at p - 1]), so that greedy
+    # decisions carry a wide logit margin that depends on the attention
+    # (models/synthetic.py)
     successor_margin: float = 0.0
 
 

@@ -98,38 +98,116 @@ def build_synthetic_model(config: ModelConfig, *, seed: int = 0, device: str | t
     return model.eval()
 
 
-# Final residual RMS of the random model above (measured at the Llama-3.2-1B
-# shape: 3.8 after 16 layers); the planted embedding matches it.
-_EMBED_RMS = 4.0
+# The previous-token plant: query head 1 of kv head 1 in layer 0 attends to the
+# token one position back, through RoPE.  Its q and k are constants (weight
+# rows zero, biases set) in the first _PLANT_PLANES rotary planes, plane i
+# weighted _PLANT_DECAY**i, with k rotated one position ahead of q, so the
+# score at distance delta is A * sum_i w_i cos(theta_i (delta - 1)): A at
+# delta = 1 and at least 0.149 A (Llama-3.2-1B RoPE; 0.20 A Qwen3-8B) below
+# that at every other distance up to 16 384.  A = _PLANT_SCORE nats after the
+# 1/sqrt(head_dim) scale, so the head's softmax puts all but ~e^-15 of its
+# mass on the previous token, whatever else the compact KV holds.
+_PLANT_LAYER = 0
+_PLANT_PLANES = 16
+_PLANT_DECAY = 0.8
+_PLANT_SCORE = 100.0
+# RMS of the planted head's output in the residual stream (about that of the
+# rest of the final residual of these random models)
+_PLANT_RESIDUAL_RMS = 3.0
+
+
+def _plant_heads(config: ModelConfig) -> tuple[int, int]:
+    """(kv head, query head) of the planted previous-token head."""
+    g = config.num_attention_heads // config.num_key_value_heads
+    if g < 2:
+        raise ValueError("the previous-token plant needs at least two query heads per kv head")
+    kv = 1 if config.num_key_value_heads > 1 else 0
+    return kv, kv * g + 1  # query head kv*g carries the DMS decision channel
 
 
 @torch.no_grad()
 def _plant_successor_table(model, config: ModelConfig, seed: int, device, std: float) -> None:
     """Random weights give nearly flat logits: at the Llama-3.2-1B shape the
-    top two of 128 256 logits are typically 1-2 bf16 ulps apart, so any two
+    top two of 128 256 logits are typically 1-2 bf16 ulps apart, so two
     correct implementations that round differently disagree on greedy tokens
-    within a few steps.  This plants the margin a trained model has: the token
-    embeddings are scaled to the residual stream's size (so the current
-    token stays a large part of the final hidden state) and LM-head row
-    succ[t] gets successor_margin * unit(e_t) added, for a seeded permutation
-    succ.  The greedy token after t is then succ[t] by a wide margin (about
-    successor_margin * 0.7 * sqrt(hidden) logits against a random maximum
-    near 4), whatever the context contributes to the other logits."""
-    emb = model.model.embed_tokens.weight
-    e = emb.data.float() * (_EMBED_RMS / std)
-    emb.data = e.to(torch.bfloat16)
+    within a few steps.  This plants the margin a trained model has, through
+    attention: a previous-token head in layer 0 (constants above) copies its
+    value row of the previous token, W_v RMSNorm(e[prev]), through its o_proj
+    block (scaled so its output has RMS _PLANT_RESIDUAL_RMS) into the
+    residual stream as c[prev]; LM-head row succ[t] gets successor_margin *
+    unit(c[t]) added for a seeded permutation succ.  The greedy token at
+    position p is then succ[token at p - 1] by a wide margin, and it is
+    retrieved by the decode attention from the compact FP8 K/V rows appended
+    in the previous step (with RoPE of q and k at their positions): an
+    engine whose attention, RoPE, appends or K/V addressing are wrong loses
+    the previous token and with it the planted margin."""
+    kv, qh = _plant_heads(config)
+    d, hidden = config.head_dim, config.hidden_size
+    attn = model.model.layers[_PLANT_LAYER].self_attn
+    # RoPE angle per position step of each plane, from the model's own table
+    cos_sin = attn.rotary_emb.cos_sin_cache if hasattr(attn, "rotary_emb") else None
+    if cos_sin is None:
+        cos_sin = next(m.cos_sin_cache for m in model.modules() if hasattr(m, "cos_sin_cache"))
+    row1 = cos_sin[1].reshape(-1).float().to(device)
+    theta = torch.atan2(row1[d // 2:], row1[:d // 2])[:_PLANT_PLANES]
+    w = _PLANT_DECAY ** torch.arange(_PLANT_PLANES, dtype=torch.float32, device=device)
+    w = w / w.sum()
+    raw = _PLANT_SCORE * math.sqrt(d)  # q.k at distance 1, before the 1/sqrt(d) scale
+    qkv = attn.qkv_proj
+    q_rows = slice(qh * d, (qh + 1) * d)
+    k0 = config.num_attention_heads * d
+    k_rows = slice(k0 + kv * d, k0 + (kv + 1) * d)
+    qv = torch.zeros(d, device=device)
+    kv_vec = torch.zeros(d, device=device)
+    planes = torch.arange(_PLANT_PLANES, device=device)
+    if config.qk_norm:
+        # the per-head RMSNorm fixes |q| = |k| = sqrt(d) * gain on the planted
+        # dims: sqrt(w_i) per plane before the norm, the gain in the norm
+        # weights (shared by the layer's heads; the other dims keep weight 1)
+        amp = torch.sqrt(w)
+        gain = math.sqrt(raw / d)
+        for norm in (attn.q_norm, attn.k_norm):
+            nw = norm.weight.data.float()
+            nw[planes] = gain
+            nw[planes + d // 2] = gain
+            norm.weight.data = nw.to(torch.bfloat16)
+    else:
+        amp = torch.sqrt(raw * w)
+    qv[planes] = amp
+    kv_vec[planes] = amp * torch.cos(theta)
+    kv_vec[planes + d // 2] = amp * torch.sin(theta)
+    for rows, vec in ((q_rows, qv), (k_rows, kv_vec)):
+        qkv.weight.data[rows] = 0
+        qkv.bias.data[rows] = vec.to(torch.bfloat16)
+    # c[t]: what the head writes into the residual stream for previous token t
+    v_rows = slice(k0 + config.num_key_value_heads * d + kv * d, k0 + config.num_key_value_heads * d + (kv + 1) * d)
+    w_v = qkv.weight.data[v_rows].float()
+    o = attn.o_proj.weight
+    w_o = o.data[:, qh * d:(qh + 1) * d].float()
+    emb = model.model.embed_tokens.weight.data
+    unit_c = torch.empty((config.vocab_size, hidden), device=device, dtype=torch.float32)
+    rms_sum = 0.0
+    for t0 in range(0, config.vocab_size, 16384):
+        e = emb[t0:t0 + 16384].float()
+        x = e * torch.rsqrt(e.pow(2).mean(dim=1, keepdim=True) + config.rms_norm_eps)
+        c = (x @ w_v.T) @ w_o.T
+        n = c.norm(dim=1, keepdim=True)
+        rms_sum += float((n / math.sqrt(hidden)).sum())
+        unit_c[t0:t0 + 16384] = c / n.clamp_min(1e-12)
+    beta = _PLANT_RESIDUAL_RMS / (rms_sum / config.vocab_size)
+    o.data[:, qh * d:(qh + 1) * d] = (w_o * beta).to(torch.bfloat16)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed * 104729 + 17)
     succ = torch.randperm(config.vocab_size, generator=gen, device=device)
-    unit = e / e.norm(dim=1, keepdim=True)
     head = model.lm_head.weight.data.float()
-    head[succ] += float(config.successor_margin) * unit
+    head[succ] += float(config.successor_margin) * unit_c
     model.lm_head.weight.data = head.to(torch.bfloat16)
-    del e, unit, head
+    del unit_c, head
 
 
 def successor_table(config: ModelConfig, seed: int, device) -> torch.Tensor:
-    """The planted successor permutation of a model built with successor_margin."""
+    """The planted successor permutation of a model built with successor_margin:
+    the greedy token at position p is succ[token at p - 1]."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed * 104729 + 17)
     return torch.randperm(config.vocab_size, generator=gen, device=device)

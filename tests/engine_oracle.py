@@ -16,10 +16,12 @@ def int4_weights(module):
     return ((q - 8.0) * s + z).to(torch.bfloat16).float()
 
 
-def oracle_for(runner, config, *, quant: bool, dms: dict):
+def oracle_for(runner, config, *, quant: bool, dms: dict, capacity_tokens: int | None = None):
     """The CPU model oracle holding ``runner``'s weights; with ``quant`` the
     FP8 / INT4 weights of the converted linears and the modules' own route
-    decisions, so it computes what the engine's dispatch computes."""
+    decisions, so it computes what the engine's dispatch computes.
+    ``capacity_tokens``: the oracle's span arena per layer (default the
+    engine's)."""
     from oracle.model import OracleModel, weights_from_model
     model = runner.model
     kw = {}
@@ -55,5 +57,5 @@ def oracle_for(runner, config, *, quant: bool, dms: dict):
     weights = weights_from_model(model)
     return OracleModel(weights, config.hf_config, window_size=dms["dms_window_size"],
                        alpha_scale=dms["dms_alpha_scale"], alpha_offset=dms["dms_alpha_offset"],
-                       capacity_tokens=runner.compact_kv_manager.capacity_tokens,
+                       capacity_tokens=capacity_tokens or runner.compact_kv_manager.capacity_tokens,
                        max_model_len=config.max_model_len, **kw)

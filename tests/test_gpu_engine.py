@@ -302,7 +302,7 @@ def test_preempted_sequences_follow_the_oracle_on_the_gpu(monkeypatch, cap):
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_TRITON", "1")
     monkeypatch.setenv("FASTDMS_DMS_EXPIRY_INTERVAL", "1")
     monkeypatch.setenv("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
-    cfg = replace(PRESETS["tiny-llama"], successor_margin=0.3)
+    cfg = replace(PRESETS["tiny-llama"], successor_margin=1.0)
     llm = LLM(cfg, max_model_len=1024, max_num_seqs=4, max_num_batched_tokens=4096, fused_greedy_head=True,
               compact_kv_capacity_tokens=cap, compact_admission="preempt", compact_decode_reserve_tokens=4,
               compact_kv_layout="span", **DMS)
