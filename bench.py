@@ -18,7 +18,11 @@ Prints one JSON line:
                    launch / average launch time, measured with HIP events around
                    graph replays of that kernel on the live decode state
   cpu_baseline     the fp32 torch-CPU oracle (oracle/model.py) decoding the same
-                   batch from the same compact state on the host cores
+                   batch from the same compact state on the host cores, plus a
+                   labelled CPU prefill figure and the host CPU model
+  q8b_c8           (default run) the same decode harness on configs[3], the
+                   Qwen3-8B shape the metric also names: decode tok/s, prefill
+                   tok/s, greedy loop and its attention roofline (--no-8b skips)
 """
 from __future__ import annotations
 
@@ -166,6 +170,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-scaling", action="store_true", help="skip the attention batch-scaling points")
+    p.add_argument("--no-8b", action="store_true",
+                   help="l1b-c8: skip the Qwen3-8B-shape (configs[3]) decode run of the same line")
     p.add_argument("--no-fast-loop", action="store_true",
                    help="skip the device-side greedy loop over the rest of the generation (counter runs)")
     p.add_argument("--requests", type=int, default=32, help="multitenant: number of requests")
@@ -691,10 +697,128 @@ def cpu_baseline(llm, seqs, budget_s: float):
         if time.perf_counter() - t0 >= budget_s:
             break
     dt = time.perf_counter() - t0
+    # prefill: the oracle packs the first prefill_tokens of one prompt (fresh
+    # compact state, same weights); tok/s = prompt tokens / wall time, as the
+    # reference harness defines prefill throughput
+    prefill_tokens = min(1024, len(seqs[0].prompt_token_ids))
+    porc = OracleModel(orc.w, cfg, window_size=md.window_size, alpha_scale=md.alpha_scale,
+                       alpha_offset=md.alpha_offset, capacity_tokens=1 << 16, max_model_len=mgr.max_model_len,
+                       fp8_scales="calibrate" if scaled else "unit")
+    t1 = time.perf_counter()
+    porc.prefill([(0, list(seqs[0].prompt_token_ids[:prefill_tokens]), 1)])
+    pdt = time.perf_counter() - t1
     return {"value": round(len(seqs) * steps / dt, 3), "unit": "tok/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "cpu_model": _cpu_model(),
             "sample": f"{steps} decode steps of the same {len(seqs)}-sequence batch from the GPU's compact state "
-                      f"after the timed steps (fp32 torch-CPU oracle, {os.cpu_count()} host cpus)"}
+                      f"after the timed steps (fp32 torch-CPU oracle, {os.cpu_count()} host cpus)",
+            "prefill": {"value": round(prefill_tokens / pdt, 2), "unit": "tok/s",
+                        "sample": f"one {prefill_tokens}-token prompt (the first tokens of the batch's first "
+                                  f"prompt) prefilled and packed by the same oracle, all layers"}}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (what lscpu reports as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_decode_workload(args, config: str, *, extras: bool):
+    """One BASELINE decode configuration: build, warm up, prefill the batch
+    (prefill_tok_s), time args.steps decode steps of the engine (value), the
+    device-side greedy loop over the rest of the generation, and the decode
+    attention roofline on the live state.  With ``extras`` also the CPU
+    baseline, the attention batch scaling and the compaction / expiry
+    rooflines.  Returns (result dict, decode seconds)."""
+    import numpy as np
+    import torch
+    from fastdms_amd import LLM, SamplingParams
+
+    model, batch, lo, hi, workload = CONFIGS[config]
+    model = args.model or model
+    batch = args.batch or batch
+    lo = args.min_prompt or lo
+    hi = args.max_prompt or hi
+    rng = np.random.default_rng(args.seed)
+    lens = rng.integers(lo, hi + 1, batch).tolist()
+    progress(f"{config}: building {model}, prompts {lens}")
+    llm = LLM(model, max_model_len=hi + args.gen, max_num_seqs=batch, max_num_batched_tokens=sum(lens),
+              dms_window_size=256, dms_alpha_scale=10.0, dms_alpha_offset=5.0, kv_cache_dtype="float8_e4m3fn",
+              seed=args.seed, enforce_eager=args.eager, compact_kv_fp8_scales=args.kv_scales)
+    vocab = llm.config.hf_config.vocab_size
+    # warm-up generation of the same prompt lengths (first-call library set-up,
+    # graph capture), then freed; the reference times post-warm-up as well
+    progress(f"{config}: warm-up generation")
+    wrng = np.random.default_rng(args.seed + 1)
+    warm_sp = SamplingParams(temperature=0.0, max_tokens=2, ignore_eos=True)
+    for n in lens:
+        llm.add_request(wrng.integers(0, vocab, n).tolist(), warm_sp)
+    while not llm.is_finished():
+        llm.step()
+    sp = SamplingParams(temperature=0.0, max_tokens=args.gen, ignore_eos=True)
+    seqs = [llm.add_request(rng.integers(0, vocab, n).tolist(), sp) for n in lens]
+    torch.cuda.synchronize()
+    progress(f"{config}: prefill")
+    t0 = time.perf_counter()
+    llm.step()  # prefill of all prompts
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        llm.step()
+    torch.cuda.synchronize()
+    progress(f"{config}: timing {args.steps} decode steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        llm.step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    value = batch * args.steps / dt
+    progress(f"{config}: decode {value:.1f} tok/s")
+    # the engine launches a certain next decode step before reading back the
+    # current one (FASTDMS_AMD_DECODE_LOOKAHEAD): finish it before driving the
+    # runner directly
+    llm.drain()
+    fast = None
+    left = min(s.max_tokens - s.num_completion_tokens for s in seqs)
+    if left >= 8 and not args.no_fast_loop:  # the device-side greedy loop over the rest of the generation
+        progress(f"{config}: greedy fast loop, {left} steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        llm.model_runner.run_compact_greedy_decode_loop(seqs, left)
+        fast_dt = time.perf_counter() - t0
+        fast = {"tok_s": round(batch * left / fast_dt, 2), "ms_per_step": round(fast_dt / left * 1e3, 4),
+                "steps": left}
+        progress(f"{config}: fast loop {fast['tok_s']:.1f} tok/s")
+    out = {"value": round(value, 2), "ms_per_step": round(dt / args.steps * 1e3, 4),
+           "config": {"workload": workload, "model": model, "global_batch": batch, "seq_len": int(max(lens)),
+                      "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager,
+                      "kv_scales": ("per (layer, kv head), calibrated" if args.kv_scales == "calibrate"
+                                    else "unit"),
+                      "linear_weights": "fp8_e4m3 (FASTDMS_FP8_WEIGHTS=1)" if os.environ.get(
+                          "FASTDMS_FP8_WEIGHTS", "0").strip().lower() in ("1", "true", "yes", "on") else "bf16"},
+           "prefill_tok_s": round(sum(lens) / prefill_s, 1), "decode_fast_loop": fast}
+    if extras and not args.no_cpu_baseline:  # before the roofline replays re-append rows
+        progress(f"{config}: cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(llm, seqs, args.cpu_seconds)
+    progress(f"{config}: attention roofline")
+    out["roofline"] = attention_roofline(llm, seqs, args.attn_replays, config)
+    if extras:
+        progress("attention scaling")
+        out["roofline_scaling"] = attention_scaling(llm, seqs) if not args.no_scaling else None
+        progress("compaction roofline")
+        out["compaction_roofline"] = compaction_roofline(lens, config=config)
+        progress("expiry roofline")
+        out["expiry_roofline"] = expiry_roofline(config=config)
+    llm.exit()
+    del llm, seqs
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out, dt
 
 
 def main():
@@ -706,105 +830,34 @@ def main():
     # the engine steps one token at a time here (value); the device-side
     # greedy loop is timed separately on the same batch (decode_fast_loop)
     os.environ.setdefault("FASTDMS_COMPACT_GREEDY_FAST_LOOP", "0")
-    import numpy as np
-    import torch
-    from fastdms_amd import LLM, SamplingParams
-
     if args.config == "multitenant":
         return run_multitenant(args)
-    model, batch, lo, hi, workload = CONFIGS[args.config]
-    args.model = args.model or model
-    args.batch = args.batch or batch
-    args.min_prompt = args.min_prompt or lo
-    args.max_prompt = args.max_prompt or hi
     if args.warmup + args.steps > args.gen - 1:
         sys.exit(f"warmup + steps must be <= gen - 1 = {args.gen - 1}")
-    rng = np.random.default_rng(args.seed)
-    lens = rng.integers(args.min_prompt, args.max_prompt + 1, args.batch).tolist()
-    progress(f"{args.config}: building {args.model}, prompts {lens}")
-    llm = LLM(args.model, max_model_len=args.max_prompt + args.gen, max_num_seqs=args.batch,
-              max_num_batched_tokens=sum(lens), dms_window_size=256, dms_alpha_scale=10.0, dms_alpha_offset=5.0,
-              kv_cache_dtype="float8_e4m3fn", seed=args.seed, enforce_eager=args.eager,
-              compact_kv_fp8_scales=args.kv_scales)
-    vocab = llm.config.hf_config.vocab_size
-    # warm-up generation of the same prompt lengths (first-call library set-up,
-    # graph capture), then freed; the reference times post-warm-up as well
-    progress("warm-up generation")
-    wrng = np.random.default_rng(args.seed + 1)
-    warm_sp = SamplingParams(temperature=0.0, max_tokens=2, ignore_eos=True)
-    for n in lens:
-        llm.add_request(wrng.integers(0, vocab, n).tolist(), warm_sp)
-    while not llm.is_finished():
-        llm.step()
-    sp = SamplingParams(temperature=0.0, max_tokens=args.gen, ignore_eos=True)
-    seqs = [llm.add_request(rng.integers(0, vocab, n).tolist(), sp) for n in lens]
-    torch.cuda.synchronize()
-    progress("prefill")
-    t0 = time.perf_counter()
-    llm.step()  # prefill of all prompts
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    for _ in range(args.warmup):
-        llm.step()
-    torch.cuda.synchronize()
-    progress(f"timing {args.steps} decode steps")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        llm.step()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    value = args.batch * args.steps / dt
-    progress(f"decode {value:.1f} tok/s")
-    # the engine launches a certain next decode step before reading back the
-    # current one (FASTDMS_AMD_DECODE_LOOKAHEAD): finish it before driving the
-    # runner directly
-    llm.drain()
-    fast = None
-    left = min(s.max_tokens - s.num_completion_tokens for s in seqs)
-    if left >= 8 and not args.no_fast_loop:  # the device-side greedy loop over the rest of the generation
-        progress(f"greedy fast loop, {left} steps")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        llm.model_runner.run_compact_greedy_decode_loop(seqs, left)
-        fast_dt = time.perf_counter() - t0
-        fast = {"tok_s": round(args.batch * left / fast_dt, 2), "ms_per_step": round(fast_dt / left * 1e3, 4),
-                "steps": left}
-        progress(f"fast loop {fast['tok_s']:.1f} tok/s")
-    cpu = None
-    if not args.no_cpu_baseline:  # before the roofline replays re-append rows
-        progress("cpu baseline")
-        cpu = cpu_baseline(llm, seqs, args.cpu_seconds)
-    progress("attention roofline")
-    roof = attention_roofline(llm, seqs, args.attn_replays, args.config)
-    progress("attention scaling")
-    scaling = attention_scaling(llm, seqs) if not args.no_scaling else None
-    progress("compaction roofline")
-    pack = compaction_roofline(lens, config=args.config)
-    progress("expiry roofline")
-    expiry = expiry_roofline(config=args.config)
-    copy_bw = hbm_copy_gbps()
+    res, _ = run_decode_workload(args, args.config, extras=True)
+    # the metric names both shapes: the default run also times configs[3]
+    # (Qwen3-8B shape, c=8, 8192-token prompts) with the same harness
+    q8b = None
+    if args.config == "l1b-c8" and not args.no_8b and not (args.model or args.batch or args.min_prompt
+                                                           or args.max_prompt):
+        q8b, _ = run_decode_workload(args, "q8b-c8", extras=False)
     out = {
         "metric": "decode tok/s @ctx8192 c=8 (1B/8B shapes); compact-attn HBM GB/s % of peak",
-        "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "value": res["value"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16 activations/weights, fp8_e4m3 compact KV", "data": "synthetic",
-        "config": {"workload": workload,
-                   "model": args.model, "global_batch": args.batch, "seq_len": int(max(lens)),
-                   "prompt_lens": lens, "parallelism": "single GPU", "graphs": not args.eager,
-                   "kv_scales": "per (layer, kv head), calibrated" if args.kv_scales == "calibrate" else "unit",
-                   "linear_weights": "fp8_e4m3 (FASTDMS_FP8_WEIGHTS=1)" if os.environ.get(
-                       "FASTDMS_FP8_WEIGHTS", "0").strip().lower() in ("1", "true", "yes", "on") else "bf16"},
-        "prefill_tok_s": round(sum(lens) / prefill_s, 1),
-        "decode_fast_loop": fast,
-        "roofline": roof,
-        "roofline_scaling": scaling,
-        "compaction_roofline": pack,
-        "expiry_roofline": expiry,
-        "hbm_copy_gbps": round(copy_bw, 1),
-        "cpu_baseline": cpu,
+        "config": res["config"],
+        "prefill_tok_s": res["prefill_tok_s"],
+        "decode_fast_loop": res["decode_fast_loop"],
+        "roofline": res["roofline"],
+        "roofline_scaling": res.get("roofline_scaling"),
+        "compaction_roofline": res.get("compaction_roofline"),
+        "expiry_roofline": res.get("expiry_roofline"),
+        "hbm_copy_gbps": round(hbm_copy_gbps(), 1),
+        "cpu_baseline": res.get("cpu_baseline"),
+        "q8b_c8": q8b,
     }
     print(json.dumps(out))
-    llm.exit()
 
 
 if __name__ == "__main__":
