@@ -197,7 +197,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     and the int32 / int64 metadata."""
     import torch
     from fastdms_amd.layers.compact_attention import (attention_split_plan, attention_waves, mfma_heavy_rows,
-                                                      compact_decode_attention,
+                                                      compact_decode_attention, fused_decode_attention_planned,
                                                       compact_decode_attention_paged,
                                                       fused_decode_attention_supported,
                                                       fused_dms_rope_store_compact_decode_attention,
@@ -235,9 +235,35 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     cos_sin = runner.model.model.layers[0].self_attn.rotary_emb.cos_sin_cache
     fused = fused_decode_attention_supported(q, k, v, arenas[0][0])
     out = torch.empty_like(q)
+    plan = runner.decode_plan if (mgr.paged and fused) else None
+    if plan is not None:
+        # the step's work plan for this state: the plan kernel on copies of the
+        # pool state with live - 1, so it re-derives the last step's append
+        # rows (no page pops: those pages are already held) and the engine's
+        # state is left as it is
+        from fastdms_amd import _native as nat
+        lv1 = (live - 1).contiguous()
+        held = mgr.pages_held[:, start:start + b].clone()
+        bt_c = bt.clone()
+        stack, top = mgr.page_stack.clone(), mgr.page_top.clone()
+        ovf = torch.zeros(1, dtype=torch.int32, device="cuda")
+        slot_c = torch.empty_like(lv1)
+        nat.call("fdms_paged_prepare_decode_plan", lv1.data_ptr(), *lv1.stride(), slot_c.data_ptr(),
+                 *slot_c.stride(), bt_c.data_ptr(), *bt_c.stride()[:3], held.data_ptr(), *held.stride(),
+                 stack.data_ptr(), stack.stride(0), top.data_ptr(), mgr.max_pages, ovf.data_ptr(),
+                 positions.data_ptr(), plan.items.data_ptr(), plan.items.stride(0), plan.count.data_ptr(),
+                 plan.max_items, cfg.num_hidden_layers, b, hkv, nat.stream())
+        torch.cuda.synchronize()
+        if int(ovf.item()) or not torch.equal(slot_c, slot) or not torch.equal(lv1, live):
+            raise RuntimeError("attention roofline: the plan does not reproduce the decode state")
 
     def launch(l):
-        if fused:
+        if plan is not None:
+            ks, vs = mgr.layer_kv_scales(l)
+            fused_decode_attention_planned(q, k, v, cos_sin, arenas[l][0], arenas[l][1], evict, plan, l,
+                                           num_kv_heads=hkv, alpha_scale=md.alpha_scale,
+                                           alpha_offset=md.alpha_offset, out=out, k_scale=ks, v_scale=vs)
+        elif fused:
             ks, vs = mgr.layer_kv_scales(l)
             fused_dms_rope_store_compact_decode_attention(
                 q, k, v, cos_sin, arenas[l][0], arenas[l][1], slot[l], evict, positions,
@@ -285,7 +311,11 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     bytes_per_launch = (kv_bytes + io_bytes) / nl
     mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
     splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
-    if mfma:  # per-pair split counts, as the kernel derives them (layer 0)
+    if plan is not None:  # the step's work plan (layer 0)
+        per_pair = (lv[0] + 511) // 512
+        splits = {"rows_per_item": 512, "items": int(plan.count[0]), "grid": plan.grid_items(b, hkv),
+                  "max_per_pair": int(per_pair.max())}
+    elif mfma:  # per-pair split counts, as the kernel derives them (layer 0)
         splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma,
                                                   waves=attention_waves(d, fused, b * hkv), head_dim=d)
         heavy = mfma_heavy_rows(-(-split_rows // 64) * 64, d, b * hkv)
@@ -296,7 +326,8 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     achieved = bytes_per_launch / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic("decode_attention_pmc_traffic.json", config),
-            "kernel": ("decode_attn_mfma_kernel<fused>" if fused else
+            "kernel": ("decode_attn_mfma_kernel<fused, planned>" if plan is not None else
+                       "decode_attn_mfma_kernel<fused>" if fused else
                        "decode_attn_mfma_kernel" if mfma else "decode_attn_wave_kernel"),
             "layout": "paged (16-row pages)" if bt is not None else "span",
             "avg_launch_us": round(per_launch_s * 1e6, 3),

@@ -20,6 +20,7 @@
 #include <mutex>
 
 #include "fdms_common.h"
+#include "fdms_plan.h"
 
 using namespace fdms;
 
@@ -1086,8 +1087,9 @@ struct DecodePre {
 // at 128, which stays at 130 without spilling): once a launch fills the chip
 // the kernel is bound by how many rows are in flight (7 % faster at 128
 // sequences than at the unconstrained 130 VGPRs).
-template <int D, int NW, bool PAGED, bool FUSED>
+template <int D, int NW, bool PAGED, bool FUSED, bool PLANNED = false>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(
+    const int32_t* __restrict__ plan, const int32_t* __restrict__ plan_count,
     const int32_t* __restrict__ live_counts, int lc_b, int lc_h, const int32_t* __restrict__ fslot, int sm_b,
     int sm_h, const int64_t* __restrict__ fpositions, int num_pairs, int num_kv_heads,
     const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, uint8_t* __restrict__ ck,
@@ -1119,33 +1121,65 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   // XCD and their partials meet in its L2.  Pair (b, h) takes ns =
   // ceil(live / split_rows) splits (at most num_splits) of at most
   // split_rows rows each.
-  const int lin = blockIdx.x;
-  const int padded_pairs = ((num_pairs + kXcds - 1) / kXcds) * kXcds;
-  const int split = lin / padded_pairs;
-  const int pair = lin - split * padded_pairs;
-  if (pair >= num_pairs) return;  // uniform per workgroup
-  const int b = pair / num_kv_heads;
-  const int h = pair - b * num_kv_heads;
+  static_assert(!PLANNED || (PAGED && FUSED && NW * 64 == kPlanRows), "a plan item is one group per wave");
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the group loop scalar
   const int lane = tid & 63;
   const int jj = lane & 3, ss = lane >> 2;
   const int G = group_size;
-
-  // Prologue order (each step issues what does not depend on the step after
-  // it, so the first K/V rows arrive after three memory latencies: live
-  // count, page ids, rows): the per-pair scalars (live count, the fused
-  // step's position and append slot), then the raw rows as bits (no use
-  // before the span loads are out), then the RoPE table row.
+  int split, pair, b, h, live;
   int64_t fpos = 0;
   int32_t app_slot = -1;
-  if constexpr (FUSED) fpos = fpositions[b];
-  const int live = live_counts[(int64_t)b * lc_b + (int64_t)h * lc_h];
-  if constexpr (FUSED) {
-    app_slot = fslot[(int64_t)b * sm_b + (int64_t)h * sm_h];
-    // the three loads share one wait: keeps the position load from being
-    // sunk past the early exit below into a round trip of its own
-    asm volatile("" ::"s"(fpos), "s"(live), "s"(app_slot));
+  [[maybe_unused]] int plan_ns = 1, plan_t0 = 0, plan_t1 = 0;
+  [[maybe_unused]] bool plan_new = false;
+  [[maybe_unused]] int64_t plan_qrow[4] = {0, 0, 0, 0};
+  if constexpr (PLANNED) {
+    // The workgroup's plan item (fdms_plan.h), one 16-byte word per lane
+    // (lanes past the item re-read its last word), and the layer's item
+    // count, in one memory latency: everything the K/V loads need.
+    const int cnt = plan_count[0];
+    const uint4 w = reinterpret_cast<const uint4*>(plan + (int64_t)blockIdx.x * kPlanInts)[min(lane, kPlanInts / 4 - 1)];
+    if ((int)blockIdx.x >= cnt) return;  // uniform: past the step's items
+    pair = __builtin_amdgcn_readlane((int)w.x, 0);
+    plan_t0 = __builtin_amdgcn_readlane((int)w.y, 0);
+    plan_t1 = __builtin_amdgcn_readlane((int)w.z, 0);
+    const int sw = __builtin_amdgcn_readlane((int)w.w, 0);
+    live = __builtin_amdgcn_readlane((int)w.x, 1);
+    app_slot = __builtin_amdgcn_readlane((int)w.y, 1);
+    fpos = __builtin_amdgcn_readlane((int)w.z, 1);
+    plan_new = (__builtin_amdgcn_readlane((int)w.w, 1) & 1) != 0;
+    split = sw & 0xFFFF;
+    plan_ns = sw >> 16;
+    // this wave's group: the page ids of its four 16-row quarters
+    const int pl = kPlanHeader / 4 + wave;
+    plan_qrow[0] = (int64_t)__builtin_amdgcn_readlane((int)w.x, pl) << kPlanPageShift;
+    plan_qrow[1] = (int64_t)__builtin_amdgcn_readlane((int)w.y, pl) << kPlanPageShift;
+    plan_qrow[2] = (int64_t)__builtin_amdgcn_readlane((int)w.z, pl) << kPlanPageShift;
+    plan_qrow[3] = (int64_t)__builtin_amdgcn_readlane((int)w.w, pl) << kPlanPageShift;
+    b = pair / num_kv_heads;
+    h = pair - b * num_kv_heads;
+  } else {
+    const int lin = blockIdx.x;
+    const int padded_pairs = ((num_pairs + kXcds - 1) / kXcds) * kXcds;
+    split = lin / padded_pairs;
+    pair = lin - split * padded_pairs;
+    if (pair >= num_pairs) return;  // uniform per workgroup
+    b = pair / num_kv_heads;
+    h = pair - b * num_kv_heads;
+
+    // Prologue order (each step issues what does not depend on the step after
+    // it, so the first K/V rows arrive after three memory latencies: live
+    // count, page ids, rows): the per-pair scalars (live count, the fused
+    // step's position and append slot), then the raw rows as bits (no use
+    // before the span loads are out), then the RoPE table row.
+    if constexpr (FUSED) fpos = fpositions[b];
+    live = live_counts[(int64_t)b * lc_b + (int64_t)h * lc_h];
+    if constexpr (FUSED) {
+      app_slot = fslot[(int64_t)b * sm_b + (int64_t)h * sm_h];
+      // the three loads share one wait: keeps the position load from being
+      // sunk past the early exit below into a round trip of its own
+      asm volatile("" ::"s"(fpos), "s"(live), "s"(app_slot));
+    }
   }
 
   // q elements of this thread (non-fused path without RoPE)
@@ -1203,19 +1237,27 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   // a pair up to split_rows rows is one workgroup (no merge); a longer one
   // takes splits of heavy_rows rows (<= split_rows), so the pairs that pay
   // the merge chain get shorter loops
-  const int ns = live <= split_rows ? 1 : min(num_splits, (live + heavy_rows - 1) / heavy_rows);
-  if (split >= ns) return;  // uniform per workgroup
-  const int per = (((live + ns - 1) / ns) + 63) & ~63;
-  const int t0 = min(live, split * per);
-  int t1 = min(live, t0 + per);
-  // Fused preprocess: the step's token is rank live - 1 (slot >= 0); its row is
-  // being written by this launch, so no workgroup reads it back -- the split
-  // holding that rank adds the token from the values it computes itself.
+  int ns, t0, t1;
   bool new_tok = false;
-  if constexpr (FUSED) {
-    if (app_slot >= 0 && live > 0) {
-      new_tok = t0 < live && t1 == live;
-      t1 = min(t1, live - 1);
+  if constexpr (PLANNED) {
+    ns = plan_ns;
+    t0 = plan_t0;
+    t1 = plan_t1;  // the plan already leaves the appended rank out
+    new_tok = plan_new;
+  } else {
+    ns = live <= split_rows ? 1 : min(num_splits, (live + heavy_rows - 1) / heavy_rows);
+    if (split >= ns) return;  // uniform per workgroup
+    const int per = (((live + ns - 1) / ns) + 63) & ~63;
+    t0 = min(live, split * per);
+    t1 = min(live, t0 + per);
+    // Fused preprocess: the step's token is rank live - 1 (slot >= 0); its row is
+    // being written by this launch, so no workgroup reads it back -- the split
+    // holding that rank adds the token from the values it computes itself.
+    if constexpr (FUSED) {
+      if (app_slot >= 0 && live > 0) {
+        new_tok = t0 < live && t1 == live;
+        t1 = min(t1, live - 1);
+      }
     }
   }
   const int ngroups = max(0, (t1 - t0 + 63) >> 6);
@@ -1230,6 +1272,15 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   // had the live-count and page-id latencies to land), so the preprocess
   // below never waits for span rows.
   MfmaGroup<D> cur;
+  if constexpr (PLANNED) {
+    // the page ids came with the item: the group's K/V loads go out right
+    // behind the raw rows (the preprocess waits for those only)
+    if (ngroups > 0) {
+      MfmaGroupAddr<D> ga;
+      mfma_group_addr_paged<D>(ga, ck, cv, c_s, plan_qrow, kPlanPageShift, t0 + wave * 64, t1, lane);
+      mfma_issue_group<D>(cur, ga);
+    }
+  } else {
   int32_t pid = 0;  // paged: lane kk reads the page id of quarter kk
   if constexpr (PAGED) {
     if (ngroups > 0 && lane < 4) {
@@ -1250,6 +1301,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
       mfma_group_addr<D, false>(ga, kspan, vspan, c_s, addr, b, h, g0, t1, lane);
     }
     mfma_issue_group<D>(cur, ga);
+  }
   }
   [[maybe_unused]] float fx1 = __uint_as_float(fb1 << 16), fx2 = __uint_as_float(fb2 << 16);
   if constexpr (FUSED) {
@@ -1398,8 +1450,10 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     }
     // the registers are free again: the wave's next group goes in flight now
     // and lands while the softmax and P.V below run
-    if (gidx + NW < ngroups)
-      mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
+    if constexpr (!PLANNED) {  // a plan item has at most one group per wave
+      if (gidx + NW < ngroups)
+        mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
+    }
     // scores, online softmax per head
     const int tb = t0 + gidx * 64 + ss;
     float sc[4];
@@ -1594,7 +1648,8 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
     if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h)) return (int)hipErrorInvalidValue;
 #define FDMS_MFMA_ARGS                                                                                          \
-  live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h,    \
+  nullptr, nullptr, live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads,                \
+      (const bf16_t*)q, qs_b, qs_h,                                                                                   \
       (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,   \
       page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows,              \
       fdms_attn_heavy_rows(rows, head_dim, pairs), scale,                                                                            \
@@ -1699,7 +1754,8 @@ static int fused_decode_attention(
     return (int)hipErrorInvalidValue;
 #define FDMS_FUSED_LAUNCH(DD, NWV, PG)                                                                               \
   hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0,     \
-                     (hipStream_t)stream, live_counts, (int)lc_b, (int)lc_h, slot_mapping, (int)sm_b, (int)sm_h,      \
+                     (hipStream_t)stream, nullptr, nullptr, live_counts, (int)lc_b, (int)lc_h, slot_mapping,          \
+                     (int)sm_b, (int)sm_h,                                                                            \
                      positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,               \
                      (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,          \
                      page_shift, paged, (bf16_t*)out, os_b, os_h,                                                     \
@@ -1755,6 +1811,53 @@ FDMS_EXPORT int fdms_fused_decode_attention_paged(
                                 out, os_b, os_h, workspace, counters, batch, num_kv_heads, group_size, head_dim,
                                 num_splits, split_rows, scale, k_scale, v_scale, q_norm, k_norm, norm_eps, stream,
                                 block_tables, bt_b, bt_h, page_size);
+}
+
+// Planned form of fdms_fused_decode_attention_paged (no reference
+// counterpart): the layer's work plan from fdms_paged_prepare_decode_plan
+// (plan = that layer's items, plan_count = its item count) replaces the live
+// counts, append rows, positions and block tables; the grid holds max_items
+// workgroups (those past the step's count exit after their first load), each
+// one item of at most 512 ranks with one 64-row group per wave.  num_splits
+// bounds the items of one pair (the workspace holds pairs * num_splits *
+// group_size * (head_dim + 2) floats).  The decision, RoPE, append and
+// attention are those of the unplanned launch; only the rank ranges of the
+// splits (and so the fp32 summation order) differ.
+FDMS_EXPORT int fdms_fused_decode_attention_planned(
+    const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int32_t* plan,
+    const int32_t* plan_count, int max_items, uint8_t* evict_out, int64_t ev_b, int64_t ev_h, float alpha_scale,
+    float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v, int64_t c_s, void* out,
+    int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads, int group_size,
+    int head_dim, int num_splits, float scale, const float* k_scale, const float* v_scale, const void* q_norm,
+    const void* k_norm, float norm_eps, void* stream) {
+  if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4 || max_items <= 0)
+    return (int)hipErrorInvalidValue;
+  if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535) return (int)hipErrorInvalidValue;
+  if (batch == 0) return 0;
+  if (!q || !k || !v || !cos_sin || !plan || !plan_count || !evict_out || !compact_k || !compact_v || !out)
+    return (int)hipErrorInvalidValue;
+  if ((uintptr_t)plan % 16 || c_s % 16 || ((uintptr_t)compact_k % 16) || ((uintptr_t)compact_v % 16))
+    return (int)hipErrorInvalidValue;
+  if (num_splits > 1 && (!workspace || !counters)) return (int)hipErrorInvalidValue;
+  const int pairs = batch * num_kv_heads;
+  if (pairs > 65535) return (int)hipErrorInvalidValue;
+  if ((q_norm && ((uintptr_t)q_norm & 1)) || (k_norm && ((uintptr_t)k_norm & 1)) || !(norm_eps >= 0.0f))
+    return (int)hipErrorInvalidValue;
+  const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, nullptr,
+                      nullptr, 0, 0, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
+                      positive_scale, (const bf16_t*)q_norm, (const bf16_t*)k_norm, norm_eps};
+#define FDMS_PLANNED_LAUNCH(DD)                                                                                    \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 8, true, true, true>), dim3((unsigned)max_items),             \
+                     dim3(8 * kWave), 0, (hipStream_t)stream, plan, plan_count, nullptr, 0, 0, nullptr, 0, 0,     \
+                     nullptr, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,             \
+                     (uint8_t*)compact_v, c_s, nullptr, 0, 0, nullptr, 0, 0, kPlanPageShift, 1, (bf16_t*)out,      \
+                     os_b, os_h, workspace, counters, group_size, num_splits, kPlanRows, kPlanRows, scale,         \
+                     nullptr, 0, 0, nullptr, pre, k_scale, v_scale)
+  if (head_dim == 64) FDMS_PLANNED_LAUNCH(64); else FDMS_PLANNED_LAUNCH(128);
+#undef FDMS_PLANNED_LAUNCH
+  FDMS_LAUNCH_CHECK();
+  return 0;
 }
 
 // ---------------------------------------------------------------------------

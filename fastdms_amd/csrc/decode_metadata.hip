@@ -7,7 +7,10 @@
 //          (the appended token's DMS decision, after the forward).
 // One thread per (layer, seq, head); one launch for all layers.  Launch-bound.
 #include "fdms_common.h"
+#include "fdms_plan.h"
 #include "fdms_pool.h"
+
+using namespace fdms;
 
 __global__ void prepare_decode_kernel(const int32_t* __restrict__ base, int64_t b_l, int64_t b_b, int64_t b_h,
                                       int32_t* __restrict__ live, int64_t l_l, int64_t l_b, int64_t l_h,
@@ -139,6 +142,175 @@ FDMS_EXPORT int fdms_paged_prepare_decode(int32_t* live, int64_t l_l, int64_t l_
                      live, l_l, l_b, l_h, slot_out, s_l, s_b, s_h, block_table, bt_l, bt_b, bt_h, pages_held, hd_l,
                      hd_b, hd_h, page_stack, stack_stride, page_top, max_pages, overflow, num_seqs, num_kv_heads,
                      total);
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// The same slot assignment with the step's attention work plan (fdms_plan.h):
+// one workgroup per layer, so the layer's page pops need no atomics -- the
+// spans that need a page take stack entries top-1, top-2, ... in (seq, head)
+// order of a block prefix count (pops past the stack fail: slot -1, overflow).
+// Then each span's ceil(live / kPlanRows) items are listed at the block prefix
+// of the item counts, with their rank ranges, split indices, append row,
+// position and page ids.  plan_count[l] = the layer's items.
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanMaxPairsPerThread = 8;  // pairs per layer <= 8192
+
+// Exclusive prefix over the block of one value per thread; returns the
+// thread's prefix, *total the block's sum.  Every thread must call it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_buf, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_buf[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+  const int nw = blockDim.x >> 6;
+  for (int w = 0; w < nw; ++w) {
+    const int t = s_buf[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // s_buf is reused by the next scan
+  *total = all;
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void paged_prepare_decode_plan_kernel(
+    int32_t* __restrict__ live, int64_t l_l, int64_t l_b, int64_t l_h, int32_t* __restrict__ slot, int64_t s_l,
+    int64_t s_b, int64_t s_h, int32_t* __restrict__ bt, int64_t bt_l, int64_t bt_b, int64_t bt_h,
+    int32_t* __restrict__ held, int64_t hd_l, int64_t hd_b, int64_t hd_h, const int32_t* __restrict__ stack,
+    int64_t stack_stride, int32_t* __restrict__ top, int max_pages, int32_t* __restrict__ overflow,
+    const int64_t* __restrict__ positions, int32_t* __restrict__ plan, int64_t plan_l,
+    int32_t* __restrict__ plan_count, int max_items, int num_seqs, int num_kv_heads) {
+  __shared__ int s_buf[kPlanThreads / 64];
+  const int l = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int pairs = num_seqs * num_kv_heads;
+  int n[kPlanMaxPairsPerThread], np[kPlanMaxPairsPerThread];
+  bool need[kPlanMaxPairsPerThread];
+  int needs = 0;
+#pragma unroll
+  for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
+    const int p = tid + k * kPlanThreads;
+    n[k] = np[k] = 0;
+    need[k] = false;
+    if (p < pairs) {
+      const int b = p / num_kv_heads, h = p - b * num_kv_heads;
+      n[k] = live[l * l_l + b * l_b + h * l_h];
+      np[k] = held[l * hd_l + b * hd_b + h * hd_h];
+      need[k] = n[k] >= (np[k] << kPagedShift);
+      needs += need[k] ? 1 : 0;
+    }
+  }
+  // pops in (seq, head) order: a thread's pairs are p = tid + k * kPlanThreads,
+  // so rank the needers k-major: all threads' first pairs, then their second ...
+  int top0 = top[l];
+  int pops_before_k = 0;
+  int item_count[kPlanMaxPairsPerThread];
+  int32_t app[kPlanMaxPairsPerThread];
+#pragma unroll
+  for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
+    app[k] = -1;
+    item_count[k] = 0;
+    if (k * kPlanThreads >= pairs) break;  // uniform
+    int tot = 0;
+    const int j = block_exclusive_scan(need[k] ? 1 : 0, s_buf, &tot) + pops_before_k;
+    pops_before_k += tot;
+    const int p = tid + k * kPlanThreads;
+    if (p >= pairs) continue;
+    const int b = p / num_kv_heads, h = p - b * num_kv_heads;
+    int32_t* btr = bt + l * bt_l + b * bt_b + h * bt_h;
+    bool ok = true;
+    if (need[k]) {
+      ok = np[k] < max_pages && j < top0;
+      if (ok) {
+        btr[np[k]] = stack[l * stack_stride + top0 - 1 - j];
+        held[l * hd_l + b * hd_b + h * hd_h] = np[k] + 1;
+      } else {
+        atomicExch(overflow, 1);
+      }
+    }
+    if (ok) {
+      app[k] = (btr[n[k] >> kPagedShift] << kPagedShift) + (n[k] & ((1 << kPagedShift) - 1));
+      live[l * l_l + b * l_b + h * l_h] = n[k] + 1;
+      n[k] += 1;
+    }
+    slot[l * s_l + b * s_b + h * s_h] = app[k];
+    item_count[k] = plan_items_of(n[k]);
+  }
+  if (tid == 0) top[l] = max(0, top0 - pops_before_k);
+  // items: list position = block prefix of the item counts, k-major like the pops
+  int items_before_k = 0;
+  int32_t* lp = plan + l * plan_l;
+#pragma unroll
+  for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
+    if (k * kPlanThreads >= pairs) break;  // uniform
+    int tot = 0;
+    const int first = block_exclusive_scan(item_count[k], s_buf, &tot) + items_before_k;
+    items_before_k += tot;
+    const int p = tid + k * kPlanThreads;
+    if (p >= pairs || item_count[k] == 0) continue;
+    const int b = p / num_kv_heads, h = p - b * num_kv_heads;
+    const int32_t* btr = bt + l * bt_l + b * bt_b + h * bt_h;
+    const int lv = n[k], ni = item_count[k];
+    const int per = plan_split_rows(lv, ni);
+    const int pos = (int)positions[b];
+    for (int s = 0; s < ni; ++s) {
+      const int idx = first + s;
+      if (idx >= max_items) {
+        atomicExch(overflow, 1);
+        break;
+      }
+      const int r0 = min(lv, s * per);
+      int r1 = min(lv, r0 + per);
+      int flags = 0;
+      if (app[k] >= 0 && r0 < lv && r1 == lv) {
+        flags = 1;
+        r1 = lv - 1;
+      }
+      int32_t* it = lp + (int64_t)idx * kPlanInts;
+      reinterpret_cast<int4*>(it)[0] = make_int4(p, r0, r1, s | (ni << 16));
+      reinterpret_cast<int4*>(it)[1] = make_int4(lv, app[k], pos, flags);
+      const int last = max(r1 - 1, r0);
+#pragma unroll
+      for (int j = 0; j < kPlanPages; j += 4) {
+        int4 w;
+        w.x = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 0), last) >> kPagedShift] : -1;
+        w.y = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 1), last) >> kPagedShift] : -1;
+        w.z = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 2), last) >> kPagedShift] : -1;
+        w.w = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 3), last) >> kPagedShift] : -1;
+        reinterpret_cast<int4*>(it + kPlanHeader)[j / 4] = w;
+      }
+    }
+  }
+  if (tid == 0) plan_count[l] = min(items_before_k, max_items);
+}
+
+FDMS_EXPORT int fdms_paged_prepare_decode_plan(int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h,
+                                               int32_t* slot_out, int64_t s_l, int64_t s_b, int64_t s_h,
+                                               int32_t* block_table, int64_t bt_l, int64_t bt_b, int64_t bt_h,
+                                               int32_t* pages_held, int64_t hd_l, int64_t hd_b, int64_t hd_h,
+                                               const int32_t* page_stack, int64_t stack_stride, int32_t* page_top,
+                                               int max_pages, int32_t* overflow, const int64_t* positions,
+                                               int32_t* plan, int64_t plan_l, int32_t* plan_count, int max_items,
+                                               int num_layers, int num_seqs, int num_kv_heads, void* stream) {
+  if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0 || max_pages <= 0 || max_items <= 0)
+    return (int)hipErrorInvalidValue;
+  if ((int64_t)num_seqs * num_kv_heads > (int64_t)kPlanThreads * kPlanMaxPairsPerThread)
+    return (int)hipErrorInvalidValue;
+  if (!live || !slot_out || !block_table || !pages_held || !page_stack || !page_top || !overflow || !positions ||
+      !plan || !plan_count)
+    return (int)hipErrorInvalidValue;
+  if (((uintptr_t)plan % 16) || plan_l % 4 || plan_l < (int64_t)max_items * kPlanInts) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(paged_prepare_decode_plan_kernel, dim3(num_layers), dim3(kPlanThreads), 0, (hipStream_t)stream,
+                     live, l_l, l_b, l_h, slot_out, s_l, s_b, s_h, block_table, bt_l, bt_b, bt_h, pages_held, hd_l,
+                     hd_b, hd_h, page_stack, stack_stride, page_top, max_pages, overflow, positions, plan, plan_l,
+                     plan_count, max_items, num_seqs, num_kv_heads);
   FDMS_LAUNCH_CHECK();
   return 0;
 }

@@ -20,7 +20,7 @@ import torch
 
 from .. import _native as nat
 from ..config import Config
-from ..layers.compact_attention import reserve_attention_workspace
+from ..layers.compact_attention import DecodePlan, decode_plan_enabled, reserve_attention_workspace
 from ..layers import quant_env as qe
 from ..layers.linear import convert_linear_modules_to_fp8, reserve_linear_workspace
 from ..models.synthetic import build_synthetic_model
@@ -106,6 +106,10 @@ class ModelRunner:
         self.static_slot = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads), device=self.device,
                                        dtype=torch.int32)
         self.static_tokens = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        # the paged decode step's attention work plan (static: captured graphs keep its address)
+        self.decode_plan = (DecodePlan(self.device, self.num_layers, self.max_num_seqs * self.num_kv_heads,
+                                       config.max_model_len + 1)
+                            if self.compact_kv_manager.paged and decode_plan_enabled() else None)
         self.prompt_stages: dict[int, PromptStage] = {}  # long prompts between their chunks
         self.pinned_ids = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
@@ -297,8 +301,9 @@ class ModelRunner:
         mgr = self.compact_kv_manager
         L, H = self.num_layers, self.num_kv_heads
         slot = self.static_slot[:, :batch]
+        plan = self.decode_plan if mgr.paged else None
         if mgr.paged:
-            bt, live = mgr.paged_prepare_decode(start, batch, slot)
+            bt, live = mgr.paged_prepare_decode(start, batch, slot, plan=plan, positions=self.static_positions)
             base = None
         else:
             bt = None
@@ -312,7 +317,7 @@ class ModelRunner:
         set_context(False, block_tables=bt, compact_kv_enabled=True, compact_base_offsets=base,
                     compact_live_counts=live, compact_slot_mapping=slot, compact_max_live_count=max_live_hint,
                     dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale, dms_alpha_offset=md.alpha_offset,
-                    dms_layer_evictions_buffer=evict)
+                    dms_layer_evictions_buffer=evict, compact_plan=plan)
         ids = self.static_input_ids[:batch]
         pos = self.static_positions[:batch]
         logits = None

@@ -327,20 +327,32 @@ class PagedCompactKVManager(CompactKVManager):
                 st.live_upper_bound = max(st.live_upper_bound, n)
 
     # -- decode ------------------------------------------------------------------
-    def paged_prepare_decode(self, start: int, batch: int, slot_out: torch.Tensor) -> tuple:
+    def paged_prepare_decode(self, start: int, batch: int, slot_out: torch.Tensor, plan=None,
+                             positions: torch.Tensor | None = None) -> tuple:
         """Decode append rows of slots start .. start + batch - 1, all layers,
         one launch (pops a page where a span's pages are full); returns the
         (block tables [L, B, H, P], live counts [L, B, H]) views the step's
-        attention reads."""
+        attention reads.  With ``plan`` (layers.compact_attention.DecodePlan)
+        and the step's ``positions`` (int64 [batch]) the same launch also
+        writes the step's attention work plan."""
         L, H = self.num_layers, self.num_kv_heads
         live = self.layer_major_live_counts[:, start:start + batch]
         bt = self.block_tables[:, start:start + batch]
         held = self.pages_held[:, start:start + batch]
-        nat.call("fdms_paged_prepare_decode", live.data_ptr(), live.stride(0), live.stride(1), live.stride(2),
-                 slot_out.data_ptr(), slot_out.stride(0), slot_out.stride(1), slot_out.stride(2), bt.data_ptr(),
-                 bt.stride(0), bt.stride(1), bt.stride(2), held.data_ptr(), held.stride(0), held.stride(1),
-                 held.stride(2), self.page_stack.data_ptr(), self.page_stack.stride(0), self.page_top.data_ptr(),
-                 self.max_pages, self.overflow.data_ptr(), L, batch, H, nat.stream())
+        args = (live.data_ptr(), live.stride(0), live.stride(1), live.stride(2), slot_out.data_ptr(),
+                slot_out.stride(0), slot_out.stride(1), slot_out.stride(2), bt.data_ptr(), bt.stride(0),
+                bt.stride(1), bt.stride(2), held.data_ptr(), held.stride(0), held.stride(1), held.stride(2),
+                self.page_stack.data_ptr(), self.page_stack.stride(0), self.page_top.data_ptr(), self.max_pages,
+                self.overflow.data_ptr())
+        if plan is None:
+            nat.call("fdms_paged_prepare_decode", *args, L, batch, H, nat.stream())
+        else:
+            if positions is None or positions.dtype != torch.int64 or positions.shape[0] < batch:
+                raise ValueError("a planned decode step needs the step's int64 positions")
+            if batch * H > plan.pairs:
+                raise ValueError(f"the plan holds {plan.pairs} pairs, the batch has {batch * H}")
+            nat.call("fdms_paged_prepare_decode_plan", *args, positions.data_ptr(), plan.items.data_ptr(),
+                     plan.items.stride(0), plan.count.data_ptr(), plan.max_items, L, batch, H, nat.stream())
         return bt, live
 
     def prepare_decode_metadata(self, seqs: list[Sequence]):

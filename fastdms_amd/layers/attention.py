@@ -14,6 +14,7 @@ from torch import nn
 from .. import _native as nat
 from ..utils.context import get_context
 from .compact_attention import (compact_decode_attention, compact_decode_attention_paged,
+                                fused_decode_attention_planned,
                                 fused_dms_rope_store_compact_decode_attention, store_compact_kvcache)
 
 PAGE_SIZE = 16  # rows per page of the paged compact layout (engine.paged_kv)
@@ -108,12 +109,18 @@ class Attention(nn.Module):
         append of k / v and compact attention (q / k / v raw from qkv_proj;
         q_norm / k_norm: Qwen3's per-head RMSNorm modules, applied in the
         kernel)."""
-        base, bt, live, slot = self._layer_metadata(get_context())
+        ctx = get_context()
         norms = {}
         if q_norm is not None or k_norm is not None:
             norms = dict(q_norm_weight=None if q_norm is None else q_norm.weight,
                          k_norm_weight=None if k_norm is None else k_norm.weight,
                          norm_eps=(q_norm if q_norm is not None else k_norm).eps)
+        if ctx.compact_plan is not None:  # the step's work plan (paged layout)
+            return fused_decode_attention_planned(
+                q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, evict_out, ctx.compact_plan,
+                self.layer_id, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
+                scale=self.scale, k_scale=self.compact_k_scale, v_scale=self.compact_v_scale, **norms)
+        base, bt, live, slot = self._layer_metadata(ctx)
         return fused_dms_rope_store_compact_decode_attention(
             q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, slot, evict_out, positions, base,
             live, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,

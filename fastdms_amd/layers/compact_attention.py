@@ -510,6 +510,98 @@ def fused_dms_rope_store_compact_decode_attention(
     return out
 
 
+PLAN_ROWS = 512  # ranks per work item of the planned launch (fdms_plan.h kPlanRows)
+PLAN_INTS = 40   # int32 per work item
+
+
+def decode_plan_enabled() -> bool:
+    """The paged decode step plans its attention work once per step
+    (fdms_paged_prepare_decode_plan + fdms_fused_decode_attention_planned);
+    FASTDMS_AMD_ATTN_PLAN=0 keeps the per-layer launch that partitions
+    inside the kernel (same results up to fp32 summation order)."""
+    return os.environ.get("FASTDMS_AMD_ATTN_PLAN", "1").strip() != "0"
+
+
+def plan_splits_bound(max_live: int) -> int:
+    """Items of one pair at most (its live count is at most ``max_live``)."""
+    return max(1, -(-int(max_live) // PLAN_ROWS))
+
+
+class DecodePlan:
+    """Static buffers of the step's attention work plan: ``items`` [layers,
+    max_items, 40] int32, ``count`` [layers] int32.  Sized for ``pairs``
+    (seq, kv head) pairs whose live counts stay within ``max_live``; the
+    addresses never change, so captured decode graphs keep them."""
+
+    def __init__(self, device, num_layers: int, pairs: int, max_live: int):
+        self.splits = plan_splits_bound(max_live)
+        self.max_items = pairs * self.splits
+        self.pairs = pairs
+        self.items = torch.zeros((num_layers, self.max_items, PLAN_INTS), device=device, dtype=torch.int32)
+        self.count = torch.zeros(num_layers, device=device, dtype=torch.int32)
+
+    def grid_items(self, batch: int, num_kv_heads: int) -> int:
+        """Workgroups of a planned launch over ``batch`` sequences: their items
+        at most (those past the step's count exit at once)."""
+        return batch * num_kv_heads * self.splits
+
+
+def fused_decode_attention_planned(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos_sin_cache: torch.Tensor,
+                                   compact_k: torch.Tensor, compact_v: torch.Tensor, evict_out: torch.Tensor,
+                                   plan: DecodePlan, layer_id: int, *, num_kv_heads: int, alpha_scale: float,
+                                   alpha_offset: float, scale: float | None = None, out: torch.Tensor | None = None,
+                                   k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+                                   q_norm_weight: torch.Tensor | None = None,
+                                   k_norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6) -> torch.Tensor:
+    """fused_dms_rope_store_compact_decode_attention on the paged layout with
+    the step's work plan (written by PagedCompactKVManager.paged_prepare_decode
+    with a plan): the plan's items of layer ``layer_id`` carry the pairs'
+    rank ranges, append rows, positions and page ids, so no live counts,
+    slots, positions or block tables are passed.  Same checks and results as
+    the unplanned launch (outputs up to fp32 summation order)."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
+        raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
+    batch, num_q_heads, head_dim = q.shape
+    if k.shape != (batch, num_kv_heads, head_dim) or num_q_heads % num_kv_heads:
+        raise ValueError(f"q/k shape mismatch: q={tuple(q.shape)}, k={tuple(k.shape)}, num_kv_heads={num_kv_heads}")
+    if batch * num_kv_heads > plan.pairs:
+        raise ValueError(f"the plan holds {plan.pairs} pairs, the batch has {batch * num_kv_heads}")
+    if evict_out.dtype != torch.bool or tuple(evict_out.shape) != (batch, num_kv_heads):
+        raise ValueError(f"evict_out must be bool {(batch, num_kv_heads)}")
+    if cos_sin_cache.ndim != 3 or cos_sin_cache.shape[2] != head_dim or cos_sin_cache.dtype != torch.float32:
+        raise ValueError(f"expected an fp32 cos_sin_cache [positions, 1, {head_dim}]")
+    if not fused_decode_attention_supported(q, k, v, compact_k):
+        raise ValueError("fused decode attention needs bf16 q/k/v, FP8 16-byte compact rows, group <= 4, "
+                         "head_dim 64 or 128")
+    nat.require_cuda(q, k, v, compact_k, compact_v, what="planned decode attention")
+    group = num_q_heads // num_kv_heads
+    if scale is None:
+        scale = head_dim ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    if out.stride(2) != 1:
+        raise ValueError("out needs a contiguous head_dim axis")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.shape != (head_dim,) or not w.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous bf16 [{head_dim}] tensor")
+    pairs = batch * num_kv_heads
+    ws, counters = attention_workspace(q.device, pairs * plan.splits * group * (head_dim + 2), pairs)
+    s_, off, thr, positive = dms_threshold_args(alpha_scale, alpha_offset)
+    ev = evict_out.view(torch.uint8)
+    items = plan.items[layer_id]
+    nat.call("fdms_fused_decode_attention_planned", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+             k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos_sin_cache.data_ptr(),
+             cos_sin_cache.stride(0), cos_sin_cache.stride(2), items.data_ptr(),
+             plan.count[layer_id:layer_id + 1].data_ptr(), plan.grid_items(batch, num_kv_heads), ev.data_ptr(),
+             ev.stride(0),
+             ev.stride(1), s_, off, thr, positive, compact_k.data_ptr(), compact_v.data_ptr(), compact_k.stride(0),
+             out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads,
+             group, head_dim, plan.splits, float(scale), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+             nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.ptr(q_norm_weight),
+             nat.ptr(k_norm_weight), float(norm_eps), nat.stream())
+    return out
+
+
 def _expiry(incremental: bool, *, positions_per_lh, evict_per_lh, live_counts, base_offsets, compact_k, compact_v,
             current_positions, window_size):
     num_seqs, num_kv_heads, max_capacity = positions_per_lh.shape

@@ -37,6 +37,8 @@ class Context:
     cu_seqlens_q_host: list | None = None
     # a chunk of a long prompt in this prefill batch (engine.chunked_prefill.ChunkPlan)
     prefill_chunk: object | None = None
+    # the decode step's attention work plan (layers.compact_attention.DecodePlan), or None
+    compact_plan: object | None = None
 
 
 _CONTEXT = Context()
@@ -52,13 +54,14 @@ def set_context(is_prefill, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0
                 compact_max_live_count=0, dms_capture_enabled=False, dms_alpha_scale=100.0, dms_alpha_offset=5.0,
                 dms_layer_evictions=None, dms_layer_evictions_buffer=None, streaming_pack_manager=None,
                 streaming_pack_seq_ids=None, streaming_pack_window_size=0, cu_seqlens_q_host=None,
-                prefill_chunk=None) -> None:
+                prefill_chunk=None, compact_plan=None) -> None:
     global _CONTEXT
     _CONTEXT = Context(is_prefill, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, slot_mapping,
                        context_lens, block_tables, compact_kv_enabled, compact_base_offsets, compact_live_counts,
                        compact_slot_mapping, compact_max_live_count, dms_capture_enabled, dms_alpha_scale,
                        dms_alpha_offset, dms_layer_evictions, dms_layer_evictions_buffer, streaming_pack_manager,
-                       streaming_pack_seq_ids, streaming_pack_window_size, cu_seqlens_q_host, prefill_chunk)
+                       streaming_pack_seq_ids, streaming_pack_window_size, cu_seqlens_q_host, prefill_chunk,
+                       compact_plan)
 
 
 def reset_context() -> None:

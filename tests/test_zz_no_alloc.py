@@ -96,3 +96,69 @@ def test_noalloc_rejects_sizes_beyond_its_scratch():
     # 512 sequences x 8 heads x 64 splits x 4 x 66 floats > 2^21
     rc = fn(*args, 512, 8, 4, 64, 64, 256, 0.125, None, None, None, None, 0.0, None)
     assert rc == 1  # hipErrorInvalidValue
+
+
+def _first_call_under_capture() -> None:
+    """Child process body: the process's first fdms_fused_decode_attention_noalloc
+    call is made under HIP graph capture (so the library's ticket-zeroing
+    kernel is captured, not run: the tickets rely on the device array being
+    zero at module load); three replays, with eager work and synchronizations
+    between them, each equal to the workspace entry point's eager result."""
+    rng = np.random.default_rng(5)
+    hkv, g, d = 8, 4, 64
+    case = _case(rng, 6, hkv, g, d)
+    want = _run(False, case, hkv, g, d, None, 7, 256)
+    from fastdms_amd import _native as nat
+    from fastdms_amd.engine.dms import dms_threshold_args
+    qkv, ck, cv, base, slot, live, pos, cap = case
+    b, hq = qkv.shape[0], hkv * g
+    qkv_d = from_values(qkv, numerics.DT_BF16)
+    q, k, v = (qkv_d[:, :hq * d].view(b, hq, d), qkv_d[:, hq * d:(hq + hkv) * d].view(b, hkv, d),
+               qkv_d[:, (hq + hkv) * d:].view(b, hkv, d))
+    ckd, cvd = torch.from_numpy(ck.copy()).cuda(), torch.from_numpy(cv.copy()).cuda()
+    cache = torch.from_numpy(oatt.rope_cos_sin_cache(d, 8192, 500000.0)).cuda()
+    posd, slotd = torch.from_numpy(pos).cuda(), torch.from_numpy(slot).cuda()
+    based, lived = torch.from_numpy(base).cuda(), torch.from_numpy(live).cuda()
+    ev = torch.zeros((b, hkv), dtype=torch.uint8, device="cuda")
+    out = torch.zeros((b, hq, d), dtype=torch.bfloat16, device="cuda")
+    s_, off, thr, positive = dms_threshold_args(10.0, 5.0)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+        nat.call("fdms_fused_decode_attention_noalloc", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                 k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cache.data_ptr(),
+                 cache.stride(0), cache.stride(2), posd.data_ptr(), slotd.data_ptr(), slotd.stride(0),
+                 slotd.stride(1), ev.data_ptr(), ev.stride(0), ev.stride(1), s_, off, thr, positive, ckd.data_ptr(),
+                 cvd.data_ptr(), d, based.data_ptr(), based.stride(0), based.stride(1), lived.data_ptr(),
+                 lived.stride(0), lived.stride(1), out.data_ptr(), out.stride(0), out.stride(1), b, hkv, g, d, 7,
+                 256, d ** -0.5, None, None, None, None, 0.0, nat.stream())
+    for replay in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        noise = torch.randn(1 << 20, device="cuda").sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        got = (ev.cpu(), out.cpu(), ckd.cpu(), cvd.cpu())
+        for w, x in zip(want, got):
+            assert torch.equal(w.view(torch.uint8) if w.dtype != torch.uint8 else w,
+                               x.view(torch.uint8) if x.dtype != torch.uint8 else x), f"replay {replay}"
+    print("first call under capture: 3 replays equal", flush=True)
+
+
+def test_first_call_on_a_device_under_graph_capture():
+    """In a fresh process (the library keeps its per-device set-up for the
+    process's lifetime) the first allocation-free call is captured."""
+    require_gpu()
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    code = ("import sys; sys.path[:0] = [%r, %r]; import test_zz_no_alloc as t; t._first_call_under_capture()"
+            % (str(root), str(root / "tests")))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                         env=dict(os.environ))
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0 and "3 replays equal" in res.stdout
