@@ -248,11 +248,12 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
         stack, top = mgr.page_stack.clone(), mgr.page_top.clone()
         ovf = torch.zeros(1, dtype=torch.int32, device="cuda")
         slot_c = torch.empty_like(lv1)
+        p_rows, p_heavy, p_splits = plan.partition(b * hkv)
         nat.call("fdms_paged_prepare_decode_plan", lv1.data_ptr(), *lv1.stride(), slot_c.data_ptr(),
                  *slot_c.stride(), bt_c.data_ptr(), *bt_c.stride()[:3], held.data_ptr(), *held.stride(),
                  stack.data_ptr(), stack.stride(0), top.data_ptr(), mgr.max_pages, ovf.data_ptr(),
-                 positions.data_ptr(), plan.items.data_ptr(), plan.items.stride(0), plan.count.data_ptr(),
-                 plan.max_items, cfg.num_hidden_layers, b, hkv, nat.stream())
+                 positions.data_ptr(), plan.items.data_ptr(), plan.items.stride(0), p_rows, p_heavy, p_splits,
+                 cfg.num_hidden_layers, b, hkv, nat.stream())
         torch.cuda.synchronize()
         if int(ovf.item()) or not torch.equal(slot_c, slot) or not torch.equal(lv1, live):
             raise RuntimeError("attention roofline: the plan does not reproduce the decode state")
@@ -260,7 +261,7 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     def launch(l):
         if plan is not None:
             ks, vs = mgr.layer_kv_scales(l)
-            fused_decode_attention_planned(q, k, v, cos_sin, arenas[l][0], arenas[l][1], evict, plan, l,
+            fused_decode_attention_planned(q, k, v, cos_sin, arenas[l][0], arenas[l][1], evict, positions, plan, l,
                                            num_kv_heads=hkv, alpha_scale=md.alpha_scale,
                                            alpha_offset=md.alpha_offset, out=out, k_scale=ks, v_scale=vs)
         elif fused:
@@ -312,9 +313,11 @@ def attention_roofline(llm, seqs, replays: int, config: str = "l1b-c8"):
     mfma = mfma_attention_path(q, arenas[0][0], hq // hkv)
     splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma)
     if plan is not None:  # the step's work plan (layer 0)
-        per_pair = (lv[0] + 511) // 512
-        splits = {"rows_per_item": 512, "items": int(plan.count[0]), "grid": plan.grid_items(b, hkv),
-                  "max_per_pair": int(per_pair.max())}
+        p_rows, p_heavy, p_splits = plan.partition(b * hkv)
+        per_pair = torch.where(lv[0] <= p_rows, torch.ones_like(lv[0]),
+                               (lv[0] + p_heavy - 1) // p_heavy).clamp(1, p_splits)
+        splits = {"planned": True, "rows_per_split": p_rows, "heavy_rows": p_heavy, "bound": p_splits,
+                  "workgroups": int(per_pair.sum()), "max_per_pair": int(per_pair.max())}
     elif mfma:  # per-pair split counts, as the kernel derives them (layer 0)
         splits, split_rows = attention_split_plan(q.device, b * hkv, hint, mfma,
                                                   waves=attention_waves(d, fused, b * hkv), head_dim=d)

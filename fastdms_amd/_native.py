@@ -60,11 +60,11 @@ SIGNATURES: dict[str, str] = {
     "fdms_paged_pack_prepare": "pllpiiiipllplllpppllllippppllpllipp",
     "fdms_paged_pack_scatter": "ppillllpllpiplllppilpppllllllplliiiiippp",
     "fdms_paged_prepare_decode": "plllplllplllplllplpipiiip",
-    "fdms_paged_prepare_decode_plan": "plllplllplllplllplpippplpiiiip",
+    "fdms_paged_prepare_decode_plan": "plllplllplllplllplpipppliiiiiip",
     "fdms_paged_free": "piplllplllplllplpiip",
     "fdms_paged_expiry": "iplllplllplllplllplllplpppllpiiiip",
     "fdms_fused_decode_attention_paged": "pllpllpllpllppllpllfffipplpllipllpllppiiiiiifppppfp",
-    "fdms_fused_decode_attention_planned": "pllpllpllpllppipllfffipplpllppiiiiifppppfp",
+    "fdms_fused_decode_attention_planned": "pllpllpllpllpppllfffipplpllppiiiiifppppfp",
     "fdms_fp8_gemm": "plpplpppliiip",
 }
 

@@ -37,11 +37,11 @@ CFLAGS = [
 FILE_FLAGS = {
     "prefill_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # The decode attention kernels take the arguments their first loads need
-    # first (the plan pointers of the planned launch, then the live counts,
-    # append rows and positions of the others); preloading them into SGPRs at
+    # first (the plan of the planned launch, the live counts, append rows and
+    # positions of the others); preloading them into SGPRs at
     # wave launch takes one scalar memory round trip off each workgroup's start (code objects carry a fallback
     # prologue that loads them for firmware without preload support).
-    "compact_attention.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=11"],
+    "compact_attention.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
 }
 
 

@@ -1076,9 +1076,10 @@ struct DecodePre {
 };
 
 
-// The first nine arguments are what a workgroup needs before its first
-// loads (its pair, live count, and for the fused kernel the step's append
-// slot and position); this file is built with them preloaded into SGPRs at
+// The first ten arguments are what a workgroup needs before its first
+// loads (the planned launch's work plan; its pair, live count, and for the
+// fused kernel the step's append slot and position); this file is built with
+// them preloaded into SGPRs at
 // wave launch (-amdgpu-kernarg-preload-count), which takes one scalar memory
 // round trip off that chain (the page table is read only after the live
 // count, by when the other arguments have landed).  Strides are int32 (the
@@ -1089,8 +1090,7 @@ struct DecodePre {
 // sequences than at the unconstrained 130 VGPRs).
 template <int D, int NW, bool PAGED, bool FUSED, bool PLANNED = false>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4))) void decode_attn_mfma_kernel(
-    const int32_t* __restrict__ plan, const int32_t* __restrict__ plan_count,
-    const int32_t* __restrict__ live_counts, int lc_b, int lc_h, const int32_t* __restrict__ fslot, int sm_b,
+    const int32_t* __restrict__ plan, const int32_t* __restrict__ live_counts, int lc_b, int lc_h, const int32_t* __restrict__ fslot, int sm_b,
     int sm_h, const int64_t* __restrict__ fpositions, int num_pairs, int num_kv_heads,
     const bf16_t* __restrict__ q, int64_t qs_b, int64_t qs_h, uint8_t* __restrict__ ck,
     uint8_t* __restrict__ cv, int64_t c_s, const int32_t* __restrict__ base_offsets, int64_t bo_b,
@@ -1121,7 +1121,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   // XCD and their partials meet in its L2.  Pair (b, h) takes ns =
   // ceil(live / split_rows) splits (at most num_splits) of at most
   // split_rows rows each.
-  static_assert(!PLANNED || (PAGED && FUSED && NW * 64 == kPlanRows), "a plan item is one group per wave");
+  static_assert(!PLANNED || (PAGED && FUSED && NW == kPlanWaves), "a plan item is two groups per wave at most");
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the group loop scalar
   const int lane = tid & 63;
@@ -1132,32 +1132,39 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
   int32_t app_slot = -1;
   [[maybe_unused]] int plan_ns = 1, plan_t0 = 0, plan_t1 = 0;
   [[maybe_unused]] bool plan_new = false;
-  [[maybe_unused]] int64_t plan_qrow[4] = {0, 0, 0, 0};
+  [[maybe_unused]] int64_t plan_qrow[4] = {0, 0, 0, 0}, plan_qrow2[4] = {0, 0, 0, 0};
   if constexpr (PLANNED) {
-    // The workgroup's plan item (fdms_plan.h), one 16-byte word per lane
-    // (lanes past the item re-read its last word), and the layer's item
-    // count, in one memory latency: everything the K/V loads need.
-    const int cnt = plan_count[0];
-    const uint4 w = reinterpret_cast<const uint4*>(plan + (int64_t)blockIdx.x * kPlanInts)[min(lane, kPlanInts / 4 - 1)];
-    if ((int)blockIdx.x >= cnt) return;  // uniform: past the step's items
-    pair = __builtin_amdgcn_readlane((int)w.x, 0);
+    // Workgroup p < num_pairs runs split 0 of pair p: its raw rows and
+    // position load at once, beside its plan item (fdms_plan.h); a later
+    // workgroup runs a further split, named by its item, up to the layer's
+    // count of those.  The item arrives as one 16-byte word per lane (lanes
+    // past the item re-read its last word) with everything the K/V loads need.
+    const int lin = blockIdx.x;
+    const bool first = lin < num_pairs;  // uniform per workgroup
+    const int extra = first ? 0 : plan[-1];  // the layer's further splits, stored before its items
+    const uint4 w = reinterpret_cast<const uint4*>(plan + (int64_t)lin * kPlanInts)[min(lane, kPlanInts / 4 - 1)];
+    if (!first && lin >= num_pairs + extra) return;  // uniform: past the step's items
+    pair = first ? lin : __builtin_amdgcn_readlane((int)w.x, 0);
+    b = pair / num_kv_heads;
+    h = pair - b * num_kv_heads;
+    fpos = fpositions[b];
     plan_t0 = __builtin_amdgcn_readlane((int)w.y, 0);
     plan_t1 = __builtin_amdgcn_readlane((int)w.z, 0);
-    const int sw = __builtin_amdgcn_readlane((int)w.w, 0);
+    split = __builtin_amdgcn_readlane((int)w.w, 0) & 0xFFFF;
+    plan_ns = __builtin_amdgcn_readlane((int)w.w, 0) >> 16;
     live = __builtin_amdgcn_readlane((int)w.x, 1);
     app_slot = __builtin_amdgcn_readlane((int)w.y, 1);
-    fpos = __builtin_amdgcn_readlane((int)w.z, 1);
     plan_new = (__builtin_amdgcn_readlane((int)w.w, 1) & 1) != 0;
-    split = sw & 0xFFFF;
-    plan_ns = sw >> 16;
-    // this wave's group: the page ids of its four 16-row quarters
+    // this wave's groups w and w + 8: the page ids of their 16-row quarters
     const int pl = kPlanHeader / 4 + wave;
     plan_qrow[0] = (int64_t)__builtin_amdgcn_readlane((int)w.x, pl) << kPlanPageShift;
     plan_qrow[1] = (int64_t)__builtin_amdgcn_readlane((int)w.y, pl) << kPlanPageShift;
     plan_qrow[2] = (int64_t)__builtin_amdgcn_readlane((int)w.z, pl) << kPlanPageShift;
     plan_qrow[3] = (int64_t)__builtin_amdgcn_readlane((int)w.w, pl) << kPlanPageShift;
-    b = pair / num_kv_heads;
-    h = pair - b * num_kv_heads;
+    plan_qrow2[0] = (int64_t)__builtin_amdgcn_readlane((int)w.x, pl + kPlanWaves) << kPlanPageShift;
+    plan_qrow2[1] = (int64_t)__builtin_amdgcn_readlane((int)w.y, pl + kPlanWaves) << kPlanPageShift;
+    plan_qrow2[2] = (int64_t)__builtin_amdgcn_readlane((int)w.z, pl + kPlanWaves) << kPlanPageShift;
+    plan_qrow2[3] = (int64_t)__builtin_amdgcn_readlane((int)w.w, pl + kPlanWaves) << kPlanPageShift;
   } else {
     const int lin = blockIdx.x;
     const int padded_pairs = ((num_pairs + kXcds - 1) / kXcds) * kXcds;
@@ -1450,9 +1457,14 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     }
     // the registers are free again: the wave's next group goes in flight now
     // and lands while the softmax and P.V below run
-    if constexpr (!PLANNED) {  // a plan item has at most one group per wave
-      if (gidx + NW < ngroups)
+    if (gidx + NW < ngroups) {
+      if constexpr (PLANNED) {  // at most two groups per wave: the second's page ids came with the item
+        MfmaGroupAddr<D> ga;
+        mfma_group_addr_paged<D>(ga, ck, cv, c_s, plan_qrow2, kPlanPageShift, t0 + (gidx + NW) * 64, t1, lane);
+        mfma_issue_group<D>(grp, ga);
+      } else {
         mfma_load_group<D, PAGED>(grp, kspan, vspan, c_s, addr, b, h, t0 + (gidx + NW) * 64, t1, lane);
+      }
     }
     // scores, online softmax per head
     const int tb = t0 + gidx * 64 + ss;
@@ -1648,7 +1660,7 @@ FDMS_EXPORT int fdms_compact_decode_attention(
     if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
     if (!fits_i32(lc_b) || !fits_i32(lc_h) || !fits_i32(bt_b) || !fits_i32(bt_h)) return (int)hipErrorInvalidValue;
 #define FDMS_MFMA_ARGS                                                                                          \
-  nullptr, nullptr, live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads,                \
+  nullptr, live_counts, (int)lc_b, (int)lc_h, nullptr, 0, 0, nullptr, pairs, num_kv_heads,                         \
       (const bf16_t*)q, qs_b, qs_h,                                                                                   \
       (uint8_t*)compact_k, (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,   \
       page_shift, paged, (bf16_t*)out, os_b, os_h, workspace, counters, group_size, num_splits, rows,              \
@@ -1754,7 +1766,7 @@ static int fused_decode_attention(
     return (int)hipErrorInvalidValue;
 #define FDMS_FUSED_LAUNCH(DD, NWV, PG)                                                                               \
   hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, NWV, PG, true>), dim3((unsigned)blocks), dim3(NWV * kWave), 0,     \
-                     (hipStream_t)stream, nullptr, nullptr, live_counts, (int)lc_b, (int)lc_h, slot_mapping,          \
+                     (hipStream_t)stream, nullptr, live_counts, (int)lc_b, (int)lc_h, slot_mapping,                   \
                      (int)sm_b, (int)sm_h,                                                                            \
                      positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,               \
                      (uint8_t*)compact_v, c_s, base_offsets, bo_b, bo_h, block_tables, (int)bt_b, (int)bt_h,          \
@@ -1815,27 +1827,25 @@ FDMS_EXPORT int fdms_fused_decode_attention_paged(
 
 // Planned form of fdms_fused_decode_attention_paged (no reference
 // counterpart): the layer's work plan from fdms_paged_prepare_decode_plan
-// (plan = that layer's items, plan_count = its item count) replaces the live
-// counts, append rows, positions and block tables; the grid holds max_items
-// workgroups (those past the step's count exit after their first load), each
-// one item of at most 512 ranks with one 64-row group per wave.  num_splits
-// bounds the items of one pair (the workspace holds pairs * num_splits *
-// group_size * (head_dim + 2) floats).  The decision, RoPE, append and
-// attention are those of the unplanned launch; only the rank ranges of the
-// splits (and so the fp32 summation order) differ.
+// (`plan` = that layer's items, its count of further splits in the int
+// before them) replaces the live counts, append rows and block tables.  The
+// grid holds num_splits x pairs workgroups: workgroup i runs item i, those
+// past the layer's items exit after one load.  With the partition the
+// unplanned launch uses (the same split_rows, heavy_rows and num_splits given
+// to the plan) the decisions, appended rows and outputs are the unplanned
+// launch's, bit for bit.
 FDMS_EXPORT int fdms_fused_decode_attention_planned(
     const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b, int64_t ks_h, const void* v,
-    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int32_t* plan,
-    const int32_t* plan_count, int max_items, uint8_t* evict_out, int64_t ev_b, int64_t ev_h, float alpha_scale,
-    float alpha_offset, float threshold, int positive_scale, void* compact_k, void* compact_v, int64_t c_s, void* out,
-    int64_t os_b, int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads, int group_size,
-    int head_dim, int num_splits, float scale, const float* k_scale, const float* v_scale, const void* q_norm,
-    const void* k_norm, float norm_eps, void* stream) {
-  if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4 || max_items <= 0)
-    return (int)hipErrorInvalidValue;
+    int64_t vs_b, int64_t vs_h, const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+    const int32_t* plan, uint8_t* evict_out, int64_t ev_b, int64_t ev_h, float alpha_scale, float alpha_offset,
+    float threshold, int positive_scale, void* compact_k, void* compact_v, int64_t c_s, void* out, int64_t os_b,
+    int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads, int group_size, int head_dim,
+    int num_splits, float scale, const float* k_scale, const float* v_scale, const void* q_norm, const void* k_norm,
+    float norm_eps, void* stream) {
+  if (batch < 0 || num_kv_heads <= 0 || group_size <= 0 || group_size > 4) return (int)hipErrorInvalidValue;
   if ((head_dim != 64 && head_dim != 128) || num_splits <= 0 || num_splits > 65535) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
-  if (!q || !k || !v || !cos_sin || !plan || !plan_count || !evict_out || !compact_k || !compact_v || !out)
+  if (!q || !k || !v || !cos_sin || !positions || !plan || !evict_out || !compact_k || !compact_v || !out)
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)plan % 16 || c_s % 16 || ((uintptr_t)compact_k % 16) || ((uintptr_t)compact_v % 16))
     return (int)hipErrorInvalidValue;
@@ -1844,13 +1854,15 @@ FDMS_EXPORT int fdms_fused_decode_attention_planned(
   if (pairs > 65535) return (int)hipErrorInvalidValue;
   if ((q_norm && ((uintptr_t)q_norm & 1)) || (k_norm && ((uintptr_t)k_norm & 1)) || !(norm_eps >= 0.0f))
     return (int)hipErrorInvalidValue;
-  const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, nullptr,
+  const int64_t blocks = (int64_t)pairs * num_splits;
+  if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  const DecodePre pre{(const bf16_t*)k, ks_b, ks_h, (const bf16_t*)v, vs_b, vs_h, cos_sin, cs_p, cs_d, positions,
                       nullptr, 0, 0, evict_out, ev_b, ev_h, alpha_scale, alpha_offset, threshold,
                       positive_scale, (const bf16_t*)q_norm, (const bf16_t*)k_norm, norm_eps};
 #define FDMS_PLANNED_LAUNCH(DD)                                                                                    \
-  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, 8, true, true, true>), dim3((unsigned)max_items),             \
-                     dim3(8 * kWave), 0, (hipStream_t)stream, plan, plan_count, nullptr, 0, 0, nullptr, 0, 0,     \
-                     nullptr, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,             \
+  hipLaunchKernelGGL((decode_attn_mfma_kernel<DD, kPlanWaves, true, true, true>), dim3((unsigned)blocks),       \
+                     dim3(kPlanWaves * kWave), 0, (hipStream_t)stream, plan, nullptr, 0, 0, nullptr, 0, 0,         \
+                     positions, pairs, num_kv_heads, (const bf16_t*)q, qs_b, qs_h, (uint8_t*)compact_k,       \
                      (uint8_t*)compact_v, c_s, nullptr, 0, 0, nullptr, 0, 0, kPlanPageShift, 1, (bf16_t*)out,      \
                      os_b, os_h, workspace, counters, group_size, num_splits, kPlanRows, kPlanRows, scale,         \
                      nullptr, 0, 0, nullptr, pre, k_scale, v_scale)

@@ -150,9 +150,11 @@ FDMS_EXPORT int fdms_paged_prepare_decode(int32_t* live, int64_t l_l, int64_t l_
 // one workgroup per layer, so the layer's page pops need no atomics -- the
 // spans that need a page take stack entries top-1, top-2, ... in (seq, head)
 // order of a block prefix count (pops past the stack fail: slot -1, overflow).
-// Then each span's ceil(live / kPlanRows) items are listed at the block prefix
-// of the item counts, with their rank ranges, split indices, append row,
-// position and page ids.  plan_count[l] = the layer's items.
+// Then each span's items go to their fixed grid positions split *
+// padded_pairs + pair: rank range, split count, live count, append row,
+// position and page ids; split 0 of pair p at item p, the further splits
+// after the pairs at the block prefix of their counts, and their number in
+// the int before the layer's items.
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanMaxPairsPerThread = 8;  // pairs per layer <= 8192
 
@@ -185,110 +187,88 @@ __global__ __launch_bounds__(kPlanThreads) void paged_prepare_decode_plan_kernel
     int64_t s_b, int64_t s_h, int32_t* __restrict__ bt, int64_t bt_l, int64_t bt_b, int64_t bt_h,
     int32_t* __restrict__ held, int64_t hd_l, int64_t hd_b, int64_t hd_h, const int32_t* __restrict__ stack,
     int64_t stack_stride, int32_t* __restrict__ top, int max_pages, int32_t* __restrict__ overflow,
-    const int64_t* __restrict__ positions, int32_t* __restrict__ plan, int64_t plan_l,
-    int32_t* __restrict__ plan_count, int max_items, int num_seqs, int num_kv_heads) {
+    const int64_t* __restrict__ positions, int32_t* __restrict__ plan, int64_t plan_l, int split_rows,
+    int heavy_rows, int num_splits, int num_seqs, int num_kv_heads) {
   __shared__ int s_buf[kPlanThreads / 64];
   const int l = blockIdx.x;
   const int tid = threadIdx.x;
   const int pairs = num_seqs * num_kv_heads;
-  int n[kPlanMaxPairsPerThread], np[kPlanMaxPairsPerThread];
-  bool need[kPlanMaxPairsPerThread];
-  int needs = 0;
+  const int top0 = top[l];
+  int pops = 0, extra_before = 0;
+  int32_t* lp = plan + l * plan_l + kPlanLead;  // the layer's items; its further-split count at lp[-1]
+  const int nt = blockDim.x;  // a multiple of 64: the batch's pairs rounded up, at most kPlanThreads
 #pragma unroll
   for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
-    const int p = tid + k * kPlanThreads;
-    n[k] = np[k] = 0;
-    need[k] = false;
+    if (k * nt >= pairs) break;  // uniform
+    const int p = tid + k * nt;
+    int n = 0, np = 0;
+    bool need = false;
+    int b = 0, h = 0;
     if (p < pairs) {
-      const int b = p / num_kv_heads, h = p - b * num_kv_heads;
-      n[k] = live[l * l_l + b * l_b + h * l_h];
-      np[k] = held[l * hd_l + b * hd_b + h * hd_h];
-      need[k] = n[k] >= (np[k] << kPagedShift);
-      needs += need[k] ? 1 : 0;
+      b = p / num_kv_heads;
+      h = p - b * num_kv_heads;
+      n = live[l * l_l + b * l_b + h * l_h];
+      np = held[l * hd_l + b * hd_b + h * hd_h];
+      need = n >= (np << kPagedShift);
     }
-  }
-  // pops in (seq, head) order: a thread's pairs are p = tid + k * kPlanThreads,
-  // so rank the needers k-major: all threads' first pairs, then their second ...
-  int top0 = top[l];
-  int pops_before_k = 0;
-  int item_count[kPlanMaxPairsPerThread];
-  int32_t app[kPlanMaxPairsPerThread];
-#pragma unroll
-  for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
-    app[k] = -1;
-    item_count[k] = 0;
-    if (k * kPlanThreads >= pairs) break;  // uniform
+    // pops in (seq, head) order: pair p = tid + k * nt ranks among the
+    // needers of this round after those of the earlier rounds
     int tot = 0;
-    const int j = block_exclusive_scan(need[k] ? 1 : 0, s_buf, &tot) + pops_before_k;
-    pops_before_k += tot;
-    const int p = tid + k * kPlanThreads;
-    if (p >= pairs) continue;
-    const int b = p / num_kv_heads, h = p - b * num_kv_heads;
+    const int j = block_exclusive_scan(need ? 1 : 0, s_buf, &tot) + pops;
+    pops += tot;
     int32_t* btr = bt + l * bt_l + b * bt_b + h * bt_h;
     bool ok = true;
-    if (need[k]) {
-      ok = np[k] < max_pages && j < top0;
+    if (need) {
+      ok = np < max_pages && j < top0;
       if (ok) {
-        btr[np[k]] = stack[l * stack_stride + top0 - 1 - j];
-        held[l * hd_l + b * hd_b + h * hd_h] = np[k] + 1;
+        btr[np] = stack[l * stack_stride + top0 - 1 - j];
+        held[l * hd_l + b * hd_b + h * hd_h] = np + 1;
       } else {
         atomicExch(overflow, 1);
       }
     }
-    if (ok) {
-      app[k] = (btr[n[k] >> kPagedShift] << kPagedShift) + (n[k] & ((1 << kPagedShift) - 1));
-      live[l * l_l + b * l_b + h * l_h] = n[k] + 1;
-      n[k] += 1;
+    int32_t app = -1;
+    if (p < pairs && ok) {
+      app = (btr[n >> kPagedShift] << kPagedShift) + (n & ((1 << kPagedShift) - 1));
+      live[l * l_l + b * l_b + h * l_h] = n + 1;
+      n += 1;
     }
-    slot[l * s_l + b * s_b + h * s_h] = app[k];
-    item_count[k] = plan_items_of(n[k]);
-  }
-  if (tid == 0) top[l] = max(0, top0 - pops_before_k);
-  // items: list position = block prefix of the item counts, k-major like the pops
-  int items_before_k = 0;
-  int32_t* lp = plan + l * plan_l;
-#pragma unroll
-  for (int k = 0; k < kPlanMaxPairsPerThread; ++k) {
-    if (k * kPlanThreads >= pairs) break;  // uniform
-    int tot = 0;
-    const int first = block_exclusive_scan(item_count[k], s_buf, &tot) + items_before_k;
-    items_before_k += tot;
-    const int p = tid + k * kPlanThreads;
-    if (p >= pairs || item_count[k] == 0) continue;
-    const int b = p / num_kv_heads, h = p - b * num_kv_heads;
-    const int32_t* btr = bt + l * bt_l + b * bt_b + h * bt_h;
-    const int lv = n[k], ni = item_count[k];
-    const int per = plan_split_rows(lv, ni);
+    if (p < pairs) slot[l * s_l + b * s_b + h * s_h] = app;
+    // the pair's items: split 0 at p, the further ones packed after the pairs
+    const int ns = (p < pairs && n > 0) ? plan_splits(n, split_rows, heavy_rows, num_splits) : 1;
+    int extra_tot = 0;
+    const int extra = block_exclusive_scan(p < pairs ? ns - 1 : 0, s_buf, &extra_tot) + extra_before;
+    extra_before += extra_tot;
+    if (p >= pairs) continue;
+    const int per = plan_split_rows(n, ns);
     const int pos = (int)positions[b];
-    for (int s = 0; s < ni; ++s) {
-      const int idx = first + s;
-      if (idx >= max_items) {
-        atomicExch(overflow, 1);
-        break;
-      }
-      const int r0 = min(lv, s * per);
-      int r1 = min(lv, r0 + per);
+    for (int sp = 0; sp < ns; ++sp) {
+      int32_t* it = lp + (int64_t)(sp == 0 ? p : pairs + extra + sp - 1) * kPlanInts;
+      const int r0 = min(n, sp * per);
+      int r1 = min(n, r0 + per);
       int flags = 0;
-      if (app[k] >= 0 && r0 < lv && r1 == lv) {
+      if (app >= 0 && r0 < n && r1 == n) {
         flags = 1;
-        r1 = lv - 1;
+        r1 = n - 1;
       }
-      int32_t* it = lp + (int64_t)idx * kPlanInts;
-      reinterpret_cast<int4*>(it)[0] = make_int4(p, r0, r1, s | (ni << 16));
-      reinterpret_cast<int4*>(it)[1] = make_int4(lv, app[k], pos, flags);
+      reinterpret_cast<int4*>(it)[0] = make_int4(p, r0, r1, sp | (ns << 16));
+      reinterpret_cast<int4*>(it)[1] = make_int4(n, app, pos, flags);
       const int last = max(r1 - 1, r0);
-#pragma unroll
-      for (int j = 0; j < kPlanPages; j += 4) {
+      const int used = r1 > r0 ? (r1 - r0 + 63) / 64 * 4 : 0;  // quarters of the item's groups
+      for (int j4 = 0; j4 < used; j4 += 4) {
         int4 w;
-        w.x = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 0), last) >> kPagedShift] : -1;
-        w.y = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 1), last) >> kPagedShift] : -1;
-        w.z = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 2), last) >> kPagedShift] : -1;
-        w.w = r1 > r0 ? btr[min(r0 + kPlanPage * (j + 3), last) >> kPagedShift] : -1;
-        reinterpret_cast<int4*>(it + kPlanHeader)[j / 4] = w;
+        w.x = btr[min(r0 + kPlanPage * (j4 + 0), last) >> kPagedShift];
+        w.y = btr[min(r0 + kPlanPage * (j4 + 1), last) >> kPagedShift];
+        w.z = btr[min(r0 + kPlanPage * (j4 + 2), last) >> kPagedShift];
+        w.w = btr[min(r0 + kPlanPage * (j4 + 3), last) >> kPagedShift];
+        reinterpret_cast<int4*>(it + kPlanHeader)[j4 / 4] = w;
       }
     }
   }
-  if (tid == 0) plan_count[l] = min(items_before_k, max_items);
+  if (tid == 0) {
+    top[l] = max(0, top0 - pops);
+    lp[-1] = extra_before;
+  }
 }
 
 FDMS_EXPORT int fdms_paged_prepare_decode_plan(int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h,
@@ -297,20 +277,28 @@ FDMS_EXPORT int fdms_paged_prepare_decode_plan(int32_t* live, int64_t l_l, int64
                                                int32_t* pages_held, int64_t hd_l, int64_t hd_b, int64_t hd_h,
                                                const int32_t* page_stack, int64_t stack_stride, int32_t* page_top,
                                                int max_pages, int32_t* overflow, const int64_t* positions,
-                                               int32_t* plan, int64_t plan_l, int32_t* plan_count, int max_items,
-                                               int num_layers, int num_seqs, int num_kv_heads, void* stream) {
-  if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0 || max_pages <= 0 || max_items <= 0)
+                                               int32_t* plan, int64_t plan_l, int split_rows, int heavy_rows,
+                                               int num_splits, int num_layers, int num_seqs, int num_kv_heads,
+                                               void* stream) {
+  if (num_layers <= 0 || num_seqs < 0 || num_kv_heads <= 0 || max_pages <= 0 || num_splits <= 0)
+    return (int)hipErrorInvalidValue;
+  if (split_rows < 64 || split_rows > kPlanRows || heavy_rows < 64 || heavy_rows > split_rows ||
+      (split_rows % 64) || (heavy_rows % 64))
     return (int)hipErrorInvalidValue;
   if ((int64_t)num_seqs * num_kv_heads > (int64_t)kPlanThreads * kPlanMaxPairsPerThread)
     return (int)hipErrorInvalidValue;
   if (!live || !slot_out || !block_table || !pages_held || !page_stack || !page_top || !overflow || !positions ||
-      !plan || !plan_count)
+      !plan)
     return (int)hipErrorInvalidValue;
-  if (((uintptr_t)plan % 16) || plan_l % 4 || plan_l < (int64_t)max_items * kPlanInts) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(paged_prepare_decode_plan_kernel, dim3(num_layers), dim3(kPlanThreads), 0, (hipStream_t)stream,
+  if (num_seqs == 0) return 0;
+  const int64_t items = (int64_t)num_splits * num_seqs * num_kv_heads;
+  if (((uintptr_t)plan % 16) || plan_l % 4 || plan_l < kPlanLead + items * kPlanInts) return (int)hipErrorInvalidValue;
+  const int pairs = num_seqs * num_kv_heads;
+  const int threads = pairs >= kPlanThreads ? kPlanThreads : ((pairs + 63) / 64) * 64;
+  hipLaunchKernelGGL(paged_prepare_decode_plan_kernel, dim3(num_layers), dim3(threads), 0, (hipStream_t)stream,
                      live, l_l, l_b, l_h, slot_out, s_l, s_b, s_h, block_table, bt_l, bt_b, bt_h, pages_held, hd_l,
                      hd_b, hd_h, page_stack, stack_stride, page_top, max_pages, overflow, positions, plan, plan_l,
-                     plan_count, max_items, num_seqs, num_kv_heads);
+                     split_rows, heavy_rows, num_splits, num_seqs, num_kv_heads);
   FDMS_LAUNCH_CHECK();
   return 0;
 }

@@ -108,8 +108,8 @@ class ModelRunner:
         self.static_tokens = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
         # the paged decode step's attention work plan (static: captured graphs keep its address)
         self.decode_plan = (DecodePlan(self.device, self.num_layers, self.max_num_seqs * self.num_kv_heads,
-                                       config.max_model_len + 1)
-                            if self.compact_kv_manager.paged and decode_plan_enabled() else None)
+                                       config.max_model_len + 1, hf.head_dim)
+                            if self.compact_kv_manager.paged and decode_plan_enabled(hf.head_dim) else None)
         self.prompt_stages: dict[int, PromptStage] = {}  # long prompts between their chunks
         self.pinned_ids = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)

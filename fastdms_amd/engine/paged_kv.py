@@ -351,8 +351,9 @@ class PagedCompactKVManager(CompactKVManager):
                 raise ValueError("a planned decode step needs the step's int64 positions")
             if batch * H > plan.pairs:
                 raise ValueError(f"the plan holds {plan.pairs} pairs, the batch has {batch * H}")
+            rows, heavy, splits = plan.partition(batch * H)
             nat.call("fdms_paged_prepare_decode_plan", *args, positions.data_ptr(), plan.items.data_ptr(),
-                     plan.items.stride(0), plan.count.data_ptr(), plan.max_items, L, batch, H, nat.stream())
+                     plan.items.stride(0), rows, heavy, splits, L, batch, H, nat.stream())
         return bt, live
 
     def prepare_decode_metadata(self, seqs: list[Sequence]):

@@ -117,8 +117,8 @@ class Attention(nn.Module):
                          norm_eps=(q_norm if q_norm is not None else k_norm).eps)
         if ctx.compact_plan is not None:  # the step's work plan (paged layout)
             return fused_decode_attention_planned(
-                q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, evict_out, ctx.compact_plan,
-                self.layer_id, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
+                q, k, v, cos_sin_cache, self.compact_k_cache, self.compact_v_cache, evict_out, positions,
+                ctx.compact_plan, self.layer_id, num_kv_heads=self.num_kv_heads, alpha_scale=alpha_scale, alpha_offset=alpha_offset,
                 scale=self.scale, k_scale=self.compact_k_scale, v_scale=self.compact_v_scale, **norms)
         base, bt, live, slot = self._layer_metadata(ctx)
         return fused_dms_rope_store_compact_decode_attention(

@@ -510,45 +510,86 @@ def fused_dms_rope_store_compact_decode_attention(
     return out
 
 
-PLAN_ROWS = 512  # ranks per work item of the planned launch (fdms_plan.h kPlanRows)
-PLAN_INTS = 40   # int32 per work item
+PLAN_ROWS = 1024  # ranks per work item at most (fdms_plan.h kPlanRows: two 64-row groups per wave)
+PLAN_INTS = 72    # int32 per work item
 
 
-def decode_plan_enabled() -> bool:
-    """The paged decode step plans its attention work once per step
-    (fdms_paged_prepare_decode_plan + fdms_fused_decode_attention_planned);
-    FASTDMS_AMD_ATTN_PLAN=0 keeps the per-layer launch that partitions
-    inside the kernel (same results up to fp32 summation order)."""
-    return os.environ.get("FASTDMS_AMD_ATTN_PLAN", "1").strip() != "0"
+def decode_plan_enabled(head_dim: int) -> bool:
+    """Whether the paged decode step plans its attention work once per step
+    (fdms_paged_prepare_decode_plan + fdms_fused_decode_attention_planned)
+    instead of partitioning inside each layer's launch.  Default: at head_dim
+    128 (measured on MI355X, Qwen3-8B shape c=8: 15.2 against 17.3 us per
+    launch, 1 854 against 1 823 decode tok/s); not at head_dim 64 (Llama-3.2-1B
+    shape c=8: the same bits 2.5 % slower, 9.26 against 9.02 us -- the heavy
+    pairs' later splits learn their pair only from the item -- and the plan
+    kernel costs more than the slot kernel it replaces).
+    FASTDMS_AMD_ATTN_PLAN=1 / 0 forces it on / off."""
+    env = os.environ.get("FASTDMS_AMD_ATTN_PLAN", "").strip()
+    if env in ("0", "1"):
+        return env == "1"
+    return head_dim == 128
 
 
-def plan_splits_bound(max_live: int) -> int:
-    """Items of one pair at most (its live count is at most ``max_live``)."""
-    return max(1, -(-int(max_live) // PLAN_ROWS))
+def plan_partition(pairs: int, head_dim: int, max_live: int) -> tuple[int, int, int]:
+    """(split_rows, heavy_rows, num_splits) of the planned launch for `pairs`
+    (seq, kv head) pairs: a pair of at most split_rows ranks is one workgroup
+    (two 64-row groups per wave of its eight), a longer one takes pieces of
+    heavy_rows ranks, at most num_splits.  At head_dim 64 this is the
+    unplanned eight-wave launch's partition (1024 / 512 rows up to 128
+    pairs, 1024 / 1024 beyond), so the two give the same bits; at head_dim
+    128 pieces of one group per wave (512 rows: the eight-wave loop over a
+    128-dim group is the longer part of a pair's chain; measured on the
+    Qwen3-8B shape).  FASTDMS_AMD_PLAN_SPLIT_ROWS / _HEAVY_ROWS override
+    (multiples of 64, heavy <= split <= 1024; tuning only)."""
+    if head_dim <= 64:
+        rows, heavy = PLAN_ROWS, (512 if pairs <= 128 else PLAN_ROWS)
+    else:
+        rows = heavy = 512
+    env_r = os.environ.get("FASTDMS_AMD_PLAN_SPLIT_ROWS", "").strip()
+    env_h = os.environ.get("FASTDMS_AMD_PLAN_HEAVY_ROWS", "").strip()
+    if env_r.isdigit():
+        rows = int(env_r)
+    if env_h.isdigit():
+        heavy = int(env_h)
+    heavy = min(heavy, rows)
+    if rows % 64 or heavy % 64 or not 64 <= heavy <= rows <= PLAN_ROWS:
+        raise ValueError(f"plan partition {rows} / {heavy} rows: multiples of 64, heavy <= split <= {PLAN_ROWS}")
+    return rows, heavy, int(min(_MFMA_CAP_SPLITS, max(1, -(-int(max_live) // heavy))))
+
+
+PLAN_LEAD = 4  # ints before a layer's items (the last: its count of further splits)
 
 
 class DecodePlan:
-    """Static buffers of the step's attention work plan: ``items`` [layers,
-    max_items, 40] int32, ``count`` [layers] int32.  Sized for ``pairs``
-    (seq, kv head) pairs whose live counts stay within ``max_live``; the
-    addresses never change, so captured decode graphs keep them."""
+    """Static buffer of the step's attention work plan, ``items`` [layers,
+    4 + items * 72] int32: per layer 4 ints (the last: the number of further
+    splits) and one item per live workgroup of a planned launch (split 0 of
+    pair p at item p, the further splits after the pairs).  Sized for every
+    batch of up to ``max_pairs`` (seq, kv head) pairs whose live counts stay
+    within ``max_live``; its address never changes, so captured decode graphs
+    keep it."""
 
-    def __init__(self, device, num_layers: int, pairs: int, max_live: int):
-        self.splits = plan_splits_bound(max_live)
-        self.max_items = pairs * self.splits
-        self.pairs = pairs
-        self.items = torch.zeros((num_layers, self.max_items, PLAN_INTS), device=device, dtype=torch.int32)
-        self.count = torch.zeros(num_layers, device=device, dtype=torch.int32)
+    def __init__(self, device, num_layers: int, max_pairs: int, max_live: int, head_dim: int):
+        self.max_live, self.head_dim, self.pairs = int(max_live), int(head_dim), int(max_pairs)
+        need = max(p * self.partition(p)[2] for p in range(1, max_pairs + 1))
+        self.items = torch.zeros((num_layers, PLAN_LEAD + need * PLAN_INTS), device=device, dtype=torch.int32)
 
-    def grid_items(self, batch: int, num_kv_heads: int) -> int:
-        """Workgroups of a planned launch over ``batch`` sequences: their items
-        at most (those past the step's count exit at once)."""
-        return batch * num_kv_heads * self.splits
+    def layer_items(self, layer_id: int) -> torch.Tensor:
+        """Layer ``layer_id``'s items (the attention launch's plan pointer)."""
+        return self.items[layer_id, PLAN_LEAD:]
+
+    def further_splits(self) -> torch.Tensor:
+        """[layers] view of each layer's count of further splits."""
+        return self.items[:, PLAN_LEAD - 1]
+
+    def partition(self, pairs: int) -> tuple[int, int, int]:
+        return plan_partition(pairs, self.head_dim, self.max_live)
 
 
 def fused_decode_attention_planned(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos_sin_cache: torch.Tensor,
                                    compact_k: torch.Tensor, compact_v: torch.Tensor, evict_out: torch.Tensor,
-                                   plan: DecodePlan, layer_id: int, *, num_kv_heads: int, alpha_scale: float,
+                                   positions: torch.Tensor, plan: DecodePlan, layer_id: int, *, num_kv_heads: int,
+                                   alpha_scale: float,
                                    alpha_offset: float, scale: float | None = None, out: torch.Tensor | None = None,
                                    k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
                                    q_norm_weight: torch.Tensor | None = None,
@@ -556,9 +597,10 @@ def fused_decode_attention_planned(q: torch.Tensor, k: torch.Tensor, v: torch.Te
     """fused_dms_rope_store_compact_decode_attention on the paged layout with
     the step's work plan (written by PagedCompactKVManager.paged_prepare_decode
     with a plan): the plan's items of layer ``layer_id`` carry the pairs'
-    rank ranges, append rows, positions and page ids, so no live counts,
-    slots, positions or block tables are passed.  Same checks and results as
-    the unplanned launch (outputs up to fp32 summation order)."""
+    rank ranges, live counts, append rows and page ids, so no live counts,
+    slots or block tables are passed; ``positions`` are the step's int64
+    positions.  Same checks and results as the unplanned launch (bit for
+    bit where both use the same partition, see plan_partition)."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
         raise ValueError("expected q [B, Hq, D] and k/v [B, Hkv, D]")
     batch, num_q_heads, head_dim = q.shape
@@ -566,6 +608,8 @@ def fused_decode_attention_planned(q: torch.Tensor, k: torch.Tensor, v: torch.Te
         raise ValueError(f"q/k shape mismatch: q={tuple(q.shape)}, k={tuple(k.shape)}, num_kv_heads={num_kv_heads}")
     if batch * num_kv_heads > plan.pairs:
         raise ValueError(f"the plan holds {plan.pairs} pairs, the batch has {batch * num_kv_heads}")
+    if positions.dtype != torch.int64 or positions.shape[0] < batch:
+        raise ValueError("positions must be int64 [batch]")
     if evict_out.dtype != torch.bool or tuple(evict_out.shape) != (batch, num_kv_heads):
         raise ValueError(f"evict_out must be bool {(batch, num_kv_heads)}")
     if cos_sin_cache.ndim != 3 or cos_sin_cache.shape[2] != head_dim or cos_sin_cache.dtype != torch.float32:
@@ -585,18 +629,18 @@ def fused_decode_attention_planned(q: torch.Tensor, k: torch.Tensor, v: torch.Te
         if w is not None and (w.dtype != torch.bfloat16 or w.shape != (head_dim,) or not w.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous bf16 [{head_dim}] tensor")
     pairs = batch * num_kv_heads
-    ws, counters = attention_workspace(q.device, pairs * plan.splits * group * (head_dim + 2), pairs)
+    splits = plan.partition(pairs)[2]
+    ws, counters = attention_workspace(q.device, pairs * splits * group * (head_dim + 2), pairs)
     s_, off, thr, positive = dms_threshold_args(alpha_scale, alpha_offset)
     ev = evict_out.view(torch.uint8)
-    items = plan.items[layer_id]
+    items = plan.layer_items(layer_id)
     nat.call("fdms_fused_decode_attention_planned", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
              k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cos_sin_cache.data_ptr(),
-             cos_sin_cache.stride(0), cos_sin_cache.stride(2), items.data_ptr(),
-             plan.count[layer_id:layer_id + 1].data_ptr(), plan.grid_items(batch, num_kv_heads), ev.data_ptr(),
+             cos_sin_cache.stride(0), cos_sin_cache.stride(2), positions.data_ptr(), items.data_ptr(), ev.data_ptr(),
              ev.stride(0),
              ev.stride(1), s_, off, thr, positive, compact_k.data_ptr(), compact_v.data_ptr(), compact_k.stride(0),
              out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), counters.data_ptr(), batch, num_kv_heads,
-             group, head_dim, plan.splits, float(scale), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
+             group, head_dim, splits, float(scale), nat.ptr(_scale_table(k_scale, num_kv_heads, "k_scale")),
              nat.ptr(_scale_table(v_scale, num_kv_heads, "v_scale")), nat.ptr(q_norm_weight),
              nat.ptr(k_norm_weight), float(norm_eps), nat.stream())
     return out

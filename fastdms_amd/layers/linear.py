@@ -367,14 +367,29 @@ def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
     return tok if greedy else y
 
 
+def fp8_gemm_impl() -> str:
+    """The FP8 GEMM of prefill row counts: "hipblaslt" (default; torch's
+    _scaled_mm with row-wise scales, the call the reference makes in
+    _fp8_linear, linear.py:652-659: a plain library GEMM, 1.8-2.2 PFLOP/s at
+    the Llama-3.2-1B prefill shapes on MI355X) or "fdms" (fdms_fp8_gemm, this
+    library's FP8 matrix-core kernel, 0.6-0.8 PFLOP/s there).
+    FASTDMS_AMD_FP8_GEMM selects; shapes hipBLASLt does not take (K or N not
+    multiples of 16) run fdms_fp8_gemm, row counts are padded to 16."""
+    impl = os.environ.get("FASTDMS_AMD_FP8_GEMM", "hipblaslt").strip().lower()
+    if impl not in ("hipblaslt", "fdms"):
+        raise ValueError(f"FASTDMS_AMD_FP8_GEMM must be 'hipblaslt' or 'fdms', got {impl!r}")
+    return impl
+
+
 def fp8_gemm(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor,
              bias: torch.Tensor | None = None, *, torch_form: bool = True,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, impl: str | None = None) -> torch.Tensor:
     """_fp8_linear for prefill row counts on the FP8 matrix cores
     (linear.py:635-662): rows quantised per row (fdms_quantize_fp8_rows), then
-    fdms_fp8_gemm: y = bf16(sum_k xq * w8 * x_scale_inv * w_scale_inv), bias
-    added in bf16.  x [M, K] bf16 / fp32, weight_fp8 [N, K] e4m3fn, K a
-    multiple of 16."""
+    y = bf16(sum_k xq * w8 * x_scale_inv * w_scale_inv) with fp32 accumulation
+    (fp8_gemm_impl: hipBLASLt's scaled GEMM or fdms_fp8_gemm), bias added in
+    bf16.  x [M, K] bf16 / fp32, weight_fp8 [N, K] e4m3fn, K a multiple of
+    16."""
     if x.dim() != 2 or weight_fp8.dim() != 2 or x.shape[1] != weight_fp8.shape[1]:
         raise ValueError(f"fp8_gemm shape mismatch: x {tuple(x.shape)}, weight {tuple(weight_fp8.shape)}")
     rows, k = x.shape
@@ -382,13 +397,27 @@ def fp8_gemm(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.
     if k % 16 or weight_fp8.stride(1) != 1 or weight_fp8.stride(0) % 16 or weight_fp8.data_ptr() % 16:
         raise ValueError("fp8_gemm needs K a multiple of 16 and 16-byte aligned weight rows")
     nat.require_cuda(x, weight_fp8, weight_scale_inv, what="fp8_gemm")
-    xq, xsi = quantize_fp8_rows(x.contiguous(), torch_form=torch_form)
     sinv = weight_scale_inv.reshape(-1).float().contiguous()
     if sinv.numel() != n:
         raise ValueError(f"weight_scale_inv has {sinv.numel()} entries for {n} rows")
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    impl = impl or fp8_gemm_impl()
+    if impl == "hipblaslt" and n % 16 == 0 and k % 16 == 0 and out is None:
+        # hipBLASLt takes row counts in multiples of 16: the quantised rows
+        # are padded with zero rows (scale 1), whose outputs are dropped
+        rows16 = -(-rows // 16) * 16
+        xq = torch.empty((rows16, k), device=x.device, dtype=torch.float8_e4m3fn)
+        xsi = torch.empty(rows16, device=x.device, dtype=torch.float32)
+        if rows16 > rows:
+            xq[rows:].view(torch.uint8).zero_()
+            xsi[rows:].fill_(1.0)
+        quantize_fp8_rows(x.contiguous(), out=xq[:rows], scale_inv=xsi[:rows], torch_form=torch_form)
+        y = torch._scaled_mm(xq, weight_fp8.t(), scale_a=xsi.reshape(-1, 1), scale_b=sinv.reshape(1, -1),
+                             out_dtype=torch.bfloat16, use_fast_accum=False)[:rows]
+        return y if b is None else y + b
+    xq, xsi = quantize_fp8_rows(x.contiguous(), torch_form=torch_form)
     if out is None:
         out = torch.empty((rows, n), device=x.device, dtype=torch.bfloat16)
-    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
     nat.call("fdms_fp8_gemm", xq.data_ptr(), xq.stride(0), xsi.data_ptr(), weight_fp8.data_ptr(),
              weight_fp8.stride(0), sinv.data_ptr(), nat.ptr(b), out.data_ptr(), out.stride(0), rows, n, k,
              nat.stream())

@@ -507,46 +507,53 @@ int fdms_fused_decode_attention_paged(const void* q, int64_t qs_b, int64_t qs_h,
 /* The decode step's attention work plan (no reference counterpart): the
  * append rows of fdms_paged_prepare_decode (one workgroup per layer: the
  * layer's page pops take stack entries top-1, top-2, ... in (seq, head)
- * order, no atomics), then per layer a list of work items in plan[l *
- * plan_l ...], one per workgroup of that layer's
- * fdms_fused_decode_attention_planned launch, and their number in
- * plan_count[l].  A span of live ranks (after the append) gets
- * ceil(live / 512) items of equal 64-aligned rank ranges; an item holds 40
- * int32: pair, first rank, end rank (the appended rank left out), split |
- * (splits of the pair << 16), live, append row, position (positions[b],
- * int64 [num_seqs]), flags (bit 0: the item holds the appended rank), then the
- * page id of each of its 32 quarters of 16 ranks.  plan 16-byte aligned,
- * plan_l >= max_items * 40; more items than max_items set *overflow.
- * num_seqs * num_kv_heads <= 8192. */
+ * order, no atomics), then per layer one work item for every live workgroup
+ * of that layer's fdms_fused_decode_attention_planned launch.  Layer l's
+ * block starts at plan + l * plan_l: 4 ints (the last one: the number of
+ * further splits), then the items, 72 int32 each: split 0 of pair p at item
+ * p, the pairs' further splits packed after the pairs in (pair, split)
+ * order.  A pair of live ranks (after the append) takes ns = 1 split if live
+ * <= split_rows, else min(num_splits, ceil(live / heavy_rows)), of
+ * ceil(live / ns) ranks rounded up to 64 (the unplanned launch's
+ * partition).  An item holds pair, first rank, end rank (the appended rank
+ * left out), split | (ns << 16), live, append row, position, flags (bit 0:
+ * the item holds the appended rank), then the page id of each of its 16-rank
+ * quarters (up to 64).  split_rows and heavy_rows multiples of 64,
+ * heavy_rows <= split_rows <= 1024; plan 16-byte aligned, plan_l a multiple
+ * of 4 and >= 4 + num_splits * num_seqs * num_kv_heads * 72; num_seqs *
+ * num_kv_heads <= 8192. */
 int fdms_paged_prepare_decode_plan(int32_t* live, int64_t l_l, int64_t l_b, int64_t l_h, int32_t* slot_out,
                                    int64_t s_l, int64_t s_b, int64_t s_h, int32_t* block_table, int64_t bt_l,
                                    int64_t bt_b, int64_t bt_h, int32_t* pages_held, int64_t hd_l, int64_t hd_b,
                                    int64_t hd_h, const int32_t* page_stack, int64_t stack_stride, int32_t* page_top,
                                    int max_pages, int32_t* overflow, const int64_t* positions, int32_t* plan,
-                                   int64_t plan_l, int32_t* plan_count, int max_items, int num_layers, int num_seqs,
-                                   int num_kv_heads, void* stream);
+                                   int64_t plan_l, int split_rows, int heavy_rows, int num_splits, int num_layers,
+                                   int num_seqs, int num_kv_heads, void* stream);
 
 /* A9 + B2-B5 on the step's plan (no reference counterpart as a launch form;
  * the computation is fdms_fused_decode_attention_paged's, i.e. the
  * reference's fused_dms_rope_store_compact_decode + compact_decode_attention,
- * compact_attention.py:67-209, 1010-1336): one layer, plan / plan_count that
- * layer's items and count from fdms_paged_prepare_decode_plan.  The grid is
- * max_items workgroups of 8 waves; each reads its item (one memory round
- * trip) and then its K/V rows, one 64-row group per wave.  num_splits bounds
- * the items of one pair: the workspace holds batch * num_kv_heads * num_splits
- * * group_size * (head_dim + 2) floats and counters batch * num_kv_heads
- * zeros.  Decisions, appended rows and outputs as the unplanned launch
- * (outputs to fp32 summation order). */
+ * compact_attention.py:67-209, 1010-1336): one layer, plan = that layer's
+ * items from fdms_paged_prepare_decode_plan (its block + 4 ints: the count of
+ * further splits is plan[-1]), positions the step's int64 positions.  The
+ * grid holds num_splits x pairs workgroups of 8 waves: workgroup p < pairs
+ * runs split 0 of pair p and loads the pair's raw rows and position with
+ * its item; a later one runs a further split named by its item, or exits
+ * past the layer's count; then its K/V rows (two 64-row groups per wave at
+ * most, their page ids from the item).  The workspace holds batch * num_kv_heads *
+ * num_splits * group_size * (head_dim + 2) floats and counters batch *
+ * num_kv_heads zeros.  Planned with the unplanned launch's partition, the
+ * decisions, appended rows and outputs are that launch's, bit for bit. */
 int fdms_fused_decode_attention_planned(const void* q, int64_t qs_b, int64_t qs_h, const void* k, int64_t ks_b,
                                         int64_t ks_h, const void* v, int64_t vs_b, int64_t vs_h,
-                                        const float* cos_sin, int64_t cs_p, int64_t cs_d, const int32_t* plan,
-                                        const int32_t* plan_count, int max_items, uint8_t* evict_out, int64_t ev_b,
-                                        int64_t ev_h, float alpha_scale, float alpha_offset, float threshold,
-                                        int positive_scale, void* compact_k, void* compact_v, int64_t c_s,
-                                        void* out, int64_t os_b, int64_t os_h, float* workspace, int* counters,
-                                        int batch, int num_kv_heads, int group_size, int head_dim, int num_splits,
-                                        float scale, const float* k_scale, const float* v_scale,
-                                        const void* q_norm, const void* k_norm, float norm_eps, void* stream);
+                                        const float* cos_sin, int64_t cs_p, int64_t cs_d, const int64_t* positions,
+                                        const int32_t* plan, uint8_t* evict_out, int64_t ev_b, int64_t ev_h,
+                                        float alpha_scale, float alpha_offset, float threshold, int positive_scale,
+                                        void* compact_k, void* compact_v, int64_t c_s, void* out, int64_t os_b,
+                                        int64_t os_h, float* workspace, int* counters, int batch, int num_kv_heads,
+                                        int group_size, int head_dim, int num_splits, float scale,
+                                        const float* k_scale, const float* v_scale, const void* q_norm,
+                                        const void* k_norm, float norm_eps, void* stream);
 
 /* FP8 GEMM for prefill row counts (replaces the torch._scaled_mm call of
  * _fp8_linear, linear.py:635-662): y[m, n] = bf16((sum_k x[m, k] * w[n, k]) *

@@ -653,110 +653,121 @@ class Emulator:
                     lv[l, b, h] = n + 1
         return 0
 
+    @staticmethod
+    def _plan_splits(n, rows, heavy, splits):
+        return 1 if n <= rows else min(splits, -(-n // heavy))
+
     def paged_prepare_decode_plan(self, live, l_l, l_b, l_h, slot, s_l, s_b, s_h, bt, bt_l, bt_b, bt_h, held, hd_l,
                                   hd_b, hd_h, stack, stack_stride, top, max_pages, overflow, positions, plan, plan_l,
-                                  plan_count, max_items, L, B, H, stream):
+                                  split_rows, heavy_rows, num_splits, L, B, H, stream):
         """The slot assignment above (its sequential pops take the stack from
         the top in (layer, seq, head) order, as the kernel's block prefix
-        does), then each layer's work items: ceil(live / 512) per span, equal
-        64-aligned rank ranges, the appended rank left out of the rows and
-        flagged, the page id of every 16-rank quarter."""
-        if max_items <= 0 or B * H > 8192 or not positions or not plan or not plan_count:
+        does), then each layer's work items: the unplanned launch's partition
+        of each span, the appended rank left out of the rows and flagged, the
+        page id of every 16-rank quarter; split 0 of pair p at item p, the
+        further splits packed after the pairs, their number in the int
+        before the layer's items."""
+        if (num_splits <= 0 or B * H > 8192 or not positions or not plan or split_rows % 64 or heavy_rows % 64
+                or not 64 <= heavy_rows <= split_rows <= 1024):
             return 1
         rc = self.paged_prepare_decode(live, l_l, l_b, l_h, slot, s_l, s_b, s_h, bt, bt_l, bt_b, bt_h, held, hd_l,
                                        hd_b, hd_h, stack, stack_stride, top, max_pages, overflow, L, B, H, stream)
         if rc or B == 0:
             return rc
+        pairs = B * H
         lv = self.view(live, torch.int32, (L, B, H), (l_l, l_b, l_h), "live")
         sv = self.view(slot, torch.int32, (L, B, H), (s_l, s_b, s_h), "slot_out")
         pos = self.view(positions, torch.int64, (B,), (1,), "positions")
-        cnt = self.view(plan_count, torch.int32, (L,), (1,), "plan_count")
-        ov = self.view(overflow, torch.int32, (1,), (1,), "overflow")
         for l in range(L):
-            items = self.view_at(plan, torch.int32, l * plan_l, (max_items, 40), (40, 1), "plan")
-            n_items = 0
+            block = self.view_at(plan, torch.int32, l * plan_l, (4 + num_splits * pairs * 72,), (1,), "plan")
+            items = block[4:].view(num_splits * pairs, 72)
+            extra = 0
             for b in range(B):
                 for h in range(H):
+                    p = b * H + h
                     n, app = int(lv[l, b, h]), int(sv[l, b, h])
-                    ni = -(-n // 512)
-                    if ni == 0:
-                        continue
-                    per = (-(-n // ni) + 63) // 64 * 64
+                    ns = self._plan_splits(n, split_rows, heavy_rows, num_splits) if n > 0 else 1
+                    per = (-(-n // ns) + 63) // 64 * 64
                     table = self.view_at(bt, torch.int32, l * bt_l + b * bt_b + h * bt_h, (max_pages,), (1,),
                                          "block_table")
-                    for sp in range(ni):
-                        if n_items >= max_items:
-                            ov[0] = 1
-                            break
+                    for sp in range(ns):
+                        it = items[p if sp == 0 else pairs + extra + sp - 1]
                         r0 = min(n, sp * per)
                         r1 = min(n, r0 + per)
                         flags = 0
                         if app >= 0 and r0 < n and r1 == n:
                             flags, r1 = 1, n - 1
                         last = max(r1 - 1, r0)
-                        pages = [int(table[min(r0 + 16 * j, last) // 16]) if r1 > r0 else -1 for j in range(32)]
-                        items[n_items] = torch.tensor([b * H + h, r0, r1, sp | (ni << 16), n, app, int(pos[b]),
-                                                       flags] + pages, dtype=torch.int32)
-                        n_items += 1
-            cnt[l] = n_items
+                        used = (r1 - r0 + 63) // 64 * 4 if r1 > r0 else 0
+                        pages = [int(table[min(r0 + 16 * j, last) // 16]) for j in range(used)]
+                        it[:8 + used] = torch.tensor([p, r0, r1, sp | (ns << 16), n, app, int(pos[b]), flags] + pages,
+                                                     dtype=torch.int32)
+                    extra += ns - 1
+            block[3] = extra
         return 0
 
-    def fused_decode_attention_planned(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d, plan,
-                                       plan_count, max_items, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv,
-                                       c_s, out, os_b, os_h, ws, counters, B, H, G, D, splits, scale, k_scale,
-                                       v_scale, q_norm, k_norm, eps, stream):
-        """Check the layer's plan (every pair's items cover its ranks once, in
-        split order, with consistent split counts, live count, append row and
-        position), rebuild each span's rows from the items' page ids alone,
-        and run the unplanned composition on them."""
+    def fused_decode_attention_planned(self, q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d,
+                                       positions, plan, ev_out, ev_b, ev_h, a_s, a_o, thr, pos_scale, ck, cv, c_s,
+                                       out, os_b, os_h, ws, counters, B, H, G, D, splits, scale, k_scale, v_scale,
+                                       q_norm, k_norm, eps, stream):
+        """Check the layer's plan (every pair's live items cover its ranks
+        once, in split order, with consistent split counts, live count, append
+        row and position; the items past its count name its pair and count),
+        rebuild each span's rows from the items' page ids alone, and run the
+        unplanned composition on them."""
         if B == 0:
             return 0
-        if max_items <= 0 or splits <= 0 or G > 4 or D not in (64, 128):
+        if splits <= 0 or G > 4 or D not in (64, 128) or not positions:
             return 1
-        n = int(self.view(plan_count, torch.int32, (1,), (1,), "plan_count")[0])
-        if n > max_items:
-            raise OutOfBounds(f"{self.name}: {n} items for a grid of {max_items}")
-        items = self.view(plan, torch.int32, (max(n, 1), 40), (40, 1), "plan")[:n].clone()
-        per_pair: dict[int, list] = {}
-        for it in items.tolist():
-            per_pair.setdefault(it[0], []).append(it)
-        if sorted(per_pair) != list(range(B * H)):
-            raise OutOfBounds(f"{self.name}: the plan covers pairs {sorted(per_pair)}, not 0 .. {B * H - 1}")
+        pairs = B * H
+        extra = int(self.view_at(plan, torch.int32, -1, (1,), (1,), "plan count")[0])
+        if not 0 <= extra <= pairs * (splits - 1):
+            raise OutOfBounds(f"{self.name}: {extra} further splits for a grid of {pairs * splits}")
+        items = self.view(plan, torch.int32, (pairs + extra, 72), (72, 1), "plan").clone().tolist()
+        pos_in = self.view(positions, torch.int64, (B,), (1,), "positions")
         live = torch.zeros((B, H), dtype=torch.int32)
         slot = torch.full((B, H), -1, dtype=torch.int32)
-        pos = torch.zeros(B, dtype=torch.int64)
-        maxp = max(1, max(-(-its[0][4] // 16) for its in per_pair.values()))
+        maxp = 1
+        its_of = {p: [items[p]] for p in range(pairs)}
+        for it in items[pairs:]:
+            if not 0 <= it[0] < pairs:
+                raise OutOfBounds(f"{self.name}: item of pair {it[0]}")
+            its_of[it[0]].append(it)
+        for p, its in its_of.items():
+            ns = its[0][3] >> 16
+            if len(its) != ns or any(it[0] != p or (it[3] & 0xFFFF) != sp or it[3] >> 16 != ns
+                                     for sp, it in enumerate(its)) or not 1 <= ns <= splits:
+                raise OutOfBounds(f"{self.name}: inconsistent items of pair {p}")
+            maxp = max(maxp, -(-its[0][4] // 16))
         table = torch.full((B, H, maxp), -1, dtype=torch.int32)
-        for pair, its in per_pair.items():
-            b, h = divmod(pair, H)
-            ni = its[0][3] >> 16
-            lv, app, p = its[0][4], its[0][5], its[0][6]
-            if [it[3] & 0xFFFF for it in its] != list(range(ni)) or any(it[3] >> 16 != ni for it in its) \
-                    or any((it[4], it[5], it[6]) != (lv, app, p) for it in its) or ni > splits:
-                raise OutOfBounds(f"{self.name}: inconsistent items of pair {pair}")
+        for p, its in its_of.items():
+            b, h = divmod(p, H)
+            lv, app, ps = its[0][4], its[0][5], its[0][6]
+            if any((it[4], it[5], it[6]) != (lv, app, ps) for it in its) or ps != int(pos_in[b]):
+                raise OutOfBounds(f"{self.name}: inconsistent items of pair {p}")
             covered = 0
-            for it in its:
+            for i, it in enumerate(its):
                 r0, r1, flags = it[1], it[2], it[7]
-                if r0 != covered or r0 % 64 or r1 < r0 or r1 - r0 > 512:
-                    raise OutOfBounds(f"{self.name}: item ranks [{r0}, {r1}) of pair {pair} after {covered}")
+                if r0 != covered or r0 % 64 or r1 < r0 or r1 - r0 > 1024:
+                    raise OutOfBounds(f"{self.name}: item ranks [{r0}, {r1}) of pair {p} after {covered}")
                 for r in range(r0, r1):
                     page = it[8 + (r - r0) // 16]
                     if table[b, h, r // 16] not in (-1, page):
-                        raise OutOfBounds(f"{self.name}: pair {pair} rank {r} on two pages")
+                        raise OutOfBounds(f"{self.name}: pair {p} rank {r} on two pages")
                     table[b, h, r // 16] = page
                 covered = r1
                 if flags & 1:
-                    if app < 0 or r1 != lv - 1 or it is not its[-1]:
-                        raise OutOfBounds(f"{self.name}: appended rank of pair {pair} misplaced")
+                    if app < 0 or r1 != lv - 1 or i != len(its) - 1:
+                        raise OutOfBounds(f"{self.name}: appended rank of pair {p} misplaced")
                     covered = lv
             if covered != lv:
-                raise OutOfBounds(f"{self.name}: pair {pair} covers {covered} of {lv} ranks")
+                raise OutOfBounds(f"{self.name}: pair {p} covers {covered} of {lv} ranks")
             if app >= 0:  # the appended rank's page: the one holding the append row
                 table[b, h, (lv - 1) // 16] = app // 16
-            live[b, h], slot[b, h], pos[b] = lv, app, p
-        self._plan_keep = (live, slot, pos, table)
+            live[b, h], slot[b, h] = lv, app
+        self._plan_keep = (live, slot, table)
         return self.fused_decode_attention_paged(q, qs_b, qs_h, k, ks_b, ks_h, v, vs_b, vs_h, cos_sin, cs_p, cs_d,
-                                                 pos.data_ptr(), slot.data_ptr(), H, 1, ev_out, ev_b, ev_h, a_s, a_o,
+                                                 positions, slot.data_ptr(), H, 1, ev_out, ev_b, ev_h, a_s, a_o,
                                                  thr, pos_scale, ck, cv, c_s, table.data_ptr(), H * maxp, maxp, 16,
                                                  live.data_ptr(), H, 1, out, os_b, os_h, ws, counters, B, H, G, D,
                                                  splits, 0, scale, k_scale, v_scale, q_norm, k_norm, eps, stream)
@@ -1320,6 +1331,9 @@ def cpu_engine():
     patch(lin, "_num_cus", lambda device: 256)
     orig_build = mr.build_synthetic_model
     patch(mr, "build_synthetic_model", lambda cfg, **k: orig_build(cfg, **{**k, "device": "cpu"}))
+    # prefill FP8 GEMMs on this library's kernel (emulated): hipBLASLt's scaled
+    # GEMM is a GPU library call, covered by the GPU tests
+    patch(lin, "fp8_gemm_impl", lambda: "fdms")
     try:
         yield emu
     finally:

@@ -490,23 +490,26 @@ def test_fp8_rows_gemm_prefill_rows(m, n, k):
     _close_bf16(y, want, "fp8 rows gemm", ulps=2.0, atol=1e-3, mag=pre)
 
 
+@pytest.mark.parametrize("impl", ["fdms", "hipblaslt"])
 @pytest.mark.parametrize("m,n,k,bias", [(1000, 3072, 2048, False), (300, 202, 272, True), (129, 130, 160, True),
                                          (17, 4096, 1024, False), (4096, 4096, 1024, False),
-                                         (4100, 4098, 272, True)])
-def test_fp8_gemm_matches_the_oracle(m, n, k, bias):
-    """fdms_fp8_gemm on the FP8 matrix cores (the _scaled_mm of _fp8_linear,
-    linear.py:635-662) at prefill row counts: full and partial 128 x 128 tiles
-    and, from 256 tiles of 256 x 256 up, the LDS-staged kernel (full and
-    partial tiles); a K tail (272 = 2 * 128 + 16), N not a multiple of 4
-    (per-element stores), bias or none; within 2 bf16 ulps of the oracle
-    (fp32 accumulation in a different order)."""
+                                         (4100, 4098, 272, True), (1024, 2048, 8192, True)])
+def test_fp8_gemm_matches_the_oracle(m, n, k, bias, impl):
+    """The prefill FP8 GEMM (the _scaled_mm of _fp8_linear, linear.py:635-662)
+    at prefill row counts, both implementations: fdms_fp8_gemm on the FP8
+    matrix cores -- full and partial 128 x 128 tiles and, from 256 tiles of
+    256 x 256 up, the LDS-staged kernel (full and partial tiles); a K tail
+    (272 = 2 * 128 + 16), N not a multiple of 4 (per-element stores) -- and
+    hipBLASLt's scaled GEMM (shapes it does not take run fdms_fp8_gemm); bias
+    or none; within 2 bf16 ulps of the oracle (fp32 accumulation in a
+    different order)."""
     require_gpu()
     from fastdms_amd.layers.linear import fp8_gemm, quantize_fp8_rows
     g = torch.Generator().manual_seed(m * 7 + n + k)
     x, w = _bf16((m, k), g), _bf16((n, k), g, 0.02)
     b = _bf16((n,), g, 0.1) if bias else None
     w8, sinv = quantize_fp8_rows(w.cuda())
-    y = fp8_gemm(x.cuda(), w8, sinv.reshape(1, -1), None if b is None else b.cuda())
+    y = fp8_gemm(x.cuda(), w8, sinv.reshape(1, -1), None if b is None else b.cuda(), impl=impl)
     w8_t, sref = olin.quantize_weight_to_fp8(w.float().numpy())
     acc = olin.fp8_linear(x.float().numpy(), w8_t, sref, quantize_x=True, torch_form=True)
     pre = torch.from_numpy(numerics.bf16_round(acc.astype(np.float32)))

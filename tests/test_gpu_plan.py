@@ -6,13 +6,14 @@ the reference partitions inside its split-K kernels, compact_attention.py:
   paged_prepare_decode_plan, tests/native_emulator.py) on random paged
   states, including spans whose pages are full (a page pop per append) and a
   pool too short for every pop: live counts, append rows, block tables, pages
-  held, stack top, overflow flag, item counts and every item, bit for bit.
+  held, stack top, overflow flag and every item slot, bit for bit.
 * fdms_fused_decode_attention_planned on that plan against the unplanned
   launch (fdms_fused_decode_attention_paged) on the same state: DMS decisions
-  and appended FP8 rows bit for bit, outputs within a bf16 rounding (the
-  splits' rank ranges, and so the fp32 summation order, differ), and both
-  against the oracle's attention over the spans gathered through the tables
-  (2e-2 max-abs-relative).
+  and appended FP8 rows bit for bit, outputs bit for bit at head_dim 64 (the
+  same partition) and within a bf16 rounding at head_dim 128 (the plan
+  splits pairs into 512-rank pieces there, so the fp32 summation order
+  differs), and both against the oracle's attention over the spans gathered
+  through the tables (2e-2 max-abs-relative).
 """
 from __future__ import annotations
 
@@ -53,47 +54,46 @@ def _state(rng, L, B, H, max_live, spare_pages, full_every=5):
     return live, held.astype(np.int32), bt, stack, top, pool, max_pages
 
 
-def _run_plan(call, t, L, B, H, max_pages, max_items):
+def _run_plan(call, t, L, B, H, max_pages, part):
+    rows, heavy, splits = part
     call("fdms_paged_prepare_decode_plan", t["live"].data_ptr(), *t["live"].stride(), t["slot"].data_ptr(),
          *t["slot"].stride(), t["bt"].data_ptr(), *t["bt"].stride()[:3], t["held"].data_ptr(), *t["held"].stride(),
          t["stack"].data_ptr(), t["stack"].stride(0), t["top"].data_ptr(), max_pages, t["overflow"].data_ptr(),
-         t["pos"].data_ptr(), t["plan"].data_ptr(), t["plan"].stride(0), t["count"].data_ptr(), max_items, L, B, H,
-         0)
+         t["pos"].data_ptr(), t["plan"].data_ptr(), t["plan"].stride(0), rows, heavy, splits, L, B, H, 0)
 
 
-def _tensors(live, held, bt, stack, top, pos, L, B, H, max_items, device):
+def _tensors(live, held, bt, stack, top, pos, L, B, H, items, device):
     mk = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
     return dict(live=mk(live), held=mk(held), bt=mk(bt), stack=mk(stack), top=mk(top), pos=mk(pos),
                 slot=torch.full((L, B, H), -7, dtype=torch.int32, device=device),
                 overflow=torch.zeros(1, dtype=torch.int32, device=device),
-                plan=torch.full((L, max_items, 40), -9, dtype=torch.int32, device=device),
-                count=torch.zeros(L, dtype=torch.int32, device=device))
+                plan=torch.full((L, 4 + items * 72), -9, dtype=torch.int32, device=device))
 
 
-@pytest.mark.parametrize("L,B,H,max_live,spare,seed", [(3, 8, 8, 2900, 64, 0), (2, 3, 8, 600, 40, 1),
-                                                       (2, 40, 8, 1500, 500, 2), (2, 8, 8, 1200, 3, 3),
-                                                       (1, 1, 2, 40, 8, 4)])
-def test_plan_kernel_equals_its_restatement(L, B, H, max_live, spare, seed):
+@pytest.mark.parametrize("L,B,H,max_live,spare,seed,part", [
+    (3, 8, 8, 2900, 64, 0, (1024, 512)), (2, 3, 8, 600, 40, 1, (1024, 512)), (2, 40, 8, 1500, 500, 2, (1024, 1024)),
+    (2, 8, 8, 1200, 3, 3, (512, 512)), (1, 1, 2, 40, 8, 4, (1024, 512)), (2, 8, 8, 3000, 64, 5, (256, 128))])
+def test_plan_kernel_equals_its_restatement(L, B, H, max_live, spare, seed, part):
     require_gpu()
     from fastdms_amd import _native as nat
     from native_emulator import Emulator
     rng = np.random.default_rng(seed)
     live, held, bt, stack, top, pool, max_pages = _state(rng, L, B, H, max_live, spare)
     pos = rng.integers(max_live, 8000, B).astype(np.int64)
-    max_items = B * H * (-(-(max_live + 1) // 512))
-    dev = _tensors(live, held, bt, stack, top, pos, L, B, H, max_items, "cuda")
-    _run_plan(lambda name, *a: nat.call(name, *a[:-1], nat.stream()), dev, L, B, H, max_pages, max_items)
+    splits = min(64, -(-(max_live + 1) // part[1]))
+    items = splits * B * H
+    dev = _tensors(live, held, bt, stack, top, pos, L, B, H, items, "cuda")
+    _run_plan(lambda name, *a: nat.call(name, *a[:-1], nat.stream()), dev, L, B, H, max_pages, (*part, splits))
     torch.cuda.synchronize()
-    cpu = _tensors(live, held, bt, stack, top, pos, L, B, H, max_items, "cpu")
+    cpu = _tensors(live, held, bt, stack, top, pos, L, B, H, items, "cpu")
     emu = Emulator()
-    _run_plan(lambda name, *a: emu(name, *a), cpu, L, B, H, max_pages, max_items)
-    for key in ("live", "slot", "bt", "held", "top", "overflow", "count"):
+    _run_plan(lambda name, *a: emu(name, *a), cpu, L, B, H, max_pages, (*part, splits))
+    for key in ("live", "slot", "bt", "held", "top", "overflow", "plan"):
         assert torch.equal(dev[key].cpu(), cpu[key]), key
-    for l in range(L):
-        n = int(cpu["count"][l])
-        assert torch.equal(dev["plan"][l, :n].cpu(), cpu["plan"][l, :n]), f"layer {l} items"
     short = int(dev["overflow"].item())
-    print(f"L{L} B{B} H{H}: items per layer {cpu['count'].tolist()}, overflow {short}, pool {pool}", flush=True)
+    further = cpu["plan"][:, 3].tolist()
+    print(f"L{L} B{B} H{H} part {part}: {B * H} first + {further} further splits per layer (grid {items}), "
+          f"overflow {short}, pool {pool}", flush=True)
     if spare == 3:
         assert short == 1, "the short pool case must run out of pages"
 
@@ -110,10 +110,11 @@ def test_planned_attention_equals_the_unplanned_launch(d, qk_norm, scales):
     max_live = 2900
     live, held, bt, stack, top, pool, max_pages = _state(rng, L, B, H, max_live, 64)
     pos = rng.integers(max_live, 8000, B).astype(np.int64)
-    plan = ca.DecodePlan("cuda", L, B * H, max_live + 1)
-    dev = _tensors(live, held, bt, stack, top, pos, L, B, H, plan.max_items, "cuda")
-    dev["plan"], dev["count"] = plan.items, plan.count
-    _run_plan(lambda name, *a: nat.call(name, *a[:-1], nat.stream()), dev, L, B, H, max_pages, plan.max_items)
+    plan = ca.DecodePlan("cuda", L, B * H, max_live + 1, d)
+    dev = _tensors(live, held, bt, stack, top, pos, L, B, H, (plan.items.shape[1] - 4) // 72, "cuda")
+    dev["plan"] = plan.items
+    _run_plan(lambda name, *a: nat.call(name, *a[:-1], nat.stream()), dev, L, B, H, max_pages,
+              plan.partition(B * H))
     assert int(dev["overflow"].item()) == 0
     rows = pool * PAGE
     ck = torch.from_numpy(numerics.to_storage(rng.standard_normal((rows, d)).astype(np.float32) * 2,
@@ -135,7 +136,7 @@ def test_planned_attention_equals_the_unplanned_launch(d, qk_norm, scales):
         vs = torch.from_numpy((0.5 + rng.random(H)).astype(np.float32)).cuda()
     ck2, cv2 = ck.clone(), cv.clone()
     ev_p = torch.empty((B, H), dtype=torch.bool, device="cuda")
-    out_p = ca.fused_decode_attention_planned(q, k, v, cache, ck, cv, ev_p, plan, 0, num_kv_heads=H,
+    out_p = ca.fused_decode_attention_planned(q, k, v, cache, ck, cv, ev_p, dev["pos"], plan, 0, num_kv_heads=H,
                                               alpha_scale=10.0, alpha_offset=5.0, k_scale=ks, v_scale=vs, **norms)
     ev_u = torch.empty((B, H), dtype=torch.bool, device="cuda")
     out_u = ca.fused_dms_rope_store_compact_decode_attention(
@@ -148,6 +149,8 @@ def test_planned_attention_equals_the_unplanned_launch(d, qk_norm, scales):
                                                                                       cv2.view(torch.uint8))
     a, u = out_p.float().cpu().numpy(), out_u.float().cpu().numpy()
     rel = float(np.abs(a - u).max() / np.abs(u).max())
+    if d == 64:  # the same partition: the same bits
+        assert torch.equal(out_p.view(torch.int16), out_u.view(torch.int16)), f"planned vs unplanned {rel:.3e}"
     assert rel <= 8e-3, f"planned vs unplanned max-abs-rel {rel:.3e}"
     # both against the oracle over the spans gathered through the tables
     lv = dev["live"][0].cpu().numpy()
@@ -179,5 +182,5 @@ def test_planned_attention_equals_the_unplanned_launch(d, qk_norm, scales):
     for name, o in (("planned", a), ("unplanned", u)):
         err = float(np.abs(o - ref).max() / np.abs(ref).max())
         assert err <= 2e-2, f"{name} vs oracle {err:.3e}"
-    print(f"d={d} qk_norm={qk_norm} scales={scales}: planned vs unplanned {rel:.2e}, items {int(plan.count[0])}",
-          flush=True)
+    print(f"d={d} qk_norm={qk_norm} scales={scales}: planned vs unplanned {rel:.2e}, partition "
+          f"{plan.partition(B * H)}", flush=True)
