@@ -57,7 +57,10 @@ class LLMEngine:
                     seqs = seqs[:1]
                     continue
                 if not any(s is not seqs[0] for s in self.scheduler.running):
-                    raise  # nothing runs that could free space: the request never fits
+                    # nothing runs that could free space: the request never fits
+                    raise CompactCapacityExhausted(
+                        f"request {seqs[0].seq_id} ({len(seqs[0])} tokens) does not fit the compact KV capacity "
+                        f"({self.config.compact_kv_capacity_tokens} tokens per layer) on its own")
                 self.scheduler.defer_prefill(seqs)
                 return None, None
 

@@ -100,7 +100,7 @@ def test_a_request_that_can_never_fit_raises():
         llm = LLM("tiny-llama", max_model_len=1024, max_num_seqs=2, max_num_batched_tokens=4096,
                   enforce_eager=True, compact_kv_capacity_tokens=40, compact_admission="preempt", **DMS)
         llm.add_request(list(range(300)), SamplingParams(temperature=0.0, max_tokens=8, ignore_eos=True))
-        with pytest.raises(CompactCapacityExhausted):
+        with pytest.raises(CompactCapacityExhausted, match=r"\(300 tokens\) does not fit .*\(40 tokens per layer\)"):
             llm.step()
 
 

@@ -500,7 +500,8 @@ def test_fp8_gemm_matches_the_oracle(m, n, k, bias, impl):
     matrix cores -- full and partial 128 x 128 tiles and, from 256 tiles of
     256 x 256 up, the LDS-staged kernel (full and partial tiles); a K tail
     (272 = 2 * 128 + 16), N not a multiple of 4 (per-element stores) -- and
-    hipBLASLt's scaled GEMM (shapes it does not take run fdms_fp8_gemm); bias
+    hipBLASLt's scaled GEMM (row counts padded to 16; N or K off 16 run
+    fdms_fp8_gemm); bias
     or none; within 2 bf16 ulps of the oracle (fp32 accumulation in a
     different order)."""
     require_gpu()
