@@ -14,6 +14,10 @@
 //            f = fp32(x) + fp32(residual) (residual optional), residual_out =
 //            bf16(f) (written by workgroup 0), a = bf16(bf16(f * rsqrt(mean(f^2)
 //            + eps)) * norm_w) -- the normalised value is the unrounded sum.
+//   PRO = 2: the same RMSNorm on rows that an EPI 4 producer finished: x holds
+//            f itself (fp32 rows) and x_amax the producer strips' sums of f^2
+//            ([M, strips]); rsqrt(sum / K + eps) is taken from those, so a
+//            workgroup reads only its own K range of f (no pass over the row).
 // and the output may go through a fused epilogue:
 //   EPI = 1: the weight holds [gate; up] (n = 2 * n_out rows, gate_up_proj) and
 //            the output is bf16(silu(bf16 gate) * bf16 up) (activation.py:8-11).
@@ -21,6 +25,12 @@
 //            workspace[split][m][n]; the consumer adds them in split order and
 //            applies the row scale 1/x_s[m] and the FP8 column scale (the merge
 //            and scaling of EPI 0, moved into the next kernel).
+//   EPI = 4: the residual add of the RMSNorm that follows (layernorm.py:32-40):
+//            with v = the finalised bf16 output, y receives f = fp32(v) +
+//            fp32(residual) as fp32 rows, residual_out = bf16(f) (it may be
+//            the residual itself: each element is read, then written, by one
+//            lane), and amax_out[m][strip] = the strip's sum of f^2 -- what a
+//            PRO 2 consumer needs to apply the norm.
 // The activation's per-row amax may come from its producer (x_amax: the
 // RMSNorm's output amax, or the per-strip output amax that EPI 0 / 1 writes to
 // amax_out) instead of a statistics pass over x.
@@ -240,7 +250,7 @@ template <typename WT, int PRO, bool QX, int EPI, int NW, int U, bool XQ = false
 __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     const bf16_t* __restrict__ x, int64_t x_s, int M, int K, const WT* __restrict__ w, int64_t w_s,
     const float* __restrict__ w_scale_inv, const bf16_t* __restrict__ bias, const bf16_t* __restrict__ norm_w,
-    float eps, const bf16_t* __restrict__ res, int64_t res_s, bf16_t* __restrict__ res_out, int64_t ro_s,
+    float eps, const bf16_t* res, int64_t res_s, bf16_t* res_out, int64_t ro_s,
     bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
     int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx,
     const bf16_t* __restrict__ g_scale, const bf16_t* __restrict__ g_zero, int group, int64_t g_s, int qx_torch,
@@ -286,11 +296,28 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   const bf16_t* xrow = x + (int64_t)(has_row ? c : 0) * x_s;
   const uint8_t* xqrow = reinterpret_cast<const uint8_t*>(x) + (int64_t)(has_row ? c : 0) * x_s;  // XQ
   const bf16_t* rrow = (PRO == 1 && res) ? res + (int64_t)(has_row ? c : 0) * res_s : nullptr;
+  const float* frow0 = reinterpret_cast<const float*>(x);  // PRO 2: the fp32 rows
   float inv = 1.0f, xsc = 1.0f;  // row statistics, read after the stats pass below
   bool xfin = true;               // F8: x * xsc of this lane's row is finite and in range
   f32x4 acc[NA];
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // PRO 2 stages each group's activation through this wave's slice of LDS:
+  // the group's fp32 rows arrive as contiguous 16-byte chunks (lane l takes
+  // columns 4 (l % kCq) .. + 3 of rows l / kCq, + kRq, ...), are normalised
+  // once and stored as bf16, and the k-blocks read their B operands back
+  // (rows padded by 16 bytes: the 16 rows of a lane group fall in distinct
+  // banks).  Each wave reads only its own slice, so no workgroup barrier.
+  constexpr int G = U * KB;                  // columns per group
+  constexpr int kCq = G / 4;                 // 16-byte fp32 chunks per row and group
+  constexpr int kRq = kCq >= 64 ? 1 : 64 / kCq;  // rows per load instruction
+  constexpr int kActRows = kMaxM;
+  constexpr int kFChunks = (kActRows + kRq - 1) / kRq;
+  constexpr int kActStride = G + 8;          // bf16 per LDS row
+  __shared__ __attribute__((aligned(16))) uint16_t s_act[PRO == 2 ? NW : 1][PRO == 2 ? kActRows : 1][PRO == 2 ? kActStride : 8];
+  const int fq_row = lane / kCq, fq_col = 4 * (lane % kCq);
+  float fq_inv[kFChunks];  // PRO 2: inv of rows fq_row + kRq * t (set after the statistics)
 
   struct Buf {
     typename WBlock<WT>::Raw w[NA][U];
@@ -298,6 +325,8 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     uint4 x[U][2];
     uint4 r[U][2];   // residual (PRO 1)
     uint4 nw[U][2];  // norm weight (PRO 1)
+    uint4 fch[kFChunks];  // PRO 2: the group's fp32 rows, this lane's chunks
+    uint2 fnw;            // PRO 2: norm weight of this lane's four columns
     uint4 w8[NA][U][2];  // F8: 32 weight bytes per lane per k-block
     uint4 x8[U][4];      // F8: 32 bf16 activations per lane per k-block
   };
@@ -338,6 +367,15 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       }
       return;
     }
+    if constexpr (PRO == 2) {
+      // chunks of rows < M only (uniform per t: rows fq_row + kRq t, clamped)
+      const int col = min(kb0 + fq_col, kend - 4);
+#pragma unroll
+      for (int t = 0; t < kFChunks; ++t)
+        if (kRq * t < M)
+          b.fch[t] = *reinterpret_cast<const uint4*>(frow0 + (int64_t)min(fq_row + kRq * t, M - 1) * x_s + col);
+      b.fnw = *reinterpret_cast<const uint2*>(norm_w + col);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = kb0 + u * kKB + 16 * g;
@@ -352,7 +390,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
           }
         }
         b.x[u][0] = b.x[u][1] = b.r[u][0] = b.r[u][1] = uint4{0u, 0u, 0u, 0u};
-        if (has_row) {
+        if (PRO != 2 && has_row) {
           const uint4* xp = reinterpret_cast<const uint4*>(xrow + k);
           b.x[u][0] = xp[0];
           b.x[u][1] = xp[1];
@@ -424,6 +462,24 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       }
       return;
     }
+    if constexpr (PRO == 2) {
+      // a = bf16(bf16(f * inv) * norm_w) of the group's rows into this wave's
+      // LDS slice (the previous group's reads are done: LDS runs a wave's
+      // instructions in order)
+      const float nwf[4] = {bf_lo(b.fnw.x), bf_hi(b.fnw.x), bf_lo(b.fnw.y), bf_hi(b.fnw.y)};
+#pragma unroll
+      for (int t = 0; t < kFChunks; ++t) {
+        const int row = fq_row + kRq * t;
+        if (kRq * t < M && row < M) {
+          const uint4 v = b.fch[t];
+          const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+          const float iv = fq_inv[t];
+          *reinterpret_cast<uint2*>(&s_act[wave][row][fq_col]) =
+              uint2{pack2(rbf(rbf(f[0] * iv) * nwf[0]), rbf(rbf(f[1] * iv) * nwf[1])),
+                    pack2(rbf(rbf(f[2] * iv) * nwf[2]), rbf(rbf(f[3] * iv) * nwf[3]))};
+        }
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (kb0 + u * kKB >= kend) break;
@@ -432,6 +488,9 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       for (int h = 0; h < 2; ++h) {
         if (PRO == 0 && !QX) {
           bo[h] = b.x[u][h];
+        } else if (PRO == 2) {
+          bo[h] = has_row ? *reinterpret_cast<const uint4*>(&s_act[wave][c][u * kKB + 16 * g + 8 * h])
+                          : uint4{0u, 0u, 0u, 0u};
         } else {
           const uint32_t v[4] = {b.x[u][h].x, b.x[u][h].y, b.x[u][h].z, b.x[u][h].w};
           const uint32_t q[4] = {b.nw[u][h].x, b.nw[u][h].y, b.nw[u][h].z, b.nw[u][h].w};
@@ -509,10 +568,23 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   }
 
+  // PRO 2: the producer's strip sums go out first (loads complete in issue
+  // order, so the reduction below waits for these alone), at most
+  // kStatLoads per lane and row, the rest read after
+  constexpr int kStatLoads = 4;
+  float sv[kRowsPerWave][kStatLoads];
+  if constexpr (PRO == 2) {
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const float* sp = x_amax + (int64_t)min(wave + rr * NW, M - 1) * x_amax_s;
+#pragma unroll
+      for (int j = 0; j < kStatLoads; ++j) sv[rr][j] = sp[min(lane + 64 * j, x_amax_n - 1)];  // masked below
+    }
+  }
+
   // with statistics to wait for, both first groups go out before them;
   // otherwise the loop below issues group 1 right after group 0
-  constexpr bool kEarly2 = PRO == 0 && QX;
-  constexpr int G = U * KB;  // columns per group
+  constexpr bool kEarly2 = (PRO == 0 && QX) || PRO == 2;
   Buf b0, b1;                // even / odd groups (no register copies between them)
   if (kw0 < kend) load(kw0, b0);
   if (kEarly2 && kw0 + G < kend) load(kw0 + G, b1);
@@ -576,6 +648,21 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       s_xs[tid] = x_scale(__uint_as_float(a));
     }
     __syncthreads();
+  } else if (PRO == 2) {
+    // the row's sum of f^2 from the producer's strips (x_amax [M, strips]),
+    // each lane summing strips lane, lane + 64, ..., then the wave
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int mm = wave + rr * NW;
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kStatLoads; ++j) ss += (lane + 64 * j < x_amax_n) ? sv[rr][j] : 0.0f;
+      const float* sp = x_amax + (int64_t)min(mm, M - 1) * x_amax_s;
+      for (int s2 = lane + 64 * kStatLoads; s2 < x_amax_n; s2 += 64) ss += sp[s2];
+      ss = wave_sum(ss);
+      if (lane == 0 && mm < M) s_inv[mm] = rsqrtf(ss / (float)K + eps);  // torch.rsqrt (layernorm.py:38)
+    }
+    __syncthreads();
   } else if (PRO == 1 || QX) {
     for (int m = wave; m < M; m += NW) {
       float inv, xs;
@@ -590,6 +677,10 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   }
 
   if (PRO == 1 && has_row) inv = s_inv[c];
+  if constexpr (PRO == 2) {
+#pragma unroll
+    for (int t = 0; t < kFChunks; ++t) fq_inv[t] = s_inv[min(fq_row + kRq * t, kActRows - 1)];
+  }
   if (QX && has_row && !amax_one) {
     xsc = s_xs[c];
     if constexpr (F8) xfin = fp8_row_finite(s_amax[c], xsc);
@@ -606,6 +697,12 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   }
 
+  // EPI 4: the residual of this lane's four columns, loaded before the
+  // reduction and the split handoff (only the finishing workgroup uses it)
+  // (rows clamped in bounds instead of a load under a lane-dependent branch)
+  uint2 rv4 = uint2{0u, 0u};
+  if (EPI == 4 && wave == 0)
+    rv4 = *reinterpret_cast<const uint2*>(res + (int64_t)min(lane & 15, M - 1) * res_s + n0 + 4 * (lane >> 4));
   // ---- reduce the waves' C fragments; lane l holds C[n = 4*(l/16) + r][m = l%16]
 #pragma unroll
   for (int a = 0; a < NA; ++a) s_acc[a][wave][lane] = acc[a];
@@ -736,6 +833,29 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
     return v;
   };
+  if (EPI == 4) {
+    // f = fp32(v) + fp32(residual): fp32 rows to y, bf16(f) to residual_out,
+    // the strip's sum of f^2 per row to amax_out[m][strip].  Lane l holds
+    // columns 4 (l / 16) .. + 3 of row l % 16: the sum runs over those four,
+    // then over lanes l ^ 16 and l ^ 32
+    const int nc = n0 + 4 * (lane >> 4);
+    float f[4];
+    const float rf[4] = {bf_lo(rv4.x), bf_hi(rv4.x), bf_lo(rv4.y), bf_hi(rv4.y)};
+    float ss = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      f[r] = finalize(t[0][r], nc + r) + rf[r];
+      ss += f[r] * f[r];
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (row_ok) {
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + (int64_t)m * y_s + nc) = f32x4{f[0], f[1], f[2], f[3]};
+      *reinterpret_cast<uint2*>(res_out + (int64_t)m * ro_s + nc) = uint2{pack2(f[0], f[1]), pack2(f[2], f[3])};
+      if (lane < 16) amax_out[(int64_t)m * strips + strip] = ss;
+    }
+    return;
+  }
   uint32_t vmax = 0;  // the row's max |output| over this strip, as abs_bits (rows >= M hold x = 0)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -779,7 +899,7 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   // k-blocks per double-buffered group (register budget: the RMSNorm prologue
   // also holds the residual and norm weight of each k-block, the activation
   // statistics hold their loads while both first groups are in flight)
-  constexpr int U = (PRO == 1 || (QX && PRO == 0)) ? 2 : 4;
+  constexpr int U = (PRO == 1 || PRO == 2 || (QX && PRO == 0)) ? 2 : 4;
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
                       a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
                       a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores, a.x_amax, a.x_amax_n, \
@@ -818,26 +938,37 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
                                     int k_splits, float* workspace, int* counters, void* y, int64_t y_stride,
                                     const float* x_amax, int x_amax_n, int64_t x_amax_stride, float* amax_out,
                                     float* row_scale_out, int x_dtype, void* stream) {
-  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 1 || epilogue < 0 ||
-      (epilogue > 1 && epilogue != 3) || quantize_x < 0 || quantize_x > 2)
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || prologue < 0 || prologue > 2 || epilogue < 0 || epilogue > 4 ||
+      epilogue == 2 || quantize_x < 0 || quantize_x > 2)
     return (int)hipErrorInvalidValue;
   if (epilogue == 3 && (prologue != 0 || bias || !workspace)) return (int)hipErrorInvalidValue;
-  // the producer's row amax replaces the activation statistics pass (no prologue)
-  if (x_amax && (prologue != 0 || quantize_x == 0 || x_amax_n < 1 || (m > 1 && x_amax_stride < x_amax_n)))
+  // prologue 2: fp32 rows f and their producer's per-strip sums of f^2 in x_amax
+  const bool stats_in = prologue == 2;
+  if (stats_in && (x_dtype != kF32 || quantize_x != 0 || !x_amax || x_amax_n < 1 ||
+                   (m > 1 && x_amax_stride < x_amax_n) || epilogue > 1))
     return (int)hipErrorInvalidValue;
-  if ((amax_out && epilogue > 1) || (row_scale_out && epilogue != 3)) return (int)hipErrorInvalidValue;
+  // the producer's row amax replaces the activation statistics pass (no prologue)
+  if (x_amax && !stats_in && (prologue != 0 || quantize_x == 0 || x_amax_n < 1 || (m > 1 && x_amax_stride < x_amax_n)))
+    return (int)hipErrorInvalidValue;
+  // epilogue 4: the residual add (residual in, residual_out may be the same
+  // rows), fp32 rows to y, the strips' sums of squares to amax_out
+  const bool stats_out = epilogue == 4;
+  if (stats_out && (prologue != 0 || quantize_x != 0 || !residual || !residual_out || !amax_out))
+    return (int)hipErrorInvalidValue;
+  if ((amax_out && epilogue > 1 && !stats_out) || (row_scale_out && epilogue != 3)) return (int)hipErrorInvalidValue;
   // an activation quantised by its producer: e4m3fn codes with their row amax
   const bool xq = x_dtype == kFP8;
-  if ((x_dtype != kBF16 && !xq) || (xq && (w_dtype != kFP8 || quantize_x == 0 || !x_amax)))
+  if ((x_dtype != kBF16 && !xq && !stats_in) || (xq && (w_dtype != kFP8 || quantize_x == 0 || !x_amax)))
     return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
-  if (!x || !w || !y || (prologue == 1 && !norm_weight)) return (int)hipErrorInvalidValue;
+  if (!x || !w || !y || (prologue >= 1 && !norm_weight)) return (int)hipErrorInvalidValue;
   if (w_dtype != kBF16 && w_dtype != kFP8) return (int)hipErrorInvalidValue;
   if (w_dtype == kFP8 && !w_scale_inv) return (int)hipErrorInvalidValue;
-  if (prologue != 1 && (residual || residual_out)) return (int)hipErrorInvalidValue;
+  if (prologue != 1 && !stats_out && (residual || residual_out)) return (int)hipErrorInvalidValue;
   // other workgroups still read x / residual while workgroup 0 writes residual_out
-  if (residual_out && (residual_out == residual || residual_out == x)) return (int)hipErrorInvalidValue;
-  if (y == x || (residual && y == residual)) return (int)hipErrorInvalidValue;
+  if (prologue == 1 && residual_out && (residual_out == residual || residual_out == x)) return (int)hipErrorInvalidValue;
+  if (stats_out && (residual_out == x || residual == x)) return (int)hipErrorInvalidValue;
+  if (y == x || (residual && y == residual) || (residual_out && y == residual_out)) return (int)hipErrorInvalidValue;
   // n = weight rows; epilogue 1 pairs row n0 with n0 + n/2 and writes n/2 columns
   const int n_out = epilogue == 1 ? n / 2 : n;
   if (n_out % 16 || (epilogue == 1 && n % 2)) return (int)hipErrorInvalidValue;
@@ -855,12 +986,18 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;  // whole k-blocks per wave
   const int wsz = w_dtype == kFP8 ? 1 : 2;
   auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
-  if (!al16(x) || !al16(w) || (x_stride * (xq ? 1 : 2)) % 16 || (w_stride * wsz) % 16) return (int)hipErrorInvalidValue;
+  if (!al16(x) || !al16(w) || (x_stride * (xq ? 1 : stats_in ? 4 : 2)) % 16 || (w_stride * wsz) % 16)
+    return (int)hipErrorInvalidValue;
+  if (stats_in && !al16(norm_weight)) return (int)hipErrorInvalidValue;
+  if (stats_out && (!al16(y) || y_stride % 4 || (uintptr_t)residual % 8 || (uintptr_t)residual_out % 8 ||
+                    res_stride % 4 || res_out_stride % 4 || res_stride < n || res_out_stride < n))
+    return (int)hipErrorInvalidValue;
   if (prologue == 1 && (!al16(norm_weight) || (residual && (!al16(residual) || (res_stride * 2) % 16)) ||
                         (residual_out && (!al16(residual_out) || (res_out_stride * 2) % 16))))
     return (int)hipErrorInvalidValue;
   if (x_stride < k || w_stride < k || y_stride < n_out) return (int)hipErrorInvalidValue;
-  if ((residual && res_stride < k) || (residual_out && res_out_stride < k)) return (int)hipErrorInvalidValue;
+  if (!stats_out && ((residual && res_stride < k) || (residual_out && res_out_stride < k)))
+    return (int)hipErrorInvalidValue;
   const int strips = n_out / 16;
   const int64_t blocks = (int64_t)((strips + kXcds - 1) / kXcds) * kXcds * k_splits;
   if (blocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
@@ -875,7 +1012,18 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   a.x_amax_s = x_amax_stride;
   a.amax_out = amax_out;
   a.row_scale_out = row_scale_out;
-  if (xq) {
+  if (stats_in) {
+    if (w_dtype == kFP8) {
+      if (epilogue == 1) launch_linear<fp8_t, 2, false, 1>(nw, grid, (hipStream_t)stream, a);
+      else launch_linear<fp8_t, 2, false, 0>(nw, grid, (hipStream_t)stream, a);
+    } else {
+      if (epilogue == 1) launch_linear<bf16_t, 2, false, 1>(nw, grid, (hipStream_t)stream, a);
+      else launch_linear<bf16_t, 2, false, 0>(nw, grid, (hipStream_t)stream, a);
+    }
+  } else if (stats_out) {
+    if (w_dtype == kFP8) launch_linear<fp8_t, 0, false, 4>(nw, grid, (hipStream_t)stream, a);
+    else launch_linear<bf16_t, 0, false, 4>(nw, grid, (hipStream_t)stream, a);
+  } else if (xq) {
     if (epilogue == 3) launch_linear<fp8_t, 0, true, 3, true>(nw, grid, (hipStream_t)stream, a);
     else if (epilogue == 1) launch_linear<fp8_t, 0, true, 1, true>(nw, grid, (hipStream_t)stream, a);
     else launch_linear<fp8_t, 0, true, 0, true>(nw, grid, (hipStream_t)stream, a);

@@ -20,8 +20,8 @@ from torch import nn
 from .. import _native as nat
 from . import quant_env as qe
 
-PRO_NONE, PRO_RMSNORM = 0, 1
-EPI_NONE, EPI_SILU_MUL, EPI_PARTIALS = 0, 1, 3
+PRO_NONE, PRO_RMSNORM, PRO_NORM_STATS = 0, 1, 2
+EPI_NONE, EPI_SILU_MUL, EPI_PARTIALS, EPI_RESIDUAL_STATS = 0, 1, 3, 4
 QX_NONE, QX_DIVIDE, QX_TORCH = 0, 1, 2   # activation quantisation: none / 448/amax / reciprocal(amax)*448
 SMALL_M_MAX_ROWS = 16
 _MAX_K_SPLITS = 8
@@ -158,6 +158,92 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None 
              None, 0, None, 0, qx if fp8 else QX_NONE, EPI_PARTIALS, int(k_splits), part.data_ptr(), None,
              part.data_ptr(), n, am_ptr or None, am_n, am_s, None, nat.ptr(row_scale), nat.DT_BF16, nat.stream())
     return SplitPartials(part, row_scale, sinv)
+
+
+def linear_residual_stats(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, f_out: torch.Tensor,
+                          ssq_out: torch.Tensor, *, weight_scale_inv: torch.Tensor | None = None,
+                          k_splits: int | None = None) -> None:
+    """A decode linear finished as the residual add of the RMSNorm that follows
+    it (fdms_linear_small_m epilogue 4; layernorm.py:32-40): with v = bf16(x @
+    W^T), f_out = fp32(v) + fp32(residual) ([rows, N] fp32), residual becomes
+    bf16(f) in place, and ssq_out[rows, N / 16] holds each 16-column strip's
+    sum of f^2 -- the statistic linear_norm_stats applies the norm from.  bf16
+    activations (no quantisation), no bias."""
+    n, k = weight.shape
+    rows = x.shape[0]
+    fp8 = weight.dtype == torch.float8_e4m3fn
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.shape[1] != k:
+        raise ValueError("linear_residual_stats expects bf16 activations [rows, K] with a contiguous last axis")
+    if (weight.dtype != torch.bfloat16 and not fp8) or (fp8 and weight_scale_inv is None):
+        raise ValueError("linear_residual_stats expects bf16 weights, or FP8 with weight_scale_inv")
+    if not small_m_supported(rows, k, n):
+        raise ValueError(f"linear_residual_stats does not support rows={rows}, K={k}, N={n}")
+    strips = n // 16
+    if (residual.dtype != torch.bfloat16 or residual.shape != (rows, n) or residual.stride(1) != 1
+            or f_out.dtype != torch.float32 or f_out.shape != (rows, n) or f_out.stride(1) != 1
+            or ssq_out.dtype != torch.float32 or not ssq_out.is_contiguous() or ssq_out.numel() < rows * strips):
+        raise ValueError("linear_residual_stats: residual bf16 [rows, N], f_out fp32 [rows, N], "
+                         "ssq_out contiguous fp32 [rows, N/16]")
+    if k_splits is None:
+        env = os.environ.get("FASTDMS_AMD_RESID_SPLITS", "").strip()  # tuning override
+        if env.isdigit() and 1 <= int(env) <= _MAX_K_SPLITS and k % (int(env) * 256) == 0:
+            k_splits = int(env)
+        else:
+            k_splits = choose_k_splits(x.device, strips, k)
+    ws = counters = None
+    if k_splits > 1:
+        ws, counters = linear_workspace(x.device, strips * k_splits * 256, strips)
+    sinv = None if weight_scale_inv is None else weight_scale_inv.reshape(-1)
+    nat.require_cuda(x, weight, residual, f_out, ssq_out, what="linear_residual_stats")
+    nat.call("fdms_linear_small_m", x.data_ptr(), x.stride(0), rows, k, weight.data_ptr(),
+             nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), None, n, PRO_NONE, None, 0.0,
+             residual.data_ptr(), residual.stride(0), residual.data_ptr(), residual.stride(0), QX_NONE,
+             EPI_RESIDUAL_STATS, int(k_splits), nat.ptr(ws), nat.ptr(counters), f_out.data_ptr(), f_out.stride(0),
+             None, 0, 0, ssq_out.data_ptr(), None, nat.DT_BF16, nat.stream())
+
+
+def linear_norm_stats(f: torch.Tensor, ssq: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+                      weight_scale_inv: torch.Tensor | None = None, epilogue: int = EPI_NONE,
+                      out: torch.Tensor | None = None, k_splits: int | None = None) -> torch.Tensor:
+    """y = RMSNorm(f) @ W^T for the fp32 rows f of a linear_residual_stats
+    producer (fdms_linear_small_m prologue 2): the norm's rsqrt(mean(f^2) +
+    eps) comes from the producer's strip sums ``ssq`` [rows, strips], the
+    normalised activation is bf16(bf16(f * rsqrt) * norm_weight) as the
+    RMSNorm makes it (layernorm.py:32-40).  epilogue EPI_SILU_MUL: W = [gate;
+    up] and the result is SiLU(gate) * up."""
+    n, k = weight.shape
+    rows = f.shape[0]
+    fp8 = weight.dtype == torch.float8_e4m3fn
+    if f.dtype != torch.float32 or f.stride(-1) != 1 or f.shape[1] != k:
+        raise ValueError("linear_norm_stats expects fp32 rows [rows, K] with a contiguous last axis")
+    if ssq.dtype != torch.float32 or ssq.dim() != 2 or ssq.shape[0] < rows or ssq.stride(1) != 1:
+        raise ValueError("ssq must be fp32 [rows, strips] with a contiguous last axis")
+    if (weight.dtype != torch.bfloat16 and not fp8) or (fp8 and weight_scale_inv is None):
+        raise ValueError("linear_norm_stats expects bf16 weights, or FP8 with weight_scale_inv")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != k or not norm_weight.is_contiguous():
+        raise ValueError("norm_weight must be contiguous bf16 [K]")
+    if epilogue not in (EPI_NONE, EPI_SILU_MUL):
+        raise ValueError(f"linear_norm_stats: epilogue {epilogue} is not supported")
+    n_out = n // 2 if epilogue == EPI_SILU_MUL else n
+    if not small_m_supported(rows, k, n_out) or (epilogue == EPI_SILU_MUL and n % 2):
+        raise ValueError(f"linear_norm_stats does not support rows={rows}, K={k}, N={n}")
+    if out is None:
+        out = torch.empty((rows, n_out), device=f.device, dtype=torch.bfloat16)
+    strips = n_out // 16
+    if k_splits is None:
+        k_splits = choose_k_splits(f.device, strips, k)
+    ws = counters = None
+    if k_splits > 1:
+        ws, counters = linear_workspace(f.device, strips * k_splits * 256 * (2 if epilogue else 1), strips)
+    sinv = None if weight_scale_inv is None else weight_scale_inv.reshape(-1)
+    nat.require_cuda(f, ssq, weight, norm_weight, out, what="linear_norm_stats")
+    nat.call("fdms_linear_small_m", f.data_ptr(), f.stride(0), rows, k, weight.data_ptr(),
+             nat.DT_FP8 if fp8 else nat.DT_BF16, weight.stride(0), nat.ptr(sinv), nat.ptr(bias), n, PRO_NORM_STATS,
+             norm_weight.data_ptr(), float(eps), None, 0, None, 0, QX_NONE, int(epilogue), int(k_splits),
+             nat.ptr(ws), nat.ptr(counters), out.data_ptr(), out.stride(0), ssq.data_ptr(), ssq.shape[1],
+             ssq.stride(0), None, None, nat.DT_F32, nat.stream())
+    return out
 
 
 def linear_workspace(device: torch.device, n_floats: int, n_counters: int):

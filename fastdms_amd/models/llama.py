@@ -24,7 +24,8 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
 from ..layers.layernorm import RMSNorm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, LinearBase, MergedColumnParallelLinear, QKVParallelLinear,
-                             RowParallelLinear, linear_partials, small_m_supported)
+                             RowParallelLinear, linear_norm_stats, linear_partials, linear_residual_stats,
+                             small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -110,6 +111,21 @@ def _linear_from_norm(lin: LinearBase, h: torch.Tensor, am: torch.Tensor | None,
 
 def _defer_splitk_enabled() -> bool:
     return os.environ.get("FASTDMS_AMD_DEFER_SPLITK", "1").strip() != "0"
+
+
+def _norm_stats_enabled(hidden_size: int) -> bool:
+    """RMSNorms split between the linears around them on the bf16 decode path
+    (LlamaModel._forward_decode_norm_stats).  Default: at hidden sizes from
+    4096 (measured on MI355X, Qwen3-8B shape c=8: 1 927 against 1 850 decode
+    tok/s); not at 2048 (Llama-3.2-1B shape c=8: 7 720 against 7 758 -- the
+    fp32 activation rows and the norm prologue cost qkv and gate_up 2.3 and
+    3.3 us, the in-kernel split merge o_proj and down_proj 1.8 us each,
+    about what the two RMSNorm launches per layer cost).
+    FASTDMS_AMD_NORM_STATS=1 / 0 forces it on / off."""
+    env = os.environ.get("FASTDMS_AMD_NORM_STATS", "").strip()
+    if env in ("0", "1"):
+        return env == "1"
+    return hidden_size >= 4096
 
 
 class LlamaAttention(nn.Module):
@@ -267,11 +283,17 @@ class LlamaModel(nn.Module):
         with ``greedy_out`` writes the greedy token ids there (the head's GEMV
         fused with the argmax) and returns None.
 
-        (The RMSNorm stays a kernel of its own: folded into the GEMM prologue,
-        every workgroup would re-read and re-normalise the whole activation,
-        which costs more at M <= 16 than the launch it saves.)"""
+        With bf16 linears (``_norm_stats_path``) the RMSNorms between layers are
+        no kernels of their own: o_proj and down_proj finish as the residual
+        add (fp32 rows f, the residual in place, per-strip sums of f^2) and
+        qkv / gate_up apply the norm from those sums as they load their
+        activation (fdms_linear_small_m epilogue 4 / prologue 2).  Otherwise
+        (FP8 / INT4 routes, which quantise the normalised activation) each
+        RMSNorm is a kernel that merges its producer's split partials."""
         x = self.embed_tokens(input_ids)
         rows, dev = input_ids.shape[0], x.device
+        if self._norm_stats_path(rows):
+            return self._forward_decode_norm_stats(x, positions, lm_head, greedy_out)
         res = None
         for layer in self.layers:
             attn, mlp = layer.self_attn, layer.mlp
@@ -288,6 +310,50 @@ class LlamaModel(nn.Module):
             act = _linear_from_norm(mlp.gate_up_proj, h, am, epilogue=EPI_SILU_MUL, amax_out=am_act)
             x = _deferred_linear(mlp.down_proj, act, x_amax=am_act)
         h, _ = self.norm(x, res)
+        if greedy_out is not None:
+            lm_head.greedy_into(h, greedy_out)
+            return None
+        return lm_head.logits(h)
+
+    def _norm_stats_path(self, rows: int) -> bool:
+        if not _norm_stats_enabled(self.norm.weight.numel()) or len(self.layers) < 2:
+            return False
+        for layer in self.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            lins = (attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj)
+            if any(lin.route(rows)[0] != "bf16" for lin in lins):
+                return False
+            if attn.o_proj.bias is not None or mlp.down_proj.bias is not None:
+                return False
+        return True
+
+    def _forward_decode_norm_stats(self, x: torch.Tensor, positions: torch.Tensor, lm_head: LinearBase,
+                                   greedy_out: torch.Tensor | None) -> torch.Tensor | None:
+        """forward_decode_fused on bf16 linears: the first layer's input RMSNorm
+        and the final one are kernels, every RMSNorm in between is split
+        between the linear before it (the residual add and the row sums of
+        squares) and the one after it (the scaling)."""
+        rows, hidden = x.shape
+        f = torch.empty((rows, hidden), device=x.device, dtype=torch.float32)
+        ssq = torch.empty((rows, hidden // 16), device=x.device, dtype=torch.float32)
+        res = x  # the embedding rows are the first residual, updated in place from here on
+        h = self.layers[0].input_layernorm(x)
+        last = len(self.layers) - 1
+        for i, layer in enumerate(self.layers):
+            attn, mlp = layer.self_attn, layer.mlp
+            if i == 0:
+                qkv = attn.qkv_proj.run(h, attn.qkv_proj.bias)
+            else:
+                norm = layer.input_layernorm
+                qkv = linear_norm_stats(f, ssq, norm.weight, norm.eps, attn.qkv_proj.weight, attn.qkv_proj.bias)
+            linear_residual_stats(attn.attend(positions, qkv), attn.o_proj.weight, res, f, ssq)
+            norm = layer.post_attention_layernorm
+            act = linear_norm_stats(f, ssq, norm.weight, norm.eps, mlp.gate_up_proj.weight, mlp.gate_up_proj.bias,
+                                    epilogue=EPI_SILU_MUL)
+            if i < last:
+                linear_residual_stats(act, mlp.down_proj.weight, res, f, ssq)
+            else:
+                h, _ = self.norm(_deferred_linear(mlp.down_proj, act), res)
         if greedy_out is not None:
             lm_head.greedy_into(h, greedy_out)
             return None

@@ -363,11 +363,21 @@ int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int6
  * quantize_x 1 / 2, x_amax required): x holds the e4m3fn codes of the
  * quantised activation (fdms_rmsnorm's q_out, same quantize_x form), row
  * stride x_stride bytes.  amax_out (optional, epilogues 0 / 1) = per-strip max
- * |y|: amax_out[row * (n_out/16) + strip].  k_splits > 1 splits K over
+ * |y|: amax_out[row * (n_out/16) + strip].  epilogue 4 (prologue 0, no
+ * activation quantisation) = the residual add of the RMSNorm that follows
+ * (layernorm.py:32-40): with v the finished bf16 output, y receives f =
+ * fp32(v) + fp32(residual) as fp32 rows (y_stride in floats, 16-byte aligned),
+ * residual_out = bf16(f) (it may be residual itself: updated in place), and
+ * amax_out[row * (n/16) + strip] = the strip's sum of f^2.  prologue 2 (x_dtype
+ * F32, quantize_x 0, epilogues 0 / 1) = that RMSNorm applied as x is loaded:
+ * x holds f (fp32 rows, x_stride in floats), x_amax [m, x_amax_n] the producer
+ * strips' sums of f^2 (x_amax_stride per row), norm_weight the norm's weight;
+ * a = bf16(bf16(f * rsqrt(sum / k + eps)) * norm_weight).  k_splits > 1 splits K over
  * workgroups: workspace holds (n_out/16) * k_splits * 256 floats (x2 for
  * epilogue 1) and counters n_out/16 ints, zero before the first call and left
  * zero.  k / k_splits a multiple of 256, n_out of 16, 16-byte aligned rows; y
- * and residual_out must not alias x / residual. */
+ * and residual_out must not alias x / residual (except epilogue 4's in-place
+ * residual). */
 int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int k, const void* w, int w_dtype,
                         int64_t w_stride, const float* w_scale_inv, const void* bias, int n, int prologue,
                         const void* norm_weight, float eps, const void* residual, int64_t res_stride,

@@ -1004,22 +1004,30 @@ class Emulator:
                        amax_out, row_scale_out, x_dtype, stream):
         """Same expressions as oracle/model.py (rmsnorm, mlp, linear) and oracle/linear.py.
         A producer's x_amax must equal x's own row amax (the kernel's contract);
-        x_dtype FP8: x holds the e4m3fn codes its producer quantised with that amax."""
+        x_dtype FP8: x holds the e4m3fn codes its producer quantised with that amax.
+        Prologue 2: x holds fp32 rows f and x_amax the per-strip sums of f^2 of an
+        epilogue-4 producer; epilogue 4: f = bf16 result + residual to y (fp32),
+        bf16(f) to residual_out, per-strip sums of f^2 to amax_out."""
         from oracle import linear as olin
         if m == 0 or n == 0:
             return 0
         n_out = n // 2 if epilogue == 1 else n
-        if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1):
+        if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1, 2) or epilogue == 2:
             return 1
-        if x_amax and (prologue or not qx or x_amax_n < 1 or (m > 1 and x_amax_s < x_amax_n)):
+        stats_in, stats_out = prologue == 2, epilogue == 4
+        if stats_in and (x_dtype != DT_F32 or qx or not x_amax or x_amax_n < 1 or epilogue > 1):
             return 1
-        if (amax_out and epilogue > 1) or (row_scale_out and epilogue != 3):
+        if stats_out and (prologue or qx or not res or not res_out or not amax_out):
+            return 1
+        if x_amax and not stats_in and (prologue or not qx or x_amax_n < 1 or (m > 1 and x_amax_s < x_amax_n)):
+            return 1
+        if (amax_out and epilogue > 1 and not stats_out) or (row_scale_out and epilogue != 3):
             return 1
         xq_in = x_dtype == DT_FP8
-        if x_dtype not in (DT_BF16, DT_FP8) or (xq_in and (w_dtype != DT_FP8 or not qx or not x_amax)):
+        if (x_dtype not in (DT_BF16, DT_FP8) and not stats_in) or (xq_in and (w_dtype != DT_FP8 or not qx or not x_amax)):
             return 1
         am = None
-        if x_amax:
+        if x_amax and not stats_in:
             self.calls.append("fdms_linear_small_m:x_amax" + (":fp8_x" if xq_in else ""))
             am = self.view(x_amax, torch.float32, (m, x_amax_n), (x_amax_s, 1), "x_amax").amax(dim=1)
             if not xq_in:
@@ -1067,6 +1075,13 @@ class Emulator:
         bv = self.view(bias, torch.bfloat16, (n,), (1,), "bias").float() if bias else None
         if xq_in:
             a = None
+        elif stats_in:
+            self.calls.append("fdms_linear_small_m:norm_stats")
+            f = self.view(x, torch.float32, (m, k), (x_s, 1), "x")
+            ss = self.view(x_amax, torch.float32, (m, x_amax_n), (x_amax_s, 1), "x_amax").sum(dim=1, keepdim=True)
+            a = (f * torch.rsqrt(ss / k + eps)).to(torch.bfloat16).float()
+            nw = self.view(norm_w, torch.bfloat16, (k,), (1,), "norm_weight").float()
+            a = (a * nw).to(torch.bfloat16).float()
         elif prologue == 1:
             xv = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
             f = xv + (self.view(res, torch.bfloat16, (m, k), (res_s, 1), "residual").float() if res else 0.0)
@@ -1099,6 +1114,15 @@ class Emulator:
         if epilogue == 1:  # gate_up -> SiluAndMul, the oracle model's mlp expression
             g, u = out[:, :n_out], out[:, n_out:]
             out = torch.nn.functional.silu(g) * u
+        if stats_out:
+            self.calls.append("fdms_linear_small_m:residual_stats")
+            rv = self.view(res, torch.bfloat16, (m, n), (res_s, 1), "residual").float()
+            f = out + rv
+            self.view(res_out, torch.bfloat16, (m, n), (ro_s, 1), "residual_out").copy_(f.to(torch.bfloat16))
+            self.view(y, torch.float32, (m, n), (y_s, 1), "y").copy_(f)
+            self.view(amax_out, torch.float32, (m, n // 16), (n // 16, 1), "amax_out").copy_(
+                (f * f).reshape(m, n // 16, 16).sum(dim=2))
+            return 0
         yb = out.to(torch.bfloat16)
         self.view(y, torch.bfloat16, (m, n_out), (y_s, 1), "y").copy_(yb)
         if amax_out:

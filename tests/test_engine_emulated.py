@@ -37,6 +37,18 @@ def test_engine_glue_matches_oracle(model, lens, gen, layout):
     _run(model, lens, gen, fused_head=False, layout=layout)
 
 
+@pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 64], 10), ("tiny-qwen3", [129, 700], 8)])
+def test_norm_stats_decode_matches_oracle(monkeypatch, model, lens, gen):
+    """The decode step with the RMSNorms split between the linears around them
+    (o_proj / down_proj finish the residual add and the row sums of squares,
+    qkv / gate_up apply the norm: fdms_linear_small_m epilogue 4 / prologue 2;
+    the default at hidden sizes from 4096) against the oracle's logits, and
+    that path is the one that ran."""
+    monkeypatch.setenv("FASTDMS_AMD_NORM_STATS", "1")
+    calls = _run(model, lens, gen, fused_head=False)
+    assert "fdms_linear_small_m:norm_stats" in calls and "fdms_linear_small_m:residual_stats" in calls
+
+
 @pytest.mark.parametrize("model,lens,gen", [("tiny-llama", [300, 517, 64], 12), ("tiny-qwen3", [129, 700], 8)])
 def test_engine_fused_greedy_head_matches_oracle_tokens(monkeypatch, model, lens, gen):
     """Decode with the LM-head GEMV fused with the argmax: no logits, tokens

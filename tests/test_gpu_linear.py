@@ -36,6 +36,81 @@ def _close_bf16(got, want, what, ulps=1.0, atol=0.0, mag=None):
                                  f"max err {float((g - w).abs().max()):.4g}")
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("m,n,k,splits", [(8, 2048, 2048, 1), (8, 2048, 8192, 2), (3, 512, 4096, 4),
+                                          (16, 1024, 2048, 2), (1, 2048, 8192, 1)])
+def test_residual_stats_epilogue(m, n, k, splits, fp8):
+    """Epilogue 4, the residual add of the RMSNorm after a decode linear
+    (layernorm.py:32-40): with y the same launch's epilogue-0 result (bf16),
+    f = fp32(y) + fp32(residual) bit for bit, the residual updated in place to
+    bf16(f) bit for bit, each 16-column strip's sum of f^2 within fp32
+    summation error of the float64 sum; bf16 and FP8 weights (no activation
+    quantisation)."""
+    require_gpu()
+    from fastdms_amd.layers.linear import linear_residual_stats, linear_small_m, quantize_fp8_rows
+    g = torch.Generator().manual_seed(m * 131 + n + splits + fp8)
+    x, w = _bf16((m, k), g).cuda(), _bf16((n, k), g, 0.02).cuda()
+    sinv = None
+    if fp8:
+        w, sinv = quantize_fp8_rows(w)
+    res = _bf16((m, n), g).cuda()
+    y = linear_small_m(x, w, weight_scale_inv=sinv, quantize_x=False, k_splits=splits)
+    res0 = res.clone()
+    f = torch.full((m, n), float("nan"), device="cuda")
+    ssq = torch.full((m, n // 16), float("nan"), device="cuda")
+    linear_residual_stats(x, w, res, f, ssq, weight_scale_inv=sinv, k_splits=splits)
+    torch.cuda.synchronize()
+    f_want = y.float() + res0.float()
+    assert torch.equal(f, f_want), "f = fp32(y) + fp32(residual)"
+    assert torch.equal(res, f_want.to(torch.bfloat16)), "residual = bf16(f)"
+    want = f_want.double().pow(2).view(m, n // 16, 16).sum(-1)
+    err = float(((ssq.double() - want).abs() / want.clamp(min=1e-30)).max())
+    assert err <= 2e-6, f"strip sums of squares: max rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("m,n,k,epi", [(8, 3072, 2048, 0), (8, 16384, 2048, 1), (1, 512, 2048, 0),
+                                       (16, 1024, 4096, 1), (3, 4096, 8192, 0)])
+def test_norm_stats_prologue(m, n, k, epi):
+    """Prologue 2 on an epilogue-4 producer's output (fp32 rows f, strip sums
+    of f^2): y = bf16(bf16(f * rsqrt(mean f^2 + eps)) * norm_w) @ W^T (+ SiLU*up
+    for epilogue 1), within 2 bf16 ulps of the float64 product of that
+    activation built from the oracle's own sum of squares (the kernel adds the
+    strip sums in another order, so an element may round the other way); and
+    the same chain against fdms_rmsnorm (+ residual) followed by the plain
+    linear, the RMSNorm path the decode step had before."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    from fastdms_amd.layers.linear import (EPI_SILU_MUL, linear_norm_stats, linear_residual_stats,
+                                           linear_small_m)
+    g = torch.Generator().manual_seed(m * 7 + n + k + epi)
+    kp = 2048
+    xp, wp = _bf16((m, kp), g).cuda(), _bf16((k, kp), g, 0.03).cuda()  # the producer linear
+    res = _bf16((m, k), g).cuda()
+    nw = (1.0 + 0.2 * torch.randn(k, generator=g)).to(torch.bfloat16).cuda()
+    w = _bf16((n, k), g, 0.02).cuda()
+    eps = 1e-5
+    # the previous path: the producer's bf16 rows, fdms_rmsnorm with the residual, a plain linear
+    yp = linear_small_m(xp, wp)
+    h_old, res_old = rms_norm(yp, nw, eps, residual=res)
+    out_old = linear_small_m(h_old, w, epilogue=epi)
+    f = torch.empty((m, k), device="cuda")
+    ssq = torch.empty((m, k // 16), device="cuda")
+    linear_residual_stats(xp, wp, res, f, ssq)
+    out = linear_norm_stats(f, ssq, nw, eps, w, epilogue=EPI_SILU_MUL if epi else 0)
+    torch.cuda.synchronize()
+    assert torch.equal(res, res_old), "residual"
+    ff = f.double().cpu()
+    inv = torch.rsqrt(ff.pow(2).mean(-1, keepdim=True) + eps).float()
+    a = (f.cpu() * inv).to(torch.bfloat16).float()
+    a = (a * nw.float().cpu()).to(torch.bfloat16).double()
+    ref = a @ w.double().cpu().T
+    if epi:
+        gt, up = ref[:, :n // 2].to(torch.bfloat16).float(), ref[:, n // 2:].to(torch.bfloat16).float()
+        ref = torch.nn.functional.silu(gt) * up
+    _close_bf16(out, ref.to(torch.bfloat16), "norm-stats linear vs oracle", ulps=2.0, atol=2e-3)
+    _close_bf16(out, out_old.cpu(), "norm-stats linear vs rmsnorm + linear", ulps=2.0, atol=2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_quantize_fp8_rows_bit_exact(dtype):
     require_gpu()
