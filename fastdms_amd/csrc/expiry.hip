@@ -10,13 +10,16 @@
 //
 // One block per (layer, sequence, kv head); one launch covers every layer
 // (per-layer arena pointers come from a device pointer table), where the
-// reference launches once per layer.  Slots are scanned in 256-slot chunks
-// with ballot ranks.  Moves are in place with dst <= src, so every chunk (and
-// every register-sized pass inside it) reads all of its sources before any
-// thread writes: a destination can only alias a source that an earlier pass
-// already read.  Only rows whose rank changes are touched (the reference's
-// full kernel rewrites every kept row).  Rows move as raw bytes, so one kernel
-// serves every arena dtype.
+// reference launches once per layer.  The span's metadata is read in chunks of
+// 2048 slots (slot c0 + 256 j + thread: every load instruction reads
+// contiguous slots); keep / move ranks in slot order come from per-(j, wave)
+// ballot counts behind one barrier.  Only rows whose rank changes move (the
+// reference's full kernel rewrites every kept row), in passes of 32 KB per
+// workgroup: a pass reads all of its sources before any thread writes (a
+// destination may alias a source of the same pass), and the next pass's reads
+// go out with this pass's writes -- every destination lies below every later
+// source (dst = rank <= src, sources ascend).  Rows move as raw bytes, so one
+// kernel serves every arena dtype.
 #include "fdms_vec.h"
 
 using namespace fdms;
@@ -24,67 +27,73 @@ using namespace fdms;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnitsPerThread = 8;
+constexpr int kWaves = kThreads / 64;
+constexpr int kSlots = 8;                      // metadata slots per thread and chunk
+constexpr int kChunk = kThreads * kSlots;      // 2048
+constexpr int kMoveBytes = 128;                // row bytes per thread and pass (32 KB per workgroup)
+constexpr int kLdsPages = 2048;                // page-table entries staged in LDS (spans up to 32768 rows)
 
-__device__ __forceinline__ int block_rank(bool keep, int* s_wave, int* total) {
-  const uint64_t m = __ballot(keep);
-  const int lane = __lane_id();
-  const int wave = threadIdx.x >> 6;
-  const int prefix = __popcll(m & ((1ull << lane) - 1ull));
-  if (lane == 0) s_wave[wave] = __popcll(m);
-  __syncthreads();
-  int off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kThreads / kWave; ++w) {
-    const int c = s_wave[w];
-    off += (w < wave) ? c : 0;
-    tot += c;
-  }
-  *total = tot;
-  return off + prefix;
-}
-
-// Copy n_moves rows (src slot s_src[i] -> dst slot s_dst[i], both relative to
-// the span base) for K and V, in passes that read everything before writing.
 // Physical arena row of span slot r: base + r (flat spans) or, paged,
 // table[r >> 4] * 16 + (r & 15).
 __device__ __forceinline__ int64_t slot_row(int64_t base, const int32_t* table, int r) {
   return table ? ((int64_t)table[r >> 4] << 4) + (r & 15) : base + r;
 }
 
+// Row-move passes over the chunk's move list (s_src / s_dst, ascending
+// sources): K rows then V rows, UNIT bytes per access.
 template <int UNIT>
-__device__ void move_rows(uint8_t* ck, uint8_t* cv, int64_t base, int64_t c_s_bytes, int64_t row_bytes,
-                          const int* s_src, const int* s_dst, int n_moves, const int32_t* table) {
-  const int units_per_row = (int)(row_bytes / UNIT);
-  const int total = n_moves * units_per_row * 2;
-  for (int p0 = 0; p0 < total; p0 += kThreads * kUnitsPerThread) {
-    Vec<uint8_t, UNIT> buf[kUnitsPerThread];
-    int64_t dst_off[kUnitsPerThread];
-    uint8_t* dst_arena[kUnitsPerThread];
+struct Mover {
+  static constexpr int kU = kMoveBytes / UNIT < 16 ? kMoveBytes / UNIT : 16;  // units per thread and pass
+  uint8_t* ck;
+  uint8_t* cv;
+  int64_t base, c_s_bytes;
+  const int32_t* table;
+  int units_per_row, n_moves, total;
+  const int* s_src;
+  const int* s_dst;
+
+  __device__ __forceinline__ void read(int p0, Vec<uint8_t, UNIT>* buf, int64_t* dst_off, int* which) const {
 #pragma unroll
-    for (int j = 0; j < kUnitsPerThread; ++j) {
-      const int u = p0 + j * kThreads + threadIdx.x;
-      dst_arena[j] = nullptr;
+    for (int j = 0; j < kU; ++j) {
+      const int u = p0 + j * kThreads + (int)threadIdx.x;
+      which[j] = -1;
       if (u < total) {
-        const int which = u / (n_moves * units_per_row);  // 0 = K, 1 = V
-        const int uu = u - which * n_moves * units_per_row;
+        const int w = u / (n_moves * units_per_row);  // 0 = K, 1 = V
+        const int uu = u - w * n_moves * units_per_row;
         const int r = uu / units_per_row;
         const int64_t off = (int64_t)(uu - r * units_per_row) * UNIT;
-        uint8_t* arena = which ? cv : ck;
-        buf[j] = *reinterpret_cast<const Vec<uint8_t, UNIT>*>(arena + slot_row(base, table, s_src[r]) * c_s_bytes +
-                                                              off);
-        dst_arena[j] = arena;
+        const uint8_t* arena = w ? cv : ck;
+        buf[j] = *reinterpret_cast<const Vec<uint8_t, UNIT>*>(arena + slot_row(base, table, s_src[r]) * c_s_bytes + off);
         dst_off[j] = slot_row(base, table, s_dst[r]) * c_s_bytes + off;
+        which[j] = w;
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kUnitsPerThread; ++j) {
-      if (dst_arena[j]) *reinterpret_cast<Vec<uint8_t, UNIT>*>(dst_arena[j] + dst_off[j]) = buf[j];
-    }
-    __syncthreads();
   }
-}
+  __device__ __forceinline__ void write(const Vec<uint8_t, UNIT>* buf, const int64_t* dst_off, const int* which) const {
+#pragma unroll
+    for (int j = 0; j < kU; ++j)
+      if (which[j] >= 0) *reinterpret_cast<Vec<uint8_t, UNIT>*>((which[j] ? cv : ck) + dst_off[j]) = buf[j];
+  }
+  // every pass: its reads, a barrier (all reads of the pass done), its
+  // writes; pass p + 1's reads are issued before pass p's writes
+  __device__ void run() const {
+    constexpr int kPass = kThreads * kU;
+    if (total <= 0) return;
+    Vec<uint8_t, UNIT> b0[kU], b1[kU];
+    int64_t o0[kU], o1[kU];
+    int w0[kU], w1[kU];
+    read(0, b0, o0, w0);
+    for (int p0 = 0; p0 < total; p0 += 2 * kPass) {
+      __syncthreads();
+      if (p0 + kPass < total) read(p0 + kPass, b1, o1, w1);
+      write(b0, o0, w0);
+      if (p0 + kPass >= total) break;
+      __syncthreads();
+      if (p0 + 2 * kPass < total) read(p0 + 2 * kPass, b0, o0, w0);
+      write(b1, o1, w1);
+    }
+  }
+};
 
 // Paged spans of the expiry launch (table == nullptr: flat spans).  After the
 // re-compaction a span keeps ceil(live / 16) pages; the rest go back to the
@@ -122,11 +131,11 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
     uint8_t* compact_k, uint8_t* compact_v, const uint64_t* __restrict__ layer_k, const uint64_t* __restrict__ layer_v,
     int64_t row_bytes, int64_t c_s_bytes, const int64_t* __restrict__ current_positions, int num_kv_heads,
     int window, const PagedSpans pg) {
-  __shared__ int s_wave[kThreads / kWave];
-  __shared__ int s_wave_mv[kThreads / kWave];
-  __shared__ int s_src[kThreads];
-  __shared__ int s_dst[kThreads];
-  __shared__ int s_first;
+  __shared__ int s_cnt[kSlots][kWaves];  // kept, then moved, slots per (j, wave)
+  __shared__ int s_hit[kSlots][kWaves];  // INCREMENTAL: first hit of (j, wave), or kChunk
+  __shared__ int s_src[kChunk];
+  __shared__ int s_dst[kChunk];
+  __shared__ int32_t s_table[kLdsPages];  // paged: the span's page ids, read once
 
   const int l = blockIdx.y;
   const int s = blockIdx.x / num_kv_heads;
@@ -142,102 +151,132 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
   const int64_t cur = current_positions[s];
   const int live = *live_p;
   const int tid = threadIdx.x;
-
-  if (!INCREMENTAL) {
-    int running = 0;
-    for (int c0 = 0; c0 < live; c0 += kThreads) {
-      const int slot = c0 + tid;
-      const bool valid = slot < live;
-      int32_t p = -1;
-      uint8_t e = 0;
-      if (valid) {
-        p = pos[slot];
-        e = ev[slot];
-      }
-      const bool keep = valid && ((e == 0) || (cur - (int64_t)p) <= (int64_t)window);
-      int total = 0;
-      const int r = running + block_rank(keep, s_wave, &total);  // barrier: all reads done
-      const bool move = keep && r != slot;
-      const uint64_t mm = __ballot(move);
-      // compact list of moves (ordered by slot) for the row copy
-      {
-        const int lane = __lane_id();
-        const int wave = tid >> 6;
-        if (lane == 0) s_wave_mv[wave] = __popcll(mm);
-        __syncthreads();
-        int off = 0, nmv = 0;
-#pragma unroll
-        for (int w = 0; w < kThreads / kWave; ++w) {
-          off += (w < wave) ? s_wave_mv[w] : 0;
-          nmv += s_wave_mv[w];
-        }
-        if (move) {
-          const int idx = off + __popcll(mm & ((1ull << lane) - 1ull));
-          s_src[idx] = slot;
-          s_dst[idx] = r;
-          pos[r] = p;
-          ev[r] = e;
-        }
-        __syncthreads();
-        if (nmv) move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, nmv, table);
-      }
-      running += total;
-      __syncthreads();
-    }
-    for (int slot = running + tid; slot < live; slot += kThreads) {
-      pos[slot] = -1;
-      ev[slot] = 0;
-    }
-    if (tid == 0) {
-      *live_p = running;
-      if (table) release_pages(pg, l, table, held, running);
-    }
-    return;
-  }
-
-  // incremental: first expired slot
+  const int lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
   const int64_t cutoff = cur - (int64_t)window;
-  if (tid == 0) s_first = live;
-  __syncthreads();
-  for (int c0 = 0; c0 < live; c0 += kThreads) {
-    const int slot = c0 + tid;
-    bool hit = false;
-    if (slot < live) hit = ev[slot] != 0 && (int64_t)pos[slot] < cutoff;
-    const uint64_t m = __ballot(hit);
-    if (m && __lane_id() == 0) atomicMin(&s_first, c0 + (tid & ~63) + (int)__ffsll((unsigned long long)m) - 1);
-    __syncthreads();
-    const int f = s_first;
-    __syncthreads();
-    if (f < live) break;
+
+  // paged: the span's block-table row into LDS (its loads go out with the
+  // first chunk's metadata loads), so a row move waits for one memory round
+  // trip, not two
+  const int n_pages = (live + 15) >> 4;
+  const int32_t* tbl = table;
+  if (table && n_pages <= kLdsPages) {
+    for (int i = tid; i < n_pages; i += kThreads) s_table[i] = table[i];
+    tbl = s_table;  // made visible by the first chunk's barriers
   }
-  const int first = s_first;
-  if (first >= live) return;
-  for (int c0 = first; c0 < live - 1; c0 += kThreads) {
-    const int slot = c0 + tid;
-    const bool move = slot < live - 1;
-    int32_t p = -1;
-    uint8_t e = 0;
-    if (move) {
-      p = pos[slot + 1];
-      e = ev[slot + 1];
+  int running = 0;       // slots kept before this chunk
+  int first = live;      // INCREMENTAL: the removed slot, once found
+  for (int c0 = 0; c0 < live; c0 += kChunk) {
+    int32_t p[kSlots];
+    uint8_t e[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int slot = min(c0 + j * kThreads + tid, live - 1);  // clamped: every load in bounds
+      p[j] = pos[slot];
+      e[j] = ev[slot];
     }
-    const int n = min(kThreads, live - 1 - c0);
-    if (tid < n) {
-      s_src[tid] = slot + 1;
-      s_dst[tid] = slot;
+    bool keep[kSlots];
+    if (INCREMENTAL) {
+      if (first == live) {  // uniform: look for the first expired slot in this chunk
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) {
+          const int slot = c0 + j * kThreads + tid;
+          const uint64_t m = __ballot(slot < live && e[j] != 0 && (int64_t)p[j] < cutoff);
+          if (lane == 0) s_hit[j][wave] = m ? j * kThreads + wave * 64 + (int)__ffsll((unsigned long long)m) - 1 : kChunk;
+        }
+        __syncthreads();
+        int f = kChunk;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j)
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) f = min(f, s_hit[j][w]);
+        if (f < kChunk) first = c0 + f;
+      }
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) keep[j] = c0 + j * kThreads + tid < live && c0 + j * kThreads + tid != first;
+    } else {
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j)
+        keep[j] = c0 + j * kThreads + tid < live && (e[j] == 0 || (cur - (int64_t)p[j]) <= (int64_t)window);
     }
-    __syncthreads();  // all metadata reads of this chunk done
-    if (move) {
-      pos[slot] = p;
-      ev[slot] = e;
+    // ranks in slot order (j-major, then thread): kept and moved counts per (j, wave)
+    uint64_t km[kSlots], mm[kSlots];
+    int rank_in[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      km[j] = __ballot(keep[j]);
+      rank_in[j] = __popcll(km[j] & below);
     }
-    move_rows<UNIT>(ck, cv, base, c_s_bytes, row_bytes, s_src, s_dst, n, table);
+    // a slot moves when it is kept and slots before it (in this chunk or
+    // earlier) were removed: its rank differs from its slot
+    int kept_before_wave[kSlots];
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) s_cnt[j][wave] = __popcll(km[j]);
+    }
+    __syncthreads();  // all metadata reads of the chunk done; counts published
+    int acc = 0, tot = 0;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int c = s_cnt[j][w];
+        if (w == wave) kept_before_wave[j] = acc;
+        acc += c;
+      }
+    }
+    tot = acc;
+    int rank[kSlots];
+    bool mv[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      rank[j] = running + kept_before_wave[j] + rank_in[j];
+      mv[j] = keep[j] && rank[j] != c0 + j * kThreads + tid;
+      mm[j] = __ballot(mv[j]);
+    }
+    __syncthreads();  // the kept counts are read: reuse s_cnt for the move counts
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) s_cnt[j][wave] = __popcll(mm[j]);
+    }
+    __syncthreads();
+    int macc = 0;
+    int moved_before_wave[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        if (w == wave) moved_before_wave[j] = macc;
+        macc += s_cnt[j][w];
+      }
+    }
+    const int n_moves = macc;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      if (mv[j]) {
+        const int idx = moved_before_wave[j] + __popcll(mm[j] & below);
+        s_src[idx] = c0 + j * kThreads + tid;
+        s_dst[idx] = rank[j];
+        pos[rank[j]] = p[j];
+        ev[rank[j]] = e[j];
+      }
+    }
+    __syncthreads();  // the move list is complete
+    if (n_moves) {
+      Mover<UNIT> mvr{ck, cv, base, c_s_bytes, tbl, (int)(row_bytes / UNIT), n_moves,
+                      n_moves * (int)(row_bytes / UNIT) * 2, s_src, s_dst};
+      mvr.run();
+    }
+    running += tot;
+    __syncthreads();  // s_src / s_dst / s_cnt are reused by the next chunk
+  }
+  for (int slot = running + tid; slot < live; slot += kThreads) {
+    pos[slot] = -1;
+    ev[slot] = 0;
   }
   if (tid == 0) {
-    pos[live - 1] = -1;
-    ev[live - 1] = 0;
-    *live_p = live - 1;
-    if (table) release_pages(pg, l, table, held, live - 1);
+    *live_p = running;
+    if (table) release_pages(pg, l, table, held, running);
   }
 }
 
