@@ -439,8 +439,10 @@ def _pmc_traffic(name: str, config: str):
     path = ROOT / "profiles" / name
     try:
         d = json.loads(path.read_text())
+        if "configs" in d:  # one summary per bench config
+            return d["configs"][config]["traffic_bytes_per_launch"] if config in d["configs"] else None
         return d["traffic_bytes_per_launch"] if d.get("config") == config else None
-    except (OSError, KeyError, ValueError):
+    except (OSError, KeyError, ValueError, TypeError):
         return None
 
 
@@ -632,7 +634,7 @@ def expiry_roofline(replays: int = 10, layers: int = 16, seqs: int = 8, heads: i
     # around its replay time the kernels, not the host's launch calls
     g = torch.cuda.CUDAGraph()
     st = torch.cuda.Stream()
-    with torch.cuda.stream(st):
+    with torch.inference_mode(), torch.cuda.stream(st):  # as the engine's own captures
         with torch.cuda.graph(g, stream=st):
             for _ in range(replays):
                 run()
