@@ -232,7 +232,11 @@ def linear_norm_stats(f: torch.Tensor, ssq: torch.Tensor, norm_weight: torch.Ten
         out = torch.empty((rows, n_out), device=f.device, dtype=torch.bfloat16)
     strips = n_out // 16
     if k_splits is None:
-        k_splits = choose_k_splits(f.device, strips, k)
+        env = os.environ.get("FASTDMS_AMD_NORM_SPLITS", "").strip()  # tuning override
+        if env.isdigit() and 1 <= int(env) <= _MAX_K_SPLITS and k % (int(env) * 256) == 0:
+            k_splits = int(env)
+        else:
+            k_splits = choose_k_splits(f.device, strips, k)
     ws = counters = None
     if k_splits > 1:
         ws, counters = linear_workspace(f.device, strips * k_splits * 256 * (2 if epilogue else 1), strips)
