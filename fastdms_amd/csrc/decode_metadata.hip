@@ -255,13 +255,18 @@ __global__ __launch_bounds__(kPlanThreads) void paged_prepare_decode_plan_kernel
       reinterpret_cast<int4*>(it)[1] = make_int4(n, app, pos, flags);
       const int last = max(r1 - 1, r0);
       const int used = r1 > r0 ? (r1 - r0 + 63) / 64 * 4 : 0;  // quarters of the item's groups
-      for (int j4 = 0; j4 < used; j4 += 4) {
-        int4 w;
-        w.x = btr[min(r0 + kPlanPage * (j4 + 0), last) >> kPagedShift];
-        w.y = btr[min(r0 + kPlanPage * (j4 + 1), last) >> kPagedShift];
-        w.z = btr[min(r0 + kPlanPage * (j4 + 2), last) >> kPagedShift];
-        w.w = btr[min(r0 + kPlanPage * (j4 + 3), last) >> kPagedShift];
-        reinterpret_cast<int4*>(it + kPlanHeader)[j4 / 4] = w;
+      // the item's page ids are table entries r0 / 16 .. (clamped at the
+      // page of its last rank): every load goes out before the first store
+      // (unconditional, indices in bounds), one memory latency per item
+      if (n > 0) {
+        const int q0 = r0 >> kPagedShift, ql = min(last, n - 1) >> kPagedShift;  // a held page, even for an empty item
+        int32_t ids[kPlanPages];
+#pragma unroll
+        for (int j = 0; j < kPlanPages; ++j) ids[j] = btr[min(q0 + j, ql)];
+#pragma unroll
+        for (int j4 = 0; j4 < kPlanPages; j4 += 4)
+          if (j4 < used)
+            reinterpret_cast<int4*>(it + kPlanHeader)[j4 / 4] = make_int4(ids[j4], ids[j4 + 1], ids[j4 + 2], ids[j4 + 3]);
       }
     }
   }
