@@ -50,6 +50,7 @@ SIGNATURES: dict[str, str] = {
     "fdms_rmsnorm": "pllippplplifpplip",
     "fdms_silu_mul": "pplip",
     "fdms_embedding_fp8": "plplplplip",
+    "fdms_embedding_rmsnorm": "plpllpfplplip",
     "fdms_rmsnorm_partials": "pilppplplifpppplip",
     "fdms_quantize_fp8_rows": "pilliplpip",
     "fdms_linear_small_m": "pliipilppiipfplpliiippplpilppip",

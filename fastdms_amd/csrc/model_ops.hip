@@ -61,10 +61,17 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
                                                            int64_t split_stride, const float* __restrict__ row_scale,
                                                            const float* __restrict__ col_scale,
                                                            float* __restrict__ amax_out, uint8_t* __restrict__ q_out,
-                                                           int64_t q_stride, int q_mode) {
+                                                           int64_t q_stride, int q_mode,
+                                                           const int64_t* __restrict__ ids, int64_t vocab) {
   __shared__ float s_red[kThreads / kWave];
   const int64_t row = blockIdx.x;
-  const bf16_t* x = PART ? nullptr : in + (row / heads) * in_stride + (row % heads) * in_head_stride;
+  // ids (optional, embedding rows): input row r is table row ids[r] (in_stride
+  // per row); an id outside [0, vocab) reads row 0 and yields NaN rows
+  const int64_t id = ids ? ids[row] : 0;
+  const bool id_ok = !ids || (id >= 0 && id < vocab);
+  const bf16_t* x = PART ? nullptr
+                         : ids ? in + (id_ok ? id : 0) * in_stride
+                               : in + (row / heads) * in_stride + (row % heads) * in_head_stride;
   const bool has_res = residual != nullptr;  // uniform
   const bf16_t* rs = has_res ? residual + row * (int64_t)hidden : weight;  // a valid address either way
   constexpr int V = 8;
@@ -120,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
       for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(f32_to_bf16(xf[i]));
     } else {
 #pragma unroll
-      for (int i = 0; i < V; ++i) xf[i] = bf16_to_f32(xv[j].v[i].bits);
+      for (int i = 0; i < V; ++i) xf[i] = id_ok ? bf16_to_f32(xv[j].v[i].bits) : __builtin_nanf("");
     }
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -258,7 +265,8 @@ FDMS_EXPORT int fdms_rmsnorm(const void* in, int64_t in_stride, int64_t in_head_
   hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                  \
                      (hipStream_t)stream, (const bf16_t*)in, (const bf16_t*)residual, (const bf16_t*)weight,        \
                      (bf16_t*)out, (bf16_t*)residual_out, hidden, in_stride, in_head_stride, heads, out_stride, eps, \
-                     nullptr, 0, (int64_t)0, nullptr, nullptr, amax_out, (uint8_t*)q_out, q_stride, q_mode)
+                     nullptr, 0, (int64_t)0, nullptr, nullptr, amax_out, (uint8_t*)q_out, q_stride, q_mode, nullptr,    \
+                     (int64_t)0)
   const int per = (hidden + 8 * kThreads - 1) / (8 * kThreads);
   if (per == 1) FDMS_RMSNORM(1);
   else if (per == 2) FDMS_RMSNORM(2);
@@ -288,7 +296,8 @@ FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64
   hipLaunchKernelGGL((rmsnorm_kernel<true, KSV, PERV>), dim3((unsigned)rows), dim3(kThreads), 0,                   \
                      (hipStream_t)stream, nullptr, (const bf16_t*)residual, (const bf16_t*)weight, (bf16_t*)out,      \
                      (bf16_t*)residual_out, hidden, (int64_t)0, (int64_t)0, 1, out_stride, eps, partials, k_splits,   \
-                     split_stride, row_scale, col_scale, amax_out, (uint8_t*)q_out, q_stride, q_mode)
+                     split_stride, row_scale, col_scale, amax_out, (uint8_t*)q_out, q_stride, q_mode, nullptr,        \
+                     (int64_t)0)
 #define FDMS_RMSNORM_PART_PER(PERV)                   \
   if (k_splits == 1) FDMS_RMSNORM_PART(1, PERV);      \
   else if (k_splits == 2) FDMS_RMSNORM_PART(2, PERV); \
@@ -305,6 +314,35 @@ FDMS_EXPORT int fdms_rmsnorm_partials(const float* partials, int k_splits, int64
   }
 #undef FDMS_RMSNORM_PART_PER
 #undef FDMS_RMSNORM_PART
+  FDMS_LAUNCH_CHECK();
+  return 0;
+}
+
+// Embedding gather + RMSNorm of the gathered rows in one launch (the decode
+// step's first layer: F.embedding, embed_head.py:87-104, then the first
+// input_layernorm without residual, layernorm.py:16-28): rows_out[i] =
+// table[ids[i]] (the first residual), out[i] = RMSNorm(rows_out[i]), the same
+// bits as fdms_rmsnorm of the gathered rows.  An id outside [0, vocab) gives
+// NaN rows in both (the reference's index_select raises there).
+FDMS_EXPORT int fdms_embedding_rmsnorm(const int64_t* ids, int64_t n, const void* table, int64_t table_stride,
+                                       int64_t vocab, const void* weight, float eps, void* out, int64_t out_stride,
+                                       void* rows_out, int64_t rows_stride, int hidden, void* stream) {
+  if (n < 0 || hidden <= 0 || hidden % 8 || hidden > 8 * kThreads * 4 || vocab <= 0) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  if (!ids || !table || !weight || !out || !rows_out || n > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+  if (!fdms_aligned16(table, weight, out, rows_out) || (table_stride | out_stride | rows_stride) % 8 ||
+      table_stride < hidden || out_stride < hidden || rows_stride != hidden)
+    return (int)hipErrorInvalidValue;
+#define FDMS_EMB_RMSNORM(PERV)                                                                                    \
+  hipLaunchKernelGGL((rmsnorm_kernel<false, 0, PERV>), dim3((unsigned)n), dim3(kThreads), 0, (hipStream_t)stream,   \
+                     (const bf16_t*)table, nullptr, (const bf16_t*)weight, (bf16_t*)out, (bf16_t*)rows_out, hidden,  \
+                     table_stride, (int64_t)0, 1, out_stride, eps, nullptr, 0, (int64_t)0, nullptr, nullptr, nullptr, \
+                     nullptr, (int64_t)0, 0, ids, vocab)
+  const int per = (hidden + 8 * kThreads - 1) / (8 * kThreads);
+  if (per == 1) FDMS_EMB_RMSNORM(1);
+  else if (per == 2) FDMS_EMB_RMSNORM(2);
+  else FDMS_EMB_RMSNORM(4);
+#undef FDMS_EMB_RMSNORM
   FDMS_LAUNCH_CHECK();
   return 0;
 }

@@ -67,6 +67,28 @@ class VocabParallelEmbedding(nn.Module):
         return F.embedding(x, self.weight)
 
 
+def embedding_rms_norm(ids: torch.Tensor, table: torch.Tensor, norm_weight: torch.Tensor,
+                       eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(RMSNorm(table[ids]), table[ids]) in one launch (fdms_embedding_rmsnorm):
+    the decode step's bf16 embedding gather (embed_head.py:87-104) and the
+    first decoder layer's input_layernorm without residual (layernorm.py:
+    16-28), whose input rows are the step's first residual.  Bit-identical to
+    rms_norm(F.embedding(ids, table)); an id outside the table gives NaN rows."""
+    if table.dtype != torch.bfloat16 or table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("embedding_rms_norm expects a bf16 [vocab, hidden] table with a contiguous last axis")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != table.shape[1]:
+        raise ValueError("norm_weight must be bf16 [hidden]")
+    flat = ids.reshape(-1).to(torch.long).contiguous()
+    n, hidden = flat.numel(), table.shape[1]
+    out = torch.empty((n, hidden), device=table.device, dtype=torch.bfloat16)
+    rows = torch.empty((n, hidden), device=table.device, dtype=torch.bfloat16)
+    nat.require_cuda(flat, table, norm_weight, what="embedding_rms_norm")
+    nat.call("fdms_embedding_rmsnorm", flat.data_ptr(), n, table.data_ptr(), table.stride(0), table.shape[0],
+             norm_weight.data_ptr(), float(eps), out.data_ptr(), out.stride(0), rows.data_ptr(), rows.stride(0),
+             hidden, nat.stream())
+    return out, rows
+
+
 def fp8_rerank_topk(x: torch.Tensor, candidates: torch.Tensor, weight_fp8: torch.Tensor,
                     weight_scale_inv: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """embed_head.py:214-302: per row, FP8 scores (448/amax activation

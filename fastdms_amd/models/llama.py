@@ -21,7 +21,7 @@ from ..layers.attention import Attention
 from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled, compact_attention_splitk_enabled,
                                         dms_decode_store_transient_k_enabled, dms_fused_decode_preprocess_enabled,
                                         fused_decode_attention_supported, fused_dms_rope_store_compact_decode)
-from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding
+from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding, embedding_rms_norm
 from ..layers.layernorm import RMSNorm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, LinearBase, MergedColumnParallelLinear, QKVParallelLinear,
                              RowParallelLinear, linear_norm_stats, linear_partials, linear_residual_stats,
@@ -290,17 +290,21 @@ class LlamaModel(nn.Module):
         activation (fdms_linear_small_m epilogue 4 / prologue 2).  Otherwise
         (FP8 / INT4 routes, which quantise the normalised activation) each
         RMSNorm is a kernel that merges its producer's split partials."""
-        x = self.embed_tokens(input_ids)
-        rows, dev = input_ids.shape[0], x.device
+        rows = input_ids.shape[0]
+        x, h0 = self._embed_first_norm(input_ids, rows)
+        dev = x.device
         if self._norm_stats_path(rows):
-            return self._forward_decode_norm_stats(x, positions, lm_head, greedy_out)
+            return self._forward_decode_norm_stats(x, h0, positions, lm_head, greedy_out)
         res = None
-        for layer in self.layers:
+        for i, layer in enumerate(self.layers):
             attn, mlp = layer.self_attn, layer.mlp
             # an FP8 linear's activation statistics come from its producer: the
             # RMSNorms quantise qkv's / gate_up's input themselves, gate_up hands
             # down_proj its per-strip output amax
-            h, res, am = _norm_into(layer.input_layernorm, x, res, attn.qkv_proj, rows)
+            if i == 0 and h0 is not None:
+                h, res, am = h0, x, None  # the first norm came with the embedding rows
+            else:
+                h, res, am = _norm_into(layer.input_layernorm, x, res, attn.qkv_proj, rows)
             qkv = _linear_from_norm(attn.qkv_proj, h, am)
             o = _deferred_linear(attn.o_proj, attn.attend(positions, qkv))
             h, res, am = _norm_into(layer.post_attention_layernorm, o, res, mlp.gate_up_proj, rows)
@@ -327,8 +331,20 @@ class LlamaModel(nn.Module):
                 return False
         return True
 
-    def _forward_decode_norm_stats(self, x: torch.Tensor, positions: torch.Tensor, lm_head: LinearBase,
-                                   greedy_out: torch.Tensor | None) -> torch.Tensor | None:
+    def _embed_first_norm(self, input_ids: torch.Tensor, rows: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """(embedding rows, the first input_layernorm of them or None).  With a
+        bf16 table and a first qkv that takes bf16 rows, one launch gathers the
+        rows and normalises them (fdms_embedding_rmsnorm); otherwise the gather
+        alone (the FP8 table's kernel, or F.embedding), normalised later."""
+        emb, norm = self.embed_tokens, self.layers[0].input_layernorm
+        if (not emb._fp8_embedding_enabled and emb.weight.dtype == torch.bfloat16 and emb.weight.numel() > 0
+                and self.layers[0].self_attn.qkv_proj.x_quant_mode(rows) == 0):
+            h, x = embedding_rms_norm(input_ids, emb.weight, norm.weight, norm.eps)
+            return x, h
+        return emb(input_ids), None
+
+    def _forward_decode_norm_stats(self, x: torch.Tensor, h0: torch.Tensor | None, positions: torch.Tensor,
+                                   lm_head: LinearBase, greedy_out: torch.Tensor | None) -> torch.Tensor | None:
         """forward_decode_fused on bf16 linears: the first layer's input RMSNorm
         and the final one are kernels, every RMSNorm in between is split
         between the linear before it (the residual add and the row sums of
@@ -337,7 +353,7 @@ class LlamaModel(nn.Module):
         f = torch.empty((rows, hidden), device=x.device, dtype=torch.float32)
         ssq = torch.empty((rows, hidden // 16), device=x.device, dtype=torch.float32)
         res = x  # the embedding rows are the first residual, updated in place from here on
-        h = self.layers[0].input_layernorm(x)
+        h = h0 if h0 is not None else self.layers[0].input_layernorm(x)
         last = len(self.layers) - 1
         for i, layer in enumerate(self.layers):
             attn, mlp = layer.self_attn, layer.mlp

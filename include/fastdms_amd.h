@@ -307,6 +307,18 @@ int fdms_silu_mul(const void* x, void* out, int64_t rows, int f, void* stream);
 int fdms_embedding_fp8(const int64_t* ids, int64_t n, const void* table, int64_t table_stride, const float* scale_inv,
                        int64_t vocab, void* out, int64_t out_stride, int dim, void* stream);
 
+/* (f)2 / B9 — the decode step's bf16 embedding gather and its first RMSNorm in
+ * one launch (F.embedding, fastdms/layers/embed_head.py:87-104, then the first
+ * decoder layer's input_layernorm without residual, layernorm.py:16-28):
+ * rows_out[i, :] = table[ids[i], :] (the first residual, contiguous rows:
+ * rows_stride == hidden) and out[i, :] = RMSNorm(rows_out[i, :]) with
+ * `weight` / `eps`, bit-identical to fdms_rmsnorm of the gathered rows.  An id
+ * outside [0, vocab) gives NaN rows in both.  hidden % 8 == 0, 16-byte
+ * aligned rows. */
+int fdms_embedding_rmsnorm(const int64_t* ids, int64_t n, const void* table, int64_t table_stride, int64_t vocab,
+                           const void* weight, float eps, void* out, int64_t out_stride, void* rows_out,
+                           int64_t rows_stride, int hidden, void* stream);
+
 /* RMSNorm (+ residual) whose input row r is bf16(sum over s < k_splits of
  * partials[s * split_stride + r * hidden + c]) in split order: the merge of a
  * split-K fdms_linear_small_m (epilogue 3) done by its consumer, as the

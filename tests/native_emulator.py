@@ -944,6 +944,24 @@ class Emulator:
         self._store_row_amax(amax_out, o, q_out, q_stride, q_mode)
         return 0
 
+    def embedding_rmsnorm(self, ids, n, table, t_s, vocab, weight, eps, out, o_s, rows_out, r_s, hidden, stream):
+        """rows_out = table[ids] (NaN rows for ids outside the table), out = their RMSNorm."""
+        if n < 0 or hidden <= 0 or hidden % 8 or vocab <= 0 or r_s != hidden or t_s < hidden or o_s < hidden:
+            return 1
+        if n == 0:
+            return 0
+        idv = self.view(ids, torch.int64, (n,), (1,), "ids")
+        ok = (idv >= 0) & (idv < vocab)
+        tab = self.view(table, torch.bfloat16, (vocab, hidden), (t_s, 1), "table")
+        f = tab[torch.where(ok, idv, torch.zeros_like(idv))].float()
+        f[~ok] = float("nan")
+        self.view(rows_out, torch.bfloat16, (n, hidden), (r_s, 1), "rows_out").copy_(f.to(torch.bfloat16))
+        w = self.view(weight, torch.bfloat16, (hidden,), (1,), "weight").float()
+        inv = torch.rsqrt((f * f).sum(-1, keepdim=True) / hidden + eps)
+        o = ((f * inv).to(torch.bfloat16).float() * w).to(torch.bfloat16)
+        self.view(out, torch.bfloat16, (n, hidden), (o_s, 1), "out").copy_(o)
+        return 0
+
     def embedding_fp8(self, ids, n, table, t_s, scale_inv, vocab, out, o_s, dim, stream):
         """bf16(bf16(e4m3fn row) * bf16(scale_inv)), NaN rows for ids outside [0, vocab)."""
         if n < 0 or dim <= 0 or dim % 8 or vocab <= 0 or t_s < dim or o_s < dim:

@@ -130,6 +130,37 @@ def test_fp8_embedding_gather_matches_the_oracle(vocab, dim, n):
     assert torch.equal(y[0], emb(torch.tensor([3], device="cuda")).cpu()[0])
 
 
+@pytest.mark.parametrize("vocab,hidden,n", [(128256, 2048, 8), (151936, 4096, 8), (1000, 264, 37)])
+def test_embedding_rms_norm_equals_gather_then_rmsnorm(vocab, hidden, n):
+    """fdms_embedding_rmsnorm (the decode step's bf16 gather + first
+    input_layernorm in one launch): the gathered rows equal F.embedding bit for
+    bit, the normalised rows equal fdms_rmsnorm of them bit for bit (the same
+    kernel) and the oracle's RMSNorm (layernorm.py:16-28) within one bf16 ulp;
+    ids outside the table give NaN rows in both outputs."""
+    require_gpu()
+    from fastdms_amd.layers.embed_head import embedding_rms_norm
+    from fastdms_amd.layers.layernorm import rms_norm
+    g = torch.Generator().manual_seed(vocab + n)
+    table = (torch.randn((vocab, hidden), generator=g) * 0.5).to(torch.bfloat16).cuda()
+    w = (1.0 + 0.2 * torch.randn(hidden, generator=g)).to(torch.bfloat16).cuda()
+    ids = torch.randint(0, vocab, (n,), generator=g).cuda()
+    h, rows = embedding_rms_norm(ids, table, w, 1e-5)
+    want_rows = torch.nn.functional.embedding(ids, table)
+    want_h = rms_norm(want_rows, w, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(rows, want_rows)
+    assert torch.equal(h, want_h)
+    ref, _ = _rms_ref(want_rows.cpu(), w.cpu(), 1e-5)
+    _ulp_close(h, ref, "embedding rmsnorm")
+    bad = ids.clone()
+    bad[0], bad[-1] = -1, vocab
+    h2, rows2 = embedding_rms_norm(bad, table, w, 1e-5)
+    torch.cuda.synchronize()
+    for t in (h2, rows2):
+        assert torch.isnan(t[0].float()).all() and torch.isnan(t[-1].float()).all()
+        assert torch.equal(t[1:-1], (h if t is h2 else rows)[1:-1])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_argmax_rows_matches_torch(dtype):
     """Lowest index on ties; NaN wins (torch.argmax semantics), so the id is
