@@ -944,7 +944,8 @@ FDMS_EXPORT int fdms_linear_small_m(const void* x, int64_t x_stride, int m, int 
   if (epilogue == 3 && (prologue != 0 || bias || !workspace)) return (int)hipErrorInvalidValue;
   // prologue 2: fp32 rows f and their producer's per-strip sums of f^2 in x_amax
   const bool stats_in = prologue == 2;
-  if (stats_in && (x_dtype != kF32 || quantize_x != 0 || !x_amax || x_amax_n < 1 ||
+  // (one sum per 16-column producer strip: x_amax_n = k / 16, all summed into the norm)
+  if (stats_in && (x_dtype != kF32 || quantize_x != 0 || !x_amax || x_amax_n != k / 16 || k % 16 ||
                    (m > 1 && x_amax_stride < x_amax_n) || epilogue > 1))
     return (int)hipErrorInvalidValue;
   // the producer's row amax replaces the activation statistics pass (no prologue)

@@ -179,9 +179,10 @@ def linear_residual_stats(x: torch.Tensor, weight: torch.Tensor, residual: torch
     if not small_m_supported(rows, k, n):
         raise ValueError(f"linear_residual_stats does not support rows={rows}, K={k}, N={n}")
     strips = n // 16
+    # the kernel writes ssq_out[row * strips + strip]: exactly [rows, N/16]
     if (residual.dtype != torch.bfloat16 or residual.shape != (rows, n) or residual.stride(1) != 1
             or f_out.dtype != torch.float32 or f_out.shape != (rows, n) or f_out.stride(1) != 1
-            or ssq_out.dtype != torch.float32 or not ssq_out.is_contiguous() or ssq_out.numel() < rows * strips):
+            or ssq_out.dtype != torch.float32 or not ssq_out.is_contiguous() or ssq_out.shape != (rows, strips)):
         raise ValueError("linear_residual_stats: residual bf16 [rows, N], f_out fp32 [rows, N], "
                          "ssq_out contiguous fp32 [rows, N/16]")
     if k_splits is None:
@@ -217,8 +218,10 @@ def linear_norm_stats(f: torch.Tensor, ssq: torch.Tensor, norm_weight: torch.Ten
     fp8 = weight.dtype == torch.float8_e4m3fn
     if f.dtype != torch.float32 or f.stride(-1) != 1 or f.shape[1] != k:
         raise ValueError("linear_norm_stats expects fp32 rows [rows, K] with a contiguous last axis")
-    if ssq.dtype != torch.float32 or ssq.dim() != 2 or ssq.shape[0] < rows or ssq.stride(1) != 1:
-        raise ValueError("ssq must be fp32 [rows, strips] with a contiguous last axis")
+    # every column of ssq is summed into the row's norm: one per producer strip (K / 16)
+    if (ssq.dtype != torch.float32 or ssq.dim() != 2 or ssq.shape[0] < rows or ssq.shape[1] != k // 16
+            or ssq.stride(1) != 1):
+        raise ValueError("ssq must be fp32 [rows, K/16] (the producer's strip sums) with a contiguous last axis")
     if (weight.dtype != torch.bfloat16 and not fp8) or (fp8 and weight_scale_inv is None):
         raise ValueError("linear_norm_stats expects bf16 weights, or FP8 with weight_scale_inv")
     if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != k or not norm_weight.is_contiguous():

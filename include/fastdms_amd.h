@@ -382,8 +382,8 @@ int fdms_quantize_fp8_rows(const void* in, int in_dtype, int64_t in_stride, int6
  * residual_out = bf16(f) (it may be residual itself: updated in place), and
  * amax_out[row * (n/16) + strip] = the strip's sum of f^2.  prologue 2 (x_dtype
  * F32, quantize_x 0, epilogues 0 / 1) = that RMSNorm applied as x is loaded:
- * x holds f (fp32 rows, x_stride in floats), x_amax [m, x_amax_n] the producer
- * strips' sums of f^2 (x_amax_stride per row), norm_weight the norm's weight;
+ * x holds f (fp32 rows, x_stride in floats), x_amax [m, x_amax_n = k/16] the
+ * producer strips' sums of f^2 (x_amax_stride per row), norm_weight the norm's weight;
  * a = bf16(bf16(f * rsqrt(sum / k + eps)) * norm_weight).  k_splits > 1 splits K over
  * workgroups: workspace holds (n_out/16) * k_splits * 256 floats (x2 for
  * epilogue 1) and counters n_out/16 ints, zero before the first call and left

@@ -1033,7 +1033,7 @@ class Emulator:
         if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or prologue not in (0, 1, 2) or epilogue == 2:
             return 1
         stats_in, stats_out = prologue == 2, epilogue == 4
-        if stats_in and (x_dtype != DT_F32 or qx or not x_amax or x_amax_n < 1 or epilogue > 1):
+        if stats_in and (x_dtype != DT_F32 or qx or not x_amax or x_amax_n != k // 16 or k % 16 or epilogue > 1):
             return 1
         if stats_out and (prologue or qx or not res or not res_out or not amax_out):
             return 1

@@ -34,6 +34,14 @@ def test_rejected_arguments_return_invalid_value_without_launching():
     # unaligned / odd-sized copy and a bad dtype code are rejected before any launch
     assert lib.fdms_copy_bytes(None, None, 15, 1, None) == 1
     assert lib.fdms_convert(ctypes.c_void_p(16), 9, ctypes.c_void_p(16), 0, 4, None) == 1
+    # the norm prologue (2) sums one statistic per 16-column producer strip:
+    # x_amax_n must be k / 16 (here k = 2048: 128), 127 and 129 are rejected
+    # (distinct aligned addresses, never dereferenced: every other argument is valid)
+    x, w, nw, y, st = (ctypes.c_void_p(i << 12) for i in range(1, 6))
+    for bad_n in (127, 129):
+        assert lib.fdms_linear_small_m(x, 2048, 8, 2048, w, _native.DT_BF16, 2048, None, None, 4096, 2, nw, 1e-5,
+                                       None, 0, None, 0, 0, 0, 1, None, None, y, 4096, st, bad_n, 128, None,
+                                       None, _native.DT_F32, None) == 1
 
 
 def _integration_python_blocks():

@@ -150,3 +150,26 @@ def test_convert_linear_modules_scope(monkeypatch):
     monkeypatch.setenv("FASTDMS_FP8_ATTENTION_ROW1_SHADOW", "0")
     monkeypatch.setenv("FASTDMS_FP8_WEIGHT_SCOPE", "mlp_down")
     assert L.convert_linear_modules_to_fp8(root) == 1 and calls[0][0] == "layers.0.mlp.down_proj"
+
+
+def test_norm_stats_buffers_must_match_the_strips():
+    """The split RMSNorm's statistics buffer is exactly [rows, N / 16]: the
+    producer writes row * strips + strip and the consumer sums every column
+    of its row into the norm, so a wider buffer is rejected before any launch
+    (CPU tensors: the shape checks come first)."""
+    from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_norm_stats, linear_residual_stats
+    rows, k, n = 8, 2048, 4096
+    x = torch.zeros(rows, k, dtype=torch.bfloat16)
+    w = torch.zeros(n, k, dtype=torch.bfloat16)
+    res = torch.zeros(rows, n, dtype=torch.bfloat16)
+    f = torch.zeros(rows, n)
+    with pytest.raises(ValueError, match="ssq_out"):
+        linear_residual_stats(x, w, res, f, torch.zeros(rows, n // 16 + 16))
+    with pytest.raises(ValueError, match="ssq_out"):
+        linear_residual_stats(x, w, res, f, torch.zeros(rows * n // 16 + 64))
+    nw = torch.ones(n, dtype=torch.bfloat16)
+    w2 = torch.zeros(2 * 1024, n, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ssq must be"):
+        linear_norm_stats(f, torch.zeros(rows, n // 16 + 1), nw, 1e-5, w2, epilogue=EPI_SILU_MUL)
+    with pytest.raises(ValueError, match="ssq must be"):
+        linear_norm_stats(f, torch.zeros(rows, n // 32), nw, 1e-5, w2, epilogue=EPI_SILU_MUL)
