@@ -101,11 +101,16 @@ class ModelRunner:
                                                   (hf.num_attention_heads + 2 * hf.num_key_value_heads) * hf.head_dim))
         self.evict_buffer = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads),
                                         device=self.device, dtype=torch.bool)
-        self.static_input_ids = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
         self.static_positions = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
         self.static_slot = torch.zeros((self.num_layers, self.max_num_seqs, self.num_kv_heads), device=self.device,
                                        dtype=torch.int32)
-        self.static_tokens = torch.zeros(self.max_num_seqs, device=self.device, dtype=torch.int64)
+        # a decode step's input ids and, at its end, its greedy ids (the next
+        # step's input when the device feeds it); one more int64 after them
+        # holds the page pool's overflow flag, so one copy reads both back
+        self._readback = torch.zeros(self.max_num_seqs + 1, device=self.device, dtype=torch.int64)
+        self.static_tokens = self._readback[:self.max_num_seqs]
+        if self.compact_kv_manager.paged:
+            self.compact_kv_manager.bind_overflow(self._readback[self.max_num_seqs:].view(torch.int32)[:1])
         # the paged decode step's attention work plan (static: captured graphs keep its address)
         self.decode_plan = (DecodePlan(self.device, self.num_layers, self.max_num_seqs * self.num_kv_heads,
                                        config.max_model_len + 1, hf.head_dim)
@@ -115,7 +120,7 @@ class ModelRunner:
         self.pinned_pos = torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True)
         # decode lookahead (run_decode): two pinned sets each for the sampled
         # ids read back and the positions sent, alternating per staged step
-        self._tok_ring = [torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True) for _ in range(2)]
+        self._tok_ring = [torch.zeros(self.max_num_seqs + 1, dtype=torch.int64, pin_memory=True) for _ in range(2)]
         self._pos_ring = [torch.zeros(self.max_num_seqs, dtype=torch.int64, pin_memory=True) for _ in range(2)]
         self._ring = 0
         self._lookahead: dict | None = None  # the decode step in flight ahead of the host
@@ -318,7 +323,7 @@ class ModelRunner:
                     compact_live_counts=live, compact_slot_mapping=slot, compact_max_live_count=max_live_hint,
                     dms_capture_enabled=True, dms_alpha_scale=md.alpha_scale, dms_alpha_offset=md.alpha_offset,
                     dms_layer_evictions_buffer=evict, compact_plan=plan)
-        ids = self.static_input_ids[:batch]
+        ids = self.static_tokens[:batch]  # read before the step's own ids overwrite them
         pos = self.static_positions[:batch]
         logits = None
         if self.model.decode_fused_supported(batch):
@@ -407,13 +412,15 @@ class ModelRunner:
         return self._lookahead is not None
 
     def _stage_tokens(self, batch: int):
-        """Queue the copies of the step's page-pool overflow flag and sampled
-        ids to pinned memory; return (id buffer, event marking both done)."""
-        if self.compact_kv_manager.paged:
-            self.compact_kv_manager.stage_overflow_check()
+        """Queue the copy of the step's sampled ids (and, paged, the page
+        pool's overflow flag after them: one copy) to pinned memory; return
+        (that buffer, event marking it done)."""
         buf = self._tok_ring[self._ring]
         self._ring ^= 1
-        buf[:batch].copy_(self.static_tokens[:batch], non_blocking=True)
+        if self.compact_kv_manager.paged:
+            buf.copy_(self._readback, non_blocking=True)
+        else:
+            buf[:batch].copy_(self.static_tokens[:batch], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
         return buf, ev
@@ -454,7 +461,7 @@ class ModelRunner:
             for i, seq in enumerate(seqs):
                 self.pinned_ids[i] = seq.last_token
                 self.pinned_pos[i] = positions[i]
-            self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+            self.static_tokens[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
             self.static_positions[:batch].copy_(self.pinned_pos[:batch], non_blocking=True)
             self._replay_decode(start, batch, hint)
             self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs))
@@ -466,7 +473,7 @@ class ModelRunner:
             for i, p in enumerate(positions):
                 pos[i] = p
             self.static_positions[:batch].copy_(pos[:batch], non_blocking=True)
-            self.static_input_ids[:batch].copy_(self.static_tokens[:batch])  # the ids of the step in flight
+            # its input ids are the step in flight's greedy ids, already in static_tokens
             self._replay_decode(start, batch, hint)
             self.compact_live_tokens_peak = max(self.compact_live_tokens_peak, mgr.max_live_upper_bound(seqs) + 1)
             nhost, nev = self._stage_tokens(batch)
@@ -474,7 +481,7 @@ class ModelRunner:
         done.synchronize()
         out = host[:batch].tolist()
         if mgr.paged:
-            mgr.check_overflow(sync=False)
+            mgr.raise_if_overflow(int(host[self.max_num_seqs:].view(torch.int32)[0]))
         return out
 
     @torch.inference_mode()
@@ -509,14 +516,12 @@ class ModelRunner:
                                  pin_memory=True)
         for i, seq in enumerate(seqs):
             self.pinned_ids[i] = seq.last_token
-        self.static_input_ids[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
+        self.static_tokens[:batch].copy_(self.pinned_ids[:batch], non_blocking=True)
         tokens = torch.empty((max_steps, batch), device=self.device, dtype=torch.int64)
         for step in range(max_steps):
             start, hint = self._begin_decode_step(seqs, pos_table[step].tolist())
             self.static_positions[:batch].copy_(pos_table[step], non_blocking=True)
-            if step:
-                self.static_input_ids[:batch].copy_(self.static_tokens[:batch])
-            self._replay_decode(start, batch, hint)
+            self._replay_decode(start, batch, hint)  # its input ids: the previous step's, in static_tokens
             tokens[step].copy_(self.static_tokens[:batch])
         if mgr.paged:
             mgr.stage_overflow_check()

@@ -179,6 +179,20 @@ class PagedCompactKVManager(CompactKVManager):
             b.sync_pages, b.appended, b.packed = int(self._prefill_pages_host[i]), 0, True
         self._prefill_check = []
 
+    def bind_overflow(self, flag: torch.Tensor) -> None:
+        """Keep the overflow flag in ``flag`` (int32 [1] on this device), e.g.
+        beside the decode step's sampled ids so that one copy reads both back.
+        Before any launch that records ``self.overflow`` (graph capture)."""
+        if flag.dtype != torch.int32 or flag.numel() != 1 or flag.device != self.overflow.device:
+            raise ValueError("the overflow flag must be one int32 on the pool's device")
+        flag.copy_(self.overflow)
+        self.overflow = flag
+
+    def raise_if_overflow(self, flag: int) -> None:
+        """check_overflow on a flag value the caller read back itself."""
+        if flag:
+            raise RuntimeError("paged compact KV: a page pop found the pool empty (host page accounting failed)")
+
     def stage_overflow_check(self) -> None:
         """Queue a copy of the device overflow flag into pinned memory (read by
         check_overflow after the caller's next host sync)."""
