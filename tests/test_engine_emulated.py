@@ -317,3 +317,31 @@ def test_chunked_prefill_state_equals_the_unchunked_state():
     assert torch.equal(lc, lu) and tc == tu
     for (kc, vc, pc), (ku, vu, pu) in zip(rc, ru):
         assert torch.equal(kc, ku) and torch.equal(vc, vu) and torch.equal(pc, pu)
+
+
+@pytest.mark.parametrize("lookahead", [False, True])
+def test_decode_step_reports_a_page_pool_overflow(monkeypatch, lookahead):
+    """The page pool's overflow flag reaches the host with the step's token ids
+    (one read-back): a flag the device set (here by hand, as a failed page pop
+    would) makes the decode step raise, with and without the lookahead.  Set
+    between steps, the flag travels with the next step launched; with the
+    lookahead that step is already in flight with its read-back queued, so
+    the raise comes one step later."""
+    if not lookahead:
+        monkeypatch.setenv("FASTDMS_AMD_DECODE_LOOKAHEAD", "0")
+    with cpu_engine():
+        from fastdms_amd import LLM, SamplingParams
+        llm = LLM("tiny-llama", max_model_len=2048, max_num_seqs=8, max_num_batched_tokens=16384,
+                  enforce_eager=True, fused_greedy_head=True, compact_kv_layout="paged", **DMS)
+        mgr = llm.model_runner.compact_kv_manager
+        rng = np.random.default_rng(5)
+        sp = SamplingParams(temperature=0.0, max_tokens=6, ignore_eos=True)
+        for n in (80, 120):
+            llm.add_request(rng.integers(0, 512, n).tolist(), sp)
+        llm.step()  # prefill
+        llm.step()  # a clean decode step
+        mgr.overflow.fill_(1)
+        if lookahead:
+            llm.step()  # the step in flight: its read-back was queued before the flag was set
+        with pytest.raises(RuntimeError, match="pool empty"):
+            llm.step()
