@@ -55,8 +55,8 @@ SIGNATURES: dict[str, str] = {
     "fdms_quantize_fp8_rows": "pilliplpip",
     "fdms_linear_small_m": "pliipilppiipfplpliiippplpilppip",
     "fdms_linear_argmax_small_m": "pliipilppiiiipppppp",
-    "fdms_linear_int4_small_m": "pliiplppilpiiipppppplp",
-    "fdms_quantize_int4_groups": "pilliiiplpplp",
+    "fdms_linear_int4_small_m": "pliiplpilpiiipppppplp",
+    "fdms_quantize_int4_groups": "pilliiiplplp",
     "fdms_fp8_rerank_topk": "pliiplpipipp",
     "fdms_paged_pack_prepare": "pllpiiiipllplllpppllllippppllpllipp",
     "fdms_paged_pack_scatter": "ppillllpllpiplllppilpppllllllplliiiiippp",

@@ -79,13 +79,12 @@ template <typename WT> struct WBlock;
 // bf16 weights: a lane group reads 16 bf16 = 32 B per k-block
 template <> struct WBlock<bf16_t> {
   struct Raw { uint4 v[2]; };
-  static constexpr bool kGrouped = false;
   static __device__ __forceinline__ void load(const bf16_t* row, int k, Raw& r) {
     const uint4* p = reinterpret_cast<const uint4*>(row + k);
     r.v[0] = p[0];
     r.v[1] = p[1];
   }
-  static __device__ __forceinline__ void to_ops(const Raw& r, float, float, uint4* op0, uint4* op1) {
+  static __device__ __forceinline__ void to_ops(const Raw& r, uint4* op0, uint4* op1) {
     *op0 = r.v[0];
     *op1 = r.v[1];
   }
@@ -93,11 +92,10 @@ template <> struct WBlock<bf16_t> {
 // FP8 weights: 16 fp8 = 16 B per k-block, converted to two bf16x8 operands
 template <> struct WBlock<fp8_t> {
   using Raw = uint4;
-  static constexpr bool kGrouped = false;
   static __device__ __forceinline__ void load(const fp8_t* row, int k, Raw& r) {
     r = *reinterpret_cast<const uint4*>(row + k);
   }
-  static __device__ __forceinline__ void to_ops(const Raw& r, float, float, uint4* op0, uint4* op1) {
+  static __device__ __forceinline__ void to_ops(const Raw& r, uint4* op0, uint4* op1) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
     uint32_t o[8];
 #pragma unroll
@@ -111,30 +109,10 @@ template <> struct WBlock<fp8_t> {
     *op1 = uint4{o[4], o[5], o[6], o[7]};
   }
 };
-// INT4 weights: byte j of a row holds k = 2j (low nibble) and 2j + 1 (high);
-// 16 k = 8 B per k-block; w = bf16((q - 8) * scale + zero) with the bf16
-// scale / zero of the k-block's group (linear.py:436-458, 462-478).
-template <> struct WBlock<u4x2_t> {
-  using Raw = uint2;
-  static constexpr bool kGrouped = true;
-  static __device__ __forceinline__ void load(const u4x2_t* row, int k, Raw& r) {
-    r = *reinterpret_cast<const uint2*>(row + k / 2);
-  }
-  static __device__ __forceinline__ void to_ops(const Raw& r, float s, float z, uint4* op0, uint4* op1) {
-    const uint32_t w[2] = {r.x, r.y};
-    uint32_t o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t word = w[i >> 2];
-      const int sh = (i & 3) * 8;
-      const float lo = (float)((int)((word >> sh) & 0xFu) - 8) * s + z;
-      const float hi = (float)((int)((word >> (sh + 4)) & 0xFu) - 8) * s + z;
-      o[i] = pack2(lo, hi);
-    }
-    *op0 = uint4{o[0], o[1], o[2], o[3]};
-    *op1 = uint4{o[4], o[5], o[6], o[7]};
-  }
-};
+// the generic path's per-k-block weight registers (INT4 weights take the
+// 128-column path, which keeps its codes in Buf::w4)
+template <typename WT> struct WRaw { using type = typename WBlock<WT>::Raw; };
+template <> struct WRaw<u4x2_t> { using type = uint32_t; };
 
 template <typename WT> __device__ __forceinline__ constexpr bool is_fp8() { return false; }
 template <> __device__ __forceinline__ constexpr bool is_fp8<fp8_t>() { return true; }
@@ -253,7 +231,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     float eps, const bf16_t* res, int64_t res_s, bf16_t* res_out, int64_t ro_s,
     bf16_t* __restrict__ y, int64_t y_s, int n_out, int strips, int ksplit, float* __restrict__ ws,
     int* __restrict__ counters, float* __restrict__ part_val, int* __restrict__ part_idx,
-    const bf16_t* __restrict__ g_scale, const bf16_t* __restrict__ g_zero, int group, int64_t g_s, int qx_torch,
+    const uint32_t* __restrict__ g_sz, int group, int64_t g_s, int qx_torch,
     int bf16_scores, const float* __restrict__ x_amax, int x_amax_n, int64_t x_amax_s, float* __restrict__ amax_out,
     float* __restrict__ row_scale_out) {
   constexpr int NA = EPI == 1 ? 2 : 1;  // accumulators (strips) per workgroup
@@ -265,7 +243,13 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   // XQ: x already holds the e4m3fn codes of the quantised activation (its
   // producer quantised it with the row amax it hands over in x_amax)
   static_assert(!XQ || F8, "a pre-quantised activation needs FP8 weights");
-  constexpr int KB = F8 ? 2 * kKB : kKB;
+  // INT4 weights use the same 128-column k-blocks: lane group g reads 16
+  // bytes (32 codes) of its row for columns 32g .. 32g + 31 -- one group of
+  // the scale_zeros layout (group >= 32) -- and dequantises them into four
+  // bf16 operands for v_mfma_f32_16x16x32_bf16 (MFMA j: columns 32g + 8j ..)
+  constexpr bool I4 = is_int4<WT>();
+  static_assert(!I4 || (PRO == 0 && !QX), "INT4 weights take bf16 activations, no prologue");
+  constexpr int KB = (F8 || I4) ? 2 * kKB : kKB;
   __shared__ float s_inv[kMaxM], s_xs[kMaxM];
   __shared__ f32x4 s_acc[NA][NW][64];
   __shared__ int s_last;
@@ -320,18 +304,44 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
   float fq_inv[kFChunks];  // PRO 2: inv of rows fq_row + kRq * t (set after the statistics)
 
   struct Buf {
-    typename WBlock<WT>::Raw w[NA][U];
-    float gs[NA][U], gz[NA][U];  // INT4 group scale / zero
+    typename WRaw<WT>::type w[NA][U];
+    uint32_t gsz[NA][U];  // I4: the group's (scale, zero) as two bf16
     uint4 x[U][2];
     uint4 r[U][2];   // residual (PRO 1)
     uint4 nw[U][2];  // norm weight (PRO 1)
     uint4 fch[kFChunks];  // PRO 2: the group's fp32 rows, this lane's chunks
     uint2 fnw;            // PRO 2: norm weight of this lane's four columns
     uint4 w8[NA][U][2];  // F8: 32 weight bytes per lane per k-block
-    uint4 x8[U][4];      // F8: 32 bf16 activations per lane per k-block
+    uint4 x8[U][4];      // F8 / I4: 32 bf16 activations per lane per k-block
+    uint4 w4[NA][U];     // I4: 32 weight codes per lane per k-block
   };
   auto load = [&](int kb0, Buf& b) {
-    if constexpr (F8) {
+    if constexpr (I4) {
+      // activation chunks first (from L2), then codes and (scale, zero);
+      // a last half block's lane groups 2 and 3 read clamped columns that
+      // compute zeroes
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB < kend) {
+          const int kl = min(kb0 + u * KB + 32 * g, kend - 32);
+          const uint4* xp = reinterpret_cast<const uint4*>(xrow + kl);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) b.x8[u][i] = xp[i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB < kend) {
+          const int kl = min(kb0 + u * KB + 32 * g, kend - 32);
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            b.w4[a][u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(wrow[a]) + kl / 2);
+            // group kl / group of weight row n: consecutive lanes read consecutive rows
+            b.gsz[a][u] = g_sz[(int64_t)(kl / group) * g_s + (n0 + c + (a ? n_out : 0))];
+          }
+        }
+      }
+    } else if constexpr (F8) {
       // the group's activation loads go out before its weight loads: loads
       // complete in issue order, so the activation (from L2) is quantised
       // while the weights are still on their way from HBM.  Branch-free: a
@@ -365,43 +375,38 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
           }
         }
       }
-      return;
-    }
-    if constexpr (PRO == 2) {
-      // chunks of rows < M only (uniform per t: rows fq_row + kRq t, clamped)
-      const int col = min(kb0 + fq_col, kend - 4);
+    } else {
+      if constexpr (PRO == 2) {
+        // chunks of rows < M only (uniform per t: rows fq_row + kRq t, clamped)
+        const int col = min(kb0 + fq_col, kend - 4);
 #pragma unroll
-      for (int t = 0; t < kFChunks; ++t)
-        if (kRq * t < M)
-          b.fch[t] = *reinterpret_cast<const uint4*>(frow0 + (int64_t)min(fq_row + kRq * t, M - 1) * x_s + col);
-      b.fnw = *reinterpret_cast<const uint2*>(norm_w + col);
-    }
+        for (int t = 0; t < kFChunks; ++t)
+          if (kRq * t < M)
+            b.fch[t] = *reinterpret_cast<const uint4*>(frow0 + (int64_t)min(fq_row + kRq * t, M - 1) * x_s + col);
+        b.fnw = *reinterpret_cast<const uint2*>(norm_w + col);
+      }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = kb0 + u * kKB + 16 * g;
-      if (kb0 + u * kKB < kend) {
+      for (int u = 0; u < U; ++u) {
+        const int k = kb0 + u * kKB + 16 * g;
+        if (kb0 + u * kKB < kend) {
 #pragma unroll
-        for (int a = 0; a < NA; ++a) {
-          WBlock<WT>::load(wrow[a], k, b.w[a][u]);
-          if (WBlock<WT>::kGrouped) {
-            const int64_t gi = (int64_t)(n0 + c + (a ? n_out : 0)) * g_s + k / group;
-            b.gs[a][u] = ld<bf16_t>(g_scale + gi);
-            b.gz[a][u] = ld<bf16_t>(g_zero + gi);
+          for (int a = 0; a < NA; ++a) {
+            WBlock<WT>::load(wrow[a], k, b.w[a][u]);
           }
-        }
-        b.x[u][0] = b.x[u][1] = b.r[u][0] = b.r[u][1] = uint4{0u, 0u, 0u, 0u};
-        if (PRO != 2 && has_row) {
-          const uint4* xp = reinterpret_cast<const uint4*>(xrow + k);
-          b.x[u][0] = xp[0];
-          b.x[u][1] = xp[1];
-          if (PRO == 1) {
-            const uint4* np = reinterpret_cast<const uint4*>(norm_w + k);
-            b.nw[u][0] = np[0];
-            b.nw[u][1] = np[1];
-            if (rrow) {
-              const uint4* rp = reinterpret_cast<const uint4*>(rrow + k);
-              b.r[u][0] = rp[0];
-              b.r[u][1] = rp[1];
+          b.x[u][0] = b.x[u][1] = b.r[u][0] = b.r[u][1] = uint4{0u, 0u, 0u, 0u};
+          if (PRO != 2 && has_row) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xrow + k);
+            b.x[u][0] = xp[0];
+            b.x[u][1] = xp[1];
+            if (PRO == 1) {
+              const uint4* np = reinterpret_cast<const uint4*>(norm_w + k);
+              b.nw[u][0] = np[0];
+              b.nw[u][1] = np[1];
+              if (rrow) {
+                const uint4* rp = reinterpret_cast<const uint4*>(rrow + k);
+                b.r[u][0] = rp[0];
+                b.r[u][1] = rp[1];
+              }
             }
           }
         }
@@ -409,7 +414,38 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
     }
   };
   auto compute = [&](int kb0, const Buf& b) {
-    if constexpr (F8) {
+    if constexpr (I4) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * KB >= kend) break;
+        const bool xv = kb0 + u * KB + 32 * g < kend && has_row;  // this lane group's columns and row exist
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          // w = bf16((q - 8) * s + z) as one fma of the code: q * s + (z - 8s)
+          // (z - 8s exact for the symmetric zero 0); each byte of the masked
+          // word converts in one v_cvt_f32_ubyte, the high nibbles as 16q
+          // (with s / 16)
+          const float sc = bf_lo(b.gsz[a][u]), zc = bf_hi(b.gsz[a][u]);
+          const float c8 = __builtin_fmaf(-8.0f, sc, zc), s16 = sc * 0.0625f;
+          const uint32_t wd[4] = {b.w4[a][u].x, b.w4[a][u].y, b.w4[a][u].z, b.w4[a][u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = wd[j] & 0xF0F0F0F0u;
+            const uint4 aw = uint4{
+                pack2(__builtin_fmaf((float)(lo & 0xFFu), sc, c8),
+                      __builtin_fmaf((float)(hi & 0xFFu), s16, c8)),
+                pack2(__builtin_fmaf((float)((lo >> 8) & 0xFFu), sc, c8),
+                      __builtin_fmaf((float)((hi >> 8) & 0xFFu), s16, c8)),
+                pack2(__builtin_fmaf((float)((lo >> 16) & 0xFFu), sc, c8),
+                      __builtin_fmaf((float)((hi >> 16) & 0xFFu), s16, c8)),
+                pack2(__builtin_fmaf((float)((lo >> 24) & 0xFFu), sc, c8),
+                      __builtin_fmaf((float)((hi >> 24) & 0xFFu), s16, c8))};
+            const uint4 bx = xv ? b.x8[u][j] : uint4{0u, 0u, 0u, 0u};
+            acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aw), as_bf16x8(bx), acc[a], 0, 0, 0);
+          }
+        }
+      }
+    } else if constexpr (F8) {
       // every block's activation quantised first (it arrives before the
       // weights), then the MFMAs
       uint32_t qx[U][8];
@@ -460,73 +496,72 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
           acc[a] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aw, bx, acc[a], 0, 0, 0, 127, 0, 127);
         }
       }
-      return;
-    }
-    if constexpr (PRO == 2) {
-      // a = bf16(bf16(f * inv) * norm_w) of the group's rows into this wave's
-      // LDS slice (the previous group's reads are done: LDS runs a wave's
-      // instructions in order)
-      const float nwf[4] = {bf_lo(b.fnw.x), bf_hi(b.fnw.x), bf_lo(b.fnw.y), bf_hi(b.fnw.y)};
+    } else {
+      if constexpr (PRO == 2) {
+        // a = bf16(bf16(f * inv) * norm_w) of the group's rows into this wave's
+        // LDS slice (the previous group's reads are done: LDS runs a wave's
+        // instructions in order)
+        const float nwf[4] = {bf_lo(b.fnw.x), bf_hi(b.fnw.x), bf_lo(b.fnw.y), bf_hi(b.fnw.y)};
 #pragma unroll
-      for (int t = 0; t < kFChunks; ++t) {
-        const int row = fq_row + kRq * t;
-        if (kRq * t < M && row < M) {
-          const uint4 v = b.fch[t];
-          const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-          const float iv = fq_inv[t];
-          *reinterpret_cast<uint2*>(&s_act[wave][row][fq_col]) =
-              uint2{pack2(rbf(rbf(f[0] * iv) * nwf[0]), rbf(rbf(f[1] * iv) * nwf[1])),
-                    pack2(rbf(rbf(f[2] * iv) * nwf[2]), rbf(rbf(f[3] * iv) * nwf[3]))};
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (kb0 + u * kKB >= kend) break;
-      uint4 bo[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (PRO == 0 && !QX) {
-          bo[h] = b.x[u][h];
-        } else if (PRO == 2) {
-          bo[h] = has_row ? *reinterpret_cast<const uint4*>(&s_act[wave][c][u * kKB + 16 * g + 8 * h])
-                          : uint4{0u, 0u, 0u, 0u};
-        } else {
-          const uint32_t v[4] = {b.x[u][h].x, b.x[u][h].y, b.x[u][h].z, b.x[u][h].w};
-          const uint32_t q[4] = {b.nw[u][h].x, b.nw[u][h].y, b.nw[u][h].z, b.nw[u][h].w};
-          const uint32_t rs[4] = {b.r[u][h].x, b.r[u][h].y, b.r[u][h].z, b.r[u][h].w};
-          uint32_t o[4];
-          float f[8];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float lo = bf_lo(v[i]), hi = bf_hi(v[i]);
-            if (PRO == 1) {
-              lo = rbf(rbf((lo + bf_lo(rs[i])) * inv) * bf_lo(q[i]));
-              hi = rbf(rbf((hi + bf_hi(rs[i])) * inv) * bf_hi(q[i]));
-            }
-            f[2 * i] = lo;
-            f[2 * i + 1] = hi;
-            o[i] = pack2(lo, hi);
+        for (int t = 0; t < kFChunks; ++t) {
+          const int row = fq_row + kRq * t;
+          if (kRq * t < M && row < M) {
+            const uint4 v = b.fch[t];
+            const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+            const float iv = fq_inv[t];
+            *reinterpret_cast<uint2*>(&s_act[wave][row][fq_col]) =
+                uint2{pack2(rbf(rbf(f[0] * iv) * nwf[0]), rbf(rbf(f[1] * iv) * nwf[1])),
+                      pack2(rbf(rbf(f[2] * iv) * nwf[2]), rbf(rbf(f[3] * iv) * nwf[3]))};
           }
-          if (QX) {  // fp8 quantised activation (exact in bf16), four values per conversion
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-              const uint32_t q8 = f32x4_to_fp8x4(f[4 * i] * xsc, f[4 * i + 1] * xsc, f[4 * i + 2] * xsc,
-                                                 f[4 * i + 3] * xsc);
-              o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, false));
-              o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, true));
-            }
-          }
-          bo[h] = uint4{o[0], o[1], o[2], o[3]};
         }
       }
 #pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        uint4 a0, a1;
-        WBlock<WT>::to_ops(b.w[a][u], WBlock<WT>::kGrouped ? b.gs[a][u] : 0.0f,
-                           WBlock<WT>::kGrouped ? b.gz[a][u] : 0.0f, &a0, &a1);
-        acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(bo[0]), acc[a], 0, 0, 0);
-        acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(bo[1]), acc[a], 0, 0, 0);
+      for (int u = 0; u < U; ++u) {
+        if (kb0 + u * kKB >= kend) break;
+        uint4 bo[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (PRO == 0 && !QX) {
+            bo[h] = b.x[u][h];
+          } else if (PRO == 2) {
+            bo[h] = has_row ? *reinterpret_cast<const uint4*>(&s_act[wave][c][u * kKB + 16 * g + 8 * h])
+                            : uint4{0u, 0u, 0u, 0u};
+          } else {
+            const uint32_t v[4] = {b.x[u][h].x, b.x[u][h].y, b.x[u][h].z, b.x[u][h].w};
+            const uint32_t q[4] = {b.nw[u][h].x, b.nw[u][h].y, b.nw[u][h].z, b.nw[u][h].w};
+            const uint32_t rs[4] = {b.r[u][h].x, b.r[u][h].y, b.r[u][h].z, b.r[u][h].w};
+            uint32_t o[4];
+            float f[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float lo = bf_lo(v[i]), hi = bf_hi(v[i]);
+              if (PRO == 1) {
+                lo = rbf(rbf((lo + bf_lo(rs[i])) * inv) * bf_lo(q[i]));
+                hi = rbf(rbf((hi + bf_hi(rs[i])) * inv) * bf_hi(q[i]));
+              }
+              f[2 * i] = lo;
+              f[2 * i + 1] = hi;
+              o[i] = pack2(lo, hi);
+            }
+            if (QX) {  // fp8 quantised activation (exact in bf16), four values per conversion
+#pragma unroll
+              for (int i = 0; i < 2; ++i) {
+                const uint32_t q8 = f32x4_to_fp8x4(f[4 * i] * xsc, f[4 * i + 1] * xsc, f[4 * i + 2] * xsc,
+                                                   f[4 * i + 3] * xsc);
+                o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, false));
+                o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)q8, 1.0f, true));
+              }
+            }
+            bo[h] = uint4{o[0], o[1], o[2], o[3]};
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          uint4 a0, a1;
+          WBlock<WT>::to_ops(b.w[a][u], &a0, &a1);
+          acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(bo[0]), acc[a], 0, 0, 0);
+          acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(bo[1]), acc[a], 0, 0, 0);
+        }
       }
     }
   };
@@ -887,7 +922,7 @@ struct LinArgs {
   const bf16_t* x; int64_t x_s; int M, K; const void* w; int64_t w_s; const float* wsi; const bf16_t* bias;
   const bf16_t* norm_w; float eps; const bf16_t* res; int64_t res_s; bf16_t* res_out; int64_t ro_s;
   bf16_t* y; int64_t y_s; int n_out, strips, ksplit; float* ws; int* counters; float* pval; int* pidx;
-  const bf16_t* g_scale = nullptr; const bf16_t* g_zero = nullptr; int group = 1; int64_t g_s = 0;
+  const uint32_t* g_sz = nullptr; int group = 1; int64_t g_s = 0;
   int qx_torch = 0; int bf16_scores = 1;
   const float* x_amax = nullptr; int x_amax_n = 0; int64_t x_amax_s = 0; float* amax_out = nullptr;
   float* row_scale_out = nullptr;
@@ -899,10 +934,10 @@ void launch_linear(int nw, dim3 grid, hipStream_t st, const LinArgs& a) {
   // k-blocks per double-buffered group (register budget: the RMSNorm prologue
   // also holds the residual and norm weight of each k-block, the activation
   // statistics hold their loads while both first groups are in flight)
-  constexpr int U = (PRO == 1 || PRO == 2 || (QX && PRO == 0)) ? 2 : 4;
+  constexpr int U = (PRO == 1 || PRO == 2 || (QX && PRO == 0) || std::is_same_v<WT, u4x2_t>) ? 2 : 4;
 #define FDMS_LIN_ARGS a.x, a.x_s, a.M, a.K, w, a.w_s, a.wsi, a.bias, a.norm_w, a.eps, a.res, a.res_s, a.res_out, \
                       a.ro_s, a.y, a.y_s, a.n_out, a.strips, a.ksplit, a.ws, a.counters, a.pval, a.pidx, \
-                      a.g_scale, a.g_zero, a.group, a.g_s, a.qx_torch, a.bf16_scores, a.x_amax, a.x_amax_n, \
+                      a.g_sz, a.group, a.g_s, a.qx_torch, a.bf16_scores, a.x_amax, a.x_amax_n, \
                       a.x_amax_s, a.amax_out, a.row_scale_out
   if (nw == 8) {
     hipLaunchKernelGGL((linear_small_m_kernel<WT, PRO, QX, EPI, 8, U, XQ>), grid, dim3(512), 0, st, FDMS_LIN_ARGS);
@@ -1232,15 +1267,16 @@ FDMS_EXPORT int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, 
 // C5 — W4A16 decode linear: the small-M kernel with INT4 weights (no
 // activation quantisation or prologue; epilogue 0 plain, 1 SiLU*up, 2 greedy).
 FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
-                                         int64_t w_stride_bytes, const void* group_scale, const void* group_zero,
-                                         int group_size, int64_t g_stride, const void* bias, int n, int epilogue,
+                                         int64_t w_stride_bytes, const void* scale_zeros, int group_size,
+                                         int64_t sz_stride, const void* bias, int n, int epilogue,
                                          int k_splits, float* workspace, int* counters, float* part_val,
                                          int* part_idx, int64_t* out_tokens, void* y, int64_t y_stride,
                                          void* stream) {
   if (m < 0 || m > kMaxM || k <= 0 || n < 0 || epilogue < 0 || epilogue > 2) return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
-  if (!x || !w_packed || !group_scale || !group_zero) return (int)hipErrorInvalidValue;
-  if (group_size < 16 || (group_size & (group_size - 1)) || k % group_size || g_stride < k / group_size)
+  if (!x || !w_packed || !scale_zeros || ((uintptr_t)scale_zeros % 4)) return (int)hipErrorInvalidValue;
+  // a lane group's 32 columns of a 128-column k-block lie in one group
+  if (group_size < 32 || (group_size & (group_size - 1)) || k % group_size || sz_stride < n)
     return (int)hipErrorInvalidValue;
   if (epilogue == 2 ? (!part_val || !part_idx || !out_tokens) : !y) return (int)hipErrorInvalidValue;
   const int n_out = epilogue == 1 ? n / 2 : n;
@@ -1256,7 +1292,7 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
     if ((v == 4 || v == 8) && kc % (kKB * v) == 0) nw = v;
   }
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
-  if (((uintptr_t)x % 16) || ((uintptr_t)w_packed % 8) || (x_stride * 2) % 16 || w_stride_bytes % 8 ||
+  if (((uintptr_t)x % 16) || ((uintptr_t)w_packed % 16) || (x_stride * 2) % 16 || w_stride_bytes % 16 ||
       x_stride < k || w_stride_bytes * 2 < k || (epilogue != 2 && y_stride < n_out))
     return (int)hipErrorInvalidValue;
   if (y && (y == x)) return (int)hipErrorInvalidValue;
@@ -1266,10 +1302,9 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
   LinArgs a{(const bf16_t*)x, x_stride, m, k, w_packed, w_stride_bytes, nullptr, (const bf16_t*)bias, nullptr, 0.0f,
             nullptr, 0, nullptr, 0, (bf16_t*)y, y_stride, n_out, strips, k_splits, workspace, counters, part_val,
             part_idx};
-  a.g_scale = (const bf16_t*)group_scale;
-  a.g_zero = (const bf16_t*)group_zero;
+  a.g_sz = (const uint32_t*)scale_zeros;
   a.group = group_size;
-  a.g_s = g_stride;
+  a.g_s = sz_stride;
   const dim3 grid((unsigned)blocks);
   const hipStream_t st = (hipStream_t)stream;
   if (epilogue == 2) launch_linear<u4x2_t, 0, false, 2>(nw, grid, st, a);
@@ -1288,12 +1323,14 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
 // symmetric s = amax/7 (1 for a zero group), zero = 0, q = clamp(rint(w/s), -8, 7) + 8;
 // asymmetric s = (max-min)/15 (1 if flat), zero = min + 8s (min if flat),
 // q = clamp(rint((w - zero)/s + 8), 0, 15); q uses the fp32 scale / zero, the
-// stored scale / zero are rounded to bf16.  One wave per (row, group).
+// stored scale / zero are rounded to bf16 and written as the reference's
+// scale_zeros [groups, N, 2] (linear.py:461-464; sz_s pairs between groups).
+// One wave per (row, group).
 template <typename TI>
 __global__ __launch_bounds__(256) void quantize_int4_kernel(const TI* __restrict__ w, int64_t w_s, int k, int group,
                                                             int asym, uint8_t* __restrict__ out, int64_t out_s,
-                                                            bf16_t* __restrict__ scale, bf16_t* __restrict__ zero,
-                                                            int64_t g_s, int64_t total_groups) {
+                                                            uint32_t* __restrict__ sz, int64_t sz_s,
+                                                            int64_t total_groups) {
   const int64_t gid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (gid >= total_groups) return;
   const int lane = threadIdx.x & 63;
@@ -1338,19 +1375,16 @@ __global__ __launch_bounds__(256) void quantize_int4_kernel(const TI* __restrict
     }
     dst[j] = (uint8_t)(q[0] | (q[1] << 4));
   }
-  if (lane == 0) {
-    scale[row * g_s + gi].bits = (uint16_t)f32_to_bf16(s);
-    zero[row * g_s + gi].bits = (uint16_t)f32_to_bf16(z);
-  }
+  if (lane == 0) sz[(int64_t)gi * sz_s + row] = f32_to_bf16(s) | (f32_to_bf16(z) << 16);
 }
 
 FDMS_EXPORT int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int64_t rows, int k,
                                           int group_size, int asymmetric, void* out_packed, int64_t out_stride,
-                                          void* group_scale, void* group_zero, int64_t g_stride, void* stream) {
+                                          void* scale_zeros, int64_t sz_stride, void* stream) {
   if (rows < 0 || k <= 0 || group_size < 2 || group_size % 2 || k % group_size) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
-  if (!w || !out_packed || !group_scale || !group_zero || w_stride < k || out_stride * 2 < k ||
-      g_stride < k / group_size)
+  if (!w || !out_packed || !scale_zeros || ((uintptr_t)scale_zeros % 4) || w_stride < k || out_stride * 2 < k ||
+      sz_stride < rows)
     return (int)hipErrorInvalidValue;
   const int64_t total = rows * (k / group_size);
   const int64_t blocks = (total + 3) / 4;
@@ -1358,11 +1392,11 @@ FDMS_EXPORT int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_
   if (w_dtype == kBF16) {
     hipLaunchKernelGGL(quantize_int4_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const bf16_t*)w, w_stride, k, group_size, asymmetric, (uint8_t*)out_packed, out_stride,
-                       (bf16_t*)group_scale, (bf16_t*)group_zero, g_stride, total);
+                       (uint32_t*)scale_zeros, sz_stride, total);
   } else if (w_dtype == kF32) {
     hipLaunchKernelGGL(quantize_int4_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const float*)w, w_stride, k, group_size, asymmetric, (uint8_t*)out_packed, out_stride,
-                       (bf16_t*)group_scale, (bf16_t*)group_zero, g_stride, total);
+                       (uint32_t*)scale_zeros, sz_stride, total);
   } else {
     return (int)hipErrorInvalidValue;
   }

@@ -181,11 +181,11 @@ class ParallelLMHead(VocabParallelEmbedding, LinearBase):
         path, qx, bf16_scores = self.greedy_route(rows)
         fused = small_m_supported(rows, self.input_size, self.output_size)
         if path == "int4" and fused:
-            linear_int4_small_m(x2, self.weight_int4, self.weight_int4_scale, self.weight_int4_zero,
-                                self._int4_group_size, None, greedy=True, out=out)
+            linear_int4_small_m(x2, self.weight_int4, self.weight_int4_scale_zeros, self._int4_group_size, None,
+                                greedy=True, out=out)
         elif path == "int4_rerank":
-            logits = linear_int4_small_m(x2, self.weight_int4, self.weight_int4_scale, self.weight_int4_zero,
-                                         self._int4_group_size, None)
+            logits = linear_int4_small_m(x2, self.weight_int4, self.weight_int4_scale_zeros, self._int4_group_size,
+                                         None)
             cand = logits.topk(qe.int4_lm_head_rerank_topk(), dim=-1, sorted=False).indices
             fp8_rerank_topk(x2, cand, self.weight_fp8, self.weight_scale_inv, out=out)
         elif path == "fp8" and fused:

@@ -408,7 +408,8 @@ def linear_argmax_small_m(x: torch.Tensor, weight: torch.Tensor, bias: torch.Ten
 def quantize_int4_groups(w: torch.Tensor, group_size: int, mode: str = "symmetric"):
     """INT4 group quantisation of weight rows [N, K] (linear.py:414-459).
     Returns (packed [N, K/2] uint8: q[2j] low nibble, q[2j+1] high nibble,
-    scale [N, K/group] bf16, zero [N, K/group] bf16); dequant (q - 8) * scale + zero."""
+    scale_zeros [K/group, N, 2] bf16: the reference's layout, linear.py:461-464,
+    scale in [..., 0], zero in [..., 1]); dequant (q - 8) * scale + zero."""
     mode = mode.strip().lower()
     if mode not in {"sym", "symmetric", "asym", "asymmetric", "affine"}:
         raise ValueError("int4 quant_mode must be symmetric or asymmetric")
@@ -418,24 +419,27 @@ def quantize_int4_groups(w: torch.Tensor, group_size: int, mode: str = "symmetri
     if group_size not in (32, 64, 128, 256) or k % group_size:
         raise ValueError(f"group size {group_size} must be one of 32/64/128/256 and divide K={k}")
     packed = torch.empty((n, k // 2), device=w.device, dtype=torch.uint8)
-    scale = torch.empty((n, k // group_size), device=w.device, dtype=torch.bfloat16)
-    zero = torch.empty_like(scale)
+    scale_zeros = torch.empty((k // group_size, n, 2), device=w.device, dtype=torch.bfloat16)
     nat.require_cuda(w, what="quantize_int4_groups")
     nat.call("fdms_quantize_int4_groups", w.data_ptr(), nat.dtype_code(w.dtype), w.stride(0), n, k, group_size,
-             int(mode in {"asym", "asymmetric", "affine"}), packed.data_ptr(), packed.stride(0), scale.data_ptr(),
-             zero.data_ptr(), scale.stride(0), nat.stream())
-    return packed, scale, zero
+             int(mode in {"asym", "asymmetric", "affine"}), packed.data_ptr(), packed.stride(0),
+             scale_zeros.data_ptr(), n, nat.stream())
+    return packed, scale_zeros
 
 
-def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor,
-                        group_size: int, bias: torch.Tensor | None = None, *, epilogue: int = EPI_NONE,
+def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale_zeros: torch.Tensor, group_size: int,
+                        bias: torch.Tensor | None = None, *, epilogue: int = EPI_NONE,
                         out: torch.Tensor | None = None, greedy: bool = False) -> torch.Tensor:
     """W4A16 for at most 16 rows (linear.py:462-478 semantics): y = x @
-    dequant(W)^T, or SiLU*up (epilogue 1), or greedy token ids (greedy=True)."""
+    dequant(W)^T, or SiLU*up (epilogue 1), or greedy token ids (greedy=True);
+    scale_zeros is bf16 [K/group, N, 2] (the reference's layout)."""
     n, k = packed.shape[0], packed.shape[1] * 2
     rows = x.shape[0]
     if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.shape[1] != k:
         raise ValueError("linear_int4_small_m expects bf16 activations [rows, K]")
+    if (scale_zeros.dtype != torch.bfloat16 or scale_zeros.shape != (k // group_size, n, 2)
+            or not scale_zeros.is_contiguous()):
+        raise ValueError("scale_zeros must be contiguous bf16 [K/group, N, 2]")
     n_out = n // 2 if epilogue == EPI_SILU_MUL else n
     if not small_m_supported(rows, k, n_out):
         raise ValueError(f"linear_int4_small_m does not support rows={rows}, K={k}, N={n}")
@@ -452,9 +456,9 @@ def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
         y = None
     else:
         y = out if out is not None else torch.empty((rows, n_out), device=x.device, dtype=torch.bfloat16)
-    nat.require_cuda(x, packed, scale, zero, what="linear_int4_small_m")
+    nat.require_cuda(x, packed, scale_zeros, what="linear_int4_small_m")
     nat.call("fdms_linear_int4_small_m", x.data_ptr(), x.stride(0), rows, k, packed.data_ptr(), packed.stride(0),
-             scale.data_ptr(), zero.data_ptr(), int(group_size), scale.stride(0), nat.ptr(bias), n,
+             scale_zeros.data_ptr(), int(group_size), n, nat.ptr(bias), n,
              2 if greedy else int(epilogue), int(k_splits), nat.ptr(ws), nat.ptr(counters), nat.ptr(pv), nat.ptr(pi),
              nat.ptr(tok), nat.ptr(y), 0 if y is None else y.stride(0), nat.stream())
     return tok if greedy else y
@@ -547,7 +551,8 @@ class LinearBase(nn.Module):
     """Weights [out_features, in_features] bf16, optionally shadowed or replaced
     by FP8 rows (``weight_fp8`` [N, K] = the reference's column-major
     ``weight_fp8_t``, ``weight_scale_inv`` [1, N]) and INT4 groups
-    (``weight_int4`` [N, K/2], ``weight_int4_scale`` / ``_zero`` [N, K/group])."""
+    (``weight_int4`` [N, K/2], ``weight_int4_scale_zeros`` [K/group, N, 2], the
+    reference's name and layout)."""
 
     def __init__(self, input_size: int, output_size: int, bias: bool = False):
         super().__init__()
@@ -594,10 +599,9 @@ class LinearBase(nn.Module):
         k, n = self.input_size, self.output_size
         if self.weight.numel() == 0 or k % group or not small_m_supported(1, k, n):
             return False
-        packed, scale, zero = quantize_int4_groups(self.weight.detach(), group, mode)
+        packed, scale_zeros = quantize_int4_groups(self.weight.detach(), group, mode)
         self._set_buffer("weight_int4", packed)
-        self._set_buffer("weight_int4_scale", scale)
-        self._set_buffer("weight_int4_zero", zero)
+        self._set_buffer("weight_int4_scale_zeros", scale_zeros)
         self._int4_group_size = group
         self._int4_enabled = True
         return True
@@ -700,8 +704,8 @@ class LinearBase(nn.Module):
         if amax_out is not None and not (fused and path in ("fp8", "bf16")):
             raise ValueError("amax_out needs the small-M kernel path")
         if path == "int4":
-            return linear_int4_small_m(x2.contiguous(), self.weight_int4, self.weight_int4_scale,
-                                       self.weight_int4_zero, self._int4_group_size, bias, epilogue=epilogue)
+            return linear_int4_small_m(x2.contiguous(), self.weight_int4, self.weight_int4_scale_zeros,
+                                       self._int4_group_size, bias, epilogue=epilogue)
         if path == "fp8" and fused:
             return linear_small_m(x2.contiguous(), self.weight_fp8, bias, weight_scale_inv=self.weight_scale_inv,
                                   quantize_x=qx, epilogue=epilogue, x_amax=x_amax, amax_out=amax_out)

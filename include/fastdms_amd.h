@@ -425,23 +425,26 @@ int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, int k, const
 /* C5 — W4A16 decode linear.  Replaces _int4_row1_matvec /
  * torch._weight_int4pack_mm (fastdms/layers/linear.py:462-478): y[m,n] =
  * x[m,:] . bf16((q[n,:] - 8) * scale + zero) with per-group bf16 scale / zero
- * [N, k/group_size] (g_stride per row).  The packing is this library's own:
- * w_packed[n, j] holds q[n, 2j] (low nibble) and q[n, 2j+1] (high nibble).
- * epilogue 0 = bf16(acc + bias) into y, 1 = SiLU*up of [gate; up] rows (as
- * fdms_linear_small_m), 2 = greedy argmax into out_tokens (as
+ * in the reference's scale_zeros layout (linear.py:461-464): bf16 [k/group_size,
+ * sz_stride >= n, 2], element (g, n, 0) the scale and (g, n, 1) the zero of
+ * group g of weight row n (4-byte aligned).  The weight packing is this
+ * library's own: w_packed[n, j] holds q[n, 2j] (low nibble) and q[n, 2j+1]
+ * (high nibble).  epilogue 0 = bf16(acc + bias) into y, 1 = SiLU*up of [gate;
+ * up] rows (as fdms_linear_small_m), 2 = greedy argmax into out_tokens (as
  * fdms_linear_argmax_small_m).  m <= 16. */
 int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
-                             int64_t w_stride_bytes, const void* group_scale, const void* group_zero,
-                             int group_size, int64_t g_stride, const void* bias, int n, int epilogue, int k_splits,
-                             float* workspace, int* counters, float* part_val, int* part_idx, int64_t* out_tokens,
-                             void* y, int64_t y_stride, void* stream);
+                             int64_t w_stride_bytes, const void* scale_zeros, int group_size, int64_t sz_stride,
+                             const void* bias, int n, int epilogue, int k_splits, float* workspace, int* counters,
+                             float* part_val, int* part_idx, int64_t* out_tokens, void* y, int64_t y_stride,
+                             void* stream);
 
 /* C5 — INT4 group quantisation of weight rows (linear.py:414-459, symmetric or
  * asymmetric); q is computed with the fp32 scale / zero, which are stored in
- * bf16 (456-458).  Output packed as fdms_linear_int4_small_m reads it. */
+ * bf16 (456-458) as the reference's scale_zeros [k/group_size, sz_stride >=
+ * rows, 2] (461-464).  Output packed as fdms_linear_int4_small_m reads it. */
 int fdms_quantize_int4_groups(const void* w, int w_dtype, int64_t w_stride, int64_t rows, int k, int group_size,
-                              int asymmetric, void* out_packed, int64_t out_stride, void* group_scale,
-                              void* group_zero, int64_t g_stride, void* stream);
+                              int asymmetric, void* out_packed, int64_t out_stride, void* scale_zeros,
+                              int64_t sz_stride, void* stream);
 
 /* Paged compact KV (16-row pages from a device free stack per layer; no
  * reference counterpart: the reference packs into flat spans from a host

@@ -11,8 +11,9 @@ def int4_weights(module):
     packed = module.weight_int4.cpu()
     q = torch.stack([packed & 0xF, packed >> 4], dim=-1).reshape(packed.shape[0], -1).float()
     g = module._int4_group_size
-    s = module.weight_int4_scale.float().cpu().repeat_interleave(g, dim=1)
-    z = module.weight_int4_zero.float().cpu().repeat_interleave(g, dim=1)
+    sz = module.weight_int4_scale_zeros.float().cpu()  # [K/group, N, 2] (the reference's layout)
+    s = sz[:, :, 0].t().repeat_interleave(g, dim=1)
+    z = sz[:, :, 1].t().repeat_interleave(g, dim=1)
     return ((q - 8.0) * s + z).to(torch.bfloat16).float()
 
 

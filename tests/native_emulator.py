@@ -1196,9 +1196,9 @@ class Emulator:
         self.view(out, torch.int64, (rows,), (1,), "out").copy_(torch.tensor(toks, dtype=torch.int64))
         return 0
 
-    def quantize_int4_groups(self, w, w_dtype, w_s, rows, k, group, asym, out, out_s, scale, zero, g_s, stream):
+    def quantize_int4_groups(self, w, w_dtype, w_s, rows, k, group, asym, out, out_s, scale_zeros, sz_s, stream):
         from oracle import linear as olin
-        if rows < 0 or k <= 0 or group < 2 or group % 2 or k % group:
+        if rows < 0 or k <= 0 or group < 2 or group % 2 or k % group or sz_s < rows:
             return 1
         if rows == 0:
             return 0
@@ -1206,13 +1206,13 @@ class Emulator:
         q, sc, z = olin.quantize_weight_int4(wv, group, "asymmetric" if asym else "symmetric")
         packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
         self.view(out, torch.uint8, (rows, k // 2), (out_s, 1), "packed").copy_(torch.from_numpy(packed))
-        self.view(scale, torch.bfloat16, (rows, k // group), (g_s, 1), "scale").copy_(
-            torch.from_numpy(sc).to(torch.bfloat16))
-        self.view(zero, torch.bfloat16, (rows, k // group), (g_s, 1), "zero").copy_(
-            torch.from_numpy(z).to(torch.bfloat16))
+        # the reference's scale_zeros [groups, N, 2] (sz_s pairs between groups)
+        sz = self.view(scale_zeros, torch.bfloat16, (k // group, rows, 2), (2 * sz_s, 2, 1), "scale_zeros")
+        sz[:, :, 0].copy_(torch.from_numpy(sc).to(torch.bfloat16).t())
+        sz[:, :, 1].copy_(torch.from_numpy(z).to(torch.bfloat16).t())
         return 0
 
-    def linear_int4_small_m(self, x, x_s, m, k, w, w_s, scale, zero, group, g_s, bias, n, epilogue, k_splits, ws,
+    def linear_int4_small_m(self, x, x_s, m, k, w, w_s, scale_zeros, group, sz_s, bias, n, epilogue, k_splits, ws,
                             counters, part_val, part_idx, out_tokens, y, y_s, stream):
         """W4A16 with each weight dequantised to bf16 ((q - 8) * s + z), fp32
         accumulation, the bf16 linear's bias / epilogue / greedy semantics."""
@@ -1221,13 +1221,14 @@ class Emulator:
         if m == 0 or n == 0:
             return 0
         n_out = n // 2 if epilogue == 1 else n
-        if m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or k % group or epilogue not in (0, 1, 2):
+        if (m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or k % group or epilogue not in (0, 1, 2)
+                or sz_s < n):
             return 1
         p = self.view(w, torch.uint8, (n, k // 2), (w_s, 1), "packed").numpy()
         q = np.empty((n, k), np.uint8)
         q[:, 0::2], q[:, 1::2] = p & 0xF, p >> 4
-        sc = self.view(scale, torch.bfloat16, (n, k // group), (g_s, 1), "scale").float().numpy()
-        z = self.view(zero, torch.bfloat16, (n, k // group), (g_s, 1), "zero").float().numpy()
+        sz = self.view(scale_zeros, torch.bfloat16, (k // group, n, 2), (2 * sz_s, 2, 1), "scale_zeros").float()
+        sc, z = sz[:, :, 0].t().contiguous().numpy(), sz[:, :, 1].t().contiguous().numpy()
         deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, sc, z, group).astype(np.float32)))
         a = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
         out = (a @ deq.T).to(torch.bfloat16).float()

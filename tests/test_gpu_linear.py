@@ -499,13 +499,16 @@ def test_linear_argmax_ties_and_nan():
 @pytest.mark.parametrize("group", [32, 128, 256])
 def test_quantize_int4_groups_bit_exact(mode, group):
     """C5 quantisation (linear.py:414-459): codes bit-exact vs the oracle,
-    bf16 scale / zero bit-exact; the packing puts q[2j] in the low nibble."""
+    bf16 scale / zero bit-exact in the reference's scale_zeros layout [groups,
+    N, 2] (linear.py:461-464); the packing puts q[2j] in the low nibble."""
     require_gpu()
     from fastdms_amd.layers.linear import quantize_int4_groups
     g = torch.Generator().manual_seed(group + len(mode))
     w = (torch.randn(48, 1024, generator=g) * 0.05 + (0.02 if mode == "asymmetric" else 0.0)).to(torch.bfloat16)
     w[3, :group] = 0.0
-    packed, scale, zero = quantize_int4_groups(w.cuda(), group, mode)
+    packed, scale_zeros = quantize_int4_groups(w.cuda(), group, mode)
+    assert scale_zeros.shape == (1024 // group, 48, 2) and scale_zeros.dtype == torch.bfloat16
+    scale, zero = scale_zeros[:, :, 0].t(), scale_zeros[:, :, 1].t()
     q_ref, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group, mode)
     p = packed.cpu().numpy()
     q = np.empty((48, 1024), np.uint8)
@@ -528,19 +531,19 @@ def test_linear_int4_small_m_matches_oracle(m, n, k, group):
     gen = torch.Generator().manual_seed(m + n + k)
     x, w = _bf16((m, k), gen), _bf16((n, k), gen, 0.05)
     bias = _bf16((n,), gen, 0.1)
-    packed, scale, zero = quantize_int4_groups(w.cuda(), group)
+    packed, scale_zeros = quantize_int4_groups(w.cuda(), group)
     q, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group)
     deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, s_ref, z_ref, group).astype(np.float32)))
-    y = linear_int4_small_m(x.cuda(), packed, scale, zero, group, bias.cuda())
+    y = linear_int4_small_m(x.cuda(), packed, scale_zeros, group, bias.cuda())
     want = (_ref_linear(x, deq, None).float() + bias.float()).to(torch.bfloat16)  # linear.py:475-477
     _close_bf16(y, want, "int4", ulps=2.0, atol=2e-3)
-    tok = linear_int4_small_m(x.cuda(), packed, scale, zero, group, greedy=True).cpu()
+    tok = linear_int4_small_m(x.cuda(), packed, scale_zeros, group, greedy=True).cpu()
     sc = _ref_linear(x, deq, None).double()
     for i in range(m):
         if int(tok[i]) != int(sc[i].argmax()):
             assert float(sc[i].max() - sc[i, tok[i]]) <= 1e-3 * float(sc[i].abs().max())
     if n % 32 == 0:
-        ye = linear_int4_small_m(x.cuda(), packed, scale, zero, group, epilogue=EPI_SILU_MUL)
+        ye = linear_int4_small_m(x.cuda(), packed, scale_zeros, group, epilogue=EPI_SILU_MUL)
         gu = _ref_linear(x, deq, None).float()
         f = n // 2
         _close_bf16(ye, (torch.nn.functional.silu(gu[:, :f]) * gu[:, f:]).to(torch.bfloat16), "int4 silu",
