@@ -65,9 +65,13 @@ constexpr int kKB = 64;       // k-block: columns per lane group step
 constexpr int kMaxM = 16;
 constexpr float kFp8Max = 448.0f;
 
+// two fp32 -> bf16 (round to nearest even), a in the low half: one
+// v_cvt_pk_bf16_f32 (two scalar conversions compile to two of them, a shift
+// and an or)
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  const __bf16 x = (__bf16)a, y = (__bf16)b;
-  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
 }
 __device__ __forceinline__ float rbf(float a) { return (float)(__bf16)a; }  // round to bf16
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
