@@ -126,6 +126,27 @@ def test_quantize_fp8_rows_bit_exact(dtype):
     assert np.array_equal(sinv.cpu().numpy().view(np.uint32), sinv_ref.reshape(-1).view(np.uint32))
 
 
+@pytest.mark.parametrize("k", [520, 2048, 3000, 8192, 12288, 16384, 16392])
+@pytest.mark.parametrize("torch_form", [True, False])
+def test_quantize_fp8_rows_widths(k, torch_form):
+    """bf16 activation rows of every width class of fdms_quantize_fp8_rows (one
+    16-byte chunk per thread up to 2048 columns, 2, 4 or 8 chunks up to 16384,
+    the two-pass kernel beyond): codes and scale_inv bit-exact vs the oracle's
+    quantize_rows_fp8 in both 448 / amax forms, an all-zero row scaled by 1."""
+    require_gpu()
+    from fastdms_amd.layers.linear import quantize_fp8_rows
+    g = torch.Generator().manual_seed(k + torch_form)
+    x = (torch.randn(9, k, generator=g) * 0.7).to(torch.bfloat16)
+    x[2] = 0.0
+    x[4, k - 1] = 40.0  # the row maximum in the last chunk
+    q, sinv = quantize_fp8_rows(x.cuda(), torch_form=torch_form)
+    torch.cuda.synchronize()
+    q_ref, x_scale = olin.quantize_rows_fp8(x.float().numpy(), torch_form=torch_form)
+    sinv_ref = (np.float32(1.0) / np.asarray(x_scale, np.float32)).astype(np.float32)  # scale_inv = 1 / s
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(sinv.cpu().numpy().reshape(-1).view(np.uint32), sinv_ref.reshape(-1).view(np.uint32))
+
+
 def _ref_linear(a, w, bias):
     """bf16(a @ W^T + bias) with fp32 accumulation (F.linear semantics)."""
     y = a.float() @ w.float().T
