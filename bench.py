@@ -176,9 +176,9 @@ def parse_args():
                    help="skip the device-side greedy loop over the rest of the generation (counter runs)")
     p.add_argument("--requests", type=int, default=32, help="multitenant: number of requests")
     p.add_argument("--rate", type=float, default=4.0, help="multitenant: Poisson arrival rate (requests/s)")
-    p.add_argument("--kv-cap-tokens", type=int, default=20000,
+    p.add_argument("--kv-cap-tokens", type=int, default=19000,
                    help="multitenant: compact KV capacity per layer (tokens); at the default seed the largest "
-                        "request needs just under 20000 alone, so prefills are deferred and sequences preempted")
+                        "request needs just under 19000 alone, so prefills are deferred and sequences preempted")
     p.add_argument("--eager", action="store_true", help="decode without HIP graphs")
     p.add_argument("--kv-scales", choices=["calibrate", "unit"], default="calibrate",
                    help="per-(layer, kv head) FP8 KV scales (BASELINE configs[1]-[3]) or unit scales (the "
