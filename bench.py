@@ -495,15 +495,15 @@ def compaction_roofline(lens, replays: int = 20, layers: int = 16, config: str =
     chunks = -(-cap // 256)
     max_pages = -(-cap // 16)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32).cuda()
-    gen = torch.Generator().manual_seed(2)
+    gen = torch.Generator(device="cuda").manual_seed(2)  # drawn on the device: no host copies
     keep_old = 0.125
     runs = replays + 3  # eager warm-up, capture (not run), first replay, timed replays
     pool = runs * sum(-(-(window + int(n * keep_old * 1.3)) // 16) for n in lens) * h
     per_layer = []
     for _ in range(layers):
-        k = torch.randn((t_tot, h, d), generator=gen).to(torch.bfloat16).cuda()
-        v = torch.randn((t_tot, h, d), generator=gen).to(torch.bfloat16).cuda()
-        evict = (torch.rand((t_tot, h), generator=gen) >= keep_old).to(torch.uint8).cuda()
+        k = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
+        v = torch.randn((t_tot, h, d), generator=gen, device="cuda").to(torch.bfloat16)
+        evict = (torch.rand((t_tot, h), generator=gen, device="cuda") >= keep_old).to(torch.uint8)
         ck = torch.zeros((pool * 16, d), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
         cv = torch.zeros_like(ck)
         stack = torch.arange(pool, dtype=torch.int32, device="cuda")

@@ -543,17 +543,23 @@ def test_quantize_int4_groups_bit_exact(mode, group):
     assert np.array_equal(q, q_t) and np.array_equal(s_ref, s_t) and np.array_equal(z_ref, z_t)
 
 
-@pytest.mark.parametrize("m,n,k,group", [(1, 3072, 2048, 128), (8, 2048, 8192, 256), (5, 512, 256, 32)])
-def test_linear_int4_small_m_matches_oracle(m, n, k, group):
+@pytest.mark.parametrize("m,n,k,group,mode", [(1, 3072, 2048, 128, "symmetric"), (8, 2048, 8192, 256, "symmetric"),
+                                              (5, 512, 256, 32, "symmetric"), (8, 1024, 2048, 128, "asymmetric"),
+                                              (3, 512, 768, 64, "asymmetric")])
+def test_linear_int4_small_m_matches_oracle(m, n, k, group, mode):
     """W4A16: x @ dequant(W)^T with dequant = bf16((q-8)*s + z) (the oracle's
-    float64 dequant differs by the bf16 rounding of each weight only)."""
+    float64 dequant differs by the bf16 rounding of each weight only; with an
+    asymmetric zero the kernel's q*s + (z - 8s) may round a weight the other
+    way); K off a multiple of 128 per wave (the half k-block) included."""
     require_gpu()
     from fastdms_amd.layers.linear import EPI_SILU_MUL, linear_int4_small_m, quantize_int4_groups
     gen = torch.Generator().manual_seed(m + n + k)
     x, w = _bf16((m, k), gen), _bf16((n, k), gen, 0.05)
+    if mode == "asymmetric":
+        w = (w.float() + 0.03).to(torch.bfloat16)  # groups off zero: a nonzero zero point
     bias = _bf16((n,), gen, 0.1)
-    packed, scale_zeros = quantize_int4_groups(w.cuda(), group)
-    q, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group)
+    packed, scale_zeros = quantize_int4_groups(w.cuda(), group, mode)
+    q, s_ref, z_ref = olin.quantize_weight_int4(w.float().numpy(), group, mode)
     deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, s_ref, z_ref, group).astype(np.float32)))
     y = linear_int4_small_m(x.cuda(), packed, scale_zeros, group, bias.cuda())
     want = (_ref_linear(x, deq, None).float() + bias.float()).to(torch.bfloat16)  # linear.py:475-477
