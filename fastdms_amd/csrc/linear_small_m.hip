@@ -1269,23 +1269,26 @@ FDMS_EXPORT int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, 
 }
 
 // C5 — W4A16 decode linear: the small-M kernel with INT4 weights (no
-// activation quantisation or prologue; epilogue 0 plain, 1 SiLU*up, 2 greedy).
+// activation quantisation or prologue; epilogue 0 plain, 1 SiLU*up, 2 greedy,
+// 3 fp32 split partials into workspace for the next RMSNorm to sum).
 FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
                                          int64_t w_stride_bytes, const void* scale_zeros, int group_size,
                                          int64_t sz_stride, const void* bias, int n, int epilogue,
                                          int k_splits, float* workspace, int* counters, float* part_val,
                                          int* part_idx, int64_t* out_tokens, void* y, int64_t y_stride,
                                          void* stream) {
-  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || epilogue < 0 || epilogue > 2) return (int)hipErrorInvalidValue;
+  if (m < 0 || m > kMaxM || k <= 0 || n < 0 || epilogue < 0 || epilogue > 3) return (int)hipErrorInvalidValue;
   if (m == 0 || n == 0) return 0;
   if (!x || !w_packed || !scale_zeros || ((uintptr_t)scale_zeros % 4)) return (int)hipErrorInvalidValue;
+  // epilogue 3: workspace[split][row][n] fp32 partials, no bias (the consumer adds in split order)
+  if (epilogue == 3 && (bias || !workspace)) return (int)hipErrorInvalidValue;
   // a lane group's 32 columns of a 128-column k-block lie in one group
   if (group_size < 32 || (group_size & (group_size - 1)) || k % group_size || sz_stride < n)
     return (int)hipErrorInvalidValue;
-  if (epilogue == 2 ? (!part_val || !part_idx || !out_tokens) : !y) return (int)hipErrorInvalidValue;
+  if (epilogue == 2 ? (!part_val || !part_idx || !out_tokens) : (epilogue != 3 && !y)) return (int)hipErrorInvalidValue;
   const int n_out = epilogue == 1 ? n / 2 : n;
   if (n_out % 16 || (epilogue == 1 && n % 2)) return (int)hipErrorInvalidValue;
-  if (k_splits < 1 || k_splits > 64 || k % k_splits || (k_splits > 1 && (!workspace || !counters)))
+  if (k_splits < 1 || k_splits > 64 || k % k_splits || (k_splits > 1 && epilogue != 3 && (!workspace || !counters)))
     return (int)hipErrorInvalidValue;
   const int kc = k / k_splits;
   // four waves per workgroup (eight, the override, measured 5 % slower on
@@ -1297,7 +1300,7 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
   }
   if (kc % (kKB * nw)) return (int)hipErrorInvalidValue;
   if (((uintptr_t)x % 16) || ((uintptr_t)w_packed % 16) || (x_stride * 2) % 16 || w_stride_bytes % 16 ||
-      x_stride < k || w_stride_bytes * 2 < k || (epilogue != 2 && y_stride < n_out))
+      x_stride < k || w_stride_bytes * 2 < k || (epilogue < 2 && y_stride < n_out))
     return (int)hipErrorInvalidValue;
   if (y && (y == x)) return (int)hipErrorInvalidValue;
   const int strips = n_out / 16;
@@ -1311,7 +1314,8 @@ FDMS_EXPORT int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m,
   a.g_s = sz_stride;
   const dim3 grid((unsigned)blocks);
   const hipStream_t st = (hipStream_t)stream;
-  if (epilogue == 2) launch_linear<u4x2_t, 0, false, 2>(nw, grid, st, a);
+  if (epilogue == 3) launch_linear<u4x2_t, 0, false, 3>(nw, grid, st, a);
+  else if (epilogue == 2) launch_linear<u4x2_t, 0, false, 2>(nw, grid, st, a);
   else if (epilogue == 1) launch_linear<u4x2_t, 0, false, 1>(nw, grid, st, a);
   else launch_linear<u4x2_t, 0, false, 0>(nw, grid, st, a);
   FDMS_LAUNCH_CHECK();

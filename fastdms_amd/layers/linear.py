@@ -112,6 +112,19 @@ def _amax_args(x_amax: torch.Tensor | None, rows: int) -> tuple[int, int, int]:
     return x_amax.data_ptr(), x_amax.shape[1], x_amax.stride(0)
 
 
+def _partials_buffer(device: torch.device, k_splits: int, rows: int, n: int) -> torch.Tensor:
+    """[k_splits, rows, n] fp32 view of the per-device split-partials buffer."""
+    need = k_splits * rows * n
+    idx = _device_index(device)
+    buf = _PARTIALS.get(idx)
+    if buf is None or buf.numel() < need:
+        if buf is not None:
+            _RETIRED.append(buf)
+        buf = torch.empty(max(need, SMALL_M_MAX_ROWS * 4096 * 4), device=device, dtype=torch.float32)
+        _PARTIALS[idx] = buf
+    return buf[:need].view(k_splits, rows, n)
+
+
 def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None = None, *,
                     weight_scale_inv: torch.Tensor | None = None, quantize_x: int | None = None,
                     x_amax: torch.Tensor | None = None) -> SplitPartials:
@@ -135,15 +148,8 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor, k_splits: int | None 
     am_ptr, am_n, am_s = _amax_args(x_amax if qx else None, rows)
     if k_splits is None:
         k_splits = choose_partial_splits(x.device, n // 16, k)
-    need = k_splits * rows * n
+    part = _partials_buffer(x.device, k_splits, rows, n)
     idx = _device_index(x.device)
-    buf = _PARTIALS.get(idx)
-    if buf is None or buf.numel() < need:
-        if buf is not None:
-            _RETIRED.append(buf)
-        buf = torch.empty(max(need, SMALL_M_MAX_ROWS * 4096 * 4), device=x.device, dtype=torch.float32)
-        _PARTIALS[idx] = buf
-    part = buf[:need].view(k_splits, rows, n)
     sinv = row_scale = None
     if fp8:
         sinv = weight_scale_inv.reshape(-1)
@@ -429,7 +435,8 @@ def quantize_int4_groups(w: torch.Tensor, group_size: int, mode: str = "symmetri
 
 def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale_zeros: torch.Tensor, group_size: int,
                         bias: torch.Tensor | None = None, *, epilogue: int = EPI_NONE,
-                        out: torch.Tensor | None = None, greedy: bool = False) -> torch.Tensor:
+                        out: torch.Tensor | None = None, greedy: bool = False,
+                        k_splits: int | None = None) -> torch.Tensor:
     """W4A16 for at most 16 rows (linear.py:462-478 semantics): y = x @
     dequant(W)^T, or SiLU*up (epilogue 1), or greedy token ids (greedy=True);
     scale_zeros is bf16 [K/group, N, 2] (the reference's layout)."""
@@ -444,7 +451,8 @@ def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale_zeros: torc
     if not small_m_supported(rows, k, n_out):
         raise ValueError(f"linear_int4_small_m does not support rows={rows}, K={k}, N={n}")
     strips = n_out // 16
-    k_splits = choose_k_splits(x.device, strips, k)
+    if k_splits is None:
+        k_splits = choose_k_splits(x.device, strips, k)
     ws = counters = None
     if k_splits > 1:
         ws, counters = linear_workspace(x.device, strips * k_splits * 256 * (2 if epilogue else 1), strips)
@@ -462,6 +470,31 @@ def linear_int4_small_m(x: torch.Tensor, packed: torch.Tensor, scale_zeros: torc
              2 if greedy else int(epilogue), int(k_splits), nat.ptr(ws), nat.ptr(counters), nat.ptr(pv), nat.ptr(pi),
              nat.ptr(tok), nat.ptr(y), 0 if y is None else y.stride(0), nat.stream())
     return tok if greedy else y
+
+
+def linear_int4_partials(x: torch.Tensor, packed: torch.Tensor, scale_zeros: torch.Tensor, group_size: int,
+                         k_splits: int | None = None) -> SplitPartials:
+    """W4A16 y = x @ dequant(W)^T (no bias, at most 16 rows) as fp32 split
+    partials (fdms_linear_int4_small_m epilogue 3) for the next RMSNorm to sum,
+    in the same per-device buffer as linear_partials (consume before the next
+    call)."""
+    n, k = packed.shape[0], packed.shape[1] * 2
+    rows = x.shape[0]
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.shape[1] != k:
+        raise ValueError("linear_int4_partials expects bf16 activations [rows, K]")
+    if (scale_zeros.dtype != torch.bfloat16 or scale_zeros.shape != (k // group_size, n, 2)
+            or not scale_zeros.is_contiguous()):
+        raise ValueError("scale_zeros must be contiguous bf16 [K/group, N, 2]")
+    if not small_m_supported(rows, k, n):
+        raise ValueError(f"linear_int4_partials does not support rows={rows}, K={k}, N={n}")
+    if k_splits is None:
+        k_splits = choose_partial_splits(x.device, n // 16, k)
+    part = _partials_buffer(x.device, k_splits, rows, n)
+    nat.require_cuda(x, packed, scale_zeros, what="linear_int4_partials")
+    nat.call("fdms_linear_int4_small_m", x.data_ptr(), x.stride(0), rows, k, packed.data_ptr(), packed.stride(0),
+             scale_zeros.data_ptr(), int(group_size), n, None, n, EPI_PARTIALS, int(k_splits), part.data_ptr(),
+             None, None, None, None, None, 0, nat.stream())
+    return SplitPartials(part)
 
 
 def fp8_gemm_impl() -> str:

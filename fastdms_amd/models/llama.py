@@ -24,8 +24,8 @@ from ..layers.compact_attention import (compact_attention_inline_q_rope_enabled,
 from ..layers.embed_head import ParallelLMHead, VocabParallelEmbedding, embedding_rms_norm
 from ..layers.layernorm import RMSNorm
 from ..layers.linear import (EPI_NONE, EPI_SILU_MUL, LinearBase, MergedColumnParallelLinear, QKVParallelLinear,
-                             RowParallelLinear, linear_norm_stats, linear_partials, linear_residual_stats,
-                             small_m_supported)
+                             RowParallelLinear, linear_int4_partials, linear_norm_stats, linear_partials,
+                             linear_residual_stats, small_m_supported)
 from ..layers.rotary_embedding import get_rope
 from ..utils.context import get_context
 
@@ -61,15 +61,17 @@ class ModelConfig:
 
 
 def _deferred_linear(lin: LinearBase, x: torch.Tensor, x_amax: torch.Tensor | None = None):
-    """A linear whose only consumer is an RMSNorm: on the bf16 / FP8 small-M
-    decode path its split-K merge (and the FP8 row / column scaling) moves into
-    that RMSNorm (SplitPartials), which saves the linear's merge round trips;
-    other paths return the finished tensor.  ``x_amax``: x's row amax from its
-    producer, for an FP8 linear's activation quantisation."""
+    """A linear whose only consumer is an RMSNorm: on the bf16 / FP8 / INT4
+    small-M decode path its split-K merge (and the FP8 row / column scaling)
+    moves into that RMSNorm (SplitPartials), which saves the linear's merge
+    round trips; other paths return the finished tensor.  ``x_amax``: x's row
+    amax from its producer, for an FP8 linear's activation quantisation."""
     rows = x.shape[0]
     path, qx = lin.route(rows)
-    if (_defer_splitk_enabled() and lin.bias is None and path in ("bf16", "fp8")
+    if (_defer_splitk_enabled() and lin.bias is None and path in ("bf16", "fp8", "int4")
             and small_m_supported(rows, lin.input_size, lin.output_size) and x.stride(-1) == 1):
+        if path == "int4":
+            return linear_int4_partials(x, lin.weight_int4, lin.weight_int4_scale_zeros, lin._int4_group_size)
         if path == "bf16":
             return linear_partials(x, lin.weight)
         return linear_partials(x, lin.weight_fp8, weight_scale_inv=lin.weight_scale_inv, quantize_x=qx,

@@ -431,7 +431,9 @@ int fdms_fp8_rerank_topk(const void* x, int64_t x_stride, int rows, int k, const
  * library's own: w_packed[n, j] holds q[n, 2j] (low nibble) and q[n, 2j+1]
  * (high nibble).  epilogue 0 = bf16(acc + bias) into y, 1 = SiLU*up of [gate;
  * up] rows (as fdms_linear_small_m), 2 = greedy argmax into out_tokens (as
- * fdms_linear_argmax_small_m).  m <= 16. */
+ * fdms_linear_argmax_small_m), 3 = fp32 split partials workspace[split][row][n]
+ * (no bias; as fdms_linear_small_m's epilogue 3, summed by
+ * fdms_rmsnorm_partials).  m <= 16. */
 int fdms_linear_int4_small_m(const void* x, int64_t x_stride, int m, int k, const void* w_packed,
                              int64_t w_stride_bytes, const void* scale_zeros, int group_size, int64_t sz_stride,
                              const void* bias, int n, int epilogue, int k_splits, float* workspace, int* counters,

@@ -1215,14 +1215,16 @@ class Emulator:
     def linear_int4_small_m(self, x, x_s, m, k, w, w_s, scale_zeros, group, sz_s, bias, n, epilogue, k_splits, ws,
                             counters, part_val, part_idx, out_tokens, y, y_s, stream):
         """W4A16 with each weight dequantised to bf16 ((q - 8) * s + z), fp32
-        accumulation, the bf16 linear's bias / epilogue / greedy semantics."""
+        accumulation, the bf16 linear's bias / epilogue / greedy semantics;
+        epilogue 3 writes the fp32 product as split partials (all of it in
+        split 0) for the next RMSNorm to sum."""
         from oracle import linear as olin
         from oracle import numerics
         if m == 0 or n == 0:
             return 0
         n_out = n // 2 if epilogue == 1 else n
-        if (m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or k % group or epilogue not in (0, 1, 2)
-                or sz_s < n):
+        if (m > 16 or (k // max(k_splits, 1)) % 256 or n_out % 16 or k % group or epilogue not in (0, 1, 2, 3)
+                or sz_s < n or (epilogue == 3 and (bias or not ws))):
             return 1
         p = self.view(w, torch.uint8, (n, k // 2), (w_s, 1), "packed").numpy()
         q = np.empty((n, k), np.uint8)
@@ -1231,6 +1233,12 @@ class Emulator:
         sc, z = sz[:, :, 0].t().contiguous().numpy(), sz[:, :, 1].t().contiguous().numpy()
         deq = torch.from_numpy(numerics.bf16_round(olin.int4_dequant(q, sc, z, group).astype(np.float32)))
         a = self.view(x, torch.bfloat16, (m, k), (x_s, 1), "x").float()
+        if epilogue == 3:
+            part = self.view(ws, torch.float32, (k_splits, m, n), (m * n, n, 1), "partials")
+            part.zero_()
+            part[0].copy_((a.double() @ deq.double().T).float())
+            self.calls.append("fdms_linear_int4_small_m:partials")
+            return 0
         out = (a @ deq.T).to(torch.bfloat16).float()
         if bias:  # linear.py:475-477: bias added to the bf16 matmul result
             out = (out + self.view(bias, torch.bfloat16, (n,), (1,), "bias").float()).to(torch.bfloat16).float()

@@ -100,6 +100,22 @@ def test_fp8_decode_glue_matches_the_quantised_oracle(monkeypatch):
         assert "fdms_linear_small_m:" + tag in calls, tag
 
 
+INT4_ENV = dict(FP8_ENV, FASTDMS_INT4_ROW1_WEIGHTS="1", FASTDMS_INT4_ROW1_SCOPE="all",
+                FASTDMS_INT4_ROW1_GROUP_SIZE="128", FASTDMS_INT4_ROW1_QUANT_MODE="symmetric",
+                FASTDMS_INT4_ROW1_MAX_ROWS="16")
+
+
+def test_int4_decode_glue_matches_the_quantised_oracle(monkeypatch):
+    """W4A16 decode linears (the reference's FASTDMS_INT4_ROW1_* switches, as
+    configs[4] runs them; FP8 rows for the prefill): o_proj's and down_proj's
+    split partials go to the next RMSNorm, as on the bf16 path.  Logits follow
+    the oracle holding the same dequantised INT4 weights and routes."""
+    for k, v in INT4_ENV.items():
+        monkeypatch.setenv(k, v)
+    calls = _run("tiny-llama", [300, 517, 64], 8, fused_head=False, quant=True)
+    assert "fdms_linear_int4_small_m:partials" in calls
+
+
 def _run(model, lens, gen, fused_head, layout="paged", quant=False, lookahead=False):
     """lookahead: the decode lookahead runs (the compact state is then one
     step ahead between steps and is compared once the sequences finish)."""

@@ -577,6 +577,32 @@ def test_linear_int4_small_m_matches_oracle(m, n, k, group, mode):
                     ulps=2.0, atol=2e-3)
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_int4_partials_equal_the_merged_linear(splits):
+    """W4A16 epilogue 3: the fp32 split partials summed in split order are the
+    in-kernel merge at the same split count bit for bit, and the RMSNorm that
+    sums them (the decode step's o_proj / down_proj consumer) gives the same
+    rows as the RMSNorm of the finished linear."""
+    require_gpu()
+    from fastdms_amd.layers.layernorm import rms_norm
+    from fastdms_amd.layers.linear import linear_int4_partials, linear_int4_small_m, quantize_int4_groups
+    gen = torch.Generator().manual_seed(splits)
+    m, n, k = 8, 2048, 8192
+    x, w = _bf16((m, k), gen), _bf16((n, k), gen, 0.05)
+    res = _bf16((m, n), gen)
+    nw = (1.0 + 0.2 * torch.randn(n, generator=gen)).to(torch.bfloat16).cuda()
+    packed, scale_zeros = quantize_int4_groups(w.cuda(), 128)
+    y = linear_int4_small_m(x.cuda(), packed, scale_zeros, 128, k_splits=splits)
+    part = linear_int4_partials(x.cuda(), packed, scale_zeros, 128, k_splits=splits)
+    acc = part.data[0].clone()
+    for i in range(1, splits):
+        acc = acc + part.data[i]
+    assert torch.equal(acc.to(torch.bfloat16), y), "partials summed in split order"
+    h_part, r_part = rms_norm(part, nw, 1e-5, residual=res.cuda())
+    h_y, r_y = rms_norm(y, nw, 1e-5, residual=res.cuda())
+    assert torch.equal(h_part, h_y) and torch.equal(r_part, r_y), "RMSNorm of the partials"
+
+
 @pytest.mark.parametrize("m,n,k", [(9, 2048, 2048), (40, 768, 512), (16, 3072, 1000)])
 def test_fp8_rows_gemm_prefill_rows(m, n, k):
     """_fp8_linear for prefill row counts (linear.py:635-662): torch-form
