@@ -42,8 +42,12 @@
 // group's loads are in flight while the current one runs
 // v_mfma_f32_16x16x32_bf16 with A = 16 weight rows, B = the activation rows,
 // M <= 16 padded with zeros, C = y^T).  FP8 weights are exact in bf16, so the
-// FP8 path converts in registers and uses the same MFMA; products are exact and
-// accumulate in fp32 like the reference's FP8 dot.  The waves' C fragments are
+// FP8 path without activation quantisation converts in registers and uses the
+// same MFMA; products are exact and accumulate in fp32 like the reference's
+// FP8 dot.  FP8 weights with the quantised activation, and INT4 weights, read
+// 128-column k-blocks (lane group g: columns 32g .. 32g + 31): the FP8 ones
+// multiply on v_mfma_scale_f32_16x16x128_f8f6f4, the INT4 ones are
+// dequantised to bf16 for four v_mfma_f32_16x16x32_bf16.  The waves' C fragments are
 // summed through LDS.  When there are fewer strips than CUs, K is split across
 // workgroups: each split publishes its fragment with agent-scope atomic stores
 // and the last split of a strip to arrive (device-scope ticket) sums them and
