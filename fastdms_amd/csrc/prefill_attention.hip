@@ -221,9 +221,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 // GQA-packed variant for group sizes 1, 2 and 4: a workgroup takes P =
 // 64·QT/G query positions of one KV head for all G query heads that share it,
 // so one staged K/V block feeds 64·QT query rows (wave w: head w % G,
-// positions 16·QT·(w / G) .. +16·QT-1, QT 16-row MFMA tiles; QT = 2: QT = 4
-// halves the LDS reads per MFMA but costs an occupancy step and measured no
-// faster -- the loop is bound by its VALU work, the softmax).  K/V blocks of 64 keys are
+// positions 16·QT·(w / G) .. +16·QT-1, QT 16-row MFMA tiles: QT = 4 halves
+// the LDS reads per MFMA but costs an occupancy step (3 -> 2 waves per SIMD
+// at head_dim 64), so the launcher takes it for large grids only).  K/V blocks of 64 keys are
 // double-buffered in LDS: the next block's global loads are in flight while
 // the current one is computed, and one barrier separates blocks.  V is
 // transposed in registers (4 keys x 8 dims per thread, byte permutes) so the
@@ -231,7 +231,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 // query tiles of a wave, as does every V fragment.  The softmax row sums come
 // from the matrix cores (P . 1, an extra output tile).  Softmax rescaling is
 // lazy: the running max only moves (and O / the sums are rescaled) when a block raises it
-// by more than 8 in the log2 domain, so p = exp2(s - m) stays below 256.
+// by more than 8 in the log2 domain, so p = exp2(s - m) stays below 256.  The
+// running max starts at a finite floor (-1e30) instead of -inf: the first
+// block with a visible key then takes the same grow test as every later one,
+// its rescale factor exp2((floor - m) * scale) is exactly 0, and a row whose
+// keys so far are all masked keeps the floor with p = exp2(-inf) = 0 -- the
+// same results as special-casing -inf, with fewer VALU instructions per block.
 template <int D, int G, int QT>
 __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     const bf16_t* __restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t* __restrict__ k, int64_t ks_t,
@@ -356,9 +361,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
     }
   };
 
+  constexpr float kMaxFloor = -1e30f;  // below any score; see the rescale note above
   float m_run[QT];  // raw-score running max of query lc of each tile
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
+  for (int qt = 0; qt < QT; ++qt) m_run[qt] = kMaxFloor;
   // o[qt][D/16] accumulates P . 1 on the matrix cores: column-replicated row
   // sums of the same bf16 P as the numerator, in the O layout (no shuffles)
   f32x4 o[QT][D / 16 + 1];
@@ -415,10 +421,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_gqa_kernel(
           for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, acc[qt][t][r]);
         bmax = rows_max(bmax);
         // lazy rescale: move the max only when it grows by more than 2^8 in p
-        const bool grow = m_run[qt] == -INFINITY ? bmax > -INFINITY : (bmax - m_run[qt]) * scale_log2 > 8.0f;
+        const bool grow = (bmax - m_run[qt]) * scale_log2 > 8.0f;  // bmax = -inf (all masked): false
         if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
           const float m_new = fmaxf(m_run[qt], bmax);
-          const float alpha = m_run[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * scale_log2);
+          const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - m_new) * scale_log2);  // 0 from the floor
           m_run[qt] = m_new;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -495,9 +501,19 @@ FDMS_EXPORT int fdms_prefill_attention_varlen(const void* q, int64_t qs_t, int64
   const int32_t* ck = cu_seqlens_k;
   if ((group == 1 || group == 2 || group == 4) && (head_dim == 64 || head_dim == 128) &&
       fdms_prefill_gqa_enabled()) {
-    int qt = 2;  // 16-row query tiles per wave
-    if (const char* e = std::getenv("FASTDMS_AMD_PREFILL_QT")) {  // comparison / testing
-      if (e[0] == '4' && head_dim == 64) qt = 4;
+    // 16-row query tiles per wave: four at head_dim 64 when the grid still
+    // holds kQt4MinBlocks workgroups of 256 / group positions.  Measured at the
+    // Llama-3.2-1B shape: 8 prompts of 4-8k tokens (7 900 such workgroups)
+    // run 4 % faster with four; one 8192-token prompt (1 024) runs 11 %
+    // slower, as do the smaller grids
+    constexpr int64_t kQt4MinBlocks = 4096;
+    int qt = 2;
+    if (head_dim == 64 && (int64_t)((max_seqlen_q + 256 / group - 1) / (256 / group)) * num_kv_heads * num_seqs >=
+                              kQt4MinBlocks)
+      qt = 4;
+    if (const char* e = std::getenv("FASTDMS_AMD_PREFILL_QT")) {  // comparison / testing: force 2 or 4
+      if (e[0] == '2') qt = 2;
+      else if (e[0] == '4' && head_dim == 64) qt = 4;
     }
     const int pos = 64 * qt / group;  // query positions per workgroup
     const dim3 ggrid((max_seqlen_q + pos - 1) / pos, num_kv_heads, num_seqs);

@@ -227,6 +227,43 @@ def test_prefill_attention_vs_oracle(d, lens, hq, hkv, ramp):
     assert np.mean(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 4), (4, 4)])
+def test_prefill_attention_query_tiles_agree(hq, hkv, monkeypatch):
+    """The packed kernel with two or four 16-row query tiles per wave (the
+    launcher takes four at head_dim 64 on large grids): each row's arithmetic
+    is the same, only a workgroup's span of positions differs, so the outputs
+    are bit-identical, and both match the oracle.  Keys grow along the
+    sequence, so the lazy rescale runs after the first block."""
+    require_gpu()
+    from fastdms_amd.layers.attention import prefill_attention
+    d, lens = 64, [1, 700, 1500, 64, 129]
+    t = sum(lens)
+    rng = np.random.default_rng(hq * 10 + hkv)
+    qkv = rng.standard_normal((t, (hq + 2 * hkv) * d)).astype(np.float32)
+    pos = np.concatenate([np.arange(n) / n for n in lens]).astype(np.float32)
+    qkv[:, hq * d:(hq + hkv) * d] *= (1.0 + 3.0 * pos)[:, None]
+    qkv_b = _bf16(qkv)
+    qkv_v = qkv_b.float().numpy()
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    want = oatt.causal_prefill_attention(qkv_v[:, :hq * d].reshape(t, hq, d),
+                                         qkv_v[:, hq * d:(hq + hkv) * d].reshape(t, hkv, d),
+                                         qkv_v[:, (hq + hkv) * d:].reshape(t, hkv, d), cu)
+    dq = qkv_b.cuda()
+    qd = dq[:, :hq * d].view(t, hq, d)
+    kd = dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    vd = dq[:, (hq + hkv) * d:].view(t, hkv, d)
+    outs = {}
+    for qt in ("2", "4"):
+        monkeypatch.setenv("FASTDMS_AMD_PREFILL_QT", qt)
+        outs[qt] = prefill_attention(qd, kd, vd, torch.from_numpy(cu).cuda(), max(lens), d ** -0.5)
+        torch.cuda.synchronize()
+    assert torch.equal(outs["2"], outs["4"])
+    got = outs["4"].float().cpu().numpy()
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err <= 2e-2, f"max-abs-rel error {err:.3g}"
+    assert np.mean(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 4e-3) > 0.99
+
+
 @pytest.mark.parametrize("d,lens,cuts,hq,hkv", [
     (64, [300, 517, 64], [128, 100, 0], 8, 2),     # G = 4, prefix a multiple of 64 / not / none
     (128, [700, 129], [511, 128], 8, 2),
