@@ -131,15 +131,16 @@ class LLMEngine:
             # admitted (and, checked by the runner, none of it finishes now)
             token_ids = runner.run(seqs, False, lookahead=lookahead and not self.scheduler.waiting) if seqs else []
         dt = time.perf_counter() - t0
+        # llm_engine.py:51-52: a prefill step counts the tokens it computed (a
+        # chunk of a long prompt, a re-prefill's tokens), read before
+        # postprocess clears them; a decode step counts its sequences
+        num_tokens = sum(s.num_scheduled_tokens for s in seqs) if is_prefill else len(seqs)
         self.scheduler.postprocess(seqs, token_ids, is_prefill)
         fast = self._greedy_fast_loop(seqs) if is_prefill else None
         freed = self.scheduler.consume_freed_seq_ids()
         if freed:
             self.model_runner.free_compact(freed)
         outputs = [(seq.seq_id, seq.completion_token_ids) for seq in seqs if seq.is_finished]
-        num_tokens = sum(seq.num_scheduled_tokens or len(seq) for seq in seqs) if is_prefill else len(seqs)
-        if is_prefill:
-            num_tokens = sum(len(s.prompt_token_ids) for s in seqs)
         self.last_step_stats = {"is_prefill": is_prefill, "seconds": dt, "tokens": num_tokens, "fast_loop": fast}
         return outputs, (num_tokens if is_prefill else -len(seqs))
 

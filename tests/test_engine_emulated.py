@@ -269,8 +269,14 @@ def _generate(lens, gen, budget, seed=9, max_model_len=2048):
     rng = np.random.default_rng(seed)
     sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
     seqs = [llm.add_request(rng.integers(0, 512, n).tolist(), sp) for n in lens]
+    prefill_counts = []
     while not llm.is_finished():
-        llm.step()
+        _, num = llm.step()
+        if num > 0:
+            prefill_counts.append(num)
+    # llm_engine.py:51-52: a prefill step reports the tokens it computed, so
+    # the chunks of the prompts add up to their lengths, each within the budget
+    assert sum(prefill_counts) == sum(lens) and max(prefill_counts) <= budget
     return llm, [list(s.completion_token_ids) for s in seqs]
 
 
