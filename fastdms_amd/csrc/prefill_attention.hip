@@ -221,9 +221,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attn_kernel(
 // GQA-packed variant for group sizes 1, 2 and 4: a workgroup takes P =
 // 64·QT/G query positions of one KV head for all G query heads that share it,
 // so one staged K/V block feeds 64·QT query rows (wave w: head w % G,
-// positions 16·QT·(w / G) .. +16·QT-1, QT 16-row MFMA tiles: QT = 4 halves
-// the LDS reads per MFMA but costs an occupancy step (3 -> 2 waves per SIMD
-// at head_dim 64), so the launcher takes it for large grids only).  K/V blocks of 64 keys are
+// positions 16·QT·(w / G) .. +16·QT-1, QT 16-row MFMA tiles; QT = 2: QT = 4
+// halves the LDS reads per MFMA but costs an occupancy step (3 -> 2 waves per
+// SIMD at head_dim 64) and measured no faster).  K/V blocks of 64 keys are
 // double-buffered in LDS: the next block's global loads are in flight while
 // the current one is computed, and one barrier separates blocks.  V is
 // transposed in registers (4 keys x 8 dims per thread, byte permutes) so the
@@ -501,19 +501,12 @@ FDMS_EXPORT int fdms_prefill_attention_varlen(const void* q, int64_t qs_t, int64
   const int32_t* ck = cu_seqlens_k;
   if ((group == 1 || group == 2 || group == 4) && (head_dim == 64 || head_dim == 128) &&
       fdms_prefill_gqa_enabled()) {
-    // 16-row query tiles per wave: four at head_dim 64 when the grid still
-    // holds kQt4MinBlocks workgroups of 256 / group positions.  Measured at the
-    // Llama-3.2-1B shape: 8 prompts of 4-8k tokens (7 900 such workgroups)
-    // run 4 % faster with four; one 8192-token prompt (1 024) runs 11 %
-    // slower, as do the smaller grids
-    constexpr int64_t kQt4MinBlocks = 4096;
+    // 16-row query tiles per wave.  Four (head_dim 64 only) measured within
+    // 1 % of two on the Llama-3.2-1B c=8 prompts and 15 % slower on one
+    // 8192-token prompt, so two is the default
     int qt = 2;
-    if (head_dim == 64 && (int64_t)((max_seqlen_q + 256 / group - 1) / (256 / group)) * num_kv_heads * num_seqs >=
-                              kQt4MinBlocks)
-      qt = 4;
-    if (const char* e = std::getenv("FASTDMS_AMD_PREFILL_QT")) {  // comparison / testing: force 2 or 4
-      if (e[0] == '2') qt = 2;
-      else if (e[0] == '4' && head_dim == 64) qt = 4;
+    if (const char* e = std::getenv("FASTDMS_AMD_PREFILL_QT")) {  // comparison / testing
+      if (e[0] == '4' && head_dim == 64) qt = 4;
     }
     const int pos = 64 * qt / group;  // query positions per workgroup
     const dim3 ggrid((max_seqlen_q + pos - 1) / pos, num_kv_heads, num_seqs);

@@ -229,11 +229,11 @@ def test_prefill_attention_vs_oracle(d, lens, hq, hkv, ramp):
 
 @pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 4), (4, 4)])
 def test_prefill_attention_query_tiles_agree(hq, hkv, monkeypatch):
-    """The packed kernel with two or four 16-row query tiles per wave (the
-    launcher takes four at head_dim 64 on large grids): each row's arithmetic
-    is the same, only a workgroup's span of positions differs, so the outputs
-    are bit-identical, and both match the oracle.  Keys grow along the
-    sequence, so the lazy rescale runs after the first block."""
+    """The packed kernel with two or four 16-row query tiles per wave (four
+    is selectable at head_dim 64): each row's arithmetic is the same, only a
+    workgroup's span of positions differs, so the outputs are bit-identical,
+    and both match the oracle.  Keys grow along the sequence, so the lazy
+    rescale runs after the first block."""
     require_gpu()
     from fastdms_amd.layers.attention import prefill_attention
     d, lens = 64, [1, 700, 1500, 64, 129]
