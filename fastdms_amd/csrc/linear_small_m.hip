@@ -427,6 +427,10 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
       for (int u = 0; u < U; ++u) {
         if (kb0 + u * KB >= kend) break;
         const bool xv = kb0 + u * KB + 32 * g < kend && has_row;  // this lane group's columns and row exist
+        // the activation operands, zeroed where they do not exist, shared by both strips
+        uint4 bxs[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bxs[j] = xv ? b.x8[u][j] : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
           // w = bf16((q - 8) * s + z) as one fma of the code: q * s + (z - 8s)
@@ -438,7 +442,12 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
           const uint32_t wd[4] = {b.w4[a][u].x, b.w4[a][u].y, b.w4[a][u].z, b.w4[a][u].w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = wd[j] & 0xF0F0F0F0u;
+            uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = wd[j] & 0xF0F0F0F0u;
+            // hide the masks' known zero bits from the compiler: it would
+            // otherwise narrow (lo >> 8i) & 0xFF to a 4-bit field extract
+            // plus a byte-0 conversion, two instructions instead of one
+            // v_cvt_f32_ubyte<i> per code
+            asm("" : "+v"(lo), "+v"(hi));
             const uint4 aw = uint4{
                 pack2(__builtin_fmaf((float)(lo & 0xFFu), sc, c8),
                       __builtin_fmaf((float)(hi & 0xFFu), s16, c8)),
@@ -448,8 +457,7 @@ __global__ __launch_bounds__(NW * 64) void linear_small_m_kernel(
                       __builtin_fmaf((float)((hi >> 16) & 0xFFu), s16, c8)),
                 pack2(__builtin_fmaf((float)((lo >> 24) & 0xFFu), sc, c8),
                       __builtin_fmaf((float)((hi >> 24) & 0xFFu), s16, c8))};
-            const uint4 bx = xv ? b.x8[u][j] : uint4{0u, 0u, 0u, 0u};
-            acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aw), as_bf16x8(bx), acc[a], 0, 0, 0);
+            acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aw), as_bf16x8(bxs[j]), acc[a], 0, 0, 0);
           }
         }
       }
