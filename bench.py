@@ -709,6 +709,31 @@ def hbm_copy_gbps(nbytes: int = 1 << 30) -> float:
     return 2 * nbytes * reps / (e0.elapsed_time(e1) / 1e3) / 1e9
 
 
+def counter_calibration(reps: int = 3) -> None:
+    """Dispatches of known traffic for reading HBM counters (run under
+    rocprofv3 --pmc): per repetition a gather and a scatter of random 64-byte
+    and 128-byte rows of a 64 MiB table (16 MiB moved each) and a contiguous
+    16 MiB copy, in that order."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(0)
+    n = 1 << 20
+    src64 = torch.randint(0, 255, (n, 64), dtype=torch.uint8, device="cuda", generator=g)
+    src128 = torch.randint(0, 255, (n // 2, 128), dtype=torch.uint8, device="cuda", generator=g)
+    idx64 = torch.randperm(n, device="cuda", generator=g)[: n // 4]
+    idx128 = torch.randperm(n // 2, device="cuda", generator=g)[: n // 8]
+    vals64 = torch.randint(0, 255, (n // 4, 64), dtype=torch.uint8, device="cuda", generator=g)
+    vals128 = torch.randint(0, 255, (n // 8, 128), dtype=torch.uint8, device="cuda", generator=g)
+    dst64, dst128 = torch.zeros_like(src64), torch.zeros_like(src128)
+    flat = torch.empty(n // 4 * 64, dtype=torch.uint8, device="cuda")
+    for _ in range(reps):
+        src64[idx64]
+        src128[idx128]
+        dst64[idx64] = vals64
+        dst128[idx128] = vals128
+        flat.copy_(vals64.view(-1))
+        torch.cuda.synchronize()
+
+
 def cpu_baseline(llm, seqs, budget_s: float):
     """The fp32 torch-CPU oracle decoding the same batch from a copy of the
     GPU's compact state (same weights, same live spans), for ~budget_s seconds."""
