@@ -39,47 +39,74 @@ __device__ __forceinline__ int64_t slot_row(int64_t base, const int32_t* table, 
   return table ? ((int64_t)table[r >> 4] << 4) + (r & 15) : base + r;
 }
 
+// The register type of one UNIT-byte access (a plain vector type: the HIP
+// uint4 struct kept the move buffers in scratch memory).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+template <int UNIT> struct UnitReg;
+template <> struct UnitReg<16> { using type = u32x4_t; };
+template <> struct UnitReg<4> { using type = uint32_t; };
+template <> struct UnitReg<1> { using type = uint8_t; };
+
+// Global-memory pointers: the arenas arrive as integers (a per-layer pointer
+// table), and through a generic pointer every row access would be a flat
+// access, which also counts against the LDS counter -- each LDS read of the
+// move list or page table would then wait for all row loads in flight.
+#define FDMS_GLOBAL __attribute__((address_space(1)))
+
 // Row-move passes over the chunk's move list (s_src / s_dst, ascending
-// sources): K rows then V rows, UNIT bytes per access.
-template <int UNIT>
+// sources): K rows then V rows, UNIT bytes per access.  A pass's loads are
+// unconditional (the units past the end repeat the last one) so that none
+// of them waits for its data before the next is issued, and the units stay
+// in registers.  TBL: 0 flat spans (row = base + slot), 1 paged with the
+// span's page table staged in LDS, 2 paged with the table read from global
+// memory (spans longer than the staging).
+template <int UNIT, int TBL>
 struct Mover {
   static constexpr int kU = kMoveBytes / UNIT < 16 ? kMoveBytes / UNIT : 16;  // units per thread and pass
-  uint8_t* ck;
-  uint8_t* cv;
+  using U = typename UnitReg<UNIT>::type;
+  FDMS_GLOBAL uint8_t* ck;
+  FDMS_GLOBAL uint8_t* cv;
   int64_t base, c_s_bytes;
-  const int32_t* table;
+  const int32_t* table;  // TBL 1: the kernel's LDS copy; TBL 2: global
   int units_per_row, n_moves, total;
   const int* s_src;
   const int* s_dst;
 
-  __device__ __forceinline__ void read(int p0, Vec<uint8_t, UNIT>* buf, int64_t* dst_off, int* which) const {
-#pragma unroll
-    for (int j = 0; j < kU; ++j) {
-      const int u = p0 + j * kThreads + (int)threadIdx.x;
-      which[j] = -1;
-      if (u < total) {
-        const int w = u / (n_moves * units_per_row);  // 0 = K, 1 = V
-        const int uu = u - w * n_moves * units_per_row;
-        const int r = uu / units_per_row;
-        const int64_t off = (int64_t)(uu - r * units_per_row) * UNIT;
-        const uint8_t* arena = w ? cv : ck;
-        buf[j] = *reinterpret_cast<const Vec<uint8_t, UNIT>*>(arena + slot_row(base, table, s_src[r]) * c_s_bytes + off);
-        dst_off[j] = slot_row(base, table, s_dst[r]) * c_s_bytes + off;
-        which[j] = w;
-      }
+  __device__ __forceinline__ int64_t row(int r) const {
+    if constexpr (TBL == 0) {
+      return base + r;
+    } else if constexpr (TBL == 1) {
+      return ((int64_t)table[r >> 4] << 4) + (r & 15);
+    } else {
+      return ((int64_t)((const FDMS_GLOBAL int32_t*)table)[r >> 4] << 4) + (r & 15);
     }
   }
-  __device__ __forceinline__ void write(const Vec<uint8_t, UNIT>* buf, const int64_t* dst_off, const int* which) const {
+  __device__ __forceinline__ void read(int p0, U* buf, int64_t* dst_off, int* which) const {
+#pragma unroll
+    for (int j = 0; j < kU; ++j) {
+      const int u0 = p0 + j * kThreads + (int)threadIdx.x;
+      const int u = min(u0, total - 1);  // total > 0
+      const int w = u / (n_moves * units_per_row);  // 0 = K, 1 = V
+      const int uu = u - w * n_moves * units_per_row;
+      const int r = uu / units_per_row;
+      const int64_t off = (int64_t)(uu - r * units_per_row) * UNIT;
+      const FDMS_GLOBAL uint8_t* arena = w ? cv : ck;
+      buf[j] = *reinterpret_cast<const FDMS_GLOBAL U*>(arena + row(s_src[r]) * c_s_bytes + off);
+      dst_off[j] = row(s_dst[r]) * c_s_bytes + off;
+      which[j] = u0 < total ? w : -1;
+    }
+  }
+  __device__ __forceinline__ void write(const U* buf, const int64_t* dst_off, const int* which) const {
 #pragma unroll
     for (int j = 0; j < kU; ++j)
-      if (which[j] >= 0) *reinterpret_cast<Vec<uint8_t, UNIT>*>((which[j] ? cv : ck) + dst_off[j]) = buf[j];
+      if (which[j] >= 0) *reinterpret_cast<FDMS_GLOBAL U*>((which[j] ? cv : ck) + dst_off[j]) = buf[j];
   }
   // every pass: its reads, a barrier (all reads of the pass done), its
   // writes; pass p + 1's reads are issued before pass p's writes
-  __device__ void run() const {
+  __device__ __forceinline__ void run() const {
     constexpr int kPass = kThreads * kU;
     if (total <= 0) return;
-    Vec<uint8_t, UNIT> b0[kU], b1[kU];
+    U b0[kU], b1[kU];
     int64_t o0[kU], o1[kU];
     int w0[kU], w1[kU];
     read(0, b0, o0, w0);
@@ -263,9 +290,16 @@ __global__ __launch_bounds__(kThreads) void dms_expiry_kernel(
     }
     __syncthreads();  // the move list is complete
     if (n_moves) {
-      Mover<UNIT> mvr{ck, cv, base, c_s_bytes, tbl, (int)(row_bytes / UNIT), n_moves,
-                      n_moves * (int)(row_bytes / UNIT) * 2, s_src, s_dst};
-      mvr.run();
+      auto* gk = (FDMS_GLOBAL uint8_t*)ck;
+      auto* gv = (FDMS_GLOBAL uint8_t*)cv;
+      const int upr = (int)(row_bytes / UNIT), total = n_moves * upr * 2;
+      if (!table) {
+        Mover<UNIT, 0>{gk, gv, base, c_s_bytes, nullptr, upr, n_moves, total, s_src, s_dst}.run();
+      } else if (tbl == s_table) {  // uniform
+        Mover<UNIT, 1>{gk, gv, base, c_s_bytes, s_table, upr, n_moves, total, s_src, s_dst}.run();
+      } else {
+        Mover<UNIT, 2>{gk, gv, base, c_s_bytes, table, upr, n_moves, total, s_src, s_dst}.run();
+      }
     }
     running += tot;
     __syncthreads();  // s_src / s_dst / s_cnt are reused by the next chunk
