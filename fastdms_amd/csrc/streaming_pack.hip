@@ -67,6 +67,7 @@ __device__ __forceinline__ SeqSpan seq_span(const int32_t* cu, int b, int single
 // trip per batch, not per chunk); each wave counts its 64 tokens of every
 // chunk with a ballot, and the running offset is accumulated uniformly.
 constexpr int kPrepBatch = 32;
+static_assert(kPrepBatch <= 64 && (kPrepBatch & (kPrepBatch - 1)) == 0, "one chunk per lane of a wave");
 
 // Page pool of one layer (paged compact KV): the free page ids are
 // stack[0 .. *top); a (seq, head) span owns pages bt[row * bt_b + h * bt_h + j],
@@ -139,14 +140,24 @@ __global__ __launch_bounds__(kChunk) void pack_prepare_kernel(
       if (lane == 0) s_cnt[j][wave] = __popcll(m);
     }
     __syncthreads();
+    // lane j < kPrepBatch of every wave: chunk c0 + j's kept count, then an
+    // inclusive scan over the lanes (every wave computes the same running
+    // offset; wave 0 stores the chunk offsets) -- one LDS round trip per
+    // batch instead of one per chunk
+    int tot = 0;
+    if (lane < kPrepBatch) {
 #pragma unroll
-    for (int j = 0; j < kPrepBatch; ++j) {
-      int tot = 0;
-#pragma unroll
-      for (int w = 0; w < kChunk / kWave; ++w) tot += s_cnt[j][w];
-      if (tid == j && c0 + j < max_chunks) offsets[b * of_b + h * of_h + (c0 + j) * of_c] = running;
-      running += tot;
+      for (int w = 0; w < kChunk / kWave; ++w) tot += s_cnt[lane][w];
     }
+    int incl = tot;
+#pragma unroll
+    for (int o = 1; o < kPrepBatch; o <<= 1) {
+      const int up = __shfl_up(incl, o);
+      if (lane >= o) incl += up;
+    }
+    if (wave == 0 && lane < kPrepBatch && c0 + lane < max_chunks)
+      offsets[b * of_b + h * of_h + (c0 + lane) * of_c] = running + incl - tot;
+    running += __shfl(incl, kPrepBatch - 1);
     if (c0 + kPrepBatch < max_chunks) __syncthreads();  // s_cnt is reused by the next batch
   }
   if (tid == 0) live_out[b * lo_b + h * lo_h] = running;
