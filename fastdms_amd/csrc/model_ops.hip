@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const bf16_t* __restr
   const float rscale = (PART && row_scale) ? row_scale[row] : 1.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int cc = min((threadIdx.x + j * kThreads) * V, hidden - V);
+    const int cc = min(((int)threadIdx.x + j * kThreads) * V, hidden - V);  // int min (an unsigned operand picks the double overload)
     wv[j] = *reinterpret_cast<const Vec<bf16_t, V>*>(weight + cc);
     if constexpr (PART) cs[j] = *reinterpret_cast<const Vec<float, V>*>(csrc + cc);
     if constexpr (PART && KS > 0) {
