@@ -47,10 +47,14 @@ FILE_FLAGS = {
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(HERE), "-c", str(src), "-o", str(obj)]
+    # the compiler's per-kernel resource report (registers, scratch, spills,
+    # LDS, occupancy) is kept beside the object: tests/test_codegen.py reads it
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(HERE), "-c", str(src), "-o", str(obj),
+           "-Rpass-analysis=kernel-resource-usage"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+    (BUILD_DIR / (src.stem + ".resources.txt")).write_text(res.stderr)
     return obj
 
 
